@@ -1,0 +1,143 @@
+/*
+ * nca_hip.h - C ABI of the MI355X (gfx950) NCA step / rollout library `libnca_hip.so`.
+ *
+ * Every entry point takes plain device pointers and sizes, returns an int status (NCA_OK = 0)
+ * and, on failure, leaves a message readable with nca_last_error() (thread-local). Calls are
+ * ordered on the given HIP stream (a hipStream_t passed as void*, NULL = default stream) and
+ * never synchronise the host. The library allocates no device memory: the caller owns every
+ * buffer, including the packed weights (nca_packed_weights_bytes / nca_pack_weights).
+ *
+ * Tensor layouts are the reference's: states (rows, C, H, W) fp32 contiguous (NCHW), given
+ * masks (rows, H, W) uint8, clamp values (rows, c_in, H, W) fp32. A "row" is one rollout,
+ * i.e. one (board, trial) pair flattened board-major: row = board * K + trial (reference
+ * src/nca/rollout.py:143-146).
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   nca_step          <- the step protocol `step(x, given4, clamp, fire, noise, noise_mask,
+ *                        clock) -> x` of make_step (src/nca/engine/step.py:74-209, call at
+ *                        184-207) and NCA.step (src/nca/model.py:503-559)
+ *   nca_rollout       <- the per-step loops inference_block / InferenceEngine.__call__
+ *                        (src/nca/engine/inference.py:9-71) and rollout()'s step loop
+ *                        (src/nca/rollout.py:203-247), fused into one launch
+ *   nca_fire_mask     <- draw_step's fire mask (src/nca/engine/rng.py:51-69) and
+ *                        NCA.sample_fire_mask (src/nca/model.py:567-593)
+ *   nca_readout       <- NCA.scores / confidence / board_confidence / decode
+ *                        (src/nca/model.py:596-633)
+ *   nca_conf_select   <- conf_at_k's per-board selection (src/nca/rollout.py:317-334)
+ */
+#ifndef NCA_HIP_H
+#define NCA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    NCA_OK = 0,
+    NCA_ERR_INVALID = 1,     /* bad argument (NULL pointer, inconsistent sizes) */
+    NCA_ERR_UNSUPPORTED = 2, /* a cell shape or option this build does not implement */
+    NCA_ERR_HIP = 3          /* a HIP runtime call failed */
+};
+
+enum { NCA_PAD_ZERO = 0, NCA_PAD_WALL = 1, NCA_PAD_WRAP = 2 };      /* model.py:140-152 */
+enum { NCA_HEAD_MLP = 0, NCA_HEAD_L2 = 1 };                         /* model.py:596-609 */
+enum { NCA_FP32 = 0, NCA_BF16 = 1 };
+
+/* The cell: "kernels" perception with `heads` 3x3 kernels (head-major features, F = heads*C),
+ * ReLU MLP F -> hidden -> C, no group normalisation, no time embedding (NCAConfig,
+ * src/nca/model.py:47-137). precision NCA_BF16 reproduces the rounding points of bf16 autocast:
+ * perception input, z, h and dx rounded to bf16, fp32 accumulation and fp32 state. */
+typedef struct nca_cell_desc {
+    int32_t channels;   /* C */
+    int32_t heads;      /* perception kernels (4) */
+    int32_t hidden;     /* MLP hidden width */
+    int32_t c_in;       /* clamped input slice [in_offset, in_offset + c_in) */
+    int32_t in_offset;
+    int32_t c_out;      /* readout slice [out_offset, out_offset + c_out) */
+    int32_t out_offset;
+    int32_t n_out;      /* readout classes (logits of the mlp head, tokens of the l2 head) */
+    int32_t padding;    /* NCA_PAD_* */
+    int32_t head_kind;  /* NCA_HEAD_* */
+    int32_t precision;  /* NCA_FP32 | NCA_BF16 */
+} nca_cell_desc;
+
+/* fp32 device pointers in the reference's parameter layouts. */
+typedef struct nca_cell_weights {
+    const float *kernels; /* perceive.weight (heads, 1, 3, 3) */
+    const float *w1;      /* update.fc1.weight (hidden, F, 1, 1) */
+    const float *b1;      /* update.fc1.bias (hidden) */
+    const float *w2;      /* update.fc2.weight (C, hidden, 1, 1) */
+    const float *b2;      /* update.fc2.bias (C) */
+    const float *head_w;  /* mlp: head.weight (n_out, c_out, 1, 1); l2: out_embed (n_out, c_out) */
+    const float *head_b;  /* mlp: head.bias (n_out); l2: NULL */
+    const float *pad_vec; /* wall border value (C) (model.py:320-325); may be NULL unless WALL */
+} nca_cell_weights;
+
+/* Which rows and how they fire. */
+typedef struct nca_fire_desc {
+    uint64_t seed;              /* Philox key when step_seeds is NULL */
+    const uint64_t *step_seeds; /* device (n_steps): per-step keys (engine/rng.py:37-39), or NULL */
+    const uint8_t *fire_in;     /* device (n_steps, rows, H, W) injected masks in {0,1}, or NULL */
+    int64_t row0;               /* global index of row 0 (Philox counter) */
+    int64_t step0;              /* global index of the first step (Philox counter) */
+    float p_fire;               /* firing probability */
+    float p_low;                /* adaptive firing: probability of confident cells */
+    float tau;                  /* adaptive firing: confidence threshold (strict >) */
+    int32_t adaptive;           /* 0 = uniform p_fire, 1 = confidence-gated (model.py:589-593) */
+    int32_t given_confident;    /* adaptive: given cells count as confident (rollout.py:36) */
+} nca_fire_desc;
+
+/* Bytes of the packed-weight buffer for this cell, 0 if the cell is unsupported. */
+size_t nca_packed_weights_bytes(const nca_cell_desc *cell);
+
+/* Convert the reference-layout fp32 weights into the kernels' MFMA fragment layout (bf16 or
+ * fp32 per cell->precision). `packed` must hold nca_packed_weights_bytes(cell) bytes. */
+int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void *packed,
+                     void *stream);
+
+/* Run n_steps NCA steps on `rows` states of H x W cells: x_out = step^n(x_in). x_in and x_out
+ * may alias. noise (rows, C, H, W) is added after the residual update when n_steps == 1
+ * (model.py:544-546), NULL otherwise. conf_out (rows) receives the board confidence of the
+ * final state (model.py:631-633), fired_out (rows) the number of fired cells over the call
+ * (rollout.py:233); either may be NULL. */
+int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
+                float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
+                float *conf_out, int32_t *fired_out, void *stream);
+
+/* One step with an injected fire mask (rows, H, W) fp32 in {0,1}: the make_step drop-in. */
+int nca_step(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+             int32_t width, const float *x, const uint8_t *given, const float *clamp,
+             const float *fire, const float *noise, float *x_out, void *stream);
+
+/* Fire mask of one step: out (rows, H, W) uint8. conf_cell (rows, H, W) and given are read only
+ * when fire->adaptive. fire->fire_in and fire->step_seeds are ignored (key = fire->seed). */
+int nca_fire_mask(int64_t rows, int32_t height, int32_t width, const nca_fire_desc *fire,
+                  int64_t step, const float *conf_cell, const uint8_t *given, uint8_t *out,
+                  void *stream);
+
+/* Readout of fp32 states x (rows, C, H, W): per-cell confidence (rows, H, W), board confidence
+ * (rows) and argmax class index (rows, H, W); each output may be NULL. */
+int nca_readout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                int32_t width, const float *x, float *conf_cell, float *conf_board,
+                int32_t *argmax, void *stream);
+
+/* conf@K selection: best[n] = first argmax over trials t < k of conf[n, t] (alive[n, t] == 0
+ * counts as -inf; alive may be NULL). conf (N, K) fp32, best (N) int32. */
+int nca_conf_select(const float *conf, const uint8_t *alive, int32_t n_boards, int32_t k_trials,
+                    int32_t k, int32_t *best, void *stream);
+
+/* Last error message of the calling thread ("" if none). */
+const char *nca_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+int nca_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NCA_HIP_H */

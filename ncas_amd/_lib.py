@@ -1,0 +1,149 @@
+"""ctypes bindings of `libnca_hip.so` (the C ABI declared in include/nca_hip.h).
+
+The library is loaded from the package directory. There is no fallback: when it is missing or
+cannot be loaded every operator raises, so a silent CPU path can never stand in for the HIP one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_SO = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnca_hip.so")
+
+NCA_OK, NCA_ERR_INVALID, NCA_ERR_UNSUPPORTED, NCA_ERR_HIP = 0, 1, 2, 3
+PADDING = {"zero": 0, "wall": 1, "wrap": 2}
+HEAD = {"mlp": 0, "l2": 1}
+PRECISION = {"fp32": 0, "bf16": 1}
+
+EXPORTS = (
+    "nca_packed_weights_bytes",
+    "nca_pack_weights",
+    "nca_rollout",
+    "nca_step",
+    "nca_fire_mask",
+    "nca_readout",
+    "nca_conf_select",
+    "nca_last_error",
+    "nca_version",
+)
+
+
+class CellDesc(ctypes.Structure):
+    _fields_ = [
+        ("channels", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("c_in", ctypes.c_int32),
+        ("in_offset", ctypes.c_int32),
+        ("c_out", ctypes.c_int32),
+        ("out_offset", ctypes.c_int32),
+        ("n_out", ctypes.c_int32),
+        ("padding", ctypes.c_int32),
+        ("head_kind", ctypes.c_int32),
+        ("precision", ctypes.c_int32),
+    ]
+
+
+class CellWeights(ctypes.Structure):
+    _fields_ = [
+        ("kernels", ctypes.c_void_p),
+        ("w1", ctypes.c_void_p),
+        ("b1", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("b2", ctypes.c_void_p),
+        ("head_w", ctypes.c_void_p),
+        ("head_b", ctypes.c_void_p),
+        ("pad_vec", ctypes.c_void_p),
+    ]
+
+
+class FireDesc(ctypes.Structure):
+    _fields_ = [
+        ("seed", ctypes.c_uint64),
+        ("step_seeds", ctypes.c_void_p),
+        ("fire_in", ctypes.c_void_p),
+        ("row0", ctypes.c_int64),
+        ("step0", ctypes.c_int64),
+        ("p_fire", ctypes.c_float),
+        ("p_low", ctypes.c_float),
+        ("tau", ctypes.c_float),
+        ("adaptive", ctypes.c_int32),
+        ("given_confident", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return _SO
+
+
+def load():
+    """Load the HIP library (raises RuntimeError when it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_SO):
+        raise RuntimeError(
+            f"{_SO} is not built: run `python -m ncas_amd.build` (or __graft_entry__.build())"
+        )
+    L = ctypes.CDLL(_SO)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    L.nca_packed_weights_bytes.argtypes = [ctypes.POINTER(CellDesc)]
+    L.nca_packed_weights_bytes.restype = ctypes.c_size_t
+    L.nca_pack_weights.argtypes = [ctypes.POINTER(CellDesc), ctypes.POINTER(CellWeights), vp, vp]
+    L.nca_rollout.argtypes = [
+        ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, ctypes.POINTER(FireDesc),
+        i32, vp, vp, vp, vp,
+    ]
+    L.nca_step.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, vp, vp, vp]
+    L.nca_fire_mask.argtypes = [i64, i32, i32, ctypes.POINTER(FireDesc), i64, vp, vp, vp, vp]
+    L.nca_readout.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, vp]
+    L.nca_conf_select.argtypes = [vp, vp, i32, i32, i32, vp, vp]
+    L.nca_last_error.restype = ctypes.c_char_p
+    L.nca_version.restype = ctypes.c_int
+    for name in EXPORTS:
+        getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
+    _lib = L
+    return L
+
+
+def check(rc: int, what: str) -> None:
+    if rc == NCA_OK:
+        return
+    msg = load().nca_last_error().decode(errors="replace")
+    if rc in (NCA_ERR_INVALID, NCA_ERR_UNSUPPORTED):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors must be on the same GPU: the HIP path has no CPU fallback."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(
+                f"the HIP operators need GPU tensors (got a tensor on {t.device}); "
+                "there is no CPU implementation"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev

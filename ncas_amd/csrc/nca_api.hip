@@ -1,0 +1,429 @@
+// C ABI of libnca_hip.so (declared in include/nca_hip.h): argument checks, weight packing,
+// launch planning and the small kernels (fire mask, readout, conf@K selection).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/nca_hip.h"
+#include "nca_device.h"
+#include "nca_layout.h"
+#include "nca_rollout.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(NCA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return NCA_OK;
+}
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per workgroup
+
+bool shape_supported(int C, int hidden) {
+    return (C == 16 && hidden == 128) || (C == 32 && hidden == 256) || (C == 64 && hidden == 256);
+}
+
+int check_cell(const nca_cell_desc *d) {
+    if (!d) return fail(NCA_ERR_INVALID, "cell descriptor is NULL");
+    if (d->heads != 4)
+        return fail(NCA_ERR_UNSUPPORTED, "heads=%d: only 4 perception kernels are implemented", d->heads);
+    if (!shape_supported(d->channels, d->hidden))
+        return fail(NCA_ERR_UNSUPPORTED,
+                    "cell C=%d hidden=%d is not built (built: 16/128, 32/256, 64/256)", d->channels,
+                    d->hidden);
+    if (d->c_in < 0 || d->in_offset < 0 || d->in_offset + d->c_in > d->channels)
+        return fail(NCA_ERR_INVALID, "input slice [%d, %d) exceeds the state", d->in_offset,
+                    d->in_offset + d->c_in);
+    if (d->c_out < 1 || d->out_offset < 0 || d->out_offset + d->c_out > d->channels)
+        return fail(NCA_ERR_INVALID, "output slice [%d, %d) exceeds the state", d->out_offset,
+                    d->out_offset + d->c_out);
+    if (d->n_out < 1 || d->n_out > 16) return fail(NCA_ERR_UNSUPPORTED, "n_out=%d (1..16)", d->n_out);
+    if (d->padding < NCA_PAD_ZERO || d->padding > NCA_PAD_WRAP)
+        return fail(NCA_ERR_INVALID, "padding=%d", d->padding);
+    if (d->head_kind != NCA_HEAD_MLP && d->head_kind != NCA_HEAD_L2)
+        return fail(NCA_ERR_INVALID, "head_kind=%d", d->head_kind);
+    if (d->precision != NCA_FP32 && d->precision != NCA_BF16)
+        return fail(NCA_ERR_INVALID, "precision=%d", d->precision);
+    return NCA_OK;
+}
+
+nca::PackedLayout layout_of(const nca_cell_desc *d) {
+    return nca::packed_layout(d->channels, d->heads, d->hidden, d->c_out, d->n_out,
+                              d->precision == NCA_BF16);
+}
+
+// ------------------------------------------------------------------------------------------
+// Weight packing
+__global__ void pack_small(const float *src, int n, float *dst, int round_bf16) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float v = src ? src[i] : 0.0f;
+        dst[i] = round_bf16 ? nca::round_bf16(v) : v;
+    }
+}
+
+// A fragments of an (M x K) row-major matrix (M, K multiples of 16 and of the k-tile).
+__global__ void pack_frags(const float *src, int M, int K, int bf16, void *dst) {
+    const int total = M * K;
+    const int ktile = bf16 ? 32 : 4;
+    const int nkt = K / ktile;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        int m, k;
+        if (bf16) {
+            const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
+            const int kt = blk % nkt, mt = blk / nkt;
+            m = mt * 16 + (lane & 15);
+            k = kt * 32 + 8 * (lane >> 4) + s;
+            reinterpret_cast<__bf16 *>(dst)[e] = (__bf16)src[(size_t)m * K + k];
+        } else {
+            const int lane = e & 63, blk = e >> 6;
+            const int kt = blk % nkt, mt = blk / nkt;
+            m = mt * 16 + (lane & 15);
+            k = kt * 4 + (lane >> 4);
+            reinterpret_cast<float *>(dst)[e] = src[(size_t)m * K + k];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Fire mask of one step
+__global__ void fire_mask_kernel(int64_t rows, int hw, uint64_t seed, int64_t row0, uint32_t step,
+                                 float p, float p_low, float tau, int adaptive, int given_conf,
+                                 const float *conf, const uint8_t *given, uint8_t *out) {
+    const int nq = (hw + 3) >> 2;
+    const int64_t total = rows * nq;
+    for (int64_t it = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; it < total;
+         it += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = it / nq;
+        const int qq = (int)(it - r * nq);
+        float u[4];
+        nca::cell_uniforms4(seed, (uint32_t)(row0 + r), step, (uint32_t)qq, u);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int q = 4 * qq + e;
+            if (q >= hw) break;
+            const int64_t cell = r * hw + q;
+            float pc = p;
+            if (adaptive) {
+                const bool confident = conf[cell] > tau || (given_conf && given && given[cell]);
+                if (confident) pc = p_low;
+            }
+            out[cell] = u[e] < pc ? 1 : 0;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Readout: one workgroup per row, cells in chunks of the workgroup size; the board sum runs in
+// cell order on one lane so that its rounding matches the sequential definition.
+__global__ void readout_kernel(const float *x, int C, int hw, int out_off, int c_out, int n_out,
+                               int head_kind, const float *headw, const float *headb,
+                               float *conf_cell, float *conf_board, int32_t *argmax) {
+    __shared__ float chunk[256];
+    const int64_t r = blockIdx.x;
+    const float *xr = x + (r * C + out_off) * (int64_t)hw;
+    float sum = 0.0f;
+    for (int base = 0; base < hw; base += 256) {
+        const int q = base + threadIdx.x;
+        if (q < hw) {
+            int am;
+            const float cf = nca::cell_readout(xr + q, hw, c_out, n_out, head_kind, headw, headb, &am);
+            if (conf_cell) conf_cell[r * hw + q] = cf;
+            if (argmax) argmax[r * hw + q] = am;
+            chunk[threadIdx.x] = cf;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int n = hw - base < 256 ? hw - base : 256;
+            for (int i = 0; i < n; ++i) sum = __fadd_rn(sum, chunk[i]);
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0 && conf_board) conf_board[r] = __fdiv_rn(sum, (float)hw);
+}
+
+// ------------------------------------------------------------------------------------------
+// conf@K: one wavefront per board; (value, index) pairs reduced across lanes with the
+// first-maximum rule (ties -> lower index; NaN counts as the largest, like np.argmax).
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    const bool vn = v != v, bn = bv != bv;
+    if (vn != bn) return vn;
+    if (!vn && v != bv) return v > bv;
+    return i < bi;
+}
+
+__global__ void conf_select_kernel(const float *conf, const uint8_t *alive, int N, int K, int k,
+                                   int32_t *best) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= N) return;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int t = lane; t < k; t += 64) {
+        float v = conf[(int64_t)wave * K + t];
+        if (alive && !alive[(int64_t)wave * K + t]) v = -INFINITY;
+        if (bi == 0x7fffffff || better(v, t, bv, bi)) {
+            bv = v;
+            bi = t;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oi != 0x7fffffff && (bi == 0x7fffffff || better(ov, oi, bv, bi))) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) best[wave] = bi == 0x7fffffff ? 0 : bi;
+}
+
+// ------------------------------------------------------------------------------------------
+// Rollout launch
+struct Plan {
+    nca::LdsPlan lds;
+    int R;
+};
+
+template <int C, int HD, bool BF16>
+int launch_rollout(nca::RolloutParams p, hipStream_t st) {
+    int R = (int)((p.rows + 255) / 256);
+    if (R < 1) R = 1;
+    if (R > 16) R = 16;
+    nca::LdsPlan L{};
+    for (; R >= 1; --R) {
+        L = nca::lds_plan<C, HD, BF16>(R, p.H, p.W, p.c_in, p.c_out, p.n_out);
+        if (L.total <= kLdsBytes) break;
+    }
+    if (R < 1)
+        return fail(NCA_ERR_UNSUPPORTED,
+                    "a %dx%d grid with C=%d does not fit the LDS-resident rollout kernel", p.H, p.W, C);
+    p.rows_per_wg = R;
+    p.l_P = L.P;
+    p.l_M = L.M;
+    p.l_Z = L.Z;
+    p.l_H = L.H;
+    p.l_clamp = L.clamp;
+    p.l_given = L.given;
+    p.l_fire = L.fire;
+    p.l_conf = L.conf;
+    p.l_fired = L.fired;
+    p.l_head = L.head;
+    auto kfn = nca::rollout_resident<C, HD, BF16>;
+    int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total),
+                       "hipFuncSetAttribute");
+    if (rc) return rc;
+    const int64_t grid = (p.rows + R - 1) / R;
+    hipLaunchKernelGGL(kfn, dim3((unsigned)grid), dim3(256), L.total, st, p);
+    return hip_check(hipGetLastError(), "rollout launch");
+}
+
+int dispatch_rollout(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
+    const bool bf = d->precision == NCA_BF16;
+    if (d->channels == 16 && d->hidden == 128)
+        return bf ? launch_rollout<16, 128, true>(p, st) : launch_rollout<16, 128, false>(p, st);
+    if (d->channels == 32 && d->hidden == 256)
+        return bf ? launch_rollout<32, 256, true>(p, st) : launch_rollout<32, 256, false>(p, st);
+    if (d->channels == 64 && d->hidden == 256)
+        return bf ? launch_rollout<64, 256, true>(p, st) : launch_rollout<64, 256, false>(p, st);
+    return fail(NCA_ERR_UNSUPPORTED, "cell C=%d hidden=%d", d->channels, d->hidden);
+}
+
+nca::RolloutParams base_params(const nca_cell_desc *d, const void *packed, int64_t rows, int H,
+                               int W) {
+    nca::RolloutParams p;
+    memset(&p, 0, sizeof(p));
+    const nca::PackedLayout L = layout_of(d);
+    p.packed = static_cast<const unsigned char *>(packed);
+    p.rows = rows;
+    p.H = H;
+    p.W = W;
+    p.c_in = d->c_in;
+    p.in_off = d->in_offset;
+    p.c_out = d->c_out;
+    p.out_off = d->out_offset;
+    p.n_out = d->n_out;
+    p.head_kind = d->head_kind;
+    p.padding = d->padding;
+    p.off_kern = (unsigned)L.kern;
+    p.off_b1 = (unsigned)L.b1;
+    p.off_b2 = (unsigned)L.b2;
+    p.off_headw = (unsigned)L.headw;
+    p.off_headb = (unsigned)L.headb;
+    p.off_padv = (unsigned)L.padv;
+    p.off_w1 = (unsigned)L.w1;
+    p.off_w2 = (unsigned)L.w2;
+    return p;
+}
+
+int check_grid(int64_t rows, int H, int W) {
+    if (rows < 0 || H < 1 || W < 1) return fail(NCA_ERR_INVALID, "rows=%lld H=%d W=%d", (long long)rows, H, W);
+    if ((int64_t)H * W > (1 << 24)) return fail(NCA_ERR_UNSUPPORTED, "grid %dx%d too large", H, W);
+    return NCA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *nca_last_error(void) { return g_err; }
+
+int nca_version(void) { return 100; }
+
+size_t nca_packed_weights_bytes(const nca_cell_desc *cell) {
+    if (check_cell(cell)) return 0;
+    return layout_of(cell).total;
+}
+
+int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void *packed, void *stream) {
+    g_err[0] = 0;
+    int rc = check_cell(cell);
+    if (rc) return rc;
+    if (!w || !w->kernels || !w->w1 || !w->b1 || !w->w2 || !w->b2 || !w->head_w || !packed)
+        return fail(NCA_ERR_INVALID, "NULL weight pointer");
+    if (cell->head_kind == NCA_HEAD_MLP && !w->head_b) return fail(NCA_ERR_INVALID, "mlp head needs head_b");
+    if (cell->padding == NCA_PAD_WALL && !w->pad_vec) return fail(NCA_ERR_INVALID, "wall padding needs pad_vec");
+    const nca::PackedLayout L = layout_of(cell);
+    const bool bf = cell->precision == NCA_BF16;
+    hipStream_t st = as_stream(stream);
+    unsigned char *pk = static_cast<unsigned char *>(packed);
+    const int C = cell->channels, HD = cell->hidden, F = cell->heads * C;
+    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->kernels, cell->heads * 9,
+                       reinterpret_cast<float *>(pk + L.kern), (int)bf);
+    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->b1, HD, reinterpret_cast<float *>(pk + L.b1), (int)bf);
+    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->b2, C, reinterpret_cast<float *>(pk + L.b2), (int)bf);
+    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->head_w, cell->n_out * cell->c_out,
+                       reinterpret_cast<float *>(pk + L.headw), 0);
+    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->head_b, cell->n_out,
+                       reinterpret_cast<float *>(pk + L.headb), 0);
+    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->pad_vec, C, reinterpret_cast<float *>(pk + L.padv), 0);
+    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, (int)bf, (void *)(pk + L.w1));
+    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w2, C, HD, (int)bf, (void *)(pk + L.w2));
+    return hip_check(hipGetLastError(), "pack launch");
+}
+
+int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
+                float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
+                float *conf_out, int32_t *fired_out, void *stream) {
+    g_err[0] = 0;
+    int rc = check_cell(cell);
+    if (rc) return rc;
+    if ((rc = check_grid(rows, height, width))) return rc;
+    if (rows == 0) return NCA_OK;
+    if (!packed || !x_in || !given || (!clamp && cell->c_in > 0) || !x_out || !fire)
+        return fail(NCA_ERR_INVALID, "NULL pointer argument");
+    if (n_steps < 0) return fail(NCA_ERR_INVALID, "n_steps=%d", n_steps);
+    if (noise && n_steps != 1) return fail(NCA_ERR_INVALID, "noise needs n_steps == 1");
+    if (fire->adaptive && fire->fire_in) return fail(NCA_ERR_INVALID, "adaptive firing with injected masks");
+    nca::RolloutParams p = base_params(cell, packed, rows, height, width);
+    p.x_in = x_in;
+    p.x_out = x_out;
+    p.given = given;
+    p.clamp = clamp;
+    p.fire_u8 = fire->fire_in;
+    p.noise = noise;
+    p.step_seeds = fire->step_seeds;
+    p.conf_out = conf_out;
+    p.fired_out = fired_out;
+    p.seed = fire->seed;
+    p.row0 = fire->row0;
+    p.step0 = fire->step0;
+    p.n_steps = n_steps;
+    p.p = fire->p_fire;
+    p.p_low = fire->p_low;
+    p.tau = fire->tau;
+    p.adaptive = fire->adaptive;
+    p.given_confident = fire->given_confident;
+    return dispatch_rollout(cell, p, as_stream(stream));
+}
+
+int nca_step(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+             int32_t width, const float *x, const uint8_t *given, const float *clamp,
+             const float *fire, const float *noise, float *x_out, void *stream) {
+    g_err[0] = 0;
+    int rc = check_cell(cell);
+    if (rc) return rc;
+    if ((rc = check_grid(rows, height, width))) return rc;
+    if (rows == 0) return NCA_OK;
+    if (!packed || !x || !given || (!clamp && cell->c_in > 0) || !fire || !x_out)
+        return fail(NCA_ERR_INVALID, "NULL pointer argument");
+    nca::RolloutParams p = base_params(cell, packed, rows, height, width);
+    p.x_in = x;
+    p.x_out = x_out;
+    p.given = given;
+    p.clamp = clamp;
+    p.fire_f32 = fire;
+    p.noise = noise;
+    p.n_steps = 1;
+    return dispatch_rollout(cell, p, as_stream(stream));
+}
+
+int nca_fire_mask(int64_t rows, int32_t height, int32_t width, const nca_fire_desc *fire,
+                  int64_t step, const float *conf_cell, const uint8_t *given, uint8_t *out,
+                  void *stream) {
+    g_err[0] = 0;
+    int rc = check_grid(rows, height, width);
+    if (rc) return rc;
+    if (!fire || !out) return fail(NCA_ERR_INVALID, "NULL pointer argument");
+    if (fire->adaptive && !conf_cell) return fail(NCA_ERR_INVALID, "adaptive firing needs conf_cell");
+    if (rows == 0) return NCA_OK;
+    const int hw = height * width;
+    const int64_t items = rows * ((hw + 3) / 4);
+    const int blocks = (int)((items + 255) / 256 < 65536 ? (items + 255) / 256 : 65536);
+    hipLaunchKernelGGL(fire_mask_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), rows, hw,
+                       fire->seed, fire->row0, (uint32_t)step, fire->p_fire, fire->p_low, fire->tau,
+                       fire->adaptive, fire->given_confident, conf_cell, given, out);
+    return hip_check(hipGetLastError(), "fire mask launch");
+}
+
+int nca_readout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                int32_t width, const float *x, float *conf_cell, float *conf_board,
+                int32_t *argmax, void *stream) {
+    g_err[0] = 0;
+    int rc = check_cell(cell);
+    if (rc) return rc;
+    if ((rc = check_grid(rows, height, width))) return rc;
+    if (!packed || !x) return fail(NCA_ERR_INVALID, "NULL pointer argument");
+    if (rows == 0) return NCA_OK;
+    if (rows > 0x7fffffff) return fail(NCA_ERR_UNSUPPORTED, "rows=%lld", (long long)rows);
+    const nca::PackedLayout L = layout_of(cell);
+    const unsigned char *pk = static_cast<const unsigned char *>(packed);
+    hipLaunchKernelGGL(readout_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), x,
+                       cell->channels, height * width, cell->out_offset, cell->c_out, cell->n_out,
+                       cell->head_kind, reinterpret_cast<const float *>(pk + L.headw),
+                       reinterpret_cast<const float *>(pk + L.headb), conf_cell, conf_board, argmax);
+    return hip_check(hipGetLastError(), "readout launch");
+}
+
+int nca_conf_select(const float *conf, const uint8_t *alive, int32_t n_boards, int32_t k_trials,
+                    int32_t k, int32_t *best, void *stream) {
+    g_err[0] = 0;
+    if (!conf || !best) return fail(NCA_ERR_INVALID, "NULL pointer argument");
+    if (n_boards < 0 || k_trials < 1 || k < 1)
+        return fail(NCA_ERR_INVALID, "N=%d K=%d k=%d", n_boards, k_trials, k);
+    if (n_boards == 0) return NCA_OK;
+    if (k > k_trials) k = k_trials;
+    const int64_t threads = (int64_t)n_boards * 64;
+    hipLaunchKernelGGL(conf_select_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), conf, alive, n_boards, k_trials, k, best);
+    return hip_check(hipGetLastError(), "conf select launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,53 @@
+// Packed-weight layout, shared by the host code and the kernels.
+//
+// The packed buffer holds, at 256-byte aligned offsets:
+//   kern   float[heads * 9]   perception kernels (bf16-rounded values for bf16 cells)
+//   b1     float[hidden]      fc1 bias (bf16-rounded for bf16 cells: autocast casts it)
+//   b2     float[C]           fc2 bias (idem)
+//   headw  float[n_out*c_out] readout head weight / l2 token embeddings (fp32: the readout
+//                             runs outside autocast, reference src/nca/rollout.py:184-186)
+//   headb  float[n_out]
+//   padv   float[C]           wall border value
+//   w1     MFMA A fragments of fc1: [m-tile (hidden/16)][k-tile][lane 64][slot]
+//   w2     MFMA A fragments of fc2: [m-tile (C/16)][k-tile][lane 64][slot]
+// bf16 cells use v_mfma_f32_16x16x32_bf16 fragments (k-tile 32, 8 bf16 slots per lane:
+// A[i = lane % 16][k = 8 * (lane / 16) + slot]); fp32 cells use v_mfma_f32_16x16x4_f32
+// fragments (k-tile 4, one float per lane: A[i = lane % 16][k = lane / 16]).
+#pragma once
+
+#include <stddef.h>
+
+namespace nca {
+
+struct PackedLayout {
+    size_t kern, b1, b2, headw, headb, padv, w1, w2, total;
+};
+
+__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+__host__ __device__ inline PackedLayout packed_layout(int C, int heads, int hidden, int c_out,
+                                                      int n_out, bool bf16) {
+    PackedLayout L;
+    size_t o = 0;
+    L.kern = o;
+    o = align256(o + sizeof(float) * heads * 9);
+    L.b1 = o;
+    o = align256(o + sizeof(float) * hidden);
+    L.b2 = o;
+    o = align256(o + sizeof(float) * C);
+    L.headw = o;
+    o = align256(o + sizeof(float) * n_out * c_out);
+    L.headb = o;
+    o = align256(o + sizeof(float) * n_out);
+    L.padv = o;
+    o = align256(o + sizeof(float) * C);
+    const size_t esz = bf16 ? 2 : 4;
+    L.w1 = o;
+    o = align256(o + esz * (size_t)hidden * heads * C);
+    L.w2 = o;
+    o = align256(o + esz * (size_t)C * hidden);
+    L.total = o;
+    return L;
+}
+
+}  // namespace nca

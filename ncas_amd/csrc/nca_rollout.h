@@ -1,0 +1,488 @@
+// The LDS-resident multi-step rollout kernel (gfx950).
+//
+// One workgroup of 4 waves owns `rows_per_wg` rows (rollouts) for the whole call: their states
+// are loaded from HBM once, advanced `n_steps` steps inside LDS, and written back once. One
+// step of the reference cell (src/nca/model.py:503-559) is, per 16-cell tile:
+//
+//   stencil  all 256 lanes: z[cell][k*C + c] = sum_taps kern[k][tap] * P[nbr(cell, tap)][c]
+//            from the perception buffer P (LDS, 1-cell halo, bf16 or fp32), into Z (LDS);
+//   fc1      wave w owns hidden units [w*HD/4, (w+1)*HD/4): h^T = W1 z^T on MFMA with its W1
+//            fragments resident in registers (A operand), z^T read from Z as the B operand;
+//            bias + ReLU (+ bf16 rounding) fused, h written to H (LDS);
+//   fc2      wave w owns output channels [16w, 16w+16) (C / 16 m-tiles spread over the waves):
+//            dx^T = W2 h^T on MFMA with register-resident W2 fragments;
+//   update   in the fc2 accumulator layout (lane: 4 consecutive channels of one cell):
+//            u = x + fire * dx (+ noise), clamp of the given cells' input slice, written to the
+//            fp32 state and to the other perception buffer (ping-pong across steps).
+//
+// The fire mask of a step is drawn once per step for all cells (Philox, or read from an
+// injected mask); adaptive firing reads the pre-step confidence first. With wrap padding the
+// halo of the new perception buffer is refreshed after each step; wall / zero halos are
+// constant. The board confidence of the final state is computed in-kernel.
+//
+// Precision: BF16 reproduces bf16 autocast (perception input, z, h, dx rounded to bf16, fp32
+// accumulation, fp32 state held in a separate fp32 buffer M); fp32 keeps everything fp32 and
+// uses v_mfma_f32_16x16x4_f32 (the perception buffer is then the state itself).
+#pragma once
+
+#include "nca_device.h"
+#include "nca_layout.h"
+
+namespace nca {
+
+struct RolloutParams {
+    const float *x_in;
+    float *x_out;
+    const uint8_t *given;
+    const float *clamp;
+    const unsigned char *packed;
+    const uint8_t *fire_u8;      // injected masks (n_steps, rows, HW), or null
+    const float *fire_f32;       // injected mask of a single step (rows, HW), or null
+    const float *noise;          // (rows, C, HW), single step only, or null
+    const uint64_t *step_seeds;  // (n_steps) or null
+    float *conf_out;
+    int32_t *fired_out;
+    int64_t rows;
+    int H, W;
+    int c_in, in_off, c_out, out_off, n_out, head_kind, padding;
+    uint64_t seed;
+    int64_t row0, step0;
+    int n_steps;
+    float p, p_low, tau;
+    int adaptive, given_confident;
+    int rows_per_wg;
+    unsigned off_kern, off_b1, off_b2, off_headw, off_headb, off_padv, off_w1, off_w2;
+    unsigned l_P, l_M, l_Z, l_H, l_clamp, l_given, l_fire, l_conf, l_fired, l_head;
+};
+
+template <int C, int HD, bool BF16>
+struct Shape {
+    static constexpr int NH = 4;            // perception kernels
+    static constexpr int F = NH * C;        // features
+    static constexpr int NW = 4;            // waves per workgroup
+    static constexpr int NT = NW * 64;      // threads
+    static constexpr int KT = BF16 ? 32 : 4;  // MFMA k per instruction
+    static constexpr int HPW = HD / NW;     // hidden units per wave
+    static constexpr int MT1 = HPW / 16;    // fc1 m-tiles per wave
+    static constexpr int KT1 = F / KT;      // fc1 k-tiles
+    static constexpr int MT2 = C / 16;      // fc2 m-tiles (all waves)
+    static constexpr int MT2W = (MT2 + NW - 1) / NW;  // fc2 m-tiles per wave (max)
+    static constexpr int KT2 = HD / KT;     // fc2 k-tiles
+    static constexpr int ES = BF16 ? 2 : 4;  // bytes per element of P, Z, H
+    static constexpr int CP = C + 4;        // P channel stride (elements)
+    static constexpr int MP = C + 4;        // M channel stride (floats)
+    static constexpr int ZS = F + (BF16 ? 8 : 4);   // Z row stride (elements)
+    static constexpr int HS = HD + (BF16 ? 8 : 4);  // H row stride (elements)
+    static_assert(HD % 64 == 0, "hidden must be a multiple of 64");
+    static_assert(C % 16 == 0 && C <= 64, "channels must be 16, 32, 48 or 64");
+    static_assert(16 * (C / 4) <= NT, "stencil items exceed the workgroup");
+};
+
+// LDS plan for R rows of an H x W grid.
+struct LdsPlan {
+    unsigned P, M, Z, H, clamp, given, fire, conf, fired, head, total;
+};
+
+template <int C, int HD, bool BF16>
+inline LdsPlan lds_plan(int R, int H, int W, int c_in, int c_out, int n_out) {
+    using S = Shape<C, HD, BF16>;
+    const unsigned hw = (unsigned)H * W, hwp = (unsigned)(H + 2) * (W + 2);
+    auto al = [](unsigned v) { return (v + 15u) & ~15u; };
+    LdsPlan p;
+    unsigned o = 0;
+    p.P = o;
+    o = al(o + 2u * R * hwp * S::CP * S::ES);
+    p.M = o;
+    o = al(o + (BF16 ? (unsigned)R * hw * S::MP * 4u : 0u));
+    p.Z = o;
+    o = al(o + 16u * S::ZS * S::ES);
+    p.H = o;
+    o = al(o + 16u * S::HS * S::ES);
+    p.clamp = o;
+    o = al(o + (unsigned)R * hw * c_in * 4u);
+    p.given = o;
+    o = al(o + (unsigned)R * hw);
+    p.fire = o;
+    o = al(o + (unsigned)R * hw * 4u);
+    p.conf = o;
+    o = al(o + (unsigned)R * hw * 4u);
+    p.fired = o;
+    o = al(o + (unsigned)R * 4u);
+    p.head = o;
+    o = al(o + (unsigned)(n_out * c_out + n_out) * 4u);
+    p.total = o;
+    return p;
+}
+
+// 4 consecutive elements of P / Z / H as floats.
+template <bool BF16>
+__device__ __forceinline__ void lds_load4(const unsigned char *base, int elem, float v[4]) {
+    if constexpr (BF16) {
+        const uint2 u = *reinterpret_cast<const uint2 *>(base + 2 * elem);
+        v[0] = bf16_lo(u.x);
+        v[1] = bf16_hi(u.x);
+        v[2] = bf16_lo(u.y);
+        v[3] = bf16_hi(u.y);
+    } else {
+        const float4 u = *reinterpret_cast<const float4 *>(base + 4 * elem);
+        v[0] = u.x;
+        v[1] = u.y;
+        v[2] = u.z;
+        v[3] = u.w;
+    }
+}
+
+template <bool BF16>
+__device__ __forceinline__ void lds_store4(unsigned char *base, int elem, const float v[4]) {
+    if constexpr (BF16) {
+        uint2 u;
+        u.x = pack_bf16x2(v[0], v[1]);
+        u.y = pack_bf16x2(v[2], v[3]);
+        *reinterpret_cast<uint2 *>(base + 2 * elem) = u;
+    } else {
+        *reinterpret_cast<float4 *>(base + 4 * elem) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+template <bool BF16>
+struct Frag;
+template <>
+struct Frag<true> {
+    typedef bf16x8 type;
+    static __device__ __forceinline__ type load_lds(const unsigned char *base, int elem) {
+        return *reinterpret_cast<const bf16x8 *>(base + 2 * elem);
+    }
+    static __device__ __forceinline__ f32x4 mfma(type a, type b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct Frag<false> {
+    typedef float type;
+    static __device__ __forceinline__ type load_lds(const unsigned char *base, int elem) {
+        return *reinterpret_cast<const float *>(base + 4 * elem);
+    }
+    static __device__ __forceinline__ f32x4 mfma(type a, type b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+};
+
+template <int C, int HD, bool BF16>
+__global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
+    using S = Shape<C, HD, BF16>;
+    using FR = Frag<BF16>;
+    using fr_t = typename FR::type;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, l16 = lane & 15;
+    const int H = a.H, W = a.W, HWn = H * W, Wp = W + 2, HWp = (H + 2) * Wp;
+    const int Rcap = a.rows_per_wg;
+    const int64_t rbase = (int64_t)blockIdx.x * Rcap;
+    const int Rw = (int)((a.rows - rbase) < Rcap ? (a.rows - rbase) : Rcap);
+    const int ncell = Rw * HWn;
+    const int ntile = (ncell + 15) >> 4;
+
+    unsigned char *Pb = smem + a.l_P;
+    float *M = reinterpret_cast<float *>(smem + a.l_M);
+    unsigned char *Zb = smem + a.l_Z;
+    unsigned char *Hb = smem + a.l_H;
+    float *clampL = reinterpret_cast<float *>(smem + a.l_clamp);
+    uint8_t *givenL = smem + a.l_given;
+    float *fireL = reinterpret_cast<float *>(smem + a.l_fire);
+    float *confL = reinterpret_cast<float *>(smem + a.l_conf);
+    int *firedL = reinterpret_cast<int *>(smem + a.l_fired);
+    float *headL = reinterpret_cast<float *>(smem + a.l_head);
+    const int c_in = a.c_in, in_off = a.in_off;
+
+    // ---- weights: stencil kernels (uniform), biases, MFMA fragments in registers
+    const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
+    float kw[4][9];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < 9; ++t) kw[k][t] = kern[k * 9 + t];
+
+    const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
+    const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
+    fr_t w1f[S::MT1][S::KT1];
+    f32x4 b1v[S::MT1];
+#pragma unroll
+    for (int mt = 0; mt < S::MT1; ++mt) {
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt) {
+            const size_t idx = ((size_t)(wave * S::MT1 + mt) * S::KT1 + kt) * 64 + lane;
+            w1f[mt][kt] = reinterpret_cast<const fr_t *>(a.packed + a.off_w1)[idx];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[wave * S::HPW + 16 * mt + 4 * g + v];
+    }
+    fr_t w2f[S::MT2W][S::KT2];
+    f32x4 b2v[S::MT2W];
+#pragma unroll
+    for (int j = 0; j < S::MT2W; ++j) {
+        const int mt2 = wave + S::NW * j;
+#pragma unroll
+        for (int kt = 0; kt < S::KT2; ++kt) {
+            const size_t idx = ((size_t)(mt2 < S::MT2 ? mt2 : 0) * S::KT2 + kt) * 64 + lane;
+            w2f[j][kt] = reinterpret_cast<const fr_t *>(a.packed + a.off_w2)[idx];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) b2v[j][v] = mt2 < S::MT2 ? b2[16 * mt2 + 4 * g + v] : 0.0f;
+    }
+
+    // ---- load rows: state, clamp, given, head weights; halo of both perception buffers
+    auto pidx = [&](int buf, int r, int pi) { return ((buf * Rcap + r) * HWp + pi) * S::CP; };
+    for (int e = tid; e < Rw * C * HWn; e += S::NT) {
+        const int r = e / (C * HWn), rem = e - r * C * HWn, c = rem / HWn, q = rem - c * HWn;
+        const float v = a.x_in[rbase * C * HWn + e];
+        const int i = q / W, j = q - i * W;
+        const int pe = pidx(0, r, (i + 1) * Wp + (j + 1)) + c;
+        if constexpr (BF16) {
+            M[(r * HWn + q) * S::MP + c] = v;
+            reinterpret_cast<__bf16 *>(Pb)[pe] = (__bf16)v;
+        } else {
+            reinterpret_cast<float *>(Pb)[pe] = v;
+        }
+    }
+    for (int e = tid; e < Rw * c_in * HWn; e += S::NT) {
+        const int r = e / (c_in * HWn), rem = e - r * c_in * HWn, ci = rem / HWn, q = rem - ci * HWn;
+        clampL[(r * HWn + q) * c_in + ci] = a.clamp[rbase * c_in * HWn + e];
+    }
+    for (int e = tid; e < Rw * HWn; e += S::NT) givenL[e] = a.given[rbase * HWn + e];
+    for (int e = tid; e < Rcap; e += S::NT) firedL[e] = 0;
+    {
+        const float *hw = reinterpret_cast<const float *>(a.packed + a.off_headw);
+        const float *hb = reinterpret_cast<const float *>(a.packed + a.off_headb);
+        const int nw = a.n_out * a.c_out;
+        for (int e = tid; e < nw + a.n_out; e += S::NT) headL[e] = e < nw ? hw[e] : hb[e - nw];
+    }
+    const int nhalo = 2 * Wp + 2 * H;
+    auto halo_cell = [&](int h, int &ip, int &jp) {
+        if (h < Wp) {
+            ip = 0;
+            jp = h;
+        } else if (h < 2 * Wp) {
+            ip = H + 1;
+            jp = h - Wp;
+        } else if (h < 2 * Wp + H) {
+            ip = h - 2 * Wp + 1;
+            jp = 0;
+        } else {
+            ip = h - 2 * Wp - H + 1;
+            jp = W + 1;
+        }
+    };
+    if (a.padding != 2) {  // wall / zero: constant halo in both buffers
+        const float *padv = reinterpret_cast<const float *>(a.packed + a.off_padv);
+        for (int e = tid; e < 2 * Rw * nhalo * C; e += S::NT) {
+            const int c = e % C, rest = e / C, h = rest % nhalo, rb = rest / nhalo;
+            const int r = rb % Rw, buf = rb / Rw;
+            int ip, jp;
+            halo_cell(h, ip, jp);
+            const float v = a.padding == 1 ? padv[c] : 0.0f;
+            const int pe = pidx(buf, r, ip * Wp + jp) + c;
+            if constexpr (BF16)
+                reinterpret_cast<__bf16 *>(Pb)[pe] = (__bf16)v;
+            else
+                reinterpret_cast<float *>(Pb)[pe] = v;
+        }
+    }
+    __syncthreads();
+    auto wrap_halo = [&](int buf) {
+        for (int e = tid; e < Rw * nhalo * (C / 4); e += S::NT) {
+            const int qd = e % (C / 4), rest = e / (C / 4), h = rest % nhalo, r = rest / nhalo;
+            int ip, jp;
+            halo_cell(h, ip, jp);
+            const int si = (ip - 1 + H) % H, sj = (jp - 1 + W) % W;
+            float v[4];
+            lds_load4<BF16>(Pb, pidx(buf, r, (si + 1) * Wp + sj + 1) + 4 * qd, v);
+            lds_store4<BF16>(Pb, pidx(buf, r, ip * Wp + jp) + 4 * qd, v);
+        }
+    };
+    if (a.padding == 2) {
+        wrap_halo(0);
+        __syncthreads();
+    }
+
+    // fp32 state of a cell (for readout): M in bf16 mode, the perception buffer in fp32 mode
+    auto state_ptr = [&](int buf, int cell) -> const float * {
+        if constexpr (BF16) {
+            return M + cell * S::MP;
+        } else {
+            const int r = cell / HWn, q = cell - r * HWn, i = q / W, j = q - i * W;
+            return reinterpret_cast<const float *>(Pb) + pidx(buf, r, (i + 1) * Wp + j + 1);
+        }
+    };
+
+    int cur = 0;
+    const int nq = (HWn + 3) >> 2;
+    for (int s = 0; s < a.n_steps; ++s) {
+        // ---- phase A: fire mask of every cell of the workgroup
+        for (int it = tid; it < Rw * nq; it += S::NT) {
+            const int r = it / nq, qq = it - r * nq;
+            float u[4] = {0.f, 0.f, 0.f, 0.f};
+            if (!a.fire_u8 && !a.fire_f32) {
+                const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
+                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s),
+                               (uint32_t)qq, u);
+            }
+            int cnt = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int q = 4 * qq + e;
+                if (q >= HWn) break;
+                const int cell = r * HWn + q;
+                float f;
+                if (a.fire_u8) {
+                    f = a.fire_u8[((int64_t)s * a.rows + rbase + r) * HWn + q] ? 1.0f : 0.0f;
+                } else if (a.fire_f32) {
+                    f = a.fire_f32[(rbase + r) * HWn + q];
+                } else {
+                    float pc = a.p;
+                    if (a.adaptive) {
+                        int am;
+                        const float cf = cell_readout(state_ptr(cur, cell) + a.out_off, 1, a.c_out,
+                                                      a.n_out, a.head_kind, headL,
+                                                      headL + a.n_out * a.c_out, &am);
+                        const bool confident = cf > a.tau || (a.given_confident && givenL[cell]);
+                        if (confident) pc = a.p_low;
+                    }
+                    f = u[e] < pc ? 1.0f : 0.0f;
+                }
+                fireL[cell] = f;
+                cnt += f != 0.0f;
+            }
+            if (cnt) atomicAdd(&firedL[r], cnt);
+        }
+        __syncthreads();
+
+        // ---- phase B: tiles of 16 cells
+        const int nxt = cur ^ 1;
+        for (int tile = 0; tile < ntile; ++tile) {
+            // stencil -> Z
+            if (tid < 16 * (C / 4)) {
+                const int n = tid & 15, qd = tid >> 4;
+                const int gc = tile * 16 + n;
+                float acc[4][4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
+                if (gc < ncell) {
+                    const int r = gc / HWn, q = gc - r * HWn, i = q / W, j = q - i * W;
+                    const int pc = pidx(cur, r, (i + 1) * Wp + (j + 1)) + 4 * qd;
+#pragma unroll
+                    for (int dy = -1; dy <= 1; ++dy)
+#pragma unroll
+                        for (int dx = -1; dx <= 1; ++dx) {
+                            float v[4];
+                            lds_load4<BF16>(Pb, pc + (dy * Wp + dx) * S::CP, v);
+                            const int t = (dy + 1) * 3 + (dx + 1);
+#pragma unroll
+                            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                                for (int c = 0; c < 4; ++c) acc[k][c] = __builtin_fmaf(kw[k][t], v[c], acc[k][c]);
+                        }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) lds_store4<BF16>(Zb, n * S::ZS + k * C + 4 * qd, acc[k]);
+            }
+            __syncthreads();
+
+            // fc1: h^T = relu(W1 z^T + b1) for this wave's hidden units -> H
+            {
+                f32x4 acc[S::MT1];
+#pragma unroll
+                for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt) {
+                    const fr_t bfrag = FR::load_lds(Zb, l16 * S::ZS + kt * S::KT + (BF16 ? 8 * g : g));
+#pragma unroll
+                    for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = FR::mfma(w1f[mt][kt], bfrag, acc[mt]);
+                }
+#pragma unroll
+                for (int mt = 0; mt < S::MT1; ++mt) {
+                    float h[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) h[v] = acc[mt][v] > 0.0f ? acc[mt][v] : 0.0f;
+                    lds_store4<BF16>(Hb, l16 * S::HS + wave * S::HPW + 16 * mt + 4 * g, h);
+                }
+            }
+            __syncthreads();
+
+            // fc2 + residual update + clamp for this wave's output channels
+#pragma unroll
+            for (int jj = 0; jj < S::MT2W; ++jj) {
+                const int mt2 = wave + S::NW * jj;
+                if (mt2 < S::MT2) {
+                    f32x4 acc2 = b2v[jj];
+#pragma unroll
+                    for (int kt = 0; kt < S::KT2; ++kt) {
+                        const fr_t bfrag = FR::load_lds(Hb, l16 * S::HS + kt * S::KT + (BF16 ? 8 * g : g));
+                        acc2 = FR::mfma(w2f[jj][kt], bfrag, acc2);
+                    }
+                    const int gc = tile * 16 + l16;
+                    if (gc < ncell) {
+                        const int c0 = 16 * mt2 + 4 * g;
+                        const int r = gc / HWn, q = gc - r * HWn, i = q / W, j = q - i * W;
+                        const int pi = (i + 1) * Wp + j + 1;
+                        float xo[4];
+                        if constexpr (BF16) {
+                            const float4 m4 = *reinterpret_cast<const float4 *>(M + gc * S::MP + c0);
+                            xo[0] = m4.x;
+                            xo[1] = m4.y;
+                            xo[2] = m4.z;
+                            xo[3] = m4.w;
+                        } else {
+                            lds_load4<false>(Pb, pidx(cur, r, pi) + c0, xo);
+                        }
+                        const float f = fireL[gc];
+                        const bool gv = givenL[gc] != 0;
+                        float u[4];
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) {
+                            const float dxv = BF16 ? round_bf16(acc2[v]) : acc2[v];
+                            u[v] = __fadd_rn(xo[v], __fmul_rn(f, dxv));
+                            if (a.noise) u[v] = __fadd_rn(u[v], a.noise[((rbase + r) * C + c0 + v) * HWn + q]);
+                            const int c = c0 + v;
+                            if (gv && c >= in_off && c < in_off + c_in) u[v] = clampL[gc * c_in + (c - in_off)];
+                        }
+                        if constexpr (BF16)
+                            *reinterpret_cast<float4 *>(M + gc * S::MP + c0) = make_float4(u[0], u[1], u[2], u[3]);
+                        lds_store4<BF16>(Pb, pidx(nxt, r, pi) + c0, u);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (a.padding == 2) {
+            wrap_halo(nxt);
+            __syncthreads();
+        }
+        cur = nxt;
+    }
+
+    // ---- write back the state, the board confidence and the fired counts
+    for (int e = tid; e < Rw * C * HWn; e += S::NT) {
+        const int r = e / (C * HWn), rem = e - r * C * HWn, c = rem / HWn, q = rem - c * HWn;
+        a.x_out[rbase * C * HWn + e] = state_ptr(cur, r * HWn + q)[c];
+    }
+    if (a.conf_out) {
+        for (int cell = tid; cell < ncell; cell += S::NT) {
+            int am;
+            confL[cell] = cell_readout(state_ptr(cur, cell) + a.out_off, 1, a.c_out, a.n_out,
+                                       a.head_kind, headL, headL + a.n_out * a.c_out, &am);
+        }
+        __syncthreads();
+        for (int r = tid; r < Rw; r += S::NT) {
+            float sum = 0.0f;
+            for (int q = 0; q < HWn; ++q) sum = __fadd_rn(sum, confL[r * HWn + q]);
+            a.conf_out[rbase + r] = __fdiv_rn(sum, (float)HWn);
+        }
+    }
+    if (a.fired_out)
+        for (int r = tid; r < Rw; r += S::NT) a.fired_out[rbase + r] = firedL[r];
+}
+
+}  // namespace nca

