@@ -136,6 +136,11 @@ const char *nca_last_error(void);
 /* ABI version (major * 100 + minor). */
 int nca_version(void);
 
+/* Kernel selection for bf16 rollouts: 0 = automatic (the streamed kernel where the grid allows
+ * it), 1 = always the generic kernel. Process-wide; used by the tests to check both paths
+ * against each other. No counterpart in the reference. */
+int nca_set_kernel_path(int path);
+
 #ifdef __cplusplus
 }
 #endif

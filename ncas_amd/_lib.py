@@ -28,6 +28,7 @@ EXPORTS = (
     "nca_conf_select",
     "nca_last_error",
     "nca_version",
+    "nca_set_kernel_path",
 )
 
 
@@ -106,6 +107,7 @@ def load():
     L.nca_conf_select.argtypes = [vp, vp, i32, i32, i32, vp, vp]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
+    L.nca_set_kernel_path.argtypes = [ctypes.c_int]
     for name in EXPORTS:
         getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     _lib = L

@@ -7,10 +7,11 @@
 #include <stdio.h>
 #include <string.h>
 
-#include "../../include/nca_hip.h"
+#include "nca_hip.h"
 #include "nca_device.h"
 #include "nca_layout.h"
 #include "nca_rollout.h"
+#include "nca_rollout_stream.h"
 
 namespace {
 
@@ -33,6 +34,9 @@ int hip_check(hipError_t e, const char *what) {
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
 
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per workgroup
+
+// Test hook: route bf16 rollouts to the generic kernel (nca_set_kernel_path).
+int g_force_generic = 0;
 
 bool shape_supported(int C, int hidden) {
     return (C == 16 && hidden == 128) || (C == 32 && hidden == 256) || (C == 64 && hidden == 256);
@@ -96,6 +100,19 @@ __global__ void pack_frags(const float *src, int M, int K, int bf16, void *dst) 
             k = kt * 4 + (lane >> 4);
             reinterpret_cast<float *>(dst)[e] = src[(size_t)m * K + k];
         }
+    }
+}
+
+// fc2 fragments for the wave-specialised kernel (see nca_layout.h), bf16.
+__global__ void pack_w2k(const float *w2, int C, int HD, __bf16 *dst) {
+    const int hpw = HD / 4, kt2n = hpw / 32, mt2n = C / 16;
+    const int total = C * HD;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
+        const int kt = blk % kt2n, m2 = (blk / kt2n) % mt2n, q = blk / (kt2n * mt2n);
+        const int ch = 16 * m2 + (lane & 15);
+        const int hid = q * hpw + 16 * (2 * kt + s / 4) + 4 * (lane >> 4) + (s % 4);
+        dst[e] = (__bf16)w2[(size_t)ch * HD + hid];
     }
 }
 
@@ -200,7 +217,7 @@ struct Plan {
     int R;
 };
 
-template <int C, int HD, bool BF16>
+template <int C, int HD, bool BF16, bool NOISE>
 int launch_rollout(nca::RolloutParams p, hipStream_t st) {
     int R = (int)((p.rows + 255) / 256);
     if (R < 1) R = 1;
@@ -224,7 +241,8 @@ int launch_rollout(nca::RolloutParams p, hipStream_t st) {
     p.l_conf = L.conf;
     p.l_fired = L.fired;
     p.l_head = L.head;
-    auto kfn = nca::rollout_resident<C, HD, BF16>;
+    p.l_cinfo = L.cinfo;
+    auto kfn = nca::rollout_resident<C, HD, BF16, NOISE>;
     int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total),
                        "hipFuncSetAttribute");
@@ -234,14 +252,64 @@ int launch_rollout(nca::RolloutParams p, hipStream_t st) {
     return hip_check(hipGetLastError(), "rollout launch");
 }
 
-int dispatch_rollout(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
+// Streamed bf16 kernel: two row groups per workgroup; needs W + 1 <= 16 (single perception
+// buffer).
+template <int C, int HD>
+int launch_stream(const nca::RolloutParams &p, hipStream_t st, bool *used) {
+    *used = false;
+    if (p.W + 1 > 16 || p.noise || p.fire_f32) return NCA_OK;
+    int rg = (int)((p.rows + 511) / 512);
+    if (rg > 8) rg = 8;
+    if (rg < 1) rg = 1;
+    nca::StPlan L{};
+    for (; rg >= 1; --rg) {
+        L = nca::st_plan<C, HD>(rg, p.H, p.W, p.c_out, p.n_out);
+        if (L.total <= kLdsBytes) break;
+    }
+    if (rg < 1) return NCA_OK;
+    nca::StParams sp;
+    sp.a = p;
+    sp.rg = rg;
+    sp.l_P = L.P;
+    sp.l_M = L.M;
+    sp.l_Z = L.Z;
+    sp.l_D = L.D;
+    sp.l_given = L.given;
+    sp.l_fire = L.fire;
+    sp.l_fired = L.fired;
+    sp.l_head = L.head;
+    sp.l_cinfo = L.cinfo;
+    sp.l_conf = L.conf;
+    sp.l_trash = L.trash;
+    sp.off_w2k = p.off_w2k;
+    auto kfn = nca::rollout_stream<C, HD>;
+    int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total),
+                       "hipFuncSetAttribute");
+    if (rc) return rc;
+    const int64_t grid = (p.rows + 2 * rg - 1) / (2 * rg);
+    hipLaunchKernelGGL(kfn, dim3((unsigned)grid), dim3(256), L.total, st, sp);
+    *used = true;
+    return hip_check(hipGetLastError(), "rollout launch");
+}
+
+template <int C, int HD>
+int launch_cell(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
     const bool bf = d->precision == NCA_BF16;
-    if (d->channels == 16 && d->hidden == 128)
-        return bf ? launch_rollout<16, 128, true>(p, st) : launch_rollout<16, 128, false>(p, st);
-    if (d->channels == 32 && d->hidden == 256)
-        return bf ? launch_rollout<32, 256, true>(p, st) : launch_rollout<32, 256, false>(p, st);
-    if (d->channels == 64 && d->hidden == 256)
-        return bf ? launch_rollout<64, 256, true>(p, st) : launch_rollout<64, 256, false>(p, st);
+    if (bf && !g_force_generic) {
+        bool used = false;
+        const int rc = launch_stream<C, HD>(p, st, &used);
+        if (rc || used) return rc;
+    }
+    if (p.noise)
+        return bf ? launch_rollout<C, HD, true, true>(p, st) : launch_rollout<C, HD, false, true>(p, st);
+    return bf ? launch_rollout<C, HD, true, false>(p, st) : launch_rollout<C, HD, false, false>(p, st);
+}
+
+int dispatch_rollout(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
+    if (d->channels == 16 && d->hidden == 128) return launch_cell<16, 128>(d, p, st);
+    if (d->channels == 32 && d->hidden == 256) return launch_cell<32, 256>(d, p, st);
+    if (d->channels == 64 && d->hidden == 256) return launch_cell<64, 256>(d, p, st);
     return fail(NCA_ERR_UNSUPPORTED, "cell C=%d hidden=%d", d->channels, d->hidden);
 }
 
@@ -269,6 +337,7 @@ nca::RolloutParams base_params(const nca_cell_desc *d, const void *packed, int64
     p.off_padv = (unsigned)L.padv;
     p.off_w1 = (unsigned)L.w1;
     p.off_w2 = (unsigned)L.w2;
+    p.off_w2k = (unsigned)L.w2k;
     return p;
 }
 
@@ -285,6 +354,12 @@ extern "C" {
 const char *nca_last_error(void) { return g_err; }
 
 int nca_version(void) { return 100; }
+
+int nca_set_kernel_path(int path) {
+    if (path != 0 && path != 1) return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic)", path);
+    g_force_generic = path;
+    return NCA_OK;
+}
 
 size_t nca_packed_weights_bytes(const nca_cell_desc *cell) {
     if (check_cell(cell)) return 0;
@@ -315,6 +390,8 @@ int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void 
     hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->pad_vec, C, reinterpret_cast<float *>(pk + L.padv), 0);
     hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, (int)bf, (void *)(pk + L.w1));
     hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w2, C, HD, (int)bf, (void *)(pk + L.w2));
+    if (bf)
+        hipLaunchKernelGGL(pack_w2k, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2k));
     return hip_check(hipGetLastError(), "pack launch");
 }
 

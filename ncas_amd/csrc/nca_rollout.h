@@ -1,28 +1,37 @@
 // The LDS-resident multi-step rollout kernel (gfx950).
 //
 // One workgroup of 4 waves owns `rows_per_wg` rows (rollouts) for the whole call: their states
-// are loaded from HBM once, advanced `n_steps` steps inside LDS, and written back once. One
-// step of the reference cell (src/nca/model.py:503-559) is, per 16-cell tile:
+// are loaded from HBM once, advanced `n_steps` steps inside LDS and written back once. One step
+// of the reference cell (src/nca/model.py:503-559) is computed over tiles of 16 cells:
 //
-//   stencil  all 256 lanes: z[cell][k*C + c] = sum_taps kern[k][tap] * P[nbr(cell, tap)][c]
-//            from the perception buffer P (LDS, 1-cell halo, bf16 or fp32), into Z (LDS);
+//   stencil  all lanes: z[cell][k*C + c] = sum_taps kern[k][tap] * P[nbr(cell, tap)][c] from
+//            the perception buffer P (LDS, 1-cell halo) into Z (LDS). bf16 cells use
+//            v_dot2_f32_bf16 on tap pairs; fp32 cells use fp32 FMAs.
 //   fc1      wave w owns hidden units [w*HD/4, (w+1)*HD/4): h^T = W1 z^T on MFMA with its W1
-//            fragments resident in registers (A operand), z^T read from Z as the B operand;
-//            bias + ReLU (+ bf16 rounding) fused, h written to H (LDS);
-//   fc2      wave w owns output channels [16w, 16w+16) (C / 16 m-tiles spread over the waves):
-//            dx^T = W2 h^T on MFMA with register-resident W2 fragments;
+//            fragments resident in registers (A operand) and z^T read from Z (B operand); bias
+//            (accumulator init) and ReLU fused, h written to H (LDS).
+//   fc2      wave w owns output channels [16w, 16w+16) (C/16 m-tiles spread over the waves):
+//            dx^T = W2 h^T with register-resident W2 fragments.
 //   update   in the fc2 accumulator layout (lane: 4 consecutive channels of one cell):
-//            u = x + fire * dx (+ noise), clamp of the given cells' input slice, written to the
-//            fp32 state and to the other perception buffer (ping-pong across steps).
+//            u = x + fire * dx (+ noise); input-slice channels of given cells are frozen at
+//            their clamp value; written to the fp32 state and the other perception buffer.
 //
-// The fire mask of a step is drawn once per step for all cells (Philox, or read from an
-// injected mask); adaptive firing reads the pre-step confidence first. With wrap padding the
-// halo of the new perception buffer is refreshed after each step; wall / zero halos are
-// constant. The board confidence of the final state is computed in-kernel.
+// Software pipeline: Z and H are double-buffered so that one barrier interval holds fc2 and the
+// update of tile t-1, fc1 of tile t and the stencil of tile t+1 - MFMA and VALU work of the same
+// wave that the hardware overlaps - with a single workgroup barrier per tile.
+//
+// The fire mask of a step is drawn once for all cells (Philox, or read from injected masks);
+// adaptive firing reads the pre-step confidence first. With wrap padding the halo of the new
+// perception buffer is refreshed after each step; wall / zero halos are constant. The board
+// confidence of the final state is computed in-kernel.
+//
+// Clamp: the first step of a launch resets the input slice of given cells to the clamp values
+// (model.py:430-438); the state then holds exactly those values, so later steps keep them by
+// not updating those channels, which is bitwise the same as clamping again.
 //
 // Precision: BF16 reproduces bf16 autocast (perception input, z, h, dx rounded to bf16, fp32
-// accumulation, fp32 state held in a separate fp32 buffer M); fp32 keeps everything fp32 and
-// uses v_mfma_f32_16x16x4_f32 (the perception buffer is then the state itself).
+// accumulation, fp32 state in a separate buffer M); fp32 keeps everything fp32 and uses
+// v_mfma_f32_16x16x4_f32 (the perception buffer is then the state itself).
 #pragma once
 
 #include "nca_device.h"
@@ -51,8 +60,8 @@ struct RolloutParams {
     float p, p_low, tau;
     int adaptive, given_confident;
     int rows_per_wg;
-    unsigned off_kern, off_b1, off_b2, off_headw, off_headb, off_padv, off_w1, off_w2;
-    unsigned l_P, l_M, l_Z, l_H, l_clamp, l_given, l_fire, l_conf, l_fired, l_head;
+    unsigned off_kern, off_b1, off_b2, off_headw, off_headb, off_padv, off_w1, off_w2, off_w2k;
+    unsigned l_P, l_M, l_Z, l_H, l_clamp, l_given, l_fire, l_conf, l_fired, l_head, l_cinfo;
 };
 
 template <int C, int HD, bool BF16>
@@ -73,14 +82,17 @@ struct Shape {
     static constexpr int MP = C + 4;        // M channel stride (floats)
     static constexpr int ZS = F + (BF16 ? 8 : 4);   // Z row stride (elements)
     static constexpr int HS = HD + (BF16 ? 8 : 4);  // H row stride (elements)
+    static constexpr int ZBUF = 16 * ZS;    // elements per Z buffer
+    static constexpr int HBUF = 16 * HS;    // elements per H buffer
+    static constexpr int NSI = 16 * (C / 4);  // stencil items per tile (16 cells x C/4 quads)
     static_assert(HD % 64 == 0, "hidden must be a multiple of 64");
     static_assert(C % 16 == 0 && C <= 64, "channels must be 16, 32, 48 or 64");
-    static_assert(16 * (C / 4) <= NT, "stencil items exceed the workgroup");
+    static_assert(NSI <= NT, "stencil items exceed the workgroup");
 };
 
 // LDS plan for R rows of an H x W grid.
 struct LdsPlan {
-    unsigned P, M, Z, H, clamp, given, fire, conf, fired, head, total;
+    unsigned P, M, Z, H, clamp, given, fire, conf, fired, head, cinfo, total;
 };
 
 template <int C, int HD, bool BF16>
@@ -95,9 +107,9 @@ inline LdsPlan lds_plan(int R, int H, int W, int c_in, int c_out, int n_out) {
     p.M = o;
     o = al(o + (BF16 ? (unsigned)R * hw * S::MP * 4u : 0u));
     p.Z = o;
-    o = al(o + 16u * S::ZS * S::ES);
+    o = al(o + 2u * S::ZBUF * S::ES);
     p.H = o;
-    o = al(o + 16u * S::HS * S::ES);
+    o = al(o + 2u * S::HBUF * S::ES);
     p.clamp = o;
     o = al(o + (unsigned)R * hw * c_in * 4u);
     p.given = o;
@@ -110,11 +122,12 @@ inline LdsPlan lds_plan(int R, int H, int W, int c_in, int c_out, int n_out) {
     o = al(o + (unsigned)R * 4u);
     p.head = o;
     o = al(o + (unsigned)(n_out * c_out + n_out) * 4u);
+    p.cinfo = o;
+    o = al(o + (unsigned)R * hw * 4u);
     p.total = o;
     return p;
 }
 
-// 4 consecutive elements of P / Z / H as floats.
 template <bool BF16>
 __device__ __forceinline__ void lds_load4(const unsigned char *base, int elem, float v[4]) {
     if constexpr (BF16) {
@@ -167,7 +180,9 @@ struct Frag<false> {
     }
 };
 
-template <int C, int HD, bool BF16>
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t u) { return __builtin_bit_cast(bf16x2, u); }
+
+template <int C, int HD, bool BF16, bool NOISE>
 __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
     using S = Shape<C, HD, BF16>;
     using FR = Frag<BF16>;
@@ -182,6 +197,7 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
     const int Rw = (int)((a.rows - rbase) < Rcap ? (a.rows - rbase) : Rcap);
     const int ncell = Rw * HWn;
     const int ntile = (ncell + 15) >> 4;
+    const int PBUF = Rcap * HWp * S::CP;  // elements per perception buffer
 
     unsigned char *Pb = smem + a.l_P;
     float *M = reinterpret_cast<float *>(smem + a.l_M);
@@ -193,16 +209,26 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
     float *confL = reinterpret_cast<float *>(smem + a.l_conf);
     int *firedL = reinterpret_cast<int *>(smem + a.l_fired);
     float *headL = reinterpret_cast<float *>(smem + a.l_head);
+    int *cinfo = reinterpret_cast<int *>(smem + a.l_cinfo);  // P centre element of cell g
     const int c_in = a.c_in, in_off = a.in_off;
 
-    // ---- weights: stencil kernels (uniform), biases, MFMA fragments in registers
+    // ---- stencil kernels: bf16 tap pairs (bf16 cells) or floats (fp32 cells), uniform
     const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
     float kw[4][9];
+    uint32_t kp[4][5];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 4; ++k) {
 #pragma unroll
         for (int t = 0; t < 9; ++t) kw[k][t] = kern[k * 9 + t];
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) kp[k][pr] = pack_bf16x2(kw[k][2 * pr], kw[k][2 * pr + 1]);
+        kp[k][4] = pack_bf16x2(kw[k][8], 0.0f);
+    }
+    int toff[9];  // tap offsets in P elements, tap = (dy + 1) * 3 + (dx + 1)
+#pragma unroll
+    for (int t = 0; t < 9; ++t) toff[t] = ((t / 3 - 1) * Wp + (t % 3 - 1)) * S::CP;
 
+    // ---- MFMA fragments and biases in registers
     const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
     const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
     fr_t w1f[S::MT1][S::KT1];
@@ -219,6 +245,7 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
     }
     fr_t w2f[S::MT2W][S::KT2];
     f32x4 b2v[S::MT2W];
+    bool inslice[S::MT2W][4];
 #pragma unroll
     for (int j = 0; j < S::MT2W; ++j) {
         const int mt2 = wave + S::NW * j;
@@ -228,16 +255,22 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             w2f[j][kt] = reinterpret_cast<const fr_t *>(a.packed + a.off_w2)[idx];
         }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) b2v[j][v] = mt2 < S::MT2 ? b2[16 * mt2 + 4 * g + v] : 0.0f;
+        for (int v = 0; v < 4; ++v) {
+            const int c = 16 * mt2 + 4 * g + v;
+            b2v[j][v] = mt2 < S::MT2 ? b2[c] : 0.0f;
+            inslice[j][v] = c >= in_off && c < in_off + c_in;
+        }
     }
 
-    // ---- load rows: state, clamp, given, head weights; halo of both perception buffers
-    auto pidx = [&](int buf, int r, int pi) { return ((buf * Rcap + r) * HWp + pi) * S::CP; };
+    // ---- load rows: state, clamp, given, head weights, cell table; halos
+    auto pcen = [&](int r, int q) {  // P centre element (buffer 0) of cell q of row r
+        const int i = q / W, j = q - i * W;
+        return (r * HWp + (i + 1) * Wp + (j + 1)) * S::CP;
+    };
     for (int e = tid; e < Rw * C * HWn; e += S::NT) {
         const int r = e / (C * HWn), rem = e - r * C * HWn, c = rem / HWn, q = rem - c * HWn;
         const float v = a.x_in[rbase * C * HWn + e];
-        const int i = q / W, j = q - i * W;
-        const int pe = pidx(0, r, (i + 1) * Wp + (j + 1)) + c;
+        const int pe = pcen(r, q) + c;
         if constexpr (BF16) {
             M[(r * HWn + q) * S::MP + c] = v;
             reinterpret_cast<__bf16 *>(Pb)[pe] = (__bf16)v;
@@ -249,7 +282,11 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
         const int r = e / (c_in * HWn), rem = e - r * c_in * HWn, ci = rem / HWn, q = rem - ci * HWn;
         clampL[(r * HWn + q) * c_in + ci] = a.clamp[rbase * c_in * HWn + e];
     }
-    for (int e = tid; e < Rw * HWn; e += S::NT) givenL[e] = a.given[rbase * HWn + e];
+    for (int e = tid; e < ncell; e += S::NT) {
+        givenL[e] = a.given[rbase * HWn + e];
+        const int r = e / HWn;
+        cinfo[e] = pcen(r, e - r * HWn);
+    }
     for (int e = tid; e < Rcap; e += S::NT) firedL[e] = 0;
     {
         const float *hw = reinterpret_cast<const float *>(a.packed + a.off_headw);
@@ -281,7 +318,7 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             int ip, jp;
             halo_cell(h, ip, jp);
             const float v = a.padding == 1 ? padv[c] : 0.0f;
-            const int pe = pidx(buf, r, ip * Wp + jp) + c;
+            const int pe = buf * PBUF + (r * HWp + ip * Wp + jp) * S::CP + c;
             if constexpr (BF16)
                 reinterpret_cast<__bf16 *>(Pb)[pe] = (__bf16)v;
             else
@@ -296,8 +333,8 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             halo_cell(h, ip, jp);
             const int si = (ip - 1 + H) % H, sj = (jp - 1 + W) % W;
             float v[4];
-            lds_load4<BF16>(Pb, pidx(buf, r, (si + 1) * Wp + sj + 1) + 4 * qd, v);
-            lds_store4<BF16>(Pb, pidx(buf, r, ip * Wp + jp) + 4 * qd, v);
+            lds_load4<BF16>(Pb, buf * PBUF + (r * HWp + (si + 1) * Wp + sj + 1) * S::CP + 4 * qd, v);
+            lds_store4<BF16>(Pb, buf * PBUF + (r * HWp + ip * Wp + jp) * S::CP + 4 * qd, v);
         }
     };
     if (a.padding == 2) {
@@ -310,22 +347,180 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
         if constexpr (BF16) {
             return M + cell * S::MP;
         } else {
-            const int r = cell / HWn, q = cell - r * HWn, i = q / W, j = q - i * W;
-            return reinterpret_cast<const float *>(Pb) + pidx(buf, r, (i + 1) * Wp + j + 1);
+            return reinterpret_cast<const float *>(Pb) + buf * PBUF + cinfo[cell];
         }
     };
 
-    int cur = 0;
+    // ---- pipeline stages ------------------------------------------------------------------
+    const int st_n = tid & 15, st_qd = tid >> 4;
+
+    // centre offset of this lane's stencil cell in tile t (padding cells read a valid cell;
+    // their features are never used)
+    auto stencil_pc = [&](int t) {
+        const int gq = t * 16 + st_n;
+        return cinfo[gq < ncell ? gq : ncell - 1];
+    };
+    // stencil of a tile (this lane's cell centre pc) from perception buffer `cur` into Z buffer zb
+    auto stencil = [&](int pc, int zb, int cur) {
+        if constexpr (S::NSI < S::NT) {
+            if (tid >= S::NSI) return;  // whole waves (NSI is a multiple of 64)
+        }
+        const int base = cur * PBUF + pc + 4 * st_qd;
+        float acc[4][4];
+        if constexpr (BF16) {
+            uint2 nb[9];
+#pragma unroll
+            for (int t9 = 0; t9 < 9; ++t9) nb[t9] = *reinterpret_cast<const uint2 *>(Pb + 2 * (base + toff[t9]));
+            uint32_t pr[5][4];  // [tap pair][channel]: (bf16 of tap 2p, bf16 of tap 2p+1)
+#pragma unroll
+            for (int p2 = 0; p2 < 4; ++p2) {
+                const uint2 x0 = nb[2 * p2], x1 = nb[2 * p2 + 1];
+                pr[p2][0] = __builtin_amdgcn_perm(x1.x, x0.x, 0x05040100u);
+                pr[p2][1] = __builtin_amdgcn_perm(x1.x, x0.x, 0x07060302u);
+                pr[p2][2] = __builtin_amdgcn_perm(x1.y, x0.y, 0x05040100u);
+                pr[p2][3] = __builtin_amdgcn_perm(x1.y, x0.y, 0x07060302u);
+            }
+            pr[4][0] = nb[8].x & 0xffffu;
+            pr[4][1] = nb[8].x >> 16;
+            pr[4][2] = nb[8].y & 0xffffu;
+            pr[4][3] = nb[8].y >> 16;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int p2 = 0; p2 < 5; ++p2)
+                        s = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), s, false);
+                    acc[k][c] = s;
+                }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
+#pragma unroll
+            for (int t9 = 0; t9 < 9; ++t9) {
+                float v[4];
+                lds_load4<false>(Pb, base + toff[t9], v);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[k][c] = __builtin_fmaf(kw[k][t9], v[c], acc[k][c]);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) lds_store4<BF16>(Zb, zb * S::ZBUF + st_n * S::ZS + k * C + 4 * st_qd, acc[k]);
+    };
+
+    // fc1 of the tile in Z buffer zb -> H buffer hb
+    auto fc1 = [&](int zb, int hb) {
+        fr_t zf[S::KT1];
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt)
+            zf[kt] = FR::load_lds(Zb, zb * S::ZBUF + l16 * S::ZS + kt * S::KT + (BF16 ? 8 * g : g));
+        f32x4 acc[S::MT1];
+#pragma unroll
+        for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt)
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = FR::mfma(w1f[mt][kt], zf[kt], acc[mt]);
+#pragma unroll
+        for (int mt = 0; mt < S::MT1; ++mt) {
+            float h[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) h[v] = acc[mt][v] > 0.0f ? acc[mt][v] : 0.0f;
+            lds_store4<BF16>(Hb, hb * S::HBUF + l16 * S::HS + wave * S::HPW + 16 * mt + 4 * g, h);
+        }
+    };
+
+    // per-lane cell of the update of tile t: (cell, centre offset, fire, given)
+    struct Upd {
+        int gq, gc, pc;
+        float f;
+        bool gv;
+    };
+    auto upd_info = [&](int t) {
+        Upd u;
+        u.gq = t * 16 + l16;
+        u.gc = u.gq < ncell ? u.gq : ncell - 1;
+        u.pc = cinfo[u.gc];
+        u.f = fireL[u.gc];
+        u.gv = givenL[u.gc] != 0;
+        return u;
+    };
+    // fc2 + update of one tile (H buffer hb), state buffers cur -> nxt. Input-slice channels of
+    // given cells keep their value (the first step's clamp is applied by clamp_pass). With
+    // `full` the tile has no padding cells and the stores are unconditional.
+    auto fc2_update = [&](const Upd &ui, int hb, int cur, int nxt, bool full) {
+#pragma unroll
+        for (int jj = 0; jj < S::MT2W; ++jj) {
+            const int mt2 = wave + S::NW * jj;
+            if (S::MT2 % S::NW != 0 && mt2 >= S::MT2) continue;  // uniform per wave
+            const int gc = ui.gc;
+            const int c0 = 16 * mt2 + 4 * g;
+            float xo[4];
+            if constexpr (BF16) {
+                const float4 m4 = *reinterpret_cast<const float4 *>(M + gc * S::MP + c0);
+                xo[0] = m4.x;
+                xo[1] = m4.y;
+                xo[2] = m4.z;
+                xo[3] = m4.w;
+            } else {
+                lds_load4<false>(Pb, cur * PBUF + ui.pc + c0, xo);
+            }
+            fr_t hf[S::KT2];
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt)
+                hf[kt] = FR::load_lds(Hb, hb * S::HBUF + l16 * S::HS + kt * S::KT + (BF16 ? 8 * g : g));
+            f32x4 acc2 = b2v[jj];
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt) acc2 = FR::mfma(w2f[jj][kt], hf[kt], acc2);
+            float u[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float dxv = BF16 ? round_bf16(acc2[v]) : acc2[v];
+                float uv = __fadd_rn(xo[v], __fmul_rn(ui.f, dxv));
+                if constexpr (NOISE) {
+                    const int r = gc / HWn;
+                    uv = __fadd_rn(uv, a.noise[((rbase + r) * C + c0 + v) * HWn + (gc - r * HWn)]);
+                }
+                u[v] = (ui.gv && inslice[jj][v]) ? xo[v] : uv;
+            }
+            if (full || ui.gq < ncell) {
+                if constexpr (BF16)
+                    *reinterpret_cast<float4 *>(M + gc * S::MP + c0) = make_float4(u[0], u[1], u[2], u[3]);
+                lds_store4<BF16>(Pb, nxt * PBUF + ui.pc + c0, u);
+            }
+        }
+    };
+
+    // the first step's clamp: input slice of given cells := clamp values (state buffer buf)
+    auto clamp_pass = [&](int buf) {
+        for (int e = tid; e < ncell * c_in; e += S::NT) {
+            const int cell = e / c_in, ci = e - cell * c_in;
+            if (!givenL[cell]) continue;
+            const float v = clampL[e];
+            const int c = in_off + ci;
+            if constexpr (BF16) {
+                M[cell * S::MP + c] = v;
+                reinterpret_cast<__bf16 *>(Pb)[buf * PBUF + cinfo[cell] + c] = (__bf16)v;
+            } else {
+                reinterpret_cast<float *>(Pb)[buf * PBUF + cinfo[cell] + c] = v;
+            }
+        }
+    };
+
+    // fire mask of step s for every cell of the workgroup (state buffer cur holds the pre-step state)
     const int nq = (HWn + 3) >> 2;
-    for (int s = 0; s < a.n_steps; ++s) {
-        // ---- phase A: fire mask of every cell of the workgroup
+    auto draw_fire = [&](int s, int cur) {
         for (int it = tid; it < Rw * nq; it += S::NT) {
             const int r = it / nq, qq = it - r * nq;
             float u[4] = {0.f, 0.f, 0.f, 0.f};
             if (!a.fire_u8 && !a.fire_f32) {
                 const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
-                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s),
-                               (uint32_t)qq, u);
+                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
             }
             int cnt = 0;
 #pragma unroll
@@ -339,123 +534,167 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
                 } else if (a.fire_f32) {
                     f = a.fire_f32[(rbase + r) * HWn + q];
                 } else {
-                    float pc = a.p;
+                    float pcell = a.p;
                     if (a.adaptive) {
                         int am;
-                        const float cf = cell_readout(state_ptr(cur, cell) + a.out_off, 1, a.c_out,
-                                                      a.n_out, a.head_kind, headL,
-                                                      headL + a.n_out * a.c_out, &am);
+                        const float cf = cell_readout(state_ptr(cur, cell) + a.out_off, 1, a.c_out, a.n_out,
+                                                      a.head_kind, headL, headL + a.n_out * a.c_out, &am);
                         const bool confident = cf > a.tau || (a.given_confident && givenL[cell]);
-                        if (confident) pc = a.p_low;
+                        if (confident) pcell = a.p_low;
                     }
-                    f = u[e] < pc ? 1.0f : 0.0f;
+                    f = u[e] < pcell ? 1.0f : 0.0f;
                 }
                 fireL[cell] = f;
                 cnt += f != 0.0f;
             }
             if (cnt) atomicAdd(&firedL[r], cnt);
         }
-        __syncthreads();
+    };
 
-        // ---- phase B: tiles of 16 cells
-        const int nxt = cur ^ 1;
-        for (int tile = 0; tile < ntile; ++tile) {
-            // stencil -> Z
-            if (tid < 16 * (C / 4)) {
-                const int n = tid & 15, qd = tid >> 4;
-                const int gc = tile * 16 + n;
-                float acc[4][4];
+    // ---- bf16 steady-state interval, hand-interleaved -----------------------------------
+    // fc1 MFMAs of tile t are issued k-tile by k-tile, each group followed by a slice of the
+    // stencil of tile t+1 (tap-pair packing first, then the dot2 chains) so that the VALU work
+    // runs while the matrix core is busy; then fc2 of tile t-1 with the fc1 epilogue, then the
+    // update of tile t-1. sched_barrier(0) keeps the groups in this order.
+    auto interval_bf16 = [&](const Upd &ui, int spc, int zb, int hb1, int hb2, int zb_next, int cur, int nxt) {
+        // ---- LDS loads
+        fr_t zf[S::KT1];
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
+        for (int kt = 0; kt < S::KT1; ++kt) zf[kt] = FR::load_lds(Zb, zb * S::ZBUF + l16 * S::ZS + kt * S::KT + 8 * g);
+        const bool st_on = S::NSI == S::NT || tid < S::NSI;
+        const int sbase = cur * PBUF + spc + 4 * st_qd;
+        uint2 nb[9];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
-                if (gc < ncell) {
-                    const int r = gc / HWn, q = gc - r * HWn, i = q / W, j = q - i * W;
-                    const int pc = pidx(cur, r, (i + 1) * Wp + (j + 1)) + 4 * qd;
+        for (int t9 = 0; t9 < 9; ++t9) nb[t9] = *reinterpret_cast<const uint2 *>(Pb + 2 * (sbase + toff[t9]));
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- tap pairs
+        uint32_t pr[5][4];
 #pragma unroll
-                    for (int dy = -1; dy <= 1; ++dy)
+        for (int p2 = 0; p2 < 4; ++p2) {
+            const uint2 x0 = nb[2 * p2], x1 = nb[2 * p2 + 1];
+            pr[p2][0] = __builtin_amdgcn_perm(x1.x, x0.x, 0x05040100u);
+            pr[p2][1] = __builtin_amdgcn_perm(x1.x, x0.x, 0x07060302u);
+            pr[p2][2] = __builtin_amdgcn_perm(x1.y, x0.y, 0x05040100u);
+            pr[p2][3] = __builtin_amdgcn_perm(x1.y, x0.y, 0x07060302u);
+        }
+        pr[4][0] = nb[8].x & 0xffffu;
+        pr[4][1] = nb[8].x >> 16;
+        pr[4][2] = nb[8].y & 0xffffu;
+        pr[4][3] = nb[8].y >> 16;
+        // ---- fc1 MFMAs interleaved with the stencil's 16 dot2 chains (head k, channel c)
+        f32x4 acc[S::MT1];
 #pragma unroll
-                        for (int dx = -1; dx <= 1; ++dx) {
-                            float v[4];
-                            lds_load4<BF16>(Pb, pc + (dy * Wp + dx) * S::CP, v);
-                            const int t = (dy + 1) * 3 + (dx + 1);
+        for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+        float zs[16];
+        constexpr int CH = (16 + S::KT1 - 1) / S::KT1;  // chains per k-tile group
 #pragma unroll
-                            for (int k = 0; k < 4; ++k)
+        for (int kt = 0; kt < S::KT1; ++kt) {
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                                for (int c = 0; c < 4; ++c) acc[k][c] = __builtin_fmaf(kw[k][t], v[c], acc[k][c]);
-                        }
-                }
+            for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = FR::mfma(w1f[mt][kt], zf[kt], acc[mt]);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) lds_store4<BF16>(Zb, n * S::ZS + k * C + 4 * qd, acc[k]);
-            }
-            __syncthreads();
-
-            // fc1: h^T = relu(W1 z^T + b1) for this wave's hidden units -> H
-            {
-                f32x4 acc[S::MT1];
+            for (int j = kt * CH; j < (kt + 1) * CH && j < 16; ++j) {
+                const int k = j >> 2, c = j & 3;
+                float sum = 0.0f;
 #pragma unroll
-                for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
-#pragma unroll
-                for (int kt = 0; kt < S::KT1; ++kt) {
-                    const fr_t bfrag = FR::load_lds(Zb, l16 * S::ZS + kt * S::KT + (BF16 ? 8 * g : g));
-#pragma unroll
-                    for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = FR::mfma(w1f[mt][kt], bfrag, acc[mt]);
-                }
-#pragma unroll
-                for (int mt = 0; mt < S::MT1; ++mt) {
-                    float h[4];
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) h[v] = acc[mt][v] > 0.0f ? acc[mt][v] : 0.0f;
-                    lds_store4<BF16>(Hb, l16 * S::HS + wave * S::HPW + 16 * mt + 4 * g, h);
-                }
-            }
-            __syncthreads();
-
-            // fc2 + residual update + clamp for this wave's output channels
-#pragma unroll
-            for (int jj = 0; jj < S::MT2W; ++jj) {
-                const int mt2 = wave + S::NW * jj;
-                if (mt2 < S::MT2) {
-                    f32x4 acc2 = b2v[jj];
-#pragma unroll
-                    for (int kt = 0; kt < S::KT2; ++kt) {
-                        const fr_t bfrag = FR::load_lds(Hb, l16 * S::HS + kt * S::KT + (BF16 ? 8 * g : g));
-                        acc2 = FR::mfma(w2f[jj][kt], bfrag, acc2);
-                    }
-                    const int gc = tile * 16 + l16;
-                    if (gc < ncell) {
-                        const int c0 = 16 * mt2 + 4 * g;
-                        const int r = gc / HWn, q = gc - r * HWn, i = q / W, j = q - i * W;
-                        const int pi = (i + 1) * Wp + j + 1;
-                        float xo[4];
-                        if constexpr (BF16) {
-                            const float4 m4 = *reinterpret_cast<const float4 *>(M + gc * S::MP + c0);
-                            xo[0] = m4.x;
-                            xo[1] = m4.y;
-                            xo[2] = m4.z;
-                            xo[3] = m4.w;
-                        } else {
-                            lds_load4<false>(Pb, pidx(cur, r, pi) + c0, xo);
-                        }
-                        const float f = fireL[gc];
-                        const bool gv = givenL[gc] != 0;
-                        float u[4];
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) {
-                            const float dxv = BF16 ? round_bf16(acc2[v]) : acc2[v];
-                            u[v] = __fadd_rn(xo[v], __fmul_rn(f, dxv));
-                            if (a.noise) u[v] = __fadd_rn(u[v], a.noise[((rbase + r) * C + c0 + v) * HWn + q]);
-                            const int c = c0 + v;
-                            if (gv && c >= in_off && c < in_off + c_in) u[v] = clampL[gc * c_in + (c - in_off)];
-                        }
-                        if constexpr (BF16)
-                            *reinterpret_cast<float4 *>(M + gc * S::MP + c0) = make_float4(u[0], u[1], u[2], u[3]);
-                        lds_store4<BF16>(Pb, pidx(nxt, r, pi) + c0, u);
-                    }
-                }
+                for (int p2 = 0; p2 < 5; ++p2)
+                    sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), sum, false);
+                zs[j] = sum;
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- fc2 of tile t-1 (H loads issued now; H of tile t-1 is complete since the last barrier)
+        f32x4 acc2[S::MT2W];
+        float xo[S::MT2W][4];
+#pragma unroll
+        for (int jj = 0; jj < S::MT2W; ++jj) {
+            const int mt2 = wave + S::NW * jj;
+            if (S::MT2 % S::NW != 0 && mt2 >= S::MT2) continue;
+            const int c0 = 16 * mt2 + 4 * g;
+            const float4 m4 = *reinterpret_cast<const float4 *>(M + ui.gc * S::MP + c0);
+            xo[jj][0] = m4.x;
+            xo[jj][1] = m4.y;
+            xo[jj][2] = m4.z;
+            xo[jj][3] = m4.w;
+            fr_t hf[S::KT2];
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt) hf[kt] = FR::load_lds(Hb, hb2 * S::HBUF + l16 * S::HS + kt * S::KT + 8 * g);
+            acc2[jj] = b2v[jj];
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt) acc2[jj] = FR::mfma(w2f[jj][kt], hf[kt], acc2[jj]);
+        }
+        // ---- fc1 epilogue -> H[hb1]; stencil results -> Z[zb_next]
+#pragma unroll
+        for (int mt = 0; mt < S::MT1; ++mt) {
+            float h[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) h[v] = acc[mt][v] > 0.0f ? acc[mt][v] : 0.0f;
+            lds_store4<true>(Hb, hb1 * S::HBUF + l16 * S::HS + wave * S::HPW + 16 * mt + 4 * g, h);
+        }
+        if (st_on) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) lds_store4<true>(Zb, zb_next * S::ZBUF + st_n * S::ZS + k * C + 4 * st_qd, &zs[4 * k]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // ---- update of tile t-1
+#pragma unroll
+        for (int jj = 0; jj < S::MT2W; ++jj) {
+            const int mt2 = wave + S::NW * jj;
+            if (S::MT2 % S::NW != 0 && mt2 >= S::MT2) continue;
+            const int c0 = 16 * mt2 + 4 * g;
+            float u[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float dxv = round_bf16(acc2[jj][v]);
+                const float uv = __fadd_rn(xo[jj][v], __fmul_rn(ui.f, dxv));
+                u[v] = (ui.gv && inslice[jj][v]) ? xo[jj][v] : uv;
+            }
+            *reinterpret_cast<float4 *>(M + ui.gc * S::MP + c0) = make_float4(u[0], u[1], u[2], u[3]);
+            lds_store4<true>(Pb, nxt * PBUF + ui.pc + c0, u);
+        }
+    };
+
+    // ---- steps ------------------------------------------------------------------------------
+    int cur = 0;
+    for (int s = 0; s < a.n_steps; ++s) {
+        const int nxt = cur ^ 1;
+        draw_fire(s, cur);
+        stencil(stencil_pc(0), 0, cur);
         __syncthreads();
+        // interval 0: fc1(0) + stencil(1)
+        fc1(0, 0);
+        if (ntile > 1) stencil(stencil_pc(1), 1, cur);
+        __syncthreads();
+        // steady state: fc2/update(t-1), fc1(t), stencil(t+1) in one barrier interval; the cell
+        // info of the next interval is read one interval ahead so that every LDS load of an
+        // interval can be issued at its start
+        Upd ui = upd_info(0);
+        int spc = ntile > 2 ? stencil_pc(2) : 0;
+        for (int t = 1; t + 1 < ntile; ++t) {
+            const Upd ui_n = upd_info(t);
+            const int spc_n = stencil_pc(t + 2 < ntile ? t + 2 : ntile - 1);
+            if constexpr (BF16 && !NOISE) {
+                interval_bf16(ui, spc, t & 1, t & 1, (t - 1) & 1, (t + 1) & 1, cur, nxt);
+            } else {
+                fc2_update(ui, (t - 1) & 1, cur, nxt, true);
+                fc1(t & 1, t & 1);
+                stencil(spc, (t + 1) & 1, cur);
+            }
+            __syncthreads();
+            ui = ui_n;
+            spc = spc_n;
+        }
+        if (ntile > 1) {
+            fc2_update(upd_info(ntile - 2), (ntile - 2) & 1, cur, nxt, false);
+            fc1((ntile - 1) & 1, (ntile - 1) & 1);
+            __syncthreads();
+        }
+        fc2_update(upd_info(ntile - 1), (ntile - 1) & 1, cur, nxt, false);
+        __syncthreads();
+        if (s == 0 && c_in > 0) {
+            clamp_pass(nxt);
+            __syncthreads();
+        }
         if (a.padding == 2) {
             wrap_halo(nxt);
             __syncthreads();
@@ -471,8 +710,8 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
     if (a.conf_out) {
         for (int cell = tid; cell < ncell; cell += S::NT) {
             int am;
-            confL[cell] = cell_readout(state_ptr(cur, cell) + a.out_off, 1, a.c_out, a.n_out,
-                                       a.head_kind, headL, headL + a.n_out * a.c_out, &am);
+            confL[cell] = cell_readout(state_ptr(cur, cell) + a.out_off, 1, a.c_out, a.n_out, a.head_kind,
+                                       headL, headL + a.n_out * a.c_out, &am);
         }
         __syncthreads();
         for (int r = tid; r < Rw; r += S::NT) {

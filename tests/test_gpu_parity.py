@@ -328,3 +328,30 @@ def test_rollout_api_end_to_end():
     exact = (res.pred == b.targets[:, None]).all(axis=(2, 3))
     assert set(conf_at_k(exact, res.conf, res.alive, [1, 4])) == {1, 4}
     assert set(pass_at_k(exact, res.alive, [1, 4])) == {1, 4}
+
+
+@pytest.mark.parametrize("name", ["maze_c16", "sudoku_c64", "maze_hard_c32", "ref_maze_ood"])
+@pytest.mark.parametrize("n_boards,k", [(5, 3), (1, 1), (33, 2)])
+def test_wave_specialised_and_generic_kernels_agree(name, n_boards, k):
+    """bf16 rollouts run by the wave-specialised kernel (default) and by the generic kernel both
+    match the oracle, for odd row counts (a partial last workgroup, an empty row group)."""
+    from ncas_amd import _lib
+
+    _say("ws vs generic", name, n_boards, k)
+    m, md, x, g4, cl = _case(name, n_boards=n_boards, k=k)
+    xr, fr = O.rollout(oracle_cell(m), x, g4, cl, 24, "bf16", seed=4, p_fire=0.6)
+    out = {}
+    L = _lib.load()
+    try:
+        for path in (0, 1):
+            assert L.nca_set_kernel_path(path) == 0
+            with torch.no_grad():
+                y, conf, f = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 24, seed=4,
+                                           p_fire=0.6, precision="bf16", want_fired=True)
+            out[path] = (y.cpu(), conf.cpu(), f.cpu())
+    finally:
+        L.nca_set_kernel_path(0)
+    for path in (0, 1):
+        assert state_error(name, "bf16", out[path][0], xr) <= 1.0, path
+        assert torch.equal(out[path][2].long(), fr), path
+    assert (out[0][0] - out[1][0]).abs().max().item() <= TOL["bf16"] * 2
