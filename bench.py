@@ -95,6 +95,16 @@ def cpu_baseline(budget_s: float = 15.0):
     }
 
 
+def calibration_copy(mib: int) -> None:
+    """One device-to-device copy of `mib` MiB: reads and writes exactly that many bytes."""
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, device="cuda:0")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
+
+
 def run_gpu(precision, steps, warmup):
     from ncas_amd.inference import rollout_steps
     from ncas_amd.readout import conf_select
@@ -150,11 +160,16 @@ def main():
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp32", action="store_true", help="skip the secondary fp32 run")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first copy this many MiB device-to-device (a kernel of known traffic "
+                         "for scaling HBM counters), outside the timed region")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1"}))
         sys.exit(2)
 
+    if args.calib_copy_mib:
+        calibration_copy(args.calib_copy_mib)
     res = run_gpu(args.precision, args.steps, args.warmup)
     print(f"# gpu {args.precision}: {res['value']:.4g} cell-updates/s, kernel ms {res['kernel_ms']}",
           file=sys.stderr, flush=True)

@@ -1,0 +1,141 @@
+"""The C ABI without a GPU: the library loads, exports every function that include/nca_hip.h
+declares, its structs have the header's layout, and argument checks fail with the documented
+status codes before any device work."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from ncas_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nca_hip.h")
+
+
+def _declared_functions() -> set[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\**\s*(nca_[a-z_0-9]+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.library_path()):
+        pytest.skip("libnca_hip.so is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_and_bindings_list_the_same_functions():
+    declared = _declared_functions()
+    assert len(declared) >= 10
+    assert declared == set(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_function(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """sizeof / offsetof of the header's structs, compiled with the host C compiler, against the
+    ctypes mirrors."""
+    structs = {"nca_cell_desc": _lib.CellDesc, "nca_cell_weights": _lib.CellWeights,
+               "nca_fire_desc": _lib.FireDesc}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "nca_hip.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    for cname, cls in structs.items():
+        assert int(out[cname]) == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert int(out[f"{cname}.{fname}"]) == getattr(cls, fname).offset, (cname, fname)
+
+
+def _cell(**kw):
+    d = dict(channels=64, heads=4, hidden=256, c_in=10, in_offset=0, c_out=16, out_offset=10,
+             n_out=9, padding=2, head_kind=0, precision=1)
+    d.update(kw)
+    return _lib.CellDesc(**d)
+
+
+def test_version_and_packed_sizes(lib):
+    assert lib.nca_version() == 100
+    for prec in (0, 1):
+        n = lib.nca_packed_weights_bytes(ctypes.byref(_cell(precision=prec)))
+        assert n > 0 and n % 256 == 0
+    # the bf16 layout carries the extra fc2 fragment order
+    assert lib.nca_packed_weights_bytes(ctypes.byref(_cell(precision=1))) > \
+        lib.nca_packed_weights_bytes(ctypes.byref(_cell(precision=0))) // 2
+    for bad in (dict(channels=48), dict(hidden=100), dict(heads=3), dict(n_out=40),
+                dict(c_in=70), dict(padding=7), dict(precision=5)):
+        assert lib.nca_packed_weights_bytes(ctypes.byref(_cell(**bad))) == 0, bad
+
+
+def test_argument_errors_return_status_and_message(lib):
+    cell = _cell()
+    fire = _lib.FireDesc(seed=1, p_fire=0.5)
+    rc = lib.nca_rollout(ctypes.byref(cell), None, 4, 9, 9, None, None, None, None,
+                         ctypes.byref(fire), 8, None, None, None, None)
+    assert rc == _lib.NCA_ERR_INVALID
+    assert b"NULL" in lib.nca_last_error()
+    rc = lib.nca_rollout(ctypes.byref(_cell(channels=48)), None, 4, 9, 9, None, None, None, None,
+                         ctypes.byref(fire), 8, None, None, None, None)
+    assert rc == _lib.NCA_ERR_UNSUPPORTED
+    rc = lib.nca_rollout(ctypes.byref(cell), None, -1, 9, 9, None, None, None, None,
+                         ctypes.byref(fire), 8, None, None, None, None)
+    assert rc == _lib.NCA_ERR_INVALID
+    # zero rows is a valid empty call
+    assert lib.nca_rollout(ctypes.byref(cell), None, 0, 9, 9, None, None, None, None,
+                           ctypes.byref(fire), 8, None, None, None, None) == _lib.NCA_OK
+    assert lib.nca_step(ctypes.byref(cell), None, 2, 0, 9, None, None, None, None, None, None,
+                        None) == _lib.NCA_ERR_INVALID
+    assert lib.nca_fire_mask(4, 9, 9, None, 0, None, None, None, None) == _lib.NCA_ERR_INVALID
+    adaptive = _lib.FireDesc(seed=1, p_fire=0.5, p_low=0.1, tau=0.9, adaptive=1)
+    assert lib.nca_fire_mask(4, 9, 9, ctypes.byref(adaptive), 0, None, None,
+                             ctypes.c_void_p(8), None) == _lib.NCA_ERR_INVALID
+    assert b"conf_cell" in lib.nca_last_error()
+    assert lib.nca_conf_select(None, None, 2, 4, 4, None, None) == _lib.NCA_ERR_INVALID
+    assert lib.nca_conf_select(ctypes.c_void_p(8), None, 2, 0, 4, ctypes.c_void_p(8),
+                               None) == _lib.NCA_ERR_INVALID
+    assert lib.nca_set_kernel_path(7) == _lib.NCA_ERR_INVALID
+    assert lib.nca_set_kernel_path(0) == _lib.NCA_OK
+
+
+def test_check_maps_status_to_python_exceptions(lib):
+    lib.nca_set_kernel_path(9)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.NCA_ERR_INVALID, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.NCA_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.NCA_ERR_HIP, "x")
+    _lib.check(_lib.NCA_OK, "x")
+
+
+def test_operators_refuse_cpu_tensors():
+    """The HIP path has no CPU implementation: CPU tensors are rejected, never computed."""
+    import torch
+
+    from ncas_amd.inference import rollout_steps
+    from ncas_amd.model import build_model
+
+    m = build_model("maze_c16")
+    x = torch.zeros(1, 16, 13, 13)
+    g = torch.zeros(1, 1, 13, 13, dtype=torch.bool)
+    c = torch.zeros(1, 4, 13, 13)
+    with pytest.raises((ValueError, RuntimeError)):
+        rollout_steps(m, x, g, c, 2)

@@ -1,0 +1,344 @@
+"""Pins the oracle's step (pad, perception, MLP, residual update, clamp) and readout on the CPU.
+
+Each check compares the oracle with something fixed independently of its own code: brute-force
+loops, closed forms of the fixed kernels, invariants of the padding modes, fp64 GEMMs written
+with numpy, and torch's CPU autocast for the bf16 rounding points. A plausible slip in the
+oracle (convolution instead of cross-correlation, channel-major instead of head-major features,
+a transposed weight, clamp before the update, a missing bias) fails at least one of them.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from ncas_amd.model import build_model, fixed_kernels
+from oracle import nca_oracle as O
+from tests.cells import initial_state, make_model, oracle_cell, boards_for
+
+torch.set_grad_enabled(False)
+
+
+def _rand_cell(C=4, K=4, hidden=8, padding="zero", head="mlp", seed=0, c_in=2, n_out=3):
+    g = torch.Generator().manual_seed(seed)
+    return O.OracleCell(
+        channels=C, heads=K, hidden=hidden, c_in=c_in, in_offset=0, c_out=C - c_in,
+        out_offset=c_in, padding=padding, head=head,
+        kernels=torch.randn(K, 1, 3, 3, generator=g, dtype=torch.float64),
+        w1=torch.randn(hidden, K * C, generator=g, dtype=torch.float64),
+        b1=torch.randn(hidden, generator=g, dtype=torch.float64),
+        w2=torch.randn(C, hidden, generator=g, dtype=torch.float64),
+        b2=torch.randn(C, generator=g, dtype=torch.float64),
+        head_w=torch.randn(n_out, C - c_in, generator=g, dtype=torch.float64),
+        head_b=torch.randn(n_out, generator=g, dtype=torch.float64) if head == "mlp" else None,
+        pad_vec=torch.randn(C, generator=g, dtype=torch.float64),
+    )
+
+
+# ---------------------------------------------------------------- perception (model.py:161-178)
+
+
+def _perceive_loops(xp, kernels):
+    """z[b, k*C + c, i, j] = sum_{dy, dx} w[k, dy, dx] * xp[b, c, i + dy, j + dx]."""
+    B, C, Hp, Wp = xp.shape
+    K = kernels.shape[0]
+    H, W = Hp - 2, Wp - 2
+    z = np.zeros((B, K * C, H, W))
+    xpn, kn = xp.numpy(), kernels.numpy()
+    for b in range(B):
+        for k in range(K):
+            for c in range(C):
+                for i in range(H):
+                    for j in range(W):
+                        s = 0.0
+                        for dy in range(3):
+                            for dx in range(3):
+                                s += kn[k, 0, dy, dx] * xpn[b, c, i + dy, j + dx]
+                        z[b, k * C + c, i, j] = s
+    return z
+
+
+def test_perceive_matches_brute_force_cross_correlation():
+    g = torch.Generator().manual_seed(1)
+    xp = torch.randn(2, 3, 6, 7, generator=g, dtype=torch.float64)
+    kern = torch.randn(4, 1, 3, 3, generator=g, dtype=torch.float64)
+    z = O.perceive(xp, kern, 4, 5)
+    np.testing.assert_allclose(z.numpy(), _perceive_loops(xp, kern), rtol=0, atol=1e-12)
+
+
+def test_perceive_is_block_diagonal_dense_conv():
+    """tests/test_model.py:34-49 of the reference: head-major shared-kernel perception equals a
+    dense conv whose weight is block diagonal per (head, channel)."""
+    g = torch.Generator().manual_seed(2)
+    C, K = 5, 3
+    kern = torch.randn(K, 1, 3, 3, generator=g, dtype=torch.float64)
+    w = torch.zeros(K * C, C, 3, 3, dtype=torch.float64)
+    for k in range(K):
+        for c in range(C):
+            w[k * C + c, c] = kern[k, 0]
+    xp = torch.randn(2, C, 9, 9, generator=g, dtype=torch.float64)
+    np.testing.assert_allclose(O.perceive(xp, kern, 7, 7).numpy(), F.conv2d(xp, w).numpy(),
+                               atol=1e-12)
+
+
+def test_fixed_kernels_closed_forms():
+    """Identity copies, Sobel-x/8 and Sobel-y/8 return the slopes of a linear ramp (sign fixes
+    cross-correlation orientation), the Laplacian/16 annihilates ramps and maps i^2 to 0.5."""
+    k = fixed_kernels().to(torch.float64)
+    assert torch.equal(k[2, 0], k[1, 0].T)  # Sobel-y is Sobel-x transposed
+    H, W = 6, 7
+    i = torch.arange(H + 2, dtype=torch.float64)[:, None]
+    j = torch.arange(W + 2, dtype=torch.float64)[None, :]
+    a, b, c0 = 0.75, -1.25, 0.5
+    ramp = (a * j + b * i + c0).expand(H + 2, W + 2)[None, None]
+    z = O.perceive(ramp, k, H, W)[0]
+    np.testing.assert_allclose(z[0].numpy(), ramp[0, 0, 1:-1, 1:-1].numpy(), atol=1e-12)
+    np.testing.assert_allclose(z[1].numpy(), np.full((H, W), a), atol=1e-12)
+    np.testing.assert_allclose(z[2].numpy(), np.full((H, W), b), atol=1e-12)
+    np.testing.assert_allclose(z[3].numpy(), np.zeros((H, W)), atol=1e-12)
+    quad = (i**2).expand(H + 2, W + 2)[None, None].clone()
+    np.testing.assert_allclose(O.perceive(quad, k, H, W)[0, 3].numpy(), np.full((H, W), 0.5),
+                               atol=1e-12)
+
+
+def test_pad_modes():
+    """model.py:140-152: wall border = pad_vec (corners included), wrap = circular, zero."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 3, 4, 5, generator=g, dtype=torch.float64)
+    pv = torch.tensor([1.5, -2.0, 0.25], dtype=torch.float64)
+    xw = O.pad(x, "wall", pv)
+    assert torch.equal(xw[:, :, 1:-1, 1:-1], x)
+    border = torch.ones(6, 7, dtype=torch.bool)
+    border[1:-1, 1:-1] = False
+    for c in range(3):
+        assert torch.all(xw[:, c][:, border] == pv[c])
+    xr = O.pad(x, "wrap", None)
+    assert torch.equal(xr[:, :, 0, 1:-1], x[:, :, -1])
+    assert torch.equal(xr[:, :, -1, 1:-1], x[:, :, 0])
+    assert torch.equal(xr[:, :, 1:-1, 0], x[:, :, :, -1])
+    assert torch.equal(xr[:, :, 0, 0], x[:, :, -1, -1])
+    xz = O.pad(x, "zero", None)
+    assert torch.all(xz[:, :, border] == 0)
+
+
+def test_wrap_padding_is_translation_equivariant():
+    """tests/test_model.py:116-121 of the reference, on the full sense-update."""
+    cell = _rand_cell(padding="wrap", seed=4)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 4, 7, 6, generator=g, dtype=torch.float64)
+    d = O.sense_update(cell, x, "fp64")
+    dr = O.sense_update(cell, torch.roll(x, (2, 3), dims=(2, 3)), "fp64")
+    np.testing.assert_allclose(torch.roll(d, (2, 3), dims=(2, 3)).numpy(), dr.numpy(), atol=1e-10)
+
+
+def test_wall_border_blocks_information():
+    """tests/test_model.py:106-113: with wall padding the corner cell's update does not depend
+    on anything beyond the grid (here: on the other batch entries or on the far side)."""
+    cell = _rand_cell(padding="wall", seed=6)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(1, 4, 5, 5, generator=g, dtype=torch.float64)
+    y = x.clone()
+    y[:, :, -1, :] += 10.0  # far edge changes; the top-left 3x3 neighbourhood does not
+    d1, d2 = O.sense_update(cell, x, "fp64"), O.sense_update(cell, y, "fp64")
+    np.testing.assert_allclose(d1[..., :2, :2].numpy(), d2[..., :2, :2].numpy(), atol=1e-12)
+    dw = O.sense_update(cell, torch.cat([x, y]), "fp64")
+    np.testing.assert_allclose(dw[:1].numpy(), d1.numpy(), atol=1e-12)
+
+
+# ---------------------------------------------------------------- MLP (model.py:277-287)
+
+
+def test_sense_update_matches_fp64_gemm():
+    """dx = W2 relu(W1 z + b1) + b2 per cell, written with numpy einsum in fp64."""
+    cell = _rand_cell(C=6, hidden=10, seed=8, padding="zero")
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 6, 4, 5, generator=g, dtype=torch.float64)
+    z = _perceive_loops(F.pad(x, (1, 1, 1, 1)), cell.kernels)  # (B, K*C, H, W)
+    h = np.einsum("hf,bfij->bhij", cell.w1.numpy(), z) + cell.b1.numpy()[None, :, None, None]
+    h = np.maximum(h, 0.0)
+    dx = np.einsum("ch,bhij->bcij", cell.w2.numpy(), h) + cell.b2.numpy()[None, :, None, None]
+    np.testing.assert_allclose(O.sense_update(cell, x, "fp64").numpy(), dx, rtol=1e-12, atol=1e-12)
+    d32 = O.sense_update(cell, x.float(), "fp32").double().numpy()
+    np.testing.assert_allclose(d32, dx, rtol=1e-4, atol=1e-4)
+
+
+def _autocast_reference_dx(cell: O.OracleCell, x: torch.Tensor) -> torch.Tensor:
+    """The reference's forward under torch.autocast(cpu, bf16): perception as a grouped
+    conv2d, fc1 / fc2 as 1x1 conv2d (model.py:161-178, 277-287); autocast picks the casts."""
+    B, C, H, W = x.shape
+    K = cell.kernels.shape[0]
+    xp = O.pad(x, cell.padding, cell.pad_vec.float())
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        z = F.conv2d(xp.reshape(B * C, 1, H + 2, W + 2), cell.kernels.float())
+        z = z.view(B, C, K, H, W).transpose(1, 2).reshape(B, K * C, H, W)
+        h = F.conv2d(z, cell.w1.float()[:, :, None, None], cell.b1.float())
+        h = torch.relu(h)
+        dx = F.conv2d(h, cell.w2.float()[:, :, None, None], cell.b2.float())
+    assert dx.dtype == torch.bfloat16
+    return dx.float()
+
+
+@pytest.mark.parametrize("name", ["sudoku_c64", "maze_c16"])
+def test_bf16_rounding_points_match_cpu_autocast(name):
+    """The oracle's bf16 mode sits within a bf16 rounding of torch's CPU autocast forward and
+    closer to it than the fp32 mode is."""
+    m = make_model(name, seed=1)
+    cell = oracle_cell(m)
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(2, m.cfg.channels, 6, 6, generator=gen)
+    ref = _autocast_reference_dx(cell, x)
+    bf = O.sense_update(cell, x, "bf16")
+    f32 = O.sense_update(cell, x, "fp32")
+    err_bf = (bf - ref).abs()
+    assert err_bf.max().item() <= 2e-2
+    assert err_bf.mean().item() < (f32 - ref).abs().mean().item()
+
+
+# ---------------------------------------------------------------- step (model.py:503-559)
+
+
+def test_zero_fire_is_the_identity_and_full_fire_adds_dx():
+    cell = _rand_cell(seed=10)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 4, 5, 5, generator=g, dtype=torch.float64)
+    given = torch.zeros(2, 1, 5, 5, dtype=torch.bool)
+    clamp = torch.zeros(2, 2, 5, 5, dtype=torch.float64)
+    out0 = O.step(cell, x, given, clamp, torch.zeros(2, 1, 5, 5), "fp64")
+    assert torch.equal(out0, x)
+    out1 = O.step(cell, x, given, clamp, torch.ones(2, 1, 5, 5), "fp64")
+    np.testing.assert_allclose(out1.numpy(), (x + O.sense_update(cell, x, "fp64")).numpy(),
+                               atol=1e-12)
+
+
+def test_step_fire_mask_selects_cells():
+    cell = _rand_cell(seed=12)
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(1, 4, 5, 5, generator=g, dtype=torch.float64)
+    fire = (torch.rand(1, 1, 5, 5, generator=g) < 0.5).double()
+    given = torch.zeros(1, 1, 5, 5, dtype=torch.bool)
+    out = O.step(cell, x, given, torch.zeros(1, 2, 5, 5, dtype=torch.float64), fire, "fp64")
+    dx = O.sense_update(cell, x, "fp64")
+    still = fire[0, 0] == 0
+    assert torch.equal(out[0][:, still], x[0][:, still])
+    np.testing.assert_allclose(out[0][:, ~still].numpy(), (x + dx)[0][:, ~still].numpy(),
+                               atol=1e-12)
+
+
+def test_clamp_after_update_and_noise():
+    """model.py:544-559: noise is added to the updated state, then the input slice of given
+    cells is overwritten with the clamp values; other channels and cells keep the update."""
+    cell = _rand_cell(seed=14)
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(1, 4, 5, 5, generator=g, dtype=torch.float64)
+    given = torch.rand(1, 1, 5, 5, generator=g) < 0.4
+    clamp = torch.randn(1, 2, 5, 5, generator=g, dtype=torch.float64)
+    noise = torch.randn(1, 4, 5, 5, generator=g, dtype=torch.float64)
+    fire = torch.ones(1, 1, 5, 5)
+    out = O.step(cell, x, given, clamp, fire, "fp64", noise=noise)
+    u = x + O.sense_update(cell, x, "fp64") + noise
+    gm = given[0, 0]
+    np.testing.assert_allclose(out[0, :2][:, gm].numpy(), clamp[0][:, gm].numpy(), atol=0)
+    np.testing.assert_allclose(out[0, :2][:, ~gm].numpy(), u[0, :2][:, ~gm].numpy(), atol=1e-12)
+    np.testing.assert_allclose(out[0, 2:].numpy(), u[0, 2:].numpy(), atol=1e-12)
+
+
+def test_rollout_composes_single_steps():
+    """rollout over n steps == n calls of step with the same Philox masks."""
+    m = make_model("maze_c16", seed=3)
+    cell = oracle_cell(m)
+    b = boards_for("maze_c16", 2, 13, seed=4)
+    x, given4, clamp = initial_state(m, b)
+    xr, fired = O.rollout(cell, x, given4, clamp, 5, "fp32", seed=7, p_fire=0.5)
+    xs = x.clone()
+    nf = torch.zeros(x.shape[0], dtype=torch.int64)
+    for s in range(5):
+        fire = O.fire_masks_np(7, 0, x.shape[0], s, x.shape[2], x.shape[3], 0.5)
+        nf += fire.reshape(x.shape[0], -1).sum(1).long()
+        xs = O.step(cell, xs, given4, clamp, fire, "fp32")
+    assert torch.equal(xr, xs)
+    assert torch.equal(torch.as_tensor(fired).long(), nf)
+
+
+# ---------------------------------------------------------------- readout (model.py:596-633)
+
+
+def _readout_fp64(x, out_offset, c_out, head, hw, hb):
+    xo = x[:, out_offset:out_offset + c_out].astype(np.float64)  # (B, c_out, H, W)
+    if head == "mlp":
+        logits = np.einsum("vc,bcij->bvij", hw.astype(np.float64), xo) + hb[None, :, None, None]
+        p = np.exp(logits - logits.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        scores = p
+    else:
+        d = xo[:, None] - hw.astype(np.float64)[None, :, :, None, None]
+        scores = 1.0 / (1.0 + np.sqrt((d**2).sum(2) + 1e-8))
+    conf = np.clip(scores.max(1), 0, 1)
+    return conf, conf.mean((1, 2)), scores.argmax(1)
+
+
+@pytest.mark.parametrize("head", ["mlp", "l2"])
+def test_readout_matches_fp64(head):
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal((3, 6, 4, 5)).astype(np.float32)
+    hw = rng.standard_normal((5, 4)).astype(np.float32)
+    hb = rng.standard_normal(5).astype(np.float32) if head == "mlp" else None
+    cc, cb, am = O.clib.readout(x, 2, 4, {"mlp": 0, "l2": 1}[head], hw, hb)
+    rc, rb, ra = _readout_fp64(x, 2, 4, head, hw, hb)
+    np.testing.assert_allclose(cc, rc, rtol=2e-6, atol=2e-7)
+    np.testing.assert_allclose(cb, rb, rtol=2e-6, atol=2e-7)
+    assert np.array_equal(am, ra)
+
+
+def test_readout_argmax_first_maximum_on_ties():
+    x = np.zeros((1, 2, 1, 3), np.float32)
+    x[0, :, 0, 1] = [1.0, 1.0]
+    hw = np.array([[1.0, 0.0], [0.0, 1.0], [1.0, 0.0]], np.float32)  # classes 0 and 2 tie
+    hb = np.zeros(3, np.float32)
+    _, _, am = O.clib.readout(x, 0, 2, 0, hw, hb)
+    assert am.reshape(-1).tolist() == [0, 0, 0]
+    x[0, 1, 0, 2] = 2.0
+    _, _, am = O.clib.readout(x, 0, 2, 0, hw, hb)
+    assert am.reshape(-1)[2] == 1
+
+
+# ---------------------------------------------------------------- conf@K (rollout.py:317-350)
+
+
+def test_conf_at_k_known_answers():
+    """tests/test_rollout.py:63-68 and tests/test_regressions_evaluation.py:68-73."""
+    from ncas_amd.rollout import conf_at_k, pass_at_k
+
+    metric = np.array([[True, False, False], [False, False, True]])
+    conf = np.array([[0.1, 0.9, 0.5], [0.2, 0.3, 0.9]])
+    alive = np.ones((2, 3), dtype=bool)
+    for f in (conf_at_k, O.conf_at_k):
+        assert f(metric, conf, alive, [1, 2, 3]) == {1: 0.5, 2: 0.0, 3: 0.5}
+    for f in (pass_at_k, O.pass_at_k):
+        assert f(metric, alive, [1, 3]) == {1: 0.5, 3: 1.0}
+    metric = np.array([[1.0], [0.0]])
+    conf = np.ones((2, 1))
+    alive = np.ones((2, 1), bool)
+    for f in (conf_at_k, O.conf_at_k):
+        assert f(metric, conf, alive, [1])[1] == 0.5
+        assert f(metric, conf, alive, [1], weights=np.array([0.9, 0.1]))[1] == 0.9
+
+
+def test_conf_select_c_matches_numpy_first_argmax():
+    rng = np.random.default_rng(17)
+    conf = rng.integers(0, 4, (50, 16)).astype(np.float32) / 4  # many ties
+    alive = (rng.random((50, 16)) < 0.8).astype(np.uint8)
+    for k in (1, 5, 16, 40):
+        kk = min(k, 16)
+        ref = np.where(alive[:, :kk] > 0, conf[:, :kk], -np.inf).argmax(1)
+        assert np.array_equal(O.clib.conf_select(conf, alive, k), ref)
+
+
+# ---------------------------------------------------------------- model structure
+
+
+def test_parameter_counts_of_reference_presets():
+    """tests/test_model.py:29-31: 10,420 (maze_ood) and 41,284 (maze_hard)."""
+    for name, n in (("maze_ood", 10420), ("maze_hard", 41284)):
+        assert sum(p.numel() for p in build_model(name).parameters()) == n
