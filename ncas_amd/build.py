@@ -10,7 +10,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 LIB = os.path.join(HERE, "libnca_hip.so")
-SOURCES = ["nca_api.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -18,19 +17,21 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # keep hipcc from emitting packed-fp32 VALU ops (v_pk_*_f32) in any kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",
 ]
+# per-source extra flags
+SOURCES = {
+    "nca_api.hip": [],
+    # the streamed kernel keeps MFMA results and accumulators in VGPRs (its weight fragments are
+    # pinned to AGPRs), so the VALU work on them needs no v_accvgpr copies
+    "nca_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source into the shared library; always recompiles."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, "-I", INCLUDE, "-o", tmp, *srcs]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -42,6 +43,19 @@ def build(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{errs}")
     if verbose and errs.strip():
         print(errs, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source and link the shared library; always recompiles."""
+    objs = []
+    for src, extra in SOURCES.items():
+        obj = os.path.join(CSRC, os.path.splitext(src)[0] + ".o")
+        _run([HIPCC, *FLAGS, *extra, "-I", INCLUDE, "-c", "-o", obj, os.path.join(CSRC, src)], verbose)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    for obj in objs:
+        os.remove(obj)
     os.replace(tmp, LIB)
     return LIB
 

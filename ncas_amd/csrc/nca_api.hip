@@ -11,7 +11,7 @@
 #include "nca_device.h"
 #include "nca_layout.h"
 #include "nca_rollout.h"
-#include "nca_rollout_stream.h"
+#include "nca_stream.h"
 
 namespace {
 
@@ -80,8 +80,10 @@ __global__ void pack_small(const float *src, int n, float *dst, int round_bf16) 
     }
 }
 
-// A fragments of an (M x K) row-major matrix (M, K multiples of 16 and of the k-tile).
-__global__ void pack_frags(const float *src, int M, int K, int bf16, void *dst) {
+// A fragments of an (M x K) row-major matrix (M, K multiples of 16 and of the k-tile). qC > 0
+// (bf16 only) reorders the k axis quad-major: fragment column k = 16 iq + 4 head + ch reads
+// matrix column head * qC + 4 iq + ch.
+__global__ void pack_frags(const float *src, int M, int K, int bf16, int qC, void *dst) {
     const int total = M * K;
     const int ktile = bf16 ? 32 : 4;
     const int nkt = K / ktile;
@@ -92,6 +94,7 @@ __global__ void pack_frags(const float *src, int M, int K, int bf16, void *dst) 
             const int kt = blk % nkt, mt = blk / nkt;
             m = mt * 16 + (lane & 15);
             k = kt * 32 + 8 * (lane >> 4) + s;
+            if (qC > 0) k = ((k >> 2) & 3) * qC + 4 * (k >> 4) + (k & 3);
             reinterpret_cast<__bf16 *>(dst)[e] = (__bf16)src[(size_t)m * K + k];
         } else {
             const int lane = e & 63, blk = e >> 6;
@@ -252,53 +255,12 @@ int launch_rollout(nca::RolloutParams p, hipStream_t st) {
     return hip_check(hipGetLastError(), "rollout launch");
 }
 
-// Streamed bf16 kernel: two row groups per workgroup; needs W + 1 <= 16 (single perception
-// buffer).
-template <int C, int HD>
-int launch_stream(const nca::RolloutParams &p, hipStream_t st, bool *used) {
-    *used = false;
-    if (p.W + 1 > 16 || p.noise || p.fire_f32) return NCA_OK;
-    int rg = (int)((p.rows + 511) / 512);
-    if (rg > 8) rg = 8;
-    if (rg < 1) rg = 1;
-    nca::StPlan L{};
-    for (; rg >= 1; --rg) {
-        L = nca::st_plan<C, HD>(rg, p.H, p.W, p.c_out, p.n_out);
-        if (L.total <= kLdsBytes) break;
-    }
-    if (rg < 1) return NCA_OK;
-    nca::StParams sp;
-    sp.a = p;
-    sp.rg = rg;
-    sp.l_P = L.P;
-    sp.l_M = L.M;
-    sp.l_Z = L.Z;
-    sp.l_D = L.D;
-    sp.l_given = L.given;
-    sp.l_fire = L.fire;
-    sp.l_fired = L.fired;
-    sp.l_head = L.head;
-    sp.l_cinfo = L.cinfo;
-    sp.l_conf = L.conf;
-    sp.l_trash = L.trash;
-    sp.off_w2k = p.off_w2k;
-    auto kfn = nca::rollout_stream<C, HD>;
-    int rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total),
-                       "hipFuncSetAttribute");
-    if (rc) return rc;
-    const int64_t grid = (p.rows + 2 * rg - 1) / (2 * rg);
-    hipLaunchKernelGGL(kfn, dim3((unsigned)grid), dim3(256), L.total, st, sp);
-    *used = true;
-    return hip_check(hipGetLastError(), "rollout launch");
-}
-
 template <int C, int HD>
 int launch_cell(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
     const bool bf = d->precision == NCA_BF16;
-    if (bf && !g_force_generic) {
+    if (bf && C == 64 && HD == 256 && !g_force_generic) {
         bool used = false;
-        const int rc = launch_stream<C, HD>(p, st, &used);
+        const int rc = hip_check(nca::launch_stream64(p, st, kLdsBytes, &used), "streamed rollout launch");
         if (rc || used) return rc;
     }
     if (p.noise)
@@ -338,6 +300,7 @@ nca::RolloutParams base_params(const nca_cell_desc *d, const void *packed, int64
     p.off_w1 = (unsigned)L.w1;
     p.off_w2 = (unsigned)L.w2;
     p.off_w2k = (unsigned)L.w2k;
+    p.off_w1q = (unsigned)L.w1q;
     return p;
 }
 
@@ -388,10 +351,12 @@ int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void 
     hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->head_b, cell->n_out,
                        reinterpret_cast<float *>(pk + L.headb), 0);
     hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->pad_vec, C, reinterpret_cast<float *>(pk + L.padv), 0);
-    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, (int)bf, (void *)(pk + L.w1));
-    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w2, C, HD, (int)bf, (void *)(pk + L.w2));
-    if (bf)
+    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, (int)bf, 0, (void *)(pk + L.w1));
+    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w2, C, HD, (int)bf, 0, (void *)(pk + L.w2));
+    if (bf) {
         hipLaunchKernelGGL(pack_w2k, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2k));
+        hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, 1, C, (void *)(pk + L.w1q));
+    }
     return hip_check(hipGetLastError(), "pack launch");
 }
 

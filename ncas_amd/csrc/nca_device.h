@@ -77,27 +77,31 @@ __device__ __forceinline__ float readout_expf(float x) {
     return __builtin_ldexpf(y, (int)n);
 }
 
-// Confidence and argmax of one cell whose output slice is xo[c * cstride], c < c_out.
+// Confidence and argmax of one cell whose output channel c (c < c_out) is xo(c).
 // head_kind 0: mlp head (hw (n_out, c_out), hb (n_out)), conf = max softmax = 1 / sum exp(l - max).
 // head_kind 1: l2 head (hw = token embeddings (n_out, c_out)), conf = max 1/(1 + |x - e|).
-__device__ __forceinline__ float cell_readout(const float *xo, int cstride, int c_out, int n_out,
-                                              int head_kind, const float *hw, const float *hb,
-                                              int *argmax) {
+template <class X>
+__device__ __forceinline__ float cell_readout_fn(X xo, int c_out, int n_out, int head_kind, const float *hw,
+                                                 const float *hb, int *argmax) {
     float best = 0.0f;
     int bi = 0;
     if (head_kind == 0) {
-        float logits[16];
+        // pass 1: the maximum logit; pass 2: the sum of exponentials (logits recomputed in the
+        // same order, so both passes see identical values)
         for (int v = 0; v < n_out; ++v) {
             float acc = hb[v];
-            for (int c = 0; c < c_out; ++c) acc = __builtin_fmaf(hw[v * c_out + c], xo[c * cstride], acc);
-            logits[v] = acc;
+            for (int c = 0; c < c_out; ++c) acc = __builtin_fmaf(hw[v * c_out + c], xo(c), acc);
             if (v == 0 || acc > best) {
                 best = acc;
                 bi = v;
             }
         }
         float s = 0.0f;
-        for (int v = 0; v < n_out; ++v) s = s + readout_expf(logits[v] - best);
+        for (int v = 0; v < n_out; ++v) {
+            float acc = hb[v];
+            for (int c = 0; c < c_out; ++c) acc = __builtin_fmaf(hw[v * c_out + c], xo(c), acc);
+            s = s + readout_expf(acc - best);
+        }
         float conf = __fdiv_rn(1.0f, s);
         if (conf > 1.0f) conf = 1.0f;
         if (conf < 0.0f) conf = 0.0f;
@@ -107,7 +111,7 @@ __device__ __forceinline__ float cell_readout(const float *xo, int cstride, int 
     for (int v = 0; v < n_out; ++v) {
         float d2 = 0.0f;
         for (int c = 0; c < c_out; ++c) {
-            const float d = xo[c * cstride] - hw[v * c_out + c];
+            const float d = xo(c) - hw[v * c_out + c];
             d2 = __builtin_fmaf(d, d, d2);
         }
         const float sc = __fdiv_rn(1.0f, 1.0f + __fsqrt_rn(d2 + 1e-8f));
@@ -120,6 +124,13 @@ __device__ __forceinline__ float cell_readout(const float *xo, int cstride, int 
     if (best > 1.0f) best = 1.0f;
     if (best < 0.0f) best = 0.0f;
     return best;
+}
+
+// The same with the output slice at xo[c * cstride].
+__device__ __forceinline__ float cell_readout(const float *xo, int cstride, int c_out, int n_out,
+                                              int head_kind, const float *hw, const float *hb,
+                                              int *argmax) {
+    return cell_readout_fn([&](int c) { return xo[c * cstride]; }, c_out, n_out, head_kind, hw, hb, argmax);
 }
 
 #pragma clang fp contract(on)

@@ -13,6 +13,8 @@
 //   w2k    (bf16 only) fc2 fragments per hidden quarter q = 0..3, for the kernel that feeds
 //          fc1's accumulators straight into fc2: [q][m-tile][k-tile][lane][slot] with
 //          A[i][slot] = W2[16 m + i][q*hidden/4 + 16*(2 k + slot/4) + 4*(lane/16) + slot%4]
+//   w1q    (bf16 only) fc1 fragments like w1 with the feature (k) axis in quad-major order:
+//          k = 16 iq + 4 head + ch holds feature head * C + 4 iq + ch
 // bf16 cells use v_mfma_f32_16x16x32_bf16 fragments (k-tile 32, 8 bf16 slots per lane:
 // A[i = lane % 16][k = 8 * (lane / 16) + slot]); fp32 cells use v_mfma_f32_16x16x4_f32
 // fragments (k-tile 4, one float per lane: A[i = lane % 16][k = lane / 16]).
@@ -23,7 +25,7 @@
 namespace nca {
 
 struct PackedLayout {
-    size_t kern, b1, b2, headw, headb, padv, w1, w2, w2k, total;
+    size_t kern, b1, b2, headw, headb, padv, w1, w2, w2k, w1q, total;
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -51,6 +53,8 @@ __host__ __device__ inline PackedLayout packed_layout(int C, int heads, int hidd
     o = align256(o + esz * (size_t)C * hidden);
     L.w2k = o;  // bf16 cells: fc2 fragments in the order of the wave-specialised kernel
     o = align256(o + (bf16 ? 2 * (size_t)C * hidden : 0));
+    L.w1q = o;  // bf16 cells: fc1 fragments in quad-major feature order
+    o = align256(o + (bf16 ? 2 * (size_t)hidden * heads * C : 0));
     L.total = o;
     return L;
 }

@@ -1,30 +1,43 @@
-// Streamed LDS-resident rollout kernel for bf16 cells (gfx950): the fast path of the bf16
-// rollout on grids up to 15 cells wide.
+// Streamed LDS-resident rollout kernel for bf16 cells with C = 64 channels and 256 hidden units
+// (gfx950): the fast path of the bf16 rollout on grids up to 15 cells wide.
 //
-// One workgroup of 4 waves (one per SIMD, up to 512 registers per lane) owns 2*rg rows for the
-// whole call, split into two row groups. The tiles of group 0 step p, group 1 step p, group 0
-// step p+1, ... form one continuous stream. Interval i of the stream (one workgroup barrier)
-// holds three stages of three different tiles, all issued by every wave:
+// One workgroup of 4 waves (one per SIMD) owns 2*rg rows (rollouts) for the whole call, split
+// into two row groups. The 16-cell tiles of group 0 step s, group 1 step s, group 0 step s+1, ...
+// form one stream. Interval i of the stream (one workgroup barrier) runs three stages of three
+// different tiles, all issued by every wave:
 //
-//   stencil  tile i:    the 3x3 perception as v_mfma_f32_4x4x4_16b_bf16: each block of 4 lanes
-//                       multiplies 4 cells' tap vectors (bf16 pairs from v_perm) by the 4 kernels'
-//                       taps, giving z of 4 heads for 4 cells per instruction; 12 instructions per
-//                       lane cover its cell x 4 channels x 9 taps. z (bf16) -> Z[i&1] (LDS).
-//   MLP      tile i-1:  fc1 on v_mfma_f32_16x16x32_bf16 with W1 resident in registers (wave w owns
-//                       hidden units [w*HD/4, (w+1)*HD/4)), B operand from Z; bias + ReLU + bf16
-//                       in registers; fc2 over the wave's own hidden units with the fc1
-//                       accumulators as B operand directly (W2 fragments packed in that k order);
-//                       the 4 per-wave partial sums of dx go to D[(i-1)&1] (LDS, fp32).
-//   update   tile i-2:  dx = bf16(b2 + sum of the 4 partials); x += fire * dx into the fp32 state
-//                       M and the bf16 perception buffer P; clamped channels of given cells frozen.
+//   stencil tile i     the 3x3 perception on v_mfma_f32_4x4x4_16b_bf16. Lane (cell n, channel
+//                      quad iq) reads the 9 taps of its 4 channels (bf16) from the perception
+//                      buffer P; each 4-lane block multiplies 4 cells' tap vectors by the 4
+//                      kernels, giving z of 4 heads for 4 cells per instruction (12 per lane).
+//                      z (bf16) -> feature tile Z[i & 1].
+//   MLP tile i-1       fc1 on v_mfma_f32_16x16x32_bf16 with W1 resident in AGPRs (wave w owns
+//                      hidden units [64w, 64w+64)), B operand read from Z; bias + ReLU + bf16
+//                      in registers; fc2 over the wave's own hidden units with the fc1
+//                      accumulators as B operand (W2 fragments packed in that k order). The four
+//                      waves' partial sums of dx go to D[(i-1) & 1].
+//   update tile i-2    dx = bf16(b2 + sum of the 4 partials); x += fire * dx into the fp32 state
+//                      M and the bf16 perception buffer P; the clamped input channels of given
+//                      cells are frozen.
 //
-// While one group's tiles run, the other group's end-of-step work - the first step's clamp, the
-// wrap halo refresh, the next step's fire mask - takes the intervals 1-3 after its last update, so
-// the pipeline never drains between steps.
+// P is single-buffered: the update of tile i-2 runs in the same interval as the stencil of tile
+// i, whose neighbourhoods reach W+1 <= 16 cells back, so never into tile i-2. A group's
+// end-of-step work runs in the intervals 2 and 3 of the other group's tiles:
+//   * the first step's clamp (phase 1);
+//   * the wrap-halo refresh and the fire masks of the next steps (phase 2).
+// So the pipeline never drains between steps.
 //
-// P is single-buffered: the update of tile i-2 runs with the stencil of tile i, whose 3x3
-// neighbourhoods reach W+1 <= 16 cells back, i.e. never into tile i-2; wrap halos are refreshed
-// only after the group's step.
+// LDS layouts are chosen for gfx950's banks (reads: 64 banks, ds_read_b64 in groups of 32
+// lanes, ds_read_b128 in two 8-lane groups; writes: 32 banks, 16 lanes per cycle for b64 and 8
+// for b128) so that the hot accesses are conflict-free:
+//   * P: cell stride 144 B, padded row pitch RP = 144 (W + 2) + 224, so that the byte address
+//     of cell q is 144 q + const mod 256 and a tile's 16 cells x 2 quads hit 32 distinct bank
+//     pairs for every tap;
+//   * M and D: 288 B per cell row, 16-byte chunk c of cell n stored at chunk c ^ ((n >> 2) & 1);
+//   * Z: 576 B per cell row, features in quad-major order (16 iq + 4 head + ch), chunk c of row
+//     r stored at chunk c ^ (2 ((r >> 2) & 3)).
+// Fire masks of non-adaptive rollouts are drawn for up to 16 steps at a time (one Philox
+// evaluation per 4 cells, as in the standalone mask kernel) into a byte ring in LDS.
 #pragma once
 
 #include <type_traits>
@@ -34,127 +47,142 @@
 namespace nca {
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
-template <int C, int HD>
-struct StShape {
-    static constexpr int F = 4 * C;
-    static constexpr int HPW = HD / 4;        // hidden units per wave
-    static constexpr int MT1 = HPW / 16;      // fc1 m-tiles per wave
-    static constexpr int KT1 = F / 32;        // fc1 k-tiles
-    static constexpr int MT2 = C / 16;        // fc2 m-tiles (all channels)
-    static constexpr int KT2 = MT1 / 2;       // fc2 k-tiles over the wave's own hidden units
-    static constexpr int CP = C + 4;          // P channel stride (bf16 elements)
-    static constexpr int MP = C + 4;          // M channel stride (floats)
-    static constexpr int ZS = F + 8;          // Z row stride (bf16 elements)
-    static constexpr int DS = C + 4;          // partial row stride (floats)
-    static constexpr int ZBUF = 16 * ZS;      // bf16 elements per Z buffer
-    static constexpr int DBUF = 4 * 16 * DS;  // floats per partial buffer (4 waves)
-    static constexpr int NQ = C / 4;          // channel quads
-    static constexpr int QW = NQ / 4;         // waves with stencil / update items (C/16)
-    static_assert(MT1 % 2 == 0, "fc2 k-tiles need an even number of fc1 m-tiles");
-    static_assert(NQ % 4 == 0, "channels must be a multiple of 16");
+struct St64 {
+    static constexpr int C = 64, HD = 256, F = 256;
+    static constexpr int MT1 = 4, KT1 = 8, MT2 = 4, KT2 = 2;
+    static constexpr int CS = 144;   // P bytes per cell (64 bf16 + 8 pad)
+    static constexpr int MS = 288;   // M bytes per cell (64 fp32 + 8 pad)
+    static constexpr int ZS = 576;   // Z bytes per cell row (256 bf16 + 32 pad)
+    static constexpr int DS = 288;   // D bytes per cell row (64 fp32 + 8 pad)
+    static constexpr int ZBUF = 16 * ZS;
+    static constexpr int DBUF = 64 * DS;
+    static constexpr int RPAD = 224;  // (-2 * CS) mod 256
 };
 
 struct StPlan {
-    unsigned P, M, Z, D, given, fire, fired, head, cinfo, conf, trash, total;
+    unsigned P, Ptrash, M, Z, D, cinfo, fire, fired, head, hcp, total;
+    int RP, PB, G, NB;
 };
 
-template <int C, int HD>
-inline StPlan st_plan(int rg, int H, int W, int c_out, int n_out) {
-    using S = StShape<C, HD>;
-    const unsigned R = 2u * rg, hw = (unsigned)H * W, hwp = (unsigned)(H + 2) * (W + 2);
-    auto al = [](unsigned v) { return (v + 15u) & ~15u; };
+inline unsigned st_al16(unsigned v) { return (v + 15u) & ~15u; }
+
+// rg rows per group, NB fire-mask slots. G (cells per group, a multiple of 32 and >= 64) gives an
+// even number (>= 4) of tiles per group step.
+inline StPlan st_plan(int rg, int H, int W, int c_out, int n_out, int NB) {
+    using S = St64;
     StPlan p;
+    const int HWn = H * W;
+    p.RP = (W + 2) * S::CS + S::RPAD;
+    const int pb0 = (H + 2) * p.RP;
+    p.PB = pb0 + (((S::CS * HWn - pb0) % 256) + 256) % 256;
+    const int g = (rg * HWn + 31) & ~31;
+    p.G = g < 64 ? 64 : g;
+    p.NB = NB;
     unsigned o = 0;
     p.P = o;
-    o = al(o + R * hwp * S::CP * 2u);
+    o = st_al16(o + 2u * rg * (unsigned)p.PB);
+    p.Ptrash = o;
+    o = st_al16(o + 16u * S::CS);
     p.M = o;
-    o = al(o + R * hw * S::MP * 4u);
+    o = st_al16(o + 2u * p.G * S::MS);
     p.Z = o;
-    o = al(o + 2u * S::ZBUF * 2u);
+    o += 2u * S::ZBUF;
     p.D = o;
-    o = al(o + 2u * S::DBUF * 4u);
-    p.given = o;
-    o = al(o + R * hw);
-    p.fire = o;
-    o = al(o + R * hw * 4u);
-    p.fired = o;
-    o = al(o + R * 4u);
-    p.head = o;
-    o = al(o + (unsigned)(n_out * c_out + n_out) * 4u);
+    o += 2u * S::DBUF;
     p.cinfo = o;
-    o = al(o + R * hw * 4u);
-    p.conf = o;
-    o = al(o + R * hw * 4u);
-    p.trash = o;  // stores of padding lanes in the branch-free interval: 16 cells of M and of P
-    o = al(o + 16u * S::MP * 4u + 16u * S::CP * 2u);
+    o = st_al16(o + 2u * p.G * 8u);
+    p.fire = o;
+    o = st_al16(o + (unsigned)NB * 2u * p.G);
+    p.fired = o;
+    o = st_al16(o + 2u * rg * 4u);
+    p.head = o;
+    o = st_al16(o + (unsigned)(n_out * c_out + n_out) * 4u);
+    p.hcp = o;
+    o = st_al16(o + (unsigned)(2 * (W + 2) + 2 * H) * 4u);
     p.total = o;
     return p;
 }
 
 struct StParams {
     RolloutParams a;
-    int rg;  // rows per group
-    unsigned l_P, l_M, l_Z, l_D, l_given, l_fire, l_fired, l_head, l_cinfo, l_conf, l_trash;
-    unsigned off_w2k;
+    int rg, G, RP, PB, NB;
+    unsigned l_P, l_Ptrash, l_M, l_Z, l_D, l_cinfo, l_fire, l_fired, l_head, l_hcp;
+    unsigned off_w1q, off_w2k;
 };
 
-template <int C, int HD>
-__global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
-    using S = StShape<C, HD>;
+__device__ __forceinline__ uint2 lds_ld64(const unsigned char *s, unsigned off) {
+    return *reinterpret_cast<const uint2 *>(s + off);
+}
+__device__ __forceinline__ float4 lds_ld128f(const unsigned char *s, unsigned off) {
+    return *reinterpret_cast<const float4 *>(s + off);
+}
+__device__ __forceinline__ void lds_st64(unsigned char *s, unsigned off, uint2 v) {
+    *reinterpret_cast<uint2 *>(s + off) = v;
+}
+__device__ __forceinline__ void lds_st128f(unsigned char *s, unsigned off, float4 v) {
+    *reinterpret_cast<float4 *>(s + off) = v;
+}
+// ReLU of two packed bf16 values: a negative bf16 is a negative int16.
+__device__ __forceinline__ uint32_t relu_bf16x2(uint32_t v) {
+    const s16x2 x = __builtin_bit_cast(s16x2, v);
+    const s16x2 z = {0, 0};
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(x, z));
+}
+__device__ __forceinline__ short bf16_bits(float v) { return __builtin_bit_cast(short, (__bf16)v); }
+
+__global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
+    using S = St64;
     const RolloutParams &a = sp.a;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = lane >> 4, l16 = lane & 15;
-    const int H = a.H, W = a.W, HWn = H * W, Wp = W + 2, HWp = (H + 2) * Wp;
-    const int rg = sp.rg;
+    const int g = lane >> 4, n = lane & 15;  // n: cell of the tile (MFMA column), g: lane group
+    const int iq = 4 * wave + g;             // channel quad of the lane's stencil / update items
+    const int H = a.H, W = a.W, HWn = H * W;
+    const int rg = sp.rg, G = sp.G, RP = sp.RP, PB = sp.PB, NB = sp.NB;
+    const int tg = G >> 4;
     const int64_t rbase = (int64_t)blockIdx.x * 2 * rg;
     const int Rw = (int)((a.rows - rbase) < 2 * rg ? (a.rows - rbase) : 2 * rg);
     const int rows0 = Rw < rg ? Rw : rg, rows1 = Rw - rows0;
-    const int ncg0 = rows0 * HWn, ncg1 = rows1 * HWn;
-    // stream tiles per group: at least 4 (room for the other group's end-of-step work)
-    const int tgr0 = (ncg0 + 15) >> 4, tgr1 = (ncg1 + 15) >> 4;
-    const int tg0 = tgr0 > 4 ? tgr0 : 4, tg1 = tgr1 > 4 ? tgr1 : 4;
-    const int cb1 = rg * HWn;
-    auto ncg = [&](int grp) { return grp ? ncg1 : ncg0; };
-    auto tg = [&](int grp) { return grp ? tg1 : tg0; };
-    auto cbase = [&](int grp) { return grp ? cb1 : 0; };
 
-    __bf16 *P = reinterpret_cast<__bf16 *>(smem + sp.l_P);
-    unsigned char *Pb = smem + sp.l_P;
-    float *M = reinterpret_cast<float *>(smem + sp.l_M);
-    unsigned char *Zb = smem + sp.l_Z;
-    float *Dp = reinterpret_cast<float *>(smem + sp.l_D);
-    uint8_t *givenL = smem + sp.l_given;
-    float *fireL = reinterpret_cast<float *>(smem + sp.l_fire);
     int *firedL = reinterpret_cast<int *>(smem + sp.l_fired);
     float *headL = reinterpret_cast<float *>(smem + sp.l_head);
-    int *cinfo = reinterpret_cast<int *>(smem + sp.l_cinfo);
-    float *confL = reinterpret_cast<float *>(smem + sp.l_conf);
-    const int c_in = a.c_in, in_off = a.in_off;
+    unsigned *hcp = reinterpret_cast<unsigned *>(smem + sp.l_hcp);
+    uint2 *cinfo = reinterpret_cast<uint2 *>(smem + sp.l_cinfo);
+    unsigned char *fireB = smem + sp.l_fire;
 
-    // ---- registers: MLP fragments and biases
+    // byte offset of (workgroup cell c, channel ch) in M; of the centre of cell q of board rw in P
+    auto m_off = [&](int c, int ch) -> unsigned {
+        return sp.l_M + (unsigned)c * S::MS + 16u * (unsigned)((ch >> 2) ^ ((c >> 2) & 1)) + 4u * (ch & 3);
+    };
+    auto p_cell = [&](int rw, int q) -> unsigned {
+        const int i = q / W, j = q - i * W;
+        return sp.l_P + (unsigned)(rw * PB + (i + 1) * RP + (j + 1) * S::CS);
+    };
+    auto m_at = [&](int c, int ch) -> float & { return *reinterpret_cast<float *>(smem + m_off(c, ch)); };
+    auto wg_cell = [&](int rw, int q) { return (rw >= rg ? G + (rw - rg) * HWn : rw * HWn) + q; };
+
+    // ---- registers: MLP weight fragments (AGPRs) and biases
     bf16x8 w1f[S::MT1][S::KT1];
     bf16x8 w2f[S::MT2][S::KT2];
     f32x4 b1v[S::MT1];
     {
-        const bf16x8 *w1 = reinterpret_cast<const bf16x8 *>(a.packed + a.off_w1);
+        const bf16x8 *w1 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w1q);
         const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2k);
         const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
 #pragma unroll
         for (int mt = 0; mt < S::MT1; ++mt) {
 #pragma unroll
-            for (int kt = 0; kt < S::KT1; ++kt) w1f[mt][kt] = w1[((size_t)(wave * S::MT1 + mt) * S::KT1 + kt) * 64 + lane];
+            for (int kt = 0; kt < S::KT1; ++kt) w1f[mt][kt] = w1[((wave * S::MT1 + mt) * S::KT1 + kt) * 64 + lane];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[wave * S::HPW + 16 * mt + 4 * g + v];
+            for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[wave * 64 + 16 * mt + 4 * g + v];
         }
 #pragma unroll
         for (int m2 = 0; m2 < S::MT2; ++m2)
 #pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) w2f[m2][kt] = w2[((size_t)(wave * S::MT2 + m2) * S::KT2 + kt) * 64 + lane];
-        // keep the MFMA weight fragments in AGPRs: the MFMAs read their A operand from there, so
-        // the VGPRs stay free for the per-tile working set
+            for (int kt = 0; kt < S::KT2; ++kt) w2f[m2][kt] = w2[((wave * S::MT2 + m2) * S::KT2 + kt) * 64 + lane];
 #pragma unroll
         for (int mt = 0; mt < S::MT1; ++mt)
 #pragma unroll
@@ -164,51 +192,71 @@ __global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
 #pragma unroll
             for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[m2][kt]));
     }
-    // stencil / update items: lane -> (cell l16 of the tile, channel quad wave*4 + g)
-    const bool item = wave < S::QW;
-    const int iq = wave * 4 + g;                 // channel quad of the lane's items
-    // 4x4x4 MFMA B operand: lane's column j = lane % 4 is kernel j; taps 0-3, 4-7, 8
-    s16x4 kb[3];
-    float b2q[4];
-    bool insl[4];
-    int toff[9];
+    // stencil B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 placed at the
+    // k slot of channel c (the A operand of tap 8 is the 4 channels' tap-8 values as loaded)
+    s16x4 kb0, kb1, kb2[4];
     {
         const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
-        const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
         const int j = lane & 3;
 #pragma unroll
-        for (int grp3 = 0; grp3 < 3; ++grp3)
+        for (int k = 0; k < 4; ++k) {
+            kb0[k] = bf16_bits(kern[j * 9 + k]);
+            kb1[k] = bf16_bits(kern[j * 9 + 4 + k]);
+        }
+        const short k8 = bf16_bits(kern[j * 9 + 8]);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int t = 4 * grp3 + k;
-                kb[grp3][k] = __builtin_bit_cast(short, (__bf16)(t < 9 ? kern[j * 9 + t] : 0.0f));
-            }
-        const int qq = item ? iq : 0;
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
+    }
+    float b2q[4];
+    bool insl[4];
+    {
+        const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const int c = 4 * qq + v;
+            const int c = 4 * iq + v;
             b2q[v] = b2[c];
-            insl[v] = c >= in_off && c < in_off + c_in;
+            insl[v] = c >= a.in_off && c < a.in_off + a.c_in;
         }
-#pragma unroll
-        for (int t = 0; t < 9; ++t) toff[t] = ((t / 3 - 1) * Wp + (t % 3 - 1)) * S::CP;
     }
+    // lane-constant LDS offsets
+    const int hsw = (n >> 2) & 1;
+    const unsigned kM = (unsigned)n * S::MS + 16u * (unsigned)(iq ^ hsw);                       // + l_M + cb MS
+    const unsigned kDr = sp.l_D + (unsigned)n * S::DS + 16u * (unsigned)(iq ^ hsw);              // + w4 16 DS
+    const unsigned kDw = sp.l_D + (unsigned)(wave * 16 + n) * S::DS + 16u * (unsigned)(g ^ hsw);  // + 64 m2
+    const int sig = 2 * ((n >> 2) & 3);
+    const unsigned kZ0 = sp.l_Z + (unsigned)n * S::ZS + 16u * (unsigned)(g ^ (sig & 3));
+    const unsigned kZe = kZ0 + 64u * (unsigned)(sig >> 2), kZo = kZ0 - 64u * (unsigned)(sig >> 2);
+    unsigned kZw;
+    {
+        const int j = lane & 3, b = lane >> 2;
+        kZw = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 16u * (unsigned)((2 * iq + (j >> 1)) ^ (2 * (b & 3))) +
+              8u * (unsigned)(j & 1);
+    }
+    const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS);  // + centre: top-left tap
+    const unsigned RP2 = 2u * RP;
 
-    // ---- load rows
-    auto pcen = [&](int r, int q) {
-        const int i = q / W, j = q - i * W;
-        return (r * HWp + (i + 1) * Wp + (j + 1)) * S::CP;
-    };
-    for (int e = tid; e < Rw * C * HWn; e += 256) {
-        const int r = e / (C * HWn), rem = e - r * C * HWn, c = rem / HWn, q = rem - c * HWn;
-        const float v = a.x_in[rbase * C * HWn + e];
-        M[(r * HWn + q) * S::MP + c] = v;
-        P[pcen(r, q) + c] = (__bf16)v;
+    // ---- load rows and tables
+    for (int e = tid; e < Rw * S::C * HWn; e += 256) {
+        const int rw = e / (S::C * HWn), rem = e - rw * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
+        const float v = a.x_in[rbase * S::C * HWn + e];
+        m_at(wg_cell(rw, q), ch) = v;
+        *reinterpret_cast<__bf16 *>(smem + p_cell(rw, q) + 2 * ch) = (__bf16)v;
     }
-    for (int e = tid; e < Rw * HWn; e += 256) {
-        givenL[e] = a.given[rbase * HWn + e];
-        const int r = e / HWn;
-        cinfo[e] = pcen(r, e - r * HWn);
+    for (int c = tid; c < 2 * G; c += 256) {
+        const int grp = c >= G, qg = c - grp * G, nr = grp ? rows1 : rows0;
+        uint2 ci;
+        if (qg < nr * HWn) {
+            const int r = qg / HWn, q = qg - r * HWn, rw = grp * rg + r;
+            ci.x = p_cell(rw, q);
+            ci.y = ci.x | (a.given[(rbase + rw) * HWn + q] ? 0x80000000u : 0u);
+        } else {
+            // padding cell: the stencil reads a real cell, update stores go to the trash cells
+            ci.x = nr > 0 ? p_cell(grp * rg + nr - 1, HWn - 1) : p_cell(0, 0);
+            ci.y = sp.l_Ptrash + (unsigned)(c & 15) * S::CS;
+        }
+        cinfo[c] = ci;
     }
     for (int e = tid; e < 2 * rg; e += 256) firedL[e] = 0;
     {
@@ -217,8 +265,9 @@ __global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
         const int nw = a.n_out * a.c_out;
         for (int e = tid; e < nw + a.n_out; e += 256) headL[e] = e < nw ? hw[e] : hb[e - nw];
     }
-    const int nhalo = 2 * Wp + 2 * H;
-    auto halo_cell = [&](int h, int &ip, int &jp) __attribute__((always_inline)) {
+    const int Wp = W + 2, nhalo = 2 * Wp + 2 * H;
+    for (int h = tid; h < nhalo; h += 256) {
+        int ip, jp;
         if (h < Wp) {
             ip = 0;
             jp = h;
@@ -232,71 +281,105 @@ __global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
             ip = h - 2 * Wp - H + 1;
             jp = W + 1;
         }
-    };
+        const int si = (ip - 1 + H) % H, sj = (jp - 1 + W) % W;
+        const unsigned dst = (unsigned)(ip * RP + jp * S::CS), src = (unsigned)((si + 1) * RP + (sj + 1) * S::CS);
+        hcp[h] = dst | (src << 16);
+    }
+    __syncthreads();
     if (a.padding != 2) {
         const float *padv = reinterpret_cast<const float *>(a.packed + a.off_padv);
-        for (int e = tid; e < Rw * nhalo * C; e += 256) {
-            const int c = e % C, rest = e / C, h = rest % nhalo, r = rest / nhalo;
-            int ip, jp;
-            halo_cell(h, ip, jp);
-            P[(r * HWp + ip * Wp + jp) * S::CP + c] = (__bf16)(a.padding == 1 ? padv[c] : 0.0f);
-        }
-    }
-    auto wrap_halo = [&](int grp) __attribute__((always_inline)) {
-        const int r0 = grp * rg, nr = grp ? rows1 : rows0;
-        for (int e = tid; e < nr * nhalo * S::NQ; e += 256) {
-            const int qd = e % S::NQ, rest = e / S::NQ, h = rest % nhalo, r = r0 + rest / nhalo;
-            int ip, jp;
-            halo_cell(h, ip, jp);
-            const int si = (ip - 1 + H) % H, sj = (jp - 1 + W) % W;
-            *reinterpret_cast<uint2 *>(Pb + 2 * ((r * HWp + ip * Wp + jp) * S::CP + 4 * qd)) =
-                *reinterpret_cast<const uint2 *>(Pb + 2 * ((r * HWp + (si + 1) * Wp + sj + 1) * S::CP + 4 * qd));
-        }
-    };
-    auto clamp_pass = [&](int grp) __attribute__((always_inline)) {
-        const int c0 = cbase(grp), n = ncg(grp);
-        for (int e = tid; e < n * c_in; e += 256) {
-            const int cell = c0 + e / c_in, ci = e % c_in;
-            if (!givenL[cell]) continue;
-            const int r = cell / HWn, q = cell - r * HWn;
-            const float v = a.clamp[((rbase + r) * c_in + ci) * HWn + q];
-            M[cell * S::MP + in_off + ci] = v;
-            P[cinfo[cell] + in_off + ci] = (__bf16)v;
-        }
-    };
-    const int nq4 = (HWn + 3) >> 2;
-    auto draw_fire = [&](int grp, int s) __attribute__((always_inline)) {
-        const int r0 = grp * rg, nr = grp ? rows1 : rows0;
-        for (int it = tid; it < nr * nq4; it += 256) {
-            const int r = r0 + it / nq4, qq = it % nq4;
-            float u[4] = {0.f, 0.f, 0.f, 0.f};
-            if (!a.fire_u8) {
-                const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
-                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+        for (int r = 0; r < Rw; ++r)
+            for (int e = tid; e < nhalo * S::C; e += 256) {
+                const int h = e >> 6, ch = e & 63;
+                const unsigned dst = hcp[h] & 0xffffu;
+                *reinterpret_cast<__bf16 *>(smem + sp.l_P + (unsigned)(r * PB) + dst + 2 * ch) =
+                    (__bf16)(a.padding == 1 ? padv[ch] : 0.0f);
             }
+    }
+    // wrap halo of one group's boards: 16-byte chunks of 8 channels
+    auto wrap_halo = [&](int grp) __attribute__((always_inline)) {
+        const int nr = grp ? rows1 : rows0;
+        for (int r = 0; r < nr; ++r) {
+            const unsigned base = sp.l_P + (unsigned)((grp * rg + r) * PB);
+            for (int e = tid; e < nhalo * 8; e += 256) {
+                const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
+                const float4 v = lds_ld128f(smem, base + (hc >> 16) + o);
+                lds_st128f(smem, base + (hc & 0xffffu) + o, v);
+            }
+        }
+    };
+    // first step's clamp of the given cells of one group (model.py:430-438)
+    auto clamp_pass = [&](int grp) __attribute__((always_inline)) {
+        const int nr = grp ? rows1 : rows0, c_in = a.c_in;
+        for (int e = tid; e < nr * HWn * c_in; e += 256) {
+            const int cell = e / c_in, ci = e - cell * c_in;
+            const int r = cell / HWn, q = cell - r * HWn, rw = grp * rg + r;
+            if (!a.given[(rbase + rw) * HWn + q]) continue;
+            const float v = a.clamp[((rbase + rw) * c_in + ci) * HWn + q];
+            m_at(grp * G + cell, a.in_off + ci) = v;
+            *reinterpret_cast<__bf16 *>(smem + p_cell(rw, q) + 2 * (a.in_off + ci)) = (__bf16)v;
+        }
+    };
+    // fire masks: batched Philox draws for steps s0 .. s0 + NB - 1 (non-adaptive, no injected
+    // masks), or one step (adaptive confidence gating or injected masks)
+    const int nq4 = (HWn + 3) >> 2;
+    const bool batched = !a.adaptive && !a.fire_u8;
+    auto draw_batch = [&](int grp, int s0) __attribute__((always_inline)) {
+        const int nr = grp ? rows1 : rows0;
+        const int per_row = NB * nq4;
+        for (int it = tid; it < nr * per_row; it += 256) {
+            const int r = it / per_row, rem = it - r * per_row, sl = rem / nq4, qq = rem - sl * nq4;
+            const int s = s0 + sl;
+            if (s >= a.n_steps) continue;
+            const int rw = grp * rg + r;
+            const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
+            float u[4];
+            cell_uniforms4(key, (uint32_t)(a.row0 + rbase + rw), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+            unsigned char *fb = fireB + (unsigned)(sl * 2 * G + grp * G + r * HWn);
             int cnt = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int q = 4 * qq + e;
+                if (q < HWn) {
+                    const int f = u[e] < a.p;
+                    fb[q] = (unsigned char)f;
+                    cnt += f;
+                }
+            }
+            if (cnt) atomicAdd(&firedL[rw], cnt);
+        }
+    };
+    auto draw_step = [&](int grp, int s) __attribute__((always_inline)) {
+        const int nr = grp ? rows1 : rows0;
+        for (int it = tid; it < nr * nq4; it += 256) {
+            const int r = it / nq4, qq = it - r * nq4, rw = grp * rg + r;
+            float u[4] = {0.f, 0.f, 0.f, 0.f};
+            if (!a.fire_u8) {
+                const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
+                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + rw), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+            }
+            int cnt = 0;
+            for (int e = 0; e < 4; ++e) {
+                const int q = 4 * qq + e;
                 if (q >= HWn) break;
-                const int cell = r * HWn + q;
-                float f;
+                const int c = grp * G + r * HWn + q;
+                int f;
                 if (a.fire_u8) {
-                    f = a.fire_u8[((int64_t)s * a.rows + rbase + r) * HWn + q] ? 1.0f : 0.0f;
+                    f = a.fire_u8[((int64_t)s * a.rows + rbase + rw) * HWn + q] != 0;
                 } else {
                     float pc = a.p;
                     if (a.adaptive) {
                         int am;
-                        const float cf = cell_readout(M + cell * S::MP + a.out_off, 1, a.c_out, a.n_out, a.head_kind,
-                                                      headL, headL + a.n_out * a.c_out, &am);
-                        if (cf > a.tau || (a.given_confident && givenL[cell])) pc = a.p_low;
+                        const float cf = cell_readout_fn([&](int v) { return m_at(c, a.out_off + v); }, a.c_out,
+                                                         a.n_out, a.head_kind, headL, headL + a.n_out * a.c_out, &am);
+                        if (cf > a.tau || (a.given_confident && a.given[(rbase + rw) * HWn + q])) pc = a.p_low;
                     }
-                    f = u[e] < pc ? 1.0f : 0.0f;
+                    f = u[e] < pc;
                 }
-                fireL[cell] = f;
-                cnt += f != 0.0f;
+                fireB[c] = (unsigned char)f;
+                cnt += f;
             }
-            if (cnt) atomicAdd(&firedL[r], cnt);
+            if (cnt) atomicAdd(&firedL[rw], cnt);
         }
     };
     __syncthreads();
@@ -305,101 +388,104 @@ __global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
         wrap_halo(1);
     }
     if (a.n_steps > 0) {
-        draw_fire(0, 0);
-        draw_fire(1, 0);
+        if (batched) {
+            draw_batch(0, 0);
+            draw_batch(1, 0);
+        } else {
+            draw_step(0, 0);
+            draw_step(1, 0);
+        }
     }
     __syncthreads();
 
-    // ---- the tile stream
-    const int T = a.n_steps * (tg0 + tg1);
-    struct Pos {
-        int grp, j, s;
-    };
-    auto advance = [&](Pos &p) __attribute__((always_inline)) {
-        if (++p.j == tg(p.grp)) {
-            p.j = 0;
-            p.grp ^= 1;
-            if (p.grp == 0) ++p.s;
+    // ---- the tile stream. Interval i: stencil of tile i, MLP of tile i-1, update of tile i-2;
+    // tile k belongs to run k / tg (group run & 1, step run >> 1), position k % tg in the run.
+    const int T = a.n_steps * 2 * tg;
+    int js = 0, runs = 0;  // stencil tile position
+    int ju = 0, runu = 0;  // update tile position
+    int slot_u = 0;        // fire slot of the update tile's step
+    uint2 cis = cinfo[n], ciu = cis;
+    auto adv = [&](int &j, int &run) __attribute__((always_inline)) {
+        if (++j == tg) {
+            j = 0;
+            ++run;
         }
     };
-    Pos ps = {0, 0, 0}, pu = {0, 0, 0};
-    int m_grp = 0, m_s = 0, m_phase = 0;
 
-    float *Mtrash = reinterpret_cast<float *>(smem + sp.l_trash);
-    const int ptrash = (int)((sp.l_trash + 16u * S::MP * 4u - sp.l_P) / 2u);  // P element offset
-
-    // one interval of the stream. FULL: every stage has a tile (no uniform branches; padding
-    // lanes store to the trash rows); PAR: i & 1 when FULL (constant buffer offsets).
-    auto interval = [&](int i, auto full_c, auto par_c) __attribute__((always_inline)) {
-        constexpr bool FULL = decltype(full_c)::value;
-        constexpr int PAR = decltype(par_c)::value;
-        const int zs = FULL ? PAR : (i & 1), zf_b = FULL ? 1 - PAR : ((i - 1) & 1);
-        const int nv_s = FULL ? min(16, ncg(ps.grp) - 16 * ps.j) : (i < T ? min(16, ncg(ps.grp) - 16 * ps.j) : 0);
-        const int nv_u = FULL ? min(16, ncg(pu.grp) - 16 * pu.j) : (i >= 2 ? min(16, ncg(pu.grp) - 16 * pu.j) : 0);
-        const bool do_st = FULL || (item && nv_s > 0);
-        const bool do_fc = FULL || (i >= 1 && i <= T);
-        const bool do_up = FULL || (item && nv_u > 0);
-
+    auto interval = [&](auto st_c, auto fc_c, auto up_c, auto par_c) __attribute__((always_inline)) {
+        constexpr bool DST = decltype(st_c)::value, DFC = decltype(fc_c)::value, DUP = decltype(up_c)::value;
+        constexpr unsigned PAR = decltype(par_c)::value;
+        // next tiles' table entries (prefetched; the tables never change)
+        int js_n = js, runs_n = runs, ju_n = ju, runu_n = runu;
+        if (DST) adv(js_n, runs_n);
+        if (DUP) adv(ju_n, runu_n);
+        const int cbu = (runu & 1) * G + 16 * ju;
+        uint2 cis_n = cis, ciu_n = ciu;
+        if (DST) cis_n = cinfo[(runs_n & 1) * G + 16 * js_n + n];
+        if (DUP || DFC) ciu_n = cinfo[(runu_n & 1) * G + 16 * ju_n + n];
         // ---- LDS loads of the interval
         uint2 nb[9];
-        if (do_st) {
-            const int cell = cbase(ps.grp) + 16 * ps.j + (l16 < nv_s ? l16 : nv_s - 1);
-            const int base = cinfo[cell] + 4 * iq;
-#pragma unroll
-            for (int t9 = 0; t9 < 9; ++t9) nb[t9] = *reinterpret_cast<const uint2 *>(Pb + 2 * (base + toff[t9]));
+        if (DST) {
+            const unsigned r0 = cis.x + kPs, r1 = r0 + (unsigned)RP, r2 = r0 + RP2;
+            nb[0] = lds_ld64(smem, r0);
+            nb[1] = lds_ld64(smem, r0 + S::CS);
+            nb[2] = lds_ld64(smem, r0 + 2 * S::CS);
+            nb[3] = lds_ld64(smem, r1);
+            nb[4] = lds_ld64(smem, r1 + S::CS);
+            nb[5] = lds_ld64(smem, r1 + 2 * S::CS);
+            nb[6] = lds_ld64(smem, r2);
+            nb[7] = lds_ld64(smem, r2 + S::CS);
+            nb[8] = lds_ld64(smem, r2 + 2 * S::CS);
         }
         bf16x8 zf[S::KT1];
-        if (do_fc) {
+        if (DFC) {
 #pragma unroll
             for (int kt = 0; kt < S::KT1; ++kt)
-                zf[kt] = *reinterpret_cast<const bf16x8 *>(Zb + 2 * (zf_b * S::ZBUF + l16 * S::ZS + kt * 32 + 8 * g));
+                zf[kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
+                                                           64u * kt);
         }
         float4 pv[4], m4;
-        float f = 0.0f;
+        float fu = 0.0f;
+        unsigned madr = 0, padr = 0;
         bool gv = false;
-        int ucell = 0, upc = 0;
-        if (do_up) {
-            ucell = cbase(pu.grp) + 16 * pu.j + (l16 < nv_u ? l16 : nv_u - 1);
-            const float *dp = Dp + (FULL ? PAR : ((i - 2) & 1)) * S::DBUF + l16 * S::DS + 4 * iq;
+        if (DUP) {
 #pragma unroll
-            for (int w4 = 0; w4 < 4; ++w4) pv[w4] = *reinterpret_cast<const float4 *>(dp + w4 * 16 * S::DS);
-            m4 = *reinterpret_cast<const float4 *>(M + ucell * S::MP + 4 * iq);
-            f = fireL[ucell];
-            gv = givenL[ucell] != 0;
-            upc = cinfo[ucell];
+            for (int w4 = 0; w4 < 4; ++w4) pv[w4] = lds_ld128f(smem, kDr + PAR * S::DBUF + (unsigned)w4 * 16u * S::DS);
+            madr = sp.l_M + (unsigned)cbu * S::MS + kM;
+            m4 = lds_ld128f(smem, madr);
+            fu = (float)fireB[(unsigned)(slot_u * 2 * G + cbu + n)];
+            gv = (int)ciu.y < 0;
+            padr = (ciu.y & 0x7fffffffu) + 8u * iq;
         }
-        // ---- stencil of tile i on the 4x4x4 MFMA
-        if (do_st) {
+        // ---- stencil of tile i
+        if (DST) {
             f32x4 zc[4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int sel = (c & 1) ? 0x07060302 : 0x05040100;
+                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
                 const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nb[1].x : nb[1].y, c < 2 ? nb[0].x : nb[0].y, sel);
                 const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nb[3].x : nb[3].y, c < 2 ? nb[2].x : nb[2].y, sel);
                 const uint32_t p45 = __builtin_amdgcn_perm(c < 2 ? nb[5].x : nb[5].y, c < 2 ? nb[4].x : nb[4].y, sel);
                 const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nb[7].x : nb[7].y, c < 2 ? nb[6].x : nb[6].y, sel);
-                const uint32_t w8 = c < 2 ? nb[8].x : nb[8].y;
-                const uint32_t p8 = (c & 1) ? (w8 >> 16) : (w8 & 0xffffu);
                 const s16x4 a0 = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
                 const s16x4 a1 = __builtin_bit_cast(s16x4, make_uint2(p45, p67));
-                const s16x4 a2 = __builtin_bit_cast(s16x4, make_uint2(p8, 0u));
+                const s16x4 a2 = __builtin_bit_cast(s16x4, nb[8]);
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
-                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a0, kb[0], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a1, kb[1], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb[2], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a0, kb0, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a1, kb1, d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c], d, 0, 0, 0);
                 zc[c] = d;
             }
-            const int j = lane & 3, cb = 4 * ((lane >> 2) & 3);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 uint2 o;
                 o.x = pack_bf16x2(zc[0][r], zc[1][r]);
                 o.y = pack_bf16x2(zc[2][r], zc[3][r]);
-                *reinterpret_cast<uint2 *>(Zb + 2 * (zs * S::ZBUF + (cb + r) * S::ZS + j * C + 4 * iq)) = o;
+                lds_st64(smem, kZw + PAR * S::ZBUF + (unsigned)r * S::ZS, o);
             }
         }
         // ---- MLP of tile i-1
-        if (do_fc) {
+        if (DFC) {
             f32x4 acc[S::MT1];
 #pragma unroll
             for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
@@ -410,24 +496,25 @@ __global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
                     acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zf[kt], acc[mt], 0, 0, 0);
             bf16x8 hf[S::KT2];
 #pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt)
-#pragma unroll
-                for (int s2 = 0; s2 < 8; ++s2) {
-                    const float hv = acc[2 * kt + s2 / 4][s2 % 4];
-                    hf[kt][s2] = (__bf16)(hv > 0.0f ? hv : 0.0f);
-                }
-            float *dpw = Dp + (FULL ? 1 - PAR : ((i - 1) & 1)) * S::DBUF + (wave * 16 + l16) * S::DS;
+            for (int kt = 0; kt < S::KT2; ++kt) {
+                uint4 hv;
+                hv.x = relu_bf16x2(pack_bf16x2(acc[2 * kt][0], acc[2 * kt][1]));
+                hv.y = relu_bf16x2(pack_bf16x2(acc[2 * kt][2], acc[2 * kt][3]));
+                hv.z = relu_bf16x2(pack_bf16x2(acc[2 * kt + 1][0], acc[2 * kt + 1][1]));
+                hv.w = relu_bf16x2(pack_bf16x2(acc[2 * kt + 1][2], acc[2 * kt + 1][3]));
+                hf[kt] = __builtin_bit_cast(bf16x8, hv);
+            }
 #pragma unroll
             for (int m2 = 0; m2 < S::MT2; ++m2) {
                 f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kt = 0; kt < S::KT2; ++kt)
                     acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[m2][kt], hf[kt], acc2, 0, 0, 0);
-                *reinterpret_cast<float4 *>(dpw + 16 * m2 + 4 * g) = make_float4(acc2[0], acc2[1], acc2[2], acc2[3]);
+                lds_st128f(smem, kDw + (PAR ^ 1u) * S::DBUF + 64u * m2, make_float4(acc2[0], acc2[1], acc2[2], acc2[3]));
             }
         }
         // ---- update of tile i-2
-        if (do_up) {
+        if (DUP) {
             float dsum[4] = {b2q[0], b2q[1], b2q[2], b2q[3]};
 #pragma unroll
             for (int w4 = 0; w4 < 4; ++w4) {
@@ -440,60 +527,84 @@ __global__ void __launch_bounds__(256, 1) rollout_stream(StParams sp) {
             float u[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float uv = __fadd_rn(xo[v], __fmul_rn(f, round_bf16(dsum[v])));
+                const float uv = __builtin_fmaf(fu, round_bf16(dsum[v]), xo[v]);  // fu in {0, 1}: exact
                 u[v] = (gv && insl[v]) ? xo[v] : uv;
             }
-            const bool valid = l16 < nv_u;
-            float *mdst = valid ? M + ucell * S::MP + 4 * iq : Mtrash + l16 * S::MP + 4 * iq;
-            const int pdst = valid ? upc + 4 * iq : ptrash + l16 * S::CP + 4 * iq;
-            *reinterpret_cast<float4 *>(mdst) = make_float4(u[0], u[1], u[2], u[3]);
-            lds_store4<true>(Pb, pdst, u);
+            lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
+            lds_st64(smem, padr, make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3])));
         }
-        // ---- end-of-step work of the group whose last tile was updated 1-3 intervals ago
-        if (m_phase == 1 && m_s == 0 && c_in > 0) clamp_pass(m_grp);
-        if (m_phase == 2 && a.padding == 2) wrap_halo(m_grp);
-        if (m_phase == 3 && m_s + 1 < a.n_steps) draw_fire(m_grp, m_s + 1);
-        // bookkeeping (wave-uniform)
-        m_phase = m_phase > 0 && m_phase < 3 ? m_phase + 1 : 0;
-        if (i >= 2 && i - 2 < T) {
-            if (pu.j == tg(pu.grp) - 1) {
-                m_grp = pu.grp;
-                m_s = pu.s;
-                m_phase = 1;
+        // advance: a new even run is the next step, whose fire slot follows
+        js = js_n;
+        runs = runs_n;
+        cis = cis_n;
+        if (DUP) {
+            if (runu_n != runu && (runu_n & 1) == 0) slot_u = slot_u + 1 == NB ? 0 : slot_u + 1;
+            ju = ju_n;
+            runu = runu_n;
+        }
+        ciu = ciu_n;
+    };
+    // end-of-step work of the group of run `run`, whose last update was two intervals ago
+    // (phase 1: first-step clamp) or three (phase 2: wrap halo, next fire masks)
+    auto eos1 = [&](int run) __attribute__((always_inline)) {
+        if ((run >> 1) == 0 && a.c_in > 0) clamp_pass(run & 1);
+    };
+    auto eos2 = [&](int run) __attribute__((always_inline)) {
+        const int grp = run & 1, s = run >> 1;
+        if (a.padding == 2) wrap_halo(grp);
+        if (s + 1 < a.n_steps) {
+            if (batched) {
+                if ((s + 1) % NB == 0) draw_batch(grp, s + 1);
+            } else {
+                draw_step(grp, s + 1);
             }
-            advance(pu);
         }
-        if (i < T) advance(ps);
-        __syncthreads();
     };
     using F_ = std::integral_constant<bool, false>;
     using T_ = std::integral_constant<bool, true>;
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-    // the branch-free body needs every lane to own stencil / update items and real tiles only
-    const bool fast = S::QW == 4 && tgr0 >= 4 && tgr1 >= 4;
-    int i = 0;
-    if (fast) {
-        for (; i < 2 && i < T + 2; ++i) interval(i, F_{}, P0{});
-        for (; i + 1 < T; i += 2) {
-            interval(i, T_{}, P0{});
-            interval(i + 1, T_{}, P1{});
+    using P0 = std::integral_constant<unsigned, 0>;
+    using P1 = std::integral_constant<unsigned, 1>;
+    if (T > 0) {
+        interval(T_{}, F_{}, F_{}, P0{});
+        __syncthreads();
+        interval(T_{}, T_{}, F_{}, P1{});
+        __syncthreads();
+        // steady state: intervals i, i+1 (i even). Interval i is at position jm of its run;
+        // jm == 2 -> phase 1 (at i) and phase 2 (at i+1) of the previous run
+        int jm = 2, erun = -1;
+        for (int i = 2; i < T; i += 2) {
+            interval(T_{}, T_{}, T_{}, P0{});
+            if (jm == 2 && erun >= 0) eos1(erun);
+            __syncthreads();
+            interval(T_{}, T_{}, T_{}, P1{});
+            if (jm == 2 && erun >= 0) eos2(erun);
+            __syncthreads();
+            jm += 2;
+            if (jm == tg) {
+                jm = 0;
+                ++erun;
+            }
         }
+        interval(F_{}, T_{}, T_{}, P0{});
+        __syncthreads();
+        interval(F_{}, F_{}, T_{}, P1{});
+        __syncthreads();
+        eos1(2 * a.n_steps - 1);  // the last run's first-step clamp (one-step calls)
+        __syncthreads();
     }
-    for (; i < T + 2; ++i) interval(i, F_{}, P0{});
-    if (m_phase == 1 && m_s == 0 && c_in > 0) clamp_pass(m_grp);
-    __syncthreads();
 
     // ---- write back
-    for (int e = tid; e < Rw * C * HWn; e += 256) {
-        const int r = e / (C * HWn), rem = e - r * C * HWn, c = rem / HWn, q = rem - c * HWn;
-        a.x_out[rbase * C * HWn + e] = M[(r * HWn + q) * S::MP + c];
+    for (int e = tid; e < Rw * S::C * HWn; e += 256) {
+        const int rw = e / (S::C * HWn), rem = e - rw * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
+        a.x_out[rbase * S::C * HWn + e] = m_at(wg_cell(rw, q), ch);
     }
     if (a.conf_out) {
+        float *confL = reinterpret_cast<float *>(smem + sp.l_D);  // D is free now
         for (int cell = tid; cell < Rw * HWn; cell += 256) {
+            const int rw = cell / HWn, c = wg_cell(rw, cell - rw * HWn);
             int am;
-            confL[cell] = cell_readout(M + cell * S::MP + a.out_off, 1, a.c_out, a.n_out, a.head_kind, headL,
-                                       headL + a.n_out * a.c_out, &am);
+            confL[cell] = cell_readout_fn([&](int v) { return m_at(c, a.out_off + v); }, a.c_out, a.n_out,
+                                          a.head_kind, headL, headL + a.n_out * a.c_out, &am);
         }
         __syncthreads();
         for (int r = tid; r < Rw; r += 256) {

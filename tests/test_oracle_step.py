@@ -18,9 +18,6 @@ from ncas_amd.model import build_model, fixed_kernels
 from oracle import nca_oracle as O
 from tests.cells import initial_state, make_model, oracle_cell, boards_for
 
-torch.set_grad_enabled(False)
-
-
 def _rand_cell(C=4, K=4, hidden=8, padding="zero", head="mlp", seed=0, c_in=2, n_out=3):
     g = torch.Generator().manual_seed(seed)
     return O.OracleCell(
@@ -36,9 +33,7 @@ def _rand_cell(C=4, K=4, hidden=8, padding="zero", head="mlp", seed=0, c_in=2, n
         pad_vec=torch.randn(C, generator=g, dtype=torch.float64),
     )
 
-
 # ---------------------------------------------------------------- perception (model.py:161-178)
-
 
 def _perceive_loops(xp, kernels):
     """z[b, k*C + c, i, j] = sum_{dy, dx} w[k, dy, dx] * xp[b, c, i + dy, j + dx]."""
@@ -59,14 +54,12 @@ def _perceive_loops(xp, kernels):
                         z[b, k * C + c, i, j] = s
     return z
 
-
 def test_perceive_matches_brute_force_cross_correlation():
     g = torch.Generator().manual_seed(1)
     xp = torch.randn(2, 3, 6, 7, generator=g, dtype=torch.float64)
     kern = torch.randn(4, 1, 3, 3, generator=g, dtype=torch.float64)
     z = O.perceive(xp, kern, 4, 5)
     np.testing.assert_allclose(z.numpy(), _perceive_loops(xp, kern), rtol=0, atol=1e-12)
-
 
 def test_perceive_is_block_diagonal_dense_conv():
     """tests/test_model.py:34-49 of the reference: head-major shared-kernel perception equals a
@@ -81,7 +74,6 @@ def test_perceive_is_block_diagonal_dense_conv():
     xp = torch.randn(2, C, 9, 9, generator=g, dtype=torch.float64)
     np.testing.assert_allclose(O.perceive(xp, kern, 7, 7).numpy(), F.conv2d(xp, w).numpy(),
                                atol=1e-12)
-
 
 def test_fixed_kernels_closed_forms():
     """Identity copies, Sobel-x/8 and Sobel-y/8 return the slopes of a linear ramp (sign fixes
@@ -102,7 +94,6 @@ def test_fixed_kernels_closed_forms():
     np.testing.assert_allclose(O.perceive(quad, k, H, W)[0, 3].numpy(), np.full((H, W), 0.5),
                                atol=1e-12)
 
-
 def test_pad_modes():
     """model.py:140-152: wall border = pad_vec (corners included), wrap = circular, zero."""
     g = torch.Generator().manual_seed(3)
@@ -122,7 +113,6 @@ def test_pad_modes():
     xz = O.pad(x, "zero", None)
     assert torch.all(xz[:, :, border] == 0)
 
-
 def test_wrap_padding_is_translation_equivariant():
     """tests/test_model.py:116-121 of the reference, on the full sense-update."""
     cell = _rand_cell(padding="wrap", seed=4)
@@ -131,7 +121,6 @@ def test_wrap_padding_is_translation_equivariant():
     d = O.sense_update(cell, x, "fp64")
     dr = O.sense_update(cell, torch.roll(x, (2, 3), dims=(2, 3)), "fp64")
     np.testing.assert_allclose(torch.roll(d, (2, 3), dims=(2, 3)).numpy(), dr.numpy(), atol=1e-10)
-
 
 def test_wall_border_blocks_information():
     """tests/test_model.py:106-113: with wall padding the corner cell's update does not depend
@@ -146,9 +135,7 @@ def test_wall_border_blocks_information():
     dw = O.sense_update(cell, torch.cat([x, y]), "fp64")
     np.testing.assert_allclose(dw[:1].numpy(), d1.numpy(), atol=1e-12)
 
-
 # ---------------------------------------------------------------- MLP (model.py:277-287)
-
 
 def test_sense_update_matches_fp64_gemm():
     """dx = W2 relu(W1 z + b1) + b2 per cell, written with numpy einsum in fp64."""
@@ -162,7 +149,6 @@ def test_sense_update_matches_fp64_gemm():
     np.testing.assert_allclose(O.sense_update(cell, x, "fp64").numpy(), dx, rtol=1e-12, atol=1e-12)
     d32 = O.sense_update(cell, x.float(), "fp32").double().numpy()
     np.testing.assert_allclose(d32, dx, rtol=1e-4, atol=1e-4)
-
 
 def _autocast_reference_dx(cell: O.OracleCell, x: torch.Tensor) -> torch.Tensor:
     """The reference's forward under torch.autocast(cpu, bf16): perception as a grouped
@@ -179,7 +165,6 @@ def _autocast_reference_dx(cell: O.OracleCell, x: torch.Tensor) -> torch.Tensor:
     assert dx.dtype == torch.bfloat16
     return dx.float()
 
-
 @pytest.mark.parametrize("name", ["sudoku_c64", "maze_c16"])
 def test_bf16_rounding_points_match_cpu_autocast(name):
     """The oracle's bf16 mode sits within a bf16 rounding of torch's CPU autocast forward and
@@ -195,9 +180,7 @@ def test_bf16_rounding_points_match_cpu_autocast(name):
     assert err_bf.max().item() <= 2e-2
     assert err_bf.mean().item() < (f32 - ref).abs().mean().item()
 
-
 # ---------------------------------------------------------------- step (model.py:503-559)
-
 
 def test_zero_fire_is_the_identity_and_full_fire_adds_dx():
     cell = _rand_cell(seed=10)
@@ -211,7 +194,6 @@ def test_zero_fire_is_the_identity_and_full_fire_adds_dx():
     np.testing.assert_allclose(out1.numpy(), (x + O.sense_update(cell, x, "fp64")).numpy(),
                                atol=1e-12)
 
-
 def test_step_fire_mask_selects_cells():
     cell = _rand_cell(seed=12)
     g = torch.Generator().manual_seed(13)
@@ -224,7 +206,6 @@ def test_step_fire_mask_selects_cells():
     assert torch.equal(out[0][:, still], x[0][:, still])
     np.testing.assert_allclose(out[0][:, ~still].numpy(), (x + dx)[0][:, ~still].numpy(),
                                atol=1e-12)
-
 
 def test_clamp_after_update_and_noise():
     """model.py:544-559: noise is added to the updated state, then the input slice of given
@@ -243,7 +224,6 @@ def test_clamp_after_update_and_noise():
     np.testing.assert_allclose(out[0, :2][:, ~gm].numpy(), u[0, :2][:, ~gm].numpy(), atol=1e-12)
     np.testing.assert_allclose(out[0, 2:].numpy(), u[0, 2:].numpy(), atol=1e-12)
 
-
 def test_rollout_composes_single_steps():
     """rollout over n steps == n calls of step with the same Philox masks."""
     m = make_model("maze_c16", seed=3)
@@ -260,9 +240,7 @@ def test_rollout_composes_single_steps():
     assert torch.equal(xr, xs)
     assert torch.equal(torch.as_tensor(fired).long(), nf)
 
-
 # ---------------------------------------------------------------- readout (model.py:596-633)
-
 
 def _readout_fp64(x, out_offset, c_out, head, hw, hb):
     xo = x[:, out_offset:out_offset + c_out].astype(np.float64)  # (B, c_out, H, W)
@@ -277,7 +255,6 @@ def _readout_fp64(x, out_offset, c_out, head, hw, hb):
     conf = np.clip(scores.max(1), 0, 1)
     return conf, conf.mean((1, 2)), scores.argmax(1)
 
-
 @pytest.mark.parametrize("head", ["mlp", "l2"])
 def test_readout_matches_fp64(head):
     rng = np.random.default_rng(16)
@@ -290,7 +267,6 @@ def test_readout_matches_fp64(head):
     np.testing.assert_allclose(cb, rb, rtol=2e-6, atol=2e-7)
     assert np.array_equal(am, ra)
 
-
 def test_readout_argmax_first_maximum_on_ties():
     x = np.zeros((1, 2, 1, 3), np.float32)
     x[0, :, 0, 1] = [1.0, 1.0]
@@ -302,9 +278,7 @@ def test_readout_argmax_first_maximum_on_ties():
     _, _, am = O.clib.readout(x, 0, 2, 0, hw, hb)
     assert am.reshape(-1)[2] == 1
 
-
 # ---------------------------------------------------------------- conf@K (rollout.py:317-350)
-
 
 def test_conf_at_k_known_answers():
     """tests/test_rollout.py:63-68 and tests/test_regressions_evaluation.py:68-73."""
@@ -324,7 +298,6 @@ def test_conf_at_k_known_answers():
         assert f(metric, conf, alive, [1])[1] == 0.5
         assert f(metric, conf, alive, [1], weights=np.array([0.9, 0.1]))[1] == 0.9
 
-
 def test_conf_select_c_matches_numpy_first_argmax():
     rng = np.random.default_rng(17)
     conf = rng.integers(0, 4, (50, 16)).astype(np.float32) / 4  # many ties
@@ -334,9 +307,7 @@ def test_conf_select_c_matches_numpy_first_argmax():
         ref = np.where(alive[:, :kk] > 0, conf[:, :kk], -np.inf).argmax(1)
         assert np.array_equal(O.clib.conf_select(conf, alive, k), ref)
 
-
 # ---------------------------------------------------------------- model structure
-
 
 def test_parameter_counts_of_reference_presets():
     """tests/test_model.py:29-31: 10,420 (maze_ood) and 41,284 (maze_hard)."""
