@@ -19,6 +19,11 @@
  *   nca_rollout       <- the per-step loops inference_block / InferenceEngine.__call__
  *                        (src/nca/engine/inference.py:9-71) and rollout()'s step loop
  *                        (src/nca/rollout.py:203-247), fused into one launch
+ *   nca_rollout_ws    <- the same loops for grids whose rows do not fit one workgroup's LDS
+ *                        (the 201x201 mazes of src/nca/tasks/maze.py, max_cells batching of
+ *                        rollout.py:101): one halo-tiled launch per step into a caller workspace
+ *   nca_rollout_workspace_bytes <- nothing in the reference (PyTorch allocates its temporaries);
+ *                        tells the caller how large that workspace must be
  *   nca_fire_mask     <- draw_step's fire mask (src/nca/engine/rng.py:51-69) and
  *                        NCA.sample_fire_mask (src/nca/model.py:567-593)
  *   nca_readout       <- NCA.scores / confidence / board_confidence / decode
@@ -108,6 +113,23 @@ int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int
                 float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
                 float *conf_out, int32_t *fired_out, void *stream);
 
+/* Bytes of workspace that nca_rollout_ws needs for this call shape: 0 when the rows fit the
+ * LDS-resident kernels (the whole rollout runs in one launch), else one state buffer
+ * (rows * C * H * W * 4 bytes) for the halo-tiled per-step path. */
+size_t nca_rollout_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height,
+                                   int32_t width);
+
+/* nca_rollout with a caller-owned device workspace. Grids whose rows do not fit the resident
+ * kernels run one halo-tiled launch per step, alternating between x_out and the workspace so
+ * that the last step lands in x_out; they need workspace_bytes >= nca_rollout_workspace_bytes
+ * unless n_steps == 1 and x_out does not alias x_in. The workspace must not overlap x_in or
+ * x_out. The arithmetic per cell is the generic resident kernel's (nca_set_kernel_path(1)). */
+int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                   int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
+                   float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
+                   float *conf_out, int32_t *fired_out, void *workspace, size_t workspace_bytes,
+                   void *stream);
+
 /* One step with an injected fire mask (rows, H, W) fp32 in {0,1}: the make_step drop-in. */
 int nca_step(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
              int32_t width, const float *x, const uint8_t *given, const float *clamp,
@@ -136,9 +158,11 @@ const char *nca_last_error(void);
 /* ABI version (major * 100 + minor). */
 int nca_version(void);
 
-/* Kernel selection for bf16 rollouts: 0 = automatic (the streamed kernel where the grid allows
- * it), 1 = always the generic kernel. Process-wide; used by the tests to check both paths
- * against each other. No counterpart in the reference. */
+/* Kernel selection: 0 = automatic (the streamed bf16 kernel where the grid allows it, the
+ * resident kernel where the rows fit LDS, else the halo-tiled per-step kernel), 1 = never the
+ * streamed kernel, 2 = always the halo-tiled per-step kernel. Process-wide; used by the tests to
+ * check the paths against each other and by the bench to time the per-step regime. No
+ * counterpart in the reference. */
 int nca_set_kernel_path(int path);
 
 #ifdef __cplusplus

@@ -22,6 +22,8 @@ EXPORTS = (
     "nca_packed_weights_bytes",
     "nca_pack_weights",
     "nca_rollout",
+    "nca_rollout_ws",
+    "nca_rollout_workspace_bytes",
     "nca_step",
     "nca_fire_mask",
     "nca_readout",
@@ -101,6 +103,12 @@ def load():
         ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, ctypes.POINTER(FireDesc),
         i32, vp, vp, vp, vp,
     ]
+    L.nca_rollout_ws.argtypes = [
+        ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, ctypes.POINTER(FireDesc),
+        i32, vp, vp, vp, vp, ctypes.c_size_t, vp,
+    ]
+    L.nca_rollout_workspace_bytes.argtypes = [ctypes.POINTER(CellDesc), i64, i32, i32]
+    L.nca_rollout_workspace_bytes.restype = ctypes.c_size_t
     L.nca_step.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, vp, vp, vp]
     L.nca_fire_mask.argtypes = [i64, i32, i32, ctypes.POINTER(FireDesc), i64, vp, vp, vp, vp]
     L.nca_readout.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, vp]

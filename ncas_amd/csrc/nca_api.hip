@@ -12,6 +12,7 @@
 #include "nca_layout.h"
 #include "nca_rollout.h"
 #include "nca_stream.h"
+#include "nca_tiled_launch.h"
 
 namespace {
 
@@ -35,8 +36,9 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per workgroup
 
-// Test hook: route bf16 rollouts to the generic kernel (nca_set_kernel_path).
-int g_force_generic = 0;
+// Kernel selection (nca_set_kernel_path): 0 automatic, 1 generic resident kernel for bf16,
+// 2 the halo-tiled per-step kernel for every grid.
+int g_path = 0;
 
 bool shape_supported(int C, int hidden) {
     return (C == 16 && hidden == 128) || (C == 32 && hidden == 256) || (C == 64 && hidden == 256);
@@ -215,22 +217,51 @@ __global__ void conf_select_kernel(const float *conf, const uint8_t *alive, int 
 
 // ------------------------------------------------------------------------------------------
 // Rollout launch
-struct Plan {
-    nca::LdsPlan lds;
+__global__ void fill_i32(int32_t *p, int64_t n, int32_t v) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// Rows per workgroup and LDS plan of the resident kernel; false when one row does not fit.
+template <int C, int HD, bool BF16>
+bool resident_plan(int64_t rows, int H, int W, int c_in, int c_out, int n_out, int *R_out, nca::LdsPlan *L) {
+    int R = (int)((rows + 255) / 256);
+    if (R < 1) R = 1;
+    if (R > 16) R = 16;
+    for (; R >= 1; --R) {
+        *L = nca::lds_plan<C, HD, BF16>(R, H, W, c_in, c_out, n_out);
+        if (L->total <= kLdsBytes) {
+            *R_out = R;
+            return true;
+        }
+    }
+    return false;
+}
+
+template <int C, int HD>
+bool resident_fits(bool bf, int64_t rows, int H, int W, int c_in, int c_out, int n_out) {
     int R;
-};
+    nca::LdsPlan L;
+    return bf ? resident_plan<C, HD, true>(rows, H, W, c_in, c_out, n_out, &R, &L)
+              : resident_plan<C, HD, false>(rows, H, W, c_in, c_out, n_out, &R, &L);
+}
+
+// Does the call run on the LDS-resident kernels (true) or the halo-tiled per-step kernel?
+bool takes_resident(const nca_cell_desc *d, int64_t rows, int H, int W) {
+    if (g_path == 2) return false;
+    const bool bf = d->precision == NCA_BF16;
+    const int C = d->channels, HD = d->hidden;
+    if (C == 16 && HD == 128) return resident_fits<16, 128>(bf, rows, H, W, d->c_in, d->c_out, d->n_out);
+    if (C == 32 && HD == 256) return resident_fits<32, 256>(bf, rows, H, W, d->c_in, d->c_out, d->n_out);
+    if (C == 64 && HD == 256) return resident_fits<64, 256>(bf, rows, H, W, d->c_in, d->c_out, d->n_out);
+    return false;
+}
 
 template <int C, int HD, bool BF16, bool NOISE>
 int launch_rollout(nca::RolloutParams p, hipStream_t st) {
-    int R = (int)((p.rows + 255) / 256);
-    if (R < 1) R = 1;
-    if (R > 16) R = 16;
+    int R = 0;
     nca::LdsPlan L{};
-    for (; R >= 1; --R) {
-        L = nca::lds_plan<C, HD, BF16>(R, p.H, p.W, p.c_in, p.c_out, p.n_out);
-        if (L.total <= kLdsBytes) break;
-    }
-    if (R < 1)
+    if (!resident_plan<C, HD, BF16>(p.rows, p.H, p.W, p.c_in, p.c_out, p.n_out, &R, &L))
         return fail(NCA_ERR_UNSUPPORTED,
                     "a %dx%d grid with C=%d does not fit the LDS-resident rollout kernel", p.H, p.W, C);
     p.rows_per_wg = R;
@@ -255,10 +286,87 @@ int launch_rollout(nca::RolloutParams p, hipStream_t st) {
     return hip_check(hipGetLastError(), "rollout launch");
 }
 
+size_t state_bytes(const nca_cell_desc *d, int64_t rows, int H, int W) {
+    return (size_t)rows * d->channels * (size_t)H * W * sizeof(float);
+}
+
+bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
+    const char *pa = static_cast<const char *>(a), *pb = static_cast<const char *>(b);
+    return pa < pb + nb && pb < pa + na;
+}
+
+// The per-step path: n_steps launches of the halo-tiled kernel, ping-ponging between x_out and
+// the workspace so that the last step lands in x_out; then the final board confidence.
+int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st, void *ws, size_t ws_bytes) {
+    const size_t sb = state_bytes(d, p.rows, p.H, p.W);
+    const int n = p.n_steps;
+    const bool alias = p.x_in == p.x_out;
+    if (!alias && overlaps(p.x_in, sb, p.x_out, sb))
+        return fail(NCA_ERR_INVALID, "x_in and x_out overlap without being the same buffer");
+    float *wsf = static_cast<float *>(ws);
+    if (n > 1 || (n == 1 && alias)) {
+        if (!ws || ws_bytes < sb)
+            return fail(NCA_ERR_UNSUPPORTED,
+                        "a %d-step rollout of a %dx%d grid with C=%d runs step by step and needs a "
+                        "workspace of %zu bytes (nca_rollout_workspace_bytes, nca_rollout_ws)",
+                        n, p.H, p.W, d->channels, sb);
+        if (overlaps(ws, sb, p.x_in, sb) || overlaps(ws, sb, p.x_out, sb))
+            return fail(NCA_ERR_INVALID, "the workspace overlaps x_in or x_out");
+    }
+    if (p.fired_out) {
+        hipLaunchKernelGGL(fill_i32, dim3((unsigned)((p.rows + 255) / 256 < 4096 ? (p.rows + 255) / 256 : 4096)),
+                           dim3(256), 0, st, p.fired_out, p.rows, 0);
+        int rc = hip_check(hipGetLastError(), "fill launch");
+        if (rc) return rc;
+    }
+    if (n == 0) {
+        if (!alias) {
+            int rc = hip_check(hipMemcpyAsync(p.x_out, p.x_in, sb, hipMemcpyDeviceToDevice, st), "state copy");
+            if (rc) return rc;
+        }
+    } else {
+        const float *src = p.x_in;
+        for (int s = 0; s < n; ++s) {
+            float *dst;
+            if (!alias || n % 2 == 0)
+                dst = ((n - 1 - s) % 2 == 0) ? p.x_out : wsf;
+            else
+                dst = (s % 2 == 0) ? wsf : p.x_out;
+            nca::RolloutParams q = p;
+            q.x_in = src;
+            q.x_out = dst;
+            q.noise = s == 0 ? p.noise : nullptr;
+            bool ok = false;
+            int rc = hip_check(nca::tiled_step(d->channels, d->hidden, d->precision == NCA_BF16, q, s, s == 0, st, &ok),
+                               "tiled step launch");
+            if (rc) return rc;
+            if (!ok)
+                return fail(NCA_ERR_UNSUPPORTED, "no window of a %dx%d grid with C=%d fits the LDS", p.H, p.W,
+                            d->channels);
+            src = dst;
+        }
+        if (src != p.x_out) {
+            int rc = hip_check(hipMemcpyAsync(p.x_out, src, sb, hipMemcpyDeviceToDevice, st), "state copy");
+            if (rc) return rc;
+        }
+    }
+    if (p.conf_out) {
+        if (p.rows > 0x7fffffff) return fail(NCA_ERR_UNSUPPORTED, "rows=%lld", (long long)p.rows);
+        const float *hw = reinterpret_cast<const float *>(p.packed + p.off_headw);
+        const float *hb = reinterpret_cast<const float *>(p.packed + p.off_headb);
+        hipLaunchKernelGGL(readout_kernel, dim3((unsigned)p.rows), dim3(256), 0, st, p.x_out, d->channels, p.H * p.W,
+                           d->out_offset, d->c_out, d->n_out, d->head_kind, hw, hb, (float *)nullptr, p.conf_out,
+                           (int32_t *)nullptr);
+        return hip_check(hipGetLastError(), "readout launch");
+    }
+    return NCA_OK;
+}
+
 template <int C, int HD>
-int launch_cell(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
+int launch_cell(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st, void *ws, size_t ws_bytes) {
     const bool bf = d->precision == NCA_BF16;
-    if (bf && C == 64 && HD == 256 && !g_force_generic) {
+    if (!takes_resident(d, p.rows, p.H, p.W)) return run_tiled(d, p, st, ws, ws_bytes);
+    if (bf && C == 64 && HD == 256 && g_path == 0) {
         bool used = false;
         const int rc = hip_check(nca::launch_stream64(p, st, kLdsBytes, &used), "streamed rollout launch");
         if (rc || used) return rc;
@@ -268,10 +376,11 @@ int launch_cell(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t
     return bf ? launch_rollout<C, HD, true, false>(p, st) : launch_rollout<C, HD, false, false>(p, st);
 }
 
-int dispatch_rollout(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st) {
-    if (d->channels == 16 && d->hidden == 128) return launch_cell<16, 128>(d, p, st);
-    if (d->channels == 32 && d->hidden == 256) return launch_cell<32, 256>(d, p, st);
-    if (d->channels == 64 && d->hidden == 256) return launch_cell<64, 256>(d, p, st);
+int dispatch_rollout(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st, void *ws = nullptr,
+                     size_t ws_bytes = 0) {
+    if (d->channels == 16 && d->hidden == 128) return launch_cell<16, 128>(d, p, st, ws, ws_bytes);
+    if (d->channels == 32 && d->hidden == 256) return launch_cell<32, 256>(d, p, st, ws, ws_bytes);
+    if (d->channels == 64 && d->hidden == 256) return launch_cell<64, 256>(d, p, st, ws, ws_bytes);
     return fail(NCA_ERR_UNSUPPORTED, "cell C=%d hidden=%d", d->channels, d->hidden);
 }
 
@@ -319,9 +428,15 @@ const char *nca_last_error(void) { return g_err; }
 int nca_version(void) { return 100; }
 
 int nca_set_kernel_path(int path) {
-    if (path != 0 && path != 1) return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic)", path);
-    g_force_generic = path;
+    if (path < 0 || path > 2) return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic, 2 tiled)", path);
+    g_path = path;
     return NCA_OK;
+}
+
+size_t nca_rollout_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width) {
+    if (check_cell(cell) || check_grid(rows, height, width)) return 0;
+    if (takes_resident(cell, rows, height, width)) return 0;
+    return state_bytes(cell, rows, height, width);
 }
 
 size_t nca_packed_weights_bytes(const nca_cell_desc *cell) {
@@ -360,10 +475,11 @@ int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void 
     return hip_check(hipGetLastError(), "pack launch");
 }
 
-int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
-                int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
-                float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
-                float *conf_out, int32_t *fired_out, void *stream) {
+int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                   int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
+                   float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
+                   float *conf_out, int32_t *fired_out, void *workspace, size_t workspace_bytes,
+                   void *stream) {
     g_err[0] = 0;
     int rc = check_cell(cell);
     if (rc) return rc;
@@ -393,7 +509,15 @@ int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int
     p.tau = fire->tau;
     p.adaptive = fire->adaptive;
     p.given_confident = fire->given_confident;
-    return dispatch_rollout(cell, p, as_stream(stream));
+    return dispatch_rollout(cell, p, as_stream(stream), workspace, workspace_bytes);
+}
+
+int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
+                float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
+                float *conf_out, int32_t *fired_out, void *stream) {
+    return nca_rollout_ws(cell, packed, rows, height, width, x_in, given, clamp, x_out, fire, n_steps, noise,
+                          conf_out, fired_out, nullptr, 0, stream);
 }
 
 int nca_step(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,

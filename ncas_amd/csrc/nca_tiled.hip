@@ -1,0 +1,91 @@
+// The halo-tiled per-step kernel's translation unit: window planning and launch of one step.
+#include <hip/hip_runtime.h>
+
+#include <string.h>
+
+#include "nca_tiled_launch.h"
+#include "nca_tiled.h"
+
+namespace nca {
+
+namespace {
+
+constexpr unsigned kTiledLds = 160u * 1024u;
+
+int cu_count() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) return 256;
+    return n;
+}
+
+// Window TW = min(W, 32) (a 128-byte row segment of one channel), TH the largest height up to
+// 512 / TW cells whose LDS plan fits.
+template <int C, int HD, bool BF16>
+bool choose_window(int H, int W, int c_out, int n_out, int *TH, int *TW, TiledPlan *L) {
+    const int tw = W < 32 ? W : 32;
+    int th = 512 / tw;
+    if (th > H) th = H;
+    if (th < 1) th = 1;
+    for (; th >= 1; --th) {
+        *L = tiled_plan<C, HD, BF16>(th, tw, c_out, n_out);
+        if (L->total <= kTiledLds) {
+            *TH = th;
+            *TW = tw;
+            return true;
+        }
+    }
+    return false;
+}
+
+template <int C, int HD, bool BF16, bool NOISE>
+hipError_t launch(const RolloutParams &p, int step, int first, hipStream_t st, bool *ok) {
+    TiledParams tp;
+    memset(&tp, 0, sizeof(tp));
+    TiledPlan L;
+    *ok = choose_window<C, HD, BF16>(p.H, p.W, p.c_out, p.n_out, &tp.TH, &tp.TW, &L);
+    if (!*ok) return hipSuccess;
+    tp.a = p;
+    tp.step = step;
+    tp.first = first;
+    tp.tiles_y = (p.H + tp.TH - 1) / tp.TH;
+    tp.tiles_x = (p.W + tp.TW - 1) / tp.TW;
+    tp.n_windows = p.rows * tp.tiles_y * tp.tiles_x;
+    tp.l_P = L.P;
+    tp.l_M = L.M;
+    tp.l_Z = L.Z;
+    tp.l_H = L.H;
+    tp.l_given = L.given;
+    tp.l_fire = L.fire;
+    tp.l_cinfo = L.cinfo;
+    tp.l_head = L.head;
+    tp.l_fired = L.fired;
+    auto kfn = step_tiled<C, HD, BF16, NOISE>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
+    if (e != hipSuccess) return e;
+    static const int n_cu = cu_count();
+    const int64_t grid = tp.n_windows < n_cu ? tp.n_windows : n_cu;
+    if (grid < 1) return hipSuccess;
+    hipLaunchKernelGGL(kfn, dim3((unsigned)grid), dim3(256), L.total, st, tp);
+    return hipGetLastError();
+}
+
+template <int C, int HD>
+hipError_t launch_cell(bool bf16, const RolloutParams &p, int step, int first, hipStream_t st, bool *ok) {
+    if (bf16) return p.noise ? launch<C, HD, true, true>(p, step, first, st, ok) : launch<C, HD, true, false>(p, step, first, st, ok);
+    return p.noise ? launch<C, HD, false, true>(p, step, first, st, ok) : launch<C, HD, false, false>(p, step, first, st, ok);
+}
+
+}  // namespace
+
+hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, hipStream_t st,
+                      bool *ok) {
+    *ok = false;
+    if (C == 16 && HD == 128) return launch_cell<16, 128>(bf16, p, step, first, st, ok);
+    if (C == 32 && HD == 256) return launch_cell<32, 256>(bf16, p, step, first, st, ok);
+    if (C == 64 && HD == 256) return launch_cell<64, 256>(bf16, p, step, first, st, ok);
+    return hipSuccess;
+}
+
+}  // namespace nca

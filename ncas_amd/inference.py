@@ -87,13 +87,17 @@ def rollout_steps(
     fired = torch.empty((B,), dtype=torch.int32, device=dev) if want_fired else None
     fd = fire_desc(seed, cfg.fire_rate if p_fire is None else p_fire, p_low, tau,
                    given_confident, row0, step0, ss, m8)
+    L = _lib.load()
+    # rows that do not fit one workgroup's LDS run step by step through a workspace buffer
+    ws_bytes = L.nca_rollout_workspace_bytes(ctypes.byref(pk.desc), B, H, W)
+    ws = torch.empty((ws_bytes // 4,), dtype=torch.float32, device=dev) if ws_bytes else None
     _lib.check(
-        _lib.load().nca_rollout(
+        L.nca_rollout_ws(
             ctypes.byref(pk.desc), pk.buf.data_ptr(), B, H, W, xs.data_ptr(), g8.data_ptr(),
             cl.data_ptr(), out.data_ptr(), ctypes.byref(fd), int(n_steps), None,
-            _lib.ptr(conf), _lib.ptr(fired), _lib.stream_of(dev),
+            _lib.ptr(conf), _lib.ptr(fired), _lib.ptr(ws), ws_bytes, _lib.stream_of(dev),
         ),
-        "nca_rollout",
+        "nca_rollout_ws",
     )
     return out, conf, fired
 

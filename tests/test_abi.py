@@ -115,6 +115,26 @@ def test_argument_errors_return_status_and_message(lib):
     assert lib.nca_set_kernel_path(0) == _lib.NCA_OK
 
 
+def test_workspace_query_and_refusal_without_workspace(lib):
+    """Rows that fit the resident kernels need no workspace; a 201x201 grid needs one state
+    buffer, and a multi-step call without it is refused before any device work."""
+    c16 = _cell(channels=16, hidden=128, c_in=4, c_out=4, out_offset=4, n_out=4, padding=1)
+    assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell()), 32768, 9, 9) == 0
+    assert lib.nca_rollout_workspace_bytes(ctypes.byref(c16), 16, 201, 201) == 16 * 16 * 201 * 201 * 4
+    assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell(channels=48)), 4, 9, 9) == 0
+    fire = _lib.FireDesc(seed=1, p_fire=0.5)
+    p = ctypes.c_void_p(1 << 20)
+    rc = lib.nca_rollout_ws(ctypes.byref(c16), p, 16, 201, 201, p, p, p, ctypes.c_void_p(1 << 40),
+                            ctypes.byref(fire), 3, None, None, None, None, 0, None)
+    assert rc == _lib.NCA_ERR_UNSUPPORTED and b"workspace" in lib.nca_last_error()
+    rc = lib.nca_rollout(ctypes.byref(c16), p, 16, 201, 201, p, p, p, ctypes.c_void_p(1 << 40),
+                         ctypes.byref(fire), 3, None, None, None, None)
+    assert rc == _lib.NCA_ERR_UNSUPPORTED
+    assert lib.nca_set_kernel_path(2) == _lib.NCA_OK
+    assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell()), 8, 9, 9) == 8 * 64 * 81 * 4
+    assert lib.nca_set_kernel_path(0) == _lib.NCA_OK
+
+
 def test_check_maps_status_to_python_exceptions(lib):
     lib.nca_set_kernel_path(9)
     with pytest.raises(ValueError):
