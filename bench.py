@@ -1,18 +1,25 @@
 """Benchmark of the NCA rollout on one MI355X: cell-updates/s and roofline fraction.
 
-Workload (one bench "step" = one pass of the hot path over one batch): 256 random valid Sudoku
-boards (17-30 clues, seed 0), K=128 trials each (32,768 rows), 9x9 grid, C=64, 4 perception
-kernels (identity / Sobel-x / Sobel-y / Laplacian), MLP 256 -> 256 -> 64, p_fire=0.5, D=256
-steps in one launch of the LDS-resident kernel, then the conf@K selection over the 128 trials.
-Weights N(0, 0.02) (synthetic), states zero-initialised and clamped; inputs resident in HBM
-before the timed region.
+Default workload (one bench "step" = one pass of the hot path over one batch): 256 random valid
+Sudoku boards (17-30 clues, seed 0), K=128 trials each (32,768 rows), 9x9 grid, C=64, 4
+perception kernels (identity / Sobel-x / Sobel-y / Laplacian), MLP 256 -> 256 -> 64,
+p_fire=0.5, D=256 steps in one launch of the LDS-resident kernel, then the conf@K selection over
+the 128 trials. Weights N(0, 0.02) (synthetic), states zero-initialised and clamped; inputs
+resident in HBM before the timed region.
 
-value = rows * 81 * D * steps / wall seconds (cell-updates/s). The roofline block prices the
-rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) = 168,448 per
-cell-update) against the MI355X dense MFMA peak of the compute type, with the kernel's average
-duration taken from HIP events recorded around every launch on its stream. The cpu_baseline
-times the CPU oracle (PyTorch-CPU restatement of the reference step, fp32, all host threads) on
-a bounded row sample of the same workload.
+`--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16, D=13,000, p_fire=0.5) and
+`--workload hardmaze30` (1,000 hard mazes 30x30 with 10 % extra openings, K=64 -> 64,000 rows,
+C=32, MLP 128 -> 256 -> 32, D=200, p_fire=0.8 gated to 0.2 above confidence 0.9) time the
+halo-tiled per-step path the same way.
+
+value = rows * H * W * D * steps / wall seconds (cell-updates/s). The roofline block prices the
+rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) per cell-update, the
+reference's count_step_flops convention) against the MI355X dense MFMA peak of the compute type,
+or, for the per-step path when it is lower, its algorithmic HBM bytes (the fp32 state read and
+written once per step plus the given mask: 8 C + 1 bytes per cell-update) against 8 TB/s. The
+kernel time comes from HIP events recorded on the launch stream around every rollout call. The
+cpu_baseline times the CPU oracle (PyTorch-CPU restatement of the reference step, fp32, all host
+threads) on a bounded row sample of the same workload.
 """
 
 from __future__ import annotations
@@ -30,68 +37,112 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_TFLOPS = {"bf16": 2500.0, "fp32": 157.3}
-N_BOARDS, K_TRIALS, DEPTH, GRID = 256, 128, 256, 9
-C, F, HID = 64, 256, 256
-FLOP_PER_CELL_UPDATE = 2 * (36 * C + F * HID + HID * C)  # 168,448
+PEAK_HBM_GBS = 8000.0
+
+WORKLOADS = {
+    "sudoku9": dict(
+        preset="sudoku_c64", task="sudoku", boards=256, k=128, depth=256, grid=9, p_fire=0.5,
+        desc="sudoku 9x9: 256 boards x K=128 trials = 32768 rows, D=256 steps, C=64, 4 kernels, "
+             "MLP 256-256-64, p_fire=0.5, conf@K selection"),
+    "maze201": dict(
+        preset="maze_c16", task="maze", boards=16, k=1, depth=13000, grid=201, p_fire=0.5,
+        desc="maze 201x201: 16 DFS mazes, D=13000 steps, C=16, 4 kernels, MLP 64-128-16, "
+             "p_fire=0.5, one halo-tiled launch per step"),
+    "hardmaze30": dict(
+        preset="maze_hard_c32", task="maze", boards=1000, k=64, depth=200, grid=30, p_fire=0.8,
+        p_low=0.2, tau=0.9, extra=0.10,
+        desc="hard maze 30x30 (+10% openings): 1000 boards x K=64 = 64000 rows, D=200 steps, "
+             "C=32, MLP 128-256-32, p_fire=0.8 gated to 0.2 above confidence 0.9, conf@K, "
+             "one halo-tiled launch per step"),
+}
 
 
-def make_workload(device, seed=0):
+def _cell_dims(preset):
+    from ncas_amd.model import build_model
+
+    cfg = build_model(preset).cfg
+    C, hid = cfg.channels, cfg.hidden
+    return C, 4 * C, hid
+
+
+def flop_per_cell_update(preset):
+    C, F, hid = _cell_dims(preset)
+    return 2 * (36 * C + F * hid + hid * C)
+
+
+def hbm_bytes_per_cell_update(preset):
+    C, _, _ = _cell_dims(preset)
+    return 8 * C + 1
+
+
+def make_boards(wl, seed=0):
+    from ncas_amd.tasks import maze_boards, sudoku_boards
+
+    if wl["task"] == "sudoku":
+        return sudoku_boards(wl["boards"], seed)
+    return maze_boards(wl["boards"], wl["grid"], seed, extra_openings=wl.get("extra", 0.0))
+
+
+def make_workload(wl, device, seed=0):
     from ncas_amd.model import build_model, init_weights
-    from ncas_amd.tasks import sudoku_boards
 
-    model = init_weights(build_model("sudoku_c64"), seed=seed, std=0.02, zero_last=False)
+    model = init_weights(build_model(wl["preset"]), seed=seed, std=0.02, zero_last=False)
     model = model.to(device)
-    boards = sudoku_boards(N_BOARDS, seed)
-    inputs = torch.from_numpy(np.repeat(boards.inputs, K_TRIALS, 0)).to(device)
-    given = torch.from_numpy(np.repeat(boards.given, K_TRIALS, 0)).to(device)
-    x = torch.zeros((inputs.shape[0], C, GRID, GRID), device=device)
+    boards = make_boards(wl, seed)
+    inputs = torch.from_numpy(np.repeat(boards.inputs, wl["k"], 0)).to(device)
+    given = torch.from_numpy(np.repeat(boards.given, wl["k"], 0)).to(device)
+    C = model.cfg.channels
+    x = torch.zeros((inputs.shape[0], C, *inputs.shape[1:]), device=device)
     given4 = given[:, None]
     clamp = model.clamp_values(inputs)
     x = model.apply_clamp(x, given4, clamp).contiguous()
     return model, x, given4, clamp
 
 
-def traffic_from_profiles(precision):
-    path = os.path.join(ROOT, "profiles", f"rollout_c3_{precision}_traffic.json")
+def traffic_from_profiles(name, precision):
+    path = os.path.join(ROOT, "profiles", f"rollout_{name}_{precision}_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def cpu_baseline(budget_s: float = 15.0):
+def cpu_baseline(wl, budget_s: float = 15.0):
     """The CPU oracle (fp32) on a row sample of the workload; cell-updates/s."""
     from ncas_amd.model import build_model, init_weights
-    from ncas_amd.tasks import sudoku_boards
     from oracle import nca_oracle as O
 
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from cells import oracle_cell
 
     torch.set_num_threads(os.cpu_count() or 1)
-    model = init_weights(build_model("sudoku_c64"), seed=0, std=0.02, zero_last=False)
+    model = init_weights(build_model(wl["preset"]), seed=0, std=0.02, zero_last=False)
     cell = oracle_cell(model)
-    rows = 256
-    boards = sudoku_boards(rows // 8, 0)
-    inputs = torch.from_numpy(np.repeat(boards.inputs, 8, 0))
-    given4 = torch.from_numpy(np.repeat(boards.given, 8, 0))[:, None]
+    sub = dict(wl, boards=max(1, min(wl["boards"], 4096 // (wl["grid"] ** 2) + 1)))
+    boards = make_boards(sub, 0)
+    k = max(1, min(wl["k"], 1024 // len(boards.inputs)))
+    inputs = torch.from_numpy(np.repeat(boards.inputs, k, 0))
+    given4 = torch.from_numpy(np.repeat(boards.given, k, 0))[:, None]
     clamp = model.clamp_values(inputs)
-    x = model.apply_clamp(torch.zeros(rows, C, GRID, GRID), given4, clamp)
+    rows, H, W = inputs.shape
+    x = model.apply_clamp(torch.zeros(rows, model.cfg.channels, H, W), given4, clamp)
+    kw = dict(seed=0, p_fire=wl["p_fire"], p_low=wl.get("p_low"), tau=wl.get("tau"))
     with torch.no_grad():
-        O.rollout(cell, x, given4, clamp, 1, "fp32", seed=0, p_fire=0.5)  # warm-up
+        O.rollout(cell, x, given4, clamp, 1, "fp32", **kw)  # warm-up
         t0 = time.perf_counter()
-        O.rollout(cell, x, given4, clamp, 2, "fp32", seed=0, p_fire=0.5)
+        O.rollout(cell, x, given4, clamp, 2, "fp32", **kw)
         per_step = (time.perf_counter() - t0) / 2
-        steps = max(2, min(DEPTH, int(budget_s / max(per_step, 1e-6))))
+        steps = max(2, min(wl["depth"], int(budget_s / max(per_step, 1e-6))))
         t0 = time.perf_counter()
-        O.rollout(cell, x, given4, clamp, steps, "fp32", seed=0, p_fire=0.5)
+        O.rollout(cell, x, given4, clamp, steps, "fp32", **kw)
         dt = time.perf_counter() - t0
     return {
-        "value": rows * GRID * GRID * steps / dt,
+        "value": rows * H * W * steps / dt,
         "unit": "cell-updates/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{rows} rows of the 9x9 C=64 workload x {steps} steps, fp32, {dt:.1f} s",
+        "sample": f"{rows} rows of the {H}x{W} C={model.cfg.channels} workload x {steps} steps, "
+                  f"fp32, {dt:.1f} s",
     }
 
 
@@ -105,26 +156,27 @@ def calibration_copy(mib: int) -> None:
     del a, b
 
 
-def run_gpu(precision, steps, warmup):
+def run_gpu(wl, precision, steps, warmup):
     from ncas_amd.inference import rollout_steps
     from ncas_amd.readout import conf_select
 
     dev = torch.device("cuda:0")
-    model, x, given4, clamp = make_workload(dev)
+    model, x, given4, clamp = make_workload(wl, dev)
     model.packed(precision, dev)
-    rows = x.shape[0]
+    rows, _, H, W = x.shape
     out = torch.empty_like(x)
     stream = torch.cuda.current_stream(dev)
+    n_boards, k = wl["boards"], wl["k"]
 
     def one(seed, ev=None):
         if ev:
             ev[0].record(stream)
-        _, conf, _ = rollout_steps(model, x, given4, clamp, DEPTH, seed=seed, p_fire=0.5,
+        _, conf, _ = rollout_steps(model, x, given4, clamp, wl["depth"], seed=seed,
+                                   p_fire=wl["p_fire"], p_low=wl.get("p_low"), tau=wl.get("tau"),
                                    precision=precision, out=out, want_conf=True)
         if ev:
             ev[1].record(stream)
-        best = conf_select(conf.view(N_BOARDS, K_TRIALS), None, K_TRIALS)
-        return best
+        return conf_select(conf.view(n_boards, k), None, k)
 
     with torch.no_grad():
         for i in range(warmup):
@@ -138,18 +190,37 @@ def run_gpu(precision, steps, warmup):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     kernel_ms = [a.elapsed_time(b) for a, b in events]
-    cell_updates = rows * GRID * GRID * DEPTH
+    cell_updates = rows * H * W * wl["depth"]
     avg_kernel_s = float(np.mean(kernel_ms)) / 1e3
-    achieved = cell_updates * FLOP_PER_CELL_UPDATE / avg_kernel_s / 1e12
+    rate = cell_updates / avg_kernel_s
+    tflops = rate * flop_per_cell_update(wl["preset"]) / 1e12
     return {
         "value": cell_updates * steps / wall,
         "ms_per_step": wall / steps * 1e3,
         "kernel_ms": kernel_ms,
-        "achieved_tflops": achieved,
-        "frac": achieved / PEAK_TFLOPS[precision],
+        "kernel_rate": rate,
+        "achieved_tflops": tflops,
+        "frac": tflops / PEAK_TFLOPS[precision],
         "best_first": best[:4].tolist(),
         "rows": rows,
     }
+
+
+def roofline(name, wl, precision, res):
+    """Binding ceiling of the workload's dominant kernel: MFMA FLOPs for the resident kernel;
+    the lower of MFMA FLOPs and HBM bytes for the per-step path."""
+    flops = flop_per_cell_update(wl["preset"])
+    mfma_ceiling = PEAK_TFLOPS[precision] * 1e12 / flops
+    block = {"bound": "mfma", "achieved": res["achieved_tflops"], "peak": PEAK_TFLOPS[precision],
+             "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic_from_profiles(name, precision)}
+    if name != "sudoku9":
+        nbytes = hbm_bytes_per_cell_update(wl["preset"])
+        hbm_ceiling = PEAK_HBM_GBS * 1e9 / nbytes
+        if hbm_ceiling < mfma_ceiling:
+            gbs = res["kernel_rate"] * nbytes / 1e9
+            block.update(bound="hbm", achieved=gbs, peak=PEAK_HBM_GBS, unit="GB/s",
+                         frac=gbs / PEAK_HBM_GBS)
+    return block
 
 
 def main():
@@ -157,6 +228,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", choices=list(WORKLOADS), default="sudoku9")
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp32", action="store_true", help="skip the secondary fp32 run")
@@ -168,18 +240,20 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1"}))
         sys.exit(2)
 
+    wl = WORKLOADS[args.workload]
     if args.calib_copy_mib:
         calibration_copy(args.calib_copy_mib)
-    res = run_gpu(args.precision, args.steps, args.warmup)
-    print(f"# gpu {args.precision}: {res['value']:.4g} cell-updates/s, kernel ms {res['kernel_ms']}",
-          file=sys.stderr, flush=True)
+    res = run_gpu(wl, args.precision, args.steps, args.warmup)
+    print(f"# gpu {args.workload} {args.precision}: {res['value']:.4g} cell-updates/s, "
+          f"kernel ms {res['kernel_ms']}", file=sys.stderr, flush=True)
     other = None
     if not args.no_fp32 and args.precision == "bf16":
-        o = run_gpu("fp32", max(1, min(args.steps, 2)), 0)
+        o = run_gpu(wl, "fp32", max(1, min(args.steps, 2)), 0)
         other = {"dtype": "fp32", "value": o["value"], "ms_per_step": o["ms_per_step"],
                  "roofline_frac": o["frac"], "achieved_tflops": o["achieved_tflops"]}
         print(f"# gpu fp32: {o['value']:.4g} cell-updates/s", file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None if args.no_cpu else cpu_baseline(wl)
+    H = W = wl["grid"]
     line = {
         "metric": "cell-updates/sec on 1 MI355X (9x9 K=128 D=256) + % of roofline",
         "value": res["value"],
@@ -194,25 +268,19 @@ def main():
         "dtype": args.precision,
         "data": "synthetic",
         "config": {
-            "workload": "sudoku 9x9: 256 boards x K=128 trials = 32768 rows, D=256 steps, "
-                        "C=64, 4 kernels, MLP 256-256-64, p_fire=0.5, conf@K selection",
+            "workload": wl["desc"],
             "rows": res["rows"],
-            "grid": [GRID, GRID],
-            "depth": DEPTH,
-            "k_trials": K_TRIALS,
+            "grid": [H, W],
+            "depth": wl["depth"],
+            "k_trials": wl["k"],
         },
-        "roofline": {
-            "bound": "mfma",
-            "achieved": res["achieved_tflops"],
-            "peak": PEAK_TFLOPS[args.precision],
-            "unit": "TFLOP/s",
-            "frac": res["frac"],
-            "traffic": traffic_from_profiles(args.precision),
-        },
+        "roofline": roofline(args.workload, wl, args.precision, res),
         "cpu_baseline": cpu,
         "kernel_ms": res["kernel_ms"],
         "secondary": other,
     }
+    if args.workload != "sudoku9":
+        line["metric"] = f"cell-updates/sec on 1 MI355X ({H}x{W} {args.workload})"
     if cpu:
         line["speedup_vs_cpu"] = res["value"] / cpu["value"]
     print(json.dumps(line), flush=True)

@@ -114,16 +114,17 @@ int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int
                 float *conf_out, int32_t *fired_out, void *stream);
 
 /* Bytes of workspace that nca_rollout_ws needs for this call shape: 0 when the rows fit the
- * LDS-resident kernels (the whole rollout runs in one launch), else one state buffer
- * (rows * C * H * W * 4 bytes) for the halo-tiled per-step path. */
+ * LDS-resident kernels (the whole rollout runs in one launch), else two state buffers
+ * (2 * rows * C * H * W * 4 bytes) for the halo-tiled per-step path. */
 size_t nca_rollout_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height,
                                    int32_t width);
 
 /* nca_rollout with a caller-owned device workspace. Grids whose rows do not fit the resident
- * kernels run one halo-tiled launch per step, alternating between x_out and the workspace so
- * that the last step lands in x_out; they need workspace_bytes >= nca_rollout_workspace_bytes
- * unless n_steps == 1 and x_out does not alias x_in. The workspace must not overlap x_in or
- * x_out. The arithmetic per cell is the generic resident kernel's (nca_set_kernel_path(1)). */
+ * kernels run one halo-tiled launch per step: the first step reads x_in, the steps in between
+ * keep the state in the workspace (cell-major, two buffers), the last writes x_out. They need
+ * workspace_bytes >= nca_rollout_workspace_bytes (one state buffer suffices for n_steps == 2
+ * or an in-place single step, none for an out-of-place single step). The workspace must not
+ * overlap x_in or x_out. The arithmetic per cell is the generic resident kernel's (nca_set_kernel_path(1)). */
 int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
                    int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
                    float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,

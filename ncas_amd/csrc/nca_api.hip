@@ -295,22 +295,23 @@ bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
     return pa < pb + nb && pb < pa + na;
 }
 
-// The per-step path: n_steps launches of the halo-tiled kernel, ping-ponging between x_out and
-// the workspace so that the last step lands in x_out; then the final board confidence.
+// The per-step path: n_steps launches of the halo-tiled kernel. The first step reads the
+// caller's NCHW x_in and the last writes NCHW x_out; the steps in between alternate between the
+// two halves A, B of the workspace in cell-major order. One step in place goes through A.
 int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st, void *ws, size_t ws_bytes) {
     const size_t sb = state_bytes(d, p.rows, p.H, p.W);
     const int n = p.n_steps;
     const bool alias = p.x_in == p.x_out;
     if (!alias && overlaps(p.x_in, sb, p.x_out, sb))
         return fail(NCA_ERR_INVALID, "x_in and x_out overlap without being the same buffer");
-    float *wsf = static_cast<float *>(ws);
-    if (n > 1 || (n == 1 && alias)) {
-        if (!ws || ws_bytes < sb)
+    const size_t need = n >= 3 ? 2 * sb : (n == 2 || (n == 1 && alias)) ? sb : 0;
+    if (need) {
+        if (!ws || ws_bytes < need)
             return fail(NCA_ERR_UNSUPPORTED,
                         "a %d-step rollout of a %dx%d grid with C=%d runs step by step and needs a "
                         "workspace of %zu bytes (nca_rollout_workspace_bytes, nca_rollout_ws)",
-                        n, p.H, p.W, d->channels, sb);
-        if (overlaps(ws, sb, p.x_in, sb) || overlaps(ws, sb, p.x_out, sb))
+                        n, p.H, p.W, d->channels, need);
+        if (overlaps(ws, need, p.x_in, sb) || overlaps(ws, need, p.x_out, sb))
             return fail(NCA_ERR_INVALID, "the workspace overlaps x_in or x_out");
     }
     if (p.fired_out) {
@@ -319,6 +320,8 @@ int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t s
         int rc = hip_check(hipGetLastError(), "fill launch");
         if (rc) return rc;
     }
+    float *A = static_cast<float *>(ws);
+    float *B = A ? A + sb / sizeof(float) : nullptr;
     if (n == 0) {
         if (!alias) {
             int rc = hip_check(hipMemcpyAsync(p.x_out, p.x_in, sb, hipMemcpyDeviceToDevice, st), "state copy");
@@ -327,17 +330,15 @@ int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t s
     } else {
         const float *src = p.x_in;
         for (int s = 0; s < n; ++s) {
-            float *dst;
-            if (!alias || n % 2 == 0)
-                dst = ((n - 1 - s) % 2 == 0) ? p.x_out : wsf;
-            else
-                dst = (s % 2 == 0) ? wsf : p.x_out;
+            const bool last = s == n - 1;
+            float *dst = last ? (alias && n == 1 ? A : p.x_out) : ((s & 1) ? B : A);
             nca::RolloutParams q = p;
             q.x_in = src;
             q.x_out = dst;
             q.noise = s == 0 ? p.noise : nullptr;
             bool ok = false;
-            int rc = hip_check(nca::tiled_step(d->channels, d->hidden, d->precision == NCA_BF16, q, s, s == 0, st, &ok),
+            int rc = hip_check(nca::tiled_step(d->channels, d->hidden, d->precision == NCA_BF16, q, s, s == 0,
+                                               s == 0, last, st, &ok),
                                "tiled step launch");
             if (rc) return rc;
             if (!ok)
@@ -436,7 +437,7 @@ int nca_set_kernel_path(int path) {
 size_t nca_rollout_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width) {
     if (check_cell(cell) || check_grid(rows, height, width)) return 0;
     if (takes_resident(cell, rows, height, width)) return 0;
-    return state_bytes(cell, rows, height, width);
+    return 2 * state_bytes(cell, rows, height, width);
 }
 
 size_t nca_packed_weights_bytes(const nca_cell_desc *cell) {

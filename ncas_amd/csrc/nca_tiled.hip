@@ -20,11 +20,11 @@ int cu_count() {
 }
 
 // Window TW = min(W, 32) (a 128-byte row segment of one channel), TH the largest height up to
-// 512 / TW cells whose LDS plan fits.
+// 1024 / TW cells whose LDS plan fits.
 template <int C, int HD, bool BF16>
 bool choose_window(int H, int W, int c_out, int n_out, int *TH, int *TW, TiledPlan *L) {
     const int tw = W < 32 ? W : 32;
-    int th = 512 / tw;
+    int th = 1024 / tw;
     if (th > H) th = H;
     if (th < 1) th = 1;
     for (; th >= 1; --th) {
@@ -39,7 +39,8 @@ bool choose_window(int H, int W, int c_out, int n_out, int *TH, int *TW, TiledPl
 }
 
 template <int C, int HD, bool BF16, bool NOISE>
-hipError_t launch(const RolloutParams &p, int step, int first, hipStream_t st, bool *ok) {
+hipError_t launch(const RolloutParams &p, int step, int first, int in_nchw, int out_nchw, hipStream_t st,
+                  bool *ok) {
     TiledParams tp;
     memset(&tp, 0, sizeof(tp));
     TiledPlan L;
@@ -48,6 +49,8 @@ hipError_t launch(const RolloutParams &p, int step, int first, hipStream_t st, b
     tp.a = p;
     tp.step = step;
     tp.first = first;
+    tp.in_nchw = in_nchw;
+    tp.out_nchw = out_nchw;
     tp.tiles_y = (p.H + tp.TH - 1) / tp.TH;
     tp.tiles_x = (p.W + tp.TW - 1) / tp.TW;
     tp.n_windows = p.rows * tp.tiles_y * tp.tiles_x;
@@ -72,19 +75,23 @@ hipError_t launch(const RolloutParams &p, int step, int first, hipStream_t st, b
 }
 
 template <int C, int HD>
-hipError_t launch_cell(bool bf16, const RolloutParams &p, int step, int first, hipStream_t st, bool *ok) {
-    if (bf16) return p.noise ? launch<C, HD, true, true>(p, step, first, st, ok) : launch<C, HD, true, false>(p, step, first, st, ok);
-    return p.noise ? launch<C, HD, false, true>(p, step, first, st, ok) : launch<C, HD, false, false>(p, step, first, st, ok);
+hipError_t launch_cell(bool bf16, const RolloutParams &p, int step, int first, int in_nchw, int out_nchw,
+                       hipStream_t st, bool *ok) {
+    if (bf16)
+        return p.noise ? launch<C, HD, true, true>(p, step, first, in_nchw, out_nchw, st, ok)
+                       : launch<C, HD, true, false>(p, step, first, in_nchw, out_nchw, st, ok);
+    return p.noise ? launch<C, HD, false, true>(p, step, first, in_nchw, out_nchw, st, ok)
+                   : launch<C, HD, false, false>(p, step, first, in_nchw, out_nchw, st, ok);
 }
 
 }  // namespace
 
-hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, hipStream_t st,
-                      bool *ok) {
+hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, int in_nchw,
+                      int out_nchw, hipStream_t st, bool *ok) {
     *ok = false;
-    if (C == 16 && HD == 128) return launch_cell<16, 128>(bf16, p, step, first, st, ok);
-    if (C == 32 && HD == 256) return launch_cell<32, 256>(bf16, p, step, first, st, ok);
-    if (C == 64 && HD == 256) return launch_cell<64, 256>(bf16, p, step, first, st, ok);
+    if (C == 16 && HD == 128) return launch_cell<16, 128>(bf16, p, step, first, in_nchw, out_nchw, st, ok);
+    if (C == 32 && HD == 256) return launch_cell<32, 256>(bf16, p, step, first, in_nchw, out_nchw, st, ok);
+    if (C == 64 && HD == 256) return launch_cell<64, 256>(bf16, p, step, first, in_nchw, out_nchw, st, ok);
     return hipSuccess;
 }
 

@@ -120,7 +120,7 @@ def test_workspace_query_and_refusal_without_workspace(lib):
     buffer, and a multi-step call without it is refused before any device work."""
     c16 = _cell(channels=16, hidden=128, c_in=4, c_out=4, out_offset=4, n_out=4, padding=1)
     assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell()), 32768, 9, 9) == 0
-    assert lib.nca_rollout_workspace_bytes(ctypes.byref(c16), 16, 201, 201) == 16 * 16 * 201 * 201 * 4
+    assert lib.nca_rollout_workspace_bytes(ctypes.byref(c16), 16, 201, 201) == 2 * 16 * 16 * 201 * 201 * 4
     assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell(channels=48)), 4, 9, 9) == 0
     fire = _lib.FireDesc(seed=1, p_fire=0.5)
     p = ctypes.c_void_p(1 << 20)
@@ -131,7 +131,7 @@ def test_workspace_query_and_refusal_without_workspace(lib):
                          ctypes.byref(fire), 3, None, None, None, None)
     assert rc == _lib.NCA_ERR_UNSUPPORTED
     assert lib.nca_set_kernel_path(2) == _lib.NCA_OK
-    assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell()), 8, 9, 9) == 8 * 64 * 81 * 4
+    assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell()), 8, 9, 9) == 2 * 8 * 64 * 81 * 4
     assert lib.nca_set_kernel_path(0) == _lib.NCA_OK
 
 

@@ -182,7 +182,7 @@ def test_tiled_workspace_alias_and_errors():
     B, C, H, W = x.shape
     xd, g8, cd = x.to(DEV), g4.to(torch.uint8).to(DEV), cl.to(DEV)
     ws_bytes = L.nca_rollout_workspace_bytes(ctypes.byref(pk.desc), B, H, W)
-    assert ws_bytes == B * C * H * W * 4
+    assert ws_bytes == 2 * B * C * H * W * 4
     ws = torch.empty(ws_bytes // 4, device=DEV)
     st = _lib.stream_of(DEV)
     fd = fire_desc(4, 0.5)
@@ -193,14 +193,22 @@ def test_tiled_workspace_alias_and_errors():
                                 None, None, None, None if work is None else work.data_ptr(),
                                 nbytes, st)
 
-    for n in (1, 2, 3, 4):
+    refs = {0: xd}
+    for n in (1, 2, 3, 4, 5):
         ref = torch.empty_like(xd)
         assert run(xd, ref, n) == 0
         inplace = xd.clone()
         assert run(inplace, inplace, n) == 0
         torch.cuda.synchronize()
         assert torch.equal(ref, inplace), n
+        assert not torch.equal(ref, refs[n - 1]), n
+        refs[n] = ref
+    half = torch.empty_like(xd)
+    assert run(xd, half, 2, ws, ws_bytes // 2) == 0  # two steps need one buffer
+    torch.cuda.synchronize()
+    assert torch.equal(half, refs[2])
     out = torch.empty_like(xd)
+    assert run(xd, out, 3, ws, ws_bytes // 2) == _lib.NCA_ERR_UNSUPPORTED
     assert run(xd, out, 3, None, 0) == _lib.NCA_ERR_UNSUPPORTED
     assert b"workspace" in L.nca_last_error()
     assert run(xd, out, 1, None, 0) == 0  # one out-of-place step needs none
