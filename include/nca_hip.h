@@ -29,6 +29,14 @@
  *   nca_readout       <- NCA.scores / confidence / board_confidence / decode
  *                        (src/nca/model.py:596-633)
  *   nca_conf_select   <- conf_at_k's per-board selection (src/nca/rollout.py:317-334)
+ *   nca_bptt_forward  <- the BPTT chunk's forward in Engine.train_iteration (run_steps with grad,
+ *                        src/nca/engine/engine.py:478-489 -> run_block, step.py:212-246): the
+ *                        chunk's states, kept instead of autograd's per-step activations
+ *   nca_bptt_backward <- its backward ((loss * scale).backward(), engine.py:497, through
+ *                        _FusedCellUpdate.backward ops.py:269-294, the MLP and the shared-kernel
+ *                        perception backward ops.py:79-94) with the loss of step.py:243-245 /
+ *                        train.py:183-207 normalised as in engine.py:490
+ *   nca_bptt_workspace_bytes <- nothing in the reference (autograd allocates); workspace size
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -152,6 +160,50 @@ int nca_readout(const nca_cell_desc *cell, const void *packed, int64_t rows, int
  * counts as -inf; alive may be NULL). conf (N, K) fp32, best (N) int32. */
 int nca_conf_select(const float *conf, const uint8_t *alive, int32_t n_boards, int32_t k_trials,
                     int32_t k, int32_t *best, void *stream);
+
+/* Gradients of the cell's parameters, fp32 device buffers in the reference's layouts. */
+typedef struct nca_cell_grads {
+    float *kernels; /* (heads, 1, 3, 3) */
+    float *w1;      /* (hidden, F, 1, 1) */
+    float *b1;      /* (hidden) */
+    float *w2;      /* (C, hidden, 1, 1) */
+    float *b2;      /* (C) */
+    float *head_w;  /* (n_out, c_out, 1, 1) */
+    float *head_b;  /* (n_out) */
+} nca_cell_grads;
+
+/* The chunk loss: sum_t w_t * step_loss(x_{t+1}) / max(sum_t w_t, 1), step_loss = the mean over
+ * cells (or the loss_mask-weighted mean, sum(l * mask) / max(sum(mask), 1)) of the per-cell
+ * cross-entropy of the mlp head's logits against the target class. */
+typedef struct nca_bptt_loss {
+    const int32_t *targets;     /* device (rows, H, W) class index in [0, n_out) */
+    const float *loss_mask;     /* device (rows, H, W) or NULL */
+    const float *step_weights;  /* host (n_chunk): loss weight of each chunk step */
+} nca_bptt_loss;
+
+/* Workspace bytes of nca_bptt_backward for this shape (0 if the cell is unsupported). */
+size_t nca_bptt_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height,
+                                int32_t width, int32_t n_chunk);
+
+/* Forward of a BPTT chunk: states (n_chunk + 1, rows, C, H, W) receives x0 and the state after
+ * every step (the same kernels and results as nca_rollout, one step per call). fire->adaptive
+ * must be 0. States are all that the backward needs: it recomputes everything else. */
+int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                     int32_t width, const float *x0, const uint8_t *given, const float *clamp,
+                     const nca_fire_desc *fire, int32_t n_chunk, float *states, void *stream);
+
+/* Backward of the chunk whose forward wrote `states` (same cell, packed weights, fire desc).
+ * w->w1 and w->w2 are the fp32 master weights (rounded to bf16 on load for bf16 cells, as the
+ * forward used them). grad_final (rows, C, H, W), the gradient of a later loss w.r.t. the last
+ * state, may be NULL (zero). Writes the parameter gradients of the chunk loss into `grads`
+ * (overwritten, not accumulated), grad_x0 (rows, C, H, W; may be NULL), and the loss value into
+ * loss_out (device scalar; may be NULL). Deterministic: every sum has a fixed order. */
+int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_cell_weights *w,
+                      int64_t rows, int32_t height, int32_t width, const float *states,
+                      const uint8_t *given, const nca_fire_desc *fire, int32_t n_chunk,
+                      const nca_bptt_loss *loss, const float *grad_final, nca_cell_grads *grads,
+                      float *grad_x0, float *loss_out, void *workspace, size_t workspace_bytes,
+                      void *stream);
 
 /* Last error message of the calling thread ("" if none). */
 const char *nca_last_error(void);

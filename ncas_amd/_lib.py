@@ -31,6 +31,9 @@ EXPORTS = (
     "nca_last_error",
     "nca_version",
     "nca_set_kernel_path",
+    "nca_bptt_workspace_bytes",
+    "nca_bptt_forward",
+    "nca_bptt_backward",
 )
 
 
@@ -78,6 +81,15 @@ class FireDesc(ctypes.Structure):
     ]
 
 
+class CellGrads(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")]
+
+
+class BpttLoss(ctypes.Structure):
+    _fields_ = [("targets", ctypes.c_void_p), ("loss_mask", ctypes.c_void_p),
+                ("step_weights", ctypes.c_void_p)]
+
+
 _lib = None
 
 
@@ -113,6 +125,15 @@ def load():
     L.nca_fire_mask.argtypes = [i64, i32, i32, ctypes.POINTER(FireDesc), i64, vp, vp, vp, vp]
     L.nca_readout.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, vp]
     L.nca_conf_select.argtypes = [vp, vp, i32, i32, i32, vp, vp]
+    L.nca_bptt_workspace_bytes.argtypes = [ctypes.POINTER(CellDesc), i64, i32, i32, i32]
+    L.nca_bptt_workspace_bytes.restype = ctypes.c_size_t
+    L.nca_bptt_forward.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp,
+                                   ctypes.POINTER(FireDesc), i32, vp, vp]
+    L.nca_bptt_backward.argtypes = [
+        ctypes.POINTER(CellDesc), vp, ctypes.POINTER(CellWeights), i64, i32, i32, vp, vp,
+        ctypes.POINTER(FireDesc), i32, ctypes.POINTER(BpttLoss), vp, ctypes.POINTER(CellGrads), vp,
+        vp, vp, ctypes.c_size_t, vp,
+    ]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
     L.nca_set_kernel_path.argtypes = [ctypes.c_int]

@@ -29,6 +29,7 @@ SOURCES = {
     # pinned to AGPRs), so the VALU work on them needs no v_accvgpr copies
     "nca_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_tiled.hip": [],
+    "nca_bptt.hip": [],
 }
 
 

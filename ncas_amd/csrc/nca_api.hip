@@ -13,6 +13,7 @@
 #include "nca_rollout.h"
 #include "nca_stream.h"
 #include "nca_tiled_launch.h"
+#include "nca_status.h"
 
 namespace {
 
@@ -33,6 +34,18 @@ int hip_check(hipError_t e, const char *what) {
 }
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace
+
+namespace nca {
+
+int set_error(int code, const char *msg) { return fail(code, "%s", msg); }
+void clear_error() { g_err[0] = 0; }
+int hip_status(hipError_t e, const char *what) { return hip_check(e, what); }
+
+}  // namespace nca
+
+namespace {
 
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per workgroup
 

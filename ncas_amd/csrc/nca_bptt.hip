@@ -1,0 +1,702 @@
+// BPTT of an NCA chunk on gfx950 (nca_bptt_forward / nca_bptt_backward, include/nca_hip.h).
+//
+// Forward: the chunk's steps run on the rollout kernels one step per call, and every state of
+// the chunk is kept (n + 1 states); nothing else is stored. Backward: the steps are walked in
+// reverse; each step recomputes its perception z and hidden activation h from the saved state
+// (the forward's rounding points for bf16 cells) instead of reading stored activations:
+//
+//   front      per cell: the loss gradient of the step's output state (cross-entropy of the
+//              mlp head's logits, reference src/nca/train.py:183-207, weighted as in
+//              src/nca/engine/step.py:243-245 and normalised as in engine.py:490), plus the
+//              gradient arriving from the next step; the clamp's backward zeroes the input
+//              slice of given cells (ops.py:276-294): g_u; the fire mask gives g_dx = g_u * fire
+//   stencil_z  z = perception of the saved state (feature-major, F x cells)
+//   GEMMs      h = relu(W1 z + b1); g_a = (W2^T g_dx) * [h > 0]; g_z = W1^T g_a  (fp32 MFMA)
+//   stencil_t  g_x = g_u + the transposed stencil of g_z (padding-aware: wall / zero halos take
+//              no gradient, wrap halos give it to the wrapped cell), the next step's gradient
+//   partials   dW1 = g_a z^T, dW2 = g_dx h^T, db1, db2, dkernels, dhead: split-K partial sums over
+//              32 fixed cell ranges, added into one accumulator per step in a fixed order
+//
+// so the gradients are deterministic (the same bits on every run). Gradients are the exact fp32
+// gradients of the forward as computed: for bf16 cells the rounding points are straight-through
+// (derivative 1), and the backward uses the forward's bf16-rounded weights and inputs.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "nca_hip.h"
+#include "nca_device.h"
+#include "nca_layout.h"
+#include "nca_status.h"
+
+namespace {
+
+constexpr int kSplit = 32;   // cell ranges of the split-K weight-gradient sums
+constexpr int kThreads = 256;
+
+struct Dims {
+    int C, F, HD, c_in, in_off, c_out, out_off, n_out, padding, bf16;
+    int H, W, HW;
+    int64_t rows, M;  // M = rows * HW cells
+};
+
+// Offsets (floats) of every gradient in one flat parameter vector: kernels, w1, b1, w2, b2,
+// head_w, head_b.
+struct ParamLayout {
+    int64_t K, W1, B1, W2, B2, HW, HB, P;
+};
+
+ParamLayout param_layout(const Dims &d) {
+    ParamLayout L;
+    int64_t o = 0;
+    L.K = o;
+    o += 4 * 9;
+    L.W1 = o;
+    o += (int64_t)d.HD * d.F;
+    L.B1 = o;
+    o += d.HD;
+    L.W2 = o;
+    o += (int64_t)d.C * d.HD;
+    L.B2 = o;
+    o += d.C;
+    L.HW = o;
+    o += (int64_t)d.n_out * d.c_out;
+    L.HB = o;
+    o += d.n_out;
+    L.P = o;
+    return L;
+}
+
+// Workspace (floats, 64-float aligned pieces).
+struct WsLayout {
+    int64_t Z, Hb, Ga, Gz, Gdx, GL, Gu, Gx0, Gx1, part, acc, lossp, denom, total;
+    int front_blocks;
+};
+
+WsLayout ws_layout(const Dims &d, int n) {
+    const ParamLayout P = param_layout(d);
+    auto al = [](int64_t v) { return (v + 63) & ~(int64_t)63; };
+    WsLayout L;
+    int64_t o = 0;
+    L.Z = o;
+    o = al(o + (int64_t)d.F * d.M);
+    L.Hb = o;
+    o = al(o + (int64_t)d.HD * d.M);
+    L.Ga = o;
+    o = al(o + (int64_t)d.HD * d.M);
+    L.Gz = o;
+    o = al(o + (int64_t)d.F * d.M);
+    L.Gdx = o;
+    o = al(o + (int64_t)d.C * d.M);
+    L.GL = o;
+    o = al(o + (int64_t)d.n_out * d.M);
+    L.Gu = o;
+    o = al(o + (int64_t)d.C * d.M);
+    L.Gx0 = o;
+    o = al(o + (int64_t)d.C * d.M);
+    L.Gx1 = o;
+    o = al(o + (int64_t)d.C * d.M);
+    L.part = o;
+    o = al(o + (int64_t)kSplit * P.P);
+    L.acc = o;
+    o = al(o + P.P);
+    L.front_blocks = (int)((d.M + kThreads - 1) / kThreads);
+    L.lossp = o;
+    o = al(o + (int64_t)(n > 0 ? n : 1) * L.front_blocks);
+    L.denom = o;
+    o = al(o + 1);
+    L.total = o;
+    return L;
+}
+
+// The neighbour of cell (i, j) at (i + dy, j + dx): its cell index, or -1 for a constant halo
+// cell (wall / zero padding); wrap padding wraps around (reference src/nca/model.py:140-152).
+__device__ __forceinline__ int neighbour(int i, int j, int dy, int dx, int H, int W, int padding) {
+    int a = i + dy, b = j + dx;
+    if (a >= 0 && a < H && b >= 0 && b < W) return a * W + b;
+    if (padding != 2) return -1;
+    a = (a + H) % H;
+    b = (b + W) % W;
+    return a * W + b;
+}
+
+// Block-wide sum of one float per thread in a fixed tree order (deterministic).
+__device__ float block_sum(float v, float *red) {
+    const int t = threadIdx.x;
+    red[t] = v;
+    __syncthreads();
+    for (int s = kThreads / 2; s > 0; s >>= 1) {
+        if (t < s) red[t] = __fadd_rn(red[t], red[t + s]);
+        __syncthreads();
+    }
+    const float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+__global__ void zero_f32(float *p, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0.0f;
+}
+
+// denom = max(sum of the loss mask, 1) in a fixed order (train.py:204-205).
+__global__ void mask_sum(const float *mask, int64_t n, float *out) {
+    __shared__ float red[kThreads];
+    float s = 0.0f;
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) s = __fadd_rn(s, mask[i]);
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) *out = s < 1.0f ? 1.0f : s;
+}
+
+struct FrontArgs {
+    Dims d;
+    const float *x1;        // the step's output state (rows, C, H, W)
+    const float *gin;       // gradient w.r.t. x1 from the later steps, or null
+    const uint8_t *given;   // (rows, HW)
+    const int32_t *targets;  // (rows, HW)
+    const float *mask;      // (rows, HW) or null
+    const float *denom;     // device scalar: max(sum(mask), 1), used with mask
+    float wscale;           // w_t / sum(w) (/ M without a mask); 0: the step has no loss term
+    const float *head_w, *head_b;
+    // fire mask of the step
+    const uint8_t *fire_u8;  // (rows, HW) slice of the injected masks, or null
+    const uint64_t *key_ptr;  // per-step Philox key (device), or null: key
+    uint64_t key;
+    int64_t row0;
+    uint32_t step;
+    float p;
+    float *Gu, *Gdx, *GL, *lossp;
+};
+
+__global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
+    __shared__ float red[kThreads];
+    const Dims &d = a.d;
+    const int64_t m = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+    float lossc = 0.0f;
+    if (m < d.M) {
+        const int64_t row = m / d.HW;
+        const int q = (int)(m - row * d.HW);
+        float f;
+        if (a.fire_u8) {
+            f = a.fire_u8[m] ? 1.0f : 0.0f;
+        } else {
+            float u[4];
+            nca::cell_uniforms4(a.key_ptr ? *a.key_ptr : a.key, (uint32_t)(a.row0 + row), a.step, (uint32_t)(q >> 2), u);
+            const int e4 = q & 3;
+            const float uq = e4 == 0 ? u[0] : e4 == 1 ? u[1] : e4 == 2 ? u[2] : u[3];
+            f = uq < a.p ? 1.0f : 0.0f;
+        }
+        const bool gv = a.given[m] != 0;
+        const float *x1 = a.x1 + row * d.C * (int64_t)d.HW + q;
+        // logits, softmax and the cross-entropy gradient (n_out <= 16; static register indices)
+        float gl[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) gl[v] = 0.0f;
+        if (a.wscale != 0.0f) {
+            const float scale = a.mask ? a.wscale * a.mask[m] / *a.denom : a.wscale;
+            float l[16];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                l[v] = 0.0f;
+                if (v < d.n_out) {
+                    float acc = a.head_b[v];
+                    for (int c = 0; c < d.c_out; ++c)
+                        acc = __builtin_fmaf(a.head_w[v * d.c_out + c], x1[(int64_t)(d.out_off + c) * d.HW], acc);
+                    l[v] = acc;
+                    mx = fmaxf(mx, acc);
+                }
+            }
+            float s = 0.0f, lt = mx;
+            const int tgt = a.targets[m];
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (v < d.n_out) {
+                    s += expf(l[v] - mx);
+                    if (v == tgt) lt = l[v];
+                }
+            lossc = (mx + logf(s) - lt) * scale;
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (v < d.n_out) gl[v] = (expf(l[v] - mx) / s - (v == tgt ? 1.0f : 0.0f)) * scale;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            if (v < d.n_out) a.GL[v * d.M + m] = gl[v];
+        const float *gin = a.gin ? a.gin + row * d.C * (int64_t)d.HW + q : nullptr;
+        float *gu = a.Gu + row * d.C * (int64_t)d.HW + q;
+        for (int c = 0; c < d.C; ++c) {
+            float g = gin ? gin[(int64_t)c * d.HW] : 0.0f;
+            const int co = c - d.out_off;
+            if (co >= 0 && co < d.c_out) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    if (v < d.n_out) g = __builtin_fmaf(a.head_w[v * d.c_out + co], gl[v], g);
+            }
+            if (gv && c >= d.in_off && c < d.in_off + d.c_in) g = 0.0f;
+            gu[(int64_t)c * d.HW] = g;
+            a.Gdx[c * d.M + m] = g * f;
+        }
+    }
+    const float s = block_sum(lossc, red);
+    if (threadIdx.x == 0) a.lossp[blockIdx.x] = s;
+}
+
+// The perception input of tap (dy, dx) of cell (i, j), channel c of row xr: the state (or the
+// halo value), rounded to bf16 for bf16 cells like the forward's perception buffer.
+__device__ __forceinline__ float tap_value(const float *xr, const Dims &d, int i, int j, int dy, int dx, int c,
+                                           const float *padv) {
+    const int nq = neighbour(i, j, dy, dx, d.H, d.W, d.padding);
+    float v = nq >= 0 ? xr[nq] : (d.padding == 1 ? padv[c] : 0.0f);
+    return d.bf16 ? nca::round_bf16(v) : v;
+}
+
+// z (F x M, feature-major) of the state x (rows, C, H, W); one thread per (row, channel, cell).
+__global__ void __launch_bounds__(kThreads) stencil_z_kernel(Dims d, const float *x, const float *kern,
+                                                             const float *padv, float *Z) {
+    const int64_t e = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+    if (e >= d.rows * d.C * (int64_t)d.HW) return;
+    const int64_t row = e / ((int64_t)d.C * d.HW);
+    const int rem = (int)(e - row * d.C * (int64_t)d.HW), c = rem / d.HW, q = rem - c * d.HW;
+    const int i = q / d.W, j = q - i * d.W;
+    const float *xr = x + (row * d.C + c) * (int64_t)d.HW;
+    float xv[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
+    const int64_t m = row * d.HW + q;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
+        Z[(int64_t)(k * d.C + c) * d.M + m] = d.bf16 ? nca::round_bf16(acc) : acc;
+    }
+}
+
+// g_x = g_u + transposed stencil of g_z, one thread per (row, channel, cell) in NCHW order.
+__global__ void __launch_bounds__(kThreads) stencil_t_kernel(Dims d, const float *Gu, const float *Gz,
+                                                             const float *kern, float *gx) {
+    const int64_t e = blockIdx.x * (int64_t)kThreads + threadIdx.x;
+    if (e >= d.rows * d.C * (int64_t)d.HW) return;
+    const int64_t row = e / ((int64_t)d.C * d.HW);
+    const int rem = (int)(e - row * d.C * (int64_t)d.HW), c = rem / d.HW, q = rem - c * d.HW;
+    const int i = q / d.W, j = q - i * d.W;
+    float g = Gu[e];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        // cell q' whose tap t reads this cell: q = q' + (dy, dx)
+        const int qs = neighbour(i, j, -(t / 3 - 1), -(t % 3 - 1), d.H, d.W, d.padding);
+        if (qs < 0) continue;
+        const int64_t ms = row * d.HW + qs;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], Gz[(int64_t)(k * d.C + c) * d.M + ms], g);
+    }
+    gx[e] = g;
+}
+
+// dkernels partials: block s sums g_z[k C + c][m] * xp[c][m + tap] over its cell range.
+__global__ void __launch_bounds__(kThreads) dkern_kernel(Dims d, const float *x, const float *Gz, const float *padv,
+                                                         float *part, int64_t P, int64_t offK) {
+    __shared__ float red[kThreads];
+    const int s = blockIdx.x;
+    const int64_t per = (d.M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < d.M ? m0 + per : d.M;
+    float acc[36];
+#pragma unroll
+    for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
+    const int64_t items = m1 > m0 ? (m1 - m0) * d.C : 0;
+    for (int64_t it = threadIdx.x; it < items; it += kThreads) {
+        const int c = (int)(it % d.C);
+        const int64_t m = m0 + it / d.C, row = m / d.HW;
+        const int q = (int)(m - row * d.HW), i = q / d.W, j = q - i * d.W;
+        const float *xr = x + (row * d.C + c) * (int64_t)d.HW;
+        float xv[9];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float gz = Gz[(int64_t)(k * d.C + c) * d.M + m];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gz, xv[t], acc[k * 9 + t]);
+        }
+    }
+    for (int v = 0; v < 36; ++v) {
+        const float r = block_sum(acc[v], red);
+        if (threadIdx.x == 0) part[s * P + offK + v] = r;
+    }
+}
+
+// dhead partials: pair p < n_out c_out is (v, c): sum g_l[v] x1[out_off + c]; pair n_out c_out + v
+// is the bias: sum g_l[v]; block s over its cell range, cells in order.
+__global__ void __launch_bounds__(kThreads) dhead_kernel(Dims d, const float *x1, const float *GL, float *part,
+                                                         int64_t P, int64_t offHW, int64_t offHB) {
+    const int s = blockIdx.x;
+    const int64_t per = (d.M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < d.M ? m0 + per : d.M;
+    const int npw = d.n_out * d.c_out;
+    for (int p = threadIdx.x; p < npw + d.n_out; p += kThreads) {
+        const int v = p < npw ? p / d.c_out : p - npw, c = p < npw ? p - v * d.c_out : -1;
+        float acc = 0.0f;
+        for (int64_t m = m0; m < m1; ++m) {
+            const float g = GL[v * d.M + m];
+            if (c < 0) {
+                acc = __fadd_rn(acc, g);
+            } else {
+                const int64_t row = m / d.HW;
+                const int q = (int)(m - row * d.HW);
+                acc = __builtin_fmaf(g, x1[(row * d.C + d.out_off + c) * (int64_t)d.HW + q], acc);
+            }
+        }
+        part[s * P + (c < 0 ? offHB + v : offHW + p)] = acc;
+    }
+}
+
+// Row sums of a feature-major matrix G (R x M): block (r, s) over cell range s.
+__global__ void __launch_bounds__(kThreads) rowsum_kernel(const float *G, int64_t M, float *part, int64_t P,
+                                                          int64_t off) {
+    __shared__ float red[kThreads];
+    const int r = blockIdx.x, s = blockIdx.y;
+    const int64_t per = (M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < M ? m0 + per : M;
+    float acc = 0.0f;
+    for (int64_t m = m0 + threadIdx.x; m < m1; m += kThreads) acc = __fadd_rn(acc, G[r * M + m]);
+    const float t = block_sum(acc, red);
+    if (threadIdx.x == 0) part[s * P + off + r] = t;
+}
+
+// acc[i] += sum over the kSplit partials in split order.
+__global__ void reduce_acc_kernel(const float *part, int64_t P, float *acc) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < P; i += (int64_t)gridDim.x * blockDim.x) {
+        float s = 0.0f;
+        for (int k = 0; k < kSplit; ++k) s = __fadd_rn(s, part[k * P + i]);
+        acc[i] = __fadd_rn(acc[i], s);
+    }
+}
+
+// The loss of the chunk: sum over steps and front blocks in order.
+__global__ void loss_kernel(const float *lossp, int n, int blocks, float *out) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float s = 0.0f;
+    for (int t = n - 1; t >= 0; --t)
+        for (int b = 0; b < blocks; ++b) s = __fadd_rn(s, lossp[t * blocks + b]);
+    *out = s;
+}
+
+__global__ void copy_kernel(const float *src, float *dst, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+// ------------------------------------------------------------------------------------------
+// fp32 GEMM on v_mfma_f32_16x16x4_f32: C (M x N) = A (M x K) B (K x N) with strided operands
+// (A(m, k) = A[m sam + k sak], B(k, n) = B[k sbk + n sbn], one of each pair of strides being 1),
+// 64 x 64 block tiles, 16-deep k slices through LDS, each of the 4 waves a 32 x 32 quadrant.
+// Split-K: block z sums k in [z kps, (z + 1) kps) and writes its partial at C + z * csplit.
+// Epilogues: 0 store (+ row bias), 1 fc1: bias, bf16 rounding for bf16 cells, ReLU,
+// 2 mask: times [mask(m, n) > 0].
+struct GemmArgs {
+    const float *A;
+    int64_t sam, sak;
+    const float *B;
+    int64_t sbk, sbn;
+    float *Cm;
+    int64_t ldc, csplit;
+    int64_t M, N, K, kps;
+    const float *bias;  // per row m
+    const float *mask;
+    int64_t ldmask;
+    int epi, round_in, round_out;  // round_in: round A to bf16 on load (the forward's bf16 weights)
+};
+
+constexpr int GBM = 64, GBN = 64, GBK = 16;
+
+__global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
+    __shared__ float As[GBK][GBM + 4];
+    __shared__ float Bs[GBK][GBN + 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t m0 = (int64_t)blockIdx.y * GBM, n0 = (int64_t)blockIdx.x * GBN;
+    const int64_t kb = (int64_t)blockIdx.z * g.kps, ke = kb + g.kps < g.K ? kb + g.kps : g.K;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool a_kfast = g.sak == 1, b_nfast = g.sbn == 1;
+    for (int64_t k0 = kb; k0 < ke; k0 += GBK) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int e = tid + 256 * r;
+            const int am = a_kfast ? e >> 4 : e & 63, ak = a_kfast ? e & 15 : e >> 6;
+            const int64_t gm = m0 + am, gk = k0 + ak;
+            float v = 0.0f;
+            if (gm < g.M && gk < ke) v = g.A[gm * g.sam + gk * g.sak];
+            As[ak][am] = g.round_in ? nca::round_bf16(v) : v;
+            const int bn = b_nfast ? e & 63 : e >> 4, bk = b_nfast ? e >> 6 : e & 15;
+            const int64_t gn = n0 + bn, gk2 = k0 + bk;
+            Bs[bk][bn] = (gn < g.N && gk2 < ke) ? g.B[gk2 * g.sbk + gn * g.sbn] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < GBK; kk += 4) {
+            float af[2], bfv[2];
+#pragma unroll
+            for (int a = 0; a < 2; ++a) af[a] = As[kk + (lane >> 4)][wm * 32 + a * 16 + (lane & 15)];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) bfv[b] = Bs[kk + (lane >> 4)][wn * 32 + b * 16 + (lane & 15)];
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[a], bfv[b], acc[a][b], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    float *Cz = g.Cm + (int64_t)blockIdx.z * g.csplit;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int64_t gm = m0 + wm * 32 + a * 16 + 4 * (lane >> 4) + v;
+                const int64_t gn = n0 + wn * 32 + b * 16 + (lane & 15);
+                if (gm >= g.M || gn >= g.N) continue;
+                float r = acc[a][b][v];
+                if (g.bias) r = __fadd_rn(r, g.bias[gm]);
+                if (g.epi == 1) {
+                    if (g.round_out) r = nca::round_bf16(r);
+                    r = r > 0.0f ? r : 0.0f;
+                } else if (g.epi == 2) {
+                    r = g.mask[gm * g.ldmask + gn] > 0.0f ? r : 0.0f;
+                }
+                Cz[gm * g.ldc + gn] = r;
+            }
+}
+
+int gemm(const GemmArgs &g, int splits, hipStream_t st) {
+    const int64_t gx = (g.N + GBN - 1) / GBN, gy = (g.M + GBM - 1) / GBM;
+    if (gx > 0x7fffffff || gy > 65535) return nca::set_error(NCA_ERR_UNSUPPORTED, "GEMM grid too large");
+    hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)gx, (unsigned)gy, (unsigned)splits), dim3(256), 0, st, g);
+    return nca::hip_status(hipGetLastError(), "gemm launch");
+}
+
+int check_dims(const nca_cell_desc *cell, int64_t rows, int32_t H, int32_t W, int32_t n, Dims *d) {
+    if (!cell) return nca::set_error(NCA_ERR_INVALID, "cell descriptor is NULL");
+    if (cell->heads != 4) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT needs 4 perception kernels");
+    if (cell->head_kind != NCA_HEAD_MLP)
+        return nca::set_error(NCA_ERR_UNSUPPORTED, "the BPTT loss is the cross-entropy of an mlp head");
+    if (cell->n_out < 1 || cell->n_out > 16) return nca::set_error(NCA_ERR_UNSUPPORTED, "n_out must be 1..16");
+    if (rows < 0 || H < 1 || W < 1 || n < 0) return nca::set_error(NCA_ERR_INVALID, "bad rows / grid / n_chunk");
+    d->C = cell->channels;
+    d->F = 4 * cell->channels;
+    d->HD = cell->hidden;
+    d->c_in = cell->c_in;
+    d->in_off = cell->in_offset;
+    d->c_out = cell->c_out;
+    d->out_off = cell->out_offset;
+    d->n_out = cell->n_out;
+    d->padding = cell->padding;
+    d->bf16 = cell->precision == NCA_BF16;
+    d->H = H;
+    d->W = W;
+    d->HW = H * W;
+    d->rows = rows;
+    d->M = rows * (int64_t)H * W;
+    if (d->M * (int64_t)(d->F > d->HD ? d->F : d->HD) > ((int64_t)1 << 40))
+        return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT batch too large");
+    return NCA_OK;
+}
+
+unsigned grid_for(int64_t n) {
+    const int64_t b = (n + kThreads - 1) / kThreads;
+    return (unsigned)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t nca_bptt_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width,
+                                int32_t n_chunk) {
+    Dims d;
+    if (nca_packed_weights_bytes(cell) == 0 || check_dims(cell, rows, height, width, n_chunk, &d)) return 0;
+    return (size_t)ws_layout(d, n_chunk).total * sizeof(float);
+}
+
+int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height, int32_t width,
+                     const float *x0, const uint8_t *given, const float *clamp, const nca_fire_desc *fire,
+                     int32_t n_chunk, float *states, void *stream) {
+    nca::clear_error();
+    Dims d;
+    int rc = check_dims(cell, rows, height, width, n_chunk, &d);
+    if (rc) return rc;
+    if (!fire || !states || !x0) return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    if (fire->adaptive) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT chunks fire uniformly (no confidence gating)");
+    const int64_t sn = d.rows * d.C * (int64_t)d.HW;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (rows == 0) return NCA_OK;
+    if (states != x0) {
+        rc = nca::hip_status(hipMemcpyAsync(states, x0, sn * sizeof(float), hipMemcpyDeviceToDevice, st), "state copy");
+        if (rc) return rc;
+    }
+    for (int t = 0; t < n_chunk; ++t) {
+        nca_fire_desc f = *fire;
+        f.step0 = fire->step0 + t;
+        if (fire->step_seeds) f.step_seeds = fire->step_seeds + t;
+        if (fire->fire_in) f.fire_in = fire->fire_in + (int64_t)t * d.rows * d.HW;
+        rc = nca_rollout_ws(cell, packed, rows, height, width, states + t * sn, given, clamp, states + (t + 1) * sn, &f,
+                            1, nullptr, nullptr, nullptr, nullptr, 0, stream);
+        if (rc) return rc;
+    }
+    return NCA_OK;
+}
+
+int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_cell_weights *w, int64_t rows,
+                      int32_t height, int32_t width, const float *states, const uint8_t *given,
+                      const nca_fire_desc *fire, int32_t n_chunk, const nca_bptt_loss *loss,
+                      const float *grad_final, nca_cell_grads *grads, float *grad_x0, float *loss_out,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    nca::clear_error();
+    Dims d;
+    int rc = check_dims(cell, rows, height, width, n_chunk, &d);
+    if (rc) return rc;
+    const size_t pk = nca_packed_weights_bytes(cell);
+    if (pk == 0) return NCA_ERR_UNSUPPORTED;  // message set by the packing check
+    if (!packed || !w || !w->w1 || !w->w2 || !states || !given || !fire || !loss || !grads)
+        return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    if (!grads->kernels || !grads->w1 || !grads->b1 || !grads->w2 || !grads->b2 || !grads->head_w || !grads->head_b)
+        return nca::set_error(NCA_ERR_INVALID, "NULL gradient pointer");
+    if (fire->adaptive) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT chunks fire uniformly (no confidence gating)");
+    if (n_chunk > 0 && (!loss->step_weights || !loss->targets))
+        return nca::set_error(NCA_ERR_INVALID, "the loss needs step_weights and targets");
+    const WsLayout L = ws_layout(d, n_chunk);
+    if (!workspace || workspace_bytes < (size_t)L.total * sizeof(float)) {
+        char msg[160];
+        snprintf(msg, sizeof(msg), "BPTT needs a workspace of %zu bytes (nca_bptt_workspace_bytes)",
+                 (size_t)L.total * sizeof(float));
+        return nca::set_error(NCA_ERR_INVALID, msg);
+    }
+    float wsum = 0.0f;
+    for (int t = 0; t < n_chunk; ++t) wsum += loss->step_weights[t];
+    const float wden = wsum < 1.0f ? 1.0f : wsum;  // weights.sum().clamp_min(1), engine.py:490
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const ParamLayout P = param_layout(d);
+    const nca::PackedLayout PL = nca::packed_layout(d.C, 4, d.HD, d.c_out, d.n_out, d.bf16);
+    const unsigned char *pb = static_cast<const unsigned char *>(packed);
+    const float *kern = reinterpret_cast<const float *>(pb + PL.kern);
+    const float *b1 = reinterpret_cast<const float *>(pb + PL.b1);
+    const float *headw = reinterpret_cast<const float *>(pb + PL.headw);
+    const float *headb = reinterpret_cast<const float *>(pb + PL.headb);
+    const float *padv = reinterpret_cast<const float *>(pb + PL.padv);
+    float *ws = static_cast<float *>(workspace);
+    float *Z = ws + L.Z, *Hb = ws + L.Hb, *Ga = ws + L.Ga, *Gz = ws + L.Gz, *Gdx = ws + L.Gdx, *GL = ws + L.GL;
+    float *Gu = ws + L.Gu, *Gx[2] = {ws + L.Gx0, ws + L.Gx1}, *part = ws + L.part, *acc = ws + L.acc;
+    float *lossp = ws + L.lossp, *denom = ws + L.denom;
+    const int64_t sn = d.rows * d.C * (int64_t)d.HW;
+
+    hipLaunchKernelGGL(zero_f32, dim3(64), dim3(256), 0, st, acc, P.P);
+    hipLaunchKernelGGL(zero_f32, dim3(64), dim3(256), 0, st, lossp, (int64_t)(n_chunk > 0 ? n_chunk : 1) * L.front_blocks);
+    if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
+    if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;
+
+    const float *gin = grad_final;
+    for (int t = n_chunk - 1; t >= 0 && d.M > 0; --t) {
+        const float *xt = states + t * sn, *x1 = states + (t + 1) * sn;
+        float *gx = (t == 0 && grad_x0) ? grad_x0 : Gx[t & 1];
+        // front: loss gradient, clamp and fire
+        FrontArgs fa;
+        memset(&fa, 0, sizeof(fa));
+        fa.d = d;
+        fa.x1 = x1;
+        fa.gin = gin;
+        fa.given = given;
+        fa.targets = loss->targets;
+        fa.mask = loss->loss_mask;
+        fa.denom = denom;
+        const float wt = loss->step_weights[t] / wden;
+        fa.wscale = loss->loss_mask ? wt : wt / (float)d.M;
+        fa.head_w = headw;
+        fa.head_b = headb;
+        fa.fire_u8 = fire->fire_in ? fire->fire_in + (int64_t)t * d.rows * d.HW : nullptr;
+        fa.key_ptr = fire->step_seeds ? fire->step_seeds + t : nullptr;
+        fa.key = fire->seed;
+        fa.row0 = fire->row0;
+        fa.step = (uint32_t)(fire->step0 + t);
+        fa.p = fire->p_fire;
+        fa.Gu = Gu;
+        fa.Gdx = Gdx;
+        fa.GL = GL;
+        fa.lossp = lossp + (int64_t)t * L.front_blocks;
+        hipLaunchKernelGGL(front_kernel, dim3(L.front_blocks), dim3(kThreads), 0, st, fa);
+        // recompute z and h from the saved state
+        hipLaunchKernelGGL(stencil_z_kernel, dim3(grid_for(sn)), dim3(kThreads), 0, st, d, xt, kern, padv, Z);
+        if ((rc = nca::hip_status(hipGetLastError(), "bptt front / stencil"))) return rc;
+        GemmArgs g;
+        memset(&g, 0, sizeof(g));
+        // h = relu(W1 z + b1): (HD x F) (F x M)
+        g.A = w->w1; g.sam = d.F; g.sak = 1;
+        g.B = Z; g.sbk = d.M; g.sbn = 1;
+        g.Cm = Hb; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.F; g.kps = d.F;
+        g.bias = b1; g.epi = 1; g.round_in = d.bf16; g.round_out = d.bf16;
+        if ((rc = gemm(g, 1, st))) return rc;
+        // g_a = (W2^T g_dx) * [h > 0]: (HD x C) (C x M)
+        memset(&g, 0, sizeof(g));
+        g.A = w->w2; g.sam = 1; g.sak = d.HD;
+        g.B = Gdx; g.sbk = d.M; g.sbn = 1;
+        g.Cm = Ga; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.C; g.kps = d.C;
+        g.mask = Hb; g.ldmask = d.M; g.epi = 2; g.round_in = d.bf16;
+        if ((rc = gemm(g, 1, st))) return rc;
+        // g_z = W1^T g_a: (F x HD) (HD x M)
+        memset(&g, 0, sizeof(g));
+        g.A = w->w1; g.sam = 1; g.sak = d.F;
+        g.B = Ga; g.sbk = d.M; g.sbn = 1;
+        g.Cm = Gz; g.ldc = d.M; g.M = d.F; g.N = d.M; g.K = d.HD; g.kps = d.HD;
+        g.round_in = d.bf16;
+        if ((rc = gemm(g, 1, st))) return rc;
+        // gradient of the step's input state
+        hipLaunchKernelGGL(stencil_t_kernel, dim3(grid_for(sn)), dim3(kThreads), 0, st, d, Gu, Gz, kern, gx);
+        // weight-gradient partials over kSplit cell ranges
+        const int64_t kps = (((d.M + kSplit - 1) / kSplit) + GBK - 1) / GBK * GBK;
+        memset(&g, 0, sizeof(g));
+        g.A = Ga; g.sam = d.M; g.sak = 1;  // dW1 = g_a z^T: (HD x M) (M x F)
+        g.B = Z; g.sbk = 1; g.sbn = d.M;
+        g.Cm = part + P.W1; g.ldc = d.F; g.csplit = P.P; g.M = d.HD; g.N = d.F; g.K = d.M; g.kps = kps;
+        if ((rc = gemm(g, kSplit, st))) return rc;
+        memset(&g, 0, sizeof(g));
+        g.A = Gdx; g.sam = d.M; g.sak = 1;  // dW2 = g_dx h^T: (C x M) (M x HD)
+        g.B = Hb; g.sbk = 1; g.sbn = d.M;
+        g.Cm = part + P.W2; g.ldc = d.HD; g.csplit = P.P; g.M = d.C; g.N = d.HD; g.K = d.M; g.kps = kps;
+        if ((rc = gemm(g, kSplit, st))) return rc;
+        hipLaunchKernelGGL(rowsum_kernel, dim3(d.HD, kSplit), dim3(kThreads), 0, st, Ga, d.M, part, P.P, P.B1);
+        hipLaunchKernelGGL(rowsum_kernel, dim3(d.C, kSplit), dim3(kThreads), 0, st, Gdx, d.M, part, P.P, P.B2);
+        hipLaunchKernelGGL(dkern_kernel, dim3(kSplit), dim3(kThreads), 0, st, d, xt, Gz, padv, part, P.P, P.K);
+        hipLaunchKernelGGL(dhead_kernel, dim3(kSplit), dim3(kThreads), 0, st, d, x1, GL, part, P.P, P.HW, P.HB);
+        hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
+        if ((rc = nca::hip_status(hipGetLastError(), "bptt step kernels"))) return rc;
+        gin = gx;
+    }
+    if (grad_x0) {
+        if (n_chunk == 0 || d.M == 0) {
+            if (grad_final) hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, grad_final, grad_x0, sn);
+            else hipLaunchKernelGGL(zero_f32, dim3(256), dim3(256), 0, st, grad_x0, sn);
+        }
+    }
+    // the gradients in the reference's parameter layouts
+    hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.K, grads->kernels, (int64_t)36);
+    hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, acc + P.W1, grads->w1, (int64_t)d.HD * d.F);
+    hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.B1, grads->b1, (int64_t)d.HD);
+    hipLaunchKernelGGL(copy_kernel, dim3(64), dim3(256), 0, st, acc + P.W2, grads->w2, (int64_t)d.C * d.HD);
+    hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(256), 0, st, acc + P.B2, grads->b2, (int64_t)d.C);
+    hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.HW, grads->head_w, (int64_t)d.n_out * d.c_out);
+    hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.HB, grads->head_b, (int64_t)d.n_out);
+    if (loss_out) {
+        if (n_chunk > 0 && d.M > 0)
+            hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(64), 0, st, lossp, n_chunk, L.front_blocks, loss_out);
+        else
+            hipLaunchKernelGGL(zero_f32, dim3(1), dim3(64), 0, st, loss_out, (int64_t)1);
+    }
+    return nca::hip_status(hipGetLastError(), "bptt finish");
+}
+
+}  // extern "C"

@@ -15,7 +15,12 @@ of the reference's maze presets):
                      `x.float()` after every step (engine/step.py:240-242), fire masks drawn
                      from the Philox rule (`oracle/philox.py`) instead of torch's generator;
 * `readout`        - model.py:596-633 through the C restatement (`nca_oracle.c`), whose fixed
-                     operation order is what the GPU readout must match bit for bit.
+                     operation order is what the GPU readout must match bit for bit;
+* `chunk_loss`,
+  `bptt_chunk`     - the BPTT chunk of engine.py:366-517: `n` steps with gradient, loss
+                     sum_t w_t * step_loss(x_{t+1}) / sum_t w_t with the per-cell cross-entropy of
+                     the mlp head's logits (train.py:183-207, step.py:243-245), differentiated by
+                     torch autograd in fp64 (the parameters, and optionally x_0).
 
 Precision modes: "fp32" and "fp64" compute everything in that type. "bf16" reproduces the
 rounding points of the reference under `torch.autocast(bfloat16)` (engine/step.py:240-242,
@@ -97,11 +102,27 @@ def _dtype(precision: str) -> torch.dtype:
     return torch.float64 if precision == "fp64" else torch.float32
 
 
-def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32") -> torch.Tensor:
-    """Perception + MLP: the proposed dx of every cell (model.py:489-495)."""
+class _RoundBF16(torch.autograd.Function):
+    """Round to bf16 with an identity backward: the exact gradient of the rounded forward (the
+    rounding is piecewise constant, so its derivative is taken as 1, i.e. straight-through)."""
+
+    @staticmethod
+    def forward(ctx, t):
+        return t.to(torch.bfloat16).to(t.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g
+
+
+def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32",
+                 dtype: torch.dtype | None = None, ste: bool = False) -> torch.Tensor:
+    """Perception + MLP: the proposed dx of every cell (model.py:489-495). `dtype` overrides the
+    compute type (fp64 for gradients); `ste` makes the bf16 rounding points straight-through."""
     B, C, H, W = x.shape
-    dt = _dtype(precision)
+    dt = dtype or _dtype(precision)
     bf = precision == "bf16"
+    _bf = _RoundBF16.apply if ste else globals()["_bf"]
     x = x.to(dt)
     xp = pad(x, cell.padding, cell.pad_vec.to(dt))
     k = cell.kernels.to(dt)
@@ -132,11 +153,11 @@ def apply_clamp(cell: OracleCell, x, given4, clamp):
     return out
 
 
-def step(cell: OracleCell, x, given4, clamp, fire, precision="fp32", noise=None):
+def step(cell: OracleCell, x, given4, clamp, fire, precision="fp32", noise=None, dtype=None, ste=False):
     """One step (model.py:503-559 without time embedding / normalisation). fire: (B,1,H,W)."""
-    dt = _dtype(precision)
+    dt = dtype or _dtype(precision)
     x = x.to(dt)
-    dx = sense_update(cell, x, precision)
+    dx = sense_update(cell, x, precision, dtype, ste)
     u = x + fire.to(dt) * dx.to(dt)
     if noise is not None:
         u = u + noise.to(dt)
@@ -202,6 +223,64 @@ def rollout(
         if trace is not None:
             trace(t, x)
     return x, fired
+
+
+def chunk_loss(cell: OracleCell, x0, given4, clamp, masks, targets, weights, precision="fp32",
+               loss_mask=None, ste=True, final_cotangent=None):
+    """The BPTT chunk's loss (engine.py:474-490 with the chunk's run_block, step.py:236-245):
+    `n` steps from x0 with fire masks `masks` (n, B, 1, H, W), then
+    L = sum_t w_t * step_loss(x_{t+1}) / max(sum_t w_t, 1), where step_loss is the mean (or the
+    loss_mask weighted mean, train.py:196-207) over cells of the cross-entropy of the mlp head's
+    logits against `targets` (B, H, W) class indices (train.py:190-192). Computed in fp64,
+    differentiable w.r.t. the cell's tensors and x0; bf16 cells round at the forward's points
+    (straight-through when `ste`). `final_cotangent` adds sum(x_n * final_cotangent), whose
+    gradient w.r.t. the last state is that cotangent (a later loss's gradient)."""
+    dt = torch.float64
+    x = x0.to(dt)
+    w = torch.as_tensor(weights, dtype=dt)
+    total = x.new_zeros(())
+    sl = slice(cell.out_offset, cell.out_offset + cell.c_out)
+    for t in range(masks.shape[0]):
+        x = step(cell, x, given4, clamp, masks[t], precision, dtype=dt, ste=ste)
+        if w[t] == 0:
+            continue
+        logits = torch.einsum("vc,bchw->bvhw", cell.head_w.to(dt), x[:, sl]) \
+            + cell.head_b.to(dt)[None, :, None, None]
+        per_cell = F.cross_entropy(logits, targets.long(), reduction="none")
+        if loss_mask is not None:
+            lm = loss_mask.to(dt)
+            step_l = (per_cell * lm).sum() / lm.sum().clamp_min(1)
+        else:
+            step_l = per_cell.mean()
+        total = total + w[t] * step_l
+    total = total / w.sum().clamp_min(1)
+    if final_cotangent is not None:
+        total = total + (x * final_cotangent.to(dt)).sum()
+    return total
+
+
+def bptt_chunk(cell: OracleCell, x0, given4, clamp, masks, targets, weights, precision="fp32",
+               loss_mask=None, grad_x0=False, ste=True, final_cotangent=None):
+    """`chunk_loss` and its gradients by torch autograd in fp64.
+
+    Returns (loss float, grads dict of fp64 tensors: kernels, w1, b1, w2, b2, head_w, head_b,
+    and x0 when grad_x0)."""
+    dt = torch.float64
+    names = ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")
+    params = {k: getattr(cell, k).detach().to(dt).clone().requires_grad_(True) for k in names}
+    c = OracleCell(**{**cell.__dict__, **params})
+    x = x0.detach().to(dt).clone().requires_grad_(grad_x0)
+    loss = chunk_loss(c, x, given4, clamp, masks, targets, weights, precision, loss_mask, ste,
+                      final_cotangent)
+    wrt = [params[k] for k in names] + ([x] if grad_x0 else [])
+    if not loss.requires_grad:  # every step weight is zero: a constant loss
+        grads = [None] * len(wrt)
+    else:
+        grads = torch.autograd.grad(loss, wrt, allow_unused=True)
+    out = {k: (g if g is not None else torch.zeros_like(params[k])) for k, g in zip(names, grads)}
+    if grad_x0:
+        out["x0"] = grads[-1] if grads[-1] is not None else torch.zeros_like(x)
+    return float(loss.detach()), out
 
 
 def conf_at_k(metric, conf, alive, ks, weights=None):

@@ -45,7 +45,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     """sizeof / offsetof of the header's structs, compiled with the host C compiler, against the
     ctypes mirrors."""
     structs = {"nca_cell_desc": _lib.CellDesc, "nca_cell_weights": _lib.CellWeights,
-               "nca_fire_desc": _lib.FireDesc}
+               "nca_fire_desc": _lib.FireDesc, "nca_cell_grads": _lib.CellGrads,
+               "nca_bptt_loss": _lib.BpttLoss}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "nca_hip.h"', "int main(void) {"]
     for cname, cls in structs.items():
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
@@ -133,6 +134,24 @@ def test_workspace_query_and_refusal_without_workspace(lib):
     assert lib.nca_set_kernel_path(2) == _lib.NCA_OK
     assert lib.nca_rollout_workspace_bytes(ctypes.byref(_cell()), 8, 9, 9) == 2 * 8 * 64 * 81 * 4
     assert lib.nca_set_kernel_path(0) == _lib.NCA_OK
+
+
+def test_bptt_argument_checks(lib):
+    c32 = _cell(channels=32, hidden=256, c_in=4, c_out=4, out_offset=4, n_out=2, padding=1)
+    n = lib.nca_bptt_workspace_bytes(ctypes.byref(c32), 64, 30, 30, 32)
+    M = 64 * 900
+    assert n >= 4 * M * (2 * 128 + 2 * 256 + 4 * 32)  # z, g_z, h, g_a, g_dx, g_u, 2 x g_x
+    assert lib.nca_bptt_workspace_bytes(ctypes.byref(_cell(head_kind=1)), 4, 9, 9, 8) == 0
+    assert b"mlp head" in lib.nca_last_error()
+    fire = _lib.FireDesc(seed=1, p_fire=0.5)
+    rc = lib.nca_bptt_backward(ctypes.byref(c32), None, None, 4, 30, 30, None, None,
+                               ctypes.byref(fire), 4, None, None, None, None, None, None, 0, None)
+    assert rc == _lib.NCA_ERR_INVALID and b"NULL" in lib.nca_last_error()
+    adaptive = _lib.FireDesc(seed=1, p_fire=0.5, p_low=0.1, tau=0.9, adaptive=1)
+    p = ctypes.c_void_p(1 << 20)
+    rc = lib.nca_bptt_forward(ctypes.byref(c32), p, 4, 30, 30, p, p, p, ctypes.byref(adaptive), 4,
+                              p, None)
+    assert rc == _lib.NCA_ERR_UNSUPPORTED
 
 
 def test_check_maps_status_to_python_exceptions(lib):

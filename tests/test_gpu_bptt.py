@@ -1,0 +1,208 @@
+"""The BPTT chunk on the GPU (nca_bptt_forward / nca_bptt_backward through the C ABI) against the
+fp64 autograd oracle, plus the engine's train_iteration around it.
+
+* fp32 cells: loss and every parameter gradient (and d L / d x0) within a relative norm error
+  of 1e-4 of the oracle over multi-step chunks with sparse step weights, a loss mask, wall /
+  wrap padding and injected or Philox fire masks.
+* bf16 cells: the single-step vector-Jacobian product from the GPU's own state (so that both
+  sides differentiate the same rounded operands) within 5e-3; multi-step chunks within 5e-2
+  of the oracle (bf16 rounding flips in the forward move the states by up to 2e-2).
+* The chunk's saved states are the rollout kernels' states bit for bit; gradients are
+  bitwise reproducible; chaining two chunks through grad_final / grad_x0 equals one chunk.
+"""
+
+from __future__ import annotations
+
+import copy
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+sys.path.insert(0, __file__.rsplit("/", 1)[0])
+from cells import CELLS, DYN, boards_for, initial_state, make_model, oracle_cell, perturbed_model  # noqa: E402
+
+from ncas_amd import _lib  # noqa: E402
+from ncas_amd.inference import rollout_steps  # noqa: E402
+from ncas_amd.tasks import maze_boards  # noqa: E402
+from ncas_amd.train import Engine, bptt_chunk  # noqa: E402
+from oracle import nca_oracle as O  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+NAMES = ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _rel(a, b):
+    a = a.detach().double().cpu().reshape(-1)
+    b = b.detach().double().cpu().reshape(-1)
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def _case(name, n_boards=2, k=2, steps=5, seed=0):
+    preset, size = CELLS[name]
+    m = make_model(name, seed)
+    b = boards_for(preset, n_boards, size, seed)
+    x, g4, cl = initial_state(m, b, k=k, sigma=0.15, seed=seed)
+    B, C, H, W = x.shape
+    g = torch.Generator().manual_seed(seed + 3)
+    masks = (torch.rand((steps, B, 1, H, W), generator=g) < 0.6).float()
+    targets = torch.randint(0, len(m.cfg.output_tokens), (B, H, W), generator=g)
+    return m, copy.deepcopy(m).to(DEV), x, g4, cl, masks, targets
+
+
+def _gpu_chunk(md, x, g4, cl, targets, weights, precision, **kw):
+    with torch.no_grad():
+        return bptt_chunk(md, x.to(DEV), g4.to(DEV), cl.to(DEV), targets.to(DEV), weights,
+                          precision=precision, want_grad_x0=True, **kw)
+
+
+@pytest.mark.parametrize("name", ["maze_hard_c32", "maze_c16", "sudoku_c64"])
+def test_bptt_fp32_matches_oracle(name):
+    _say("bptt fp32", name)
+    m, md, x, g4, cl, masks, targets = _case(name)
+    weights = [1.0, 0.0, 0.5, 0.0, 1.0]
+    lm = (torch.rand(targets.shape, generator=torch.Generator().manual_seed(9)) < 0.8).float()
+    for mask in (None, lm):
+        res = _gpu_chunk(md, x, g4, cl, targets, weights, "fp32", masks=masks.to(DEV),
+                         loss_mask=None if mask is None else mask.to(DEV))
+        loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, weights,
+                                 "fp32", loss_mask=mask, grad_x0=True)
+        assert abs(float(res.loss) - loss) <= 1e-5 * abs(loss), (float(res.loss), loss)
+        for k in NAMES:
+            assert _rel(res.grads[k], ref[k]) <= 1e-4, (k, _rel(res.grads[k], ref[k]))
+        assert _rel(res.grad_x0, ref["x0"]) <= 1e-4
+
+
+def test_bptt_philox_masks_and_step_seeds():
+    """Fire masks drawn in-kernel from per-step keys are the oracle's Philox masks."""
+    m, md, x, g4, cl, _, targets = _case("maze_hard_c32", steps=4)
+    B, C, H, W = x.shape
+    seeds = [11, 2**40 + 3, 7, 99]
+    masks = torch.stack([O.fire_masks_np(s, 5, B, 20 + t, H, W, 0.7) for t, s in enumerate(seeds)])
+    res = _gpu_chunk(md, x, g4, cl, targets, [1, 1, 1, 1], "fp32", step_seeds=seeds, p_fire=0.7,
+                     row0=5, step0=20)
+    loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, [1, 1, 1, 1],
+                             "fp32", grad_x0=True)
+    assert abs(float(res.loss) - loss) <= 1e-5 * abs(loss)
+    for k in NAMES:
+        assert _rel(res.grads[k], ref[k]) <= 1e-4, k
+
+
+@pytest.mark.parametrize("name", ["maze_hard_c32", "sudoku_c64"])
+def test_bptt_bf16_single_step_vjp_from_the_gpu_state(name):
+    _say("bptt bf16 vjp", name)
+    m, md, x, g4, cl, masks, targets = _case(name, steps=4)
+    with torch.no_grad():
+        xs, _, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 6, seed=3, precision="bf16")
+    xs = xs.cpu()
+    cot = torch.randn(xs.shape, generator=torch.Generator().manual_seed(4)) * 0.01
+    res = _gpu_chunk(md, xs, g4, cl, targets, [1.0], "bf16", masks=masks[:1].to(DEV),
+                     grad_final=cot.to(DEV))
+    loss, ref = O.bptt_chunk(oracle_cell(m), xs, g4, cl, masks[:1].double(), targets, [1.0],
+                             "bf16", grad_x0=True, final_cotangent=cot.double())
+    worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
+    _say("bf16 vjp worst rel", worst, "x0", _rel(res.grad_x0, ref["x0"]))
+    assert worst <= 5e-3
+    assert _rel(res.grad_x0, ref["x0"]) <= 5e-3
+
+
+@pytest.mark.parametrize("name", ["maze_hard_c32", "maze_c16"])
+def test_bptt_bf16_chunk_near_oracle(name):
+    m, md, x, g4, cl, masks, targets = _case(name, steps=5)
+    weights = [0.5, 0.0, 1.0, 0.0, 1.0]
+    res = _gpu_chunk(md, x, g4, cl, targets, weights, "bf16", masks=masks.to(DEV))
+    loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, weights, "bf16",
+                             grad_x0=True)
+    worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
+    _say("bf16 chunk worst rel", worst, "loss", float(res.loss), loss)
+    assert abs(float(res.loss) - loss) <= 1e-3 * abs(loss)
+    assert worst <= 5e-2
+
+
+def test_bptt_states_are_the_rollout_states_and_gradients_are_reproducible():
+    m, md, x, g4, cl, masks, targets = _case("maze_hard_c32", steps=6)
+    a = _gpu_chunk(md, x, g4, cl, targets, [1] * 6, "bf16", seed=8)
+    b = _gpu_chunk(md, x, g4, cl, targets, [1] * 6, "bf16", seed=8)
+    with torch.no_grad():
+        y, _, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 6, seed=8, precision="bf16")
+    assert torch.equal(a.x, y)
+    assert torch.equal(a.loss, b.loss) and torch.equal(a.grad_x0, b.grad_x0)
+    for k in NAMES:
+        assert torch.equal(a.grads[k], b.grads[k]), k
+
+
+def test_bptt_chunks_chain_through_grad_final():
+    """Steps [0, 6) in one chunk == steps [3, 6) then [0, 3) with the later chunk's d L / d x3
+    as grad_final; parameter gradients add up."""
+    m, md, x, g4, cl, masks, targets = _case("maze_c16", steps=6)
+    w = [1.0, 0.0, 0.5, 1.0, 0.0, 1.0]
+    full = _gpu_chunk(md, x, g4, cl, targets, w, "fp32", masks=masks.to(DEV))
+    with torch.no_grad():
+        x3, _, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 3, masks=masks[:3].to(DEV))
+    s = sum(w)
+    late = _gpu_chunk(md, x3, g4, cl, targets, [v / s for v in w[3:]] + [0.0] * 0, "fp32",
+                      masks=masks[3:].to(DEV))
+    # the later chunk normalises by max(sum(w[3:] / s), 1) = 1: its loss is sum w_t L_t / s
+    early = _gpu_chunk(md, x, g4, cl, targets, [v / s for v in w[:3]], "fp32",
+                       masks=masks[:3].to(DEV), grad_final=late.grad_x0)
+    for k in NAMES:
+        assert _rel(early.grads[k] + late.grads[k], full.grads[k]) <= 1e-5, k
+    assert _rel(early.grad_x0, full.grad_x0) <= 1e-5
+    assert abs(float(early.loss + late.loss) - float(full.loss)) <= 1e-6 * abs(float(full.loss))
+
+
+def test_bptt_30x30_hard_maze_chunk_matches_oracle():
+    """The training configuration's cell and grid (30x30 hard mazes, C=32, halo-tiled forward)
+    on 6 boards x 6 steps, fp32, and the memory of the full chunk (64 boards x 32 steps)."""
+    _say("bptt 30x30")
+    m = perturbed_model("maze_hard_c32", 0, *DYN["maze_hard_c32"])
+    md = copy.deepcopy(m).to(DEV)
+    b = maze_boards(6, 30, 0, extra_openings=0.1)
+    x, g4, cl = initial_state(m, b, k=1, sigma=0.15)
+    targets = m.output_index(torch.from_numpy(b.targets))
+    g = torch.Generator().manual_seed(1)
+    masks = (torch.rand((6, 6, 1, 30, 30), generator=g) < 0.8).float()
+    w = [0, 0, 1, 0, 0, 1]
+    res = _gpu_chunk(md, x, g4, cl, targets, w, "fp32", masks=masks.to(DEV))
+    loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, w, "fp32",
+                             grad_x0=True)
+    assert abs(float(res.loss) - loss) <= 1e-5 * abs(loss)
+    for k in NAMES:
+        assert _rel(res.grads[k], ref[k]) <= 1e-4, k
+    pk = md.packed("bf16", DEV)
+    ws = _lib.load().nca_bptt_workspace_bytes(ctypes.byref(pk.desc), 64, 30, 30, 32)
+    states = 33 * 64 * 32 * 900 * 4
+    _say(f"full chunk: states {states / 2**20:.1f} MiB + workspace {ws / 2**20:.1f} MiB")
+    assert 0 < ws < 512 * 2**20
+
+
+def test_engine_train_iteration_composes_prefix_chunk_suffix():
+    m, md, x, g4, cl, _, targets_idx = _case("maze_hard_c32", steps=1)
+    tokens = torch.tensor(m.cfg.output_tokens)[targets_idx]
+    batch = {"x": x.to(DEV), "given4": g4.to(DEV), "clamp": cl.to(DEV), "targets": tokens.to(DEV)}
+    seeds = np.arange(100, 110, dtype=np.int64)
+    eng = Engine(md, rollout=10, chunk=4, amp=False)
+    calls = []
+    for p in md.parameters():
+        p.grad = None
+    xf, loss, gn = eng.train_iteration(batch, seeds, 3, [1, 0, 1, 1], grad_clip=1e9,
+                                       apply_update=calls.append)
+    assert len(calls) == 1 and torch.equal(calls[0], gn)
+    with torch.no_grad():
+        x3, _, _ = rollout_steps(md, batch["x"], batch["given4"], batch["clamp"], 3,
+                                 step_seeds=seeds[:3], p_fire=m.cfg.fire_rate)
+        ref = bptt_chunk(md, x3, batch["given4"], batch["clamp"], targets_idx.to(DEV), [1, 0, 1, 1],
+                         step_seeds=seeds[3:7], p_fire=m.cfg.fire_rate)
+        xe, _, _ = rollout_steps(md, ref.x, batch["given4"], batch["clamp"], 3,
+                                 step_seeds=seeds[7:], p_fire=m.cfg.fire_rate)
+    assert torch.equal(xf, xe) and torch.equal(loss, ref.loss)
+    assert torch.equal(md.update.fc1.weight.grad, ref.grads["w1"].reshape(md.update.fc1.weight.shape))
+    total = torch.sqrt(sum((ref.grads[k].double() ** 2).sum() for k in NAMES))
+    assert abs(float(gn) - float(total)) <= 1e-5 * float(total)
