@@ -10,7 +10,10 @@ resident in HBM before the timed region.
 `--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16, D=13,000, p_fire=0.5) and
 `--workload hardmaze30` (1,000 hard mazes 30x30 with 10 % extra openings, K=64 -> 64,000 rows,
 C=32, MLP 128 -> 256 -> 32, D=200, p_fire=0.8 gated to 0.2 above confidence 0.9) time the
-halo-tiled per-step path the same way.
+halo-tiled per-step path the same way. `--workload bptt30` times one training iteration: 64
+states sampled from a replay pool of 1,024 (30x30 DFS mazes, C=32 cell, bf16 forward with fp32
+master weights), a 32-step BPTT chunk with the per-cell cross-entropy on the 2-class path
+targets, AdamW, write-back; it reports cell-steps/s and the peak activation memory.
 
 value = rows * H * W * D * steps / wall seconds (cell-updates/s). The roofline block prices the
 rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) per cell-update, the
@@ -48,6 +51,11 @@ WORKLOADS = {
         preset="maze_c16", task="maze", boards=16, k=1, depth=13000, grid=201, p_fire=0.5,
         desc="maze 201x201: 16 DFS mazes, D=13000 steps, C=16, 4 kernels, MLP 64-128-16, "
              "p_fire=0.5, one halo-tiled launch per step"),
+    "bptt30": dict(
+        preset="maze_hard_c32", task="maze", boards=1024, k=1, depth=32, grid=30, p_fire=0.8,
+        batch=64, extra=0.10,
+        desc="BPTT 30x30: batch 64 from a replay pool of 1024 maze states, 32-step chunk, C=32, "
+             "MLP 128-256-32 bf16 with fp32 master weights, per-cell CE on path targets, AdamW"),
     "hardmaze30": dict(
         preset="maze_hard_c32", task="maze", boards=1000, k=64, depth=200, grid=30, p_fire=0.8,
         p_low=0.2, tau=0.9, extra=0.10,
@@ -206,6 +214,54 @@ def run_gpu(wl, precision, steps, warmup):
     }
 
 
+def run_bptt(wl, precision, steps, warmup):
+    """Training iterations: pool sample -> 32-step BPTT chunk -> AdamW -> write-back."""
+    from ncas_amd.model import build_model, init_weights
+    from ncas_amd.train import Engine, ReplayPool
+
+    dev = torch.device("cuda:0")
+    model = init_weights(build_model(wl["preset"]), seed=0, std=0.02, zero_last=False).to(dev)
+    boards = make_boards(wl, 0)
+    pool = ReplayPool(model, boards, wl["boards"], np.random.default_rng(0),
+                      torch.Generator(device=dev).manual_seed(0))
+    eng = Engine(model, rollout=wl["depth"], chunk=wl["depth"], amp=precision == "bf16")
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-3)
+    rng = np.random.default_rng(1)
+    weights = [1.0] * wl["depth"]
+
+    def one():
+        idx, batch = pool.sample(wl["batch"], 0.25)
+        seeds = rng.integers(0, 2**62, size=wl["depth"])
+        opt.zero_grad(set_to_none=True)
+        x, loss, gn = eng.train_iteration(batch, seeds, 0, weights, 1.0, lambda g: opt.step())
+        batch["x"] = x
+        pool.write_back(idx, batch)
+        return loss
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    t0 = time.perf_counter()
+    losses = [one() for _ in range(steps)]
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    cell_steps = wl["batch"] * wl["grid"] ** 2 * wl["depth"]
+    rate = cell_steps * steps / wall
+    flops = 4 * flop_per_cell_update(wl["preset"])  # forward + recompute + dX + dW
+    tflops = rate * flops / 1e12
+    res = eng.last_chunk
+    return {
+        "value": rate, "ms_per_step": wall / steps * 1e3, "kernel_ms": None,
+        "kernel_rate": rate, "achieved_tflops": tflops, "frac": tflops / PEAK_TFLOPS["fp32"],
+        "rows": wl["batch"], "loss": [float(v) for v in losses],
+        "peak_activation_bytes": int(peak),
+        "states_bytes": res.states_bytes, "workspace_bytes": res.workspace_bytes,
+    }
+
+
 def roofline(name, wl, precision, res):
     """Binding ceiling of the workload's dominant kernel: MFMA FLOPs for the resident kernel;
     the lower of MFMA FLOPs and HBM bytes for the per-step path."""
@@ -243,6 +299,24 @@ def main():
     wl = WORKLOADS[args.workload]
     if args.calib_copy_mib:
         calibration_copy(args.calib_copy_mib)
+    if args.workload == "bptt30":
+        res = run_bptt(wl, args.precision, args.steps, args.warmup)
+        line = {
+            "metric": "BPTT cell-steps/sec on 1 MI355X (30x30 C=32, batch 64, 32-step chunk)",
+            "value": res["value"], "unit": "cell-steps/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": args.precision, "data": "synthetic",
+            "config": {"workload": wl["desc"], "rows": res["rows"], "grid": [30, 30],
+                       "depth": wl["depth"]},
+            "roofline": {"bound": "mfma", "achieved": res["achieved_tflops"],
+                         "peak": PEAK_TFLOPS["fp32"], "unit": "TFLOP/s", "frac": res["frac"],
+                         "traffic": None},
+            "peak_activation_bytes": res["peak_activation_bytes"],
+            "states_bytes": res["states_bytes"], "workspace_bytes": res["workspace_bytes"],
+            "loss": res["loss"],
+        }
+        print(json.dumps(line), flush=True)
+        return
     res = run_gpu(wl, args.precision, args.steps, args.warmup)
     print(f"# gpu {args.workload} {args.precision}: {res['value']:.4g} cell-updates/s, "
           f"kernel ms {res['kernel_ms']}", file=sys.stderr, flush=True)

@@ -15,7 +15,7 @@
 //   stencil_t  g_x = g_u + the transposed stencil of g_z (padding-aware: wall / zero halos take
 //              no gradient, wrap halos give it to the wrapped cell), the next step's gradient
 //   partials   dW1 = g_a z^T, dW2 = g_dx h^T, db1, db2, dkernels, dhead: split-K partial sums over
-//              32 fixed cell ranges, added into one accumulator per step in a fixed order
+//              256 fixed cell ranges, added into one accumulator per step in a fixed order
 //
 // so the gradients are deterministic (the same bits on every run). Gradients are the exact fp32
 // gradients of the forward as computed: for bf16 cells the rounding points are straight-through
@@ -33,7 +33,7 @@
 
 namespace {
 
-constexpr int kSplit = 32;   // cell ranges of the split-K weight-gradient sums
+constexpr int kSplit = 256;  // cell ranges of the split-K weight-gradient sums
 constexpr int kThreads = 256;
 
 struct Dims {
@@ -328,26 +328,41 @@ __global__ void __launch_bounds__(kThreads) dkern_kernel(Dims d, const float *x,
 }
 
 // dhead partials: pair p < n_out c_out is (v, c): sum g_l[v] x1[out_off + c]; pair n_out c_out + v
-// is the bias: sum g_l[v]; block s over its cell range, cells in order.
+// is the bias: sum g_l[v]. Block s over its cell range, one cell per thread, 16 pairs at a time,
+// each pair's per-thread sums reduced in a fixed tree.
 __global__ void __launch_bounds__(kThreads) dhead_kernel(Dims d, const float *x1, const float *GL, float *part,
                                                          int64_t P, int64_t offHW, int64_t offHB) {
+    __shared__ float red[kThreads];
     const int s = blockIdx.x;
     const int64_t per = (d.M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < d.M ? m0 + per : d.M;
-    const int npw = d.n_out * d.c_out;
-    for (int p = threadIdx.x; p < npw + d.n_out; p += kThreads) {
-        const int v = p < npw ? p / d.c_out : p - npw, c = p < npw ? p - v * d.c_out : -1;
-        float acc = 0.0f;
-        for (int64_t m = m0; m < m1; ++m) {
-            const float g = GL[v * d.M + m];
-            if (c < 0) {
-                acc = __fadd_rn(acc, g);
-            } else {
-                const int64_t row = m / d.HW;
-                const int q = (int)(m - row * d.HW);
-                acc = __builtin_fmaf(g, x1[(row * d.C + d.out_off + c) * (int64_t)d.HW + q], acc);
+    const int npw = d.n_out * d.c_out, np = npw + d.n_out;
+    for (int p0 = 0; p0 < np; p0 += 16) {
+        float acc[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+        for (int64_t m = m0 + threadIdx.x; m < m1; m += kThreads) {
+            const int64_t row = m / d.HW;
+            const int q = (int)(m - row * d.HW);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int p = p0 + k;
+                if (p >= np) break;
+                const int v = p < npw ? p / d.c_out : p - npw, c = p < npw ? p - v * d.c_out : -1;
+                const float g = GL[v * d.M + m];
+                acc[k] = c < 0 ? __fadd_rn(acc[k], g)
+                               : __builtin_fmaf(g, x1[(row * d.C + d.out_off + c) * (int64_t)d.HW + q], acc[k]);
             }
         }
-        part[s * P + (c < 0 ? offHB + v : offHW + p)] = acc;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int p = p0 + k;
+            if (p >= np) break;  // uniform across the block
+            const float r = block_sum(acc[k], red);
+            if (threadIdx.x == 0) {
+                const int v = p < npw ? p / d.c_out : p - npw;
+                part[s * P + (p < npw ? offHW + p : offHB + v)] = r;
+            }
+        }
     }
 }
 
@@ -372,13 +387,15 @@ __global__ void reduce_acc_kernel(const float *part, int64_t P, float *acc) {
     }
 }
 
-// The loss of the chunk: sum over steps and front blocks in order.
+// The loss of the chunk: each thread sums a fixed strided subset of the (step, block) partials,
+// then a fixed tree; one block.
 __global__ void loss_kernel(const float *lossp, int n, int blocks, float *out) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    __shared__ float red[kThreads];
+    const int64_t total = (int64_t)n * blocks;
     float s = 0.0f;
-    for (int t = n - 1; t >= 0; --t)
-        for (int b = 0; b < blocks; ++b) s = __fadd_rn(s, lossp[t * blocks + b]);
-    *out = s;
+    for (int64_t i = threadIdx.x; i < total; i += kThreads) s = __fadd_rn(s, lossp[i]);
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) *out = s;
 }
 
 __global__ void copy_kernel(const float *src, float *dst, int64_t n) {
@@ -692,7 +709,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.HB, grads->head_b, (int64_t)d.n_out);
     if (loss_out) {
         if (n_chunk > 0 && d.M > 0)
-            hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(64), 0, st, lossp, n_chunk, L.front_blocks, loss_out);
+            hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossp, n_chunk, L.front_blocks, loss_out);
         else
             hipLaunchKernelGGL(zero_f32, dim3(1), dim3(64), 0, st, loss_out, (int64_t)1);
     }
