@@ -121,15 +121,17 @@ __global__ void pack_frags(const float *src, int M, int K, int bf16, int qC, voi
     }
 }
 
-// fc2 fragments for the wave-specialised kernel (see nca_layout.h), bf16.
-__global__ void pack_w2k(const float *w2, int C, int HD, __bf16 *dst) {
-    const int hpw = HD / 4, kt2n = hpw / 32, mt2n = C / 16;
+// fc2 fragments of the streamed kernel (see nca_layout.h), bf16: the k axis follows the order in
+// which fc1's accumulators are stored, p = 64 w + 16 g + 4 mt + v -> hidden 64 w + 16 mt + 4 g + v.
+__global__ void pack_w2h(const float *w2, int C, int HD, __bf16 *dst) {
+    const int nkt = HD / 32;
     const int total = C * HD;
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
         const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
-        const int kt = blk % kt2n, m2 = (blk / kt2n) % mt2n, q = blk / (kt2n * mt2n);
-        const int ch = 16 * m2 + (lane & 15);
-        const int hid = q * hpw + 16 * (2 * kt + s / 4) + 4 * (lane >> 4) + (s % 4);
+        const int kt = blk % nkt, m = blk / nkt;
+        const int ch = 16 * m + (lane & 15);
+        const int p = 32 * kt + 8 * (lane >> 4) + s;
+        const int hid = (p & ~63) + 16 * ((p >> 2) & 3) + 4 * ((p >> 4) & 3) + (p & 3);
         dst[e] = (__bf16)w2[(size_t)ch * HD + hid];
     }
 }
@@ -422,7 +424,7 @@ nca::RolloutParams base_params(const nca_cell_desc *d, const void *packed, int64
     p.off_padv = (unsigned)L.padv;
     p.off_w1 = (unsigned)L.w1;
     p.off_w2 = (unsigned)L.w2;
-    p.off_w2k = (unsigned)L.w2k;
+    p.off_w2h = (unsigned)L.w2h;
     p.off_w1q = (unsigned)L.w1q;
     return p;
 }
@@ -483,7 +485,7 @@ int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void 
     hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, (int)bf, 0, (void *)(pk + L.w1));
     hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w2, C, HD, (int)bf, 0, (void *)(pk + L.w2));
     if (bf) {
-        hipLaunchKernelGGL(pack_w2k, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2k));
+        hipLaunchKernelGGL(pack_w2h, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2h));
         hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, 1, C, (void *)(pk + L.w1q));
     }
     return hip_check(hipGetLastError(), "pack launch");

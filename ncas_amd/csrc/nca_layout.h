@@ -10,9 +10,10 @@
 //   padv   float[C]           wall border value
 //   w1     MFMA A fragments of fc1: [m-tile (hidden/16)][k-tile][lane 64][slot]
 //   w2     MFMA A fragments of fc2: [m-tile (C/16)][k-tile][lane 64][slot]
-//   w2k    (bf16 only) fc2 fragments per hidden quarter q = 0..3, for the kernel that feeds
-//          fc1's accumulators straight into fc2: [q][m-tile][k-tile][lane][slot] with
-//          A[i][slot] = W2[16 m + i][q*hidden/4 + 16*(2 k + slot/4) + 4*(lane/16) + slot%4]
+//   w2h    (bf16 only) fc2 fragments for the streamed kernel, whose hidden activations sit in
+//          LDS in the order of fc1's accumulators: physical position p = 64 w + 16 g + 4 mt + v
+//          holds hidden unit hl(p) = 64 w + 16 mt + 4 g + v. [m-tile][k-tile][lane][slot] with
+//          A[i][slot] = W2[16 m + i][hl(32 k + 8 (lane / 16) + slot)]
 //   w1q    (bf16 only) fc1 fragments like w1 with the feature (k) axis in quad-major order:
 //          k = 16 iq + 4 head + ch holds feature head * C + 4 iq + ch
 // bf16 cells use v_mfma_f32_16x16x32_bf16 fragments (k-tile 32, 8 bf16 slots per lane:
@@ -25,7 +26,7 @@
 namespace nca {
 
 struct PackedLayout {
-    size_t kern, b1, b2, headw, headb, padv, w1, w2, w2k, w1q, total;
+    size_t kern, b1, b2, headw, headb, padv, w1, w2, w2h, w1q, total;
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -51,7 +52,7 @@ __host__ __device__ inline PackedLayout packed_layout(int C, int heads, int hidd
     o = align256(o + esz * (size_t)hidden * heads * C);
     L.w2 = o;
     o = align256(o + esz * (size_t)C * hidden);
-    L.w2k = o;  // bf16 cells: fc2 fragments in the order of the wave-specialised kernel
+    L.w2h = o;  // bf16 cells: fc2 fragments in the streamed kernel's hidden order
     o = align256(o + (bf16 ? 2 * (size_t)C * hidden : 0));
     L.w1q = o;  // bf16 cells: fc1 fragments in quad-major feature order
     o = align256(o + (bf16 ? 2 * (size_t)hidden * heads * C : 0));

@@ -1,43 +1,54 @@
 // Streamed LDS-resident rollout kernel for bf16 cells with C = 64 channels and 256 hidden units
-// (gfx950): the fast path of the bf16 rollout on grids up to 15 cells wide.
+// (gfx950): the fast path of the bf16 rollout on small grids (up to about 10x10).
 //
-// One workgroup of 4 waves (one per SIMD) owns 2*rg rows (rollouts) for the whole call, split
-// into two row groups. The 16-cell tiles of group 0 step s, group 1 step s, group 0 step s+1, ...
-// form one stream. Interval i of the stream (one workgroup barrier) runs three stages of three
-// different tiles, all issued by every wave:
+// A workgroup of 4 waves (one per SIMD) owns R rows (boards) for the whole call. The cells of its
+// boards, board after board and step after step, form one stream: stream position
+// p = (s R + r) HW + q is cell q of board r at step s. The stream is cut into 16-cell tiles (tile
+// t = positions 16t .. 16t+15; a tile may span two boards or two steps, so no cell is padding),
+// and interval i (one workgroup barrier) runs four stages on four tiles, all issued by every wave:
 //
-//   stencil tile i     the 3x3 perception on v_mfma_f32_4x4x4_16b_bf16. Lane (cell n, channel
-//                      quad iq) reads the 9 taps of its 4 channels (bf16) from the perception
-//                      buffer P; each 4-lane block multiplies 4 cells' tap vectors by the 4
-//                      kernels, giving z of 4 heads for 4 cells per instruction (12 per lane).
-//                      z (bf16) -> feature tile Z[i & 1].
-//   MLP tile i-1       fc1 on v_mfma_f32_16x16x32_bf16 with W1 resident in AGPRs (wave w owns
-//                      hidden units [64w, 64w+64)), B operand read from Z; bias + ReLU + bf16
-//                      in registers; fc2 over the wave's own hidden units with the fc1
-//                      accumulators as B operand (W2 fragments packed in that k order). The four
-//                      waves' partial sums of dx go to D[(i-1) & 1].
-//   update tile i-2    dx = bf16(b2 + sum of the 4 partials); x += fire * dx into the fp32 state
-//                      M and the bf16 perception buffer P; the clamped input channels of given
-//                      cells are frozen.
+//   stencil    tile i     the 3x3 perception on v_mfma_f32_4x4x4_16b_bf16. Lane (cell n, channel
+//                         quad iq) reads the 9 taps of its 4 channels (bf16) from the perception
+//                         buffer P; each 4-lane block multiplies 4 cells' tap vectors by the 4
+//                         kernels (12 instructions per lane). z (bf16) -> Z[i & 1].
+//   fc1        tile i-1   h = W1 z + b1 on v_mfma_f32_16x16x32_bf16; wave w owns hidden units
+//                         [64w, 64w+64) with its W1 fragments resident in AGPRs, B operand read
+//                         from Z. The accumulators stay in registers into the next interval.
+//   epilogue   tile i-2   bf16 rounding + ReLU of those accumulators (autocast rounds fc1's output
+//                         before the ReLU) -> H[i & 1]; it runs at the start of the interval, while
+//                         the interval's LDS loads are in flight.
+//   fc2+update tile i-3   dx = W2 h + b2 with wave w owning output channels [16w, 16w+16) (W2
+//                         fragments in AGPRs, B operand read from H). The accumulator layout puts
+//                         channels 16w+4g .. 16w+4g+3 of cell n in lane (n, g), which is the
+//                         update's item: x += fire * bf16(dx) into the fp32 state M and the bf16
+//                         buffer P without another exchange; the clamped input channels of given
+//                         cells keep their value.
 //
-// P is single-buffered: the update of tile i-2 runs in the same interval as the stencil of tile
-// i, whose neighbourhoods reach W+1 <= 16 cells back, so never into tile i-2. A group's
-// end-of-step work runs in the intervals 2 and 3 of the other group's tiles:
-//   * the first step's clamp (phase 1);
-//   * the wrap-halo refresh and the fire masks of the next steps (phase 2).
-// So the pipeline never drains between steps.
+// P is single-buffered: the update of tile i-3 runs in the same interval as the stencil of tile
+// i, whose neighbourhoods reach W+1 <= 16 positions back, never into tile i-3. A board's next
+// step starts (R-1) HW + 1 >= 80 positions after its previous step ended, so its first stencil
+// comes at least five tiles after the tile holding its last cell: that tile's update (three
+// intervals later) and, for wrap padding, the halo refresh of the interval after it are done
+// before the board's next stencil reads P. Adaptive (confidence-gated) and injected fire masks
+// of the board's next step are produced in that same interval. Uniform Philox masks are drawn
+// for NB steps of all boards at a time into one half of a two-half byte ring, while the other
+// half is being read.
 //
-// LDS layouts are chosen for gfx950's banks (reads: 64 banks, ds_read_b64 in groups of 32
-// lanes, ds_read_b128 in two 8-lane groups; writes: 32 banks, 16 lanes per cycle for b64 and 8
-// for b128) so that the hot accesses are conflict-free:
-//   * P: cell stride 144 B, padded row pitch RP = 144 (W + 2) + 224, so that the byte address
-//     of cell q is 144 q + const mod 256 and a tile's 16 cells x 2 quads hit 32 distinct bank
-//     pairs for every tap;
-//   * M and D: 288 B per cell row, 16-byte chunk c of cell n stored at chunk c ^ ((n >> 2) & 1);
-//   * Z: 576 B per cell row, features in quad-major order (16 iq + 4 head + ch), chunk c of row
-//     r stored at chunk c ^ (2 ((r >> 2) & 3)).
-// Fire masks of non-adaptive rollouts are drawn for up to 16 steps at a time (one Philox
-// evaluation per 4 cells, as in the standalone mask kernel) into a byte ring in LDS.
+// Clamp (model.py:430-438): the first step's perception reads the caller's state, and the
+// step's output holds the clamp values in the input slice of given cells. The load therefore
+// writes the caller's state into P and the clamped state into M; the update keeps those
+// channels of given cells at their M value, which is bitwise the reference's clamp at every step.
+//
+// LDS layouts are chosen for gfx950's banks so that the hot accesses are conflict-free:
+//   * P: cell stride 144 B, padded row pitch RP = 144 (W + 2) + 224 and board pitch PB = 144 HW
+//     mod 256, so the byte address of stream cell p is 144 p + const mod 256 within a step;
+//   * M: 272 B per cell (64 fp32 + 16 B): 16 consecutive cells hit 16 distinct 16-byte bank
+//     groups;
+//   * Z: 576 B per tile row, features in quad-major order (16 iq + 4 head + ch), chunk c of row
+//     r stored at chunk c ^ (2 ((r >> 2) & 3));
+//   * H: 528 B per tile row, the 16 hidden values of fc1 lane (n, g) of wave w contiguous at
+//     physical position 64 w + 16 g + 4 mt + v (logical hidden unit 64 w + 16 mt + 4 g + v);
+//     the fc2 fragments are packed in that order.
 #pragma once
 
 #include <type_traits>
@@ -51,52 +62,51 @@ typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 struct St64 {
     static constexpr int C = 64, HD = 256, F = 256;
-    static constexpr int MT1 = 4, KT1 = 8, MT2 = 4, KT2 = 2;
+    static constexpr int MT1 = 4, KT1 = 8, KT2 = 8;
     static constexpr int CS = 144;   // P bytes per cell (64 bf16 + 8 pad)
-    static constexpr int MS = 288;   // M bytes per cell (64 fp32 + 8 pad)
-    static constexpr int ZS = 576;   // Z bytes per cell row (256 bf16 + 32 pad)
-    static constexpr int DS = 288;   // D bytes per cell row (64 fp32 + 8 pad)
+    static constexpr int MS = 272;   // M bytes per cell (64 fp32 + 4 pad)
+    static constexpr int ZS = 576;   // Z bytes per tile row (256 bf16 + 32 pad)
+    static constexpr int HS = 528;   // H bytes per tile row (256 bf16 + 8 pad)
     static constexpr int ZBUF = 16 * ZS;
-    static constexpr int DBUF = 64 * DS;
+    static constexpr int HBUF = 16 * HS;
     static constexpr int RPAD = 224;  // (-2 * CS) mod 256
+    static constexpr int GAP = 79;    // (R-1) HW must reach this
 };
 
 struct StPlan {
-    unsigned P, Ptrash, M, Z, D, cinfo, fire, fired, head, hcp, total;
-    int RP, PB, G, NB;
+    unsigned P, M, Z, H, cinfo, ring, fired, head, hcp, total;
+    int R, RP, PB, NB, RH, RING;
 };
 
 inline unsigned st_al16(unsigned v) { return (v + 15u) & ~15u; }
 
-// rg rows per group, NB fire-mask slots. G (cells per group, a multiple of 32 and >= 64) gives an
-// even number (>= 4) of tiles per group step.
-inline StPlan st_plan(int rg, int H, int W, int c_out, int n_out, int NB) {
+// R rows per workgroup, NB steps per fire-mask batch (1 for per-step masks).
+inline StPlan st_plan(int R, int H, int W, int c_out, int n_out, int NB) {
     using S = St64;
     StPlan p;
     const int HWn = H * W;
+    p.R = R;
+    p.RH = R * HWn;
+    p.NB = NB;
+    p.RING = 2 * NB * p.RH;
     p.RP = (W + 2) * S::CS + S::RPAD;
     const int pb0 = (H + 2) * p.RP;
     p.PB = pb0 + (((S::CS * HWn - pb0) % 256) + 256) % 256;
-    const int g = (rg * HWn + 31) & ~31;
-    p.G = g < 64 ? 64 : g;
-    p.NB = NB;
     unsigned o = 0;
     p.P = o;
-    o = st_al16(o + 2u * rg * (unsigned)p.PB);
-    p.Ptrash = o;
-    o = st_al16(o + 16u * S::CS);
+    o = st_al16(o + (unsigned)R * (unsigned)p.PB);
     p.M = o;
-    o = st_al16(o + 2u * p.G * S::MS);
+    o = st_al16(o + (unsigned)p.RH * S::MS);
     p.Z = o;
     o += 2u * S::ZBUF;
-    p.D = o;
-    o += 2u * S::DBUF;
+    p.H = o;
+    o += 2u * S::HBUF;
     p.cinfo = o;
-    o = st_al16(o + 2u * p.G * 8u);
-    p.fire = o;
-    o = st_al16(o + (unsigned)NB * 2u * p.G);
+    o = st_al16(o + (unsigned)(p.RH + 16) * 8u);
+    p.ring = o;
+    o = st_al16(o + (unsigned)p.RING + 16u);
     p.fired = o;
-    o = st_al16(o + 2u * rg * 4u);
+    o = st_al16(o + (unsigned)R * 4u);
     p.head = o;
     o = st_al16(o + (unsigned)(n_out * c_out + n_out) * 4u);
     p.hcp = o;
@@ -107,9 +117,9 @@ inline StPlan st_plan(int rg, int H, int W, int c_out, int n_out, int NB) {
 
 struct StParams {
     RolloutParams a;
-    int rg, G, RP, PB, NB;
-    unsigned l_P, l_Ptrash, l_M, l_Z, l_D, l_cinfo, l_fire, l_fired, l_head, l_hcp;
-    unsigned off_w1q, off_w2k;
+    int R, RP, PB, NB, RH, RING, T;
+    unsigned l_P, l_M, l_Z, l_H, l_cinfo, l_ring, l_fired, l_head, l_hcp;
+    unsigned off_w1q, off_w2h;
 };
 
 __device__ __forceinline__ uint2 lds_ld64(const unsigned char *s, unsigned off) {
@@ -121,8 +131,17 @@ __device__ __forceinline__ float4 lds_ld128f(const unsigned char *s, unsigned of
 __device__ __forceinline__ void lds_st64(unsigned char *s, unsigned off, uint2 v) {
     *reinterpret_cast<uint2 *>(s + off) = v;
 }
+__device__ __forceinline__ void lds_st128(unsigned char *s, unsigned off, uint4 v) {
+    *reinterpret_cast<uint4 *>(s + off) = v;
+}
 __device__ __forceinline__ void lds_st128f(unsigned char *s, unsigned off, float4 v) {
     *reinterpret_cast<float4 *>(s + off) = v;
+}
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// two floats to packed bf16 (round to nearest even): one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+    const f32x2 f = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 // ReLU of two packed bf16 values: a negative bf16 is a negative int16.
 __device__ __forceinline__ uint32_t relu_bf16x2(uint32_t v) {
@@ -141,37 +160,36 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     const int g = lane >> 4, n = lane & 15;  // n: cell of the tile (MFMA column), g: lane group
     const int iq = 4 * wave + g;             // channel quad of the lane's stencil / update items
     const int H = a.H, W = a.W, HWn = H * W;
-    const int rg = sp.rg, G = sp.G, RP = sp.RP, PB = sp.PB, NB = sp.NB;
-    const int tg = G >> 4;
-    const int64_t rbase = (int64_t)blockIdx.x * 2 * rg;
-    const int Rw = (int)((a.rows - rbase) < 2 * rg ? (a.rows - rbase) : 2 * rg);
-    const int rows0 = Rw < rg ? Rw : rg, rows1 = Rw - rows0;
+    const int R = sp.R, RH = sp.RH, RP = sp.RP, PB = sp.PB, NB = sp.NB, RING = sp.RING;
+    const int64_t rbase = (int64_t)blockIdx.x * R;
+    const int Rw = (int)((a.rows - rbase) < R ? (a.rows - rbase) : R);
 
     int *firedL = reinterpret_cast<int *>(smem + sp.l_fired);
     float *headL = reinterpret_cast<float *>(smem + sp.l_head);
     unsigned *hcp = reinterpret_cast<unsigned *>(smem + sp.l_hcp);
     uint2 *cinfo = reinterpret_cast<uint2 *>(smem + sp.l_cinfo);
-    unsigned char *fireB = smem + sp.l_fire;
+    unsigned char *ring = smem + sp.l_ring;
 
-    // byte offset of (workgroup cell c, channel ch) in M; of the centre of cell q of board rw in P
-    auto m_off = [&](int c, int ch) -> unsigned {
-        return sp.l_M + (unsigned)c * S::MS + 16u * (unsigned)((ch >> 2) ^ ((c >> 2) & 1)) + 4u * (ch & 3);
-    };
-    auto p_cell = [&](int rw, int q) -> unsigned {
+    // byte offset of the centre of cell q of board r in P; of cell q of board r in M
+    auto p_cell = [&](int r, int q) -> unsigned {
         const int i = q / W, j = q - i * W;
-        return sp.l_P + (unsigned)(rw * PB + (i + 1) * RP + (j + 1) * S::CS);
+        return sp.l_P + (unsigned)(r * PB + (i + 1) * RP + (j + 1) * S::CS);
     };
-    auto m_at = [&](int c, int ch) -> float & { return *reinterpret_cast<float *>(smem + m_off(c, ch)); };
-    auto wg_cell = [&](int rw, int q) { return (rw >= rg ? G + (rw - rg) * HWn : rw * HWn) + q; };
+    auto m_cell = [&](int r, int q) -> unsigned { return sp.l_M + (unsigned)(r * HWn + q) * S::MS; };
+    auto m_at = [&](int r, int q, int ch) -> float & {
+        return *reinterpret_cast<float *>(smem + m_cell(r, q) + 4u * (unsigned)ch);
+    };
 
     // ---- registers: MLP weight fragments (AGPRs) and biases
     bf16x8 w1f[S::MT1][S::KT1];
-    bf16x8 w2f[S::MT2][S::KT2];
+    bf16x8 w2f[S::KT2];
     f32x4 b1v[S::MT1];
+    f32x4 b2v;
     {
         const bf16x8 *w1 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w1q);
-        const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2k);
+        const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2h);
         const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
+        const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
 #pragma unroll
         for (int mt = 0; mt < S::MT1; ++mt) {
 #pragma unroll
@@ -180,17 +198,15 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
             for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[wave * 64 + 16 * mt + 4 * g + v];
         }
 #pragma unroll
-        for (int m2 = 0; m2 < S::MT2; ++m2)
+        for (int kt = 0; kt < S::KT2; ++kt) w2f[kt] = w2[(wave * S::KT2 + kt) * 64 + lane];
 #pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) w2f[m2][kt] = w2[((wave * S::MT2 + m2) * S::KT2 + kt) * 64 + lane];
+        for (int v = 0; v < 4; ++v) b2v[v] = b2[4 * iq + v];
 #pragma unroll
         for (int mt = 0; mt < S::MT1; ++mt)
 #pragma unroll
             for (int kt = 0; kt < S::KT1; ++kt) asm volatile("" : "+a"(w1f[mt][kt]));
 #pragma unroll
-        for (int m2 = 0; m2 < S::MT2; ++m2)
-#pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[m2][kt]));
+        for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[kt]));
     }
     // stencil B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 placed at the
     // k slot of channel c (the A operand of tap 8 is the 4 channels' tap-8 values as loaded)
@@ -209,22 +225,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
     }
-    float b2q[4];
     bool insl[4];
-    {
-        const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int c = 4 * iq + v;
-            b2q[v] = b2[c];
-            insl[v] = c >= a.in_off && c < a.in_off + a.c_in;
-        }
+    for (int v = 0; v < 4; ++v) {
+        const int c = 4 * iq + v;
+        insl[v] = c >= a.in_off && c < a.in_off + a.c_in;
     }
     // lane-constant LDS offsets
-    const int hsw = (n >> 2) & 1;
-    const unsigned kM = (unsigned)n * S::MS + 16u * (unsigned)(iq ^ hsw);                       // + l_M + cb MS
-    const unsigned kDr = sp.l_D + (unsigned)n * S::DS + 16u * (unsigned)(iq ^ hsw);              // + w4 16 DS
-    const unsigned kDw = sp.l_D + (unsigned)(wave * 16 + n) * S::DS + 16u * (unsigned)(g ^ hsw);  // + 64 m2
     const int sig = 2 * ((n >> 2) & 3);
     const unsigned kZ0 = sp.l_Z + (unsigned)n * S::ZS + 16u * (unsigned)(g ^ (sig & 3));
     const unsigned kZe = kZ0 + 64u * (unsigned)(sig >> 2), kZo = kZ0 - 64u * (unsigned)(sig >> 2);
@@ -234,31 +241,28 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
         kZw = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 16u * (unsigned)((2 * iq + (j >> 1)) ^ (2 * (b & 3))) +
               8u * (unsigned)(j & 1);
     }
+    const unsigned kHw = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)wave + 32u * (unsigned)g;
+    const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * (unsigned)g;
     const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS);  // + centre: top-left tap
     const unsigned RP2 = 2u * RP;
+    const unsigned kCi = sp.l_cinfo + 8u * (unsigned)n;
+    const unsigned kRg = sp.l_ring + (unsigned)n;
 
-    // ---- load rows and tables
-    for (int e = tid; e < Rw * S::C * HWn; e += 256) {
-        const int rw = e / (S::C * HWn), rem = e - rw * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
-        const float v = a.x_in[rbase * S::C * HWn + e];
-        m_at(wg_cell(rw, q), ch) = v;
-        *reinterpret_cast<__bf16 *>(smem + p_cell(rw, q) + 2 * ch) = (__bf16)v;
+    // ---- load rows (phantom rows of a ragged last workgroup hold zeros and never fire)
+    for (int e = tid; e < R * S::C * HWn; e += 256) {
+        const int r = e / (S::C * HWn), rem = e - r * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
+        const float v = r < Rw ? a.x_in[rbase * S::C * HWn + e] : 0.0f;
+        m_at(r, q, ch) = v;
+        *reinterpret_cast<__bf16 *>(smem + p_cell(r, q) + 2 * ch) = (__bf16)v;
     }
-    for (int c = tid; c < 2 * G; c += 256) {
-        const int grp = c >= G, qg = c - grp * G, nr = grp ? rows1 : rows0;
+    for (int c = tid; c < RH + 16; c += 256) {
+        const int cc = c < RH ? c : c - RH, r = cc / HWn, q = cc - r * HWn;
         uint2 ci;
-        if (qg < nr * HWn) {
-            const int r = qg / HWn, q = qg - r * HWn, rw = grp * rg + r;
-            ci.x = p_cell(rw, q);
-            ci.y = ci.x | (a.given[(rbase + rw) * HWn + q] ? 0x80000000u : 0u);
-        } else {
-            // padding cell: the stencil reads a real cell, update stores go to the trash cells
-            ci.x = nr > 0 ? p_cell(grp * rg + nr - 1, HWn - 1) : p_cell(0, 0);
-            ci.y = sp.l_Ptrash + (unsigned)(c & 15) * S::CS;
-        }
+        ci.x = p_cell(r, q);
+        ci.y = m_cell(r, q) | (r < Rw && a.given[(rbase + r) * HWn + q] ? 0x80000000u : 0u);
         cinfo[c] = ci;
     }
-    for (int e = tid; e < 2 * rg; e += 256) firedL[e] = 0;
+    for (int e = tid; e < R; e += 256) firedL[e] = 0;
     {
         const float *hw = reinterpret_cast<const float *>(a.packed + a.off_headw);
         const float *hb = reinterpret_cast<const float *>(a.packed + a.off_headb);
@@ -288,7 +292,7 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     __syncthreads();
     if (a.padding != 2) {
         const float *padv = reinterpret_cast<const float *>(a.packed + a.off_padv);
-        for (int r = 0; r < Rw; ++r)
+        for (int r = 0; r < R; ++r)
             for (int e = tid; e < nhalo * S::C; e += 256) {
                 const int h = e >> 6, ch = e & 63;
                 const unsigned dst = hcp[h] & 0xffffu;
@@ -296,146 +300,191 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                     (__bf16)(a.padding == 1 ? padv[ch] : 0.0f);
             }
     }
-    // wrap halo of one group's boards: 16-byte chunks of 8 channels
-    auto wrap_halo = [&](int grp) __attribute__((always_inline)) {
-        const int nr = grp ? rows1 : rows0;
-        for (int r = 0; r < nr; ++r) {
-            const unsigned base = sp.l_P + (unsigned)((grp * rg + r) * PB);
-            for (int e = tid; e < nhalo * 8; e += 256) {
-                const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
-                const float4 v = lds_ld128f(smem, base + (hc >> 16) + o);
-                lds_st128f(smem, base + (hc & 0xffffu) + o, v);
-            }
+    // wrap halo of board r: 16-byte chunks of 8 channels
+    auto wrap_halo = [&](int r) __attribute__((always_inline)) {
+        const unsigned base = sp.l_P + (unsigned)(r * PB);
+        for (int e = tid; e < nhalo * 8; e += 256) {
+            const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
+            const float4 v = lds_ld128f(smem, base + (hc >> 16) + o);
+            lds_st128f(smem, base + (hc & 0xffffu) + o, v);
         }
     };
-    // first step's clamp of the given cells of one group (model.py:430-438)
-    auto clamp_pass = [&](int grp) __attribute__((always_inline)) {
-        const int nr = grp ? rows1 : rows0, c_in = a.c_in;
-        for (int e = tid; e < nr * HWn * c_in; e += 256) {
-            const int cell = e / c_in, ci = e - cell * c_in;
-            const int r = cell / HWn, q = cell - r * HWn, rw = grp * rg + r;
-            if (!a.given[(rbase + rw) * HWn + q]) continue;
-            const float v = a.clamp[((rbase + rw) * c_in + ci) * HWn + q];
-            m_at(grp * G + cell, a.in_off + ci) = v;
-            *reinterpret_cast<__bf16 *>(smem + p_cell(rw, q) + 2 * (a.in_off + ci)) = (__bf16)v;
-        }
+    // fire byte of stream position (s, r, q): ring slot ((s mod 2NB) RH + r HW + q); slots below
+    // 16 are mirrored after the ring so that a tile reads 16 consecutive bytes
+    auto ring_put = [&](int s, int r, int q, int f) __attribute__((always_inline)) {
+        const int o = (s % (2 * NB)) * RH + r * HWn + q;
+        ring[o] = (unsigned char)f;
+        if (o < 16) ring[RING + o] = (unsigned char)f;
     };
-    // fire masks: batched Philox draws for steps s0 .. s0 + NB - 1 (non-adaptive, no injected
-    // masks), or one step (adaptive confidence gating or injected masks)
+    // uniform Philox masks of all boards for the steps of batch b (non-adaptive, no injected
+    // masks), one Philox evaluation per 4 cells
     const int nq4 = (HWn + 3) >> 2;
     const bool batched = !a.adaptive && !a.fire_u8;
-    auto draw_batch = [&](int grp, int s0) __attribute__((always_inline)) {
-        const int nr = grp ? rows1 : rows0;
+    auto draw_batch = [&](int b) __attribute__((always_inline)) {
         const int per_row = NB * nq4;
-        for (int it = tid; it < nr * per_row; it += 256) {
+        for (int it = tid; it < R * per_row; it += 256) {
             const int r = it / per_row, rem = it - r * per_row, sl = rem / nq4, qq = rem - sl * nq4;
-            const int s = s0 + sl;
+            const int s = b * NB + sl;
             if (s >= a.n_steps) continue;
-            const int rw = grp * rg + r;
-            const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
-            float u[4];
-            cell_uniforms4(key, (uint32_t)(a.row0 + rbase + rw), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
-            unsigned char *fb = fireB + (unsigned)(sl * 2 * G + grp * G + r * HWn);
+            float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+            if (r < Rw) {
+                const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
+                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+            }
             int cnt = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int q = 4 * qq + e;
                 if (q < HWn) {
-                    const int f = u[e] < a.p;
-                    fb[q] = (unsigned char)f;
+                    const int f = r < Rw && u[e] < a.p;
+                    ring_put(s, r, q, f);
                     cnt += f;
                 }
             }
-            if (cnt) atomicAdd(&firedL[rw], cnt);
+            if (cnt) atomicAdd(&firedL[r], cnt);
         }
     };
-    auto draw_step = [&](int grp, int s) __attribute__((always_inline)) {
-        const int nr = grp ? rows1 : rows0;
-        for (int it = tid; it < nr * nq4; it += 256) {
-            const int r = it / nq4, qq = it - r * nq4, rw = grp * rg + r;
-            float u[4] = {0.f, 0.f, 0.f, 0.f};
-            if (!a.fire_u8) {
+    // masks of board r for step s: adaptive gating reads the board's current state (the state
+    // before step s), injected masks are copied
+    auto draw_step = [&](int r, int s) __attribute__((always_inline)) {
+        for (int it = tid; it < nq4; it += 256) {
+            const int qq = it;
+            float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+            if (r < Rw && !a.fire_u8) {
                 const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
-                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + rw), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
             }
             int cnt = 0;
+#pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int q = 4 * qq + e;
-                if (q >= HWn) break;
-                const int c = grp * G + r * HWn + q;
-                int f;
-                if (a.fire_u8) {
-                    f = a.fire_u8[((int64_t)s * a.rows + rbase + rw) * HWn + q] != 0;
-                } else {
-                    float pc = a.p;
-                    if (a.adaptive) {
-                        int am;
-                        const float cf = cell_readout_fn([&](int v) { return m_at(c, a.out_off + v); }, a.c_out,
-                                                         a.n_out, a.head_kind, headL, headL + a.n_out * a.c_out, &am);
-                        if (cf > a.tau || (a.given_confident && a.given[(rbase + rw) * HWn + q])) pc = a.p_low;
+                if (q >= HWn) continue;
+                int f = 0;
+                if (r < Rw) {
+                    if (a.fire_u8) {
+                        f = a.fire_u8[((int64_t)s * a.rows + rbase + r) * HWn + q] != 0;
+                    } else {
+                        float pc = a.p;
+                        if (a.adaptive) {
+                            int am;
+                            const float cf = cell_readout_fn([&](int v) { return m_at(r, q, a.out_off + v); }, a.c_out,
+                                                             a.n_out, a.head_kind, headL, headL + a.n_out * a.c_out,
+                                                             &am);
+                            if (cf > a.tau || (a.given_confident && a.given[(rbase + r) * HWn + q])) pc = a.p_low;
+                        }
+                        f = u[e] < pc;
                     }
-                    f = u[e] < pc;
                 }
-                fireB[c] = (unsigned char)f;
+                ring_put(s, r, q, f);
                 cnt += f;
             }
-            if (cnt) atomicAdd(&firedL[rw], cnt);
+            if (cnt) atomicAdd(&firedL[r], cnt);
         }
     };
     __syncthreads();
-    if (a.padding == 2) {
-        wrap_halo(0);
-        wrap_halo(1);
-    }
+    if (a.padding == 2)
+        for (int r = 0; r < R; ++r) wrap_halo(r);
     if (a.n_steps > 0) {
         if (batched) {
-            draw_batch(0, 0);
-            draw_batch(1, 0);
+            draw_batch(0);
+            draw_batch(1);
         } else {
-            draw_step(0, 0);
-            draw_step(1, 0);
+            for (int r = 0; r < R; ++r) draw_step(r, 0);
+        }
+    }
+    __syncthreads();
+    // the step's clamp lands in M (P keeps the caller's state for the first perception)
+    if (a.n_steps > 0 && a.c_in > 0) {
+        for (int e = tid; e < Rw * HWn * a.c_in; e += 256) {
+            const int cell = e / a.c_in, ci = e - cell * a.c_in;
+            const int r = cell / HWn, q = cell - r * HWn;
+            if (!a.given[(rbase + r) * HWn + q]) continue;
+            m_at(r, q, a.in_off + ci) = a.clamp[((rbase + r) * a.c_in + ci) * HWn + q];
         }
     }
     __syncthreads();
 
-    // ---- the tile stream. Interval i: stencil of tile i, MLP of tile i-1, update of tile i-2;
-    // tile k belongs to run k / tg (group run & 1, step run >> 1), position k % tg in the run.
-    const int T = a.n_steps * 2 * tg;
-    int js = 0, runs = 0;  // stencil tile position
-    int ju = 0, runu = 0;  // update tile position
-    int slot_u = 0;        // fire slot of the update tile's step
-    uint2 cis = cinfo[n], ciu = cis;
-    auto adv = [&](int &j, int &run) __attribute__((always_inline)) {
-        if (++j == tg) {
-            j = 0;
-            ++run;
+    // ---- the tile stream
+    const int T = sp.T;
+    const int total = a.n_steps * RH;
+    int i = 0;
+    int cbS = 0;               // cinfo index of the stencil tile's first cell: (16 i) mod RH
+    int cbU = RH - 48;         // the same for the update tile i-3: (16 (i-3)) mod RH, RH >= 80
+    int rbU = RING - 48;       // ring slot of the update tile's first cell: (16 (i-3)) mod RING
+    // events: end of (board, step) unit k -> wrap halo refresh / next step's masks of the board;
+    // batched masks of batch nb
+    const bool unit_events = a.padding == 2 || !batched;
+    int uk = 0, ev_unit = unit_events ? ((HWn - 1) >> 4) + 4 : 0x7fffffff;
+    int nb = 2, ev_batch = (batched && 2 * NB < a.n_steps) ? ((NB * RH) >> 4) + 4 : 0x7fffffff;
+    unsigned cis = cinfo[n].x;
+    uint2 ciu = make_uint2(0u, 0u);
+
+    f32x4 acc[S::MT1];
+#pragma unroll
+    for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+
+    auto events = [&]() __attribute__((always_inline)) {
+        while (i == ev_unit) {
+            const int r = uk % R, s = uk / R;
+            if (a.padding == 2) wrap_halo(r);
+            if (!batched && s + 1 < a.n_steps) draw_step(r, s + 1);
+            ++uk;
+            ev_unit = ((uk * HWn + HWn - 1) >> 4) + 4;
+        }
+        if (i == ev_batch) {
+            draw_batch(nb);
+            ++nb;
+            ev_batch = nb * NB < a.n_steps ? (((nb - 1) * NB * RH) >> 4) + 4 : 0x7fffffff;
         }
     };
 
-    auto interval = [&](auto st_c, auto fc_c, auto up_c, auto par_c) __attribute__((always_inline)) {
-        constexpr bool DST = decltype(st_c)::value, DFC = decltype(fc_c)::value, DUP = decltype(up_c)::value;
-        constexpr unsigned PAR = decltype(par_c)::value;
-        // next tiles' table entries (prefetched; the tables never change)
-        int js_n = js, runs_n = runs, ju_n = ju, runu_n = runu;
-        if (DST) adv(js_n, runs_n);
-        if (DUP) adv(ju_n, runu_n);
-        const int cbu = (runu & 1) * G + 16 * ju;
-        uint2 cis_n = cis, ciu_n = ciu;
-        if (DST) cis_n = cinfo[(runs_n & 1) * G + 16 * js_n + n];
-        if (DUP || DFC) ciu_n = cinfo[(runu_n & 1) * G + 16 * ju_n + n];
+    auto interval = [&](auto st_c, auto fc_c, auto ep_c, auto up_c, auto par_v, auto last_c)
+                        __attribute__((always_inline)) {
+        constexpr bool DST = decltype(st_c)::value, DFC = decltype(fc_c)::value, DEP = decltype(ep_c)::value,
+                       DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
+        const unsigned PAR = par_v;
+        // ---- epilogue of tile i-2: bf16 + ReLU of the fc1 accumulators -> H[PAR]
+        if (DEP) {
+            uint4 h0, h1;
+            h0.x = relu_bf16x2(cvt_pk_bf16(acc[0][0], acc[0][1]));
+            h0.y = relu_bf16x2(cvt_pk_bf16(acc[0][2], acc[0][3]));
+            h0.z = relu_bf16x2(cvt_pk_bf16(acc[1][0], acc[1][1]));
+            h0.w = relu_bf16x2(cvt_pk_bf16(acc[1][2], acc[1][3]));
+            h1.x = relu_bf16x2(cvt_pk_bf16(acc[2][0], acc[2][1]));
+            h1.y = relu_bf16x2(cvt_pk_bf16(acc[2][2], acc[2][3]));
+            h1.z = relu_bf16x2(cvt_pk_bf16(acc[3][0], acc[3][1]));
+            h1.w = relu_bf16x2(cvt_pk_bf16(acc[3][2], acc[3][3]));
+            lds_st128(smem, kHw + PAR * S::HBUF, h0);
+            lds_st128(smem, kHw + PAR * S::HBUF + 16u, h1);
+        }
         // ---- LDS loads of the interval
-        uint2 nb[9];
+        bf16x8 hb[S::KT2];
+        float4 m4;
+        float fu = 0.0f;
+        unsigned madr = 0, padr = 0;
+        bool gv = false;
+        if (DUP) {
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt)
+                hb[kt] = *reinterpret_cast<const bf16x8 *>(smem + kHr + (PAR ^ 1u) * S::HBUF + 64u * kt);
+            madr = (ciu.y & 0x7fffffffu) + 16u * iq;
+            m4 = lds_ld128f(smem, madr);
+            fu = (float)smem[kRg + (unsigned)rbU];
+            gv = (int)ciu.y < 0;
+            padr = ciu.x + 8u * iq;
+        }
+        uint2 nbv[9];
         if (DST) {
-            const unsigned r0 = cis.x + kPs, r1 = r0 + (unsigned)RP, r2 = r0 + RP2;
-            nb[0] = lds_ld64(smem, r0);
-            nb[1] = lds_ld64(smem, r0 + S::CS);
-            nb[2] = lds_ld64(smem, r0 + 2 * S::CS);
-            nb[3] = lds_ld64(smem, r1);
-            nb[4] = lds_ld64(smem, r1 + S::CS);
-            nb[5] = lds_ld64(smem, r1 + 2 * S::CS);
-            nb[6] = lds_ld64(smem, r2);
-            nb[7] = lds_ld64(smem, r2 + S::CS);
-            nb[8] = lds_ld64(smem, r2 + 2 * S::CS);
+            const unsigned r0 = cis + kPs, r1 = r0 + (unsigned)RP, r2 = r0 + RP2;
+            nbv[0] = lds_ld64(smem, r0);
+            nbv[1] = lds_ld64(smem, r0 + S::CS);
+            nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
+            nbv[3] = lds_ld64(smem, r1);
+            nbv[4] = lds_ld64(smem, r1 + S::CS);
+            nbv[5] = lds_ld64(smem, r1 + 2 * S::CS);
+            nbv[6] = lds_ld64(smem, r2);
+            nbv[7] = lds_ld64(smem, r2 + S::CS);
+            nbv[8] = lds_ld64(smem, r2 + 2 * S::CS);
         }
         bf16x8 zf[S::KT1];
         if (DFC) {
@@ -444,18 +493,11 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                 zf[kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
                                                            64u * kt);
         }
-        float4 pv[4], m4;
-        float fu = 0.0f;
-        unsigned madr = 0, padr = 0;
-        bool gv = false;
+        // ---- fc2 of tile i-3 (its output feeds the update below)
+        f32x4 acc2 = b2v;
         if (DUP) {
 #pragma unroll
-            for (int w4 = 0; w4 < 4; ++w4) pv[w4] = lds_ld128f(smem, kDr + PAR * S::DBUF + (unsigned)w4 * 16u * S::DS);
-            madr = sp.l_M + (unsigned)cbu * S::MS + kM;
-            m4 = lds_ld128f(smem, madr);
-            fu = (float)fireB[(unsigned)(slot_u * 2 * G + cbu + n)];
-            gv = (int)ciu.y < 0;
-            padr = (ciu.y & 0x7fffffffu) + 8u * iq;
+            for (int kt = 0; kt < S::KT2; ++kt) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[kt], hb[kt], acc2, 0, 0, 0);
         }
         // ---- stencil of tile i
         if (DST) {
@@ -463,13 +505,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nb[1].x : nb[1].y, c < 2 ? nb[0].x : nb[0].y, sel);
-                const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nb[3].x : nb[3].y, c < 2 ? nb[2].x : nb[2].y, sel);
-                const uint32_t p45 = __builtin_amdgcn_perm(c < 2 ? nb[5].x : nb[5].y, c < 2 ? nb[4].x : nb[4].y, sel);
-                const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nb[7].x : nb[7].y, c < 2 ? nb[6].x : nb[6].y, sel);
+                const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nbv[1].x : nbv[1].y, c < 2 ? nbv[0].x : nbv[0].y, sel);
+                const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nbv[3].x : nbv[3].y, c < 2 ? nbv[2].x : nbv[2].y, sel);
+                const uint32_t p45 = __builtin_amdgcn_perm(c < 2 ? nbv[5].x : nbv[5].y, c < 2 ? nbv[4].x : nbv[4].y, sel);
+                const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nbv[7].x : nbv[7].y, c < 2 ? nbv[6].x : nbv[6].y, sel);
                 const s16x4 a0 = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
                 const s16x4 a1 = __builtin_bit_cast(s16x4, make_uint2(p45, p67));
-                const s16x4 a2 = __builtin_bit_cast(s16x4, nb[8]);
+                const s16x4 a2 = __builtin_bit_cast(s16x4, nbv[8]);
                 f32x4 d = {0.f, 0.f, 0.f, 0.f};
                 d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a0, kb0, d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a1, kb1, d, 0, 0, 0);
@@ -479,14 +521,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 uint2 o;
-                o.x = pack_bf16x2(zc[0][r], zc[1][r]);
-                o.y = pack_bf16x2(zc[2][r], zc[3][r]);
+                o.x = cvt_pk_bf16(zc[0][r], zc[1][r]);
+                o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
                 lds_st64(smem, kZw + PAR * S::ZBUF + (unsigned)r * S::ZS, o);
             }
         }
-        // ---- MLP of tile i-1
+        // ---- fc1 of tile i-1 (accumulators kept for the next interval's epilogue)
         if (DFC) {
-            f32x4 acc[S::MT1];
 #pragma unroll
             for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
 #pragma unroll
@@ -494,116 +535,97 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
 #pragma unroll
                 for (int mt = 0; mt < S::MT1; ++mt)
                     acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zf[kt], acc[mt], 0, 0, 0);
-            bf16x8 hf[S::KT2];
-#pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) {
-                uint4 hv;
-                hv.x = relu_bf16x2(pack_bf16x2(acc[2 * kt][0], acc[2 * kt][1]));
-                hv.y = relu_bf16x2(pack_bf16x2(acc[2 * kt][2], acc[2 * kt][3]));
-                hv.z = relu_bf16x2(pack_bf16x2(acc[2 * kt + 1][0], acc[2 * kt + 1][1]));
-                hv.w = relu_bf16x2(pack_bf16x2(acc[2 * kt + 1][2], acc[2 * kt + 1][3]));
-                hf[kt] = __builtin_bit_cast(bf16x8, hv);
-            }
-#pragma unroll
-            for (int m2 = 0; m2 < S::MT2; ++m2) {
-                f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kt = 0; kt < S::KT2; ++kt)
-                    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[m2][kt], hf[kt], acc2, 0, 0, 0);
-                lds_st128f(smem, kDw + (PAR ^ 1u) * S::DBUF + 64u * m2, make_float4(acc2[0], acc2[1], acc2[2], acc2[3]));
-            }
         }
-        // ---- update of tile i-2
+        // ---- update of tile i-3
         if (DUP) {
-            float dsum[4] = {b2q[0], b2q[1], b2q[2], b2q[3]};
-#pragma unroll
-            for (int w4 = 0; w4 < 4; ++w4) {
-                dsum[0] += pv[w4].x;
-                dsum[1] += pv[w4].y;
-                dsum[2] += pv[w4].z;
-                dsum[3] += pv[w4].w;
-            }
+            const uint32_t d01 = cvt_pk_bf16(acc2[0], acc2[1]), d23 = cvt_pk_bf16(acc2[2], acc2[3]);
+            const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
             const float xo[4] = {m4.x, m4.y, m4.z, m4.w};
             float u[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float uv = __builtin_fmaf(fu, round_bf16(dsum[v]), xo[v]);  // fu in {0, 1}: exact
+                const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
                 u[v] = (gv && insl[v]) ? xo[v] : uv;
             }
-            lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
-            lds_st64(smem, padr, make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3])));
-        }
-        // advance: a new even run is the next step, whose fire slot follows
-        js = js_n;
-        runs = runs_n;
-        cis = cis_n;
-        if (DUP) {
-            if (runu_n != runu && (runu_n & 1) == 0) slot_u = slot_u + 1 == NB ? 0 : slot_u + 1;
-            ju = ju_n;
-            runu = runu_n;
-        }
-        ciu = ciu_n;
-    };
-    // end-of-step work of the group of run `run`, whose last update was two intervals ago
-    // (phase 1: first-step clamp) or three (phase 2: wrap halo, next fire masks)
-    auto eos1 = [&](int run) __attribute__((always_inline)) {
-        if ((run >> 1) == 0 && a.c_in > 0) clamp_pass(run & 1);
-    };
-    auto eos2 = [&](int run) __attribute__((always_inline)) {
-        const int grp = run & 1, s = run >> 1;
-        if (a.padding == 2) wrap_halo(grp);
-        if (s + 1 < a.n_steps) {
-            if (batched) {
-                if ((s + 1) % NB == 0) draw_batch(grp, s + 1);
-            } else {
-                draw_step(grp, s + 1);
+            bool ok = true;
+            if (LAST) ok = 16 * (i - 3) + n < total;
+            if (ok) {
+                lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
+                lds_st64(smem, padr, make_uint2(cvt_pk_bf16(u[0], u[1]), cvt_pk_bf16(u[2], u[3])));
             }
         }
+    };
+    // next interval: its table entries (the tables never change)
+    auto advance = [&]() __attribute__((always_inline)) {
+        ++i;
+        cbS += 16;
+        if (cbS >= RH) cbS -= RH;
+        cbU += 16;
+        if (cbU >= RH) cbU -= RH;
+        rbU += 16;
+        if (rbU >= RING) rbU -= RING;
+        cis = lds_ld64(smem, kCi + 8u * (unsigned)cbS).x;
+        ciu = lds_ld64(smem, kCi + 8u * (unsigned)cbU);
     };
     using F_ = std::integral_constant<bool, false>;
     using T_ = std::integral_constant<bool, true>;
     using P0 = std::integral_constant<unsigned, 0>;
     using P1 = std::integral_constant<unsigned, 1>;
     if (T > 0) {
-        interval(T_{}, F_{}, F_{}, P0{});
+        // prologue (T >= 5: a step has at least 80 positions)
+        interval(T_{}, F_{}, F_{}, F_{}, P0{}, F_{});
+        events();
+        advance();
         __syncthreads();
-        interval(T_{}, T_{}, F_{}, P1{});
+        interval(T_{}, T_{}, F_{}, F_{}, P1{}, F_{});
+        events();
+        advance();
         __syncthreads();
-        // steady state: intervals i, i+1 (i even). Interval i is at position jm of its run;
-        // jm == 2 -> phase 1 (at i) and phase 2 (at i+1) of the previous run
-        int jm = 2, erun = -1;
-        for (int i = 2; i < T; i += 2) {
-            interval(T_{}, T_{}, T_{}, P0{});
-            if (jm == 2 && erun >= 0) eos1(erun);
+        interval(T_{}, T_{}, T_{}, F_{}, P0{}, F_{});
+        events();
+        advance();
+        __syncthreads();
+        // steady state: i odd, then even
+        while (i + 1 < T) {
+            interval(T_{}, T_{}, T_{}, T_{}, P1{}, F_{});
+            events();
+            advance();
             __syncthreads();
-            interval(T_{}, T_{}, T_{}, P1{});
-            if (jm == 2 && erun >= 0) eos2(erun);
+            interval(T_{}, T_{}, T_{}, T_{}, P0{}, F_{});
+            events();
+            advance();
             __syncthreads();
-            jm += 2;
-            if (jm == tg) {
-                jm = 0;
-                ++erun;
-            }
         }
-        interval(F_{}, T_{}, T_{}, P0{});
+        if (i < T) {
+            interval(T_{}, T_{}, T_{}, T_{}, P1{}, F_{});
+            events();
+            advance();
+            __syncthreads();
+        }
+        // drain: i == T
+        interval(F_{}, T_{}, T_{}, T_{}, (unsigned)(i & 1), F_{});
+        events();
+        advance();
         __syncthreads();
-        interval(F_{}, F_{}, T_{}, P1{});
+        interval(F_{}, F_{}, T_{}, T_{}, (unsigned)(i & 1), F_{});
+        events();
+        advance();
         __syncthreads();
-        eos1(2 * a.n_steps - 1);  // the last run's first-step clamp (one-step calls)
+        interval(F_{}, F_{}, F_{}, T_{}, (unsigned)(i & 1), T_{});
         __syncthreads();
     }
 
     // ---- write back
     for (int e = tid; e < Rw * S::C * HWn; e += 256) {
-        const int rw = e / (S::C * HWn), rem = e - rw * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
-        a.x_out[rbase * S::C * HWn + e] = m_at(wg_cell(rw, q), ch);
+        const int r = e / (S::C * HWn), rem = e - r * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
+        a.x_out[rbase * S::C * HWn + e] = m_at(r, q, ch);
     }
     if (a.conf_out) {
-        float *confL = reinterpret_cast<float *>(smem + sp.l_D);  // D is free now
+        float *confL = reinterpret_cast<float *>(smem + sp.l_Z);  // Z is free now
         for (int cell = tid; cell < Rw * HWn; cell += 256) {
-            const int rw = cell / HWn, c = wg_cell(rw, cell - rw * HWn);
+            const int r = cell / HWn, q = cell - r * HWn;
             int am;
-            confL[cell] = cell_readout_fn([&](int v) { return m_at(c, a.out_off + v); }, a.c_out, a.n_out,
+            confL[cell] = cell_readout_fn([&](int v) { return m_at(r, q, a.out_off + v); }, a.c_out, a.n_out,
                                           a.head_kind, headL, headL + a.n_out * a.c_out, &am);
         }
         __syncthreads();
