@@ -42,13 +42,15 @@
 // LDS layouts are chosen for gfx950's banks so that the hot accesses are conflict-free:
 //   * P: cell stride 144 B, padded row pitch RP = 144 (W + 2) + 224 and board pitch PB = 144 HW
 //     mod 256, so the byte address of stream cell p is 144 p + const mod 256 within a step;
-//   * M: 272 B per cell (64 fp32 + 16 B): 16 consecutive cells hit 16 distinct 16-byte bank
-//     groups;
+//   * M: 288 B per cell (64 fp32 + 32 B);
 //   * Z: 576 B per tile row, features in quad-major order (16 iq + 4 head + ch), chunk c of row
 //     r stored at chunk c ^ (2 ((r >> 2) & 3));
-//   * H: 528 B per tile row, the 16 hidden values of fc1 lane (n, g) of wave w contiguous at
-//     physical position 64 w + 16 g + 4 mt + v (logical hidden unit 64 w + 16 mt + 4 g + v);
-//     the fc2 fragments are packed in that order.
+//   * H: 544 B per tile row, 16-byte chunk c of row n stored at chunk c ^ ((n >> 2) & 1); the 16
+//     hidden values of fc1 lane (n, g) of wave w are contiguous at physical position
+//     64 w + 16 g + 4 mt + v (logical hidden unit 64 w + 16 mt + 4 g + v); the fc2 fragments are
+//     packed in that order.
+// (Strides and swizzles measured conflict-free for these access patterns on gfx950; M at 272 B
+// and H at 528 B cost about a quarter more per read.)
 #pragma once
 
 #include <type_traits>
@@ -64,9 +66,9 @@ struct St64 {
     static constexpr int C = 64, HD = 256, F = 256;
     static constexpr int MT1 = 4, KT1 = 8, KT2 = 8;
     static constexpr int CS = 144;   // P bytes per cell (64 bf16 + 8 pad)
-    static constexpr int MS = 272;   // M bytes per cell (64 fp32 + 4 pad)
+    static constexpr int MS = 288;   // M bytes per cell (64 fp32 + 8 pad)
     static constexpr int ZS = 576;   // Z bytes per tile row (256 bf16 + 32 pad)
-    static constexpr int HS = 528;   // H bytes per tile row (256 bf16 + 8 pad)
+    static constexpr int HS = 544;   // H bytes per tile row (256 bf16 + 16 pad)
     static constexpr int ZBUF = 16 * ZS;
     static constexpr int HBUF = 16 * HS;
     static constexpr int RPAD = 224;  // (-2 * CS) mod 256
@@ -225,11 +227,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
     }
-    bool insl[4];
+    // all ones where the lane's channel 4 iq + v lies in the clamped input slice
+    unsigned imv[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int c = 4 * iq + v;
-        insl[v] = c >= a.in_off && c < a.in_off + a.c_in;
+        imv[v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
+        asm volatile("" : "+v"(imv[v]));  // kept a plain VGPR mask (no per-channel SGPR lane masks)
     }
     // lane-constant LDS offsets
     const int sig = 2 * ((n >> 2) & 3);
@@ -241,10 +245,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
         kZw = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 16u * (unsigned)((2 * iq + (j >> 1)) ^ (2 * (b & 3))) +
               8u * (unsigned)(j & 1);
     }
-    const unsigned kHw = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)wave + 32u * (unsigned)g;
-    const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * (unsigned)g;
-    const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS);  // + centre: top-left tap
-    const unsigned RP2 = 2u * RP;
+    // H row n: 16-byte chunk c stored at chunk c ^ hx, hx = (n >> 2) & 1
+    const unsigned hx = (unsigned)((n >> 2) & 1);
+    const unsigned kHw0 = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)wave + 32u * (unsigned)g + 16u * hx;
+    const unsigned kHw1 = kHw0 + 16u - 32u * hx;
+    const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * ((unsigned)g ^ hx);
+    // + centre: the top-left tap, the left taps of the middle and bottom rows
+    const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS), kPs1 = kPs + (unsigned)RP, kPs2 = kPs1 + (unsigned)RP;
     const unsigned kCi = sp.l_cinfo + 8u * (unsigned)n;
     const unsigned kRg = sp.l_ring + (unsigned)n;
 
@@ -301,13 +308,31 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
             }
     }
     // wrap halo of board r: 16-byte chunks of 8 channels
-    auto wrap_halo = [&](int r) __attribute__((always_inline)) {
+    auto wrap_halo_all = [&](int r) __attribute__((always_inline)) {
         const unsigned base = sp.l_P + (unsigned)(r * PB);
         for (int e = tid; e < nhalo * 8; e += 256) {
             const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
             const float4 v = lds_ld128f(smem, base + (hc >> 16) + o);
             lds_st128f(smem, base + (hc & 0xffffu) + o, v);
         }
+    };
+    // the thread's (at most two, nhalo <= 64) 16-byte halo chunks: board-relative source offset
+    // in the high half, destination in the low half, 0 when there is none (offset 0 is a corner
+    // halo cell, never a source)
+    unsigned hsd0 = 0, hsd1 = 0;
+    auto halo_item = [&](int e) -> unsigned {
+        if (e >= nhalo * 8) return 0u;
+        const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
+        return (((hc >> 16) + o) << 16) | ((hc & 0xffffu) + o);
+    };
+    // wrap halo of board r after one of its steps: both chunks loaded, then stored
+    auto wrap_halo = [&](int r) __attribute__((always_inline)) {
+        const unsigned base = sp.l_P + (unsigned)(r * PB);
+        float4 v0, v1;
+        if (hsd0) v0 = lds_ld128f(smem, base + (hsd0 >> 16));
+        if (hsd1) v1 = lds_ld128f(smem, base + (hsd1 >> 16));
+        if (hsd0) lds_st128f(smem, base + (hsd0 & 0xffffu), v0);
+        if (hsd1) lds_st128f(smem, base + (hsd1 & 0xffffu), v1);
     };
     // fire byte of stream position (s, r, q): ring slot ((s mod 2NB) RH + r HW + q); slots below
     // 16 are mirrored after the ring so that a tile reads 16 consecutive bytes
@@ -382,8 +407,11 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
         }
     };
     __syncthreads();
-    if (a.padding == 2)
-        for (int r = 0; r < R; ++r) wrap_halo(r);
+    if (a.padding == 2) {
+        hsd0 = halo_item(tid);
+        hsd1 = halo_item(tid + 256);
+        for (int r = 0; r < R; ++r) wrap_halo_all(r);
+    }
     if (a.n_steps > 0) {
         if (batched) {
             draw_batch(0);
@@ -414,68 +442,110 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     // events: end of (board, step) unit k -> wrap halo refresh / next step's masks of the board;
     // batched masks of batch nb
     const bool unit_events = a.padding == 2 || !batched;
-    int uk = 0, ev_unit = unit_events ? ((HWn - 1) >> 4) + 4 : 0x7fffffff;
-    int nb = 2, ev_batch = (batched && 2 * NB < a.n_steps) ? ((NB * RH) >> 4) + 4 : 0x7fffffff;
-    unsigned cis = cinfo[n].x;
-    uint2 ciu = make_uint2(0u, 0u);
+    // unit (board ur, step us) ends at stream position uend; batch nb is drawn when the update
+    // stage has passed position dpos = (nb - 1) NB RH
+    int ur = 0, us = 0, uend = HWn - 1;
+    int ev_unit = unit_events ? (uend >> 4) + 4 : 0x7fffffff;
+    int nb = 2, dpos = NB * RH;
+    int ev_batch = (batched && 2 * NB < a.n_steps) ? (dpos >> 4) + 4 : 0x7fffffff;
+    unsigned cis = cinfo[n].x, cis_n = 0;
+    uint2 ciu = make_uint2(0u, 0u), ciu_n = ciu;
 
     f32x4 acc[S::MT1];
 #pragma unroll
     for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+    bf16x8 zq[4];  // Z operands of fc1's last four k-tiles, carried into the next interval
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) zq[k][e] = (__bf16)0.0f;
 
     auto events = [&]() __attribute__((always_inline)) {
         while (i == ev_unit) {
-            const int r = uk % R, s = uk / R;
-            if (a.padding == 2) wrap_halo(r);
-            if (!batched && s + 1 < a.n_steps) draw_step(r, s + 1);
-            ++uk;
-            ev_unit = ((uk * HWn + HWn - 1) >> 4) + 4;
+            if (a.padding == 2) wrap_halo(ur);
+            if (!batched && us + 1 < a.n_steps) draw_step(ur, us + 1);
+            if (++ur == R) {
+                ur = 0;
+                ++us;
+            }
+            uend += HWn;
+            ev_unit = (uend >> 4) + 4;
         }
         if (i == ev_batch) {
             draw_batch(nb);
             ++nb;
-            ev_batch = nb * NB < a.n_steps ? (((nb - 1) * NB * RH) >> 4) + 4 : 0x7fffffff;
+            dpos += NB * RH;
+            ev_batch = nb * NB < a.n_steps ? (dpos >> 4) + 4 : 0x7fffffff;
         }
     };
 
+    // One interval, in groups separated by scheduling fences (sched_barrier) so that the order
+    // below is the issue order. fc1 of a tile is split over two intervals: k-tiles 0-3 in the
+    // interval after its stencil, k-tiles 4-7 (their Z operands loaded then and kept in
+    // registers) at the start of the next one, so each interval opens with 16 MFMAs that need
+    // no LDS data while its loads stream in. Every LDS load is requested about two groups
+    // before the MFMAs or VALU work that consume it.
+#ifndef NCA_FENCE
+#define NCA_FENCE() __builtin_amdgcn_sched_barrier(0)
+#endif
     auto interval = [&](auto st_c, auto fc_c, auto ep_c, auto up_c, auto par_v, auto last_c)
                         __attribute__((always_inline)) {
         constexpr bool DST = decltype(st_c)::value, DFC = decltype(fc_c)::value, DEP = decltype(ep_c)::value,
                        DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
         const unsigned PAR = par_v;
-        // ---- epilogue of tile i-2: bf16 + ReLU of the fc1 accumulators -> H[PAR]
-        if (DEP) {
-            uint4 h0, h1;
-            h0.x = relu_bf16x2(cvt_pk_bf16(acc[0][0], acc[0][1]));
-            h0.y = relu_bf16x2(cvt_pk_bf16(acc[0][2], acc[0][3]));
-            h0.z = relu_bf16x2(cvt_pk_bf16(acc[1][0], acc[1][1]));
-            h0.w = relu_bf16x2(cvt_pk_bf16(acc[1][2], acc[1][3]));
-            h1.x = relu_bf16x2(cvt_pk_bf16(acc[2][0], acc[2][1]));
-            h1.y = relu_bf16x2(cvt_pk_bf16(acc[2][2], acc[2][3]));
-            h1.z = relu_bf16x2(cvt_pk_bf16(acc[3][0], acc[3][1]));
-            h1.w = relu_bf16x2(cvt_pk_bf16(acc[3][2], acc[3][3]));
-            lds_st128(smem, kHw + PAR * S::HBUF, h0);
-            lds_st128(smem, kHw + PAR * S::HBUF + 16u, h1);
-        }
-        // ---- LDS loads of the interval
         bf16x8 hb[S::KT2];
-        float4 m4;
-        float fu = 0.0f;
-        unsigned madr = 0, padr = 0;
-        bool gv = false;
-        if (DUP) {
-#pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt)
-                hb[kt] = *reinterpret_cast<const bf16x8 *>(smem + kHr + (PAR ^ 1u) * S::HBUF + 64u * kt);
-            madr = (ciu.y & 0x7fffffffu) + 16u * iq;
-            m4 = lds_ld128f(smem, madr);
-            fu = (float)smem[kRg + (unsigned)rbU];
-            gv = (int)ciu.y < 0;
-            padr = ciu.x + 8u * iq;
-        }
+        bf16x8 zf[4];
         uint2 nbv[9];
+        auto load_h = [&](int kt) __attribute__((always_inline)) {
+            if (DUP) hb[kt] = *reinterpret_cast<const bf16x8 *>(smem + kHr + (PAR ^ 1u) * S::HBUF + 64u * kt);
+        };
+        auto zaddr = [&](int kt) -> const bf16x8 * {
+            return reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF + 64u * kt);
+        };
+        auto load_z = [&](int kt) __attribute__((always_inline)) {
+            if (DFC) zf[kt] = *zaddr(kt);
+        };
+        auto fc1_kt = [&](int kt, const bf16x8 &b) __attribute__((always_inline)) {
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt)
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], b, acc[mt], 0, 0, 0);
+        };
+        f32x4 acc2 = b2v;
+        auto fc2_k = [&](int k) __attribute__((always_inline)) {
+            if (DUP) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[k], hb[k], acc2, 0, 0, 0);
+        };
+        s16x4 sa0[4], sa1[4];
+        auto perms = [&](int c) __attribute__((always_inline)) {
+            if (DST) {
+                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nbv[1].x : nbv[1].y, c < 2 ? nbv[0].x : nbv[0].y, sel);
+                const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nbv[3].x : nbv[3].y, c < 2 ? nbv[2].x : nbv[2].y, sel);
+                const uint32_t p45 = __builtin_amdgcn_perm(c < 2 ? nbv[5].x : nbv[5].y, c < 2 ? nbv[4].x : nbv[4].y, sel);
+                const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nbv[7].x : nbv[7].y, c < 2 ? nbv[6].x : nbv[6].y, sel);
+                sa0[c] = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
+                sa1[c] = __builtin_bit_cast(s16x4, make_uint2(p45, p67));
+            }
+        };
+        f32x4 zc[4];
+        // the stencil of channels c0 and c0+1 with their two MFMA chains interleaved
+        auto stencil2 = [&](int c0) __attribute__((always_inline)) {
+            if (DST) {
+                const s16x4 a2 = __builtin_bit_cast(s16x4, nbv[8]);
+                f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+                d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0], kb0, d0, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0 + 1], kb0, d1, 0, 0, 0);
+                d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1[c0], kb1, d0, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1[c0 + 1], kb1, d1, 0, 0, 0);
+                d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0], d0, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0 + 1], d1, 0, 0, 0);
+                zc[c0] = d0;
+                zc[c0 + 1] = d1;
+            }
+        };
+        uint4 h0, h1;
+        // ---- G0: fc1 of tile i-2, k-tile 4; taps of tile i, first H operand
         if (DST) {
-            const unsigned r0 = cis + kPs, r1 = r0 + (unsigned)RP, r2 = r0 + RP2;
+            const unsigned r0 = cis + kPs, r1 = cis + kPs1, r2 = cis + kPs2;
             nbv[0] = lds_ld64(smem, r0);
             nbv[1] = lds_ld64(smem, r0 + S::CS);
             nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
@@ -486,38 +556,73 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
             nbv[7] = lds_ld64(smem, r2 + S::CS);
             nbv[8] = lds_ld64(smem, r2 + 2 * S::CS);
         }
-        bf16x8 zf[S::KT1];
-        if (DFC) {
-#pragma unroll
-            for (int kt = 0; kt < S::KT1; ++kt)
-                zf[kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
-                                                           64u * kt);
+        load_h(0);
+        if (DEP) fc1_kt(4, zq[0]);
+        NCA_FENCE();
+        // ---- G1: k-tile 5
+        load_h(1);
+        load_h(2);
+        load_h(3);
+        if (DEP) fc1_kt(5, zq[1]);
+        NCA_FENCE();
+        // ---- G2: k-tile 6
+        load_z(0);
+        load_z(1);
+        load_h(4);
+        if (DEP) fc1_kt(6, zq[2]);
+        NCA_FENCE();
+        // ---- G3: k-tile 7 (fc1 of tile i-2 done); permutes of channels 0-1
+        load_h(5);
+        load_h(6);
+        if (DEP) fc1_kt(7, zq[3]);
+        perms(0);
+        perms(1);
+        NCA_FENCE();
+        // ---- G4: stencil of channels 0-1, fc2 of tile i-3 starts; half of the epilogue
+        load_h(7);
+        load_z(2);
+        stencil2(0);
+        fc2_k(0);
+        fc2_k(1);
+        if (DEP) {
+            h0.x = relu_bf16x2(cvt_pk_bf16(acc[0][0], acc[0][1]));
+            h0.y = relu_bf16x2(cvt_pk_bf16(acc[0][2], acc[0][3]));
+            h0.z = relu_bf16x2(cvt_pk_bf16(acc[1][0], acc[1][1]));
+            h0.w = relu_bf16x2(cvt_pk_bf16(acc[1][2], acc[1][3]));
         }
-        // ---- fc2 of tile i-3 (its output feeds the update below)
-        f32x4 acc2 = b2v;
+        perms(2);
+        perms(3);
+        NCA_FENCE();
+        // ---- G5: stencil of channels 2-3, fc2; epilogue of tile i-2 ends -> H[PAR]
+        float4 m4;
+        float fu = 0.0f;
+        unsigned madr = 0, padr = 0, gvm = 0;
+        load_z(3);
         if (DUP) {
-#pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[kt], hb[kt], acc2, 0, 0, 0);
+            madr = (ciu.y & 0x7fffffffu) + 16u * iq;
+            m4 = lds_ld128f(smem, madr);
+            fu = (float)smem[kRg + (unsigned)rbU];
+            gvm = (unsigned)((int)ciu.y >> 31);  // all ones for a given cell
+            padr = ciu.x + 8u * iq;
         }
-        // ---- stencil of tile i
+        stencil2(2);
+        fc2_k(2);
+        fc2_k(3);
+        if (DEP) {
+            h1.x = relu_bf16x2(cvt_pk_bf16(acc[2][0], acc[2][1]));
+            h1.y = relu_bf16x2(cvt_pk_bf16(acc[2][2], acc[2][3]));
+            h1.z = relu_bf16x2(cvt_pk_bf16(acc[3][0], acc[3][1]));
+            h1.w = relu_bf16x2(cvt_pk_bf16(acc[3][2], acc[3][3]));
+            lds_st128(smem, kHw0 + PAR * S::HBUF, h0);
+            lds_st128(smem, kHw1 + PAR * S::HBUF, h1);
+        }
+        NCA_FENCE();
+        // ---- G6: fc2 ends; z of tile i -> Z[PAR]
+        fc2_k(4);
+        fc2_k(5);
+        fc2_k(6);
+        fc2_k(7);
         if (DST) {
-            f32x4 zc[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nbv[1].x : nbv[1].y, c < 2 ? nbv[0].x : nbv[0].y, sel);
-                const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nbv[3].x : nbv[3].y, c < 2 ? nbv[2].x : nbv[2].y, sel);
-                const uint32_t p45 = __builtin_amdgcn_perm(c < 2 ? nbv[5].x : nbv[5].y, c < 2 ? nbv[4].x : nbv[4].y, sel);
-                const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nbv[7].x : nbv[7].y, c < 2 ? nbv[6].x : nbv[6].y, sel);
-                const s16x4 a0 = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
-                const s16x4 a1 = __builtin_bit_cast(s16x4, make_uint2(p45, p67));
-                const s16x4 a2 = __builtin_bit_cast(s16x4, nbv[8]);
-                f32x4 d = {0.f, 0.f, 0.f, 0.f};
-                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a0, kb0, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a1, kb1, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c], d, 0, 0, 0);
-                zc[c] = d;
-            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 uint2 o;
@@ -526,17 +631,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                 lds_st64(smem, kZw + PAR * S::ZBUF + (unsigned)r * S::ZS, o);
             }
         }
-        // ---- fc1 of tile i-1 (accumulators kept for the next interval's epilogue)
+        NCA_FENCE();
+        // ---- G7: fc1 of tile i-1, k-tile 0; the update of tile i-3
         if (DFC) {
 #pragma unroll
             for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
-#pragma unroll
-            for (int kt = 0; kt < S::KT1; ++kt)
-#pragma unroll
-                for (int mt = 0; mt < S::MT1; ++mt)
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zf[kt], acc[mt], 0, 0, 0);
+            fc1_kt(0, zf[0]);
         }
-        // ---- update of tile i-3
         if (DUP) {
             const uint32_t d01 = cvt_pk_bf16(acc2[0], acc2[1]), d23 = cvt_pk_bf16(acc2[2], acc2[3]);
             const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
@@ -545,7 +646,8 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
-                u[v] = (gv && insl[v]) ? xo[v] : uv;
+                const unsigned km = imv[v] & gvm;                     // clamped: keep x
+                u[v] = __uint_as_float((km & __float_as_uint(xo[v])) | (~km & __float_as_uint(uv)));
             }
             bool ok = true;
             if (LAST) ok = 16 * (i - 3) + n < total;
@@ -554,6 +656,26 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                 lds_st64(smem, padr, make_uint2(cvt_pk_bf16(u[0], u[1]), cvt_pk_bf16(u[2], u[3])));
             }
         }
+        NCA_FENCE();
+        // ---- G8: k-tile 1; Z operands of k-tiles 4-7 for the next interval; next table entries
+        if (DFC) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) zq[k] = *zaddr(4 + k);
+            fc1_kt(1, zf[1]);
+        }
+        {  // the tables never change
+            int cs = cbS + 16, cu = cbU + 16;
+            if (cs >= RH) cs -= RH;
+            if (cu >= RH) cu -= RH;
+            cis_n = lds_ld64(smem, kCi + 8u * (unsigned)cs).x;
+            ciu_n = lds_ld64(smem, kCi + 8u * (unsigned)cu);
+        }
+        NCA_FENCE();
+        // ---- G9, G10: k-tiles 2-3
+        if (DFC) fc1_kt(2, zf[2]);
+        NCA_FENCE();
+        if (DFC) fc1_kt(3, zf[3]);
+        NCA_FENCE();
     };
     // next interval: its table entries (the tables never change)
     auto advance = [&]() __attribute__((always_inline)) {
@@ -564,8 +686,8 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
         if (cbU >= RH) cbU -= RH;
         rbU += 16;
         if (rbU >= RING) rbU -= RING;
-        cis = lds_ld64(smem, kCi + 8u * (unsigned)cbS).x;
-        ciu = lds_ld64(smem, kCi + 8u * (unsigned)cbU);
+        cis = cis_n;
+        ciu = ciu_n;
     };
     using F_ = std::integral_constant<bool, false>;
     using T_ = std::integral_constant<bool, true>;

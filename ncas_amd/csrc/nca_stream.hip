@@ -11,10 +11,11 @@ namespace nca {
 
 // Streamed bf16 kernel for C = 64, hidden = 256: R rows per workgroup with (R-1) H W >= 79, so a
 // board's next step starts five tiles after its previous one; needs W + 1 <= 16 (single
-// perception buffer), the plan within the LDS and 16-bit halo offsets.
+// perception buffer), at most 64 halo cells (two 16-byte halo chunks per thread), the plan within
+// the LDS and 16-bit halo offsets.
 hipError_t launch_stream64(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used) {
     *used = false;
-    if (p.W + 1 > 16 || p.noise || p.fire_f32) return hipSuccess;
+    if (p.W + 1 > 16 || 2 * (p.W + 2) + 2 * p.H > 64 || p.noise || p.fire_f32) return hipSuccess;
     const int hw = p.H * p.W, nq4 = (hw + 3) / 4;
     const bool batched = !p.adaptive && !p.fire_u8;
     const int R = 1 + (St64::GAP + hw - 1) / hw;
