@@ -1,28 +1,32 @@
 // Streamed LDS-resident rollout kernel for bf16 cells with C = 64 channels and 256 hidden units
 // (gfx950): the fast path of the bf16 rollout on small grids (up to about 10x10).
 //
-// A workgroup of 4 waves (one per SIMD) owns R rows (boards) for the whole call. The cells of its
-// boards, board after board and step after step, form one stream: stream position
-// p = (s R + r) HW + q is cell q of board r at step s. The stream is cut into 16-cell tiles (tile
-// t = positions 16t .. 16t+15; a tile may span two boards or two steps, so no cell is padding),
-// and interval i (one workgroup barrier) runs four stages on four tiles, all issued by every wave:
+// A workgroup owns R rows (boards) for the whole call. The cells of its boards, board after board
+// and step after step, form one stream: stream position p = (s R + r) HW + q is cell q of board r
+// at step s. The stream is cut into 16-cell tiles (tile t = positions 16t .. 16t+15; a tile may
+// span two boards or two steps, so no cell is padding).
 //
-//   stencil    tile i     the 3x3 perception on v_mfma_f32_4x4x4_16b_bf16. Lane (cell n, channel
-//                         quad iq) reads the 9 taps of its 4 channels (bf16) from the perception
-//                         buffer P; each 4-lane block multiplies 4 cells' tap vectors by the 4
-//                         kernels (12 instructions per lane). z (bf16) -> Z[i & 1].
-//   fc1        tile i-1   h = W1 z + b1 on v_mfma_f32_16x16x32_bf16; wave w owns hidden units
-//                         [64w, 64w+64) with its W1 fragments resident in AGPRs, B operand read
-//                         from Z. The accumulators stay in registers into the next interval.
-//   epilogue   tile i-2   bf16 rounding + ReLU of those accumulators (autocast rounds fc1's output
-//                         before the ReLU) -> H[i & 1]; it runs at the start of the interval, while
-//                         the interval's LDS loads are in flight.
-//   fc2+update tile i-3   dx = W2 h + b2 with wave w owning output channels [16w, 16w+16) (W2
-//                         fragments in AGPRs, B operand read from H). The accumulator layout puts
-//                         channels 16w+4g .. 16w+4g+3 of cell n in lane (n, g), which is the
-//                         update's item: x += fire * bf16(dx) into the fp32 state M and the bf16
-//                         buffer P without another exchange; the clamped input channels of given
-//                         cells keep their value.
+// The workgroup has 8 waves, two per SIMD, specialised so that one wave's MFMAs overlap the other
+// wave's VALU and LDS work on the same SIMD:
+//   hidden wave w (0-3)    owns hidden units [64w, 64w+64) with its W1 fragments in AGPRs: fc1
+//                          h = W1 z + b1 on v_mfma_f32_16x16x32_bf16 (B operand from Z), then
+//                          bf16 rounding + ReLU (autocast rounds fc1's output before the ReLU)
+//                          into H.
+//   channel wave w (4-7)   owns channels [16(w-4), 16(w-4)+16): the 3x3 perception of its
+//                          channels on v_mfma_f32_4x4x4_16b_bf16 (lane (cell n, channel quad iq)
+//                          reads the 9 taps of its 4 channels from the perception buffer P; each
+//                          4-lane block multiplies 4 cells' tap vectors by the 4 kernels) into Z;
+//                          fc2 dx = W2 h + b2 for its 16 output channels (W2 fragments in AGPRs, B
+//                          operand from H), whose accumulator layout puts channels 4 iq .. 4 iq+3 of
+//                          cell n in lane (n, g): the update x += fire * bf16(dx) into the fp32
+//                          state M and the bf16 buffer P happens in those registers; the clamped
+//                          input channels of given cells keep their value. Channel waves also do
+//                          the end-of-step work (wrap halo refresh, fire masks).
+//
+// Interval i (one workgroup barrier) runs: stencil of tile i (-> Z[i & 1]); fc1 k-tiles 0-3 of tile
+// i-1 (from Z[(i-1) & 1]; its k-tiles 4-7 operands are loaded then and kept in registers) and fc1
+// k-tiles 4-7 + epilogue of tile i-2 (-> H[i & 1]), so a hidden wave opens each interval with 16
+// MFMAs whose operands are in registers; fc2 + update of tile i-3 (from H[(i-3) & 1]).
 //
 // P is single-buffered: the update of tile i-3 runs in the same interval as the stencil of tile
 // i, whose neighbourhoods reach W+1 <= 16 positions back, never into tile i-3. A board's next
@@ -46,7 +50,7 @@
 //   * Z: 576 B per tile row, features in quad-major order (16 iq + 4 head + ch), chunk c of row
 //     r stored at chunk c ^ (2 ((r >> 2) & 3));
 //   * H: 544 B per tile row, 16-byte chunk c of row n stored at chunk c ^ ((n >> 2) & 1); the 16
-//     hidden values of fc1 lane (n, g) of wave w are contiguous at physical position
+//     hidden values of fc1 lane (n, g) of hidden wave w are contiguous at physical position
 //     64 w + 16 g + 4 mt + v (logical hidden unit 64 w + 16 mt + 4 g + v); the fc2 fragments are
 //     packed in that order.
 // (Strides and swizzles measured conflict-free for these access patterns on gfx950; M at 272 B
@@ -76,7 +80,7 @@ struct St64 {
 };
 
 struct StPlan {
-    unsigned P, M, Z, H, cinfo, ring, fired, head, hcp, total;
+    unsigned P, M, Z, H, cinfo, ring, fired, head, hcp, evp, total;
     int R, RP, PB, NB, RH, RING;
 };
 
@@ -113,6 +117,8 @@ inline StPlan st_plan(int R, int H, int W, int c_out, int n_out, int NB) {
     o = st_al16(o + (unsigned)(n_out * c_out + n_out) * 4u);
     p.hcp = o;
     o = st_al16(o + (unsigned)(2 * (W + 2) + 2 * H) * 4u);
+    p.evp = o;  // a copy of the call's parameters for the end-of-step work
+    o = st_al16(o + (unsigned)sizeof(RolloutParams));
     p.total = o;
     return p;
 }
@@ -120,7 +126,7 @@ inline StPlan st_plan(int R, int H, int W, int c_out, int n_out, int NB) {
 struct StParams {
     RolloutParams a;
     int R, RP, PB, NB, RH, RING, T;
-    unsigned l_P, l_M, l_Z, l_H, l_cinfo, l_ring, l_fired, l_head, l_hcp;
+    unsigned l_P, l_M, l_Z, l_H, l_cinfo, l_ring, l_fired, l_head, l_hcp, l_evp;
     unsigned off_w1q, off_w2h;
 };
 
@@ -153,14 +159,18 @@ __device__ __forceinline__ uint32_t relu_bf16x2(uint32_t v) {
 }
 __device__ __forceinline__ short bf16_bits(float v) { return __builtin_bit_cast(short, (__bf16)v); }
 
-__global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
+__global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
     using S = St64;
+    constexpr int NT = 512;
     const RolloutParams &a = sp.a;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, n = lane & 15;  // n: cell of the tile (MFMA column), g: lane group
-    const int iq = 4 * wave + g;             // channel quad of the lane's stencil / update items
+    const bool hidden_wave = wave < 4;
+    const int ws = wave & 3;                 // hidden slice or channel set of the wave
+    const int iq = 4 * ws + g;               // channel quad of a channel wave's lane
+    const int tb = tid - 256;                // thread index among the channel waves
     const int H = a.H, W = a.W, HWn = H * W;
     const int R = sp.R, RH = sp.RH, RP = sp.RP, PB = sp.PB, NB = sp.NB, RING = sp.RING;
     const int64_t rbase = (int64_t)blockIdx.x * R;
@@ -182,102 +192,31 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
         return *reinterpret_cast<float *>(smem + m_cell(r, q) + 4u * (unsigned)ch);
     };
 
-    // ---- registers: MLP weight fragments (AGPRs) and biases
-    bf16x8 w1f[S::MT1][S::KT1];
-    bf16x8 w2f[S::KT2];
-    f32x4 b1v[S::MT1];
-    f32x4 b2v;
-    {
-        const bf16x8 *w1 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w1q);
-        const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2h);
-        const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
-        const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
-#pragma unroll
-        for (int mt = 0; mt < S::MT1; ++mt) {
-#pragma unroll
-            for (int kt = 0; kt < S::KT1; ++kt) w1f[mt][kt] = w1[((wave * S::MT1 + mt) * S::KT1 + kt) * 64 + lane];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[wave * 64 + 16 * mt + 4 * g + v];
-        }
-#pragma unroll
-        for (int kt = 0; kt < S::KT2; ++kt) w2f[kt] = w2[(wave * S::KT2 + kt) * 64 + lane];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) b2v[v] = b2[4 * iq + v];
-#pragma unroll
-        for (int mt = 0; mt < S::MT1; ++mt)
-#pragma unroll
-            for (int kt = 0; kt < S::KT1; ++kt) asm volatile("" : "+a"(w1f[mt][kt]));
-#pragma unroll
-        for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[kt]));
-    }
-    // stencil B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 placed at the
-    // k slot of channel c (the A operand of tap 8 is the 4 channels' tap-8 values as loaded)
-    s16x4 kb0, kb1, kb2[4];
-    {
-        const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
-        const int j = lane & 3;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            kb0[k] = bf16_bits(kern[j * 9 + k]);
-            kb1[k] = bf16_bits(kern[j * 9 + 4 + k]);
-        }
-        const short k8 = bf16_bits(kern[j * 9 + 8]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
-    }
-    // all ones where the lane's channel 4 iq + v lies in the clamped input slice
-    unsigned imv[4];
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int c = 4 * iq + v;
-        imv[v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
-        asm volatile("" : "+v"(imv[v]));  // kept a plain VGPR mask (no per-channel SGPR lane masks)
-    }
-    // lane-constant LDS offsets
-    const int sig = 2 * ((n >> 2) & 3);
-    const unsigned kZ0 = sp.l_Z + (unsigned)n * S::ZS + 16u * (unsigned)(g ^ (sig & 3));
-    const unsigned kZe = kZ0 + 64u * (unsigned)(sig >> 2), kZo = kZ0 - 64u * (unsigned)(sig >> 2);
-    unsigned kZw;
-    {
-        const int j = lane & 3, b = lane >> 2;
-        kZw = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 16u * (unsigned)((2 * iq + (j >> 1)) ^ (2 * (b & 3))) +
-              8u * (unsigned)(j & 1);
-    }
-    // H row n: 16-byte chunk c stored at chunk c ^ hx, hx = (n >> 2) & 1
-    const unsigned hx = (unsigned)((n >> 2) & 1);
-    const unsigned kHw0 = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)wave + 32u * (unsigned)g + 16u * hx;
-    const unsigned kHw1 = kHw0 + 16u - 32u * hx;
-    const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * ((unsigned)g ^ hx);
-    // + centre: the top-left tap, the left taps of the middle and bottom rows
-    const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS), kPs1 = kPs + (unsigned)RP, kPs2 = kPs1 + (unsigned)RP;
-    const unsigned kCi = sp.l_cinfo + 8u * (unsigned)n;
-    const unsigned kRg = sp.l_ring + (unsigned)n;
-
     // ---- load rows (phantom rows of a ragged last workgroup hold zeros and never fire)
-    for (int e = tid; e < R * S::C * HWn; e += 256) {
+    for (int e = tid; e < R * S::C * HWn; e += NT) {
         const int r = e / (S::C * HWn), rem = e - r * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
         const float v = r < Rw ? a.x_in[rbase * S::C * HWn + e] : 0.0f;
         m_at(r, q, ch) = v;
         *reinterpret_cast<__bf16 *>(smem + p_cell(r, q) + 2 * ch) = (__bf16)v;
     }
-    for (int c = tid; c < RH + 16; c += 256) {
+    for (int c = tid; c < RH + 16; c += NT) {
         const int cc = c < RH ? c : c - RH, r = cc / HWn, q = cc - r * HWn;
         uint2 ci;
         ci.x = p_cell(r, q);
         ci.y = m_cell(r, q) | (r < Rw && a.given[(rbase + r) * HWn + q] ? 0x80000000u : 0u);
         cinfo[c] = ci;
     }
-    for (int e = tid; e < R; e += 256) firedL[e] = 0;
+    for (int e = tid; e < R; e += NT) firedL[e] = 0;
+    for (int e = tid; e < (int)(sizeof(RolloutParams) / 4); e += NT)
+        reinterpret_cast<unsigned *>(smem + sp.l_evp)[e] = reinterpret_cast<const unsigned *>(&a)[e];
     {
         const float *hw = reinterpret_cast<const float *>(a.packed + a.off_headw);
         const float *hb = reinterpret_cast<const float *>(a.packed + a.off_headb);
         const int nw = a.n_out * a.c_out;
-        for (int e = tid; e < nw + a.n_out; e += 256) headL[e] = e < nw ? hw[e] : hb[e - nw];
+        for (int e = tid; e < nw + a.n_out; e += NT) headL[e] = e < nw ? hw[e] : hb[e - nw];
     }
     const int Wp = W + 2, nhalo = 2 * Wp + 2 * H;
-    for (int h = tid; h < nhalo; h += 256) {
+    for (int h = tid; h < nhalo; h += NT) {
         int ip, jp;
         if (h < Wp) {
             ip = 0;
@@ -300,40 +239,23 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     if (a.padding != 2) {
         const float *padv = reinterpret_cast<const float *>(a.packed + a.off_padv);
         for (int r = 0; r < R; ++r)
-            for (int e = tid; e < nhalo * S::C; e += 256) {
+            for (int e = tid; e < nhalo * S::C; e += NT) {
                 const int h = e >> 6, ch = e & 63;
                 const unsigned dst = hcp[h] & 0xffffu;
                 *reinterpret_cast<__bf16 *>(smem + sp.l_P + (unsigned)(r * PB) + dst + 2 * ch) =
                     (__bf16)(a.padding == 1 ? padv[ch] : 0.0f);
             }
-    }
-    // wrap halo of board r: 16-byte chunks of 8 channels
-    auto wrap_halo_all = [&](int r) __attribute__((always_inline)) {
-        const unsigned base = sp.l_P + (unsigned)(r * PB);
-        for (int e = tid; e < nhalo * 8; e += 256) {
-            const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
-            const float4 v = lds_ld128f(smem, base + (hc >> 16) + o);
-            lds_st128f(smem, base + (hc & 0xffffu) + o, v);
+    } else {
+        for (int r = 0; r < R; ++r) {
+            const unsigned base = sp.l_P + (unsigned)(r * PB);
+            for (int e = tid; e < nhalo * 8; e += NT) {
+                const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
+                const float4 v = lds_ld128f(smem, base + (hc >> 16) + o);
+                lds_st128f(smem, base + (hc & 0xffffu) + o, v);
+            }
         }
-    };
-    // the thread's (at most two, nhalo <= 64) 16-byte halo chunks: board-relative source offset
-    // in the high half, destination in the low half, 0 when there is none (offset 0 is a corner
-    // halo cell, never a source)
-    unsigned hsd0 = 0, hsd1 = 0;
-    auto halo_item = [&](int e) -> unsigned {
-        if (e >= nhalo * 8) return 0u;
-        const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
-        return (((hc >> 16) + o) << 16) | ((hc & 0xffffu) + o);
-    };
-    // wrap halo of board r after one of its steps: both chunks loaded, then stored
-    auto wrap_halo = [&](int r) __attribute__((always_inline)) {
-        const unsigned base = sp.l_P + (unsigned)(r * PB);
-        float4 v0, v1;
-        if (hsd0) v0 = lds_ld128f(smem, base + (hsd0 >> 16));
-        if (hsd1) v1 = lds_ld128f(smem, base + (hsd1 >> 16));
-        if (hsd0) lds_st128f(smem, base + (hsd0 & 0xffffu), v0);
-        if (hsd1) lds_st128f(smem, base + (hsd1 & 0xffffu), v1);
-    };
+    }
+    // ---- end-of-step work, done by the channel waves (thread tb of 256)
     // fire byte of stream position (s, r, q): ring slot ((s mod 2NB) RH + r HW + q); slots below
     // 16 are mirrored after the ring so that a tile reads 16 consecutive bytes
     auto ring_put = [&](int s, int r, int q, int f) __attribute__((always_inline)) {
@@ -345,23 +267,23 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     // masks), one Philox evaluation per 4 cells
     const int nq4 = (HWn + 3) >> 2;
     const bool batched = !a.adaptive && !a.fire_u8;
-    auto draw_batch = [&](int b) __attribute__((always_inline)) {
+    auto draw_batch = [&](const RolloutParams &pa, int b) __attribute__((always_inline)) {
         const int per_row = NB * nq4;
-        for (int it = tid; it < R * per_row; it += 256) {
+        for (int it = tb; it < R * per_row; it += 256) {
             const int r = it / per_row, rem = it - r * per_row, sl = rem / nq4, qq = rem - sl * nq4;
             const int s = b * NB + sl;
-            if (s >= a.n_steps) continue;
+            if (s >= pa.n_steps) continue;
             float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
             if (r < Rw) {
-                const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
-                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+                const uint64_t key = pa.step_seeds ? pa.step_seeds[s] : pa.seed;
+                cell_uniforms4(key, (uint32_t)(pa.row0 + rbase + r), (uint32_t)(pa.step0 + s), (uint32_t)qq, u);
             }
             int cnt = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int q = 4 * qq + e;
                 if (q < HWn) {
-                    const int f = r < Rw && u[e] < a.p;
+                    const int f = r < Rw && u[e] < pa.p;
                     ring_put(s, r, q, f);
                     cnt += f;
                 }
@@ -371,13 +293,13 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     };
     // masks of board r for step s: adaptive gating reads the board's current state (the state
     // before step s), injected masks are copied
-    auto draw_step = [&](int r, int s) __attribute__((always_inline)) {
-        for (int it = tid; it < nq4; it += 256) {
+    auto draw_step = [&](const RolloutParams &pa, int r, int s) __attribute__((always_inline)) {
+        for (int it = tb; it < nq4; it += 256) {
             const int qq = it;
             float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-            if (r < Rw && !a.fire_u8) {
-                const uint64_t key = a.step_seeds ? a.step_seeds[s] : a.seed;
-                cell_uniforms4(key, (uint32_t)(a.row0 + rbase + r), (uint32_t)(a.step0 + s), (uint32_t)qq, u);
+            if (r < Rw && !pa.fire_u8) {
+                const uint64_t key = pa.step_seeds ? pa.step_seeds[s] : pa.seed;
+                cell_uniforms4(key, (uint32_t)(pa.row0 + rbase + r), (uint32_t)(pa.step0 + s), (uint32_t)qq, u);
             }
             int cnt = 0;
 #pragma unroll
@@ -386,16 +308,16 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                 if (q >= HWn) continue;
                 int f = 0;
                 if (r < Rw) {
-                    if (a.fire_u8) {
-                        f = a.fire_u8[((int64_t)s * a.rows + rbase + r) * HWn + q] != 0;
+                    if (pa.fire_u8) {
+                        f = pa.fire_u8[((int64_t)s * pa.rows + rbase + r) * HWn + q] != 0;
                     } else {
-                        float pc = a.p;
-                        if (a.adaptive) {
+                        float pc = pa.p;
+                        if (pa.adaptive) {
                             int am;
-                            const float cf = cell_readout_fn([&](int v) { return m_at(r, q, a.out_off + v); }, a.c_out,
-                                                             a.n_out, a.head_kind, headL, headL + a.n_out * a.c_out,
+                            const float cf = cell_readout_fn([&](int v) { return m_at(r, q, pa.out_off + v); }, pa.c_out,
+                                                             pa.n_out, pa.head_kind, headL, headL + pa.n_out * pa.c_out,
                                                              &am);
-                            if (cf > a.tau || (a.given_confident && a.given[(rbase + r) * HWn + q])) pc = a.p_low;
+                            if (cf > pa.tau || (pa.given_confident && pa.given[(rbase + r) * HWn + q])) pc = pa.p_low;
                         }
                         f = u[e] < pc;
                     }
@@ -407,23 +329,18 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
         }
     };
     __syncthreads();
-    if (a.padding == 2) {
-        hsd0 = halo_item(tid);
-        hsd1 = halo_item(tid + 256);
-        for (int r = 0; r < R; ++r) wrap_halo_all(r);
-    }
-    if (a.n_steps > 0) {
+    if (!hidden_wave && a.n_steps > 0) {
         if (batched) {
-            draw_batch(0);
-            draw_batch(1);
+            draw_batch(a, 0);
+            draw_batch(a, 1);
         } else {
-            for (int r = 0; r < R; ++r) draw_step(r, 0);
+            for (int r = 0; r < R; ++r) draw_step(a, r, 0);
         }
     }
     __syncthreads();
     // the step's clamp lands in M (P keeps the caller's state for the first perception)
     if (a.n_steps > 0 && a.c_in > 0) {
-        for (int e = tid; e < Rw * HWn * a.c_in; e += 256) {
+        for (int e = tid; e < Rw * HWn * a.c_in; e += NT) {
             const int cell = e / a.c_in, ci = e - cell * a.c_in;
             const int r = cell / HWn, q = cell - r * HWn;
             if (!a.given[(rbase + r) * HWn + q]) continue;
@@ -432,91 +349,271 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
     }
     __syncthreads();
 
-    // ---- the tile stream
+    using F_ = std::integral_constant<bool, false>;
+    using T_ = std::integral_constant<bool, true>;
+    using P0 = std::integral_constant<unsigned, 0>;
+    using P1 = std::integral_constant<unsigned, 1>;
     const int T = sp.T;
     const int total = a.n_steps * RH;
-    int i = 0;
-    int cbS = 0;               // cinfo index of the stencil tile's first cell: (16 i) mod RH
-    int cbU = RH - 48;         // the same for the update tile i-3: (16 (i-3)) mod RH, RH >= 80
-    int rbU = RING - 48;       // ring slot of the update tile's first cell: (16 (i-3)) mod RING
-    // events: end of (board, step) unit k -> wrap halo refresh / next step's masks of the board;
-    // batched masks of batch nb
-    const bool unit_events = a.padding == 2 || !batched;
-    // unit (board ur, step us) ends at stream position uend; batch nb is drawn when the update
-    // stage has passed position dpos = (nb - 1) NB RH
-    int ur = 0, us = 0, uend = HWn - 1;
-    int ev_unit = unit_events ? (uend >> 4) + 4 : 0x7fffffff;
-    int nb = 2, dpos = NB * RH;
-    int ev_batch = (batched && 2 * NB < a.n_steps) ? (dpos >> 4) + 4 : 0x7fffffff;
-    unsigned cis = cinfo[n].x, cis_n = 0;
-    uint2 ciu = make_uint2(0u, 0u), ciu_n = ciu;
-
-    f32x4 acc[S::MT1];
+    // Both wave kinds run the same interval sequence (prologue 0-2, steady state, drain T..T+2)
+    // with one workgroup barrier per interval.
+    if (T > 0 && hidden_wave) {
+        // ================= hidden waves: fc1 + epilogue
+        bf16x8 w1f[S::MT1][S::KT1];
+        f32x4 b1v[S::MT1];
+        {
+            const bf16x8 *w1 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w1q);
+            const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
 #pragma unroll
-    for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
-    bf16x8 zq[4];  // Z operands of fc1's last four k-tiles, carried into the next interval
+            for (int mt = 0; mt < S::MT1; ++mt) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+                for (int kt = 0; kt < S::KT1; ++kt) w1f[mt][kt] = w1[((ws * S::MT1 + mt) * S::KT1 + kt) * 64 + lane];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) zq[k][e] = (__bf16)0.0f;
-
-    auto events = [&]() __attribute__((always_inline)) {
-        while (i == ev_unit) {
-            if (a.padding == 2) wrap_halo(ur);
-            if (!batched && us + 1 < a.n_steps) draw_step(ur, us + 1);
-            if (++ur == R) {
-                ur = 0;
-                ++us;
+                for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[ws * 64 + 16 * mt + 4 * g + v];
             }
-            uend += HWn;
-            ev_unit = (uend >> 4) + 4;
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt)
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt) asm volatile("" : "+a"(w1f[mt][kt]));
         }
-        if (i == ev_batch) {
-            draw_batch(nb);
-            ++nb;
-            dpos += NB * RH;
-            ev_batch = nb * NB < a.n_steps ? (dpos >> 4) + 4 : 0x7fffffff;
+        const int sig = 2 * ((n >> 2) & 3);
+        const unsigned kZ0 = sp.l_Z + (unsigned)n * S::ZS + 16u * (unsigned)(g ^ (sig & 3));
+        const unsigned kZe = kZ0 + 64u * (unsigned)(sig >> 2), kZo = kZ0 - 64u * (unsigned)(sig >> 2);
+        // H row n: 16-byte chunk c stored at chunk c ^ hx, hx = (n >> 2) & 1
+        const unsigned hx = (unsigned)((n >> 2) & 1);
+        const unsigned kHw0 = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)ws + 32u * (unsigned)g + 16u * hx;
+        const unsigned kHw1 = kHw0 + 16u - 32u * hx;
+        bf16x8 zq[S::KT1];  // Z operands of a tile, loaded one interval before its fc1 runs
+#pragma unroll
+        for (int k = 0; k < S::KT1; ++k)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) zq[k][e] = (__bf16)0.0f;
+        // fcb: fc1 of tile i-2 (all 32 MFMAs from registers) and its epilogue -> H[i & 1];
+        // fca: the Z operands of tile i-1, requested once those MFMAs have read the registers
+        auto hinterval = [&](auto fca_c, auto fcb_c, auto par_v) __attribute__((always_inline)) {
+            constexpr bool FCA = decltype(fca_c)::value, FCB = decltype(fcb_c)::value;
+            const unsigned PAR = par_v;
+            if (FCB) {
+                f32x4 acc[S::MT1];
+#pragma unroll
+                for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt)
+#pragma unroll
+                    for (int mt = 0; mt < S::MT1; ++mt)
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zq[kt], acc[mt], 0, 0, 0);
+                uint4 h0, h1;
+                h0.x = relu_bf16x2(cvt_pk_bf16(acc[0][0], acc[0][1]));
+                h0.y = relu_bf16x2(cvt_pk_bf16(acc[0][2], acc[0][3]));
+                h0.z = relu_bf16x2(cvt_pk_bf16(acc[1][0], acc[1][1]));
+                h0.w = relu_bf16x2(cvt_pk_bf16(acc[1][2], acc[1][3]));
+                h1.x = relu_bf16x2(cvt_pk_bf16(acc[2][0], acc[2][1]));
+                h1.y = relu_bf16x2(cvt_pk_bf16(acc[2][2], acc[2][3]));
+                h1.z = relu_bf16x2(cvt_pk_bf16(acc[3][0], acc[3][1]));
+                h1.w = relu_bf16x2(cvt_pk_bf16(acc[3][2], acc[3][3]));
+                lds_st128(smem, kHw0 + PAR * S::HBUF, h0);
+                lds_st128(smem, kHw1 + PAR * S::HBUF, h1);
+            }
+            if (FCA) {
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt)
+                    zq[kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
+                                                               64u * kt);
+            }
+        };
+        int i = 0;
+        hinterval(F_{}, F_{}, P0{});
+        __syncthreads();
+        hinterval(T_{}, F_{}, P1{});
+        __syncthreads();
+        hinterval(T_{}, T_{}, P0{});
+        __syncthreads();
+        for (i = 3; i + 1 < T; i += 2) {
+            hinterval(T_{}, T_{}, P1{});
+            __syncthreads();
+            hinterval(T_{}, T_{}, P0{});
+            __syncthreads();
         }
-    };
+        if (i < T) {
+            hinterval(T_{}, T_{}, P1{});
+            __syncthreads();
+            ++i;
+        }
+        hinterval(T_{}, T_{}, (unsigned)(i & 1));
+        __syncthreads();
+        hinterval(F_{}, T_{}, (unsigned)((i + 1) & 1));
+        __syncthreads();
+        hinterval(F_{}, F_{}, (unsigned)(i & 1));
+        __syncthreads();
+    } else if (T > 0) {
+        // ================= channel waves: stencil, fc2 + update, end-of-step work
+        // the channel wave holds the interval's longest dependency chain: its instructions win the
+        // SIMD's issue arbitration over the hidden wave's MFMAs
+        __builtin_amdgcn_s_setprio(3);
+        bf16x8 w2f[S::KT2];
+        f32x4 b2v;
+        {
+            const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2h);
+            const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt) w2f[kt] = w2[(ws * S::KT2 + kt) * 64 + lane];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) b2v[v] = b2[4 * iq + v];
+#pragma unroll
+            for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[kt]));
+        }
+        // stencil B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 placed at the
+        // k slot of channel c (the A operand of tap 8 is the 4 channels' tap-8 values as loaded)
+        s16x4 kb0, kb1, kb2[4];
+        {
+            const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
+            const int j = lane & 3;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                kb0[k] = bf16_bits(kern[j * 9 + k]);
+                kb1[k] = bf16_bits(kern[j * 9 + 4 + k]);
+            }
+            const short k8 = bf16_bits(kern[j * 9 + 8]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
+        }
+        // all ones where the lane's channel 4 iq + v lies in the clamped input slice
+        unsigned imv[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int c = 4 * iq + v;
+            imv[v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
+            asm volatile("" : "+v"(imv[v]));  // kept a plain VGPR mask (no per-channel SGPR lane masks)
+        }
+        unsigned kZw;
+        {
+            const int j = lane & 3, b = lane >> 2;
+            kZw = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 16u * (unsigned)((2 * iq + (j >> 1)) ^ (2 * (b & 3))) +
+                  8u * (unsigned)(j & 1);
+        }
+        const unsigned hx = (unsigned)((n >> 2) & 1);
+        const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * ((unsigned)g ^ hx);
+        // + centre: the top-left tap, the left taps of the middle and bottom rows
+        const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS), kPs1 = kPs + (unsigned)RP, kPs2 = kPs1 + (unsigned)RP;
+        const unsigned kCi = sp.l_cinfo + 8u * (unsigned)n;
+        const unsigned kRg = sp.l_ring + (unsigned)n;
+        // the thread's (at most two, nhalo <= 64) 16-byte wrap-halo chunks: board-relative source
+        // offset in the high half, destination in the low half, 0 when there is none (offset 0 is
+        // a corner halo cell, never a source)
+        auto halo_item = [&](int e) -> unsigned {
+            if (e >= nhalo * 8) return 0u;
+            const unsigned hc = hcp[e >> 3], o = 16u * (unsigned)(e & 7);
+            return (((hc >> 16) + o) << 16) | ((hc & 0xffffu) + o);
+        };
+        const unsigned hsd0 = a.padding == 2 ? halo_item(tb) : 0u, hsd1 = a.padding == 2 ? halo_item(tb + 256) : 0u;
+        // wrap halo of board r after one of its steps: both chunks loaded, then stored
+        auto wrap_halo = [&](int r) __attribute__((always_inline)) {
+            const unsigned base = sp.l_P + (unsigned)(r * PB);
+            float4 v0, v1;
+            if (hsd0) v0 = lds_ld128f(smem, base + (hsd0 >> 16));
+            if (hsd1) v1 = lds_ld128f(smem, base + (hsd1 >> 16));
+            if (hsd0) lds_st128f(smem, base + (hsd0 & 0xffffu), v0);
+            if (hsd1) lds_st128f(smem, base + (hsd1 & 0xffffu), v1);
+        };
 
-    // One interval, in groups separated by scheduling fences (sched_barrier) so that the order
-    // below is the issue order. fc1 of a tile is split over two intervals: k-tiles 0-3 in the
-    // interval after its stencil, k-tiles 4-7 (their Z operands loaded then and kept in
-    // registers) at the start of the next one, so each interval opens with 16 MFMAs that need
-    // no LDS data while its loads stream in. Every LDS load is requested about two groups
-    // before the MFMAs or VALU work that consume it.
+        int i = 0;
+        int cbS = 0;         // cinfo index of the stencil tile's first cell: (16 i) mod RH
+        int cbU = RH - 48;   // the same for the update tile i-3: (16 (i-3)) mod RH, RH >= 80
+        int rbU = RING - 48; // ring slot of the update tile's first cell: (16 (i-3)) mod RING
+        // unit (board ur, step us) ends at stream position uend; batch nb is drawn when the update
+        // stage has passed position dpos = (nb - 1) NB RH
+        const bool unit_events = a.padding == 2 || !batched;
+        int ur = 0, us = 0, uend = HWn - 1;
+        int ev_unit = unit_events ? (uend >> 4) + 4 : 0x7fffffff;
+        int nb = 2, dpos = NB * RH;
+        int ev_batch = (batched && 2 * NB < a.n_steps) ? (dpos >> 4) + 4 : 0x7fffffff;
+        unsigned cis = cinfo[n].x, cis_n = 0;
+        uint2 ciu = make_uint2(0u, 0u), ciu_n = ciu;
+
+        // the end-of-step work reads the call's parameters from the LDS copy, so that they do not
+        // occupy scalar registers through the loop
+        const bool wrap = a.padding == 2;
+        auto events = [&]() __attribute__((always_inline)) {
+            const RolloutParams &ea = *reinterpret_cast<const RolloutParams *>(smem + sp.l_evp);
+            while (i == ev_unit) {
+                if (wrap) wrap_halo(ur);
+                if (!batched && us + 1 < ea.n_steps) draw_step(ea, ur, us + 1);
+                if (++ur == R) {
+                    ur = 0;
+                    ++us;
+                }
+                uend += HWn;
+                ev_unit = (uend >> 4) + 4;
+            }
+            if (i == ev_batch) {
+                draw_batch(ea, nb);
+                ++nb;
+                dpos += NB * RH;
+                ev_batch = nb * NB < ea.n_steps ? (dpos >> 4) + 4 : 0x7fffffff;
+            }
+        };
+        // st: stencil of tile i -> Z[i & 1]; up: fc2 + update of tile i-3 (H[(i-3) & 1]). The
+        // issue order is fixed by scheduling fences: all loads first, then the stencil's permutes
+        // with the fc2 chain, the stencil's MFMAs, the update, the stores.
+#ifndef NCA_CH_ORDER
+#define NCA_CH_ORDER 1
+#endif
 #ifndef NCA_FENCE
 #define NCA_FENCE() __builtin_amdgcn_sched_barrier(0)
 #endif
-    auto interval = [&](auto st_c, auto fc_c, auto ep_c, auto up_c, auto par_v, auto last_c)
-                        __attribute__((always_inline)) {
-        constexpr bool DST = decltype(st_c)::value, DFC = decltype(fc_c)::value, DEP = decltype(ep_c)::value,
-                       DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
-        const unsigned PAR = par_v;
-        bf16x8 hb[S::KT2];
-        bf16x8 zf[4];
-        uint2 nbv[9];
-        auto load_h = [&](int kt) __attribute__((always_inline)) {
-            if (DUP) hb[kt] = *reinterpret_cast<const bf16x8 *>(smem + kHr + (PAR ^ 1u) * S::HBUF + 64u * kt);
-        };
-        auto zaddr = [&](int kt) -> const bf16x8 * {
-            return reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF + 64u * kt);
-        };
-        auto load_z = [&](int kt) __attribute__((always_inline)) {
-            if (DFC) zf[kt] = *zaddr(kt);
-        };
-        auto fc1_kt = [&](int kt, const bf16x8 &b) __attribute__((always_inline)) {
+        auto cinterval = [&](auto st_c, auto up_c, auto par_v, auto last_c) __attribute__((always_inline)) {
+            constexpr bool DST = decltype(st_c)::value, DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
+            const unsigned PAR = par_v;
+            uint2 nbv[9];
+            bf16x8 hb[S::KT2];
+            float4 m4;
+            float fu = 0.0f;
+            unsigned madr = 0, padr = 0, gvm = 0;
+            auto load_taps = [&]() __attribute__((always_inline)) {
+                if (DST) {
+                    const unsigned r0 = cis + kPs, r1 = cis + kPs1, r2 = cis + kPs2;
+                    nbv[0] = lds_ld64(smem, r0);
+                    nbv[1] = lds_ld64(smem, r0 + S::CS);
+                    nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
+                    nbv[3] = lds_ld64(smem, r1);
+                    nbv[4] = lds_ld64(smem, r1 + S::CS);
+                    nbv[5] = lds_ld64(smem, r1 + 2 * S::CS);
+                    nbv[6] = lds_ld64(smem, r2);
+                    nbv[7] = lds_ld64(smem, r2 + S::CS);
+                    nbv[8] = lds_ld64(smem, r2 + 2 * S::CS);
+                }
+            };
+            auto load_h = [&]() __attribute__((always_inline)) {
+                if (DUP) {
 #pragma unroll
-            for (int mt = 0; mt < S::MT1; ++mt)
-                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], b, acc[mt], 0, 0, 0);
-        };
-        f32x4 acc2 = b2v;
-        auto fc2_k = [&](int k) __attribute__((always_inline)) {
-            if (DUP) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[k], hb[k], acc2, 0, 0, 0);
-        };
-        s16x4 sa0[4], sa1[4];
-        auto perms = [&](int c) __attribute__((always_inline)) {
-            if (DST) {
+                    for (int kt = 0; kt < S::KT2; ++kt)
+                        hb[kt] = *reinterpret_cast<const bf16x8 *>(smem + kHr + (PAR ^ 1u) * S::HBUF + 64u * kt);
+                    madr = (ciu.y & 0x7fffffffu) + 16u * iq;
+                    m4 = lds_ld128f(smem, madr);
+                    fu = (float)smem[kRg + (unsigned)rbU];
+                    gvm = (unsigned)((int)ciu.y >> 31);  // all ones for a given cell
+                    padr = ciu.x + 8u * iq;
+                }
+            };
+            if (NCA_CH_ORDER == 1) {
+                load_taps();
+                load_h();
+            } else {
+                load_h();
+                load_taps();
+            }
+            {  // next interval's table entries (the tables never change)
+                int cs = cbS + 16, cu = cbU + 16;
+                if (cs >= RH) cs -= RH;
+                if (cu >= RH) cu -= RH;
+                cis_n = lds_ld64(smem, kCi + 8u * (unsigned)cs).x;
+                ciu_n = lds_ld64(smem, kCi + 8u * (unsigned)cu);
+            }
+            NCA_FENCE();
+            s16x4 sa0[4], sa1[4];
+            auto perms = [&](int c) __attribute__((always_inline)) {
                 const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
                 const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nbv[1].x : nbv[1].y, c < 2 ? nbv[0].x : nbv[0].y, sel);
                 const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nbv[3].x : nbv[3].y, c < 2 ? nbv[2].x : nbv[2].y, sel);
@@ -524,13 +621,15 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                 const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nbv[7].x : nbv[7].y, c < 2 ? nbv[6].x : nbv[6].y, sel);
                 sa0[c] = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
                 sa1[c] = __builtin_bit_cast(s16x4, make_uint2(p45, p67));
-            }
-        };
-        f32x4 zc[4];
-        // the stencil of channels c0 and c0+1 with their two MFMA chains interleaved
-        auto stencil2 = [&](int c0) __attribute__((always_inline)) {
-            if (DST) {
-                const s16x4 a2 = __builtin_bit_cast(s16x4, nbv[8]);
+            };
+            f32x4 acc2 = b2v;
+            auto fc2_k = [&](int k) __attribute__((always_inline)) {
+                if (DUP) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[k], hb[k], acc2, 0, 0, 0);
+            };
+            f32x4 zc[4];
+            const s16x4 a2 = __builtin_bit_cast(s16x4, nbv[8]);
+            // two channels' MFMA chains interleaved
+            auto stencil2 = [&](int c0) __attribute__((always_inline)) {
                 f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
                 d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0], kb0, d0, 0, 0, 0);
                 d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0 + 1], kb0, d1, 0, 0, 0);
@@ -540,225 +639,130 @@ __global__ void __launch_bounds__(256, 1) rollout_stream64(StParams sp) {
                 d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0 + 1], d1, 0, 0, 0);
                 zc[c0] = d0;
                 zc[c0 + 1] = d1;
+            };
+            if (DST) {
+                perms(0);
+                perms(1);
+            }
+            fc2_k(0);
+            fc2_k(1);
+            NCA_FENCE();
+            if (DST) {
+                perms(2);
+                perms(3);
+                stencil2(0);
+            }
+            fc2_k(2);
+            fc2_k(3);
+            NCA_FENCE();
+            if (DST) stencil2(2);
+            fc2_k(4);
+            fc2_k(5);
+            NCA_FENCE();
+            if (DST) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    uint2 o;
+                    o.x = cvt_pk_bf16(zc[0][r], zc[1][r]);
+                    o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
+                    lds_st64(smem, kZw + PAR * S::ZBUF + (unsigned)r * S::ZS, o);
+                }
+            }
+            fc2_k(6);
+            fc2_k(7);
+            NCA_FENCE();
+            if (DUP) {
+                const uint32_t d01 = cvt_pk_bf16(acc2[0], acc2[1]), d23 = cvt_pk_bf16(acc2[2], acc2[3]);
+                const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
+                const float xo[4] = {m4.x, m4.y, m4.z, m4.w};
+                float u[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
+                    const unsigned km = imv[v] & gvm;                     // clamped: keep x
+                    u[v] = __uint_as_float((km & __float_as_uint(xo[v])) | (~km & __float_as_uint(uv)));
+                }
+                bool ok = true;
+                if (LAST) ok = 16 * (i - 3) + n < total;
+                if (ok) {
+                    lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
+                    lds_st64(smem, padr, make_uint2(cvt_pk_bf16(u[0], u[1]), cvt_pk_bf16(u[2], u[3])));
+                }
             }
         };
-        uint4 h0, h1;
-        // ---- G0: fc1 of tile i-2, k-tile 4; taps of tile i, first H operand
-        if (DST) {
-            const unsigned r0 = cis + kPs, r1 = cis + kPs1, r2 = cis + kPs2;
-            nbv[0] = lds_ld64(smem, r0);
-            nbv[1] = lds_ld64(smem, r0 + S::CS);
-            nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
-            nbv[3] = lds_ld64(smem, r1);
-            nbv[4] = lds_ld64(smem, r1 + S::CS);
-            nbv[5] = lds_ld64(smem, r1 + 2 * S::CS);
-            nbv[6] = lds_ld64(smem, r2);
-            nbv[7] = lds_ld64(smem, r2 + S::CS);
-            nbv[8] = lds_ld64(smem, r2 + 2 * S::CS);
-        }
-        load_h(0);
-        if (DEP) fc1_kt(4, zq[0]);
-        NCA_FENCE();
-        // ---- G1: k-tile 5
-        load_h(1);
-        load_h(2);
-        load_h(3);
-        if (DEP) fc1_kt(5, zq[1]);
-        NCA_FENCE();
-        // ---- G2: k-tile 6
-        load_z(0);
-        load_z(1);
-        load_h(4);
-        if (DEP) fc1_kt(6, zq[2]);
-        NCA_FENCE();
-        // ---- G3: k-tile 7 (fc1 of tile i-2 done); permutes of channels 0-1
-        load_h(5);
-        load_h(6);
-        if (DEP) fc1_kt(7, zq[3]);
-        perms(0);
-        perms(1);
-        NCA_FENCE();
-        // ---- G4: stencil of channels 0-1, fc2 of tile i-3 starts; half of the epilogue
-        load_h(7);
-        load_z(2);
-        stencil2(0);
-        fc2_k(0);
-        fc2_k(1);
-        if (DEP) {
-            h0.x = relu_bf16x2(cvt_pk_bf16(acc[0][0], acc[0][1]));
-            h0.y = relu_bf16x2(cvt_pk_bf16(acc[0][2], acc[0][3]));
-            h0.z = relu_bf16x2(cvt_pk_bf16(acc[1][0], acc[1][1]));
-            h0.w = relu_bf16x2(cvt_pk_bf16(acc[1][2], acc[1][3]));
-        }
-        perms(2);
-        perms(3);
-        NCA_FENCE();
-        // ---- G5: stencil of channels 2-3, fc2; epilogue of tile i-2 ends -> H[PAR]
-        float4 m4;
-        float fu = 0.0f;
-        unsigned madr = 0, padr = 0, gvm = 0;
-        load_z(3);
-        if (DUP) {
-            madr = (ciu.y & 0x7fffffffu) + 16u * iq;
-            m4 = lds_ld128f(smem, madr);
-            fu = (float)smem[kRg + (unsigned)rbU];
-            gvm = (unsigned)((int)ciu.y >> 31);  // all ones for a given cell
-            padr = ciu.x + 8u * iq;
-        }
-        stencil2(2);
-        fc2_k(2);
-        fc2_k(3);
-        if (DEP) {
-            h1.x = relu_bf16x2(cvt_pk_bf16(acc[2][0], acc[2][1]));
-            h1.y = relu_bf16x2(cvt_pk_bf16(acc[2][2], acc[2][3]));
-            h1.z = relu_bf16x2(cvt_pk_bf16(acc[3][0], acc[3][1]));
-            h1.w = relu_bf16x2(cvt_pk_bf16(acc[3][2], acc[3][3]));
-            lds_st128(smem, kHw0 + PAR * S::HBUF, h0);
-            lds_st128(smem, kHw1 + PAR * S::HBUF, h1);
-        }
-        NCA_FENCE();
-        // ---- G6: fc2 ends; z of tile i -> Z[PAR]
-        fc2_k(4);
-        fc2_k(5);
-        fc2_k(6);
-        fc2_k(7);
-        if (DST) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                uint2 o;
-                o.x = cvt_pk_bf16(zc[0][r], zc[1][r]);
-                o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
-                lds_st64(smem, kZw + PAR * S::ZBUF + (unsigned)r * S::ZS, o);
-            }
-        }
-        NCA_FENCE();
-        // ---- G7: fc1 of tile i-1, k-tile 0; the update of tile i-3
-        if (DFC) {
-#pragma unroll
-            for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
-            fc1_kt(0, zf[0]);
-        }
-        if (DUP) {
-            const uint32_t d01 = cvt_pk_bf16(acc2[0], acc2[1]), d23 = cvt_pk_bf16(acc2[2], acc2[3]);
-            const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
-            const float xo[4] = {m4.x, m4.y, m4.z, m4.w};
-            float u[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
-                const unsigned km = imv[v] & gvm;                     // clamped: keep x
-                u[v] = __uint_as_float((km & __float_as_uint(xo[v])) | (~km & __float_as_uint(uv)));
-            }
-            bool ok = true;
-            if (LAST) ok = 16 * (i - 3) + n < total;
-            if (ok) {
-                lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
-                lds_st64(smem, padr, make_uint2(cvt_pk_bf16(u[0], u[1]), cvt_pk_bf16(u[2], u[3])));
-            }
-        }
-        NCA_FENCE();
-        // ---- G8: k-tile 1; Z operands of k-tiles 4-7 for the next interval; next table entries
-        if (DFC) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) zq[k] = *zaddr(4 + k);
-            fc1_kt(1, zf[1]);
-        }
-        {  // the tables never change
-            int cs = cbS + 16, cu = cbU + 16;
-            if (cs >= RH) cs -= RH;
-            if (cu >= RH) cu -= RH;
-            cis_n = lds_ld64(smem, kCi + 8u * (unsigned)cs).x;
-            ciu_n = lds_ld64(smem, kCi + 8u * (unsigned)cu);
-        }
-        NCA_FENCE();
-        // ---- G9, G10: k-tiles 2-3
-        if (DFC) fc1_kt(2, zf[2]);
-        NCA_FENCE();
-        if (DFC) fc1_kt(3, zf[3]);
-        NCA_FENCE();
-    };
-    // next interval: its table entries (the tables never change)
-    auto advance = [&]() __attribute__((always_inline)) {
-        ++i;
-        cbS += 16;
-        if (cbS >= RH) cbS -= RH;
-        cbU += 16;
-        if (cbU >= RH) cbU -= RH;
-        rbU += 16;
-        if (rbU >= RING) rbU -= RING;
-        cis = cis_n;
-        ciu = ciu_n;
-    };
-    using F_ = std::integral_constant<bool, false>;
-    using T_ = std::integral_constant<bool, true>;
-    using P0 = std::integral_constant<unsigned, 0>;
-    using P1 = std::integral_constant<unsigned, 1>;
-    if (T > 0) {
-        // prologue (T >= 5: a step has at least 80 positions)
-        interval(T_{}, F_{}, F_{}, F_{}, P0{}, F_{});
+        auto advance = [&]() __attribute__((always_inline)) {
+            ++i;
+            cbS += 16;
+            if (cbS >= RH) cbS -= RH;
+            cbU += 16;
+            if (cbU >= RH) cbU -= RH;
+            rbU += 16;
+            if (rbU >= RING) rbU -= RING;
+            cis = cis_n;
+            ciu = ciu_n;
+        };
+        cinterval(T_{}, F_{}, P0{}, F_{});
         events();
         advance();
         __syncthreads();
-        interval(T_{}, T_{}, F_{}, F_{}, P1{}, F_{});
+        cinterval(T_{}, F_{}, P1{}, F_{});
         events();
         advance();
         __syncthreads();
-        interval(T_{}, T_{}, T_{}, F_{}, P0{}, F_{});
+        cinterval(T_{}, F_{}, P0{}, F_{});
         events();
         advance();
         __syncthreads();
-        // steady state: i odd, then even
         while (i + 1 < T) {
-            interval(T_{}, T_{}, T_{}, T_{}, P1{}, F_{});
+            cinterval(T_{}, T_{}, P1{}, F_{});
             events();
             advance();
             __syncthreads();
-            interval(T_{}, T_{}, T_{}, T_{}, P0{}, F_{});
+            cinterval(T_{}, T_{}, P0{}, F_{});
             events();
             advance();
             __syncthreads();
         }
         if (i < T) {
-            interval(T_{}, T_{}, T_{}, T_{}, P1{}, F_{});
+            cinterval(T_{}, T_{}, P1{}, F_{});
             events();
             advance();
             __syncthreads();
         }
-        // drain: i == T
-        interval(F_{}, T_{}, T_{}, T_{}, (unsigned)(i & 1), F_{});
+        cinterval(F_{}, T_{}, (unsigned)(i & 1), F_{});
         events();
         advance();
         __syncthreads();
-        interval(F_{}, F_{}, T_{}, T_{}, (unsigned)(i & 1), F_{});
+        cinterval(F_{}, T_{}, (unsigned)(i & 1), F_{});
         events();
         advance();
         __syncthreads();
-        interval(F_{}, F_{}, F_{}, T_{}, (unsigned)(i & 1), T_{});
+        cinterval(F_{}, T_{}, (unsigned)(i & 1), T_{});
         __syncthreads();
     }
 
     // ---- write back
-    for (int e = tid; e < Rw * S::C * HWn; e += 256) {
+    for (int e = tid; e < Rw * S::C * HWn; e += NT) {
         const int r = e / (S::C * HWn), rem = e - r * S::C * HWn, ch = rem / HWn, q = rem - ch * HWn;
         a.x_out[rbase * S::C * HWn + e] = m_at(r, q, ch);
     }
     if (a.conf_out) {
         float *confL = reinterpret_cast<float *>(smem + sp.l_Z);  // Z is free now
-        for (int cell = tid; cell < Rw * HWn; cell += 256) {
+        for (int cell = tid; cell < Rw * HWn; cell += NT) {
             const int r = cell / HWn, q = cell - r * HWn;
             int am;
             confL[cell] = cell_readout_fn([&](int v) { return m_at(r, q, a.out_off + v); }, a.c_out, a.n_out,
                                           a.head_kind, headL, headL + a.n_out * a.c_out, &am);
         }
         __syncthreads();
-        for (int r = tid; r < Rw; r += 256) {
+        for (int r = tid; r < Rw; r += NT) {
             float sum = 0.0f;
             for (int q = 0; q < HWn; ++q) sum = __fadd_rn(sum, confL[r * HWn + q]);
             a.conf_out[rbase + r] = __fdiv_rn(sum, (float)HWn);
         }
     }
     if (a.fired_out)
-        for (int r = tid; r < Rw; r += 256) a.fired_out[rbase + r] = firedL[r];
+        for (int r = tid; r < Rw; r += NT) a.fired_out[rbase + r] = firedL[r];
 }
 
 }  // namespace nca

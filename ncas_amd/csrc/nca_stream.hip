@@ -43,6 +43,7 @@ hipError_t launch_stream64(const RolloutParams &p, hipStream_t st, unsigned lds_
     sp.l_fired = L.fired;
     sp.l_head = L.head;
     sp.l_hcp = L.hcp;
+    sp.l_evp = L.evp;
     sp.off_w1q = p.off_w1q;
     sp.off_w2h = p.off_w2h;
     auto kfn = rollout_stream64;
@@ -51,7 +52,7 @@ hipError_t launch_stream64(const RolloutParams &p, hipStream_t st, unsigned lds_
     if (e != hipSuccess) return e;
     const int64_t grid = (p.rows + R - 1) / R;
     if (grid <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kfn, dim3((unsigned)grid), dim3(256), L.total, st, sp);
+    hipLaunchKernelGGL(kfn, dim3((unsigned)grid), dim3(512), L.total, st, sp);
     *used = true;
     return hipGetLastError();
 }
