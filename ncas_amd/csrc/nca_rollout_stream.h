@@ -555,10 +555,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
             }
         };
         // st: stencil of tile i -> Z[i & 1]; up: fc2 + update of tile i-3 (H[(i-3) & 1]). The
-        // issue order is fixed by scheduling fences: all loads first, then the stencil's permutes
-        // with the fc2 chain, the stencil's MFMAs, the update, the stores.
+        // issue order is fixed by scheduling fences: all loads first (the H operands before the
+        // taps), then the stencil's permutes with the fc2 chain, the stencil's MFMAs, the update,
+        // the stores.
 #ifndef NCA_CH_ORDER
-#define NCA_CH_ORDER 1
+#define NCA_CH_ORDER 2
 #endif
 #ifndef NCA_FENCE
 #define NCA_FENCE() __builtin_amdgcn_sched_barrier(0)
@@ -571,17 +572,21 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
             float4 m4;
             float fu = 0.0f;
             unsigned madr = 0, padr = 0, gvm = 0;
+            // the taps are single ds_read_b64: paired into ds_read2_b64 (neighbouring cells of one
+            // row) they hit bank conflicts and cost more than two single loads on gfx950
             auto load_taps = [&]() __attribute__((always_inline)) {
                 if (DST) {
                     const unsigned r0 = cis + kPs, r1 = cis + kPs1, r2 = cis + kPs2;
                     nbv[0] = lds_ld64(smem, r0);
-                    nbv[1] = lds_ld64(smem, r0 + S::CS);
-                    nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
                     nbv[3] = lds_ld64(smem, r1);
-                    nbv[4] = lds_ld64(smem, r1 + S::CS);
-                    nbv[5] = lds_ld64(smem, r1 + 2 * S::CS);
                     nbv[6] = lds_ld64(smem, r2);
+                    __builtin_amdgcn_sched_barrier(0);
+                    nbv[1] = lds_ld64(smem, r0 + S::CS);
+                    nbv[4] = lds_ld64(smem, r1 + S::CS);
                     nbv[7] = lds_ld64(smem, r2 + S::CS);
+                    __builtin_amdgcn_sched_barrier(0);
+                    nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
+                    nbv[5] = lds_ld64(smem, r1 + 2 * S::CS);
                     nbv[8] = lds_ld64(smem, r2 + 2 * S::CS);
                 }
             };
