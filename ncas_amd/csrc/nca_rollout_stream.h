@@ -383,36 +383,37 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
         const unsigned hx = (unsigned)((n >> 2) & 1);
         const unsigned kHw0 = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)ws + 32u * (unsigned)g + 16u * hx;
         const unsigned kHw1 = kHw0 + 16u - 32u * hx;
-        bf16x8 zq[S::KT1];  // Z operands of a tile, loaded one interval before its fc1 runs
+        // Z operands of a tile, loaded in the interval before its fc1 runs; requested at the end
+        // of the interval (once the MFMAs that read the previous ones are issued), when the other
+        // waves' loads of the interval are done
+        bf16x8 zq[S::KT1];
 #pragma unroll
         for (int k = 0; k < S::KT1; ++k)
 #pragma unroll
             for (int e = 0; e < 8; ++e) zq[k][e] = (__bf16)0.0f;
-        // fcb: fc1 of tile i-2 (all 32 MFMAs from registers) and its epilogue -> H[i & 1];
-        // fca: the Z operands of tile i-1, requested once those MFMAs have read the registers
-        auto hinterval = [&](auto fca_c, auto fcb_c, auto par_v) __attribute__((always_inline)) {
+        // fcb: fc1 of tile i-2 from zq (all 32 MFMAs from registers, m-tile by m-tile) and its
+        // epilogue -> H[i & 1], each half stored as soon as its two m-tiles are done; fca: the Z
+        // operands of tile i-1
+        auto hinterval = [&](auto fca_c, auto fcb_c, auto par_c) __attribute__((always_inline)) {
             constexpr bool FCA = decltype(fca_c)::value, FCB = decltype(fcb_c)::value;
-            const unsigned PAR = par_v;
+            constexpr unsigned PAR = decltype(par_c)::value;
             if (FCB) {
                 f32x4 acc[S::MT1];
 #pragma unroll
-                for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+                for (int mt = 0; mt < S::MT1; ++mt) {
+                    acc[mt] = b1v[mt];
 #pragma unroll
-                for (int kt = 0; kt < S::KT1; ++kt)
-#pragma unroll
-                    for (int mt = 0; mt < S::MT1; ++mt)
+                    for (int kt = 0; kt < S::KT1; ++kt)
                         acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zq[kt], acc[mt], 0, 0, 0);
-                uint4 h0, h1;
-                h0.x = relu_bf16x2(cvt_pk_bf16(acc[0][0], acc[0][1]));
-                h0.y = relu_bf16x2(cvt_pk_bf16(acc[0][2], acc[0][3]));
-                h0.z = relu_bf16x2(cvt_pk_bf16(acc[1][0], acc[1][1]));
-                h0.w = relu_bf16x2(cvt_pk_bf16(acc[1][2], acc[1][3]));
-                h1.x = relu_bf16x2(cvt_pk_bf16(acc[2][0], acc[2][1]));
-                h1.y = relu_bf16x2(cvt_pk_bf16(acc[2][2], acc[2][3]));
-                h1.z = relu_bf16x2(cvt_pk_bf16(acc[3][0], acc[3][1]));
-                h1.w = relu_bf16x2(cvt_pk_bf16(acc[3][2], acc[3][3]));
-                lds_st128(smem, kHw0 + PAR * S::HBUF, h0);
-                lds_st128(smem, kHw1 + PAR * S::HBUF, h1);
+                    if (mt & 1) {
+                        uint4 hv;
+                        hv.x = relu_bf16x2(cvt_pk_bf16(acc[mt - 1][0], acc[mt - 1][1]));
+                        hv.y = relu_bf16x2(cvt_pk_bf16(acc[mt - 1][2], acc[mt - 1][3]));
+                        hv.z = relu_bf16x2(cvt_pk_bf16(acc[mt][0], acc[mt][1]));
+                        hv.w = relu_bf16x2(cvt_pk_bf16(acc[mt][2], acc[mt][3]));
+                        lds_st128(smem, (mt == 1 ? kHw0 : kHw1) + PAR * S::HBUF, hv);
+                    }
+                }
             }
             if (FCA) {
 #pragma unroll
@@ -439,11 +440,18 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
             __syncthreads();
             ++i;
         }
-        hinterval(T_{}, T_{}, (unsigned)(i & 1));
-        __syncthreads();
-        hinterval(F_{}, T_{}, (unsigned)((i + 1) & 1));
-        __syncthreads();
-        hinterval(F_{}, F_{}, (unsigned)(i & 1));
+        // drain: intervals T, T+1 (T+2 has no hidden work) with compile-time parities
+        if (i & 1) {
+            hinterval(T_{}, T_{}, P1{});
+            __syncthreads();
+            hinterval(F_{}, T_{}, P0{});
+            __syncthreads();
+        } else {
+            hinterval(T_{}, T_{}, P0{});
+            __syncthreads();
+            hinterval(F_{}, T_{}, P1{});
+            __syncthreads();
+        }
         __syncthreads();
     } else if (T > 0) {
         // ================= channel waves: stencil, fc2 + update, end-of-step work
