@@ -23,10 +23,11 @@
 //                          input channels of given cells keep their value. Channel waves also do
 //                          the end-of-step work (wrap halo refresh, fire masks).
 //
-// Interval i (one workgroup barrier) runs: stencil of tile i (-> Z[i & 1]); fc1 k-tiles 0-3 of tile
-// i-1 (from Z[(i-1) & 1]; its k-tiles 4-7 operands are loaded then and kept in registers) and fc1
-// k-tiles 4-7 + epilogue of tile i-2 (-> H[i & 1]), so a hidden wave opens each interval with 16
-// MFMAs whose operands are in registers; fc2 + update of tile i-3 (from H[(i-3) & 1]).
+// Interval i (one workgroup barrier) runs: stencil of tile i (-> Z[i & 1]); fc1 + epilogue of
+// tile i-2 (-> H[i & 1]) from Z operands the hidden wave loaded into registers at the end of
+// interval i-1, after which it loads those of tile i-1 from Z[(i-1) & 1]; fc2 + update of tile
+// i-3 (from H[(i-1) & 1]). A hidden wave thus opens every interval with 32 MFMAs whose operands
+// are already in registers.
 //
 // P is single-buffered: the update of tile i-3 runs in the same interval as the stencil of tile
 // i, whose neighbourhoods reach W+1 <= 16 positions back, never into tile i-3. A board's next
