@@ -122,8 +122,10 @@ int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int
                 float *conf_out, int32_t *fired_out, void *stream);
 
 /* Bytes of workspace that nca_rollout_ws needs for this call shape: 0 when the rows fit the
- * LDS-resident kernels (the whole rollout runs in one launch), else two state buffers
- * (2 * rows * C * H * W * 4 bytes) for the halo-tiled per-step path. */
+ * LDS-resident kernels (the whole rollout runs in one launch; bf16 cells with C=32, hidden 256
+ * on boards up to 31 wide, such as 30x30, run one board per workgroup), else two state buffers
+ * (2 * rows * C * H * W * 4 bytes) for the halo-tiled per-step path. An in-place single step
+ * with noise always takes the tiled path and then needs one state buffer. */
 size_t nca_rollout_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height,
                                    int32_t width);
 

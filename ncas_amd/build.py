@@ -28,6 +28,7 @@ SOURCES = {
     # the streamed kernel keeps MFMA results and accumulators in VGPRs (its weight fragments are
     # pinned to AGPRs), so the VALU work on them needs no v_accvgpr copies
     "nca_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "nca_stream32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_tiled.hip": [],
     "nca_bptt.hip": [],
 }

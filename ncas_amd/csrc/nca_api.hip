@@ -136,6 +136,21 @@ __global__ void pack_w2h(const float *w2, int C, int HD, __bf16 *dst) {
     }
 }
 
+// fc2 fragments per hidden quarter (see nca_layout.h), bf16: the k axis of quarter q follows the
+// order of fc1's accumulators in the wave that owns it, slot s of lane group g of k-tile k ->
+// hidden q HD/4 + 16 (2 k + s / 4) + 4 g + s % 4.
+__global__ void pack_w2k(const float *w2, int C, int HD, __bf16 *dst) {
+    const int hpw = HD / 4, kt2n = hpw / 32, mt2n = C / 16;
+    const int total = C * HD;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
+        const int kt = blk % kt2n, m2 = (blk / kt2n) % mt2n, q = blk / (kt2n * mt2n);
+        const int ch = 16 * m2 + (lane & 15);
+        const int hid = q * hpw + 16 * (2 * kt + s / 4) + 4 * (lane >> 4) + (s % 4);
+        dst[e] = (__bf16)w2[(size_t)ch * HD + hid];
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // Fire mask of one step
 __global__ void fire_mask_kernel(int64_t rows, int hw, uint64_t seed, int64_t row0, uint32_t step,
@@ -378,9 +393,25 @@ int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t s
     return NCA_OK;
 }
 
+// bf16 cells with C = 32, hidden 256 on boards up to 31 wide (30x30 hard mazes, also the small
+// boards the generic resident kernel takes) run on the streamed C = 32 kernel: one launch for
+// the rollout, no workspace. A cell whose output slice spans two channel quads or whose head has
+// more than 4 outputs does not (gated firing reads the slice from one quad, the head from registers).
+bool takes_stream32(const nca_cell_desc *d, int64_t rows, int H, int W) {
+    (void)rows;
+    if (g_path != 0 || d->precision != NCA_BF16 || d->channels != 32 || d->hidden != 256) return false;
+    if ((d->out_offset & 3) != 0 || d->c_out > 4 || d->n_out > 4) return false;
+    return nca::stream32_fits(H, W, d->padding, d->c_out, d->n_out, kLdsBytes);
+}
+
 template <int C, int HD>
 int launch_cell(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st, void *ws, size_t ws_bytes) {
     const bool bf = d->precision == NCA_BF16;
+    if (C == 32 && HD == 256 && takes_stream32(d, p.rows, p.H, p.W)) {
+        bool used = false;
+        const int rc = hip_check(nca::launch_stream32(p, st, kLdsBytes, &used), "streamed rollout launch");
+        if (rc || used) return rc;
+    }
     if (!takes_resident(d, p.rows, p.H, p.W)) return run_tiled(d, p, st, ws, ws_bytes);
     if (bf && C == 64 && HD == 256 && g_path == 0) {
         bool used = false;
@@ -426,6 +457,7 @@ nca::RolloutParams base_params(const nca_cell_desc *d, const void *packed, int64
     p.off_w2 = (unsigned)L.w2;
     p.off_w2h = (unsigned)L.w2h;
     p.off_w1q = (unsigned)L.w1q;
+    p.off_w2k = (unsigned)L.w2k;
     return p;
 }
 
@@ -451,7 +483,7 @@ int nca_set_kernel_path(int path) {
 
 size_t nca_rollout_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width) {
     if (check_cell(cell) || check_grid(rows, height, width)) return 0;
-    if (takes_resident(cell, rows, height, width)) return 0;
+    if (takes_resident(cell, rows, height, width) || takes_stream32(cell, rows, height, width)) return 0;
     return 2 * state_bytes(cell, rows, height, width);
 }
 
@@ -487,6 +519,7 @@ int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void 
     if (bf) {
         hipLaunchKernelGGL(pack_w2h, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2h));
         hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, 1, C, (void *)(pk + L.w1q));
+        hipLaunchKernelGGL(pack_w2k, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2k));
     }
     return hip_check(hipGetLastError(), "pack launch");
 }

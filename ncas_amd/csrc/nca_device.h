@@ -126,6 +126,49 @@ __device__ __forceinline__ float cell_readout_fn(X xo, int c_out, int n_out, int
     return best;
 }
 
+// The same for a head of at most 4 outputs over at most 4 channels, its parameters in registers
+// (hw4[v][c], hb4[v]): the operations and their order are cell_readout_fn's.
+__device__ __forceinline__ float cell_readout4(const float xo[4], int c_out, int n_out, int head_kind,
+                                               const float hw4[4][4], const float hb4[4]) {
+    float best = 0.0f;
+    if (head_kind == 0) {
+        float lg[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            float acc = hb4[v];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (c < c_out) acc = __builtin_fmaf(hw4[v][c], xo[c], acc);
+            lg[v] = acc;
+            if (v < n_out && (v == 0 || acc > best)) best = acc;
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+            if (v < n_out) s = s + readout_expf(lg[v] - best);
+        float conf = __fdiv_rn(1.0f, s);
+        if (conf > 1.0f) conf = 1.0f;
+        if (conf < 0.0f) conf = 0.0f;
+        return conf;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        if (v >= n_out) continue;
+        float d2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (c >= c_out) continue;
+            const float d = xo[c] - hw4[v][c];
+            d2 = __builtin_fmaf(d, d, d2);
+        }
+        const float sc = __fdiv_rn(1.0f, 1.0f + __fsqrt_rn(d2 + 1e-8f));
+        if (v == 0 || sc > best) best = sc;
+    }
+    if (best > 1.0f) best = 1.0f;
+    if (best < 0.0f) best = 0.0f;
+    return best;
+}
+
 // The same with the output slice at xo[c * cstride].
 __device__ __forceinline__ float cell_readout(const float *xo, int cstride, int c_out, int n_out,
                                               int head_kind, const float *hw, const float *hb,

@@ -16,6 +16,10 @@
 //          A[i][slot] = W2[16 m + i][hl(32 k + 8 (lane / 16) + slot)]
 //   w1q    (bf16 only) fc1 fragments like w1 with the feature (k) axis in quad-major order:
 //          k = 16 iq + 4 head + ch holds feature head * C + 4 iq + ch
+//   w2k    (bf16 only) fc2 fragments per quarter q of the hidden units, for kernels whose waves
+//          each own a quarter and keep fc1's accumulators as the B operand:
+//          [q][m-tile][k-tile][lane][slot], A[i][slot] = W2[16 m + i][q hidden/4 +
+//          16 (2 k + slot / 4) + 4 (lane / 16) + slot % 4]
 // bf16 cells use v_mfma_f32_16x16x32_bf16 fragments (k-tile 32, 8 bf16 slots per lane:
 // A[i = lane % 16][k = 8 * (lane / 16) + slot]); fp32 cells use v_mfma_f32_16x16x4_f32
 // fragments (k-tile 4, one float per lane: A[i = lane % 16][k = lane / 16]).
@@ -26,7 +30,7 @@
 namespace nca {
 
 struct PackedLayout {
-    size_t kern, b1, b2, headw, headb, padv, w1, w2, w2h, w1q, total;
+    size_t kern, b1, b2, headw, headb, padv, w1, w2, w2h, w1q, w2k, total;
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -56,6 +60,8 @@ __host__ __device__ inline PackedLayout packed_layout(int C, int heads, int hidd
     o = align256(o + (bf16 ? 2 * (size_t)C * hidden : 0));
     L.w1q = o;  // bf16 cells: fc1 fragments in quad-major feature order
     o = align256(o + (bf16 ? 2 * (size_t)hidden * heads * C : 0));
+    L.w2k = o;  // bf16 cells: fc2 fragments per hidden quarter
+    o = align256(o + (bf16 ? 2 * (size_t)C * hidden : 0));
     L.total = o;
     return L;
 }

@@ -60,7 +60,7 @@ struct RolloutParams {
     float p, p_low, tau;
     int adaptive, given_confident;
     int rows_per_wg;
-    unsigned off_kern, off_b1, off_b2, off_headw, off_headb, off_padv, off_w1, off_w2, off_w2h, off_w1q;
+    unsigned off_kern, off_b1, off_b2, off_headw, off_headb, off_padv, off_w1, off_w2, off_w2h, off_w1q, off_w2k;
     unsigned l_P, l_M, l_Z, l_H, l_clamp, l_given, l_fire, l_conf, l_fired, l_head, l_cinfo;
 };
 

@@ -1,0 +1,705 @@
+// Streamed LDS-resident rollout kernel for bf16 cells with C = 32 channels and 256 hidden units
+// (gfx950): the rollout of boards up to 31 cells wide whose fp32 state fits the LDS (30x30: one
+// board per workgroup, 127 KB of state), D steps in one launch.
+//
+// One workgroup owns one row (board) for the whole call. Its cells, step after step, form one
+// stream: position p = s HW + q is cell q at step s. The stream is cut into 16-cell tiles (a tile
+// may span two steps, so no cell is padding).
+//
+// The state lives only in fp32, in M: the stencil reads its taps as fp32 and rounds them to bf16
+// in registers (the rounding autocast applies before the convolution), which also puts them in
+// the MFMA operand order. M holds the board inside a one-cell border of constant cells (the wall
+// value or zero), rows W+1 cells apart, so the right border cell of a row is the left border cell
+// of the next: cell (i, j) is M cell (i+1)(W+1) + j + 1, 128 bytes each.
+//
+// The workgroup has 8 waves, two per SIMD:
+//   hidden wave w (0-3)    hidden units [64w, 64w+64), W1 fragments in AGPRs: fc1 of a tile (16
+//                          v_mfma_f32_16x16x32_bf16 from Z operands loaded in the previous
+//                          interval), bf16 rounding + ReLU in registers, then fc2 over its 64
+//                          hidden units for all 32 channels (4 MFMAs whose B operand is the
+//                          epilogue's registers) -> fp32 partial sums in D.
+//   stencil wave (4, 5)    cells 8(w-4) .. 8(w-4)+7 of a tile, all 8 channel quads: lane (cell,
+//                          quad) loads the 9 taps of its 4 channels (a 16-lane group reads two
+//                          whole cells, free of bank conflicts) and runs the 3x3 perception on
+//                          v_mfma_f32_4x4x4_16b_bf16 -> Z.
+//   update wave (6, 7)     cells 8(w-6) .. 8(w-6)+7 of a tile, all quads: dx = bf16(b2 + the four
+//                          partial sums in a fixed order), x += fire dx into M; the clamped input
+//                          channels of given cells keep their value. With confidence-gated
+//                          firing the lanes of the output quad compute the cell's confidence
+//                          from its new state and fix the cell's fire decision for the next step.
+// Interval i (one workgroup barrier): stencil of tile i -> Z[i & 1]; fc1 + fc2 partials of tile
+// i-2 -> D[i & 1], then the Z operands of tile i-1 from Z[(i-1) & 1]; update of tile i-3 from
+// D[(i-1) & 1].
+//
+// M is updated in place. The stencil of tile i reads positions 16i - (W+1) .. 16i + 15 + (W+1)
+// of its step and the update of tile i-3 in the same interval writes positions 16i - 48 ..
+// 16i - 33: disjoint for W <= 31. A cell's stencil of step s+1 comes HW - (W+1) positions after
+// the stencils of its neighbours at step s, which is at least 4 intervals after their updates
+// for HW >= W + 66.
+//
+// Fire masks: a four-step byte ring in stream order (4 HW bytes and a 16-byte mirror of its
+// start, so that a tile's 16 bytes are contiguous): bit 0 fire, bit 1 (u < p_low) for gated
+// firing, bit 7 the cell's given flag. The channel waves draw the Philox uniforms of a whole step
+// two steps ahead (one evaluation per 4 cells); with gating the update writes bit 0 of the next
+// step's byte once the cell's new state, and so its confidence, is known.
+//
+// Clamp (model.py:430-438): the first step's perception reads the caller's state and every step's
+// output holds the clamp values in the input slice of given cells. M starts as the caller's state;
+// the update keeps those channels of given cells at their M value, which after the first step is
+// the clamp value. When the caller's state already holds the clamp values there (the usual case),
+// the first step needs nothing else; otherwise its updates take the values from the clamp tensor.
+//
+// LDS layouts (conflict-free for the access patterns here on gfx950's 64 banks):
+//   * M: 128 B per cell; 16-lane groups read or write two cells x 8 quads;
+//   * Z: 256 B per tile row (features in quad-major order 16 quad + 4 kernel + ch), 16-byte chunk c
+//     of row r stored at chunk c ^ zsw(r), zsw(r) = (r & 8) | (r & 3) << 1 | (r >> 2 & 1);
+//   * D: per partial 16 rows of 128 B (32 fp32), chunk c of row r stored at c ^ (r >> 1 & 7).
+#pragma once
+
+#include "nca_stream_util.h"
+
+namespace nca {
+
+struct St32 {
+    static constexpr int C = 32, HD = 256, F = 128;
+    static constexpr int MT1 = 4, KT1 = 4;  // fc1 per hidden wave: 64 hidden x 128 features
+    static constexpr int MT2 = 2, KT2 = 2;  // fc2 per hidden wave: 32 channels x its 64 hidden
+    static constexpr int MS = 128;          // M bytes per cell
+    static constexpr int ZS = 256;          // Z bytes per tile row
+    static constexpr int ZBUF = 16 * ZS;
+    static constexpr int DS = 128;          // D bytes per row of one partial
+    static constexpr int DPART = 16 * DS;
+    static constexpr int DBUF = 4 * DPART;
+    static constexpr int NSLOT = 4;  // fire ring steps
+};
+
+struct St32Plan {
+    unsigned M, Z, D, cinfo, ring, given, head, evp, flags, total;
+    int NM, RING;
+};
+
+inline St32Plan st32_plan(int H, int W, int c_out, int n_out) {
+    using S = St32;
+    St32Plan p;
+    const int HWn = H * W;
+    p.NM = (H + 1) * (W + 1) + W + 2;
+    p.RING = S::NSLOT * HWn;
+    unsigned o = 0;
+    p.M = o;
+    o = st_al16(o + (unsigned)p.NM * S::MS);
+    p.Z = o;
+    o += 2u * S::ZBUF;
+    p.D = o;
+    o += 2u * S::DBUF;
+    p.cinfo = o;  // u16 M cell index of board cell q, q < HW + 16 (the last 16 repeat the first)
+    o = st_al16(o + (unsigned)(HWn + 16) * 2u);
+    p.ring = o;
+    o = st_al16(o + (unsigned)p.RING + 16u);
+    p.given = o;
+    o = st_al16(o + (unsigned)((HWn + 31) / 32) * 4u);
+    p.head = o;
+    o = st_al16(o + (unsigned)(n_out * c_out + n_out) * 4u);
+    p.evp = o;  // a copy of the call's parameters for the per-step draws
+    o = st_al16(o + (unsigned)sizeof(RolloutParams));
+    p.flags = o;  // [0] fired count, [1] first-step clamp needed
+    o = st_al16(o + 8u);
+    p.total = o;
+    return p;
+}
+
+struct St32Params {
+    RolloutParams a;
+    int NM, RING, T;
+    // gated firing with an mlp head of 2 outputs: conf = 1/s > tau exactly when s < conf_s (s the
+    // sum of exponentials, conf_s computed on the host with IEEE division); fast_conf selects it
+    float conf_s;
+    int fast_conf;
+    unsigned l_M, l_Z, l_D, l_cinfo, l_ring, l_given, l_head, l_evp, l_flags;
+    unsigned off_w1q, off_w2k;
+};
+
+#ifndef NCA32_CH_PRIO
+#define NCA32_CH_PRIO 3  // issue priority of the stencil and update waves
+#endif
+#ifndef NCA32_ZQ_EARLY
+#define NCA32_ZQ_EARLY 0  // hidden waves load the next Z operands at the start of the interval
+#endif
+
+// zsw: the Z row swizzle (a permutation of 0..15)
+__device__ __forceinline__ unsigned zsw(unsigned r) { return (r & 8u) | ((r & 3u) << 1) | ((r >> 2) & 1u); }
+
+__global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
+    using S = St32;
+    constexpr int NT = 512;
+    const RolloutParams &a = sp.a;
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int H = a.H, W = a.W, HWn = H * W, RING = sp.RING;
+    const int64_t row = blockIdx.x;
+    const int tb = tid - 256;  // thread index among the channel waves
+
+    float *headL = reinterpret_cast<float *>(smem + sp.l_head);
+    int *flagsL = reinterpret_cast<int *>(smem + sp.l_flags);
+    unsigned short *cinfo = reinterpret_cast<unsigned short *>(smem + sp.l_cinfo);
+    unsigned *givenL = reinterpret_cast<unsigned *>(smem + sp.l_given);
+    unsigned char *ring = smem + sp.l_ring;
+
+    auto m_index = [&](int q) -> int {
+        const int i = q / W, j = q - i * W;
+        return (i + 1) * (W + 1) + j + 1;
+    };
+    auto m_at = [&](int q, int ch) -> float & {
+        return *reinterpret_cast<float *>(smem + sp.l_M + (unsigned)m_index(q) * S::MS + 4u * (unsigned)ch);
+    };
+
+    // ---- set-up: border cells, the caller's state, tables
+    {
+        const float *padv = reinterpret_cast<const float *>(a.packed + a.off_padv);
+        float *M = reinterpret_cast<float *>(smem + sp.l_M);
+        for (int e = tid; e < sp.NM * S::C; e += NT) M[e] = a.padding == 1 ? padv[e & (S::C - 1)] : 0.0f;
+    }
+    if (tid == 0) {
+        flagsL[0] = 0;
+        flagsL[1] = 0;
+    }
+    for (int e = tid; e < (HWn + 31) / 32; e += NT) givenL[e] = 0u;
+    __syncthreads();
+    {
+        const float *xr = a.x_in + row * S::C * HWn;
+        int need = 0;
+        for (int e = tid; e < S::C * HWn; e += NT) {
+            const int ch = e / HWn, q = e - ch * HWn;
+            const float v = xr[e];
+            m_at(q, ch) = v;
+            const int ci = ch - a.in_off;
+            if (ci >= 0 && ci < a.c_in && a.given[row * HWn + q] &&
+                __float_as_uint(v) != __float_as_uint(a.clamp[(row * a.c_in + ci) * HWn + q]))
+                need = 1;
+        }
+        if (need) flagsL[1] = 1;
+    }
+    for (int c = tid; c < HWn + 16; c += NT) cinfo[c] = (unsigned short)m_index(c < HWn ? c : c - HWn);
+    for (int q = tid; q < HWn; q += NT)
+        if (a.given[row * HWn + q]) atomicOr(&givenL[q >> 5], 1u << (q & 31));
+    for (int e = tid; e < (int)(sizeof(RolloutParams) / 4); e += NT)
+        reinterpret_cast<unsigned *>(smem + sp.l_evp)[e] = reinterpret_cast<const unsigned *>(&a)[e];
+    {
+        const float *hw = reinterpret_cast<const float *>(a.packed + a.off_headw);
+        const float *hb = reinterpret_cast<const float *>(a.packed + a.off_headb);
+        const int nw = a.n_out * a.c_out;
+        for (int e = tid; e < nw + a.n_out; e += NT) headL[e] = e < nw ? hw[e] : hb[e - nw];
+    }
+    __syncthreads();
+
+    // ---- fire masks of step s for all cells (channel waves, thread tb of 256). decide: the final
+    // decision of a gated step from the current M (the state before step s); otherwise gated
+    // steps get both threshold bits and their updates decide later.
+    auto ring_put = [&](int s, int q, unsigned v) __attribute__((always_inline)) {
+        const int o = (s % S::NSLOT) * HWn + q;
+        ring[o] = (unsigned char)v;
+        if (o < 16) ring[RING + o] = (unsigned char)v;
+    };
+    const int nq4 = (HWn + 3) >> 2;
+    auto draw = [&](const RolloutParams &pa, int s, bool decide) __attribute__((always_inline)) {
+        for (int it = tb; it < nq4; it += 256) {
+            float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+            if (!pa.fire_u8) {
+                const uint64_t key = pa.step_seeds ? pa.step_seeds[s] : pa.seed;
+                cell_uniforms4(key, (uint32_t)(pa.row0 + row), (uint32_t)(pa.step0 + s), (uint32_t)it, u);
+            }
+            int cnt = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int q = 4 * it + e;
+                if (q >= HWn) continue;
+                const unsigned gv = (givenL[q >> 5] >> (q & 31)) & 1u;
+                unsigned b;
+                if (pa.fire_u8) {
+                    b = pa.fire_u8[((int64_t)s * pa.rows + row) * HWn + q] != 0;
+                } else {
+                    const unsigned b0 = u[e] < pa.p, b1 = u[e] < pa.p_low;
+                    if (pa.adaptive && decide) {
+                        int am;
+                        const float cf = cell_readout_fn([&](int v) { return m_at(q, pa.out_off + v); }, pa.c_out,
+                                                         pa.n_out, pa.head_kind, headL, headL + pa.n_out * pa.c_out,
+                                                         &am);
+                        b = (cf > pa.tau || (pa.given_confident && gv)) ? b1 : b0;
+                    } else {
+                        b = pa.adaptive ? (b0 | (b1 << 1)) : b0;
+                    }
+                }
+                ring_put(s, q, b | (gv << 7));
+                if (!pa.adaptive || decide) cnt += (int)(b & 1u);
+            }
+            if (cnt) atomicAdd(&flagsL[0], cnt);
+        }
+    };
+    if (wave >= 4 && a.n_steps > 0) {
+        draw(a, 0, true);
+        if (a.n_steps > 1) draw(a, 1, false);
+    }
+    __syncthreads();
+
+    using F_ = std::integral_constant<bool, false>;
+    using T_ = std::integral_constant<bool, true>;
+    using P0 = std::integral_constant<unsigned, 0>;
+    using P1 = std::integral_constant<unsigned, 1>;
+    const int T = sp.T;
+    const int total = a.n_steps * HWn;
+    const int g = lane >> 4, n = lane & 15;
+    const int ws = wave & 3;
+
+    if (T > 0 && wave < 4) {
+        // ================= hidden waves: fc1, epilogue, fc2 partial sums
+        bf16x8 w1f[S::MT1][S::KT1];
+        bf16x8 w2f[S::MT2][S::KT2];
+        f32x4 b1v[S::MT1];
+        {
+            const bf16x8 *w1 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w1q);
+            const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2k);
+            const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt) {
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt) w1f[mt][kt] = w1[((ws * S::MT1 + mt) * S::KT1 + kt) * 64 + lane];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) b1v[mt][v] = b1[ws * 64 + 16 * mt + 4 * g + v];
+            }
+#pragma unroll
+            for (int m2 = 0; m2 < S::MT2; ++m2)
+#pragma unroll
+                for (int kt = 0; kt < S::KT2; ++kt) w2f[m2][kt] = w2[((ws * S::MT2 + m2) * S::KT2 + kt) * 64 + lane];
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt)
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt) asm volatile("" : "+a"(w1f[mt][kt]));
+#pragma unroll
+            for (int m2 = 0; m2 < S::MT2; ++m2)
+#pragma unroll
+                for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[m2][kt]));
+        }
+        // B operand of k-tile kt: features 32 kt + 8 g .. +7 of cell n = chunk 4 kt + g of Z row n
+        unsigned kZ[S::KT1];
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt)
+            kZ[kt] = sp.l_Z + (unsigned)n * S::ZS + 16u * ((unsigned)(4 * kt + g) ^ zsw((unsigned)n));
+        // partial sums of channels 16 m2 + 4 g .. +3 of cell n: chunk 4 m2 + g of this wave's D row n
+        unsigned kD[S::MT2];
+#pragma unroll
+        for (int m2 = 0; m2 < S::MT2; ++m2)
+            kD[m2] = sp.l_D + (unsigned)ws * S::DPART + (unsigned)n * S::DS +
+                     16u * ((unsigned)(4 * m2 + g) ^ ((unsigned)(n >> 1) & 7u));
+        // Z operands: tile i-1's are loaded in interval i into zqb[i & 1], fc1 of tile i-2 reads
+        // zqb[(i-1) & 1]
+        bf16x8 zqb[2][S::KT1];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int k = 0; k < S::KT1; ++k)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) zqb[b][k][e] = (__bf16)0.0f;
+        // fcb: fc1 of tile i-2, its epilogue in registers, fc2 over the wave's 64 hidden units
+        // with those registers as B operand (the W2 fragments are packed in that k order) ->
+        // D[i & 1]; fca: the Z operands of tile i-1
+        auto hinterval = [&](auto fca_c, auto fcb_c, auto par_c) __attribute__((always_inline)) {
+            constexpr bool FCA = decltype(fca_c)::value, FCB = decltype(fcb_c)::value;
+            constexpr unsigned PAR = decltype(par_c)::value;
+            auto load_z = [&]() __attribute__((always_inline)) {
+                if (FCA) {
+#pragma unroll
+                    for (int kt = 0; kt < S::KT1; ++kt)
+                        zqb[PAR][kt] = *reinterpret_cast<const bf16x8 *>(smem + kZ[kt] + (PAR ^ 1u) * S::ZBUF);
+                }
+            };
+            if (NCA32_ZQ_EARLY) load_z();
+            if (FCB) {
+                f32x4 acc[S::MT1];
+#pragma unroll
+                for (int mt = 0; mt < S::MT1; ++mt) {
+                    acc[mt] = b1v[mt];
+#pragma unroll
+                    for (int kt = 0; kt < S::KT1; ++kt)
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zqb[PAR ^ 1u][kt], acc[mt], 0,
+                                                                          0, 0);
+                }
+                bf16x8 hf[S::KT2];
+#pragma unroll
+                for (int kt = 0; kt < S::KT2; ++kt) {
+                    uint4 hv;
+                    hv.x = relu_bf16x2(cvt_pk_bf16(acc[2 * kt][0], acc[2 * kt][1]));
+                    hv.y = relu_bf16x2(cvt_pk_bf16(acc[2 * kt][2], acc[2 * kt][3]));
+                    hv.z = relu_bf16x2(cvt_pk_bf16(acc[2 * kt + 1][0], acc[2 * kt + 1][1]));
+                    hv.w = relu_bf16x2(cvt_pk_bf16(acc[2 * kt + 1][2], acc[2 * kt + 1][3]));
+                    hf[kt] = __builtin_bit_cast(bf16x8, hv);
+                }
+#pragma unroll
+                for (int m2 = 0; m2 < S::MT2; ++m2) {
+                    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int kt = 0; kt < S::KT2; ++kt)
+                        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[m2][kt], hf[kt], acc2, 0, 0, 0);
+                    lds_st128f(smem, kD[m2] + PAR * S::DBUF, make_float4(acc2[0], acc2[1], acc2[2], acc2[3]));
+                }
+            }
+            if (!NCA32_ZQ_EARLY) load_z();
+        };
+        int i = 0;
+        hinterval(F_{}, F_{}, P0{});
+        __syncthreads();
+        hinterval(T_{}, F_{}, P1{});
+        __syncthreads();
+        hinterval(T_{}, T_{}, P0{});
+        __syncthreads();
+        for (i = 3; i + 1 < T; i += 2) {
+            hinterval(T_{}, T_{}, P1{});
+            __syncthreads();
+            hinterval(T_{}, T_{}, P0{});
+            __syncthreads();
+        }
+        if (i < T) {
+            hinterval(T_{}, T_{}, P1{});
+            __syncthreads();
+            ++i;
+        }
+        // drain: intervals T, T+1 (T+2 has no hidden work)
+        if (i & 1) {
+            hinterval(T_{}, T_{}, P1{});
+            __syncthreads();
+            hinterval(F_{}, T_{}, P0{});
+            __syncthreads();
+        } else {
+            hinterval(T_{}, T_{}, P0{});
+            __syncthreads();
+            hinterval(F_{}, T_{}, P1{});
+            __syncthreads();
+        }
+        __syncthreads();
+    } else if (T > 0) {
+        // ================= channel waves: stencil (waves 4, 5) or update (waves 6, 7), and the
+        // per-step draws
+        __builtin_amdgcn_s_setprio(NCA32_CH_PRIO);
+        const bool stencil_wave = wave < 6;
+        const int cw = wave & 1;
+        const int cl = 8 * cw + (lane >> 3);  // cell of the tile
+        const int q8 = lane & 7;              // channel quad
+        int i = 0;
+        // the per-step draws: when the update stage enters step sd, step sd + 2 is drawn (its
+        // ring slot was last read by the updates of step sd - 2)
+        int sd = 0, ev_draw = 3;
+        auto events = [&]() __attribute__((always_inline)) {
+            if (i == ev_draw) {
+                const RolloutParams &ea = *reinterpret_cast<const RolloutParams *>(smem + sp.l_evp);
+                if (sd + 2 < ea.n_steps) draw(ea, sd + 2, false);
+                ++sd;
+                ev_draw = ((sd * HWn) >> 4) + 3;
+            }
+        };
+        if (stencil_wave) {
+            // B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 at the k slot of
+            // channel c (the A operand of tap 8 is the 4 channels' tap-8 values)
+            s16x4 kb0, kb1, kb2[4];
+            {
+                const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
+                const int j = lane & 3;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    kb0[k] = bf16_bits(kern[j * 9 + k]);
+                    kb1[k] = bf16_bits(kern[j * 9 + 4 + k]);
+                }
+                const short k8 = bf16_bits(kern[j * 9 + 8]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
+            }
+            // output lane (block b, kernel j) holds rows r = quads 4 (b & 1) + r of cell 8 cw + b / 2
+            unsigned kZw[4];
+            {
+                const unsigned b = (unsigned)lane >> 2, j = (unsigned)lane & 3u, r0 = 8u * cw + (b >> 1);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const unsigned chunk = 2u * (4u * (b & 1u) + (unsigned)r) + (j >> 1);
+                    kZw[r] = sp.l_Z + r0 * S::ZS + 16u * (chunk ^ zsw(r0)) + 8u * (j & 1u);
+                }
+            }
+            const unsigned RPb = (unsigned)(W + 1) * S::MS;
+            // top-left tap of M cell x: x - (W + 2)
+            const unsigned kT = sp.l_M + 16u * (unsigned)q8 - (unsigned)(W + 2) * S::MS;
+            int cbS = 0;  // board cell of the tile's first position: (16 i) mod HW
+            unsigned xs = cinfo[cl], xs_n = 0;
+            auto sinterval = [&](auto par_c) __attribute__((always_inline)) {
+                constexpr unsigned PAR = decltype(par_c)::value;
+                float4 t[9];
+                {
+                    const unsigned r0 = kT + xs * S::MS, r1 = r0 + RPb, r2 = r1 + RPb;
+                    t[0] = lds_ld128f(smem, r0);
+                    t[1] = lds_ld128f(smem, r0 + S::MS);
+                    t[2] = lds_ld128f(smem, r0 + 2 * S::MS);
+                    t[3] = lds_ld128f(smem, r1);
+                    t[4] = lds_ld128f(smem, r1 + S::MS);
+                    t[5] = lds_ld128f(smem, r1 + 2 * S::MS);
+                    t[6] = lds_ld128f(smem, r2);
+                    t[7] = lds_ld128f(smem, r2 + S::MS);
+                    t[8] = lds_ld128f(smem, r2 + 2 * S::MS);
+                    int cs = cbS + 16;
+                    if (cs >= HWn) cs -= HWn;
+                    xs_n = cinfo[cs + cl];
+                }
+                // bf16 taps in operand order: channel c, taps 0-3 / 4-7; tap 8 of the 4 channels
+                s16x4 sa0[4], sa1[4];
+                auto ch = [&](const float4 &v, int c) -> float { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    sa0[c] = __builtin_bit_cast(s16x4, make_uint2(cvt_pk_bf16(ch(t[0], c), ch(t[1], c)),
+                                                                  cvt_pk_bf16(ch(t[2], c), ch(t[3], c))));
+                    sa1[c] = __builtin_bit_cast(s16x4, make_uint2(cvt_pk_bf16(ch(t[4], c), ch(t[5], c)),
+                                                                  cvt_pk_bf16(ch(t[6], c), ch(t[7], c))));
+                }
+                const s16x4 a2 =
+                    __builtin_bit_cast(s16x4, make_uint2(cvt_pk_bf16(t[8].x, t[8].y), cvt_pk_bf16(t[8].z, t[8].w)));
+                f32x4 zc[4];
+#pragma unroll
+                for (int c0 = 0; c0 < 4; c0 += 2) {
+                    f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+                    d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0], kb0, d0, 0, 0, 0);
+                    d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0 + 1], kb0, d1, 0, 0, 0);
+                    d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1[c0], kb1, d0, 0, 0, 0);
+                    d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1[c0 + 1], kb1, d1, 0, 0, 0);
+                    d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0], d0, 0, 0, 0);
+                    d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0 + 1], d1, 0, 0, 0);
+                    zc[c0] = d0;
+                    zc[c0 + 1] = d1;
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    uint2 o;
+                    o.x = cvt_pk_bf16(zc[0][r], zc[1][r]);
+                    o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
+                    lds_st64(smem, kZw[r] + PAR * S::ZBUF, o);
+                }
+            };
+            auto advance = [&]() __attribute__((always_inline)) {
+                ++i;
+                cbS += 16;
+                if (cbS >= HWn) cbS -= HWn;
+                xs = xs_n;
+            };
+            i = 0;
+            while (i + 1 < T) {
+                sinterval(P0{});
+                events();
+                advance();
+                __syncthreads();
+                sinterval(P1{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            if (i < T) {
+                sinterval(P0{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            // drain: intervals T .. T+2 have no stencil work
+            for (int k = 0; k < 3; ++k) {
+                events();
+                ++i;
+                __syncthreads();
+            }
+        } else {
+            f32x4 b2v;
+            {
+                const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) b2v[v] = b2[4 * q8 + v];
+            }
+            // all ones where the lane's channel 4 q8 + v lies in the clamped input slice
+            unsigned imv[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int c = 4 * q8 + v;
+                imv[v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
+                asm volatile("" : "+v"(imv[v]));
+            }
+            // this lane computes the confidence (gated firing): the output slice is its quad; the
+            // head (at most 4 outputs over at most 4 channels) is held in registers
+            const bool oq = a.adaptive && q8 == (a.out_off >> 2);
+            float hw4[4][4], hb4[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                hb4[v] = v < a.n_out ? headL[a.n_out * a.c_out + v] : 0.0f;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) hw4[v][c] = (v < a.n_out && c < a.c_out) ? headL[v * a.c_out + c] : 0.0f;
+            }
+            const float tau = a.tau, conf_s = sp.conf_s;
+            const bool gconf = a.given_confident != 0, fast = sp.fast_conf != 0;
+            const bool need0 = flagsL[1] != 0;
+            const unsigned kDr = sp.l_D + (unsigned)cl * S::DS + 16u * ((unsigned)q8 ^ ((unsigned)(cl >> 1) & 7u));
+            const unsigned kM = sp.l_M + 16u * (unsigned)q8;
+            int cbU = HWn - 48;   // board cell of the update tile's first position: 16 (i-3) mod HW
+            int rbU = RING - 48;  // its ring slot: 16 (i-3) mod RING
+            int usU = -1;         // its step
+            unsigned xu = 0, xu_n = 0;
+            // gated firing: the next-step decision of the cell a lane updated in the previous
+            // interval (its new state, ring slot and drawn byte), made while this interval's loads
+            // are in flight
+            float pu[4] = {0.f, 0.f, 0.f, 0.f};
+            int pnidx = 0;
+            unsigned pnbyte = 0;
+            bool pval = false;
+            int fired_dec = 0;  // this lane's fired decisions (gated firing), added up at the end
+            auto decide = [&]() __attribute__((always_inline)) {
+                if (pval) {
+                    bool hi;
+                    if (fast) {
+                        // two logits in cell_readout_fn's order; s = exp(l0 - m) + exp(l1 - m) where
+                        // the larger term is exactly 1, so one exponential gives s
+                        float l0 = hb4[0], l1 = hb4[1];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            if (c < a.c_out) {
+                                l0 = __builtin_fmaf(hw4[0][c], pu[c], l0);
+                                l1 = __builtin_fmaf(hw4[1][c], pu[c], l1);
+                            }
+                        const float best = l1 > l0 ? l1 : l0;
+                        const float e = readout_expf((l1 > l0 ? l0 : l1) - best);
+                        hi = __fadd_rn(1.0f, e) < conf_s;
+                    } else {
+                        hi = cell_readout4(pu, a.c_out, a.n_out, a.head_kind, hw4, hb4) > tau;
+                    }
+                    const bool lo = hi || (gconf && (pnbyte & 0x80u));
+                    const bool f = ((lo ? pnbyte >> 1 : pnbyte) & 1u) != 0;
+                    const unsigned nb = (pnbyte & 0x80u) | (f ? 1u : 0u);
+                    ring[pnidx] = (unsigned char)nb;
+                    if (pnidx < 16) ring[RING + pnidx] = (unsigned char)nb;
+                    fired_dec += f ? 1 : 0;
+                }
+                pval = false;
+            };
+            auto uinterval = [&](auto up_c, auto last_c) __attribute__((always_inline)) {
+                constexpr bool DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
+                const unsigned PAR = (unsigned)(i & 1);
+                {
+                    int cu = cbU + 16;
+                    if (cu >= HWn) cu -= HWn;
+                    xu_n = cinfo[cu + cl];
+                }
+                if (!DUP) return;
+                float4 pd[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) pd[p] = lds_ld128f(smem, kDr + (PAR ^ 1u) * S::DBUF + (unsigned)p * S::DPART);
+                const unsigned madr = kM + xu * S::MS;
+                const float4 m4 = lds_ld128f(smem, madr);
+                const unsigned fb = ring[rbU + cl];
+                // the cell's step and board cell
+                const bool nxt = cbU + cl >= HWn;
+                const int sc = usU + (nxt ? 1 : 0);
+                const int qc = cbU + cl - (nxt ? HWn : 0);
+                int nidx = rbU + cl + HWn;
+                if (nidx >= RING) nidx -= RING;
+                unsigned nbyte = 0;
+                if (oq) nbyte = ring[nidx];
+                __builtin_amdgcn_sched_barrier(0);
+                if (oq) decide();
+                __builtin_amdgcn_sched_barrier(0);
+                float ds[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) ds[v] = (((b2v[v] + pd[0][v]) + pd[1][v]) + pd[2][v]) + pd[3][v];
+                const uint32_t d01 = cvt_pk_bf16(ds[0], ds[1]), d23 = cvt_pk_bf16(ds[2], ds[3]);
+                const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
+                float xo[4] = {m4.x, m4.y, m4.z, m4.w};
+                const float fu = (float)(fb & 1u);
+                const unsigned gvm = (fb & 0x80u) ? 0xffffffffu : 0u;
+                float xk[4] = {xo[0], xo[1], xo[2], xo[3]};
+                if (need0 && usU <= 0) {
+                    // first step, caller's state not clamped: the kept channels take the clamp values
+                    if (sc == 0 && gvm) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v)
+                            if (imv[v])
+                                xk[v] = a.clamp[(row * a.c_in + (4 * q8 + v - a.in_off)) * HWn + qc];
+                    }
+                }
+                float u[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
+                    const unsigned km = imv[v] & gvm;                     // clamped: keep x
+                    u[v] = __uint_as_float((km & __float_as_uint(xk[v])) | (~km & __float_as_uint(uv)));
+                }
+                bool ok = true;
+                if (LAST) ok = 16 * (i - 3) + cl < total;
+                if (ok) lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
+                if (oq) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) pu[v] = u[v];
+                    pnidx = nidx;
+                    pnbyte = nbyte;
+                    pval = ok && 16 * (i - 3) + cl + HWn < total;
+                }
+            };
+            auto advance = [&]() __attribute__((always_inline)) {
+                ++i;
+                cbU += 16;
+                if (cbU >= HWn) {
+                    cbU -= HWn;
+                    ++usU;
+                }
+                rbU += 16;
+                if (rbU >= RING) rbU -= RING;
+                xu = xu_n;
+            };
+            i = 0;
+            while (i < 3) {
+                uinterval(F_{}, F_{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            while (i < T + 2) {
+                uinterval(T_{}, F_{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            uinterval(T_{}, T_{});
+            events();
+            advance();
+            __syncthreads();
+            if (a.adaptive) {
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) fired_dec += __shfl_xor(fired_dec, o);
+                if (lane == 0 && fired_dec) atomicAdd(&flagsL[0], fired_dec);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- write back
+    {
+        float *xr = a.x_out + row * S::C * HWn;
+        for (int e = tid; e < S::C * HWn; e += NT) {
+            const int ch = e / HWn, q = e - ch * HWn;
+            xr[e] = m_at(q, ch);
+        }
+    }
+    if (a.conf_out) {
+        float *confL = reinterpret_cast<float *>(smem + sp.l_Z);  // Z and D are free now
+        for (int q = tid; q < HWn; q += NT) {
+            int am;
+            confL[q] = cell_readout_fn([&](int v) { return m_at(q, a.out_off + v); }, a.c_out, a.n_out, a.head_kind,
+                                       headL, headL + a.n_out * a.c_out, &am);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            for (int q = 0; q < HWn; ++q) sum = __fadd_rn(sum, confL[q]);
+            a.conf_out[row] = __fdiv_rn(sum, (float)HWn);
+        }
+    }
+    if (a.fired_out && tid == 0) a.fired_out[row] = flagsL[0];
+}
+
+}  // namespace nca

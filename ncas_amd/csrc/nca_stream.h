@@ -1,4 +1,5 @@
-// Entry of the streamed bf16 rollout kernel (C = 64, hidden = 256), defined in nca_stream.hip.
+// Entries of the streamed bf16 rollout kernels (C = 64 and C = 32, hidden = 256), defined in
+// nca_stream.hip and nca_stream32.hip.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -10,5 +11,13 @@ namespace nca {
 // Launches the streamed kernel when the call fits it (grid width <= 15, no noise, no single-step
 // fp32 mask, LDS plan within lds_limit bytes) and sets *used; otherwise leaves *used false.
 hipError_t launch_stream64(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used);
+
+// Whether a grid fits the streamed C = 32, hidden = 256 kernel (one board per workgroup).
+bool stream32_fits(int H, int W, int padding, int c_out, int n_out, unsigned lds_limit);
+
+// Launches the streamed C = 32 kernel when the call fits it (stream32_fits, no noise, no
+// single-step fp32 mask, gated firing with the output slice in one channel quad) and sets *used;
+// otherwise leaves *used false.
+hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used);
 
 }  // namespace nca

@@ -1,0 +1,90 @@
+// The streamed bf16 rollout kernel for C = 32, hidden = 256 (built with MFMA results in VGPRs)
+// and its launch planning.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <string.h>
+
+#include "nca_stream.h"
+#include "nca_rollout_stream32.h"
+
+namespace nca {
+
+// The gated-firing threshold on s = sum of exponentials (s >= 1) for a 2-output mlp head: the
+// readout's confidence min(max(1/s, 0), 1) (IEEE single-precision division, round to nearest)
+// exceeds tau exactly when s < the returned value, the smallest single-precision s >= 1 whose
+// confidence is <= tau (1/s does not increase with s).
+static float conf_threshold(float tau) {
+    if (!(tau < 1.0f)) return 0.0f;  // conf <= 1: never above tau
+    if (tau < 0.0f) return INFINITY;
+    auto conf_le = [&](uint32_t bits) {
+        float sv;
+        memcpy(&sv, &bits, 4);
+        volatile float num = 1.0f;
+        float c = num / sv;
+        if (c > 1.0f) c = 1.0f;
+        return c <= tau;
+    };
+    uint32_t lo = 0x3f800000u, hi = 0x7f800000u;  // 1.0 .. +inf (conf(+inf) = 0 <= tau)
+    if (conf_le(lo)) return 1.0f;
+    while (hi - lo > 1) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (conf_le(mid))
+            hi = mid;
+        else
+            lo = mid;
+    }
+    float r;
+    memcpy(&r, &hi, 4);
+    return r;
+}
+
+// One board per workgroup: needs W <= 31 (in-place update distance), H W >= W + 66 (a cell's next
+// stencil after its neighbours' updates), wall or zero padding (the border cells are constants),
+// for gated firing the output slice inside one channel quad and at most 4 outputs, and the plan
+// within the LDS.
+bool stream32_fits(int H, int W, int padding, int c_out, int n_out, unsigned lds_limit) {
+    if (W > 31 || H < 1 || W < 1 || H * W < W + 66 || padding == 2) return false;
+    const St32Plan L = st32_plan(H, W, c_out, n_out);
+    return L.total <= lds_limit && L.NM < 65536;
+}
+
+hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used) {
+    *used = false;
+    if (p.noise || p.fire_f32) return hipSuccess;
+    if (!stream32_fits(p.H, p.W, p.padding, p.c_out, p.n_out, lds_limit)) return hipSuccess;
+    if (p.adaptive && ((p.out_off & 3) != 0 || p.c_out > 4 || p.n_out > 4)) return hipSuccess;
+    const int hw = p.H * p.W;
+    if ((int64_t)p.n_steps * hw + 64 > 0x7fffffff) return hipSuccess;
+    if (p.rows > 0x7fffffff) return hipSuccess;
+    const St32Plan L = st32_plan(p.H, p.W, p.c_out, p.n_out);
+    St32Params sp;
+    memset(&sp, 0, sizeof(sp));
+    sp.a = p;
+    sp.NM = L.NM;
+    sp.RING = L.RING;
+    sp.T = (int)(((int64_t)p.n_steps * hw + 15) / 16);
+    sp.l_M = L.M;
+    sp.l_Z = L.Z;
+    sp.l_D = L.D;
+    sp.l_cinfo = L.cinfo;
+    sp.l_ring = L.ring;
+    sp.l_given = L.given;
+    sp.l_head = L.head;
+    sp.l_evp = L.evp;
+    sp.l_flags = L.flags;
+    sp.off_w1q = p.off_w1q;
+    sp.off_w2k = p.off_w2k;
+    sp.fast_conf = p.adaptive && p.head_kind == 0 && p.n_out == 2;
+    sp.conf_s = conf_threshold(p.tau);
+    auto kfn = rollout_stream32;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
+    if (e != hipSuccess) return e;
+    if (p.rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kfn, dim3((unsigned)p.rows), dim3(512), L.total, st, sp);
+    *used = true;
+    return hipGetLastError();
+}
+
+}  // namespace nca
