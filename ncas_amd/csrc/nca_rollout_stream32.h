@@ -21,12 +21,12 @@
 //   stencil wave (4, 5)    cells 8(w-4) .. 8(w-4)+7 of a tile, all 8 channel quads: lane (cell,
 //                          quad) loads the 9 taps of its 4 channels (a 16-lane group reads two
 //                          whole cells, free of bank conflicts) and runs the 3x3 perception on
-//                          v_mfma_f32_4x4x4_16b_bf16 -> Z.
+//                          v_mfma_f32_4x4x4_16b_bf16 -> Z. With confidence-gated firing the lanes
+//                          of the output quad also decide the cell's fire mask for the step from
+//                          the centre tap, the cell's state at the start of the step.
 //   update wave (6, 7)     cells 8(w-6) .. 8(w-6)+7 of a tile, all quads: dx = bf16(b2 + the four
 //                          partial sums in a fixed order), x += fire dx into M; the clamped input
-//                          channels of given cells keep their value. With confidence-gated
-//                          firing the lanes of the output quad compute the cell's confidence
-//                          from its new state and fix the cell's fire decision for the next step.
+//                          channels of given cells keep their value.
 // Interval i (one workgroup barrier): stencil of tile i -> Z[i & 1]; fc1 + fc2 partials of tile
 // i-2 -> D[i & 1], then the Z operands of tile i-1 from Z[(i-1) & 1]; update of tile i-3 from
 // D[(i-1) & 1].
@@ -40,8 +40,10 @@
 // Fire masks: a four-step byte ring in stream order (4 HW bytes and a 16-byte mirror of its
 // start, so that a tile's 16 bytes are contiguous): bit 0 fire, bit 1 (u < p_low) for gated
 // firing, bit 7 the cell's given flag. The channel waves draw the Philox uniforms of a whole step
-// two steps ahead (one evaluation per 4 cells); with gating the update writes bit 0 of the next
-// step's byte once the cell's new state, and so its confidence, is known.
+// two steps ahead (one evaluation per 4 cells); with gating the stencil of the cell's tile sets
+// bit 0 to the decision, three intervals before the update reads it. The decision needs only
+// conf > tau: for a 2-output mlp head that is s < conf_s on the sum of exponentials s (one
+// exponential, no division), with conf_s found on the host with the readout's own division.
 //
 // Clamp (model.py:430-438): the first step's perception reads the caller's state and every step's
 // output holds the clamp values in the input slice of given cells. M starts as the caller's state;
@@ -128,6 +130,8 @@ struct St32Params {
 // zsw: the Z row swizzle (a permutation of 0..15)
 __device__ __forceinline__ unsigned zsw(unsigned r) { return (r & 8u) | ((r & 3u) << 1) | ((r >> 2) & 1u); }
 
+// GATED: confidence-gated firing (a.adaptive), compiled out of the plain kernel
+template <bool GATED>
 __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     using S = St32;
     constexpr int NT = 512;
@@ -192,16 +196,15 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     }
     __syncthreads();
 
-    // ---- fire masks of step s for all cells (channel waves, thread tb of 256). decide: the final
-    // decision of a gated step from the current M (the state before step s); otherwise gated
-    // steps get both threshold bits and their updates decide later.
+    // ---- fire masks of step s for all cells (channel waves, thread tb of 256): the fire bit, or
+    // for gated firing both threshold bits (the stencil decides between them)
     auto ring_put = [&](int s, int q, unsigned v) __attribute__((always_inline)) {
         const int o = (s % S::NSLOT) * HWn + q;
         ring[o] = (unsigned char)v;
         if (o < 16) ring[RING + o] = (unsigned char)v;
     };
     const int nq4 = (HWn + 3) >> 2;
-    auto draw = [&](const RolloutParams &pa, int s, bool decide) __attribute__((always_inline)) {
+    auto draw = [&](const RolloutParams &pa, int s) __attribute__((always_inline)) {
         for (int it = tb; it < nq4; it += 256) {
             float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
             if (!pa.fire_u8) {
@@ -219,25 +222,17 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                     b = pa.fire_u8[((int64_t)s * pa.rows + row) * HWn + q] != 0;
                 } else {
                     const unsigned b0 = u[e] < pa.p, b1 = u[e] < pa.p_low;
-                    if (pa.adaptive && decide) {
-                        int am;
-                        const float cf = cell_readout_fn([&](int v) { return m_at(q, pa.out_off + v); }, pa.c_out,
-                                                         pa.n_out, pa.head_kind, headL, headL + pa.n_out * pa.c_out,
-                                                         &am);
-                        b = (cf > pa.tau || (pa.given_confident && gv)) ? b1 : b0;
-                    } else {
-                        b = pa.adaptive ? (b0 | (b1 << 1)) : b0;
-                    }
+                    b = pa.adaptive ? (b0 | (b1 << 1)) : b0;
                 }
                 ring_put(s, q, b | (gv << 7));
-                if (!pa.adaptive || decide) cnt += (int)(b & 1u);
+                if (!pa.adaptive) cnt += (int)(b & 1u);
             }
             if (cnt) atomicAdd(&flagsL[0], cnt);
         }
     };
     if (wave >= 4 && a.n_steps > 0) {
-        draw(a, 0, true);
-        if (a.n_steps > 1) draw(a, 1, false);
+        draw(a, 0);
+        if (a.n_steps > 1) draw(a, 1);
     }
     __syncthreads();
 
@@ -390,11 +385,47 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
         auto events = [&]() __attribute__((always_inline)) {
             if (i == ev_draw) {
                 const RolloutParams &ea = *reinterpret_cast<const RolloutParams *>(smem + sp.l_evp);
-                if (sd + 2 < ea.n_steps) draw(ea, sd + 2, false);
+                if (sd + 2 < ea.n_steps) draw(ea, sd + 2);
                 ++sd;
                 ev_draw = ((sd * HWn) >> 4) + 3;
             }
         };
+        // gated firing: the lanes of the output quad decide a cell's mask for the step from its
+        // state at the step's start, the centre tap of its stencil; the head (at most 4 outputs
+        // over at most 4 channels) is held in registers
+        const bool oq = GATED && q8 == (a.out_off >> 2);
+        float hw4[4][4], hb4[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            hb4[v] = v < a.n_out ? headL[a.n_out * a.c_out + v] : 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) hw4[v][c] = (v < a.n_out && c < a.c_out) ? headL[v * a.c_out + c] : 0.0f;
+        }
+        const float tau = a.tau, conf_s = sp.conf_s;
+        const bool gconf = a.given_confident != 0, fast = sp.fast_conf != 0;
+        // the fire bit from a cell's drawn byte and its state's out-slice channels xo
+        auto gated_fire = [&](const float xo[4], unsigned byte) -> bool {
+            bool hi;
+            if (fast) {
+                // two logits in cell_readout_fn's order; s = exp(l0 - m) + exp(l1 - m) where the
+                // larger term is exactly 1, so one exponential gives s
+                float l0 = hb4[0], l1 = hb4[1];
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (c < a.c_out) {
+                        l0 = __builtin_fmaf(hw4[0][c], xo[c], l0);
+                        l1 = __builtin_fmaf(hw4[1][c], xo[c], l1);
+                    }
+                const float best = l1 > l0 ? l1 : l0;
+                const float e = readout_expf((l1 > l0 ? l0 : l1) - best);
+                hi = __fadd_rn(1.0f, e) < conf_s;
+            } else {
+                hi = cell_readout4(xo, a.c_out, a.n_out, a.head_kind, hw4, hb4) > tau;
+            }
+            const bool lo = hi || (gconf && (byte & 0x80u));
+            return ((lo ? byte >> 1 : byte) & 1u) != 0;
+        };
+        int fired_dec = 0;  // this lane's fired decisions (gated firing), added up at the end
         if (stencil_wave) {
             // B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 at the k slot of
             // channel c (the A operand of tap 8 is the 4 channels' tap-8 values)
@@ -427,6 +458,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             // top-left tap of M cell x: x - (W + 2)
             const unsigned kT = sp.l_M + 16u * (unsigned)q8 - (unsigned)(W + 2) * S::MS;
             int cbS = 0;  // board cell of the tile's first position: (16 i) mod HW
+            int rbS = 0;  // its ring slot: (16 i) mod RING
             unsigned xs = cinfo[cl], xs_n = 0;
             auto sinterval = [&](auto par_c) __attribute__((always_inline)) {
                 constexpr unsigned PAR = decltype(par_c)::value;
@@ -446,6 +478,8 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                     if (cs >= HWn) cs -= HWn;
                     xs_n = cinfo[cs + cl];
                 }
+                unsigned sbyte = 0;
+                if (GATED && oq) sbyte = ring[rbS + cl];
                 // bf16 taps in operand order: channel c, taps 0-3 / 4-7; tap 8 of the 4 channels
                 s16x4 sa0[4], sa1[4];
                 auto ch = [&](const float4 &v, int c) -> float { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
@@ -478,11 +512,23 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                     o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
                     lds_st64(smem, kZw[r] + PAR * S::ZBUF, o);
                 }
+                if (GATED && oq && 16 * i + cl < total) {
+                    const float xo[4] = {t[4].x, t[4].y, t[4].z, t[4].w};
+                    const bool f = gated_fire(xo, sbyte);
+                    const unsigned nb = (sbyte & 0x80u) | (f ? 1u : 0u);
+                    int k = rbS + cl;  // ring slot, or its mirror copy past RING
+                    if (k >= RING) k -= RING;
+                    ring[k] = (unsigned char)nb;
+                    if (k < 16) ring[RING + k] = (unsigned char)nb;
+                    fired_dec += f ? 1 : 0;
+                }
             };
             auto advance = [&]() __attribute__((always_inline)) {
                 ++i;
                 cbS += 16;
                 if (cbS >= HWn) cbS -= HWn;
+                rbS += 16;
+                if (rbS >= RING) rbS -= RING;
                 xs = xs_n;
             };
             i = 0;
@@ -508,6 +554,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 ++i;
                 __syncthreads();
             }
+            if (GATED) {
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) fired_dec += __shfl_xor(fired_dec, o);
+                if (lane == 0 && fired_dec) atomicAdd(&flagsL[0], fired_dec);
+            }
         } else {
             f32x4 b2v;
             {
@@ -523,18 +574,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 imv[v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
                 asm volatile("" : "+v"(imv[v]));
             }
-            // this lane computes the confidence (gated firing): the output slice is its quad; the
-            // head (at most 4 outputs over at most 4 channels) is held in registers
-            const bool oq = a.adaptive && q8 == (a.out_off >> 2);
-            float hw4[4][4], hb4[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                hb4[v] = v < a.n_out ? headL[a.n_out * a.c_out + v] : 0.0f;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) hw4[v][c] = (v < a.n_out && c < a.c_out) ? headL[v * a.c_out + c] : 0.0f;
-            }
-            const float tau = a.tau, conf_s = sp.conf_s;
-            const bool gconf = a.given_confident != 0, fast = sp.fast_conf != 0;
             const bool need0 = flagsL[1] != 0;
             const unsigned kDr = sp.l_D + (unsigned)cl * S::DS + 16u * ((unsigned)q8 ^ ((unsigned)(cl >> 1) & 7u));
             const unsigned kM = sp.l_M + 16u * (unsigned)q8;
@@ -542,42 +581,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             int rbU = RING - 48;  // its ring slot: 16 (i-3) mod RING
             int usU = -1;         // its step
             unsigned xu = 0, xu_n = 0;
-            // gated firing: the next-step decision of the cell a lane updated in the previous
-            // interval (its new state, ring slot and drawn byte), made while this interval's loads
-            // are in flight
-            float pu[4] = {0.f, 0.f, 0.f, 0.f};
-            int pnidx = 0;
-            unsigned pnbyte = 0;
-            bool pval = false;
-            int fired_dec = 0;  // this lane's fired decisions (gated firing), added up at the end
-            auto decide = [&]() __attribute__((always_inline)) {
-                if (pval) {
-                    bool hi;
-                    if (fast) {
-                        // two logits in cell_readout_fn's order; s = exp(l0 - m) + exp(l1 - m) where
-                        // the larger term is exactly 1, so one exponential gives s
-                        float l0 = hb4[0], l1 = hb4[1];
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            if (c < a.c_out) {
-                                l0 = __builtin_fmaf(hw4[0][c], pu[c], l0);
-                                l1 = __builtin_fmaf(hw4[1][c], pu[c], l1);
-                            }
-                        const float best = l1 > l0 ? l1 : l0;
-                        const float e = readout_expf((l1 > l0 ? l0 : l1) - best);
-                        hi = __fadd_rn(1.0f, e) < conf_s;
-                    } else {
-                        hi = cell_readout4(pu, a.c_out, a.n_out, a.head_kind, hw4, hb4) > tau;
-                    }
-                    const bool lo = hi || (gconf && (pnbyte & 0x80u));
-                    const bool f = ((lo ? pnbyte >> 1 : pnbyte) & 1u) != 0;
-                    const unsigned nb = (pnbyte & 0x80u) | (f ? 1u : 0u);
-                    ring[pnidx] = (unsigned char)nb;
-                    if (pnidx < 16) ring[RING + pnidx] = (unsigned char)nb;
-                    fired_dec += f ? 1 : 0;
-                }
-                pval = false;
-            };
             auto uinterval = [&](auto up_c, auto last_c) __attribute__((always_inline)) {
                 constexpr bool DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
                 const unsigned PAR = (unsigned)(i & 1);
@@ -597,13 +600,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 const bool nxt = cbU + cl >= HWn;
                 const int sc = usU + (nxt ? 1 : 0);
                 const int qc = cbU + cl - (nxt ? HWn : 0);
-                int nidx = rbU + cl + HWn;
-                if (nidx >= RING) nidx -= RING;
-                unsigned nbyte = 0;
-                if (oq) nbyte = ring[nidx];
-                __builtin_amdgcn_sched_barrier(0);
-                if (oq) decide();
-                __builtin_amdgcn_sched_barrier(0);
                 float ds[4];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) ds[v] = (((b2v[v] + pd[0][v]) + pd[1][v]) + pd[2][v]) + pd[3][v];
@@ -632,13 +628,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 bool ok = true;
                 if (LAST) ok = 16 * (i - 3) + cl < total;
                 if (ok) lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
-                if (oq) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) pu[v] = u[v];
-                    pnidx = nidx;
-                    pnbyte = nbyte;
-                    pval = ok && 16 * (i - 3) + cl + HWn < total;
-                }
             };
             auto advance = [&]() __attribute__((always_inline)) {
                 ++i;
@@ -668,11 +657,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             events();
             advance();
             __syncthreads();
-            if (a.adaptive) {
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) fired_dec += __shfl_xor(fired_dec, o);
-                if (lane == 0 && fired_dec) atomicAdd(&flagsL[0], fired_dec);
-            }
         }
     }
     __syncthreads();

@@ -77,7 +77,7 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
     sp.off_w2k = p.off_w2k;
     sp.fast_conf = p.adaptive && p.head_kind == 0 && p.n_out == 2;
     sp.conf_s = conf_threshold(p.tau);
-    auto kfn = rollout_stream32;
+    auto kfn = p.adaptive ? rollout_stream32<true> : rollout_stream32<false>;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
     if (e != hipSuccess) return e;
