@@ -7,10 +7,11 @@ p_fire=0.5, D=256 steps in one launch of the LDS-resident kernel, then the conf@
 the 128 trials. Weights N(0, 0.02) (synthetic), states zero-initialised and clamped; inputs
 resident in HBM before the timed region.
 
-`--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16, D=13,000, p_fire=0.5) and
-`--workload hardmaze30` (1,000 hard mazes 30x30 with 10 % extra openings, K=64 -> 64,000 rows,
-C=32, MLP 128 -> 256 -> 32, D=200, p_fire=0.8 gated to 0.2 above confidence 0.9) time the
-halo-tiled per-step path the same way. `--workload bptt30` times one training iteration: 64
+`--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16, D=13,000, p_fire=0.5)
+times the halo-tiled per-step path the same way, and `--workload hardmaze30` (1,000 hard mazes
+30x30 with 10 % extra openings, K=64 -> 64,000 rows, C=32, MLP 128 -> 256 -> 32, D=200, p_fire=0.8
+gated to 0.2 above confidence 0.9) the streamed C=32 kernel (one board per workgroup, the whole
+rollout in one launch). `--workload bptt30` times one training iteration: 64
 states sampled from a replay pool of 1,024 (30x30 DFS mazes, C=32 cell, bf16 forward with fp32
 master weights), a 32-step BPTT chunk with the per-cell cross-entropy on the 2-class path
 targets, AdamW, write-back; it reports cell-steps/s and the peak activation memory.
@@ -18,7 +19,7 @@ targets, AdamW, write-back; it reports cell-steps/s and the peak activation memo
 value = rows * H * W * D * steps / wall seconds (cell-updates/s). The roofline block prices the
 rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) per cell-update, the
 reference's count_step_flops convention) against the MI355X dense MFMA peak of the compute type,
-or, for the per-step path when it is lower, its algorithmic HBM bytes (the fp32 state read and
+or, for the per-step path (maze201) when it is lower, its algorithmic HBM bytes (the fp32 state read and
 written once per step plus the given mask: 8 C + 1 bytes per cell-update) against 8 TB/s. The
 kernel time comes from HIP events recorded on the launch stream around every rollout call. The
 cpu_baseline times the CPU oracle (PyTorch-CPU restatement of the reference step, fp32, all host
@@ -61,7 +62,7 @@ WORKLOADS = {
         p_low=0.2, tau=0.9, extra=0.10,
         desc="hard maze 30x30 (+10% openings): 1000 boards x K=64 = 64000 rows, D=200 steps, "
              "C=32, MLP 128-256-32, p_fire=0.8 gated to 0.2 above confidence 0.9, conf@K, "
-             "one halo-tiled launch per step"),
+             "one streamed launch per rollout (one board per workgroup)"),
 }
 
 
@@ -263,13 +264,13 @@ def run_bptt(wl, precision, steps, warmup):
 
 
 def roofline(name, wl, precision, res):
-    """Binding ceiling of the workload's dominant kernel: MFMA FLOPs for the resident kernel;
-    the lower of MFMA FLOPs and HBM bytes for the per-step path."""
+    """Binding ceiling of the workload's dominant kernel: MFMA FLOPs for the resident kernels
+    (sudoku9, hardmaze30); the lower of MFMA FLOPs and HBM bytes for the per-step path (maze201)."""
     flops = flop_per_cell_update(wl["preset"])
     mfma_ceiling = PEAK_TFLOPS[precision] * 1e12 / flops
     block = {"bound": "mfma", "achieved": res["achieved_tflops"], "peak": PEAK_TFLOPS[precision],
              "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic_from_profiles(name, precision)}
-    if name != "sudoku9":
+    if name == "maze201":
         nbytes = hbm_bytes_per_cell_update(wl["preset"])
         hbm_ceiling = PEAK_HBM_GBS * 1e9 / nbytes
         if hbm_ceiling < mfma_ceiling:

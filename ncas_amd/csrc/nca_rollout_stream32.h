@@ -21,27 +21,29 @@
 //   stencil wave (4, 5)    cells 8(w-4) .. 8(w-4)+7 of a tile, all 8 channel quads: lane (cell,
 //                          quad) loads the 9 taps of its 4 channels (a 16-lane group reads two
 //                          whole cells, free of bank conflicts) and runs the 3x3 perception on
-//                          v_mfma_f32_4x4x4_16b_bf16 -> Z. With confidence-gated firing the lanes
-//                          of the output quad also decide the cell's fire mask for the step from
-//                          the centre tap, the cell's state at the start of the step.
+//                          v_mfma_f32_4x4x4_16b_bf16 -> Z.
 //   update wave (6, 7)     cells 8(w-6) .. 8(w-6)+7 of a tile, all quads: dx = bf16(b2 + the four
 //                          partial sums in a fixed order), x += fire dx into M; the clamped input
-//                          channels of given cells keep their value.
+//                          channels of given cells keep their value. With confidence-gated firing
+//                          the lanes of the output quad decide the cell's fire mask from its state
+//                          at the start of the step (M before the update) and pass it on to the
+//                          cell's other 7 lanes.
 // Interval i (one workgroup barrier): stencil of tile i -> Z[i & 1]; fc1 + fc2 partials of tile
-// i-2 -> D[i & 1], then the Z operands of tile i-1 from Z[(i-1) & 1]; update of tile i-3 from
-// D[(i-1) & 1].
+// i-2 -> D[i & 1], while the Z operands of tile i-1 load from Z[(i-1) & 1] into registers for the
+// next interval; update of tile i-3 from D[(i-1) & 1]. The stencil waves likewise load the next
+// tile's taps while they work on this one.
 //
-// M is updated in place. The stencil of tile i reads positions 16i - (W+1) .. 16i + 15 + (W+1)
-// of its step and the update of tile i-3 in the same interval writes positions 16i - 48 ..
-// 16i - 33: disjoint for W <= 31. A cell's stencil of step s+1 comes HW - (W+1) positions after
-// the stencils of its neighbours at step s, which is at least 4 intervals after their updates
-// for HW >= W + 66.
+// M is updated in place. The stencil waves load the taps of tile i+1 in interval i: positions
+// 16(i+1) - (W+1) .. 16(i+1) + 15 + (W+1) of its step, while the update of tile i-3 in the same
+// interval writes positions 16i - 48 .. 16i - 33: disjoint for W <= 31. Those taps hold the step's
+// state once the previous step's updates of the same cells are done, up to position
+// 16(i+1) + 16 + W - HW in tile i-4 or earlier: HW >= W + 81.
 //
 // Fire masks: a four-step byte ring in stream order (4 HW bytes and a 16-byte mirror of its
 // start, so that a tile's 16 bytes are contiguous): bit 0 fire, bit 1 (u < p_low) for gated
 // firing, bit 7 the cell's given flag. The channel waves draw the Philox uniforms of a whole step
-// two steps ahead (one evaluation per 4 cells); with gating the stencil of the cell's tile sets
-// bit 0 to the decision, three intervals before the update reads it. The decision needs only
+// two steps ahead (one evaluation per 4 cells); with gating the update chooses between the two
+// threshold bits. The decision needs only
 // conf > tau: for a 2-output mlp head that is s < conf_s on the sum of exponentials s (one
 // exponential, no division), with conf_s found on the host with the readout's own division.
 //
@@ -120,12 +122,6 @@ struct St32Params {
     unsigned off_w1q, off_w2k;
 };
 
-#ifndef NCA32_CH_PRIO
-#define NCA32_CH_PRIO 3  // issue priority of the stencil and update waves
-#endif
-#ifndef NCA32_ZQ_EARLY
-#define NCA32_ZQ_EARLY 0  // hidden waves load the next Z operands at the start of the interval
-#endif
 
 // zsw: the Z row swizzle (a permutation of 0..15)
 __device__ __forceinline__ unsigned zsw(unsigned r) { return (r & 8u) | ((r & 3u) << 1) | ((r >> 2) & 1u); }
@@ -285,8 +281,8 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
         for (int m2 = 0; m2 < S::MT2; ++m2)
             kD[m2] = sp.l_D + (unsigned)ws * S::DPART + (unsigned)n * S::DS +
                      16u * ((unsigned)(4 * m2 + g) ^ ((unsigned)(n >> 1) & 7u));
-        // Z operands: tile i-1's are loaded in interval i into zqb[i & 1], fc1 of tile i-2 reads
-        // zqb[(i-1) & 1]
+        // Z operands: tile i-1's are loaded at the start of interval i into zqb[i & 1] (they are
+        // in flight during fc1 of tile i-2, which reads zqb[(i-1) & 1])
         bf16x8 zqb[2][S::KT1];
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -307,7 +303,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                         zqb[PAR][kt] = *reinterpret_cast<const bf16x8 *>(smem + kZ[kt] + (PAR ^ 1u) * S::ZBUF);
                 }
             };
-            if (NCA32_ZQ_EARLY) load_z();
+            load_z();
             if (FCB) {
                 f32x4 acc[S::MT1];
 #pragma unroll
@@ -337,7 +333,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                     lds_st128f(smem, kD[m2] + PAR * S::DBUF, make_float4(acc2[0], acc2[1], acc2[2], acc2[3]));
                 }
             }
-            if (!NCA32_ZQ_EARLY) load_z();
         };
         int i = 0;
         hinterval(F_{}, F_{}, P0{});
@@ -373,7 +368,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     } else if (T > 0) {
         // ================= channel waves: stencil (waves 4, 5) or update (waves 6, 7), and the
         // per-step draws
-        __builtin_amdgcn_s_setprio(NCA32_CH_PRIO);
+        __builtin_amdgcn_s_setprio(3);  // issue priority over the hidden waves' MFMAs
         const bool stencil_wave = wave < 6;
         const int cw = wave & 1;
         const int cl = 8 * cw + (lane >> 3);  // cell of the tile
@@ -390,10 +385,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 ev_draw = ((sd * HWn) >> 4) + 3;
             }
         };
-        // gated firing: the lanes of the output quad decide a cell's mask for the step from its
-        // state at the step's start, the centre tap of its stencil; the head (at most 4 outputs
-        // over at most 4 channels) is held in registers
-        const bool oq = GATED && q8 == (a.out_off >> 2);
+        // gated firing: the update lanes of the output quad decide a cell's mask for the step from
+        // its state at the step's start (M before the update) and pass it to the cell's other
+        // lanes; the head (at most 4 outputs over at most 4 channels) is held in registers
+        const int oqi = a.out_off >> 2;
+        const bool oq = GATED && q8 == oqi;
         float hw4[4][4], hb4[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -457,29 +453,35 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             const unsigned RPb = (unsigned)(W + 1) * S::MS;
             // top-left tap of M cell x: x - (W + 2)
             const unsigned kT = sp.l_M + 16u * (unsigned)q8 - (unsigned)(W + 2) * S::MS;
-            int cbS = 0;  // board cell of the tile's first position: (16 i) mod HW
-            int rbS = 0;  // its ring slot: (16 i) mod RING
-            unsigned xs = cinfo[cl], xs_n = 0;
+            int cbS = 0;  // board cell of tile i's first position: (16 i) mod HW
+            // the taps of tile i are in tb[i & 1], loaded at the start of interval i-1 (tile 0's
+            // before interval 0); xs1: M cell of the lane's cell in tile i+1
+            float4 tb[2][9];
+            auto load_taps = [&](float4(&t)[9], unsigned x) __attribute__((always_inline)) {
+                const unsigned r0 = kT + x * S::MS, r1 = r0 + RPb, r2 = r1 + RPb;
+                t[0] = lds_ld128f(smem, r0);
+                t[1] = lds_ld128f(smem, r0 + S::MS);
+                t[2] = lds_ld128f(smem, r0 + 2 * S::MS);
+                t[3] = lds_ld128f(smem, r1);
+                t[4] = lds_ld128f(smem, r1 + S::MS);
+                t[5] = lds_ld128f(smem, r1 + 2 * S::MS);
+                t[6] = lds_ld128f(smem, r2);
+                t[7] = lds_ld128f(smem, r2 + S::MS);
+                t[8] = lds_ld128f(smem, r2 + 2 * S::MS);
+            };
+            load_taps(tb[0], cinfo[cl]);
+            unsigned xs1 = cinfo[16 + cl], xs2 = 0;  // HW >= 32
             auto sinterval = [&](auto par_c) __attribute__((always_inline)) {
                 constexpr unsigned PAR = decltype(par_c)::value;
-                float4 t[9];
+                // the next tile's taps (read after this interval's barrier-separated updates; the
+                // last interval's read tile T, whose cells exist but are unused)
+                load_taps(tb[PAR ^ 1u], xs1);
                 {
-                    const unsigned r0 = kT + xs * S::MS, r1 = r0 + RPb, r2 = r1 + RPb;
-                    t[0] = lds_ld128f(smem, r0);
-                    t[1] = lds_ld128f(smem, r0 + S::MS);
-                    t[2] = lds_ld128f(smem, r0 + 2 * S::MS);
-                    t[3] = lds_ld128f(smem, r1);
-                    t[4] = lds_ld128f(smem, r1 + S::MS);
-                    t[5] = lds_ld128f(smem, r1 + 2 * S::MS);
-                    t[6] = lds_ld128f(smem, r2);
-                    t[7] = lds_ld128f(smem, r2 + S::MS);
-                    t[8] = lds_ld128f(smem, r2 + 2 * S::MS);
-                    int cs = cbS + 16;
-                    if (cs >= HWn) cs -= HWn;
-                    xs_n = cinfo[cs + cl];
+                    int c2 = cbS + 32;
+                    if (c2 >= HWn) c2 -= HWn;
+                    xs2 = cinfo[c2 + cl];
                 }
-                unsigned sbyte = 0;
-                if (GATED && oq) sbyte = ring[rbS + cl];
+                const float4(&t)[9] = tb[PAR];
                 // bf16 taps in operand order: channel c, taps 0-3 / 4-7; tap 8 of the 4 channels
                 s16x4 sa0[4], sa1[4];
                 auto ch = [&](const float4 &v, int c) -> float { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; };
@@ -512,24 +514,12 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                     o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
                     lds_st64(smem, kZw[r] + PAR * S::ZBUF, o);
                 }
-                if (GATED && oq && 16 * i + cl < total) {
-                    const float xo[4] = {t[4].x, t[4].y, t[4].z, t[4].w};
-                    const bool f = gated_fire(xo, sbyte);
-                    const unsigned nb = (sbyte & 0x80u) | (f ? 1u : 0u);
-                    int k = rbS + cl;  // ring slot, or its mirror copy past RING
-                    if (k >= RING) k -= RING;
-                    ring[k] = (unsigned char)nb;
-                    if (k < 16) ring[RING + k] = (unsigned char)nb;
-                    fired_dec += f ? 1 : 0;
-                }
             };
             auto advance = [&]() __attribute__((always_inline)) {
                 ++i;
                 cbS += 16;
                 if (cbS >= HWn) cbS -= HWn;
-                rbS += 16;
-                if (rbS >= RING) rbS -= RING;
-                xs = xs_n;
+                xs1 = xs2;
             };
             i = 0;
             while (i + 1 < T) {
@@ -553,11 +543,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 events();
                 ++i;
                 __syncthreads();
-            }
-            if (GATED) {
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) fired_dec += __shfl_xor(fired_dec, o);
-                if (lane == 0 && fired_dec) atomicAdd(&flagsL[0], fired_dec);
             }
         } else {
             f32x4 b2v;
@@ -606,7 +591,15 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 const uint32_t d01 = cvt_pk_bf16(ds[0], ds[1]), d23 = cvt_pk_bf16(ds[2], ds[3]);
                 const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
                 float xo[4] = {m4.x, m4.y, m4.z, m4.w};
-                const float fu = (float)(fb & 1u);
+                unsigned fbit = fb & 1u;
+                if (GATED) {
+                    int f = 0;
+                    if (oq) f = gated_fire(xo, fb) ? 1 : 0;
+                    f = __shfl(f, (lane & ~7) | oqi);  // the cell's 8 lanes take the decision
+                    fbit = (unsigned)f;
+                    if (oq && (!LAST || 16 * (i - 3) + cl < total)) fired_dec += f;
+                }
+                const float fu = (float)fbit;
                 const unsigned gvm = (fb & 0x80u) ? 0xffffffffu : 0u;
                 float xk[4] = {xo[0], xo[1], xo[2], xo[3]};
                 if (need0 && usU <= 0) {
@@ -657,6 +650,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             events();
             advance();
             __syncthreads();
+            if (GATED) {
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) fired_dec += __shfl_xor(fired_dec, o);
+                if (lane == 0 && fired_dec) atomicAdd(&flagsL[0], fired_dec);
+            }
         }
     }
     __syncthreads();

@@ -39,12 +39,12 @@ static float conf_threshold(float tau) {
     return r;
 }
 
-// One board per workgroup: needs W <= 31 (in-place update distance), H W >= W + 66 (a cell's next
-// stencil after its neighbours' updates), wall or zero padding (the border cells are constants),
+// One board per workgroup: needs W <= 31 (in-place update distance), H W >= W + 81 (taps loaded an
+// interval ahead hold the step's state), wall or zero padding (the border cells are constants),
 // for gated firing the output slice inside one channel quad and at most 4 outputs, and the plan
 // within the LDS.
 bool stream32_fits(int H, int W, int padding, int c_out, int n_out, unsigned lds_limit) {
-    if (W > 31 || H < 1 || W < 1 || H * W < W + 66 || padding == 2) return false;
+    if (W > 31 || H < 1 || W < 1 || H * W < W + 81 || padding == 2) return false;
     const St32Plan L = st32_plan(H, W, c_out, n_out);
     return L.total <= lds_limit && L.NM < 65536;
 }

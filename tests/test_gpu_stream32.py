@@ -127,7 +127,7 @@ def test_gated_firing_fused_equals_chained_and_oracle_steps(tau_kind):
 
 
 @pytest.mark.parametrize("padding", ["zero", "wall"])
-@pytest.mark.parametrize("H,W,n", [(30, 31, 7), (9, 9, 5), (4, 24, 3), (13, 6, 9)])
+@pytest.mark.parametrize("H,W,n", [(30, 31, 7), (10, 10, 5), (5, 24, 3), (16, 6, 9)])
 def test_grids_paddings_and_partial_tiles(H, W, n, padding):
     """Random states and clamps (the caller's state does not hold the clamp values: the first
     step's update takes them from the clamp tensor), step counts whose last tile is partial."""
