@@ -137,7 +137,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
     const int g = lane >> 4, n = lane & 15;  // n: cell of the tile (MFMA column), g: lane group
     const bool hidden_wave = wave < 4;
     const int ws = wave & 3;                 // hidden slice or channel set of the wave
-    const int iq = 4 * ws + g;               // channel quad of a channel wave's lane
     const int tb = tid - 256;                // thread index among the channel waves
     const int H = a.H, W = a.W, HWn = H * W;
     const int R = sp.R, RH = sp.RH, RP = sp.RP, PB = sp.PB, NB = sp.NB, RING = sp.RING;
@@ -422,57 +421,13 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
         }
         __syncthreads();
     } else if (T > 0) {
-        // ================= channel waves: stencil, fc2 + update, end-of-step work
-        // the channel wave holds the interval's longest dependency chain: its instructions win the
-        // SIMD's issue arbitration over the hidden wave's MFMAs
+        // ================= channel waves: stencil (waves 4, 5) or fc2 + update (waves 6, 7) of
+        // channels [32 cw, 32 cw + 32), and the end-of-step work (all four)
+        // the channel waves hold the interval's longest dependency chains: their instructions win
+        // the SIMD's issue arbitration over the hidden waves' MFMAs
         __builtin_amdgcn_s_setprio(3);
-        bf16x8 w2f[S::KT2];
-        f32x4 b2v;
-        {
-            const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2h);
-            const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
-#pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) w2f[kt] = w2[(ws * S::KT2 + kt) * 64 + lane];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) b2v[v] = b2[4 * iq + v];
-#pragma unroll
-            for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[kt]));
-        }
-        // stencil B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 placed at the
-        // k slot of channel c (the A operand of tap 8 is the 4 channels' tap-8 values as loaded)
-        s16x4 kb0, kb1, kb2[4];
-        {
-            const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
-            const int j = lane & 3;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                kb0[k] = bf16_bits(kern[j * 9 + k]);
-                kb1[k] = bf16_bits(kern[j * 9 + 4 + k]);
-            }
-            const short k8 = bf16_bits(kern[j * 9 + 8]);
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
-        }
-        // all ones where the lane's channel 4 iq + v lies in the clamped input slice
-        unsigned imv[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int c = 4 * iq + v;
-            imv[v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
-            asm volatile("" : "+v"(imv[v]));  // kept a plain VGPR mask (no per-channel SGPR lane masks)
-        }
-        unsigned kZw;
-        {
-            const int j = lane & 3, b = lane >> 2;
-            kZw = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 16u * (unsigned)((2 * iq + (j >> 1)) ^ (2 * (b & 3))) +
-                  8u * (unsigned)(j & 1);
-        }
-        const unsigned hx = (unsigned)((n >> 2) & 1);
-        const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * ((unsigned)g ^ hx);
-        // + centre: the top-left tap, the left taps of the middle and bottom rows
-        const unsigned kPs = 8u * iq - (unsigned)(RP + S::CS), kPs1 = kPs + (unsigned)RP, kPs2 = kPs1 + (unsigned)RP;
+        const bool stencil_wave = wave < 6;
+        const int cw = wave & 1;
         const unsigned kCi = sp.l_cinfo + 8u * (unsigned)n;
         const unsigned kRg = sp.l_ring + (unsigned)n;
         // the thread's (at most two, nhalo <= 64) 16-byte wrap-halo chunks: board-relative source
@@ -495,9 +450,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
         };
 
         int i = 0;
-        int cbS = 0;         // cinfo index of the stencil tile's first cell: (16 i) mod RH
-        int cbU = RH - 48;   // the same for the update tile i-3: (16 (i-3)) mod RH, RH >= 80
-        int rbU = RING - 48; // ring slot of the update tile's first cell: (16 (i-3)) mod RING
         // unit (board ur, step us) ends at stream position uend; batch nb is drawn when the update
         // stage has passed position dpos = (nb - 1) NB RH
         const bool unit_events = a.padding == 2 || !batched;
@@ -505,8 +457,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
         int ev_unit = unit_events ? (uend >> 4) + 4 : 0x7fffffff;
         int nb = 2, dpos = NB * RH;
         int ev_batch = (batched && 2 * NB < a.n_steps) ? (dpos >> 4) + 4 : 0x7fffffff;
-        unsigned cis = cinfo[n].x, cis_n = 0;
-        uint2 ciu = make_uint2(0u, 0u), ciu_n = ciu;
 
         // the end-of-step work reads the call's parameters from the LDS copy, so that they do not
         // occupy scalar registers through the loop
@@ -530,196 +480,233 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                 ev_batch = nb * NB < ea.n_steps ? (dpos >> 4) + 4 : 0x7fffffff;
             }
         };
-        // st: stencil of tile i -> Z[i & 1]; up: fc2 + update of tile i-3 (H[(i-3) & 1]). The
-        // issue order is fixed by scheduling fences: all loads first (the H operands before the
-        // taps), then the stencil's permutes with the fc2 chain, the stencil's MFMAs, the update,
-        // the stores.
-#ifndef NCA_CH_ORDER
-#define NCA_CH_ORDER 2
-#endif
-#ifndef NCA_FENCE
-#define NCA_FENCE() __builtin_amdgcn_sched_barrier(0)
-#endif
-        auto cinterval = [&](auto st_c, auto up_c, auto par_v, auto last_c) __attribute__((always_inline)) {
-            constexpr bool DST = decltype(st_c)::value, DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
-            const unsigned PAR = par_v;
-            uint2 nbv[9];
-            bf16x8 hb[S::KT2];
-            float4 m4;
-            float fu = 0.0f;
-            unsigned madr = 0, padr = 0, gvm = 0;
-            // the taps are single ds_read_b64: paired into ds_read2_b64 (neighbouring cells of one
-            // row) they hit bank conflicts and cost more than two single loads on gfx950
-            auto load_taps = [&]() __attribute__((always_inline)) {
-                if (DST) {
+        if (stencil_wave) {
+            // stencil B operands: column j = lane % 4 is kernel j; taps 0-3, 4-7; tap 8 placed at
+            // the k slot of channel c % 4 (the A operand of tap 8 is 4 channels' tap-8 values)
+            s16x4 kb0, kb1, kb2[4];
+            {
+                const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
+                const int j = lane & 3;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    kb0[k] = bf16_bits(kern[j * 9 + k]);
+                    kb1[k] = bf16_bits(kern[j * 9 + 4 + k]);
+                }
+                const short k8 = bf16_bits(kern[j * 9 + 8]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) kb2[c][k] = k == c ? k8 : (short)0;
+            }
+            // lane (cell n, channel octet oc = 4 cw + g): taps of channels 8 oc .. 8 oc + 7, one
+            // 16-byte load each. Output lane (block b, kernel j) holds rows r (cells 4 (b & 3) + r)
+            // of octet 4 cw + b / 4: Z quads 2 oc and 2 oc + 1.
+            const int oc = 4 * cw + g;
+            unsigned kZw0, kZw1;
+            {
+                const int j = lane & 3, b = lane >> 2, ob = 4 * cw + (b >> 2), sw = 2 * (b & 3);
+                const unsigned base = sp.l_Z + (unsigned)(4 * (b & 3)) * S::ZS + 8u * (unsigned)(j & 1);
+                kZw0 = base + 16u * (unsigned)((2 * (2 * ob) + (j >> 1)) ^ sw);
+                kZw1 = base + 16u * (unsigned)((2 * (2 * ob + 1) + (j >> 1)) ^ sw);
+            }
+            // + centre: the top-left tap, the left taps of the middle and bottom rows
+            const unsigned kPs = 16u * (unsigned)oc - (unsigned)(RP + S::CS), kPs1 = kPs + (unsigned)RP,
+                           kPs2 = kPs1 + (unsigned)RP;
+            int cbS = 0;  // cinfo index of the stencil tile's first cell: (16 i) mod RH
+            unsigned cis = cinfo[n].x, cis_n = 0;
+            auto sinterval = [&](auto par_c) __attribute__((always_inline)) {
+                constexpr unsigned PAR = decltype(par_c)::value;
+                uint4 t[9];
+                {
                     const unsigned r0 = cis + kPs, r1 = cis + kPs1, r2 = cis + kPs2;
-                    nbv[0] = lds_ld64(smem, r0);
-                    nbv[3] = lds_ld64(smem, r1);
-                    nbv[6] = lds_ld64(smem, r2);
-                    __builtin_amdgcn_sched_barrier(0);
-                    nbv[1] = lds_ld64(smem, r0 + S::CS);
-                    nbv[4] = lds_ld64(smem, r1 + S::CS);
-                    nbv[7] = lds_ld64(smem, r2 + S::CS);
-                    __builtin_amdgcn_sched_barrier(0);
-                    nbv[2] = lds_ld64(smem, r0 + 2 * S::CS);
-                    nbv[5] = lds_ld64(smem, r1 + 2 * S::CS);
-                    nbv[8] = lds_ld64(smem, r2 + 2 * S::CS);
+                    t[0] = *reinterpret_cast<const uint4 *>(smem + r0);
+                    t[3] = *reinterpret_cast<const uint4 *>(smem + r1);
+                    t[6] = *reinterpret_cast<const uint4 *>(smem + r2);
+                    t[1] = *reinterpret_cast<const uint4 *>(smem + r0 + S::CS);
+                    t[4] = *reinterpret_cast<const uint4 *>(smem + r1 + S::CS);
+                    t[7] = *reinterpret_cast<const uint4 *>(smem + r2 + S::CS);
+                    t[2] = *reinterpret_cast<const uint4 *>(smem + r0 + 2 * S::CS);
+                    t[5] = *reinterpret_cast<const uint4 *>(smem + r1 + 2 * S::CS);
+                    t[8] = *reinterpret_cast<const uint4 *>(smem + r2 + 2 * S::CS);
+                    int cs = cbS + 16;
+                    if (cs >= RH) cs -= RH;
+                    cis_n = lds_ld64(smem, kCi + 8u * (unsigned)cs).x;
+                }
+                auto word = [&](const uint4 &v, int c) -> uint32_t {
+                    const int w = c >> 1;
+                    return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
+                };
+                // channels 4 h .. 4 h + 3 of the octet: A operands (channel c, taps 0-3 / 4-7 as
+                // packed bf16 pairs), 3 MFMAs each, then the quad's Z stores
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    f32x4 zc[4];
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) {
+                        const int c = 4 * h + cc;
+                        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                        const s16x4 sa0 = __builtin_bit_cast(
+                            s16x4, make_uint2(__builtin_amdgcn_perm(word(t[1], c), word(t[0], c), sel),
+                                              __builtin_amdgcn_perm(word(t[3], c), word(t[2], c), sel)));
+                        const s16x4 sa1 = __builtin_bit_cast(
+                            s16x4, make_uint2(__builtin_amdgcn_perm(word(t[5], c), word(t[4], c), sel),
+                                              __builtin_amdgcn_perm(word(t[7], c), word(t[6], c), sel)));
+                        const s16x4 a2 = __builtin_bit_cast(s16x4, h ? make_uint2(t[8].z, t[8].w) : make_uint2(t[8].x, t[8].y));
+                        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+                        d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0, kb0, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1, kb1, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[cc], d, 0, 0, 0);
+                        zc[cc] = d;
+                    }
+                    const unsigned kz = (h ? kZw1 : kZw0) + PAR * S::ZBUF;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        uint2 o;
+                        o.x = cvt_pk_bf16(zc[0][r], zc[1][r]);
+                        o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
+                        lds_st64(smem, kz + (unsigned)r * S::ZS, o);
+                    }
                 }
             };
-            auto load_h = [&]() __attribute__((always_inline)) {
+            auto advance = [&]() __attribute__((always_inline)) {
+                ++i;
+                cbS += 16;
+                if (cbS >= RH) cbS -= RH;
+                cis = cis_n;
+            };
+            while (i + 1 < T) {
+                sinterval(P0{});
+                events();
+                advance();
+                __syncthreads();
+                sinterval(P1{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            if (i < T) {
+                sinterval(P0{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            // drain: intervals T .. T+2 have no stencil work
+            for (int k = 0; k < 3; ++k) {
+                events();
+                ++i;
+                __syncthreads();
+            }
+        } else {
+            // fc2 of m-tiles 2 cw and 2 cw + 1 (W2 fragments in AGPRs) and the update of their
+            // channels: lane (cell n, g) holds quads iq0 = 8 cw + g and iq1 = iq0 + 4
+            const int iq0 = 8 * cw + g, iq1 = iq0 + 4;
+            bf16x8 w2f[2][S::KT2];
+            f32x4 b2v[2];
+            {
+                const bf16x8 *w2 = reinterpret_cast<const bf16x8 *>(a.packed + sp.off_w2h);
+                const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+                    for (int kt = 0; kt < S::KT2; ++kt) w2f[mt][kt] = w2[((2 * cw + mt) * S::KT2 + kt) * 64 + lane];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) b2v[mt][v] = b2[4 * (mt ? iq1 : iq0) + v];
+                }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int kt = 0; kt < S::KT2; ++kt) asm volatile("" : "+a"(w2f[mt][kt]));
+            }
+            // all ones where the lane's channel 4 iq + v lies in the clamped input slice
+            unsigned imv[2][4];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int c = 4 * (mt ? iq1 : iq0) + v;
+                    imv[mt][v] = (c >= a.in_off && c < a.in_off + a.c_in) ? 0xffffffffu : 0u;
+                    asm volatile("" : "+v"(imv[mt][v]));  // kept a plain VGPR mask
+                }
+            const unsigned hx = (unsigned)((n >> 2) & 1);
+            const unsigned kHr = sp.l_H + (unsigned)n * S::HS + 16u * ((unsigned)g ^ hx);
+            int cbU = RH - 48;    // cinfo index of the update tile's first cell: (16 (i-3)) mod RH
+            int rbU = RING - 48;  // its ring slot: (16 (i-3)) mod RING
+            uint2 ciu = make_uint2(0u, 0u), ciu_n = ciu;
+            auto uinterval = [&](auto up_c, auto last_c) __attribute__((always_inline)) {
+                constexpr bool DUP = decltype(up_c)::value, LAST = decltype(last_c)::value;
+                const unsigned PAR = (unsigned)(i & 1);
+                bf16x8 hb[S::KT2];
+                float4 m4[2];
+                unsigned madr = 0, padr = 0, gvm = 0;
+                float fu = 0.0f;
                 if (DUP) {
 #pragma unroll
                     for (int kt = 0; kt < S::KT2; ++kt)
                         hb[kt] = *reinterpret_cast<const bf16x8 *>(smem + kHr + (PAR ^ 1u) * S::HBUF + 64u * kt);
-                    madr = (ciu.y & 0x7fffffffu) + 16u * iq;
-                    m4 = lds_ld128f(smem, madr);
+                    madr = (ciu.y & 0x7fffffffu) + 16u * (unsigned)iq0;
+                    m4[0] = lds_ld128f(smem, madr);
+                    m4[1] = lds_ld128f(smem, madr + 64u);
                     fu = (float)smem[kRg + (unsigned)rbU];
                     gvm = (unsigned)((int)ciu.y >> 31);  // all ones for a given cell
-                    padr = ciu.x + 8u * iq;
+                    padr = ciu.x + 8u * (unsigned)iq0;
                 }
-            };
-            if (NCA_CH_ORDER == 1) {
-                load_taps();
-                load_h();
-            } else {
-                load_h();
-                load_taps();
-            }
-            {  // next interval's table entries (the tables never change)
-                int cs = cbS + 16, cu = cbU + 16;
-                if (cs >= RH) cs -= RH;
-                if (cu >= RH) cu -= RH;
-                cis_n = lds_ld64(smem, kCi + 8u * (unsigned)cs).x;
-                ciu_n = lds_ld64(smem, kCi + 8u * (unsigned)cu);
-            }
-            NCA_FENCE();
-            s16x4 sa0[4], sa1[4];
-            auto perms = [&](int c) __attribute__((always_inline)) {
-                const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t p01 = __builtin_amdgcn_perm(c < 2 ? nbv[1].x : nbv[1].y, c < 2 ? nbv[0].x : nbv[0].y, sel);
-                const uint32_t p23 = __builtin_amdgcn_perm(c < 2 ? nbv[3].x : nbv[3].y, c < 2 ? nbv[2].x : nbv[2].y, sel);
-                const uint32_t p45 = __builtin_amdgcn_perm(c < 2 ? nbv[5].x : nbv[5].y, c < 2 ? nbv[4].x : nbv[4].y, sel);
-                const uint32_t p67 = __builtin_amdgcn_perm(c < 2 ? nbv[7].x : nbv[7].y, c < 2 ? nbv[6].x : nbv[6].y, sel);
-                sa0[c] = __builtin_bit_cast(s16x4, make_uint2(p01, p23));
-                sa1[c] = __builtin_bit_cast(s16x4, make_uint2(p45, p67));
-            };
-            f32x4 acc2 = b2v;
-            auto fc2_k = [&](int k) __attribute__((always_inline)) {
-                if (DUP) acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[k], hb[k], acc2, 0, 0, 0);
-            };
-            f32x4 zc[4];
-            const s16x4 a2 = __builtin_bit_cast(s16x4, nbv[8]);
-            // two channels' MFMA chains interleaved
-            auto stencil2 = [&](int c0) __attribute__((always_inline)) {
-                f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
-                d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0], kb0, d0, 0, 0, 0);
-                d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0[c0 + 1], kb0, d1, 0, 0, 0);
-                d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1[c0], kb1, d0, 0, 0, 0);
-                d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1[c0 + 1], kb1, d1, 0, 0, 0);
-                d0 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0], d0, 0, 0, 0);
-                d1 = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kb2[c0 + 1], d1, 0, 0, 0);
-                zc[c0] = d0;
-                zc[c0 + 1] = d1;
-            };
-            if (DST) {
-                perms(0);
-                perms(1);
-            }
-            fc2_k(0);
-            fc2_k(1);
-            NCA_FENCE();
-            if (DST) {
-                perms(2);
-                perms(3);
-                stencil2(0);
-            }
-            fc2_k(2);
-            fc2_k(3);
-            NCA_FENCE();
-            if (DST) stencil2(2);
-            fc2_k(4);
-            fc2_k(5);
-            NCA_FENCE();
-            if (DST) {
+                {  // next interval's table entry (the tables never change)
+                    int cu = cbU + 16;
+                    if (cu >= RH) cu -= RH;
+                    ciu_n = lds_ld64(smem, kCi + 8u * (unsigned)cu);
+                }
+                if (!DUP) return;
+                f32x4 acc[2] = {b2v[0], b2v[1]};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    uint2 o;
-                    o.x = cvt_pk_bf16(zc[0][r], zc[1][r]);
-                    o.y = cvt_pk_bf16(zc[2][r], zc[3][r]);
-                    lds_st64(smem, kZw + PAR * S::ZBUF + (unsigned)r * S::ZS, o);
-                }
-            }
-            fc2_k(6);
-            fc2_k(7);
-            NCA_FENCE();
-            if (DUP) {
-                const uint32_t d01 = cvt_pk_bf16(acc2[0], acc2[1]), d23 = cvt_pk_bf16(acc2[2], acc2[3]);
-                const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
-                const float xo[4] = {m4.x, m4.y, m4.z, m4.w};
-                float u[4];
+                for (int kt = 0; kt < S::KT2; ++kt)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
-                    const unsigned km = imv[v] & gvm;                     // clamped: keep x
-                    u[v] = __uint_as_float((km & __float_as_uint(xo[v])) | (~km & __float_as_uint(uv)));
-                }
+                    for (int mt = 0; mt < 2; ++mt)
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[mt][kt], hb[kt], acc[mt], 0, 0, 0);
                 bool ok = true;
                 if (LAST) ok = 16 * (i - 3) + n < total;
-                if (ok) {
-                    lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
-                    lds_st64(smem, padr, make_uint2(cvt_pk_bf16(u[0], u[1]), cvt_pk_bf16(u[2], u[3])));
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const uint32_t d01 = cvt_pk_bf16(acc[mt][0], acc[mt][1]), d23 = cvt_pk_bf16(acc[mt][2], acc[mt][3]);
+                    const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
+                    const float xo[4] = {m4[mt].x, m4[mt].y, m4[mt].z, m4[mt].w};
+                    float u[4];
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float uv = __builtin_fmaf(fu, dx[v], xo[v]);  // fu in {0, 1}: exact
+                        const unsigned km = imv[mt][v] & gvm;                 // clamped: keep x
+                        u[v] = __uint_as_float((km & __float_as_uint(xo[v])) | (~km & __float_as_uint(uv)));
+                    }
+                    if (ok) {
+                        lds_st128f(smem, madr + 64u * mt, make_float4(u[0], u[1], u[2], u[3]));
+                        lds_st64(smem, padr + 32u * mt, make_uint2(cvt_pk_bf16(u[0], u[1]), cvt_pk_bf16(u[2], u[3])));
+                    }
                 }
+            };
+            auto advance = [&]() __attribute__((always_inline)) {
+                ++i;
+                cbU += 16;
+                if (cbU >= RH) cbU -= RH;
+                rbU += 16;
+                if (rbU >= RING) rbU -= RING;
+                ciu = ciu_n;
+            };
+            while (i < 3) {
+                uinterval(F_{}, F_{});
+                events();
+                advance();
+                __syncthreads();
             }
-        };
-        auto advance = [&]() __attribute__((always_inline)) {
-            ++i;
-            cbS += 16;
-            if (cbS >= RH) cbS -= RH;
-            cbU += 16;
-            if (cbU >= RH) cbU -= RH;
-            rbU += 16;
-            if (rbU >= RING) rbU -= RING;
-            cis = cis_n;
-            ciu = ciu_n;
-        };
-        cinterval(T_{}, F_{}, P0{}, F_{});
-        events();
-        advance();
-        __syncthreads();
-        cinterval(T_{}, F_{}, P1{}, F_{});
-        events();
-        advance();
-        __syncthreads();
-        cinterval(T_{}, F_{}, P0{}, F_{});
-        events();
-        advance();
-        __syncthreads();
-        while (i + 1 < T) {
-            cinterval(T_{}, T_{}, P1{}, F_{});
-            events();
-            advance();
-            __syncthreads();
-            cinterval(T_{}, T_{}, P0{}, F_{});
+            while (i < T + 2) {
+                uinterval(T_{}, F_{});
+                events();
+                advance();
+                __syncthreads();
+            }
+            uinterval(T_{}, T_{});
             events();
             advance();
             __syncthreads();
         }
-        if (i < T) {
-            cinterval(T_{}, T_{}, P1{}, F_{});
-            events();
-            advance();
-            __syncthreads();
-        }
-        cinterval(F_{}, T_{}, (unsigned)(i & 1), F_{});
-        events();
-        advance();
-        __syncthreads();
-        cinterval(F_{}, T_{}, (unsigned)(i & 1), F_{});
-        events();
-        advance();
-        __syncthreads();
-        cinterval(F_{}, T_{}, (unsigned)(i & 1), T_{});
-        __syncthreads();
     }
 
     // ---- write back
