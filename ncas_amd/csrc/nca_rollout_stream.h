@@ -12,22 +12,24 @@
 //                          h = W1 z + b1 on v_mfma_f32_16x16x32_bf16 (B operand from Z), then
 //                          bf16 rounding + ReLU (autocast rounds fc1's output before the ReLU)
 //                          into H.
-//   channel wave w (4-7)   owns channels [16(w-4), 16(w-4)+16): the 3x3 perception of its
-//                          channels on v_mfma_f32_4x4x4_16b_bf16 (lane (cell n, channel quad iq)
-//                          reads the 9 taps of its 4 channels from the perception buffer P; each
-//                          4-lane block multiplies 4 cells' tap vectors by the 4 kernels) into Z;
-//                          fc2 dx = W2 h + b2 for its 16 output channels (W2 fragments in AGPRs, B
-//                          operand from H), whose accumulator layout puts channels 4 iq .. 4 iq+3 of
-//                          cell n in lane (n, g): the update x += fire * bf16(dx) into the fp32
-//                          state M and the bf16 buffer P happens in those registers; the clamped
-//                          input channels of given cells keep their value. Channel waves also do
-//                          the end-of-step work (wrap halo refresh, fire masks).
+//   stencil wave (4, 5)    channels [32(w-4), 32(w-4)+32): the 3x3 perception on
+//                          v_mfma_f32_4x4x4_16b_bf16. Lane (cell n, channel octet) reads the 9
+//                          taps of its 8 channels from the perception buffer P, one 16-byte load
+//                          each; each 4-lane block multiplies 4 cells' tap vectors by the 4
+//                          kernels -> Z.
+//   update wave (6, 7)     channels [32(w-6), 32(w-6)+32): fc2 dx = W2 h + b2 for two 16-channel
+//                          m-tiles (W2 fragments in AGPRs, one read of H as the B operand of
+//                          both), whose accumulator layout puts channels 4 iq .. 4 iq+3 of cell n
+//                          in lane (n, g): the update x += fire * bf16(dx) into the fp32 state M
+//                          and the bf16 buffer P happens in those registers; the clamped input
+//                          channels of given cells keep their value.
+// The four channel waves also share the end-of-step work (wrap halo refresh, fire masks).
 //
 // Interval i (one workgroup barrier) runs: stencil of tile i (-> Z[i & 1]); fc1 + epilogue of
-// tile i-2 (-> H[i & 1]) from Z operands the hidden wave loaded into registers at the end of
-// interval i-1, after which it loads those of tile i-1 from Z[(i-1) & 1]; fc2 + update of tile
-// i-3 (from H[(i-1) & 1]). A hidden wave thus opens every interval with 32 MFMAs whose operands
-// are already in registers.
+// tile i-2 (-> H[i & 1]) from Z operands the hidden wave loaded into registers in interval i-1,
+// while it loads those of tile i-1 from Z[(i-1) & 1]; fc2 + update of tile i-3 (from
+// H[(i-1) & 1]). A hidden wave thus opens every interval with 32 MFMAs whose operands are
+// already in registers.
 //
 // P is single-buffered: the update of tile i-3 runs in the same interval as the stencil of tile
 // i, whose neighbourhoods reach W+1 <= 16 positions back, never into tile i-3. A board's next
@@ -350,20 +352,30 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
         const unsigned hx = (unsigned)((n >> 2) & 1);
         const unsigned kHw0 = sp.l_H + (unsigned)n * S::HS + 128u * (unsigned)ws + 32u * (unsigned)g + 16u * hx;
         const unsigned kHw1 = kHw0 + 16u - 32u * hx;
-        // Z operands of a tile, loaded in the interval before its fc1 runs; requested at the end
-        // of the interval (once the MFMAs that read the previous ones are issued), when the other
-        // waves' loads of the interval are done
-        bf16x8 zq[S::KT1];
+        bf16x8 zqb[2][S::KT1];
 #pragma unroll
-        for (int k = 0; k < S::KT1; ++k)
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) zq[k][e] = (__bf16)0.0f;
-        // fcb: fc1 of tile i-2 from zq (all 32 MFMAs from registers, m-tile by m-tile) and its
-        // epilogue -> H[i & 1], each half stored as soon as its two m-tiles are done; fca: the Z
-        // operands of tile i-1
+            for (int k = 0; k < S::KT1; ++k)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) zqb[q][k][e] = (__bf16)0.0f;
+        // fcb: fc1 of tile i-2 (32 MFMAs from registers, m-tile by m-tile) and its epilogue ->
+        // H[i & 1], each half stored as soon as its two m-tiles are done; fca: the Z operands of
+        // tile i-1 into zqb[i & 1], requested after the first m-tile, once the channel waves' loads
+        // that open the interval are served (fc1 of tile i-2 reads zqb[(i-1) & 1])
         auto hinterval = [&](auto fca_c, auto fcb_c, auto par_c) __attribute__((always_inline)) {
             constexpr bool FCA = decltype(fca_c)::value, FCB = decltype(fcb_c)::value;
             constexpr unsigned PAR = decltype(par_c)::value;
+            auto loadz = [&]() __attribute__((always_inline)) {
+                if (FCA) {
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int kt = 0; kt < S::KT1; ++kt)
+                        zqb[PAR][kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
+                                                                   64u * kt);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            };
             if (FCB) {
                 f32x4 acc[S::MT1];
 #pragma unroll
@@ -371,7 +383,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                     acc[mt] = b1v[mt];
 #pragma unroll
                     for (int kt = 0; kt < S::KT1; ++kt)
-                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zq[kt], acc[mt], 0, 0, 0);
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zqb[PAR ^ 1u][kt], acc[mt], 0, 0, 0);
                     if (mt & 1) {
                         uint4 hv;
                         hv.x = relu_bf16x2(cvt_pk_bf16(acc[mt - 1][0], acc[mt - 1][1]));
@@ -380,13 +392,10 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                         hv.w = relu_bf16x2(cvt_pk_bf16(acc[mt][2], acc[mt][3]));
                         lds_st128(smem, (mt == 1 ? kHw0 : kHw1) + PAR * S::HBUF, hv);
                     }
+                    if (mt == 0) loadz();
                 }
-            }
-            if (FCA) {
-#pragma unroll
-                for (int kt = 0; kt < S::KT1; ++kt)
-                    zq[kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
-                                                               64u * kt);
+            } else {
+                loadz();
             }
         };
         int i = 0;
