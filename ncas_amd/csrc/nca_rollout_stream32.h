@@ -25,9 +25,8 @@
 //   update wave (6, 7)     cells 8(w-6) .. 8(w-6)+7 of a tile, all quads: dx = bf16(b2 + the four
 //                          partial sums in a fixed order), x += fire dx into M; the clamped input
 //                          channels of given cells keep their value. With confidence-gated firing
-//                          the lanes of the output quad decide the cell's fire mask from its state
-//                          at the start of the step (M before the update) and pass it on to the
-//                          cell's other 7 lanes.
+//                          each of the cell's 8 lanes reads the output quad of its state at the
+//                          start of the step (M before the update) and makes the same decision.
 // Interval i (one workgroup barrier): stencil of tile i -> Z[i & 1]; fc1 + fc2 partials of tile
 // i-2 -> D[i & 1], while the Z operands of tile i-1 load from Z[(i-1) & 1] into registers for the
 // next interval; update of tile i-3 from D[(i-1) & 1]. The stencil waves likewise load the next
@@ -385,9 +384,9 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 ev_draw = ((sd * HWn) >> 4) + 3;
             }
         };
-        // gated firing: the update lanes of the output quad decide a cell's mask for the step from
-        // its state at the step's start (M before the update) and pass it to the cell's other
-        // lanes; the head (at most 4 outputs over at most 4 channels) is held in registers
+        // gated firing: the update lanes decide a cell's mask for the step from its state at the
+        // step's start (the output quad of M before the update, read by all 8 lanes of the cell);
+        // the head (at most 4 outputs over at most 4 channels) is held in registers
         const int oqi = a.out_off >> 2;
         const bool oq = GATED && q8 == oqi;
         float hw4[4][4], hb4[4];
@@ -575,30 +574,34 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                     xu_n = cinfo[cu + cl];
                 }
                 if (!DUP) return;
-                float4 pd[4];
-#pragma unroll
-                for (int p = 0; p < 4; ++p) pd[p] = lds_ld128f(smem, kDr + (PAR ^ 1u) * S::DBUF + (unsigned)p * S::DPART);
+                // the state loads first: with gated firing the decision is made while the partial
+                // sums are in flight
                 const unsigned madr = kM + xu * S::MS;
                 const float4 m4 = lds_ld128f(smem, madr);
                 const unsigned fb = ring[rbU + cl];
+                float4 mo4;
+                if (GATED) mo4 = lds_ld128f(smem, madr + 16u * (unsigned)(oqi - q8));  // the output quad
+                float4 pd[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) pd[p] = lds_ld128f(smem, kDr + (PAR ^ 1u) * S::DBUF + (unsigned)p * S::DPART);
                 // the cell's step and board cell
                 const bool nxt = cbU + cl >= HWn;
                 const int sc = usU + (nxt ? 1 : 0);
                 const int qc = cbU + cl - (nxt ? HWn : 0);
+                unsigned fbit = fb & 1u;
+                if (GATED) {
+                    // every lane of the cell makes the same decision from the same values
+                    const float xq[4] = {mo4.x, mo4.y, mo4.z, mo4.w};
+                    const unsigned f = gated_fire(xq, fb) ? 1u : 0u;
+                    fbit = f;
+                    if (oq && (!LAST || 16 * (i - 3) + cl < total)) fired_dec += (int)f;
+                }
                 float ds[4];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) ds[v] = (((b2v[v] + pd[0][v]) + pd[1][v]) + pd[2][v]) + pd[3][v];
                 const uint32_t d01 = cvt_pk_bf16(ds[0], ds[1]), d23 = cvt_pk_bf16(ds[2], ds[3]);
                 const float dx[4] = {bf16_lo(d01), bf16_hi(d01), bf16_lo(d23), bf16_hi(d23)};
                 float xo[4] = {m4.x, m4.y, m4.z, m4.w};
-                unsigned fbit = fb & 1u;
-                if (GATED) {
-                    int f = 0;
-                    if (oq) f = gated_fire(xo, fb) ? 1 : 0;
-                    f = __shfl(f, (lane & ~7) | oqi);  // the cell's 8 lanes take the decision
-                    fbit = (unsigned)f;
-                    if (oq && (!LAST || 16 * (i - 3) + cl < total)) fired_dec += f;
-                }
                 const float fu = (float)fbit;
                 const unsigned gvm = (fb & 0x80u) ? 0xffffffffu : 0u;
                 float xk[4] = {xo[0], xo[1], xo[2], xo[3]};
