@@ -42,9 +42,9 @@
 // start, so that a tile's 16 bytes are contiguous): bit 0 fire, bit 1 (u < p_low) for gated
 // firing, bit 7 the cell's given flag. The channel waves draw the Philox uniforms of a whole step
 // two steps ahead (one evaluation per 4 cells); with gating the update chooses between the two
-// threshold bits. The decision needs only
-// conf > tau: for a 2-output mlp head that is s < conf_s on the sum of exponentials s (one
-// exponential, no division), with conf_s found on the host with the readout's own division.
+// threshold bits. The decision needs only conf > tau: for a 2-output mlp head that is s < conf_s
+// on the sum of exponentials s (one exponential, no division), with conf_s found on the host with
+// the readout's own division.
 //
 // Clamp (model.py:430-438): the first step's perception reads the caller's state and every step's
 // output holds the clamp values in the input slice of given cells. M starts as the caller's state;
@@ -121,7 +121,6 @@ struct St32Params {
     unsigned off_w1q, off_w2k;
 };
 
-
 // zsw: the Z row swizzle (a permutation of 0..15)
 __device__ __forceinline__ unsigned zsw(unsigned r) { return (r & 8u) | ((r & 3u) << 1) | ((r >> 2) & 1u); }
 
@@ -192,7 +191,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     __syncthreads();
 
     // ---- fire masks of step s for all cells (channel waves, thread tb of 256): the fire bit, or
-    // for gated firing both threshold bits (the stencil decides between them)
+    // for gated firing both threshold bits (the update decides between them)
     auto ring_put = [&](int s, int q, unsigned v) __attribute__((always_inline)) {
         const int o = (s % S::NSLOT) * HWn + q;
         ring[o] = (unsigned char)v;
