@@ -9,15 +9,20 @@
 //              mlp head's logits, reference src/nca/train.py:183-207, weighted as in
 //              src/nca/engine/step.py:243-245 and normalised as in engine.py:490), plus the
 //              gradient arriving from the next step; the clamp's backward zeroes the input
-//              slice of given cells (ops.py:276-294): g_u; the fire mask gives g_dx = g_u * fire
+//              slice of given cells (ops.py:276-294): g_u; the fire mask gives g_dx = g_u * fire;
+//              partial sums of db2, the head's gradients and the loss
 //   stencil_z  z = perception of the saved state (feature-major, F x cells)
-//   GEMMs      h = relu(W1 z + b1); g_a = (W2^T g_dx) * [h > 0]; g_z = W1^T g_a  (fp32 MFMA)
-//   stencil_t  g_x = g_u + the transposed stencil of g_z (padding-aware: wall / zero halos take
-//              no gradient, wrap halos give it to the wrapped cell), the next step's gradient
-//   partials   dW1 = g_a z^T, dW2 = g_dx h^T, db1, db2, dkernels, dhead: split-K partial sums over
-//              256 fixed cell ranges, added into one accumulator per step in a fixed order
+//   MLP        h = relu(W1 z + b1); g_a = (W2^T g_dx) * [h > 0]; g_z = W1^T g_a: bf16 cells with
+//              32 channels and 256 hidden units in one fused kernel (mlp_back32, which also sums
+//              dW1, dW2 and db1), other cells on fp32 MFMA GEMMs
+//   stencil_back  g_x = g_u + the transposed stencil of g_z (padding-aware: wall / zero halos
+//              take no gradient, wrap halos give it to the wrapped cell), the next step's
+//              gradient, and partial sums of the kernel-weight gradient
+//   partials   dW1 = g_a z^T, dW2 = g_dx h^T (split-K GEMMs), db1 (row sums of g_a), unless fused
 //
-// so the gradients are deterministic (the same bits on every run). Gradients are the exact fp32
+// Every partial sum belongs to one of 256 fixed cell ranges (slots); each step adds its sums
+// into the slots, and one kernel adds the slots up in slot order after the last step, so the
+// gradients are deterministic (the same bits on every run). Gradients are the exact fp32
 // gradients of the forward as computed: for bf16 cells the rounding points are straight-through
 // (derivative 1), and the backward uses the forward's bf16-rounded weights and inputs.
 #include <hip/hip_runtime.h>
@@ -27,6 +32,7 @@
 #include <string.h>
 
 #include "nca_hip.h"
+#include "nca_bptt_mlp.h"
 #include "nca_device.h"
 #include "nca_layout.h"
 #include "nca_status.h"
@@ -69,13 +75,15 @@ ParamLayout param_layout(const Dims &d) {
     return L;
 }
 
-// Workspace (floats, 64-float aligned pieces).
+// Workspace (floats, 64-float aligned pieces). part holds kSplit slots of P partial sums
+// each (slot s: the cells of range s), added to by every step of the chunk and reduced once at
+// the end; lossacc holds the loss's kSplit slots.
 struct WsLayout {
-    int64_t Z, Hb, Ga, Gz, Gdx, GL, Gu, Gx0, Gx1, part, acc, lossp, denom, total;
-    int front_blocks;
+    int64_t Z, Hb, Ga, Gz, Gdx, Gu, Gx0, Gx1, part, acc, lossacc, denom, total;
 };
 
 WsLayout ws_layout(const Dims &d, int n) {
+    (void)n;
     const ParamLayout P = param_layout(d);
     auto al = [](int64_t v) { return (v + 63) & ~(int64_t)63; };
     WsLayout L;
@@ -90,8 +98,6 @@ WsLayout ws_layout(const Dims &d, int n) {
     o = al(o + (int64_t)d.F * d.M);
     L.Gdx = o;
     o = al(o + (int64_t)d.C * d.M);
-    L.GL = o;
-    o = al(o + (int64_t)d.n_out * d.M);
     L.Gu = o;
     o = al(o + (int64_t)d.C * d.M);
     L.Gx0 = o;
@@ -102,9 +108,8 @@ WsLayout ws_layout(const Dims &d, int n) {
     o = al(o + (int64_t)kSplit * P.P);
     L.acc = o;
     o = al(o + P.P);
-    L.front_blocks = (int)((d.M + kThreads - 1) / kThreads);
-    L.lossp = o;
-    o = al(o + (int64_t)(n > 0 ? n : 1) * L.front_blocks);
+    L.lossacc = o;
+    o = al(o + kSplit);
     L.denom = o;
     o = al(o + 1);
     L.total = o;
@@ -132,6 +137,31 @@ __device__ float block_sum(float v, float *red) {
         __syncthreads();
     }
     const float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+// Block-wide sums of N floats per thread over a block of WAVES waves: each wave folds its lanes
+// with a fixed xor butterfly (both partners of an exchange add the same two values, so every
+// lane ends with the same bits), then thread i < N adds the waves' totals in wave order.
+// Returns the block total of v[i] in thread i (0 in threads >= N); red holds WAVES * N floats.
+template <int N, int WAVES>
+__device__ float block_sums(const float (&v)[N], float *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        float x = v[i];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x = __fadd_rn(x, __shfl_xor(x, o));
+        if (lane == 0) red[wave * N + i] = x;
+    }
+    __syncthreads();
+    float r = 0.0f;
+    if (threadIdx.x < N) {
+        r = red[threadIdx.x];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) r = __fadd_rn(r, red[w * N + threadIdx.x]);
+    }
     __syncthreads();
     return r;
 }
@@ -167,17 +197,68 @@ struct FrontArgs {
     int64_t row0;
     uint32_t step;
     float p;
-    float *Gu, *Gdx, *GL, *lossp;
+    float *Gu, *Gdx;
+    float *part, *lossacc;  // partial-sum slots (db2, dhead) and the loss's slots
+    int64_t P, offB2, offHW, offHB;
 };
 
-__global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
-    __shared__ float red[kThreads];
+// The cross-entropy gradient of the mlp head's logits at cell m (gl[v] = d loss / d logit v,
+// times the step's scale; 0 for v >= n_out, and everywhere on a step without a loss term) and
+// the cell's loss term (reference src/nca/train.py:183-207). x1c is channel 0 of the cell in the
+// step's output state.
+__device__ __forceinline__ float head_grad(const FrontArgs &a, int m, const float *x1c, float gl[16]) {
     const Dims &d = a.d;
-    const int64_t m = blockIdx.x * (int64_t)kThreads + threadIdx.x;
-    float lossc = 0.0f;
-    if (m < d.M) {
-        const int64_t row = m / d.HW;
-        const int q = (int)(m - row * d.HW);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) gl[v] = 0.0f;
+    if (a.wscale == 0.0f) return 0.0f;
+    const float scale = a.mask ? a.wscale * a.mask[m] / *a.denom : a.wscale;
+    float l[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        l[v] = 0.0f;
+        if (v < d.n_out) {
+            float acc = a.head_b[v];
+            for (int c = 0; c < d.c_out; ++c)
+                acc = __builtin_fmaf(a.head_w[v * d.c_out + c], x1c[(int64_t)(d.out_off + c) * d.HW], acc);
+            l[v] = acc;
+            mx = fmaxf(mx, acc);
+        }
+    }
+    float s = 0.0f, lt = mx;
+    const int tgt = a.targets[m];
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        if (v < d.n_out) {
+            s += expf(l[v] - mx);
+            if (v == tgt) lt = l[v];
+        }
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+        if (v < d.n_out) gl[v] = (expf(l[v] - mx) / s - (v == tgt ? 1.0f : 0.0f)) * scale;
+    return (mx + logf(s) - lt) * scale;
+}
+
+constexpr int kFrontCh = 8;  // channels per front block
+
+// Per cell of range blockIdx.x, channels [8 blockIdx.y, 8 blockIdx.y + 8): the loss gradient of
+// the step's output state plus the gradient from the later steps; the clamp's backward zeroes
+// the input slice of given cells (reference src/nca/engine/ops.py:276-294): g_u; the fire mask
+// gives g_dx = g_u * fire. The block adds its sums of g_dx (db2) into its slot; the blocks of
+// channel group 0 also add the loss and the head's weight / bias gradients.
+__global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
+    __shared__ float red[(kThreads / 64) * 16];
+    const Dims &d = a.d;
+    const int s = blockIdx.x, c0 = kFrontCh * blockIdx.y;
+    const int per = (int)((d.M + kSplit - 1) / kSplit), m0 = s * per;
+    const int m1 = m0 + per < (int)d.M ? m0 + per : (int)d.M;
+    const bool head = blockIdx.y == 0;
+    float db2[kFrontCh];
+#pragma unroll
+    for (int j = 0; j < kFrontCh; ++j) db2[j] = 0.0f;
+    float lossv = 0.0f;
+    for (int m = m0 + threadIdx.x; m < m1; m += kThreads) {
+        const int row = m / d.HW, q = m - row * d.HW;
         float f;
         if (a.fire_u8) {
             f = a.fire_u8[m] ? 1.0f : 0.0f;
@@ -188,47 +269,22 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             const float uq = e4 == 0 ? u[0] : e4 == 1 ? u[1] : e4 == 2 ? u[2] : u[3];
             f = uq < a.p ? 1.0f : 0.0f;
         }
-        const bool gv = a.given[m] != 0;
-        const float *x1 = a.x1 + row * d.C * (int64_t)d.HW + q;
-        // logits, softmax and the cross-entropy gradient (n_out <= 16; static register indices)
+        const int64_t cb = (int64_t)row * d.C * d.HW + q;  // channel 0 of the cell
         float gl[16];
+        const float lc = head_grad(a, m, a.x1 + cb, gl);
+        if (head) lossv = __fadd_rn(lossv, lc);
+        const bool gv = a.given[m] != 0;
+        float gi[kFrontCh];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) gl[v] = 0.0f;
-        if (a.wscale != 0.0f) {
-            const float scale = a.mask ? a.wscale * a.mask[m] / *a.denom : a.wscale;
-            float l[16];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                l[v] = 0.0f;
-                if (v < d.n_out) {
-                    float acc = a.head_b[v];
-                    for (int c = 0; c < d.c_out; ++c)
-                        acc = __builtin_fmaf(a.head_w[v * d.c_out + c], x1[(int64_t)(d.out_off + c) * d.HW], acc);
-                    l[v] = acc;
-                    mx = fmaxf(mx, acc);
-                }
-            }
-            float s = 0.0f, lt = mx;
-            const int tgt = a.targets[m];
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                if (v < d.n_out) {
-                    s += expf(l[v] - mx);
-                    if (v == tgt) lt = l[v];
-                }
-            lossc = (mx + logf(s) - lt) * scale;
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                if (v < d.n_out) gl[v] = (expf(l[v] - mx) / s - (v == tgt ? 1.0f : 0.0f)) * scale;
+        for (int j = 0; j < kFrontCh; ++j) {
+            const int c = c0 + j;
+            gi[j] = (a.gin && c < d.C) ? a.gin[cb + (int64_t)c * d.HW] : 0.0f;
         }
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-            if (v < d.n_out) a.GL[v * d.M + m] = gl[v];
-        const float *gin = a.gin ? a.gin + row * d.C * (int64_t)d.HW + q : nullptr;
-        float *gu = a.Gu + row * d.C * (int64_t)d.HW + q;
-        for (int c = 0; c < d.C; ++c) {
-            float g = gin ? gin[(int64_t)c * d.HW] : 0.0f;
+        for (int j = 0; j < kFrontCh; ++j) {
+            const int c = c0 + j;
+            if (c >= d.C) break;
+            float g = gi[j];
             const int co = c - d.out_off;
             if (co >= 0 && co < d.c_out) {
 #pragma unroll
@@ -236,12 +292,54 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
                     if (v < d.n_out) g = __builtin_fmaf(a.head_w[v * d.c_out + co], gl[v], g);
             }
             if (gv && c >= d.in_off && c < d.in_off + d.c_in) g = 0.0f;
-            gu[(int64_t)c * d.HW] = g;
-            a.Gdx[c * d.M + m] = g * f;
+            a.Gu[cb + (int64_t)c * d.HW] = g;
+            const float gd = g * f;
+            a.Gdx[(int64_t)c * d.M + m] = gd;
+            db2[j] = __fadd_rn(db2[j], gd);
         }
     }
-    const float s = block_sum(lossc, red);
-    if (threadIdx.x == 0) a.lossp[blockIdx.x] = s;
+    const float r = block_sums<kFrontCh, kThreads / 64>(db2, red);
+    if (threadIdx.x < kFrontCh && c0 + (int)threadIdx.x < d.C) {
+        float *pp = a.part + s * a.P + a.offB2 + c0 + threadIdx.x;
+        *pp = __fadd_rn(*pp, r);
+    }
+    if (!head || a.wscale == 0.0f) return;  // uniform across the block
+    {
+        const float lv[1] = {lossv};
+        const float rl = block_sums<1, kThreads / 64>(lv, red);
+        if (threadIdx.x == 0) a.lossacc[s] = __fadd_rn(a.lossacc[s], rl);
+    }
+    // dhead: pair p < n_out c_out is (v, c): sum g_l[v] x1[out_off + c]; pair n_out c_out + v is
+    // the bias: sum g_l[v]; 16 pairs at a time
+    const int npw = d.n_out * d.c_out, np = npw + d.n_out;
+    for (int p0 = 0; p0 < np; p0 += 16) {
+        float acc[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
+        for (int m = m0 + threadIdx.x; m < m1; m += kThreads) {
+            const int row = m / d.HW, q = m - row * d.HW;
+            const float *x1c = a.x1 + (int64_t)row * d.C * d.HW + q;
+            float gl[16];
+            head_grad(a, m, x1c, gl);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int p = p0 + k;
+                if (p >= np) break;
+                const int v = p < npw ? p / d.c_out : p - npw, c = p < npw ? p - v * d.c_out : -1;
+                float g = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 16; ++w) g = w == v ? gl[w] : g;
+                acc[k] = c < 0 ? __fadd_rn(acc[k], g) : __builtin_fmaf(g, x1c[(int64_t)(d.out_off + c) * d.HW], acc[k]);
+            }
+        }
+        const float rh = block_sums<16, kThreads / 64>(acc, red);
+        const int p = p0 + threadIdx.x;
+        if (threadIdx.x < 16 && p < np) {
+            const int v = p < npw ? p / d.c_out : p - npw;
+            float *pp = a.part + s * a.P + (p < npw ? a.offHW + p : a.offHB + v);
+            *pp = __fadd_rn(*pp, rh);
+        }
+    }
 }
 
 // The perception input of tap (dy, dx) of cell (i, j), channel c of row xr: the state (or the
@@ -253,148 +351,129 @@ __device__ __forceinline__ float tap_value(const float *xr, const Dims &d, int i
     return d.bf16 ? nca::round_bf16(v) : v;
 }
 
-// z (F x M, feature-major) of the state x (rows, C, H, W); one thread per (row, channel, cell).
-__global__ void __launch_bounds__(kThreads) stencil_z_kernel(Dims d, const float *x, const float *kern,
-                                                             const float *padv, float *Z) {
-    const int64_t e = blockIdx.x * (int64_t)kThreads + threadIdx.x;
-    if (e >= d.rows * d.C * (int64_t)d.HW) return;
-    const int64_t row = e / ((int64_t)d.C * d.HW);
-    const int rem = (int)(e - row * d.C * (int64_t)d.HW), c = rem / d.HW, q = rem - c * d.HW;
-    const int i = q / d.W, j = q - i * d.W;
-    const float *xr = x + (row * d.C + c) * (int64_t)d.HW;
-    float xv[9];
-#pragma unroll
-    for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
-    const int64_t m = row * d.HW + q;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
-        Z[(int64_t)(k * d.C + c) * d.M + m] = d.bf16 ? nca::round_bf16(acc) : acc;
-    }
-}
-
-// g_x = g_u + transposed stencil of g_z, one thread per (row, channel, cell) in NCHW order.
-__global__ void __launch_bounds__(kThreads) stencil_t_kernel(Dims d, const float *Gu, const float *Gz,
-                                                             const float *kern, float *gx) {
-    const int64_t e = blockIdx.x * (int64_t)kThreads + threadIdx.x;
-    if (e >= d.rows * d.C * (int64_t)d.HW) return;
-    const int64_t row = e / ((int64_t)d.C * d.HW);
-    const int rem = (int)(e - row * d.C * (int64_t)d.HW), c = rem / d.HW, q = rem - c * d.HW;
-    const int i = q / d.W, j = q - i * d.W;
-    float g = Gu[e];
-#pragma unroll
-    for (int t = 0; t < 9; ++t) {
-        // cell q' whose tap t reads this cell: q = q' + (dy, dx)
-        const int qs = neighbour(i, j, -(t / 3 - 1), -(t % 3 - 1), d.H, d.W, d.padding);
-        if (qs < 0) continue;
-        const int64_t ms = row * d.HW + qs;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], Gz[(int64_t)(k * d.C + c) * d.M + ms], g);
-    }
-    gx[e] = g;
-}
-
-// dkernels partials: block s sums g_z[k C + c][m] * xp[c][m + tap] over its cell range.
-__global__ void __launch_bounds__(kThreads) dkern_kernel(Dims d, const float *x, const float *Gz, const float *padv,
-                                                         float *part, int64_t P, int64_t offK) {
-    __shared__ float red[kThreads];
-    const int s = blockIdx.x;
-    const int64_t per = (d.M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < d.M ? m0 + per : d.M;
-    float acc[36];
-#pragma unroll
-    for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
-    const int64_t items = m1 > m0 ? (m1 - m0) * d.C : 0;
-    for (int64_t it = threadIdx.x; it < items; it += kThreads) {
-        const int c = (int)(it % d.C);
-        const int64_t m = m0 + it / d.C, row = m / d.HW;
-        const int q = (int)(m - row * d.HW), i = q / d.W, j = q - i * d.W;
+// z (F x M, feature-major) of the state x (rows, C, H, W): thread (row, channel, cell) with
+// channel and cell from blockIdx.x, rows strided over blockIdx.y.
+__global__ void __launch_bounds__(kThreads) stencil_z_kernel(Dims d, const float *__restrict__ x,
+                                                             const float *__restrict__ kern,
+                                                             const float *__restrict__ padv, float *__restrict__ Z) {
+    const int e = blockIdx.x * kThreads + threadIdx.x;
+    if (e >= d.C * d.HW) return;
+    const int c = e / d.HW, q = e - c * d.HW, i = q / d.W, j = q - i * d.W;
+    for (int64_t row = blockIdx.y; row < d.rows; row += gridDim.y) {
         const float *xr = x + (row * d.C + c) * (int64_t)d.HW;
         float xv[9];
 #pragma unroll
         for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
+        const int64_t m = row * d.HW + q;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float gz = Gz[(int64_t)(k * d.C + c) * d.M + m];
+            float acc = 0.0f;
 #pragma unroll
-            for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gz, xv[t], acc[k * 9 + t]);
-        }
-    }
-    for (int v = 0; v < 36; ++v) {
-        const float r = block_sum(acc[v], red);
-        if (threadIdx.x == 0) part[s * P + offK + v] = r;
-    }
-}
-
-// dhead partials: pair p < n_out c_out is (v, c): sum g_l[v] x1[out_off + c]; pair n_out c_out + v
-// is the bias: sum g_l[v]. Block s over its cell range, one cell per thread, 16 pairs at a time,
-// each pair's per-thread sums reduced in a fixed tree.
-__global__ void __launch_bounds__(kThreads) dhead_kernel(Dims d, const float *x1, const float *GL, float *part,
-                                                         int64_t P, int64_t offHW, int64_t offHB) {
-    __shared__ float red[kThreads];
-    const int s = blockIdx.x;
-    const int64_t per = (d.M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < d.M ? m0 + per : d.M;
-    const int npw = d.n_out * d.c_out, np = npw + d.n_out;
-    for (int p0 = 0; p0 < np; p0 += 16) {
-        float acc[16];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
-        for (int64_t m = m0 + threadIdx.x; m < m1; m += kThreads) {
-            const int64_t row = m / d.HW;
-            const int q = (int)(m - row * d.HW);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int p = p0 + k;
-                if (p >= np) break;
-                const int v = p < npw ? p / d.c_out : p - npw, c = p < npw ? p - v * d.c_out : -1;
-                const float g = GL[v * d.M + m];
-                acc[k] = c < 0 ? __fadd_rn(acc[k], g)
-                               : __builtin_fmaf(g, x1[(row * d.C + d.out_off + c) * (int64_t)d.HW + q], acc[k]);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int p = p0 + k;
-            if (p >= np) break;  // uniform across the block
-            const float r = block_sum(acc[k], red);
-            if (threadIdx.x == 0) {
-                const int v = p < npw ? p / d.c_out : p - npw;
-                part[s * P + (p < npw ? offHW + p : offHB + v)] = r;
-            }
+            for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
+            Z[(int64_t)(k * d.C + c) * d.M + m] = d.bf16 ? nca::round_bf16(acc) : acc;
         }
     }
 }
 
-// Row sums of a feature-major matrix G (R x M): block (r, s) over cell range s.
-__global__ void __launch_bounds__(kThreads) rowsum_kernel(const float *G, int64_t M, float *part, int64_t P,
-                                                          int64_t off) {
-    __shared__ float red[kThreads];
-    const int r = blockIdx.x, s = blockIdx.y;
+constexpr int kBackThreads = 1024;
+
+// g_x = g_u + the transposed stencil of g_z, one thread per (row, channel, cell) in NCHW order
+// (padding-aware: wall / zero halos take no gradient, wrap halos give it to the wrapped cell),
+// and the kernel-weight gradient: sum over (c, m) of g_z[k C + c][m] * xp[c][m + tap] for every
+// (k, tap). Block s takes the elements of NCHW range s and adds its 36 sums into slot s.
+__global__ void __launch_bounds__(kBackThreads) stencil_back_kernel(
+    Dims d, const float *__restrict__ x, const float *__restrict__ Gu, const float *__restrict__ Gz,
+    const float *__restrict__ kern, const float *__restrict__ padv, float *__restrict__ gx,
+    float *__restrict__ part, int64_t P, int64_t offK) {
+    __shared__ float red[(kBackThreads / 64) * 36];
+    const int64_t total = d.rows * d.C * (int64_t)d.HW;
+    const int64_t per = (total + kSplit - 1) / kSplit, e0 = blockIdx.x * per;
+    const int64_t e1 = e0 + per < total ? e0 + per : total;
+    const int64_t ks = (int64_t)d.C * d.M;  // stride of k in g_z
+    float acc[36];
+#pragma unroll
+    for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
+    int64_t e = e0 + threadIdx.x;
+    if (e < e1) {
+        int pl = (int)(e / d.HW), q = (int)(e - (int64_t)pl * d.HW);  // plane row * C + c, cell
+        for (; e < e1; e += kBackThreads) {
+            const int row = pl / d.C, c = pl - row * d.C, i = q / d.W, j = q - i * d.W;
+            const float *xr = x + (int64_t)pl * d.HW;
+            const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * d.HW;
+            float xv[9];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
+            float g = Gu[e];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                // cell q' whose tap t reads this cell: q = q' + (dy, dx)
+                const int qs = neighbour(i, j, -(t / 3 - 1), -(t % 3 - 1), d.H, d.W, d.padding);
+                if (qs < 0) continue;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], gz[k * ks + qs], g);
+            }
+            gx[e] = g;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float gzv = gz[k * ks + q];
+#pragma unroll
+                for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gzv, xv[t], acc[k * 9 + t]);
+            }
+            q += kBackThreads;
+            if (q >= d.HW) {
+                const int w = q / d.HW;
+                pl += w;
+                q -= w * d.HW;
+            }
+        }
+    }
+    const float r = block_sums<36, kBackThreads / 64>(acc, red);
+    if (threadIdx.x < 36) {
+        float *pp = part + blockIdx.x * P + offK + threadIdx.x;
+        *pp = __fadd_rn(*pp, r);
+    }
+}
+
+// Row sums of a feature-major matrix G (R x M) over the kSplit cell ranges, added into the
+// slots: wave w of block (b, s) takes row 4 b + w over range s.
+__global__ void __launch_bounds__(kThreads) rowsum_kernel(const float *__restrict__ G, int64_t M, int R,
+                                                          float *__restrict__ part, int64_t P, int64_t off) {
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6), s = blockIdx.y;
+    if (r >= R) return;  // uniform across the wave
     const int64_t per = (M + kSplit - 1) / kSplit, m0 = s * per, m1 = m0 + per < M ? m0 + per : M;
+    const float *g = G + (int64_t)r * M;
     float acc = 0.0f;
-    for (int64_t m = m0 + threadIdx.x; m < m1; m += kThreads) acc = __fadd_rn(acc, G[r * M + m]);
-    const float t = block_sum(acc, red);
-    if (threadIdx.x == 0) part[s * P + off + r] = t;
+    for (int64_t mb = m0; mb < m1; mb += 256) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t m = mb + 64 * u + lane;
+            v[u] = m < m1 ? g[m] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc = __fadd_rn(acc, v[u]);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) acc = __fadd_rn(acc, __shfl_xor(acc, o));
+    if (lane == 0) {
+        float *pp = part + s * P + off + r;
+        *pp = __fadd_rn(*pp, acc);
+    }
 }
 
-// acc[i] += sum over the kSplit partials in split order.
+// acc[i] = the sum of the kSplit slots in slot order.
 __global__ void reduce_acc_kernel(const float *part, int64_t P, float *acc) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < P; i += (int64_t)gridDim.x * blockDim.x) {
         float s = 0.0f;
         for (int k = 0; k < kSplit; ++k) s = __fadd_rn(s, part[k * P + i]);
-        acc[i] = __fadd_rn(acc[i], s);
+        acc[i] = s;
     }
 }
 
-// The loss of the chunk: each thread sums a fixed strided subset of the (step, block) partials,
-// then a fixed tree; one block.
-__global__ void loss_kernel(const float *lossp, int n, int blocks, float *out) {
+// The loss of the chunk: the sum of the kSplit loss slots in a fixed tree; one block.
+__global__ void loss_kernel(const float *lossacc, float *out) {
     __shared__ float red[kThreads];
-    const int64_t total = (int64_t)n * blocks;
-    float s = 0.0f;
-    for (int64_t i = threadIdx.x; i < total; i += kThreads) s = __fadd_rn(s, lossp[i]);
-    s = block_sum(s, red);
+    const float s = block_sum(threadIdx.x < kSplit ? lossacc[threadIdx.x] : 0.0f, red);
     if (threadIdx.x == 0) *out = s;
 }
 
@@ -407,7 +486,8 @@ __global__ void copy_kernel(const float *src, float *dst, int64_t n) {
 // fp32 GEMM on v_mfma_f32_16x16x4_f32: C (M x N) = A (M x K) B (K x N) with strided operands
 // (A(m, k) = A[m sam + k sak], B(k, n) = B[k sbk + n sbn], one of each pair of strides being 1),
 // 64 x 64 block tiles, 16-deep k slices through LDS, each of the 4 waves a 32 x 32 quadrant.
-// Split-K: block z sums k in [z kps, (z + 1) kps) and writes its partial at C + z * csplit.
+// Split-K: block z sums k in [z kps, (z + 1) kps) and writes (or adds) its partial at
+// C + z * csplit.
 // Epilogues: 0 store (+ row bias), 1 fc1: bias, bf16 rounding for bf16 cells, ReLU,
 // 2 mask: times [mask(m, n) > 0].
 struct GemmArgs {
@@ -422,6 +502,7 @@ struct GemmArgs {
     const float *mask;
     int64_t ldmask;
     int epi, round_in, round_out;  // round_in: round A to bf16 on load (the forward's bf16 weights)
+    int accum;                     // add the result to C instead of storing it
 };
 
 constexpr int GBM = 64, GBN = 64, GBK = 16;
@@ -487,6 +568,7 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
                 } else if (g.epi == 2) {
                     r = g.mask[gm * g.ldmask + gn] > 0.0f ? r : 0.0f;
                 }
+                if (g.accum) r = __fadd_rn(Cz[gm * g.ldc + gn], r);
                 Cz[gm * g.ldc + gn] = r;
             }
 }
@@ -517,10 +599,13 @@ int check_dims(const nca_cell_desc *cell, int64_t rows, int32_t H, int32_t W, in
     d->bf16 = cell->precision == NCA_BF16;
     d->H = H;
     d->W = W;
+    if ((int64_t)H * W * d->C > 0x7fffffff) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT grid too large");
     d->HW = H * W;
     d->rows = rows;
     d->M = rows * (int64_t)H * W;
-    if (d->M * (int64_t)(d->F > d->HD ? d->F : d->HD) > ((int64_t)1 << 40))
+    // cell indices and (row, channel) planes are 32-bit in the kernels
+    if (d->M >= ((int64_t)1 << 30) || rows * d->C >= ((int64_t)1 << 30) ||
+        d->M * (int64_t)(d->F > d->HD ? d->F : d->HD) > ((int64_t)1 << 40))
         return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT batch too large");
     return NCA_OK;
 }
@@ -607,13 +692,22 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     const float *headb = reinterpret_cast<const float *>(pb + PL.headb);
     const float *padv = reinterpret_cast<const float *>(pb + PL.padv);
     float *ws = static_cast<float *>(workspace);
-    float *Z = ws + L.Z, *Hb = ws + L.Hb, *Ga = ws + L.Ga, *Gz = ws + L.Gz, *Gdx = ws + L.Gdx, *GL = ws + L.GL;
+    float *Z = ws + L.Z, *Hb = ws + L.Hb, *Ga = ws + L.Ga, *Gz = ws + L.Gz, *Gdx = ws + L.Gdx;
     float *Gu = ws + L.Gu, *Gx[2] = {ws + L.Gx0, ws + L.Gx1}, *part = ws + L.part, *acc = ws + L.acc;
-    float *lossp = ws + L.lossp, *denom = ws + L.denom;
+    float *lossacc = ws + L.lossacc, *denom = ws + L.denom;
     const int64_t sn = d.rows * d.C * (int64_t)d.HW;
 
-    hipLaunchKernelGGL(zero_f32, dim3(64), dim3(256), 0, st, acc, P.P);
-    hipLaunchKernelGGL(zero_f32, dim3(64), dim3(256), 0, st, lossp, (int64_t)(n_chunk > 0 ? n_chunk : 1) * L.front_blocks);
+    // the partial-sum slots and the loss slots are contiguous
+    hipLaunchKernelGGL(zero_f32, dim3(2048), dim3(256), 0, st, part, L.denom - L.part);
+    // the fused kernel addresses z and g_z with 32-bit byte offsets
+    const bool fused = d.bf16 && d.C == 32 && d.F == 128 && d.HD == 256 && d.M * d.F * 4 < ((int64_t)1 << 32);
+    if (fused && (rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(nca::mlp_back32),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                           (int)nca::Mb32::TOTAL),
+                                       "mlp_back32 attribute")))
+        return rc;
+    // cells per workgroup of the fused kernel: whole 32-cell tiles
+    const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
     if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;
 
@@ -643,56 +737,84 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
         fa.p = fire->p_fire;
         fa.Gu = Gu;
         fa.Gdx = Gdx;
-        fa.GL = GL;
-        fa.lossp = lossp + (int64_t)t * L.front_blocks;
-        hipLaunchKernelGGL(front_kernel, dim3(L.front_blocks), dim3(kThreads), 0, st, fa);
+        fa.part = part;
+        fa.lossacc = lossacc;
+        fa.P = P.P;
+        fa.offB2 = P.B2;
+        fa.offHW = P.HW;
+        fa.offHB = P.HB;
+        hipLaunchKernelGGL(front_kernel, dim3(kSplit, (d.C + kFrontCh - 1) / kFrontCh), dim3(kThreads), 0, st, fa);
         // recompute z and h from the saved state
-        hipLaunchKernelGGL(stencil_z_kernel, dim3(grid_for(sn)), dim3(kThreads), 0, st, d, xt, kern, padv, Z);
+        const dim3 zgrid(grid_for((int64_t)d.C * d.HW), (unsigned)(d.rows < 65535 ? d.rows : 65535));
+        hipLaunchKernelGGL(stencil_z_kernel, zgrid, dim3(kThreads), 0, st, d, xt, kern, padv, Z);
         if ((rc = nca::hip_status(hipGetLastError(), "bptt front / stencil"))) return rc;
         GemmArgs g;
-        memset(&g, 0, sizeof(g));
-        // h = relu(W1 z + b1): (HD x F) (F x M)
-        g.A = w->w1; g.sam = d.F; g.sak = 1;
-        g.B = Z; g.sbk = d.M; g.sbn = 1;
-        g.Cm = Hb; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.F; g.kps = d.F;
-        g.bias = b1; g.epi = 1; g.round_in = d.bf16; g.round_out = d.bf16;
-        if ((rc = gemm(g, 1, st))) return rc;
-        // g_a = (W2^T g_dx) * [h > 0]: (HD x C) (C x M)
-        memset(&g, 0, sizeof(g));
-        g.A = w->w2; g.sam = 1; g.sak = d.HD;
-        g.B = Gdx; g.sbk = d.M; g.sbn = 1;
-        g.Cm = Ga; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.C; g.kps = d.C;
-        g.mask = Hb; g.ldmask = d.M; g.epi = 2; g.round_in = d.bf16;
-        if ((rc = gemm(g, 1, st))) return rc;
-        // g_z = W1^T g_a: (F x HD) (HD x M)
-        memset(&g, 0, sizeof(g));
-        g.A = w->w1; g.sam = 1; g.sak = d.F;
-        g.B = Ga; g.sbk = d.M; g.sbn = 1;
-        g.Cm = Gz; g.ldc = d.M; g.M = d.F; g.N = d.M; g.K = d.HD; g.kps = d.HD;
-        g.round_in = d.bf16;
-        if ((rc = gemm(g, 1, st))) return rc;
-        // gradient of the step's input state
-        hipLaunchKernelGGL(stencil_t_kernel, dim3(grid_for(sn)), dim3(kThreads), 0, st, d, Gu, Gz, kern, gx);
-        // weight-gradient partials over kSplit cell ranges
-        const int64_t kps = (((d.M + kSplit - 1) / kSplit) + GBK - 1) / GBK * GBK;
-        memset(&g, 0, sizeof(g));
-        g.A = Ga; g.sam = d.M; g.sak = 1;  // dW1 = g_a z^T: (HD x M) (M x F)
-        g.B = Z; g.sbk = 1; g.sbn = d.M;
-        g.Cm = part + P.W1; g.ldc = d.F; g.csplit = P.P; g.M = d.HD; g.N = d.F; g.K = d.M; g.kps = kps;
-        if ((rc = gemm(g, kSplit, st))) return rc;
-        memset(&g, 0, sizeof(g));
-        g.A = Gdx; g.sam = d.M; g.sak = 1;  // dW2 = g_dx h^T: (C x M) (M x HD)
-        g.B = Hb; g.sbk = 1; g.sbn = d.M;
-        g.Cm = part + P.W2; g.ldc = d.HD; g.csplit = P.P; g.M = d.C; g.N = d.HD; g.K = d.M; g.kps = kps;
-        if ((rc = gemm(g, kSplit, st))) return rc;
-        hipLaunchKernelGGL(rowsum_kernel, dim3(d.HD, kSplit), dim3(kThreads), 0, st, Ga, d.M, part, P.P, P.B1);
-        hipLaunchKernelGGL(rowsum_kernel, dim3(d.C, kSplit), dim3(kThreads), 0, st, Gdx, d.M, part, P.P, P.B2);
-        hipLaunchKernelGGL(dkern_kernel, dim3(kSplit), dim3(kThreads), 0, st, d, xt, Gz, padv, part, P.P, P.K);
-        hipLaunchKernelGGL(dhead_kernel, dim3(kSplit), dim3(kThreads), 0, st, d, x1, GL, part, P.P, P.HW, P.HB);
-        hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
+        if (fused) {
+            nca::MlpBackArgs ma;
+            ma.Z = Z;
+            ma.Gdx = Gdx;
+            ma.w1 = w->w1;
+            ma.w2 = w->w2;
+            ma.b1 = b1;
+            ma.Gz = Gz;
+            ma.part = part;
+            ma.P = P.P;
+            ma.offW1 = P.W1;
+            ma.offB1 = P.B1;
+            ma.offW2 = P.W2;
+            ma.M = d.M;
+            ma.per = per32;
+            hipLaunchKernelGGL(nca::mlp_back32, dim3(kSplit), dim3(512), nca::Mb32::TOTAL, st, ma);
+            if ((rc = nca::hip_status(hipGetLastError(), "mlp_back32"))) return rc;
+        } else {
+            memset(&g, 0, sizeof(g));
+            // h = relu(W1 z + b1): (HD x F) (F x M)
+            g.A = w->w1; g.sam = d.F; g.sak = 1;
+            g.B = Z; g.sbk = d.M; g.sbn = 1;
+            g.Cm = Hb; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.F; g.kps = d.F;
+            g.bias = b1; g.epi = 1; g.round_in = d.bf16; g.round_out = d.bf16;
+            if ((rc = gemm(g, 1, st))) return rc;
+            // g_a = (W2^T g_dx) * [h > 0]: (HD x C) (C x M)
+            memset(&g, 0, sizeof(g));
+            g.A = w->w2; g.sam = 1; g.sak = d.HD;
+            g.B = Gdx; g.sbk = d.M; g.sbn = 1;
+            g.Cm = Ga; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.C; g.kps = d.C;
+            g.mask = Hb; g.ldmask = d.M; g.epi = 2; g.round_in = d.bf16;
+            if ((rc = gemm(g, 1, st))) return rc;
+            // g_z = W1^T g_a: (F x HD) (HD x M)
+            memset(&g, 0, sizeof(g));
+            g.A = w->w1; g.sam = 1; g.sak = d.F;
+            g.B = Ga; g.sbk = d.M; g.sbn = 1;
+            g.Cm = Gz; g.ldc = d.M; g.M = d.F; g.N = d.M; g.K = d.HD; g.kps = d.HD;
+            g.round_in = d.bf16;
+            if ((rc = gemm(g, 1, st))) return rc;
+        }
+        // gradient of the step's input state and the kernel-weight partials
+        hipLaunchKernelGGL(stencil_back_kernel, dim3(kSplit), dim3(kBackThreads), 0, st, d, xt, Gu, Gz, kern, padv, gx,
+                           part, P.P, P.K);
+        if (!fused) {
+            // weight-gradient partials over kSplit cell ranges
+            const int64_t kps = (((d.M + kSplit - 1) / kSplit) + GBK - 1) / GBK * GBK;
+            memset(&g, 0, sizeof(g));
+            g.A = Ga; g.sam = d.M; g.sak = 1;  // dW1 = g_a z^T: (HD x M) (M x F)
+            g.B = Z; g.sbk = 1; g.sbn = d.M;
+            g.Cm = part + P.W1; g.ldc = d.F; g.csplit = P.P; g.M = d.HD; g.N = d.F; g.K = d.M; g.kps = kps;
+            g.accum = 1;
+            if ((rc = gemm(g, kSplit, st))) return rc;
+            memset(&g, 0, sizeof(g));
+            g.A = Gdx; g.sam = d.M; g.sak = 1;  // dW2 = g_dx h^T: (C x M) (M x HD)
+            g.B = Hb; g.sbk = 1; g.sbn = d.M;
+            g.Cm = part + P.W2; g.ldc = d.HD; g.csplit = P.P; g.M = d.C; g.N = d.HD; g.K = d.M; g.kps = kps;
+            g.accum = 1;
+            if ((rc = gemm(g, kSplit, st))) return rc;
+            hipLaunchKernelGGL(rowsum_kernel, dim3((d.HD + 3) / 4, kSplit), dim3(kThreads), 0, st, Ga, d.M, d.HD, part,
+                               P.P, P.B1);
+        }
         if ((rc = nca::hip_status(hipGetLastError(), "bptt step kernels"))) return rc;
         gin = gx;
     }
+    // the slots summed in slot order
+    hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
     if (grad_x0) {
         if (n_chunk == 0 || d.M == 0) {
             if (grad_final) hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, grad_final, grad_x0, sn);
@@ -709,7 +831,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.HB, grads->head_b, (int64_t)d.n_out);
     if (loss_out) {
         if (n_chunk > 0 && d.M > 0)
-            hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossp, n_chunk, L.front_blocks, loss_out);
+            hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossacc, loss_out);
         else
             hipLaunchKernelGGL(zero_f32, dim3(1), dim3(64), 0, st, loss_out, (int64_t)1);
     }

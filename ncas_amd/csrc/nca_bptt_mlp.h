@@ -1,0 +1,389 @@
+// Fused MLP backward of one BPTT step for bf16 cells with C = 32 channels, F = 128 features and
+// 256 hidden units (gfx950): for a tile of 32 cells,
+//
+//   h    = relu(bf16(W1 z + b1))            recomputed (the forward's rounding points)
+//   g_a  = (W2^T g_dx) * [h > 0]
+//   g_z  = W1^T g_a                          -> HBM, for the transposed stencil
+//   dW1 += g_a z^T,  dW2 += g_dx h^T,  db1 += sum over cells of g_a   (registers)
+//
+// with every product on v_mfma_f32_16x16x32_bf16. W1, W2 (rounded from the fp32 master weights),
+// z and h are bf16 values, so their products are exact; the fp32 gradient operands g_dx and g_a
+// are split into three bf16 parts (v = hi + mid + lo exactly: each part takes the next 8 bits of
+// the significand), each multiplied exactly and accumulated in fp32, lo first. The results are
+// fp32 sums of the exact products, like an fp32 GEMM's, in another order.
+//
+// One workgroup per cell range (its slot of the partial sums), 8 waves; wave w owns hidden units
+// [32w, 32w + 32) for fc1, g_a and the weight gradients, whose accumulators stay in registers for
+// the whole range and are added into the slot at the end. MFMA operand layouts (16x16x32): lane
+// (r = lane & 15, g = lane >> 4) holds A[r][8g + j] / B[8g + j][r], j < 8, and D[4g + i][r],
+// i < 4. fc1 and g_a are computed in both orientations ([hidden][cell] and [cell][hidden]) so
+// that each later product finds its operand in registers: D[cell 4g + i][hidden r] of two cell
+// tiles is an operand whose k runs over 8 cells in the order perm(g, j) = j < 4 ? 4g + j :
+// 16 + 4g + j - 4; the LDS operands of those products use the same cell order. g_z sums over all
+// hidden units, so g_a goes through LDS (its three bf16 parts, hidden units of each 32-block in
+// the same perm order) and wave w computes g_z for features [32(w >> 1), +32) x cells
+// [16(w & 1), +16).
+//
+// Per tile: the tile's z and g_dx (prefetched into registers during the previous tile) are stored
+// to LDS; barrier; fc1, g_a, the g_a parts to LDS, dW2 and dW1; barrier; g_z.
+//
+// LDS, rows padded by one 16-byte chunk (row strides of 17, 5 and 33 chunks) so that 8
+// consecutive lanes of a 16-byte access to 8 consecutive rows touch distinct chunks of the 64
+// banks, and every address in the tile loop is a per-lane base plus a constant:
+//   ZA   z [cell 32][feature 128] bf16, 272-byte rows
+//   ZB   z [feature 128][cell 32 in perm order] bf16, 80-byte rows
+//   GA   g_dx parts [3][cell 32][channel 32] bf16, 80-byte rows
+//   GB   g_dx parts [3][channel 32][cell 32 in perm order] bf16, 80-byte rows
+//   GAL  g_a parts [3][cell 32][hidden 256, perm order in each 32-block] bf16, 528-byte rows
+//   W1T  W1^T [feature 128][hidden 256, perm order in each 32-block] bf16, 528-byte rows
+//   B1   b1 fp32
+#pragma once
+
+#include "nca_stream_util.h"
+
+namespace nca {
+
+struct MlpBackArgs {
+    const float *Z;    // z (F x M), bf16 values
+    const float *Gdx;  // g_dx (C x M)
+    const float *w1;   // fp32 master W1 (HD x F)
+    const float *w2;   // fp32 master W2 (C x HD)
+    const float *b1;   // HD
+    float *Gz;         // g_z (F x M)
+    float *part;       // partial-sum slots, P floats each; workgroup s adds into slot s
+    int64_t P, offW1, offB1, offW2, M;
+    int per;  // cells per workgroup, a multiple of 32
+};
+
+struct Mb32 {
+    static constexpr unsigned ZAR = 272, ZBR = 80, GR = 80, AR = 528;  // row strides
+    static constexpr unsigned GPART = 32 * GR;   // bytes of one g_dx part
+    static constexpr unsigned APART = 32 * AR;   // bytes of one g_a part
+    static constexpr unsigned ZA = 0, ZB = ZA + 32 * ZAR, GA = ZB + 128 * ZBR, GB = GA + 3 * GPART,
+                              GAL = GB + 3 * GPART, W1T = GAL + 3 * APART, B1 = W1T + 128 * AR,
+                              TOTAL = B1 + 1024;
+};
+
+typedef float mb_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ mb_f32x4 mb_mfma(const bf16x8 &a, const bf16x8 &b, const mb_f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8 mb_ld(const unsigned char *s, unsigned off) {
+    return *reinterpret_cast<const bf16x8 *>(s + off);
+}
+__device__ __forceinline__ bf16x8 mb_pack8(const float v[8]) {
+    const uint4 u = {cvt_pk_bf16(v[0], v[1]), cvt_pk_bf16(v[2], v[3]), cvt_pk_bf16(v[4], v[5]),
+                     cvt_pk_bf16(v[6], v[7])};
+    return __builtin_bit_cast(bf16x8, u);
+}
+// a = hi + mid + lo and b likewise, exactly; each part packed as a bf16 pair (a in the low half).
+__device__ __forceinline__ void mb_split(float a, float b, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+    hi = cvt_pk_bf16(a, b);
+    const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xffff0000u);
+    mid = cvt_pk_bf16(ra, rb);
+    const float sa = ra - __uint_as_float(mid << 16), sb = rb - __uint_as_float(mid & 0xffff0000u);
+    lo = cvt_pk_bf16(sa, sb);
+}
+// eight floats -> three bf16x8 parts
+__device__ __forceinline__ void mb_split8(const float v[8], uint4 p[3]) {
+    mb_split(v[0], v[1], p[0].x, p[1].x, p[2].x);
+    mb_split(v[2], v[3], p[0].y, p[1].y, p[2].y);
+    mb_split(v[4], v[5], p[0].z, p[1].z, p[2].z);
+    mb_split(v[6], v[7], p[0].w, p[1].w, p[2].w);
+}
+__device__ __forceinline__ int mb_perm(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4; }
+
+__global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    typedef Mb32 S;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int64_t M = a.M;
+    const int64_t mb0 = (int64_t)blockIdx.x * a.per;
+    if (mb0 >= M) return;  // uniform: an empty range adds nothing to its slot
+    const int64_t mb1 = mb0 + a.per < M ? mb0 + a.per : M;
+
+    // ---- set-up: W1^T and b1 into LDS, W1 / W2 fragments into registers
+    for (int e = tid; e < 128 * 32; e += 512) {
+        const int f = e >> 5, kb = (e >> 2) & 7, q = e & 3;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = a.w1[(32 * kb + mb_perm(q, j)) * 128 + f];
+        *reinterpret_cast<bf16x8 *>(smem + S::W1T + f * S::AR + 16 * (4 * kb + q)) = mb_pack8(v);
+    }
+    if (tid < 256) reinterpret_cast<float *>(smem + S::B1)[tid] = a.b1[tid];
+    bf16x8 w1f[2][4];  // [ht][kb]: W1[32w + 16ht + r][32kb + 8g + j]
+    bf16x8 w2f[2];     // [ht]: W2[8g + j][32w + 16ht + r]
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+        const int hid = 32 * w + 16 * ht + r;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = a.w1[hid * 128 + 32 * kb + 8 * g + j];
+            w1f[ht][kb] = mb_pack8(v);
+        }
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = a.w2[(8 * g + j) * 256 + hid];
+        w2f[ht] = mb_pack8(v);
+    }
+    mb_f32x4 dw1[2][8], dw2[2][2];  // dw1[ht][ft]: D[hid 32w+16ht+4g+i][f 16ft+r]; dw2[ct][ht]: D[ch 16ct+4g+i][hid 32w+16ht+r]
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+#pragma unroll
+        for (int y = 0; y < 8; ++y) dw1[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int y = 0; y < 2; ++y) dw2[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float db1[2] = {0.f, 0.f};  // hidden 32w + 16ht + r, this lane's cells
+
+    // ---- the tile's loads (prefetched one tile ahead): thread (row tid >> 2, q = tid & 3) loads
+    // cells perm(q, 0..7) of z row tid >> 2 and, for tid < 128, of g_dx row tid >> 2 (byte offsets
+    // below 2^32, checked by the host)
+    const bool vec = (M & 3) == 0;  // 16-byte aligned cell quads (tile starts are multiples of 32)
+    const int lrow = tid >> 2, q = tid & 3;
+    const unsigned char *zb = reinterpret_cast<const unsigned char *>(a.Z);
+    const unsigned char *gb = reinterpret_cast<const unsigned char *>(a.Gdx);
+    const uint32_t rowb = (uint32_t)lrow * (uint32_t)M * 4u;
+    float pz[8], pg[8];
+    auto load8 = [&](const unsigned char *base, int64_t m0, float v[8]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t m = m0 + 16 * h + 4 * q;
+            const uint32_t off = rowb + (uint32_t)m * 4u;
+            if (vec) {
+                const float4 x = m < mb1 ? *reinterpret_cast<const float4 *>(base + off) : float4{0.f, 0.f, 0.f, 0.f};
+                v[4 * h] = x.x;
+                v[4 * h + 1] = x.y;
+                v[4 * h + 2] = x.z;
+                v[4 * h + 3] = x.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[4 * h + e] = m + e < mb1 ? *reinterpret_cast<const float *>(base + off + 4 * e) : 0.0f;
+            }
+        }
+    };
+    auto load_tile = [&](int64_t m0) {
+        load8(zb, m0, pz);
+        if (tid < 128) load8(gb, m0, pg);
+    };
+    auto store_tile = [&]() {
+        // ZB row lrow chunk q; ZA column lrow of rows perm(q, j)
+        *reinterpret_cast<bf16x8 *>(smem + S::ZB + lrow * S::ZBR + 16 * q) = mb_pack8(pz);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            *reinterpret_cast<__bf16 *>(smem + S::ZA + mb_perm(q, j) * S::ZAR + 2 * lrow) = (__bf16)pz[j];
+        if (tid < 128) {  // GB row lrow chunk q; GA column lrow of rows perm(q, j); three parts
+            uint4 p[3];
+            mb_split8(pg, p);
+#pragma unroll
+            for (int sp = 0; sp < 3; ++sp) {
+                lds_st128(smem, S::GB + sp * S::GPART + lrow * S::GR + 16 * q, p[sp]);
+                const bf16x8 pv = __builtin_bit_cast(bf16x8, p[sp]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    *reinterpret_cast<__bf16 *>(smem + S::GA + sp * S::GPART + mb_perm(q, j) * S::GR + 2 * lrow) = pv[j];
+            }
+        }
+    };
+
+    const int ntile = (int)((mb1 - mb0 + 31) / 32);
+    load_tile(mb0);
+    for (int t = 0; t < ntile; ++t) {
+        const int64_t m0 = mb0 + 32 * (int64_t)t;
+        store_tile();
+        if (t + 1 < ntile) load_tile(m0 + 32);
+        __syncthreads();
+
+        // ---- fc1: hT[ct][ht] = D[cell 16ct+4g+i][hid 32w+16ht+r]
+        mb_f32x4 hT[2][2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y) hT[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const unsigned zo = S::ZA + r * S::ZAR + 16 * (4 * kb + g);
+            const bf16x8 z0 = mb_ld(smem, zo), z1 = mb_ld(smem, zo + 16 * S::ZAR);
+#pragma unroll
+            for (int ht = 0; ht < 2; ++ht) {
+                hT[0][ht] = mb_mfma(z0, w1f[ht][kb], hT[0][ht]);
+                hT[1][ht] = mb_mfma(z1, w1f[ht][kb], hT[1][ht]);
+            }
+        }
+        {
+            const float *b1L = reinterpret_cast<const float *>(smem + S::B1);
+#pragma unroll
+            for (int ht = 0; ht < 2; ++ht) {
+                const float bt = b1L[32 * w + 16 * ht + r];
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float vt = round_bf16(__fadd_rn(hT[ct][ht][i], bt));
+                        hT[ct][ht][i] = vt > 0.0f ? vt : 0.0f;
+                    }
+            }
+        }
+
+        // ---- g_a = (W2^T g_dx) * [h > 0]: gaT[ct][ht] like hT (parts lo, mid, hi)
+        mb_f32x4 gaT[2][2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y) gaT[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int sp = 2; sp >= 0; --sp) {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int cell = 16 * ct + r;
+                const bf16x8 gf = mb_ld(smem, S::GA + sp * S::GPART + cell * S::GR + 16 * g);
+#pragma unroll
+                for (int ht = 0; ht < 2; ++ht) gaT[ct][ht] = mb_mfma(gf, w2f[ht], gaT[ct][ht]);
+            }
+        }
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) gaT[x][y][i] = hT[x][y][i] > 0.0f ? gaT[x][y][i] : 0.0f;
+        // db1: this lane's hidden unit 32w + 16ht + r over cells 16ct + 4g + i
+#pragma unroll
+        for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) db1[ht] = __fadd_rn(db1[ht], gaT[ct][ht][i]);
+        // g_a parts, k over cells in perm order: ap[ht][sp] element j = part sp of
+        // g_a[hid 32w + 16ht + r][cell perm(g, j)]
+        bf16x8 ap[2][3];
+#pragma unroll
+        for (int ht = 0; ht < 2; ++ht) {
+            const float v[8] = {gaT[0][ht][0], gaT[0][ht][1], gaT[0][ht][2], gaT[0][ht][3],
+                                gaT[1][ht][0], gaT[1][ht][1], gaT[1][ht][2], gaT[1][ht][3]};
+            uint4 p[3];
+            mb_split8(v, p);
+#pragma unroll
+            for (int sp = 0; sp < 3; ++sp) ap[ht][sp] = __builtin_bit_cast(bf16x8, p[sp]);
+        }
+        // ... and into GAL for g_z: hidden offset o = 16ht + r of block w sits at chunk r >> 2,
+        // element 4ht + (r & 3) of the block's perm order
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int cell = mb_perm(g, j);
+            const unsigned base = S::GAL + cell * S::AR + 16 * (4 * w + (r >> 2)) + 2 * (r & 3);
+#pragma unroll
+            for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+                for (int sp = 0; sp < 3; ++sp)
+                    *reinterpret_cast<__bf16 *>(smem + base + sp * S::APART + 8 * ht) = ap[ht][sp][j];
+        }
+
+        // ---- dW2 += g_dx h^T: A = g_dx parts [channel][cells perm], B = h^T (exact bf16)
+        {
+            bf16x8 hb[2];
+#pragma unroll
+            for (int ht = 0; ht < 2; ++ht) {
+                const float v[8] = {hT[0][ht][0], hT[0][ht][1], hT[0][ht][2], hT[0][ht][3],
+                                    hT[1][ht][0], hT[1][ht][1], hT[1][ht][2], hT[1][ht][3]};
+                hb[ht] = mb_pack8(v);
+            }
+#pragma unroll
+            for (int sp = 2; sp >= 0; --sp)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const int c = 16 * ct + r;
+                    const bf16x8 gb = mb_ld(smem, S::GB + sp * S::GPART + c * S::GR + 16 * g);
+#pragma unroll
+                    for (int ht = 0; ht < 2; ++ht) dw2[ct][ht] = mb_mfma(gb, hb[ht], dw2[ct][ht]);
+                }
+        }
+        // ---- dW1 += g_a z^T: A = g_a parts (hidden x cells perm), B = z [cells perm][feature]
+#pragma unroll
+        for (int ft = 0; ft < 8; ft += 2) {
+            const int f0 = 16 * ft + r, f1 = f0 + 16;
+            const bf16x8 zb0 = mb_ld(smem, S::ZB + f0 * S::ZBR + 16 * g);
+            const bf16x8 zb1 = mb_ld(smem, S::ZB + f1 * S::ZBR + 16 * g);
+#pragma unroll
+            for (int sp = 2; sp >= 0; --sp)
+#pragma unroll
+                for (int ht = 0; ht < 2; ++ht) {
+                    dw1[ht][ft] = mb_mfma(ap[ht][sp], zb0, dw1[ht][ft]);
+                    dw1[ht][ft + 1] = mb_mfma(ap[ht][sp], zb1, dw1[ht][ft + 1]);
+                }
+        }
+        __syncthreads();
+
+        // ---- g_z = W1^T g_a: features 16 fb + 4g + i (fb = 2(w >> 1) + f) of cell 16ct + r,
+        //      even and odd hidden blocks in separate chains
+        {
+            const int ct = w & 1, fb = 2 * (w >> 1);
+            mb_f32x4 gz[2][2];
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int y = 0; y < 2; ++y) gz[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
+            const int cell = 16 * ct + r;
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb) {
+                const unsigned ko = 16 * (4 * kb + g);
+                const bf16x8 a0 = mb_ld(smem, S::W1T + (16 * fb + r) * S::AR + ko);
+                const bf16x8 a1 = mb_ld(smem, S::W1T + (16 * fb + 16 + r) * S::AR + ko);
+#pragma unroll
+                for (int sp = 2; sp >= 0; --sp) {
+                    const bf16x8 b = mb_ld(smem, S::GAL + sp * S::APART + cell * S::AR + ko);
+                    gz[0][kb & 1] = mb_mfma(a0, b, gz[0][kb & 1]);
+                    gz[1][kb & 1] = mb_mfma(a1, b, gz[1][kb & 1]);
+                }
+            }
+            const int64_t m = m0 + cell;
+            if (m < mb1) {
+                unsigned char *gzb = reinterpret_cast<unsigned char *>(a.Gz);
+                const uint32_t o0 = ((uint32_t)(16 * fb + 4 * g) * (uint32_t)M + (uint32_t)m) * 4u;
+#pragma unroll
+                for (int f = 0; f < 2; ++f)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        *reinterpret_cast<float *>(gzb + o0 + (uint32_t)(16 * f + i) * (uint32_t)M * 4u) =
+                            __fadd_rn(gz[f][0][i], gz[f][1][i]);
+            }
+        }
+    }
+
+    // ---- this range's partial sums into slot blockIdx.x
+    float *ps = a.part + (int64_t)blockIdx.x * a.P;
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+        for (int ft = 0; ft < 8; ++ft)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float *p = ps + a.offW1 + (32 * w + 16 * ht + 4 * g + i) * 128 + 16 * ft + r;
+                *p = __fadd_rn(*p, dw1[ht][ft][i]);
+            }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int ht = 0; ht < 2; ++ht)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float *p = ps + a.offW2 + (16 * ct + 4 * g + i) * 256 + 32 * w + 16 * ht + r;
+                *p = __fadd_rn(*p, dw2[ct][ht][i]);
+            }
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+        float v = db1[ht];
+        v = __fadd_rn(v, __shfl_xor(v, 16));
+        v = __fadd_rn(v, __shfl_xor(v, 32));
+        if (g == 0) {
+            float *p = ps + a.offB1 + 32 * w + 16 * ht + r;
+            *p = __fadd_rn(*p, v);
+        }
+    }
+}
+
+}  // namespace nca
