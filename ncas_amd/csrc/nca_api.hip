@@ -469,6 +469,40 @@ int check_grid(int64_t rows, int H, int W) {
 
 }  // namespace
 
+namespace nca {
+
+int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows, int H, int W, const float *x_in,
+                     const uint8_t *given, const float *clamp, float *x_out, const nca_fire_desc *fire, int n_steps,
+                     float *x_rec, int64_t rec_stride, hipStream_t st, bool *used) {
+    *used = false;
+    // anything the checks of nca_rollout_ws would refuse is left to the caller's fallback
+    if (check_cell(cell) || check_grid(rows, H, W)) {
+        g_err[0] = 0;
+        return NCA_OK;
+    }
+    if (!packed || !x_in || !given || (!clamp && cell->c_in > 0) || !x_out || !x_rec) return NCA_OK;
+    if (fire->adaptive || rows < 1 || n_steps < 1 || !takes_stream32(cell, rows, H, W)) return NCA_OK;
+    nca::RolloutParams p = base_params(cell, packed, rows, H, W);
+    p.x_in = x_in;
+    p.x_out = x_out;
+    p.given = given;
+    p.clamp = clamp;
+    p.fire_u8 = fire->fire_in;
+    p.step_seeds = fire->step_seeds;
+    p.seed = fire->seed;
+    p.row0 = fire->row0;
+    p.step0 = fire->step0;
+    p.n_steps = n_steps;
+    p.p = fire->p_fire;
+    p.p_low = fire->p_low;
+    p.tau = fire->tau;
+    p.x_rec = x_rec;
+    p.rec_stride = rec_stride;
+    return hip_check(nca::launch_stream32(p, st, kLdsBytes, used), "streamed rollout launch");
+}
+
+}  // namespace nca
+
 extern "C" {
 
 const char *nca_last_error(void) { return g_err; }

@@ -79,7 +79,7 @@ ParamLayout param_layout(const Dims &d) {
 // each (slot s: the cells of range s), added to by every step of the chunk and reduced once at
 // the end; lossacc holds the loss's kSplit slots.
 struct WsLayout {
-    int64_t Z, Hb, Ga, Gz, Gdx, Gu, Gx0, Gx1, part, acc, lossacc, denom, total;
+    int64_t Z, Hb, Ga, Gz, Gdx, Gu, Gx0, Gx1, part, acc, lossacc, denom, img, total;
 };
 
 WsLayout ws_layout(const Dims &d, int n) {
@@ -112,19 +112,23 @@ WsLayout ws_layout(const Dims &d, int n) {
     o = al(o + kSplit);
     L.denom = o;
     o = al(o + 1);
+    L.img = o;  // weight image of the fused MLP backward
+    o = al(o + nca::Mb32::IMG_BYTES / 4);
     L.total = o;
     return L;
 }
 
-// The neighbour of cell (i, j) at (i + dy, j + dx): its cell index, or -1 for a constant halo
-// cell (wall / zero padding); wrap padding wraps around (reference src/nca/model.py:140-152).
+// The neighbour of cell (i, j) at (i + dy, j + dx), |dy|, |dx| <= 1: its cell index, or -1 for a
+// constant halo cell (wall / zero padding); wrap padding wraps around (reference
+// src/nca/model.py:140-152). Selects only: the kernels load at every tap without a branch, so the
+// loads of a thread are all in flight together.
 __device__ __forceinline__ int neighbour(int i, int j, int dy, int dx, int H, int W, int padding) {
     int a = i + dy, b = j + dx;
-    if (a >= 0 && a < H && b >= 0 && b < W) return a * W + b;
-    if (padding != 2) return -1;
-    a = (a + H) % H;
-    b = (b + W) % W;
-    return a * W + b;
+    const bool in = a >= 0 && a < H && b >= 0 && b < W;
+    const bool wrap = padding == 2;
+    a = a < 0 ? H - 1 : (a >= H ? 0 : a);
+    b = b < 0 ? W - 1 : (b >= W ? 0 : b);
+    return (in || wrap) ? a * W + b : -1;
 }
 
 // Block-wide sum of one float per thread in a fixed tree order (deterministic).
@@ -202,50 +206,64 @@ struct FrontArgs {
     int64_t P, offB2, offHW, offHB;
 };
 
-// The cross-entropy gradient of the mlp head's logits at cell m (gl[v] = d loss / d logit v,
-// times the step's scale; 0 for v >= n_out, and everywhere on a step without a loss term) and
-// the cell's loss term (reference src/nca/train.py:183-207). x1c is channel 0 of the cell in the
-// step's output state.
-__device__ __forceinline__ float head_grad(const FrontArgs &a, int m, const float *x1c, float gl[16]) {
+// The output channels of a cell (x1c: channel 0 of the cell in the step's output state), loaded
+// without a branch: xo[c] for c < c_out (<= NO), 0 beyond.
+template <int NO>
+__device__ __forceinline__ void load_out(const Dims &d, const float *x1c, float xo[NO]) {
+    float v[NO];
+#pragma unroll
+    for (int c = 0; c < NO; ++c) v[c] = x1c[(int64_t)(d.out_off + (c < d.c_out ? c : 0)) * d.HW];
+#pragma unroll
+    for (int c = 0; c < NO; ++c) xo[c] = c < d.c_out ? v[c] : 0.0f;
+}
+
+// The cross-entropy gradient of the mlp head's logits at a cell with output channels xo, target
+// tgt and loss-mask value mk (gl[v] = d loss / d logit v, times the step's scale; 0 for
+// v >= n_out, and everywhere on a step without a loss term) and the cell's loss term (reference
+// src/nca/train.py:183-207). n_out, c_out <= NO.
+template <int NO>
+__device__ __forceinline__ float head_grad(const FrontArgs &a, const float xo[NO], int tgt, float mk, float gl[NO]) {
     const Dims &d = a.d;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) gl[v] = 0.0f;
+    for (int v = 0; v < NO; ++v) gl[v] = 0.0f;
     if (a.wscale == 0.0f) return 0.0f;
-    const float scale = a.mask ? a.wscale * a.mask[m] / *a.denom : a.wscale;
-    float l[16];
+    const float scale = a.mask ? a.wscale * mk / *a.denom : a.wscale;
+    float l[NO];
     float mx = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
+    for (int v = 0; v < NO; ++v) {
         l[v] = 0.0f;
         if (v < d.n_out) {
             float acc = a.head_b[v];
-            for (int c = 0; c < d.c_out; ++c)
-                acc = __builtin_fmaf(a.head_w[v * d.c_out + c], x1c[(int64_t)(d.out_off + c) * d.HW], acc);
+#pragma unroll
+            for (int c = 0; c < NO; ++c)
+                if (c < d.c_out) acc = __builtin_fmaf(a.head_w[v * d.c_out + c], xo[c], acc);
             l[v] = acc;
             mx = fmaxf(mx, acc);
         }
     }
     float s = 0.0f, lt = mx;
-    const int tgt = a.targets[m];
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
+    for (int v = 0; v < NO; ++v)
         if (v < d.n_out) {
             s += expf(l[v] - mx);
             if (v == tgt) lt = l[v];
         }
 #pragma unroll
-    for (int v = 0; v < 16; ++v)
+    for (int v = 0; v < NO; ++v)
         if (v < d.n_out) gl[v] = (expf(l[v] - mx) / s - (v == tgt ? 1.0f : 0.0f)) * scale;
     return (mx + logf(s) - lt) * scale;
 }
 
-constexpr int kFrontCh = 8;  // channels per front block
+constexpr int kFrontCh = 8;  // channels per front block (the channel count is a multiple of 8)
 
 // Per cell of range blockIdx.x, channels [8 blockIdx.y, 8 blockIdx.y + 8): the loss gradient of
 // the step's output state plus the gradient from the later steps; the clamp's backward zeroes
 // the input slice of given cells (reference src/nca/engine/ops.py:276-294): g_u; the fire mask
 // gives g_dx = g_u * fire. The block adds its sums of g_dx (db2) into its slot; the blocks of
-// channel group 0 also add the loss and the head's weight / bias gradients.
+// channel group 0 also add the loss and the head's weight / bias gradients. Every load of a cell
+// is issued before its arithmetic. n_out, c_out <= NO.
+template <int NO>
 __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
     __shared__ float red[(kThreads / 64) * 16];
     const Dims &d = a.d;
@@ -259,6 +277,14 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
     float lossv = 0.0f;
     for (int m = m0 + threadIdx.x; m < m1; m += kThreads) {
         const int row = m / d.HW, q = m - row * d.HW;
+        const int64_t cb = (int64_t)row * d.C * d.HW + q;  // channel 0 of the cell
+        float gi[kFrontCh], xo[NO];
+#pragma unroll
+        for (int j = 0; j < kFrontCh; ++j) gi[j] = a.gin ? a.gin[cb + (int64_t)(c0 + j) * d.HW] : 0.0f;
+        load_out<NO>(d, a.x1 + cb, xo);
+        const bool gv = a.given[m] != 0;
+        const int tgt = a.targets[m];
+        const float mk = a.mask ? a.mask[m] : 0.0f;
         float f;
         if (a.fire_u8) {
             f = a.fire_u8[m] ? 1.0f : 0.0f;
@@ -269,26 +295,17 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             const float uq = e4 == 0 ? u[0] : e4 == 1 ? u[1] : e4 == 2 ? u[2] : u[3];
             f = uq < a.p ? 1.0f : 0.0f;
         }
-        const int64_t cb = (int64_t)row * d.C * d.HW + q;  // channel 0 of the cell
-        float gl[16];
-        const float lc = head_grad(a, m, a.x1 + cb, gl);
+        float gl[NO];
+        const float lc = head_grad<NO>(a, xo, tgt, mk, gl);
         if (head) lossv = __fadd_rn(lossv, lc);
-        const bool gv = a.given[m] != 0;
-        float gi[kFrontCh];
 #pragma unroll
         for (int j = 0; j < kFrontCh; ++j) {
             const int c = c0 + j;
-            gi[j] = (a.gin && c < d.C) ? a.gin[cb + (int64_t)c * d.HW] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < kFrontCh; ++j) {
-            const int c = c0 + j;
-            if (c >= d.C) break;
             float g = gi[j];
             const int co = c - d.out_off;
             if (co >= 0 && co < d.c_out) {
 #pragma unroll
-                for (int v = 0; v < 16; ++v)
+                for (int v = 0; v < NO; ++v)
                     if (v < d.n_out) g = __builtin_fmaf(a.head_w[v * d.c_out + co], gl[v], g);
             }
             if (gv && c >= d.in_off && c < d.in_off + d.c_in) g = 0.0f;
@@ -299,7 +316,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
         }
     }
     const float r = block_sums<kFrontCh, kThreads / 64>(db2, red);
-    if (threadIdx.x < kFrontCh && c0 + (int)threadIdx.x < d.C) {
+    if (threadIdx.x < kFrontCh) {
         float *pp = a.part + s * a.P + a.offB2 + c0 + threadIdx.x;
         *pp = __fadd_rn(*pp, r);
     }
@@ -318,18 +335,21 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
         for (int k = 0; k < 16; ++k) acc[k] = 0.0f;
         for (int m = m0 + threadIdx.x; m < m1; m += kThreads) {
             const int row = m / d.HW, q = m - row * d.HW;
-            const float *x1c = a.x1 + (int64_t)row * d.C * d.HW + q;
-            float gl[16];
-            head_grad(a, m, x1c, gl);
+            float xo[NO], gl[NO];
+            load_out<NO>(d, a.x1 + (int64_t)row * d.C * d.HW + q, xo);
+            head_grad<NO>(a, xo, a.targets[m], a.mask ? a.mask[m] : 0.0f, gl);
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const int p = p0 + k;
                 if (p >= np) break;
                 const int v = p < npw ? p / d.c_out : p - npw, c = p < npw ? p - v * d.c_out : -1;
-                float g = 0.0f;
+                float g = 0.0f, xc = 0.0f;
 #pragma unroll
-                for (int w = 0; w < 16; ++w) g = w == v ? gl[w] : g;
-                acc[k] = c < 0 ? __fadd_rn(acc[k], g) : __builtin_fmaf(g, x1c[(int64_t)(d.out_off + c) * d.HW], acc[k]);
+                for (int w = 0; w < NO; ++w) {
+                    g = w == v ? gl[w] : g;
+                    xc = w == c ? xo[w] : xc;
+                }
+                acc[k] = c < 0 ? __fadd_rn(acc[k], g) : __builtin_fmaf(g, xc, acc[k]);
             }
         }
         const float rh = block_sums<16, kThreads / 64>(acc, red);
@@ -342,12 +362,13 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
     }
 }
 
-// The perception input of tap (dy, dx) of cell (i, j), channel c of row xr: the state (or the
-// halo value), rounded to bf16 for bf16 cells like the forward's perception buffer.
-__device__ __forceinline__ float tap_value(const float *xr, const Dims &d, int i, int j, int dy, int dx, int c,
-                                           const float *padv) {
+// The perception input of tap (dy, dx) of cell (i, j) of row xr: the state (or the halo value
+// hv), rounded to bf16 for bf16 cells like the forward's perception buffer. A halo tap loads
+// the row's first cell and discards it.
+__device__ __forceinline__ float tap_value(const float *xr, const Dims &d, int i, int j, int dy, int dx, float hv) {
     const int nq = neighbour(i, j, dy, dx, d.H, d.W, d.padding);
-    float v = nq >= 0 ? xr[nq] : (d.padding == 1 ? padv[c] : 0.0f);
+    const float x = xr[nq < 0 ? 0 : nq];
+    const float v = nq >= 0 ? x : hv;
     return d.bf16 ? nca::round_bf16(v) : v;
 }
 
@@ -359,11 +380,12 @@ __global__ void __launch_bounds__(kThreads) stencil_z_kernel(Dims d, const float
     const int e = blockIdx.x * kThreads + threadIdx.x;
     if (e >= d.C * d.HW) return;
     const int c = e / d.HW, q = e - c * d.HW, i = q / d.W, j = q - i * d.W;
+    const float hv = d.padding == 1 ? padv[c] : 0.0f;
     for (int64_t row = blockIdx.y; row < d.rows; row += gridDim.y) {
         const float *xr = x + (row * d.C + c) * (int64_t)d.HW;
         float xv[9];
 #pragma unroll
-        for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
+        for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, hv);
         const int64_t m = row * d.HW + q;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -400,17 +422,21 @@ __global__ void __launch_bounds__(kBackThreads) stencil_back_kernel(
             const int row = pl / d.C, c = pl - row * d.C, i = q / d.W, j = q - i * d.W;
             const float *xr = x + (int64_t)pl * d.HW;
             const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * d.HW;
+            const float hv = d.padding == 1 ? padv[c] : 0.0f;
             float xv[9];
 #pragma unroll
-            for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, c, padv);
+            for (int t = 0; t < 9; ++t) xv[t] = tap_value(xr, d, i, j, t / 3 - 1, t % 3 - 1, hv);
             float g = Gu[e];
 #pragma unroll
             for (int t = 0; t < 9; ++t) {
-                // cell q' whose tap t reads this cell: q = q' + (dy, dx)
+                // cell q' whose tap t reads this cell: q = q' + (dy, dx); none for a halo
                 const int qs = neighbour(i, j, -(t / 3 - 1), -(t % 3 - 1), d.H, d.W, d.padding);
-                if (qs < 0) continue;
+                const int qc = qs < 0 ? 0 : qs;
+                float gv[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], gz[k * ks + qs], g);
+                for (int k = 0; k < 4; ++k) gv[k] = gz[k * ks + qc];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) g = qs >= 0 ? __builtin_fmaf(kern[k * 9 + t], gv[k], g) : g;
             }
             gx[e] = g;
 #pragma unroll
@@ -600,6 +626,7 @@ int check_dims(const nca_cell_desc *cell, int64_t rows, int32_t H, int32_t W, in
     d->H = H;
     d->W = W;
     if ((int64_t)H * W * d->C > 0x7fffffff) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT grid too large");
+    if (d->C % 8 != 0 || cell->c_out > 16) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT needs channels % 8 == 0, c_out <= 16");
     d->HW = H * W;
     d->rows = rows;
     d->M = rows * (int64_t)H * W;
@@ -642,6 +669,12 @@ int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows
         rc = nca::hip_status(hipMemcpyAsync(states, x0, sn * sizeof(float), hipMemcpyDeviceToDevice, st), "state copy");
         if (rc) return rc;
     }
+    // the whole chunk in one launch of the streamed kernel where it takes the cell and grid
+    bool used = false;
+    if ((rc = nca::rollout_recorded(cell, packed, rows, height, width, x0, given, clamp, states + n_chunk * sn, fire,
+                                    n_chunk, states + sn, sn, st, &used)))
+        return rc;
+    if (used) return NCA_OK;
     for (int t = 0; t < n_chunk; ++t) {
         nca_fire_desc f = *fire;
         f.step0 = fire->step0 + t;
@@ -701,13 +734,17 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     hipLaunchKernelGGL(zero_f32, dim3(2048), dim3(256), 0, st, part, L.denom - L.part);
     // the fused kernel addresses z and g_z with 32-bit byte offsets
     const bool fused = d.bf16 && d.C == 32 && d.F == 128 && d.HD == 256 && d.M * d.F * 4 < ((int64_t)1 << 32);
-    if (fused && (rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(nca::mlp_back32),
+    auto mlp_kfn = (d.M & 3) == 0 ? nca::mlp_back32<true> : nca::mlp_back32<false>;
+    if (fused && (rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(mlp_kfn),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                                            (int)nca::Mb32::TOTAL),
                                        "mlp_back32 attribute")))
         return rc;
     // cells per workgroup of the fused kernel: whole 32-cell tiles
     const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
+    if (fused)
+        hipLaunchKernelGGL(nca::mlp_back32_prep, dim3(1), dim3(512), 0, st, w->w1, w->w2,
+                           reinterpret_cast<unsigned char *>(ws + L.img));
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
     if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;
 
@@ -743,7 +780,9 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
         fa.offB2 = P.B2;
         fa.offHW = P.HW;
         fa.offHB = P.HB;
-        hipLaunchKernelGGL(front_kernel, dim3(kSplit, (d.C + kFrontCh - 1) / kFrontCh), dim3(kThreads), 0, st, fa);
+        const int no = d.n_out > d.c_out ? d.n_out : d.c_out;
+        auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
+        hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
         // recompute z and h from the saved state
         const dim3 zgrid(grid_for((int64_t)d.C * d.HW), (unsigned)(d.rows < 65535 ? d.rows : 65535));
         hipLaunchKernelGGL(stencil_z_kernel, zgrid, dim3(kThreads), 0, st, d, xt, kern, padv, Z);
@@ -753,8 +792,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
             nca::MlpBackArgs ma;
             ma.Z = Z;
             ma.Gdx = Gdx;
-            ma.w1 = w->w1;
-            ma.w2 = w->w2;
+            ma.img = reinterpret_cast<const unsigned char *>(ws + L.img);
             ma.b1 = b1;
             ma.Gz = Gz;
             ma.part = part;
@@ -764,7 +802,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
             ma.offW2 = P.W2;
             ma.M = d.M;
             ma.per = per32;
-            hipLaunchKernelGGL(nca::mlp_back32, dim3(kSplit), dim3(512), nca::Mb32::TOTAL, st, ma);
+            hipLaunchKernelGGL(mlp_kfn, dim3(kSplit), dim3(512), nca::Mb32::TOTAL, st, ma);
             if ((rc = nca::hip_status(hipGetLastError(), "mlp_back32"))) return rc;
         } else {
             memset(&g, 0, sizeof(g));

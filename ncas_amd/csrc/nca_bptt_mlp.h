@@ -46,8 +46,7 @@ namespace nca {
 struct MlpBackArgs {
     const float *Z;    // z (F x M), bf16 values
     const float *Gdx;  // g_dx (C x M)
-    const float *w1;   // fp32 master W1 (HD x F)
-    const float *w2;   // fp32 master W2 (C x HD)
+    const unsigned char *img;  // the weight image written by mlp_back32_prep
     const float *b1;   // HD
     float *Gz;         // g_z (F x M)
     float *part;       // partial-sum slots, P floats each; workgroup s adds into slot s
@@ -62,6 +61,10 @@ struct Mb32 {
     static constexpr unsigned ZA = 0, ZB = ZA + 32 * ZAR, GA = ZB + 128 * ZBR, GB = GA + 3 * GPART,
                               GAL = GB + 3 * GPART, W1T = GAL + 3 * APART, B1 = W1T + 128 * AR,
                               TOTAL = B1 + 1024;
+    // weight image: W1T exactly as in LDS, then per (wave, lane) the W1 fragments [ht][kb] and
+    // the W2 fragments [ht], 16 bytes each
+    static constexpr unsigned IMG_W1T = 0, IMG_W1F = 128 * AR, IMG_W2F = IMG_W1F + 512 * 8 * 16,
+                              IMG_BYTES = IMG_W2F + 512 * 2 * 16;
 };
 
 typedef float mb_f32x4 __attribute__((ext_vector_type(4)));
@@ -94,26 +97,24 @@ __device__ __forceinline__ void mb_split8(const float v[8], uint4 p[3]) {
 }
 __device__ __forceinline__ int mb_perm(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4; }
 
-__global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+// The weight image of mlp_back32 from the fp32 master weights (rounded to bf16): W1^T in the
+// kernel's LDS layout (hidden units of each 32-block in perm order, padding zero) and the
+// register fragments of every (wave, lane). One workgroup of 512 threads.
+__global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const float *w2, unsigned char *img) {
     typedef Mb32 S;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int64_t M = a.M;
-    const int64_t mb0 = (int64_t)blockIdx.x * a.per;
-    if (mb0 >= M) return;  // uniform: an empty range adds nothing to its slot
-    const int64_t mb1 = mb0 + a.per < M ? mb0 + a.per : M;
-
-    // ---- set-up: W1^T and b1 into LDS, W1 / W2 fragments into registers
-    for (int e = tid; e < 128 * 32; e += 512) {
-        const int f = e >> 5, kb = (e >> 2) & 7, q = e & 3;
-        float v[8];
+    for (int e = tid; e < 128 * 33; e += 512) {
+        const int f = e / 33, c = e - f * 33;
+        uint4 u = {0u, 0u, 0u, 0u};
+        if (c < 32) {
+            const int kb = c >> 2, q = c & 3;
+            float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = a.w1[(32 * kb + mb_perm(q, j)) * 128 + f];
-        *reinterpret_cast<bf16x8 *>(smem + S::W1T + f * S::AR + 16 * (4 * kb + q)) = mb_pack8(v);
+            for (int j = 0; j < 8; ++j) v[j] = w1[(32 * kb + mb_perm(q, j)) * 128 + f];
+            u = __builtin_bit_cast(uint4, mb_pack8(v));
+        }
+        *reinterpret_cast<uint4 *>(img + S::IMG_W1T + f * S::AR + 16 * c) = u;
     }
-    if (tid < 256) reinterpret_cast<float *>(smem + S::B1)[tid] = a.b1[tid];
-    bf16x8 w1f[2][4];  // [ht][kb]: W1[32w + 16ht + r][32kb + 8g + j]
-    bf16x8 w2f[2];     // [ht]: W2[8g + j][32w + 16ht + r]
 #pragma unroll
     for (int ht = 0; ht < 2; ++ht) {
         const int hid = 32 * w + 16 * ht + r;
@@ -121,13 +122,40 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         for (int kb = 0; kb < 4; ++kb) {
             float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = a.w1[hid * 128 + 32 * kb + 8 * g + j];
-            w1f[ht][kb] = mb_pack8(v);
+            for (int j = 0; j < 8; ++j) v[j] = w1[hid * 128 + 32 * kb + 8 * g + j];
+            *reinterpret_cast<bf16x8 *>(img + S::IMG_W1F + (tid * 8 + 4 * ht + kb) * 16) = mb_pack8(v);
         }
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = a.w2[(8 * g + j) * 256 + hid];
-        w2f[ht] = mb_pack8(v);
+        for (int j = 0; j < 8; ++j) v[j] = w2[(8 * g + j) * 256 + hid];
+        *reinterpret_cast<bf16x8 *>(img + S::IMG_W2F + (tid * 2 + ht) * 16) = mb_pack8(v);
+    }
+}
+
+// VEC: M is a multiple of 4, so the cell quads of a tile are 16-byte aligned.
+template <bool VEC>
+__global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    typedef Mb32 S;
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t M = a.M;
+    const int64_t mb0 = (int64_t)blockIdx.x * a.per;
+    if (mb0 >= M) return;  // uniform: an empty range adds nothing to its slot
+    const int64_t mb1 = mb0 + a.per < M ? mb0 + a.per : M;
+
+    // ---- set-up: W1^T and b1 into LDS, W1 / W2 fragments into registers
+    for (int e = tid; e < (int)(128 * S::AR / 16); e += 512)
+        lds_st128(smem, S::W1T + 16 * e, *reinterpret_cast<const uint4 *>(a.img + S::IMG_W1T + 16 * e));
+    if (tid < 256) reinterpret_cast<float *>(smem + S::B1)[tid] = a.b1[tid];
+    bf16x8 w1f[2][4];  // [ht][kb]: W1[32w + 16ht + r][32kb + 8g + j]
+    bf16x8 w2f[2];     // [ht]: W2[8g + j][32w + 16ht + r]
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            w1f[ht][kb] = *reinterpret_cast<const bf16x8 *>(a.img + S::IMG_W1F + (tid * 8 + 4 * ht + kb) * 16);
+        w2f[ht] = *reinterpret_cast<const bf16x8 *>(a.img + S::IMG_W2F + (tid * 2 + ht) * 16);
     }
     mb_f32x4 dw1[2][8], dw2[2][2];  // dw1[ht][ft]: D[hid 32w+16ht+4g+i][f 16ft+r]; dw2[ct][ht]: D[ch 16ct+4g+i][hid 32w+16ht+r]
 #pragma unroll
@@ -140,9 +168,10 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
     float db1[2] = {0.f, 0.f};  // hidden 32w + 16ht + r, this lane's cells
 
     // ---- the tile's loads (prefetched one tile ahead): thread (row tid >> 2, q = tid & 3) loads
-    // cells perm(q, 0..7) of z row tid >> 2 and, for tid < 128, of g_dx row tid >> 2 (byte offsets
-    // below 2^32, checked by the host)
-    const bool vec = (M & 3) == 0;  // 16-byte aligned cell quads (tile starts are multiples of 32)
+    // cells perm(q, 0..7) of z row tid >> 2 and, in waves 0 and 1, of g_dx row tid >> 2 (byte
+    // offsets below 2^32, checked by the host). Cells past the range read cell mb0 and are zeroed
+    // when the tile is stored, so the loads need no branch and nothing uses them before then
+    // (either would make the compiler wait for them).
     const int lrow = tid >> 2, q = tid & 3;
     const unsigned char *zb = reinterpret_cast<const unsigned char *>(a.Z);
     const unsigned char *gb = reinterpret_cast<const unsigned char *>(a.Gdx);
@@ -152,31 +181,40 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t m = m0 + 16 * h + 4 * q;
-            const uint32_t off = rowb + (uint32_t)m * 4u;
-            if (vec) {
-                const float4 x = m < mb1 ? *reinterpret_cast<const float4 *>(base + off) : float4{0.f, 0.f, 0.f, 0.f};
+            if (VEC) {
+                const bool ok = m < mb1;  // the whole quad (mb1 is a multiple of 4)
+                const uint32_t off = rowb + (uint32_t)(ok ? m : mb0) * 4u;
+                const float4 x = *reinterpret_cast<const float4 *>(base + off);
                 v[4 * h] = x.x;
                 v[4 * h + 1] = x.y;
                 v[4 * h + 2] = x.z;
                 v[4 * h + 3] = x.w;
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    v[4 * h + e] = m + e < mb1 ? *reinterpret_cast<const float *>(base + off + 4 * e) : 0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = m + e < mb1;
+                    v[4 * h + e] = *reinterpret_cast<const float *>(base + rowb + (uint32_t)(ok ? m + e : mb0) * 4u);
+                }
             }
         }
     };
+    auto zero_past = [&](int64_t m0, float v[8]) {  // cells past the range
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = m0 + mb_perm(q, j) < mb1 ? v[j] : 0.0f;
+    };
     auto load_tile = [&](int64_t m0) {
         load8(zb, m0, pz);
-        if (tid < 128) load8(gb, m0, pg);
+        if (w < 2) load8(gb, m0, pg);
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int64_t m0) {
+        zero_past(m0, pz);
+        if (w < 2) zero_past(m0, pg);
         // ZB row lrow chunk q; ZA column lrow of rows perm(q, j)
         *reinterpret_cast<bf16x8 *>(smem + S::ZB + lrow * S::ZBR + 16 * q) = mb_pack8(pz);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             *reinterpret_cast<__bf16 *>(smem + S::ZA + mb_perm(q, j) * S::ZAR + 2 * lrow) = (__bf16)pz[j];
-        if (tid < 128) {  // GB row lrow chunk q; GA column lrow of rows perm(q, j); three parts
+        if (w < 2) {  // GB row lrow chunk q; GA column lrow of rows perm(q, j); three parts
             uint4 p[3];
             mb_split8(pg, p);
 #pragma unroll
@@ -194,7 +232,7 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
     load_tile(mb0);
     for (int t = 0; t < ntile; ++t) {
         const int64_t m0 = mb0 + 32 * (int64_t)t;
-        store_tile();
+        store_tile(m0);
         if (t + 1 < ntile) load_tile(m0 + 32);
         __syncthreads();
 
@@ -204,16 +242,30 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         for (int x = 0; x < 2; ++x)
 #pragma unroll
             for (int y = 0; y < 2; ++y) hT[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
+        // operands of fc1 read up front; those of g_a while fc1 finishes
+        bf16x8 zf[4][2], gf[3][2];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const unsigned zo = S::ZA + r * S::ZAR + 16 * (4 * kb + g);
-            const bf16x8 z0 = mb_ld(smem, zo), z1 = mb_ld(smem, zo + 16 * S::ZAR);
+            zf[kb][0] = mb_ld(smem, zo);
+            zf[kb][1] = mb_ld(smem, zo + 16 * S::ZAR);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
             for (int ht = 0; ht < 2; ++ht) {
-                hT[0][ht] = mb_mfma(z0, w1f[ht][kb], hT[0][ht]);
-                hT[1][ht] = mb_mfma(z1, w1f[ht][kb], hT[1][ht]);
+                hT[0][ht] = mb_mfma(zf[kb][0], w1f[ht][kb], hT[0][ht]);
+                hT[1][ht] = mb_mfma(zf[kb][1], w1f[ht][kb], hT[1][ht]);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int sp = 0; sp < 3; ++sp)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+                gf[sp][ct] = mb_ld(smem, S::GA + sp * S::GPART + (16 * ct + r) * S::GR + 16 * g);
+        __builtin_amdgcn_sched_barrier(0);
         {
             const float *b1L = reinterpret_cast<const float *>(smem + S::B1);
 #pragma unroll
@@ -236,15 +288,11 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
 #pragma unroll
             for (int y = 0; y < 2; ++y) gaT[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int sp = 2; sp >= 0; --sp) {
+        for (int sp = 2; sp >= 0; --sp)
 #pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const int cell = 16 * ct + r;
-                const bf16x8 gf = mb_ld(smem, S::GA + sp * S::GPART + cell * S::GR + 16 * g);
+            for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-                for (int ht = 0; ht < 2; ++ht) gaT[ct][ht] = mb_mfma(gf, w2f[ht], gaT[ct][ht]);
-            }
-        }
+                for (int ht = 0; ht < 2; ++ht) gaT[ct][ht] = mb_mfma(gf[sp][ct], w2f[ht], gaT[ct][ht]);
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
@@ -328,17 +376,28 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
 #pragma unroll
                 for (int y = 0; y < 2; ++y) gz[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
             const int cell = 16 * ct + r;
+            // operands of hidden block kb + 1 are read while block kb multiplies
+            const unsigned ao = S::W1T + (16 * fb + r) * S::AR + 16 * g;
+            const unsigned bo = S::GAL + cell * S::AR + 16 * g;
+            bf16x8 A[2][2], B[2][3];
+            auto ld = [&](int kb, int sl) {
+                A[sl][0] = mb_ld(smem, ao + 64 * kb);
+                A[sl][1] = mb_ld(smem, ao + 16 * S::AR + 64 * kb);
+#pragma unroll
+                for (int sp = 0; sp < 3; ++sp) B[sl][sp] = mb_ld(smem, bo + sp * S::APART + 64 * kb);
+            };
+            ld(0, 0);
 #pragma unroll
             for (int kb = 0; kb < 8; ++kb) {
-                const unsigned ko = 16 * (4 * kb + g);
-                const bf16x8 a0 = mb_ld(smem, S::W1T + (16 * fb + r) * S::AR + ko);
-                const bf16x8 a1 = mb_ld(smem, S::W1T + (16 * fb + 16 + r) * S::AR + ko);
+                if (kb + 1 < 8) ld(kb + 1, (kb + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+                const int sl = kb & 1;
 #pragma unroll
                 for (int sp = 2; sp >= 0; --sp) {
-                    const bf16x8 b = mb_ld(smem, S::GAL + sp * S::APART + cell * S::AR + ko);
-                    gz[0][kb & 1] = mb_mfma(a0, b, gz[0][kb & 1]);
-                    gz[1][kb & 1] = mb_mfma(a1, b, gz[1][kb & 1]);
+                    gz[0][sl] = mb_mfma(A[sl][0], B[sl][sp], gz[0][sl]);
+                    gz[1][sl] = mb_mfma(A[sl][1], B[sl][sp], gz[1][sl]);
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
             const int64_t m = m0 + cell;
             if (m < mb1) {

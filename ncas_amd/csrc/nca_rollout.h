@@ -51,6 +51,8 @@ struct RolloutParams {
     const uint64_t *step_seeds;  // (n_steps) or null
     float *conf_out;
     int32_t *fired_out;
+    float *x_rec;        // or null: the state after step s of the call goes to x_rec + s rec_stride
+    int64_t rec_stride;  // (the streamed C = 32 kernel only)
     int64_t rows;
     int H, W;
     int c_in, in_off, c_out, out_off, n_out, head_kind, padding;

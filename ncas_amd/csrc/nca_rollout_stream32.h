@@ -125,7 +125,8 @@ struct St32Params {
 __device__ __forceinline__ unsigned zsw(unsigned r) { return (r & 8u) | ((r & 3u) << 1) | ((r >> 2) & 1u); }
 
 // GATED: confidence-gated firing (a.adaptive), compiled out of the plain kernel
-template <bool GATED>
+// REC: also write the state after every step to a.x_rec (the BPTT chunk's forward).
+template <bool GATED, bool REC>
 __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     using S = St32;
     constexpr int NT = 512;
@@ -622,7 +623,14 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 }
                 bool ok = true;
                 if (LAST) ok = 16 * (i - 3) + cl < total;
-                if (ok) lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
+                if (ok) {
+                    lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
+                    if (REC) {  // every step's state, for the BPTT chunk
+                        float *xr = a.x_rec + (int64_t)sc * a.rec_stride + ((int64_t)row * S::C + 4 * q8) * HWn + qc;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) xr[(int64_t)v * HWn] = u[v];
+                    }
+                }
             };
             auto advance = [&]() __attribute__((always_inline)) {
                 ++i;

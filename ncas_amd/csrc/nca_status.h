@@ -4,10 +4,19 @@
 
 #include <hip/hip_runtime.h>
 
+#include "nca_hip.h"
+
 namespace nca {
 
 int set_error(int code, const char *msg);           // stores msg, returns code
 void clear_error();                                  // empties the message (start of an entry point)
 int hip_status(hipError_t e, const char *what);      // NCA_OK, or NCA_ERR_HIP with the HIP message
+
+// n_steps fused steps on the streamed C = 32 kernel that also write the state after every step
+// (step s to x_rec + s rec_stride); *used = false (nothing launched) when that kernel does not
+// take the call. The arguments are nca_rollout's, already checked by the caller.
+int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows, int H, int W, const float *x_in,
+                     const uint8_t *given, const float *clamp, float *x_out, const nca_fire_desc *fire, int n_steps,
+                     float *x_rec, int64_t rec_stride, hipStream_t st, bool *used);
 
 }  // namespace nca

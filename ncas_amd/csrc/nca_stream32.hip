@@ -77,7 +77,9 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
     sp.off_w2k = p.off_w2k;
     sp.fast_conf = p.adaptive && p.head_kind == 0 && p.n_out == 2;
     sp.conf_s = conf_threshold(p.tau);
-    auto kfn = p.adaptive ? rollout_stream32<true> : rollout_stream32<false>;
+    if (p.x_rec && p.adaptive) return hipSuccess;  // recording is for uniform firing
+    auto kfn = p.adaptive ? rollout_stream32<true, false>
+                          : (p.x_rec ? rollout_stream32<false, true> : rollout_stream32<false, false>);
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
     if (e != hipSuccess) return e;

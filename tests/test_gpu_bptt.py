@@ -126,6 +126,85 @@ def test_bptt_bf16_chunk_near_oracle(name):
     assert worst <= 1e-2
 
 
+@pytest.mark.parametrize("fire", ["seed", "step_seeds", "masks"])
+@pytest.mark.parametrize("size", [30, 13])
+def test_bptt_forward_records_every_rollout_state(fire, size):
+    """nca_bptt_forward runs a bf16 C=32 chunk as one fused launch of the streamed kernel that
+    writes the state after every step: state t equals a t-step rollout bit for bit, with Philox
+    keys, per-step keys or injected masks, on a 30x30 maze and on a 13x13 grid."""
+    from ncas_amd.rng import fire_desc
+    _say("bptt forward states", fire, size)
+    m = perturbed_model("maze_hard_c32", 2, *DYN["maze_hard_c32"])
+    b = maze_boards(3, size, 2, extra_openings=0.1)
+    x, g4, cl = initial_state(m, b, k=2, sigma=0.15, seed=2)
+    md = copy.deepcopy(m).to(DEV)
+    B, C, H, W = x.shape
+    n = 7
+    xd, gd, cd = x.to(DEV), g4.to(DEV), cl.to(DEV)
+    kw = dict(seed=5, p_fire=0.7, row0=3, step0=4)
+    ss = m8 = None
+    if fire == "step_seeds":
+        kw["step_seeds"] = [9, 2**41 + 1, 3, 4, 5, 6, 7]
+        ss = torch.as_tensor(np.asarray(kw["step_seeds"], dtype=np.int64)).to(DEV)
+    if fire == "masks":
+        g = torch.Generator().manual_seed(7)
+        masks = (torch.rand((n, B, 1, H, W), generator=g) < 0.5).float().to(DEV)
+        m8 = (masks != 0).to(torch.uint8).contiguous()
+    fd = fire_desc(kw["seed"], kw["p_fire"], None, None, True, kw["row0"], kw["step0"], ss, m8)
+    pk = md.packed("bf16", DEV)
+    states = torch.full((n + 1, B, C, H, W), float("nan"), device=DEV)
+    g8 = gd.to(torch.uint8).contiguous()
+    L = _lib.load()
+    _lib.check(L.nca_bptt_forward(ctypes.byref(pk.desc), pk.buf.data_ptr(), B, H, W, xd.data_ptr(),
+                                  g8.data_ptr(), cd.data_ptr(), ctypes.byref(fd), n,
+                                  states.data_ptr(), _lib.stream_of(DEV)), "nca_bptt_forward")
+    torch.cuda.synchronize()
+    assert torch.equal(states[0], xd)
+    with torch.no_grad():
+        for t in range(1, n + 1):
+            if fire == "masks":
+                y, _, _ = rollout_steps(md, xd, gd, cd, t, masks=masks[:t], precision="bf16")
+            else:
+                kwt = dict(kw)
+                if "step_seeds" in kwt:
+                    kwt["step_seeds"] = kwt["step_seeds"][:t]
+                y, _, _ = rollout_steps(md, xd, gd, cd, t, precision="bf16", **kwt)
+            assert torch.equal(states[t], y), t
+
+
+def test_bptt_bf16_odd_cell_count_13x13():
+    """bf16 C=32 on 13x13 boards, 3 rows (507 cells: the fused MLP backward's unaligned path, the
+    streamed forward): the single-step VJP from the GPU's state within 1e-3 of the oracle and a
+    4-step chunk within 1e-2."""
+    _say("bptt bf16 13x13")
+    m = perturbed_model("maze_hard_c32", 4, *DYN["maze_hard_c32"])
+    md = copy.deepcopy(m).to(DEV)
+    b = maze_boards(3, 13, 4, extra_openings=0.1)
+    x, g4, cl = initial_state(m, b, k=1, sigma=0.15, seed=4)
+    targets = m.output_index(torch.from_numpy(b.targets))
+    g = torch.Generator().manual_seed(5)
+    masks = (torch.rand((4, 3, 1, 13, 13), generator=g) < 0.7).float()
+    with torch.no_grad():
+        xs, _, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 5, seed=3, precision="bf16")
+    xs = xs.cpu()
+    cot = torch.randn(xs.shape, generator=torch.Generator().manual_seed(6)) * 0.01
+    res = _gpu_chunk(md, xs, g4, cl, targets, [1.0], "bf16", masks=masks[:1].to(DEV),
+                     grad_final=cot.to(DEV))
+    loss, ref = O.bptt_chunk(oracle_cell(m), xs, g4, cl, masks[:1].double(), targets, [1.0],
+                             "bf16", grad_x0=True, final_cotangent=cot.double())
+    worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
+    _say("vjp worst rel", worst)
+    assert worst <= 1e-3 and _rel(res.grad_x0, ref["x0"]) <= 1e-3
+    w = [1.0, 0.0, 0.5, 1.0]
+    res = _gpu_chunk(md, x, g4, cl, targets, w, "bf16", masks=masks.to(DEV))
+    loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, w, "bf16",
+                             grad_x0=True)
+    worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
+    _say("chunk worst rel", worst)
+    assert abs(float(res.loss) - loss) <= 1e-4 * abs(loss)
+    assert worst <= 1e-2
+
+
 def test_bptt_states_are_the_rollout_states_and_gradients_are_reproducible():
     m, md, x, g4, cl, masks, targets = _case("maze_hard_c32", steps=6)
     a = _gpu_chunk(md, x, g4, cl, targets, [1] * 6, "bf16", seed=8)
