@@ -41,6 +41,7 @@ namespace {
 
 constexpr int kSplit = 256;  // cell ranges of the split-K weight-gradient sums
 constexpr int kThreads = 256;
+constexpr int kPlaneMax = 2048;  // cells of a board whose planes the LDS stencil kernels stage
 
 struct Dims {
     int C, F, HD, c_in, in_off, c_out, out_off, n_out, padding, bf16;
@@ -79,7 +80,7 @@ ParamLayout param_layout(const Dims &d) {
 // each (slot s: the cells of range s), added to by every step of the chunk and reduced once at
 // the end; lossacc holds the loss's kSplit slots.
 struct WsLayout {
-    int64_t Z, Hb, Ga, Gz, Gdx, Gu, Gx0, Gx1, part, acc, lossacc, denom, img, total;
+    int64_t Z, Hb, Ga, Gz, Gdx, Gu, Gx0, Gx1, part, acc, lossacc, dk, denom, img, total;
 };
 
 WsLayout ws_layout(const Dims &d, int n) {
@@ -110,6 +111,8 @@ WsLayout ws_layout(const Dims &d, int n) {
     o = al(o + P.P);
     L.lossacc = o;
     o = al(o + kSplit);
+    L.dk = o;  // kernel-weight slots of the plane kernels, one per (row, channel)
+    o = al(o + (d.HW <= kPlaneMax ? d.rows * d.C * 36 : 0));
     L.denom = o;
     o = al(o + 1);
     L.img = o;  // weight image of the fused MLP backward
@@ -265,12 +268,19 @@ constexpr int kFrontCh = 8;  // channels per front block (the channel count is a
 // is issued before its arithmetic. n_out, c_out <= NO.
 template <int NO>
 __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
-    __shared__ float red[(kThreads / 64) * 16];
+    __shared__ float red[(kThreads / 64) * 32];
     const Dims &d = a.d;
     const int s = blockIdx.x, c0 = kFrontCh * blockIdx.y;
     const int per = (int)((d.M + kSplit - 1) / kSplit), m0 = s * per;
     const int m1 = m0 + per < (int)d.M ? m0 + per : (int)d.M;
     const bool head = blockIdx.y == 0;
+    // small heads (n_out, c_out <= 4): the head's gradient sums kept in registers, hs[v NO + c] of
+    // g_l[v] x1[out_off + c] and hs[NO NO + v] of g_l[v]
+    constexpr bool kRegHead = NO <= 4;
+    constexpr int NP = NO * NO + NO;
+    float hs[kRegHead ? NP : 1];
+#pragma unroll
+    for (int p = 0; p < (kRegHead ? NP : 1); ++p) hs[p] = 0.0f;
     float db2[kFrontCh];
 #pragma unroll
     for (int j = 0; j < kFrontCh; ++j) db2[j] = 0.0f;
@@ -298,6 +308,14 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
         float gl[NO];
         const float lc = head_grad<NO>(a, xo, tgt, mk, gl);
         if (head) lossv = __fadd_rn(lossv, lc);
+        if (kRegHead && head) {
+#pragma unroll
+            for (int v = 0; v < NO; ++v) {
+#pragma unroll
+                for (int c = 0; c < NO; ++c) hs[v * NO + c] = __builtin_fmaf(gl[v], xo[c], hs[v * NO + c]);
+                hs[NO * NO + v] = __fadd_rn(hs[NO * NO + v], gl[v]);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < kFrontCh; ++j) {
             const int c = c0 + j;
@@ -314,6 +332,34 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             a.Gdx[(int64_t)c * d.M + m] = gd;
             db2[j] = __fadd_rn(db2[j], gd);
         }
+    }
+    if (kRegHead && head) {  // one reduction: db2, the loss and the head's sums
+        constexpr int NV = kFrontCh + 1 + (kRegHead ? NP : 0);
+        float vals[NV];
+#pragma unroll
+        for (int j = 0; j < kFrontCh; ++j) vals[j] = db2[j];
+        vals[kFrontCh] = lossv;
+#pragma unroll
+        for (int p = 0; p < NV - kFrontCh - 1; ++p) vals[kFrontCh + 1 + p] = hs[p];
+        const float r = block_sums<NV, kThreads / 64>(vals, red);
+        const int t = threadIdx.x;
+        float *ps = a.part + s * a.P;
+        if (t < kFrontCh) {
+            ps[a.offB2 + c0 + t] = __fadd_rn(ps[a.offB2 + c0 + t], r);
+        } else if (t == kFrontCh) {
+            if (a.wscale != 0.0f) a.lossacc[s] = __fadd_rn(a.lossacc[s], r);
+        } else if (t < NV && a.wscale != 0.0f) {
+            const int p = t - kFrontCh - 1;
+            int o = -1;
+            if (p < NO * NO) {
+                const int v = p / NO, c = p - v * NO;
+                if (v < a.d.n_out && c < a.d.c_out) o = (int)a.offHW + v * a.d.c_out + c;
+            } else if (p - NO * NO < a.d.n_out) {
+                o = (int)a.offHB + p - NO * NO;
+            }
+            if (o >= 0) ps[o] = __fadd_rn(ps[o], r);
+        }
+        return;
     }
     const float r = block_sums<kFrontCh, kThreads / 64>(db2, red);
     if (threadIdx.x < kFrontCh) {
@@ -458,6 +504,137 @@ __global__ void __launch_bounds__(kBackThreads) stencil_back_kernel(
         float *pp = part + blockIdx.x * P + offK + threadIdx.x;
         *pp = __fadd_rn(*pp, r);
     }
+}
+
+// The 3x3 taps of cell (i, j) from a plane staged in LDS (halo value hv), rounded to bf16 for
+// bf16 cells.
+__device__ __forceinline__ void plane_taps(const float *xs, const Dims &d, int i, int j, float hv, float xv[9]) {
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+        const int nq = neighbour(i, j, t / 3 - 1, t % 3 - 1, d.H, d.W, d.padding);
+        const float v = nq >= 0 ? xs[nq < 0 ? 0 : nq] : hv;
+        xv[t] = d.bf16 ? nca::round_bf16(v) : v;
+    }
+}
+
+// stencil_z for boards of at most kPlaneMax cells: workgroup p stages plane p = (row, channel)
+// of x in LDS and writes that channel's 4 features of the row's cells.
+__global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float *__restrict__ x,
+                                                            const float *__restrict__ kern,
+                                                            const float *__restrict__ padv, float *__restrict__ Z) {
+    extern __shared__ float xs[];  // HW floats
+    const int pl = blockIdx.x, row = pl / d.C, c = pl - row * d.C;
+    const float *xr = x + (int64_t)pl * d.HW;
+    // staged 8 cells per thread at a time, every load issued before the LDS writes
+    for (int q0 = 0; q0 < d.HW; q0 += 8 * kThreads) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u * kThreads + threadIdx.x;
+            v[u] = xr[q < d.HW ? q : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u * kThreads + threadIdx.x;
+            if (q < d.HW) xs[q] = v[u];
+        }
+    }
+    __syncthreads();
+    const float hv = d.padding == 1 ? padv[c] : 0.0f;
+    for (int q = threadIdx.x; q < d.HW; q += kThreads) {
+        const int i = q / d.W, j = q - i * d.W;
+        float xv[9];
+        plane_taps(xs, d, i, j, hv, xv);
+        const int64_t m = (int64_t)row * d.HW + q;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
+            Z[(int64_t)(k * d.C + c) * d.M + m] = d.bf16 ? nca::round_bf16(acc) : acc;
+        }
+    }
+}
+
+// stencil_back for boards of at most kPlaneMax cells: workgroup p stages plane p = (row,
+// channel) of x and the channel's 4 planes of g_z in LDS; g_x of the plane's cells, and the
+// plane's kernel-weight sums added into its own slot dk[p][36].
+__global__ void __launch_bounds__(kThreads) stencil_back_plane(Dims d, const float *__restrict__ x,
+                                                               const float *__restrict__ Gu,
+                                                               const float *__restrict__ Gz,
+                                                               const float *__restrict__ kern,
+                                                               const float *__restrict__ padv,
+                                                               float *__restrict__ gx, float *__restrict__ dk) {
+    extern __shared__ float xs[];  // x plane, then the 4 g_z planes: 5 HW floats
+    __shared__ float red[(kThreads / 64) * 36];
+    float *gs = xs + d.HW;
+    const int pl = blockIdx.x, row = pl / d.C, c = pl - row * d.C;
+    const float *xr = x + (int64_t)pl * d.HW;
+    const int64_t ks = (int64_t)d.C * d.M;
+    const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * d.HW;
+    // staged 4 cells per thread at a time, every load issued before the LDS writes
+    for (int q0 = 0; q0 < d.HW; q0 += 4 * kThreads) {
+        float v[4][5];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * kThreads + threadIdx.x, qc = q < d.HW ? q : 0;
+            v[u][0] = xr[qc];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[u][1 + k] = gz[k * ks + qc];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int q = q0 + u * kThreads + threadIdx.x;
+            if (q < d.HW) {
+                xs[q] = v[u][0];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) gs[k * d.HW + q] = v[u][1 + k];
+            }
+        }
+    }
+    __syncthreads();
+    const float hv = d.padding == 1 ? padv[c] : 0.0f;
+    float acc[36];
+#pragma unroll
+    for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
+    for (int q = threadIdx.x; q < d.HW; q += kThreads) {
+        const int i = q / d.W, j = q - i * d.W;
+        float xv[9];
+        plane_taps(xs, d, i, j, hv, xv);
+        const int64_t e = (int64_t)pl * d.HW + q;
+        float g = Gu[e];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+            // cell q' whose tap t reads this cell: q = q' + (dy, dx); none for a halo
+            const int qs = neighbour(i, j, -(t / 3 - 1), -(t % 3 - 1), d.H, d.W, d.padding);
+            const int qc = qs < 0 ? 0 : qs;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) g = qs >= 0 ? __builtin_fmaf(kern[k * 9 + t], gs[k * d.HW + qc], g) : g;
+        }
+        gx[e] = g;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float gzv = gs[k * d.HW + q];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gzv, xv[t], acc[k * 9 + t]);
+        }
+    }
+    const float r = block_sums<36, kThreads / 64>(acc, red);
+    if (threadIdx.x < 36) {
+        float *pp = dk + (int64_t)pl * 36 + threadIdx.x;
+        *pp = __fadd_rn(*pp, r);
+    }
+}
+
+// acc[v] += the sum of the planes' kernel-weight slots: block v, each thread a fixed strided
+// subset of the planes, then a fixed tree.
+__global__ void __launch_bounds__(kThreads) reduce_dk(const float *dk, int64_t planes, float *acc) {
+    __shared__ float red[kThreads];
+    const int v = blockIdx.x;
+    float s = 0.0f;
+    for (int64_t p = threadIdx.x; p < planes; p += kThreads) s = __fadd_rn(s, dk[p * 36 + v]);
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) acc[v] = __fadd_rn(acc[v], s);
 }
 
 // Row sums of a feature-major matrix G (R x M) over the kSplit cell ranges, added into the
@@ -740,6 +917,8 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
                                                            (int)nca::Mb32::TOTAL),
                                        "mlp_back32 attribute")))
         return rc;
+    // boards small enough to stage (row, channel) planes in LDS
+    const bool planes_ok = d.HW <= kPlaneMax && d.rows * d.C <= 0x7fffffff;
     // cells per workgroup of the fused kernel: whole 32-cell tiles
     const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
     if (fused)
@@ -784,8 +963,13 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
         auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
         hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
         // recompute z and h from the saved state
-        const dim3 zgrid(grid_for((int64_t)d.C * d.HW), (unsigned)(d.rows < 65535 ? d.rows : 65535));
-        hipLaunchKernelGGL(stencil_z_kernel, zgrid, dim3(kThreads), 0, st, d, xt, kern, padv, Z);
+        if (planes_ok) {
+            hipLaunchKernelGGL(stencil_z_plane, dim3((unsigned)(d.rows * d.C)), dim3(kThreads), d.HW * sizeof(float), st,
+                               d, xt, kern, padv, Z);
+        } else {
+            const dim3 zgrid(grid_for((int64_t)d.C * d.HW), (unsigned)(d.rows < 65535 ? d.rows : 65535));
+            hipLaunchKernelGGL(stencil_z_kernel, zgrid, dim3(kThreads), 0, st, d, xt, kern, padv, Z);
+        }
         if ((rc = nca::hip_status(hipGetLastError(), "bptt front / stencil"))) return rc;
         GemmArgs g;
         if (fused) {
@@ -828,8 +1012,12 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
             if ((rc = gemm(g, 1, st))) return rc;
         }
         // gradient of the step's input state and the kernel-weight partials
-        hipLaunchKernelGGL(stencil_back_kernel, dim3(kSplit), dim3(kBackThreads), 0, st, d, xt, Gu, Gz, kern, padv, gx,
-                           part, P.P, P.K);
+        if (planes_ok)
+            hipLaunchKernelGGL(stencil_back_plane, dim3((unsigned)(d.rows * d.C)), dim3(kThreads),
+                               5 * d.HW * sizeof(float), st, d, xt, Gu, Gz, kern, padv, gx, ws + L.dk);
+        else
+            hipLaunchKernelGGL(stencil_back_kernel, dim3(kSplit), dim3(kBackThreads), 0, st, d, xt, Gu, Gz, kern, padv,
+                               gx, part, P.P, P.K);
         if (!fused) {
             // weight-gradient partials over kSplit cell ranges
             const int64_t kps = (((d.M + kSplit - 1) / kSplit) + GBK - 1) / GBK * GBK;
@@ -853,6 +1041,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     }
     // the slots summed in slot order
     hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
+    if (planes_ok) hipLaunchKernelGGL(reduce_dk, dim3(36), dim3(kThreads), 0, st, ws + L.dk, d.rows * d.C, acc + P.K);
     if (grad_x0) {
         if (n_chunk == 0 || d.M == 0) {
             if (grad_final) hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, grad_final, grad_x0, sn);
