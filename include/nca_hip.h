@@ -214,10 +214,11 @@ const char *nca_last_error(void);
 int nca_version(void);
 
 /* Kernel selection: 0 = automatic (the streamed bf16 kernel where the grid allows it, the
- * resident kernel where the rows fit LDS, else the halo-tiled per-step kernel), 1 = never the
- * streamed kernel, 2 = always the halo-tiled per-step kernel. Process-wide; used by the tests to
- * check the paths against each other and by the bench to time the per-step regime. No
- * counterpart in the reference. */
+ * resident kernel where the rows fit LDS, else the per-step path: the wave-per-tile kernel for
+ * bf16 cells with 16 channels, the halo-window kernel otherwise), 1 = never the streamed kernel,
+ * 2 = always the per-step path, 3 = always the per-step path on the halo-window kernel.
+ * Process-wide; used by the tests to check the paths against each other and by the bench to time
+ * the per-step regime. No counterpart in the reference. */
 int nca_set_kernel_path(int path);
 
 #ifdef __cplusplus

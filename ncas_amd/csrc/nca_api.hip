@@ -278,7 +278,7 @@ bool resident_fits(bool bf, int64_t rows, int H, int W, int c_in, int c_out, int
 
 // Does the call run on the LDS-resident kernels (true) or the halo-tiled per-step kernel?
 bool takes_resident(const nca_cell_desc *d, int64_t rows, int H, int W) {
-    if (g_path == 2) return false;
+    if (g_path >= 2) return false;
     const bool bf = d->precision == NCA_BF16;
     const int C = d->channels, HD = d->hidden;
     if (C == 16 && HD == 128) return resident_fits<16, 128>(bf, rows, H, W, d->c_in, d->c_out, d->n_out);
@@ -368,7 +368,7 @@ int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t s
             q.noise = s == 0 ? p.noise : nullptr;
             bool ok = false;
             int rc = hip_check(nca::tiled_step(d->channels, d->hidden, d->precision == NCA_BF16, q, s, s == 0,
-                                               s == 0, last, st, &ok),
+                                               s == 0, last, st, g_path == 3, &ok),
                                "tiled step launch");
             if (rc) return rc;
             if (!ok)
@@ -510,7 +510,7 @@ const char *nca_last_error(void) { return g_err; }
 int nca_version(void) { return 100; }
 
 int nca_set_kernel_path(int path) {
-    if (path < 0 || path > 2) return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic, 2 tiled)", path);
+    if (path < 0 || path > 3) return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic, 2 tiled, 3 windows)", path);
     g_path = path;
     return NCA_OK;
 }

@@ -1,0 +1,346 @@
+// Per-step kernel for bf16 cells with C = 16 channels and 128 hidden units on grids of any size
+// (gfx950): one NCA step of every row, x_in -> x_out, each wave on its own 16-cell tiles.
+//
+// A tile is 16 consecutive cells q0 .. q0 + 15 of one row in raster order. Lane (r = lane & 15,
+// g = lane >> 4) owns cell q0 + r, channel quad g, for the whole tile:
+//   1. its 9 taps: the 16-byte quad g of the 3x3 neighbours (cell-major state), or the padding
+//      value for a neighbour outside the grid (wall: pad_vec, zero: 0, wrap: the wrapped cell;
+//      reference src/nca/model.py:140-152), with the cell's given flag, injected mask and clamp
+//      values, all loaded for the next tile while this one computes (vmcnt counts in order, so a
+//      tile's own loads must all be older than the next tile's);
+//   2. the 3x3 perception of its 4 channels on v_dot2_f32_bf16 over tap pairs (the taps rounded
+//      to bf16 like the forward's perception buffer) -> z, through a wave-private LDS block to
+//      the fc1 operand layout;
+//   3. fc1 on v_mfma_f32_16x16x32_bf16 (W1 fragments in registers, b1 from LDS as the initial
+//      accumulators), ReLU and bf16 rounding, through the wave's LDS block to fc2's operand
+//      layout (hidden units in natural order, so every sum runs in the same order as in the
+//      halo-window and resident kernels and the results are theirs bit for bit);
+//   4. fc2: D[channel 4g + i][cell r] = the lane's own quad, so the residual update, the fire
+//      mask (Philox keyed on (seed; row, step, cell quad) like every kernel, or an injected
+//      mask) and the clamp (the input slice of given cells keeps its value; the first step of a
+//      call takes the clamp tensor's) need no other lane.
+// No workgroup barrier: a workgroup's waves share only the b1 vector in LDS. Workgroup b takes a
+// contiguous range of tiles (so most neighbour rows are in its XCD's L2); its waves interleave.
+// The first step of a call may read the caller's NCHW state and the last may write it
+// (IN_NCHW / OUT_NCHW); the steps between use the cell-major state (rows, H, W, C).
+#pragma once
+
+#include "nca_stream_util.h"
+
+namespace nca {
+
+struct Step16Params {
+    RolloutParams a;  // x_in -> x_out of this step
+    int step;         // step index within the call (Philox counter step0 + step, mask slice)
+    int first;        // first step of a call: the clamp tensor's values for the clamped channels
+    int64_t n_tiles;  // rows * tiles_per_row
+    int tiles_per_row;
+    int64_t tiles_per_wg;
+};
+
+typedef float s16_f32x4 __attribute__((ext_vector_type(4)));
+
+template <bool IN_NCHW, bool OUT_NCHW>
+__global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
+    constexpr int C = 16, HD = 128;
+    const RolloutParams &a = sp.a;
+    __shared__ float b1L[HD];
+    // per wave: z (16 cells x 64 bf16, 144-byte rows) and h (16 cells x 128 bf16, 272-byte rows)
+    __shared__ __attribute__((aligned(16))) unsigned char zL[8][16 * 144 + 16 * 272];
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int H = a.H, W = a.W, HWn = H * W;
+
+    // ---- constants: stencil kernels as bf16 pairs, W1 / W2 fragments, biases
+    const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
+    uint32_t kp[4][5];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) kp[k][pr] = pack_bf16x2(kern[k * 9 + 2 * pr], kern[k * 9 + 2 * pr + 1]);
+        kp[k][4] = pack_bf16x2(kern[k * 9 + 8], 0.0f);
+    }
+    bf16x8 w1f[8][2];  // [m-tile][k-tile]: W1[16 mt + r][32 kt + 8g + j]
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+            w1f[mt][kt] = reinterpret_cast<const bf16x8 *>(a.packed + a.off_w1)[((size_t)mt * 2 + kt) * 64 + lane];
+    bf16x8 w2f[4];  // [k-tile]: W2[r][32 kt + 8g + j]
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) w2f[kt] = reinterpret_cast<const bf16x8 *>(a.packed + a.off_w2)[(size_t)kt * 64 + lane];
+    const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
+    const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
+    if (tid < HD) b1L[tid] = b1[tid];
+    float b2v[4];
+    bool insl[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        b2v[v] = b2[4 * g + v];
+        insl[v] = 4 * g + v >= a.in_off && 4 * g + v < a.in_off + a.c_in;
+    }
+    const float4 pq = a.padding == 1 ? reinterpret_cast<const float4 *>(a.packed + a.off_padv)[g]
+                                     : float4{0.f, 0.f, 0.f, 0.f};
+    const uint32_t pqb[2] = {pack_bf16x2(pq.x, pq.y), pack_bf16x2(pq.z, pq.w)};
+    const uint64_t key = a.step_seeds ? a.step_seeds[sp.step] : a.seed;
+    __syncthreads();
+
+    // ---- this wave's tiles: t = t0 + w, t0 + w + 8, ... within the workgroup's range
+    const int64_t t_begin = (int64_t)blockIdx.x * sp.tiles_per_wg;
+    int64_t t_end = t_begin + sp.tiles_per_wg;
+    if (t_end > sp.n_tiles) t_end = sp.n_tiles;
+    unsigned char *zw = zL[w];
+    unsigned char *hw = zL[w] + 16 * 144;
+
+    // everything tile t loads: taps (float4 per tap), given flag, injected mask, clamp values
+    struct TileIn {
+        float4 tp[9];  // raw loads; halo taps are replaced by the padding value when packed
+        float fin;     // the injected float mask's value
+        float cv[4];
+        int gv, fu8;  // raw bytes (converting them here would wait for their loads)
+        int padm;     // bit tt: tap tt is a constant halo cell (wall / zero padding)
+    };
+    const bool wrap = a.padding == 2;
+    // the tile at (row, tile tir of the row): cells q0 = 16 tir .. q0 + 15
+    auto load_tile = [&](int64_t row, int tir, TileIn &in) {
+        const int q0 = 16 * tir, q = q0 + r;
+        const int i0 = q0 / W, j0 = q0 - i0 * W;  // uniform
+        int i, j;
+        if (q >= HWn) {
+            i = H - 1;
+            j = W - 1;
+        } else if (W >= 16) {  // at most one row boundary within the tile
+            const int jj = j0 + r;
+            const bool nx = jj >= W;
+            i = i0 + (nx ? 1 : 0);
+            j = jj - (nx ? W : 0);
+        } else {
+            i = q / W;
+            j = q - i * W;
+        }
+        const int qc = i * W + j;
+        // neighbour offsets in cells by row (dy) and column (dx), wrapped at the grid's edge (for
+        // wall / zero padding the wrapped cell is loaded and replaced), and the halo flags
+        const int ro[3] = {i > 0 ? -W : (H - 1) * W, 0, i < H - 1 ? W : -(H - 1) * W};
+        const int co[3] = {j > 0 ? -1 : W - 1, 0, j < W - 1 ? 1 : -(W - 1)};
+        const bool rp[3] = {i == 0 && !wrap, false, i == H - 1 && !wrap};
+        const bool cp[3] = {j == 0 && !wrap, false, j == W - 1 && !wrap};
+        in.padm = 0;
+#pragma unroll
+        for (int tt = 0; tt < 9; ++tt) {
+            const int dy = tt / 3, dx = tt % 3;
+            in.padm |= (rp[dy] || cp[dx]) ? 1 << tt : 0;
+            if (IN_NCHW) {
+                const float *xr = a.x_in + (row * C + 4 * g) * (int64_t)HWn + qc + ro[dy] + co[dx];
+                in.tp[tt] = float4{xr[0], xr[HWn], xr[2 * HWn], xr[3 * HWn]};
+            } else {
+                // byte offset from the state's base, below 2^32 (checked by the host)
+                const uint32_t off = ((uint32_t)(row * HWn) + (uint32_t)(qc + ro[dy] + co[dx])) * (uint32_t)(4 * C) +
+                                     16u * (uint32_t)g;
+                in.tp[tt] = *reinterpret_cast<const float4 *>(reinterpret_cast<const unsigned char *>(a.x_in) + off);
+            }
+        }
+        in.gv = a.given[row * HWn + qc];
+        in.fin = 0.0f;
+        in.fu8 = 0;
+        if (a.fire_f32) in.fin = a.fire_f32[row * HWn + qc];
+        if (a.fire_u8) in.fu8 = a.fire_u8[((int64_t)sp.step * a.rows + row) * HWn + qc];
+        if (sp.first) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int ci = insl[v] ? 4 * g + v - a.in_off : 0;
+                in.cv[v] = a.c_in > 0 ? a.clamp[(row * a.c_in + ci) * (int64_t)HWn + qc] : 0.0f;
+            }
+        }
+    };
+
+    int64_t cur_row = -1;
+    int fired_run = 0;  // fired cells of cur_row counted by this wave, not yet added
+    auto flush_fired = [&]() {
+        int s = fired_run;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+        if (lane == 0 && s && a.fired_out) atomicAdd(a.fired_out + cur_row, s);
+        fired_run = 0;
+    };
+
+    // what the compute of a tile keeps of its loads: the taps as bf16 pairs (halo taps replaced
+    // by the padding value), the cell's fp32 quad, flags and mask / clamp values
+    struct TileCur {
+        uint32_t tb[9][2];
+        float xo[4], fin, cv[4];
+        int gv, fu8;
+    };
+    auto unpack = [&](const TileIn &in, TileCur &cu) __attribute__((always_inline)) {
+#pragma unroll
+        for (int tt = 0; tt < 9; ++tt) {
+            const bool pad = (in.padm >> tt) & 1;
+            cu.tb[tt][0] = pad ? pqb[0] : pack_bf16x2(in.tp[tt].x, in.tp[tt].y);
+            cu.tb[tt][1] = pad ? pqb[1] : pack_bf16x2(in.tp[tt].z, in.tp[tt].w);
+        }
+        cu.xo[0] = in.tp[4].x;
+        cu.xo[1] = in.tp[4].y;
+        cu.xo[2] = in.tp[4].z;
+        cu.xo[3] = in.tp[4].w;
+        cu.fin = in.fin;
+        cu.gv = in.gv;
+        cu.fu8 = in.fu8;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) cu.cv[v] = in.cv[v];
+    };
+    // Philox fire bits of 4 tiles at a time: lane (r, g) draws cell r of the wave's tile g tiles
+    // ahead (one evaluation per cell quad, its element r & 3: tiles start at multiples of 16
+    // cells), and a ballot gives bit 16 k + r = cell r of tile k
+    uint64_t fmask = 0;
+    int kgrp = 0;
+    const int tpr = sp.tiles_per_row;
+    auto draw4 = [&](int64_t row, int tir) {
+        int ti = tir + 8 * g;
+        int64_t rw = row;
+        while (ti >= tpr) {
+            ti -= tpr;
+            ++rw;
+        }
+        float u4[4];
+        const uint32_t qd = (uint32_t)((16 * ti + r) >> 2);
+        cell_uniforms4(key, (uint32_t)(a.row0 + rw), (uint32_t)(a.step0 + sp.step), qd, u4);
+        const int e4 = r & 3;
+        const float uq = e4 == 0 ? u4[0] : e4 == 1 ? u4[1] : e4 == 2 ? u4[2] : u4[3];
+        fmask = __ballot(uq < a.p);
+    };
+    // one tile: the cells' new states to x_out
+    auto process = [&](const TileCur &cur, int64_t row, int tir) __attribute__((always_inline)) {
+        const int q = 16 * tir + r;
+        const bool valid = q < HWn;
+        const int qc = valid ? q : HWn - 1;
+
+        // 2. perception: bf16 tap pairs per channel, v_dot2 against the kernel pairs
+        {
+            const uint32_t(&tb)[9][2] = cur.tb;  // taps as bf16 pairs (channels 0,1 and 2,3)
+            uint32_t pr[5][4];  // [tap pair][channel]
+#pragma unroll
+            for (int p2 = 0; p2 < 4; ++p2) {
+                const uint32_t *x0 = tb[2 * p2], *x1 = tb[2 * p2 + 1];
+                pr[p2][0] = __builtin_amdgcn_perm(x1[0], x0[0], 0x05040100u);
+                pr[p2][1] = __builtin_amdgcn_perm(x1[0], x0[0], 0x07060302u);
+                pr[p2][2] = __builtin_amdgcn_perm(x1[1], x0[1], 0x05040100u);
+                pr[p2][3] = __builtin_amdgcn_perm(x1[1], x0[1], 0x07060302u);
+            }
+            pr[4][0] = tb[8][0] & 0xffffu;
+            pr[4][1] = tb[8][0] >> 16;
+            pr[4][2] = tb[8][1] & 0xffffu;
+            pr[4][3] = tb[8][1] >> 16;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float z[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int p2 = 0; p2 < 5; ++p2)
+                        s = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), s, false);
+                    z[c] = s;
+                }
+                // feature k C + 4g + c of cell r
+                *reinterpret_cast<uint2 *>(zw + r * 144 + 2 * (k * C + 4 * g)) =
+                    uint2{pack_bf16x2(z[0], z[1]), pack_bf16x2(z[2], z[3])};
+            }
+        }
+        // 3. fc1 (the LDS block is this wave's own: its writes above precede these reads, a
+        // wave's LDS operations complete in order)
+        __builtin_amdgcn_wave_barrier();
+        const bf16x8 zf0 = *reinterpret_cast<const bf16x8 *>(zw + r * 144 + 16 * g);
+        const bf16x8 zf1 = *reinterpret_cast<const bf16x8 *>(zw + r * 144 + 64 + 16 * g);
+        s16_f32x4 h[8];
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+            const float4 bq = *reinterpret_cast<const float4 *>(b1L + 16 * mt + 4 * g);
+            h[mt] = s16_f32x4{bq.x, bq.y, bq.z, bq.w};
+            h[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][0], zf0, h[mt], 0, 0, 0);
+            h[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][1], zf1, h[mt], 0, 0, 0);
+        }
+        // 4. fc2 on the ReLU'd bf16 activations (hidden 16 mt + 4g + i of cell r to the wave's
+        // LDS block, read back as 8 consecutive hidden units), then the update of this lane's quad
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt)  // bf16 rounding, then ReLU on the packed pairs
+            *reinterpret_cast<uint2 *>(hw + r * 272 + 2 * (16 * mt + 4 * g)) =
+                uint2{relu_bf16x2(cvt_pk_bf16(h[mt][0], h[mt][1])), relu_bf16x2(cvt_pk_bf16(h[mt][2], h[mt][3]))};
+        __builtin_amdgcn_wave_barrier();
+        s16_f32x4 dx = s16_f32x4{b2v[0], b2v[1], b2v[2], b2v[3]};
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) {
+            const bf16x8 hf = *reinterpret_cast<const bf16x8 *>(hw + r * 272 + 2 * (32 * kt + 8 * g));
+            dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[kt], hf, dx, 0, 0, 0);
+        }
+        float f;
+        if (a.fire_f32) {
+            f = cur.fin;
+        } else if (a.fire_u8) {
+            f = cur.fu8 ? 1.0f : 0.0f;
+        } else {
+            f = ((fmask >> (16 * kgrp + r)) & 1ull) ? 1.0f : 0.0f;
+        }
+        const bool gv = cur.gv != 0;
+        float xo[4] = {cur.xo[0], cur.xo[1], cur.xo[2], cur.xo[3]};
+        if (sp.first && gv) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (insl[v]) xo[v] = cur.cv[v];
+        }
+        float u[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float uv = __fadd_rn(xo[v], __fmul_rn(f, round_bf16(dx[v])));
+            u[v] = (gv && insl[v]) ? xo[v] : uv;
+        }
+        if (valid) {
+            if (OUT_NCHW) {
+                float *xr = a.x_out + (row * C + 4 * g) * (int64_t)HWn + q;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) xr[(int64_t)v * HWn] = u[v];
+            } else {
+                *reinterpret_cast<float4 *>(a.x_out + (row * HWn + q) * C + 4 * g) = make_float4(u[0], u[1], u[2], u[3]);
+            }
+        }
+        // fired cells, counted once per cell (quad 0) and added per row
+        if (a.fired_out) {
+            if (row != cur_row) {
+                if (cur_row >= 0) flush_fired();
+                cur_row = row;
+            }
+            fired_run += (valid && g == 0 && f != 0.0f) ? 1 : 0;
+        }
+    };
+
+    // the wave's tiles t = t_begin + w + 8k, at (row, tile of the row) tracked without division;
+    // two load buffers alternate so that the next tile's loads are in flight during this one
+    int64_t t = t_begin + w;
+    int64_t row = t / tpr;
+    int tir = (int)(t - row * tpr);
+    auto advance = [&](int64_t &rw, int &ti) {
+        ti += 8;
+        while (ti >= tpr) {
+            ti -= tpr;
+            ++rw;
+        }
+    };
+    TileIn nx;
+    if (t < t_end) load_tile(row, tir, nx);
+    const bool philox = !a.fire_f32 && !a.fire_u8;
+    for (; t < t_end; t += 8) {
+        TileCur cu;
+        unpack(nx, cu);  // this tile's loads, consumed before the buffer takes the next tile's
+        int64_t rn = row;
+        int tn = tir;
+        advance(rn, tn);
+        if (t + 8 < t_end) load_tile(rn, tn, nx);
+        if (philox && kgrp == 0) draw4(row, tir);
+        process(cu, row, tir);
+        kgrp = (kgrp + 1) & 3;
+        row = rn;
+        tir = tn;
+    }
+    if (a.fired_out && cur_row >= 0) flush_fired();
+}
+
+}  // namespace nca

@@ -3,6 +3,7 @@
 
 #include <string.h>
 
+#include "nca_step16.h"
 #include "nca_tiled_launch.h"
 #include "nca_tiled.h"
 
@@ -84,11 +85,34 @@ hipError_t launch_cell(bool bf16, const RolloutParams &p, int step, int first, i
                    : launch<C, HD, false, false>(p, step, first, in_nchw, out_nchw, st, ok);
 }
 
+template <bool IN_NCHW, bool OUT_NCHW>
+hipError_t launch_stream16(const RolloutParams &p, int step, int first, hipStream_t st) {
+    Step16Params sp;
+    memset(&sp, 0, sizeof(sp));
+    sp.a = p;
+    sp.step = step;
+    sp.first = first;
+    sp.tiles_per_row = (p.H * p.W + 15) / 16;
+    sp.n_tiles = p.rows * (int64_t)sp.tiles_per_row;
+    static const int n_cu = cu_count();
+    sp.tiles_per_wg = (sp.n_tiles + n_cu - 1) / n_cu;
+    const int64_t grid = (sp.n_tiles + sp.tiles_per_wg - 1) / sp.tiles_per_wg;
+    if (grid < 1) return hipSuccess;
+    hipLaunchKernelGGL((step_stream16<IN_NCHW, OUT_NCHW>), dim3((unsigned)grid), dim3(512), 0, st, sp);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, int in_nchw,
-                      int out_nchw, hipStream_t st, bool *ok) {
+                      int out_nchw, hipStream_t st, bool windows, bool *ok) {
     *ok = false;
+    if (C == 16 && HD == 128 && bf16 && !windows && !p.noise && !p.adaptive) {
+        *ok = true;
+        if (in_nchw)
+            return out_nchw ? launch_stream16<true, true>(p, step, first, st) : launch_stream16<true, false>(p, step, first, st);
+        return out_nchw ? launch_stream16<false, true>(p, step, first, st) : launch_stream16<false, false>(p, step, first, st);
+    }
     if (C == 16 && HD == 128) return launch_cell<16, 128>(bf16, p, step, first, in_nchw, out_nchw, st, ok);
     if (C == 32 && HD == 256) return launch_cell<32, 256>(bf16, p, step, first, in_nchw, out_nchw, st, ok);
     if (C == 64 && HD == 256) return launch_cell<64, 256>(bf16, p, step, first, in_nchw, out_nchw, st, ok);

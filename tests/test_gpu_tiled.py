@@ -7,6 +7,9 @@ the GPU through the C ABI.
   the C=32 cell and confidence-gated firing - and on ragged grids whose windows end mid-row,
   states stay within max-abs 1e-4 (fp32) / 2e-2 (bf16) of the CPU oracle with the same Philox
   masks, and fired counts are exact.
+* bf16 cells with 16 channels run the per-step path on the wave-per-tile kernel; it gives the
+  halo-window kernel's results (nca_set_kernel_path(3)) bit for bit on every padding and on grids
+  whose last tile ends mid-row, with Philox, per-step-key and injected masks.
 """
 
 from __future__ import annotations
@@ -218,3 +221,35 @@ def test_tiled_workspace_alias_and_errors():
     # the resident kernels need no workspace
     pk9 = copy.deepcopy(make_model("sudoku_c64")).to(DEV).packed("bf16", DEV)
     assert L.nca_rollout_workspace_bytes(ctypes.byref(pk9.desc), 32768, 9, 9) == 0
+
+
+@pytest.mark.parametrize("padding", ["zero", "wall", "wrap"])
+@pytest.mark.parametrize("H,W,B", [(201, 201, 2), (37, 45, 3), (5, 70, 3), (33, 1, 3), (3, 2, 5)])
+def test_wave_tile_kernel_equals_window_kernel_bitwise(H, W, B, padding):
+    """bf16 C=16: 6 steps (first and last in the caller's layout, the ones between cell-major) and
+    single steps, on the wave-per-tile kernel (path 2) and the halo-window kernel (path 3): the
+    same states and fired counts bit for bit."""
+    _say("wave tiles vs windows", H, W, padding)
+    kw = {"padding": padding}
+    if padding != "wall":
+        kw["wall_token"] = None
+    m = perturbed_model("maze_c16", 2, *DYN["maze_c16"], **kw)
+    md = copy.deepcopy(m).to(DEV)
+    g = torch.Generator().manual_seed(H * 1000 + W)
+    x = (torch.randn((B, 16, H, W), generator=g) * 0.3).to(DEV)
+    g4 = (torch.rand((B, 1, H, W), generator=g) < 0.3).to(DEV)
+    cl = torch.randn((B, m.cfg.c_in, H, W), generator=g).to(DEV)
+    masks = (torch.rand((6, B, 1, H, W), generator=g) < 0.5).float().to(DEV)
+    runs = [dict(seed=4, row0=2, step0=3, p_fire=0.6), dict(step_seeds=[5, 6, 7, 8, 9, 10], p_fire=0.5),
+            dict(masks=masks)]
+    for kwr in runs:
+        out = {}
+        for path in (2, 3):
+            with _path(path), torch.no_grad():
+                y, _, f = rollout_steps(md, x, g4, cl, 6, precision="bf16", want_fired=True, **kwr)
+                y1, _, f1 = rollout_steps(md, x, g4, cl, 1, precision="bf16", want_fired=True,
+                                          **{k: (v[:1] if k in ("masks", "step_seeds") else v)
+                                             for k, v in kwr.items()})
+            out[path] = (y, f, y1, f1)
+        for a, b in zip(out[2], out[3]):
+            assert torch.equal(a, b), kwr
