@@ -8,13 +8,17 @@ the 128 trials. Weights N(0, 0.02) (synthetic), states zero-initialised and clam
 resident in HBM before the timed region.
 
 `--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16, D=13,000, p_fire=0.5)
-times the halo-tiled per-step path the same way, and `--workload hardmaze30` (1,000 hard mazes
+times the per-step path (one launch of the wave-per-tile kernel per step) the same way, and
+`--workload hardmaze30` (1,000 hard mazes
 30x30 with 10 % extra openings, K=64 -> 64,000 rows, C=32, MLP 128 -> 256 -> 32, D=200, p_fire=0.8
 gated to 0.2 above confidence 0.9) the streamed C=32 kernel (one board per workgroup, the whole
 rollout in one launch). `--workload bptt30` times one training iteration: 64
 states sampled from a replay pool of 1,024 (30x30 DFS mazes, C=32 cell, bf16 forward with fp32
 master weights), a 32-step BPTT chunk with the per-cell cross-entropy on the 2-class path
-targets, AdamW, write-back; it reports cell-steps/s and the peak activation memory.
+targets, AdamW, write-back; it reports cell-steps/s and the peak activation memory. Its roofline
+prices 4x the forward FLOPs per cell-step against the fp32 peak (the gradients are fp32
+arithmetic) and also reports the same rate against the bf16 peak (frac_of_bf16_peak): the
+backward's products run on bf16 MFMA as exact three-part splits of the fp32 operands.
 
 value = rows * H * W * D * steps / wall seconds (cell-updates/s). The roofline block prices the
 rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) per cell-update, the
@@ -51,7 +55,7 @@ WORKLOADS = {
     "maze201": dict(
         preset="maze_c16", task="maze", boards=16, k=1, depth=13000, grid=201, p_fire=0.5,
         desc="maze 201x201: 16 DFS mazes, D=13000 steps, C=16, 4 kernels, MLP 64-128-16, "
-             "p_fire=0.5, one halo-tiled launch per step"),
+             "p_fire=0.5, one launch per step (wave-per-tile kernel)"),
     "bptt30": dict(
         preset="maze_hard_c32", task="maze", boards=1024, k=1, depth=32, grid=30, p_fire=0.8,
         batch=64, extra=0.10,
@@ -289,6 +293,8 @@ def main():
     ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp32", action="store_true", help="skip the secondary fp32 run")
+    ap.add_argument("--depth", type=int, default=0,
+                    help="steps per rollout instead of the workload's own (profiling runs only)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first copy this many MiB device-to-device (a kernel of known traffic "
                          "for scaling HBM counters), outside the timed region")
@@ -297,7 +303,9 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1"}))
         sys.exit(2)
 
-    wl = WORKLOADS[args.workload]
+    wl = dict(WORKLOADS[args.workload])
+    if args.depth:  # a shorter rollout of the same workload, for counter runs
+        wl["depth"] = args.depth
     if args.calib_copy_mib:
         calibration_copy(args.calib_copy_mib)
     if args.workload == "bptt30":
@@ -311,7 +319,11 @@ def main():
                        "depth": wl["depth"]},
             "roofline": {"bound": "mfma", "achieved": res["achieved_tflops"],
                          "peak": PEAK_TFLOPS["fp32"], "unit": "TFLOP/s", "frac": res["frac"],
-                         "traffic": None},
+                         "traffic": None,
+                         # the gradients are fp32 arithmetic, but their products run on bf16
+                         # MFMA as exact three-part splits of the fp32 operands (and the
+                         # forward is bf16): the same rate against the bf16 dense peak
+                         "frac_of_bf16_peak": res["achieved_tflops"] / PEAK_TFLOPS["bf16"]},
             "peak_activation_bytes": res["peak_activation_bytes"],
             "states_bytes": res["states_bytes"], "workspace_bytes": res["workspace_bytes"],
             "loss": res["loss"],

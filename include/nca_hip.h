@@ -21,7 +21,7 @@
  *                        (src/nca/rollout.py:203-247), fused into one launch
  *   nca_rollout_ws    <- the same loops for grids whose rows do not fit one workgroup's LDS
  *                        (the 201x201 mazes of src/nca/tasks/maze.py, max_cells batching of
- *                        rollout.py:101): one halo-tiled launch per step into a caller workspace
+ *                        rollout.py:101): one launch per step into a caller workspace
  *   nca_rollout_workspace_bytes <- nothing in the reference (PyTorch allocates its temporaries);
  *                        tells the caller how large that workspace must be
  *   nca_fire_mask     <- draw_step's fire mask (src/nca/engine/rng.py:51-69) and
@@ -188,8 +188,10 @@ size_t nca_bptt_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t
                                 int32_t width, int32_t n_chunk);
 
 /* Forward of a BPTT chunk: states (n_chunk + 1, rows, C, H, W) receives x0 and the state after
- * every step (the same kernels and results as nca_rollout, one step per call). fire->adaptive
- * must be 0. States are all that the backward needs: it recomputes everything else. */
+ * every step, equal to nca_rollout's states bit for bit (bf16 C=32 boards up to 31 wide: one
+ * fused launch of the streamed kernel that records every step; other cells and grids: one call
+ * per step). fire->adaptive must be 0. States are all that the backward needs: it recomputes
+ * everything else. */
 int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
                      int32_t width, const float *x0, const uint8_t *given, const float *clamp,
                      const nca_fire_desc *fire, int32_t n_chunk, float *states, void *stream);
