@@ -156,6 +156,16 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def upload(a, device: torch.device) -> torch.Tensor:
+    """A host array on the device through a fresh pinned buffer, without waiting: a copy from
+    pageable memory would first wait for all the stream's queued work (torch keeps the pinned
+    buffer alive until its copy has run). A CPU device gets a plain tensor."""
+    t = torch.as_tensor(a)
+    if torch.device(device).type != "cuda":
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 

@@ -76,7 +76,7 @@ def rollout_steps(
         m8 = (masks.detach() != 0).to(torch.uint8).contiguous()
     ss = None
     if step_seeds is not None:
-        ss = torch.as_tensor(np.asarray(step_seeds, dtype=np.int64)).to(dev)
+        ss = _lib.upload(np.asarray(step_seeds, dtype=np.int64), dev)
         if ss.numel() != n_steps:
             raise ValueError("step_seeds must have n_steps entries")
     if out is None:

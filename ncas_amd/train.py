@@ -97,7 +97,7 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
         m8 = (masks.detach() != 0).to(torch.uint8).contiguous()
     ss = None
     if step_seeds is not None:
-        ss = torch.as_tensor(np.asarray(step_seeds, dtype=np.int64)).to(dev)
+        ss = _lib.upload(np.asarray(step_seeds, dtype=np.int64), dev)
         if ss.numel() != n:
             raise ValueError("step_seeds must have one key per chunk step")
     fd = fire_desc(seed, cfg.fire_rate if p_fire is None else p_fire, None, None, True, row0,
@@ -128,8 +128,8 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                                    ctypes.byref(lossd), _lib.ptr(gf), ctypes.byref(gs),
                                    _lib.ptr(gx0), loss.data_ptr(), ws.data_ptr(), ws_bytes,
                                    stream), "nca_bptt_backward")
-    # the host arrays and master copies must outlive the queued work
-    torch.cuda.current_stream(dev).synchronize()
+    # no wait: the host arrays were read during the calls, and the device buffers freed here are
+    # reused only by later work on the same stream
     return ChunkResult(states[n].clone(), loss, grads, gx0, states.numel() * 4, ws_bytes)
 
 
@@ -210,9 +210,9 @@ class ReplayPool:
         """`n` fresh boards drawn uniformly with freshly initialised states (pool.py:58-87)."""
         idx = self.rng.integers(0, len(self.boards), size=n)
         sub = self.boards.subset(idx)
-        inputs = torch.from_numpy(sub.inputs).to(self.device)
-        targets = torch.from_numpy(sub.targets).to(self.device)
-        given = torch.from_numpy(sub.given).to(self.device)
+        inputs = _lib.upload(sub.inputs, self.device)
+        targets = _lib.upload(sub.targets, self.device)
+        given = _lib.upload(sub.given, self.device)
         x, given4, clamp = self.model.init_state(inputs, given, None, self.generator)
         return dict(x=x.detach(), given4=given4, clamp=clamp, inputs=inputs, targets=targets)
 
@@ -220,7 +220,7 @@ class ReplayPool:
         """`batch_size` pool entries without replacement, the first round(seed_ratio * batch)
         replaced by fresh boards (pool.py:90-131). Returns (indices, batch dict of copies)."""
         idx = self.rng.choice(self.size, size=batch_size, replace=False)
-        di = torch.as_tensor(idx, device=self.device)
+        di = _lib.upload(idx, self.device)
         batch = {k: getattr(self, k).index_select(0, di)
                  for k in ("x", "given4", "clamp", "inputs", "targets", "age")}
         n_fresh = int(round(seed_ratio * batch_size))
@@ -233,7 +233,7 @@ class ReplayPool:
 
     def write_back(self, idx, batch: dict) -> None:
         """Store the post-rollout states back (pool.py:166-179)."""
-        di = torch.as_tensor(idx, device=self.device)
+        di = _lib.upload(idx, self.device)
         with torch.no_grad():
             self.x[di] = batch["x"].detach()
         for k in ("given4", "clamp", "inputs", "targets"):
