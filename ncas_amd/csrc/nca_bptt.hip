@@ -626,6 +626,136 @@ __global__ void __launch_bounds__(kThreads) stencil_back_plane(Dims d, const flo
     }
 }
 
+constexpr int kStripPlanes = 4;  // (row, channel) planes per workgroup of stencil_back_strip
+
+// stencil_back for boards at most 256 wide and of at most kPlaneMax cells: workgroup b takes
+// planes [4b, 4b + 4) one after the other, each staged in LDS (x, g_u and the channel's 4 planes
+// of g_z; the next plane's loads are in flight while this one computes from LDS). Thread (band,
+// column j) walks down rows [band R, band R + R) of column j with the 3x3 neighbourhood of x and
+// g_z in registers, loading one new row of 3 columns per cell (15 LDS reads instead of 45). Per
+// cell the sums run in the order of stencil_back_kernel; the kernel-weight sums of the
+// workgroup's planes go to slot b.
+__global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const float *__restrict__ x,
+                                                               const float *__restrict__ Gu,
+                                                               const float *__restrict__ Gz,
+                                                               const float *__restrict__ kern,
+                                                               const float *__restrict__ padv,
+                                                               float *__restrict__ gx, float *__restrict__ dk) {
+    extern __shared__ float xs[];  // x plane, the 4 g_z planes, g_u: 6 HW floats
+    __shared__ float red[(kThreads / 64) * 36];
+    float *gs = xs + d.HW, *us = xs + 5 * d.HW;
+    const int H = d.H, W = d.W, HW = d.HW;
+    const bool wrap = d.padding == 2;
+    const int bands = kThreads / W, j = threadIdx.x % W, band = threadIdx.x / W;
+    const int R = (H + bands - 1) / bands, i0 = band * R, i1 = i0 + R < H ? i0 + R : H;
+    const bool active = band < bands;
+    // the 3 columns of the window: cell column index (wrapped) and whether it is a halo column
+    const int jc[3] = {j > 0 ? j - 1 : W - 1, j, j < W - 1 ? j + 1 : 0};
+    const bool jh[3] = {j == 0 && !wrap, false, j == W - 1 && !wrap};
+    const int64_t ks = (int64_t)d.C * d.M;
+    float acc[36];
+#pragma unroll
+    for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
+    const int p0 = blockIdx.x * kStripPlanes;
+    const int p1 = p0 + kStripPlanes < d.rows * d.C ? p0 + kStripPlanes : (int)(d.rows * d.C);
+    // a plane's 6 arrays, 8 cells per thread (HW <= kPlaneMax = 8 kThreads), in registers
+    float pv[8][6];
+    auto gload = [&](int pl) {
+        const int row = pl / d.C, c = pl - row * d.C;
+        const float *xr = x + (int64_t)pl * HW, *ur = Gu + (int64_t)pl * HW;
+        const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * HW;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = u * kThreads + threadIdx.x, qc = q < HW ? q : 0;
+            if (u * kThreads < HW) {  // uniform
+                pv[u][0] = xr[qc];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) pv[u][1 + k] = gz[k * ks + qc];
+                pv[u][5] = ur[qc];
+            }
+        }
+    };
+    if (p0 < p1) gload(p0);
+    for (int pl = p0; pl < p1; ++pl) {
+        const int row = pl / d.C, c = pl - row * d.C;
+        __syncthreads();  // the previous plane's reads are done
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = u * kThreads + threadIdx.x;
+            if (u * kThreads < HW && q < HW) {
+                xs[q] = pv[u][0];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) gs[k * HW + q] = pv[u][1 + k];
+                us[q] = pv[u][5];
+            }
+        }
+        __syncthreads();
+        if (pl + 1 < p1) gload(pl + 1);  // in flight while this plane computes from LDS
+        if (!active || i0 >= i1) continue;
+        const float hv = d.padding == 1 ? padv[c] : 0.0f;
+        // window row a of cell row i is grid row i + a - 1: x taps (halo value, bf16-rounded)
+        // and g_z (zero with a flag for halo cells: no transposed contribution)
+        float xw[3][3], gw[3][4][3];
+        bool hw[3][3];
+        auto load_row = [&](int a, int ii) {
+            const bool rh = (ii < 0 || ii >= H) && !wrap;
+            const int ir = ii < 0 ? H - 1 : (ii >= H ? 0 : ii);
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                const bool h = rh || jh[b];
+                const int q = ir * W + jc[b];
+                const float xv = h ? hv : xs[q];
+                xw[a][b] = d.bf16 ? nca::round_bf16(xv) : xv;
+                hw[a][b] = h;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) gw[a][k][b] = gs[k * HW + q];
+            }
+        };
+        load_row(0, i0 - 1);
+        load_row(1, i0);
+        for (int i = i0; i < i1; ++i) {
+            load_row(2, i + 1);
+            const int64_t e = (int64_t)pl * HW + i * W + j;
+            float g = us[i * W + j];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                // tap t = (dy, dx) reads x at (i + dy, j + dx); the cell whose tap t reads this
+                // cell is (i - dy, j - dx): window position (1 - dy, 1 - dx)
+                const int a = 2 - t / 3, b = 2 - t % 3;
+                if (!hw[a][b]) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], gw[a][k][b], g);
+                }
+            }
+            gx[e] = g;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float gzv = gw[1][k][1];
+#pragma unroll
+                for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gzv, xw[t / 3][t % 3], acc[k * 9 + t]);
+            }
+            // slide the window down one row
+#pragma unroll
+            for (int b = 0; b < 3; ++b) {
+                xw[0][b] = xw[1][b];
+                xw[1][b] = xw[2][b];
+                hw[0][b] = hw[1][b];
+                hw[1][b] = hw[2][b];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    gw[0][k][b] = gw[1][k][b];
+                    gw[1][k][b] = gw[2][k][b];
+                }
+            }
+        }
+    }
+    const float r = block_sums<36, kThreads / 64>(acc, red);
+    if (threadIdx.x < 36) {
+        float *pp = dk + (int64_t)blockIdx.x * 36 + threadIdx.x;
+        *pp = __fadd_rn(*pp, r);
+    }
+}
+
 // acc[v] += the sum of the planes' kernel-weight slots: block v, each thread a fixed strided
 // subset of the planes, then a fixed tree.
 __global__ void __launch_bounds__(kThreads) reduce_dk(const float *dk, int64_t planes, float *acc) {
@@ -919,6 +1049,9 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
         return rc;
     // boards small enough to stage (row, channel) planes in LDS
     const bool planes_ok = d.HW <= kPlaneMax && d.rows * d.C <= 0x7fffffff;
+    // ... and walked by columns for boards at most 256 wide (kernel-weight slot per 4 planes)
+    const bool strips_ok = planes_ok && d.W <= kThreads;
+    const int64_t strip_blocks = (d.rows * d.C + kStripPlanes - 1) / kStripPlanes;
     // cells per workgroup of the fused kernel: whole 32-cell tiles
     const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
     if (fused)
@@ -1012,7 +1145,10 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
             if ((rc = gemm(g, 1, st))) return rc;
         }
         // gradient of the step's input state and the kernel-weight partials
-        if (planes_ok)
+        if (strips_ok)
+            hipLaunchKernelGGL(stencil_back_strip, dim3((unsigned)strip_blocks), dim3(kThreads),
+                               6 * d.HW * sizeof(float), st, d, xt, Gu, Gz, kern, padv, gx, ws + L.dk);
+        else if (planes_ok)
             hipLaunchKernelGGL(stencil_back_plane, dim3((unsigned)(d.rows * d.C)), dim3(kThreads),
                                5 * d.HW * sizeof(float), st, d, xt, Gu, Gz, kern, padv, gx, ws + L.dk);
         else
@@ -1041,7 +1177,9 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     }
     // the slots summed in slot order
     hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
-    if (planes_ok) hipLaunchKernelGGL(reduce_dk, dim3(36), dim3(kThreads), 0, st, ws + L.dk, d.rows * d.C, acc + P.K);
+    if (planes_ok)
+        hipLaunchKernelGGL(reduce_dk, dim3(36), dim3(kThreads), 0, st, ws + L.dk, strips_ok ? strip_blocks : d.rows * d.C,
+                           acc + P.K);
     if (grad_x0) {
         if (n_chunk == 0 || d.M == 0) {
             if (grad_final) hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, grad_final, grad_x0, sn);
