@@ -40,7 +40,9 @@ struct Step16Params {
 
 typedef float s16_f32x4 __attribute__((ext_vector_type(4)));
 
-template <bool IN_NCHW, bool OUT_NCHW>
+// FIRST equals sp.first: the clamp values are loaded (and the loop carries them) on a call's
+// first step only
+template <bool IN_NCHW, bool OUT_NCHW, bool FIRST>
 __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     constexpr int C = 16, HD = 128;
     const RolloutParams &a = sp.a;
@@ -145,7 +147,7 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         in.fu8 = 0;
         if (a.fire_f32) in.fin = a.fire_f32[row * HWn + qc];
         if (a.fire_u8) in.fu8 = a.fire_u8[((int64_t)sp.step * a.rows + row) * HWn + qc];
-        if (sp.first) {
+        if (FIRST) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int ci = insl[v] ? 4 * g + v - a.in_off : 0;
@@ -282,7 +284,7 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         }
         const bool gv = cur.gv != 0;
         float xo[4] = {cur.xo[0], cur.xo[1], cur.xo[2], cur.xo[3]};
-        if (sp.first && gv) {
+        if (FIRST && gv) {
 #pragma unroll
             for (int v = 0; v < 4; ++v)
                 if (insl[v]) xo[v] = cur.cv[v];
@@ -327,13 +329,19 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     TileIn nx;
     if (t < t_end) load_tile(row, tir, nx);
     const bool philox = !a.fire_f32 && !a.fire_u8;
+    // vmcnt(0) (expcnt and lgkmcnt left open): the weights' loads are done before the loop, so the
+    // waits the compiler places at their uses in the loop body do not hold back the prefetch
+    __builtin_amdgcn_s_waitcnt(0x0f70);
     for (; t < t_end; t += 8) {
         TileCur cu;
         unpack(nx, cu);  // this tile's loads, consumed before the buffer takes the next tile's
         int64_t rn = row;
         int tn = tir;
         advance(rn, tn);
-        if (t + 8 < t_end) load_tile(rn, tn, nx);
+        // the last tile reloads itself (unused) rather than branching around the loads: a branch
+        // join makes the compiler wait for them before the tile's compute
+        const bool more = t + 8 < t_end;
+        load_tile(more ? rn : row, more ? tn : tir, nx);
         if (philox && kgrp == 0) draw4(row, tir);
         process(cu, row, tir);
         kgrp = (kgrp + 1) & 3;

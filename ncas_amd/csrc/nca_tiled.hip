@@ -98,7 +98,10 @@ hipError_t launch_stream16(const RolloutParams &p, int step, int first, hipStrea
     sp.tiles_per_wg = (sp.n_tiles + n_cu - 1) / n_cu;
     const int64_t grid = (sp.n_tiles + sp.tiles_per_wg - 1) / sp.tiles_per_wg;
     if (grid < 1) return hipSuccess;
-    hipLaunchKernelGGL((step_stream16<IN_NCHW, OUT_NCHW>), dim3((unsigned)grid), dim3(512), 0, st, sp);
+    if (first)
+        hipLaunchKernelGGL((step_stream16<IN_NCHW, OUT_NCHW, true>), dim3((unsigned)grid), dim3(512), 0, st, sp);
+    else
+        hipLaunchKernelGGL((step_stream16<IN_NCHW, OUT_NCHW, false>), dim3((unsigned)grid), dim3(512), 0, st, sp);
     return hipGetLastError();
 }
 
