@@ -225,7 +225,8 @@ __device__ __forceinline__ void load_out(const Dims &d, const float *x1c, float 
 // v >= n_out, and everywhere on a step without a loss term) and the cell's loss term (reference
 // src/nca/train.py:183-207). n_out, c_out <= NO.
 template <int NO>
-__device__ __forceinline__ float head_grad(const FrontArgs &a, const float xo[NO], int tgt, float mk, float gl[NO]) {
+__device__ __forceinline__ float head_grad(const FrontArgs &a, const float *hw, const float *hb, const float xo[NO], int tgt,
+                                           float mk, float gl[NO]) {
     const Dims &d = a.d;
 #pragma unroll
     for (int v = 0; v < NO; ++v) gl[v] = 0.0f;
@@ -237,10 +238,10 @@ __device__ __forceinline__ float head_grad(const FrontArgs &a, const float xo[NO
     for (int v = 0; v < NO; ++v) {
         l[v] = 0.0f;
         if (v < d.n_out) {
-            float acc = a.head_b[v];
+            float acc = hb[v];
 #pragma unroll
             for (int c = 0; c < NO; ++c)
-                if (c < d.c_out) acc = __builtin_fmaf(a.head_w[v * d.c_out + c], xo[c], acc);
+                if (c < d.c_out) acc = __builtin_fmaf(hw[v * d.c_out + c], xo[c], acc);
             l[v] = acc;
             mx = fmaxf(mx, acc);
         }
@@ -269,7 +270,13 @@ constexpr int kFrontCh = 8;  // channels per front block (the channel count is a
 template <int NO>
 __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
     __shared__ float red[(kThreads / 64) * 32];
+    // the head's weights and bias in LDS: read in the loop next to the gradient stores, from global
+    // memory each read would wait behind them
+    __shared__ float hwL[NO * NO + NO];
     const Dims &d = a.d;
+    for (int i = threadIdx.x; i < d.n_out * d.c_out; i += kThreads) hwL[i] = a.head_w[i];
+    for (int i = threadIdx.x; i < d.n_out; i += kThreads) hwL[NO * NO + i] = a.head_b[i];
+    __syncthreads();
     const int s = blockIdx.x, c0 = kFrontCh * blockIdx.y;
     const int per = (int)((d.M + kSplit - 1) / kSplit), m0 = s * per;
     const int m1 = m0 + per < (int)d.M ? m0 + per : (int)d.M;
@@ -306,7 +313,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             f = uq < a.p ? 1.0f : 0.0f;
         }
         float gl[NO];
-        const float lc = head_grad<NO>(a, xo, tgt, mk, gl);
+        const float lc = head_grad<NO>(a, hwL, hwL + NO * NO, xo, tgt, mk, gl);
         if (head) lossv = __fadd_rn(lossv, lc);
         if (kRegHead && head) {
 #pragma unroll
@@ -324,7 +331,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             if (co >= 0 && co < d.c_out) {
 #pragma unroll
                 for (int v = 0; v < NO; ++v)
-                    if (v < d.n_out) g = __builtin_fmaf(a.head_w[v * d.c_out + co], gl[v], g);
+                    if (v < d.n_out) g = __builtin_fmaf(hwL[v * d.c_out + co], gl[v], g);
             }
             if (gv && c >= d.in_off && c < d.in_off + d.c_in) g = 0.0f;
             a.Gu[cb + (int64_t)c * d.HW] = g;
@@ -383,7 +390,7 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             const int row = m / d.HW, q = m - row * d.HW;
             float xo[NO], gl[NO];
             load_out<NO>(d, a.x1 + (int64_t)row * d.C * d.HW + q, xo);
-            head_grad<NO>(a, xo, a.targets[m], a.mask ? a.mask[m] : 0.0f, gl);
+            head_grad<NO>(a, hwL, hwL + NO * NO, xo, a.targets[m], a.mask ? a.mask[m] : 0.0f, gl);
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
                 const int p = p0 + k;
