@@ -37,6 +37,12 @@
  *                        perception backward ops.py:79-94) with the loss of step.py:243-245 /
  *                        train.py:183-207 normalised as in engine.py:490
  *   nca_bptt_workspace_bytes <- nothing in the reference (autograd allocates); workspace size
+ *   nca_step_backward <- the backward of one step of make_step's step function under autograd
+ *                        (src/nca/engine/step.py:184-207): _FusedCellUpdate.backward
+ *                        (src/nca/engine/ops.py:269-294), the MLP's backward and the shared-kernel
+ *                        perception backward (ops.py:79-94); checked against the reference step's
+ *                        gradients by tests/test_engine_ops.py:251-294
+ *   nca_step_backward_workspace_bytes <- nothing in the reference (autograd allocates)
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -209,6 +215,23 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
                       float *grad_x0, float *loss_out, void *workspace, size_t workspace_bytes,
                       void *stream);
 
+/* Bytes of workspace that nca_step_backward needs for this shape (0 if the cell is unsupported). */
+size_t nca_step_backward_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height,
+                                         int32_t width);
+
+/* Vector-Jacobian product of one nca_step: given the cotangent grad_out (rows, C, H, W) of the step's
+ * output x_out = step(x, given, clamp, fire, noise), writes grads->kernels, w1, b1, w2, b2 (the
+ * parameter gradients, overwritten) and grad_x (rows, C, H, W; may be NULL). fire (rows, H, W) fp32
+ * is the step's fire value per cell (any real value: g_dx = g_u * fire); the noise and the clamp
+ * values do not enter the gradient. grads->head_w / head_b are not written (the step does not use
+ * the readout head). w->w1 and w->w2 are the fp32 weights (bf16 cells round them on load like the
+ * forward). Any head kind. Deterministic. */
+int nca_step_backward(const nca_cell_desc *cell, const void *packed, const nca_cell_weights *w,
+                      int64_t rows, int32_t height, int32_t width, const float *x,
+                      const uint8_t *given, const float *fire, const float *grad_out,
+                      nca_cell_grads *grads, float *grad_x, void *workspace,
+                      size_t workspace_bytes, void *stream);
+
 /* Last error message of the calling thread ("" if none). */
 const char *nca_last_error(void);
 
@@ -219,8 +242,9 @@ int nca_version(void);
  * resident kernel where the rows fit LDS, else the per-step path: the wave-per-tile kernel for
  * bf16 cells with 16 channels, the halo-window kernel otherwise), 1 = never the streamed kernel,
  * 2 = always the per-step path, 3 = always the per-step path on the halo-window kernel.
- * Process-wide; used by the tests to check the paths against each other and by the bench to time
- * the per-step regime. No counterpart in the reference. */
+ * Per calling thread (other threads keep their own setting); used by the tests to check the paths
+ * against each other and by the bench to time the per-step regime. No counterpart in the
+ * reference. */
 int nca_set_kernel_path(int path);
 
 #ifdef __cplusplus

@@ -34,6 +34,8 @@ EXPORTS = (
     "nca_bptt_workspace_bytes",
     "nca_bptt_forward",
     "nca_bptt_backward",
+    "nca_step_backward_workspace_bytes",
+    "nca_step_backward",
 )
 
 
@@ -133,6 +135,12 @@ def load():
         ctypes.POINTER(CellDesc), vp, ctypes.POINTER(CellWeights), i64, i32, i32, vp, vp,
         ctypes.POINTER(FireDesc), i32, ctypes.POINTER(BpttLoss), vp, ctypes.POINTER(CellGrads), vp,
         vp, vp, ctypes.c_size_t, vp,
+    ]
+    L.nca_step_backward_workspace_bytes.argtypes = [ctypes.POINTER(CellDesc), i64, i32, i32]
+    L.nca_step_backward_workspace_bytes.restype = ctypes.c_size_t
+    L.nca_step_backward.argtypes = [
+        ctypes.POINTER(CellDesc), vp, ctypes.POINTER(CellWeights), i64, i32, i32, vp, vp, vp, vp,
+        ctypes.POINTER(CellGrads), vp, vp, ctypes.c_size_t, vp,
     ]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int

@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+
 #include "nca_hip.h"
 #include "nca_device.h"
 #include "nca_layout.h"
@@ -50,8 +51,9 @@ namespace {
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per workgroup
 
 // Kernel selection (nca_set_kernel_path): 0 automatic, 1 generic resident kernel for bf16,
-// 2 the halo-tiled per-step kernel for every grid.
-int g_path = 0;
+// 2 the halo-tiled per-step kernel for every grid, 3 the halo-window kernel for every grid. Per
+// thread, so that a thread choosing a path never changes another thread's calls.
+thread_local int g_path = 0;
 
 bool shape_supported(int C, int hidden) {
     return (C == 16 && hidden == 128) || (C == 32 && hidden == 256) || (C == 64 && hidden == 256);
@@ -325,6 +327,13 @@ bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
     return pa < pb + nb && pb < pa + na;
 }
 
+// Workspace bytes the per-step path asks for (run_tiled): two state buffers for three or more
+// steps, one for two steps or an in-place single step, none otherwise.
+size_t per_step_need(const nca_cell_desc *d, int64_t rows, int H, int W, int n, bool alias) {
+    const size_t sb = state_bytes(d, rows, H, W);
+    return n >= 3 ? 2 * sb : (n == 2 || (n == 1 && alias)) ? sb : 0;
+}
+
 // The per-step path: n_steps launches of the halo-tiled kernel. The first step reads the
 // caller's NCHW x_in and the last writes NCHW x_out; the steps in between alternate between the
 // two halves A, B of the workspace in cell-major order. One step in place goes through A.
@@ -334,7 +343,7 @@ int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t s
     const bool alias = p.x_in == p.x_out;
     if (!alias && overlaps(p.x_in, sb, p.x_out, sb))
         return fail(NCA_ERR_INVALID, "x_in and x_out overlap without being the same buffer");
-    const size_t need = n >= 3 ? 2 * sb : (n == 2 || (n == 1 && alias)) ? sb : 0;
+    const size_t need = per_step_need(d, p.rows, p.H, p.W, n, alias);
     if (need) {
         if (!ws || ws_bytes < need)
             return fail(NCA_ERR_UNSUPPORTED,

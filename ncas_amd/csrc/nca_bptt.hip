@@ -199,6 +199,7 @@ struct FrontArgs {
     const float *head_w, *head_b;
     // fire mask of the step
     const uint8_t *fire_u8;  // (rows, HW) slice of the injected masks, or null
+    const float *fire_f32;   // (rows, HW) fire values of a single step's VJP (any real value), or null
     const uint64_t *key_ptr;  // per-step Philox key (device), or null: key
     uint64_t key;
     int64_t row0;
@@ -300,10 +301,12 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
         for (int j = 0; j < kFrontCh; ++j) gi[j] = a.gin ? a.gin[cb + (int64_t)(c0 + j) * d.HW] : 0.0f;
         load_out<NO>(d, a.x1 + cb, xo);
         const bool gv = a.given[m] != 0;
-        const int tgt = a.targets[m];
+        const int tgt = a.targets ? a.targets[m] : 0;  // no targets: a step without a loss term
         const float mk = a.mask ? a.mask[m] : 0.0f;
         float f;
-        if (a.fire_u8) {
+        if (a.fire_f32) {
+            f = a.fire_f32[m];
+        } else if (a.fire_u8) {
             f = a.fire_u8[m] ? 1.0f : 0.0f;
         } else {
             float u[4];
@@ -920,10 +923,13 @@ int gemm(const GemmArgs &g, int splits, hipStream_t st) {
     return nca::hip_status(hipGetLastError(), "gemm launch");
 }
 
-int check_dims(const nca_cell_desc *cell, int64_t rows, int32_t H, int32_t W, int32_t n, Dims *d) {
+// loss_head: the call computes the chunk loss, which is the cross-entropy of an mlp head (a single
+// step's VJP has no loss term and takes any head).
+int check_dims(const nca_cell_desc *cell, int64_t rows, int32_t H, int32_t W, int32_t n, Dims *d,
+               bool loss_head = true) {
     if (!cell) return nca::set_error(NCA_ERR_INVALID, "cell descriptor is NULL");
     if (cell->heads != 4) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT needs 4 perception kernels");
-    if (cell->head_kind != NCA_HEAD_MLP)
+    if (loss_head && cell->head_kind != NCA_HEAD_MLP)
         return nca::set_error(NCA_ERR_UNSUPPORTED, "the BPTT loss is the cross-entropy of an mlp head");
     if (cell->n_out < 1 || cell->n_out > 16) return nca::set_error(NCA_ERR_UNSUPPORTED, "n_out must be 1..16");
     if (rows < 0 || H < 1 || W < 1 || n < 0) return nca::set_error(NCA_ERR_INVALID, "bad rows / grid / n_chunk");
@@ -1001,35 +1007,33 @@ int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows
     return NCA_OK;
 }
 
-int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_cell_weights *w, int64_t rows,
-                      int32_t height, int32_t width, const float *states, const uint8_t *given,
-                      const nca_fire_desc *fire, int32_t n_chunk, const nca_bptt_loss *loss,
-                      const float *grad_final, nca_cell_grads *grads, float *grad_x0, float *loss_out,
-                      void *workspace, size_t workspace_bytes, void *stream) {
-    nca::clear_error();
-    Dims d;
-    int rc = check_dims(cell, rows, height, width, n_chunk, &d);
-    if (rc) return rc;
-    const size_t pk = nca_packed_weights_bytes(cell);
-    if (pk == 0) return NCA_ERR_UNSUPPORTED;  // message set by the packing check
-    if (!packed || !w || !w->w1 || !w->w2 || !states || !given || !fire || !loss || !grads)
-        return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
-    if (!grads->kernels || !grads->w1 || !grads->b1 || !grads->w2 || !grads->b2 || !grads->head_w || !grads->head_b)
-        return nca::set_error(NCA_ERR_INVALID, "NULL gradient pointer");
-    if (fire->adaptive) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT chunks fire uniformly (no confidence gating)");
-    if (n_chunk > 0 && (!loss->step_weights || !loss->targets))
-        return nca::set_error(NCA_ERR_INVALID, "the loss needs step_weights and targets");
+}  // extern "C"
+
+namespace {
+
+// The backward of n_chunk steps (nca_bptt_backward). Step t reads its input state at
+// states + t * stride and its output at states + (t + 1) * stride; stride 0 (the single-step VJP,
+// which has no loss term) reads `states` for both. fire_f32, when given, is the (rows, H, W) fire
+// value of a one-step call instead of the fire descriptor's masks. grads->head_w / head_b may be
+// NULL when no step has a loss term.
+int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
+                  const float *states, int64_t stride, const uint8_t *given, const nca_fire_desc *fire,
+                  const float *fire_f32, int32_t n_chunk, const nca_bptt_loss *loss, const float *grad_final,
+                  nca_cell_grads *grads, float *grad_x0, float *loss_out, void *workspace, size_t workspace_bytes,
+                  hipStream_t st) {
+    int rc = NCA_OK;
     const WsLayout L = ws_layout(d, n_chunk);
     if (!workspace || workspace_bytes < (size_t)L.total * sizeof(float)) {
         char msg[160];
-        snprintf(msg, sizeof(msg), "BPTT needs a workspace of %zu bytes (nca_bptt_workspace_bytes)",
+        snprintf(msg, sizeof(msg),
+                 "the backward needs a workspace of %zu bytes (nca_bptt_workspace_bytes, "
+                 "nca_step_backward_workspace_bytes)",
                  (size_t)L.total * sizeof(float));
         return nca::set_error(NCA_ERR_INVALID, msg);
     }
     float wsum = 0.0f;
     for (int t = 0; t < n_chunk; ++t) wsum += loss->step_weights[t];
     const float wden = wsum < 1.0f ? 1.0f : wsum;  // weights.sum().clamp_min(1), engine.py:490
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const ParamLayout P = param_layout(d);
     const nca::PackedLayout PL = nca::packed_layout(d.C, 4, d.HD, d.c_out, d.n_out, d.bf16);
     const unsigned char *pb = static_cast<const unsigned char *>(packed);
@@ -1069,7 +1073,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
 
     const float *gin = grad_final;
     for (int t = n_chunk - 1; t >= 0 && d.M > 0; --t) {
-        const float *xt = states + t * sn, *x1 = states + (t + 1) * sn;
+        const float *xt = states + t * stride, *x1 = states + (t + 1) * stride;
         float *gx = (t == 0 && grad_x0) ? grad_x0 : Gx[t & 1];
         // front: loss gradient, clamp and fire
         FrontArgs fa;
@@ -1086,6 +1090,7 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
         fa.head_w = headw;
         fa.head_b = headb;
         fa.fire_u8 = fire->fire_in ? fire->fire_in + (int64_t)t * d.rows * d.HW : nullptr;
+        fa.fire_f32 = fire_f32;
         fa.key_ptr = fire->step_seeds ? fire->step_seeds + t : nullptr;
         fa.key = fire->seed;
         fa.row0 = fire->row0;
@@ -1199,8 +1204,10 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
     hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.B1, grads->b1, (int64_t)d.HD);
     hipLaunchKernelGGL(copy_kernel, dim3(64), dim3(256), 0, st, acc + P.W2, grads->w2, (int64_t)d.C * d.HD);
     hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(256), 0, st, acc + P.B2, grads->b2, (int64_t)d.C);
-    hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.HW, grads->head_w, (int64_t)d.n_out * d.c_out);
-    hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.HB, grads->head_b, (int64_t)d.n_out);
+    if (grads->head_w)
+        hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.HW, grads->head_w, (int64_t)d.n_out * d.c_out);
+    if (grads->head_b)
+        hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.HB, grads->head_b, (int64_t)d.n_out);
     if (loss_out) {
         if (n_chunk > 0 && d.M > 0)
             hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossacc, loss_out);
@@ -1208,6 +1215,67 @@ int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_c
             hipLaunchKernelGGL(zero_f32, dim3(1), dim3(64), 0, st, loss_out, (int64_t)1);
     }
     return nca::hip_status(hipGetLastError(), "bptt finish");
+}
+
+}  // namespace
+
+extern "C" {
+
+int nca_bptt_backward(const nca_cell_desc *cell, const void *packed, const nca_cell_weights *w, int64_t rows,
+                      int32_t height, int32_t width, const float *states, const uint8_t *given,
+                      const nca_fire_desc *fire, int32_t n_chunk, const nca_bptt_loss *loss,
+                      const float *grad_final, nca_cell_grads *grads, float *grad_x0, float *loss_out,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    nca::clear_error();
+    Dims d;
+    int rc = check_dims(cell, rows, height, width, n_chunk, &d);
+    if (rc) return rc;
+    const size_t pk = nca_packed_weights_bytes(cell);
+    if (pk == 0) return NCA_ERR_UNSUPPORTED;  // message set by the packing check
+    if (!packed || !w || !w->w1 || !w->w2 || !states || !given || !fire || !loss || !grads)
+        return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    if (!grads->kernels || !grads->w1 || !grads->b1 || !grads->w2 || !grads->b2 || !grads->head_w || !grads->head_b)
+        return nca::set_error(NCA_ERR_INVALID, "NULL gradient pointer");
+    if (fire->adaptive) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT chunks fire uniformly (no confidence gating)");
+    if (n_chunk > 0 && (!loss->step_weights || !loss->targets))
+        return nca::set_error(NCA_ERR_INVALID, "the loss needs step_weights and targets");
+    const int64_t sn = d.rows * d.C * (int64_t)d.HW;
+    return backward_impl(d, packed, w, states, sn, given, fire, nullptr, n_chunk, loss, grad_final, grads,
+                         grad_x0, loss_out, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+size_t nca_step_backward_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width) {
+    Dims d;
+    if (nca_packed_weights_bytes(cell) == 0 || check_dims(cell, rows, height, width, 1, &d, false)) return 0;
+    return (size_t)ws_layout(d, 1).total * sizeof(float);
+}
+
+int nca_step_backward(const nca_cell_desc *cell, const void *packed, const nca_cell_weights *w, int64_t rows,
+                      int32_t height, int32_t width, const float *x, const uint8_t *given, const float *fire,
+                      const float *grad_out, nca_cell_grads *grads, float *grad_x, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+    nca::clear_error();
+    Dims d;
+    int rc = check_dims(cell, rows, height, width, 1, &d, false);
+    if (rc) return rc;
+    if (nca_packed_weights_bytes(cell) == 0) return NCA_ERR_UNSUPPORTED;  // message set by the packing check
+    if (!packed || !w || !w->w1 || !w->w2 || !x || !given || !fire || !grad_out || !grads)
+        return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    if (!grads->kernels || !grads->w1 || !grads->b1 || !grads->w2 || !grads->b2)
+        return nca::set_error(NCA_ERR_INVALID, "NULL gradient pointer");
+    // one step with no loss term: the cotangent of the step's output is all that flows back
+    nca_fire_desc fd;
+    memset(&fd, 0, sizeof(fd));
+    const float zero_weight = 0.0f;
+    nca_bptt_loss none;
+    none.targets = nullptr;
+    none.loss_mask = nullptr;
+    none.step_weights = &zero_weight;
+    nca_cell_grads g = *grads;
+    g.head_w = nullptr;
+    g.head_b = nullptr;
+    return backward_impl(d, packed, w, x, 0, given, &fd, fire, 1, &none, grad_out, &g, grad_x, nullptr,
+                         workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -214,7 +214,6 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     auto process = [&](const TileCur &cur, int64_t row, int tir) __attribute__((always_inline)) {
         const int q = 16 * tir + r;
         const bool valid = q < HWn;
-        const int qc = valid ? q : HWn - 1;
 
         // 2. perception: bf16 tap pairs per channel, v_dot2 against the kernel pairs
         {

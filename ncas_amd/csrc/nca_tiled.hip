@@ -110,7 +110,10 @@ hipError_t launch_stream16(const RolloutParams &p, int step, int first, hipStrea
 hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, int in_nchw,
                       int out_nchw, hipStream_t st, bool windows, bool *ok) {
     *ok = false;
-    if (C == 16 && HD == 128 && bf16 && !windows && !p.noise && !p.adaptive) {
+    // the wave-per-tile kernel addresses the cell-major state with 32-bit byte offsets: larger
+    // batches run on the halo-window kernel
+    const bool offsets32 = p.rows * (int64_t)p.H * p.W * 16 * (int64_t)sizeof(float) < ((int64_t)1 << 32);
+    if (C == 16 && HD == 128 && bf16 && !windows && !p.noise && !p.adaptive && offsets32) {
         *ok = true;
         if (in_nchw)
             return out_nchw ? launch_stream16<true, true>(p, step, first, st) : launch_stream16<true, false>(p, step, first, st);

@@ -28,39 +28,47 @@ from . import _lib
 OFFSETS = [(dy, dx) for dy in (-1, 0, 1) for dx in (-1, 0, 1)]
 
 
+# Readout coordinates of the maze tokens for the "semantic" embedding, keyed by (vocabulary
+# size, c_out): the reference's table (src/nca/embeddings.py:25-28), needed as is so that its
+# trained maze cells read the same inputs.
+_SEMANTIC_READOUT = {
+    (4, 2): ((0.0, -1.0), (0.0, 1.0), (1.0, 0.0), (-1.0, 0.0)),
+    (5, 3): ((0.0, 0.0, 0.0), (0.0, 0.0, 1.0), (1.0, 0.0, -1.0), (0.0, -1.0, 1.0), (0.0, 1.0, 1.0)),
+}
+
+
 def make_embeddings(vocab_size: int, dim: int, kind: str = "onehot", seed: int = 0,
                     c_out: int | None = None) -> torch.Tensor:
-    """(vocab_size, dim) token embeddings (reference src/nca/embeddings.py:31-53), plus
-    "onehot_inputs": one-hot rows for the first `dim` tokens and zero rows for the tokens that are
-    never inputs (the maze cells' output-only PATH token)."""
+    """Fixed token embeddings, a (vocab_size, dim) float tensor whose row v is what a given cell
+    of token v is clamped to (reference src/nca/embeddings.py:31-53).
+
+    * "onehot": row v is the v-th unit vector (needs dim >= vocab_size);
+    * "onehot_inputs": unit vectors for the first min(vocab_size, dim) tokens, zero rows for
+      the rest (the maze cells' output-only PATH token is never an input);
+    * "semantic": every entry -1 except the first c_out, which hold the token's readout
+      coordinates;
+    * "orthonormal": the first vocab_size rows of the Q factor of a (dim, dim) standard normal
+      matrix drawn from numpy's default_rng(seed).
+    """
     if kind == "onehot_inputs":
-        e = torch.zeros(vocab_size, dim)
-        n = min(vocab_size, dim)
-        e[torch.arange(n), torch.arange(n)] = 1.0
-        return e
+        return torch.eye(vocab_size, dim)
     if vocab_size > dim:
-        raise ValueError(f"need dim >= vocab_size, got dim={dim} < V={vocab_size}")
+        raise ValueError(f"{vocab_size} tokens do not fit {dim} embedding channels")
     if kind == "onehot":
-        e = torch.zeros(vocab_size, dim)
-        e[torch.arange(vocab_size), torch.arange(vocab_size)] = 1.0
-        return e
+        return torch.eye(vocab_size, dim)
     if kind == "semantic":
-        heads = {
-            (4, 2): [(0.0, -1.0), (0.0, 1.0), (1.0, 0.0), (-1.0, 0.0)],
-            (5, 3): [(0.0, 0.0, 0.0), (0.0, 0.0, 1.0), (1.0, 0.0, -1.0), (0.0, -1.0, 1.0),
-                     (0.0, 1.0, 1.0)],
-        }
-        head = heads.get((vocab_size, c_out))
-        if head is None:
-            raise ValueError(f"no semantic embedding for vocab {vocab_size}, c_out {c_out}")
-        e = torch.full((vocab_size, dim), -1.0)
-        e[:, :c_out] = torch.tensor(head)
+        coords = _SEMANTIC_READOUT.get((vocab_size, c_out))
+        if coords is None:
+            raise ValueError(f"no semantic readout coordinates for {vocab_size} tokens and "
+                             f"c_out={c_out}")
+        e = -torch.ones(vocab_size, dim)
+        e[:, :c_out] = torch.tensor(coords)
         return e
     if kind == "orthonormal":
-        rng = np.random.default_rng(seed)
-        q, _ = np.linalg.qr(rng.standard_normal((dim, dim)))
-        return torch.tensor(q[:vocab_size], dtype=torch.float32)
-    raise ValueError(f"unknown embedding kind {kind!r}")
+        gauss = np.random.default_rng(seed).standard_normal((dim, dim))
+        basis = np.linalg.qr(gauss)[0]
+        return torch.from_numpy(np.ascontiguousarray(basis[:vocab_size])).to(torch.float32)
+    raise ValueError(f"embedding kind {kind!r} (onehot | onehot_inputs | semantic | orthonormal)")
 
 
 def fixed_kernels() -> torch.Tensor:
@@ -175,6 +183,9 @@ class _Packed:
     key: tuple
     buf: torch.Tensor
     desc: _lib.CellDesc
+    # the fp32 sources the packing kernels read, held with the buffer so that they outlive those
+    # kernels without a host wait
+    srcs: list = field(default_factory=list)
 
 
 class NCA(nn.Module):
@@ -273,9 +284,7 @@ class NCA(nn.Module):
                                _lib.stream_of(device)),
             "nca_pack_weights",
         )
-        # keep the fp32 sources alive until the packing kernels have run
-        torch.cuda.current_stream(device).synchronize()
-        p = _Packed(key, buf, desc)
+        p = _Packed(key, buf, desc, flat)
         self._packed[(precision, str(device))] = p
         return p
 

@@ -9,10 +9,14 @@ Fire masks come from the Philox rule keyed on the global row index and step, so 
 not depend on `max_cells` or on where the trace boundaries fall. The steps between two trace
 points run as one launch of the LDS-resident kernel (`inference.rollout_steps`).
 
-Test-time noise, damage and pruning are not implemented and raise ValueError.
+Everything a rollout reports is computed on the GPU (decode, board confidence, the per-board
+exact / cell-accuracy scores over `task.eval_mask`, fired-cell counts) and kept there until one
+copy to the host at the end of the call (the reference copies at every record step,
+rollout.py:277-288). Test-time noise and damage are not implemented and raise ValueError.
 
-`conf_at_k` / `pass_at_k` are the reference's selection metrics (rollout.py:317-350);
-`select_at_k` is the same per-board choice computed on the GPU.
+`conf_at_k` / `pass_at_k` are the reference's selection metrics (rollout.py:317-350) computed on
+the GPU: the conf@K choice is the `nca_conf_select` wavefront reduction, and the metric of the
+chosen trial, the any-of-k test of pass@K and the (weighted) means are device reductions.
 """
 
 from __future__ import annotations
@@ -22,6 +26,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from . import _lib
 from .inference import rollout_steps
 from .readout import conf_select, readout
 
@@ -65,19 +70,46 @@ class RolloutResult:
         return self.pred.shape[0]
 
 
-def decode_tokens(model, x, given, inputs):
-    """Decoded tokens (B, H, W); given cells show their input token (rollout.py:74-82)."""
+def decode_tokens(model, x, given, inputs, fill_given: bool = True):
+    """Decoded tokens (B, H, W) and board confidence (B,) of states x. With `fill_given` (maze,
+    Sudoku) given cells show their input token (reference rollout.py:74-82)."""
     _, conf, idx = readout(model, x)
     tokens = torch.tensor(model.cfg.output_tokens, device=x.device)
     dec = tokens[idx.long()]
-    return torch.where(given, inputs, dec), conf
+    return (torch.where(given, inputs, dec) if fill_given else dec), conf
+
+
+class _Scorer:
+    """Per-row scores of a pass, on the device: decoded board, cell accuracy and exactness over
+    the scored cells, board confidence (reference rollout.py:181-184)."""
+
+    def __init__(self, model, task, inputs, targets, given, scored):
+        self.model, self.inputs, self.targets, self.given = model, inputs, targets, given
+        self.fill_given = getattr(task, "fill_given", True)
+        self.scored = scored
+        self.n_scored = scored.sum(dim=(1, 2)).clamp_min(1)
+
+    def __call__(self, x):
+        dec, conf = decode_tokens(self.model, x, self.given, self.inputs, self.fill_given)
+        correct = ((dec == self.targets) & self.scored).sum(dim=(1, 2))
+        return dec, correct / self.n_scored, correct == self.n_scored, conf
+
+
+def _eval_mask(task, boards) -> np.ndarray:
+    """The scored cells (reference tasks/base.py:126-132): the task's eval_mask, by default the
+    mutable cells."""
+    if task is not None and hasattr(task, "eval_mask"):
+        return np.asarray(task.eval_mask(boards), dtype=bool)
+    return ~boards.given
 
 
 @torch.no_grad()
 def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None,
             progress: bool = False) -> RolloutResult:
-    if rc.noise is not None or rc.damage_at is not None or rc.pruning:
-        raise ValueError("noise, damage and pruning are not implemented by the HIP rollout")
+    if rc.noise is not None or rc.damage_at is not None:
+        raise ValueError("test-time noise and damage are not implemented by the HIP rollout")
+    if rc.pruning:
+        raise ValueError("pruning is not implemented by the HIP rollout")
     if task_ids is not None or model.cfg.time_steps:
         raise ValueError("task / time embeddings are not implemented by the HIP rollout")
     model.eval()
@@ -96,25 +128,28 @@ def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None
     if record and (not steps or steps[-1] != rc.depth):
         steps.append(rc.depth)
     T = len(steps)
-    out_pred = np.zeros((N, K, H, W), np.int64)
-    out_conf = np.zeros((N, K), np.float32)
-    out_alive = np.ones((N, K), bool)
-    out_upd = np.zeros((N, K), np.float64)
-    tr = {k: (np.zeros((N, K, T), dt) if record else None) for k, dt in
-          (("exact", bool), ("cell", np.float32), ("conf", np.float32), ("upd", np.float64))}
-    fill_given = getattr(task, "fill_given", True)
+    rows_total = N * K
+    # every output lives on the device until the end of the call
+    pred = torch.empty((rows_total, H, W), dtype=torch.int64, device=device)
+    conf_out = torch.empty((rows_total,), dtype=torch.float32, device=device)
+    upd_out = torch.empty((rows_total,), dtype=torch.float64, device=device)
+    tr = {k: torch.zeros((rows_total, T), dtype=dt, device=device) for k, dt in
+          (("exact", torch.bool), ("cell", torch.float32), ("conf", torch.float32),
+           ("upd", torch.float64))} if record else None
+    scored_all = _eval_mask(task, boards)
     for start in range(0, N, per_pass):
-        sub = boards.subset(np.arange(start, min(N, start + per_pass)))
-        n = len(sub)
-        B = n * K
-        inputs = torch.from_numpy(np.repeat(sub.inputs, K, 0)).to(device)
-        targets = torch.from_numpy(np.repeat(sub.targets, K, 0)).to(device)
-        given = torch.from_numpy(np.repeat(sub.given, K, 0)).to(device)
-        mutable = (~given).float()
-        n_mut = mutable.sum(dim=(1, 2)).clamp_min(1)
+        stop_b = min(N, start + per_pass)
+        n = stop_b - start
+        sub = boards.subset(np.arange(start, stop_b))
+        rows = slice(start * K, stop_b * K)
+        inputs = _lib.upload(np.repeat(sub.inputs, K, 0), device)
+        targets = _lib.upload(np.repeat(sub.targets, K, 0), device)
+        given = _lib.upload(np.repeat(sub.given, K, 0), device)
+        scored = _lib.upload(np.repeat(scored_all[start:stop_b], K, 0), device)
+        score = _Scorer(model, task, inputs, targets, given, scored)
         x, given4, clamp = model.init_state(inputs, given, None, gen)
         x = x.float().contiguous()
-        updates = torch.zeros(B, dtype=torch.float64, device=device)
+        updates = torch.zeros(n * K, dtype=torch.float64, device=device)
         t = 0
         for t_rec, stop in enumerate(steps + ([] if record else [rc.depth])):
             x, _, fired = rollout_steps(
@@ -126,42 +161,60 @@ def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None
             updates += fired.double()
             t = stop
             if record:
-                dec, conf = decode_tokens(model, x, given, inputs) if fill_given else (None, None)
-                correct = ((dec == targets).float() * mutable).sum(dim=(1, 2))
-                sl = slice(start, start + n)
-                tr["exact"][sl, :, t_rec] = (correct == n_mut).view(n, K).cpu().numpy()
-                tr["cell"][sl, :, t_rec] = (correct / n_mut).view(n, K).cpu().numpy()
-                tr["conf"][sl, :, t_rec] = conf.view(n, K).cpu().numpy()
-                tr["upd"][sl, :, t_rec] = updates.view(n, K).cpu().numpy()
-        dec, conf = decode_tokens(model, x, given, inputs)
-        out_pred[start:start + n] = dec.view(n, K, H, W).cpu().numpy()
-        out_conf[start:start + n] = conf.view(n, K).cpu().numpy()
-        out_upd[start:start + n] = updates.view(n, K).cpu().numpy()
-    return RolloutResult(out_pred, out_conf, out_alive, out_upd, np.array(steps), tr["exact"],
-                         tr["cell"], tr["conf"], tr["upd"])
+                _, cell, exact, conf = score(x)
+                tr["exact"][rows, t_rec] = exact
+                tr["cell"][rows, t_rec] = cell.float()
+                tr["conf"][rows, t_rec] = conf
+                tr["upd"][rows, t_rec] = updates
+        dec, _, _, conf = score(x)
+        pred[rows] = dec
+        conf_out[rows] = conf
+        upd_out[rows] = updates
+    host = lambda t: t.cpu().numpy()  # noqa: E731
+    return RolloutResult(
+        host(pred).reshape(N, K, H, W), host(conf_out).reshape(N, K), np.ones((N, K), bool),
+        host(upd_out).reshape(N, K), np.array(steps),
+        *((host(tr[k]).reshape(N, K, T) for k in ("exact", "cell", "conf", "upd")) if record
+          else (None, None, None, None)),
+    )
+
+
+def _device_metric(metric, alive, weights):
+    dev = torch.device("cuda", torch.cuda.current_device())
+    m = _lib.upload(np.ascontiguousarray(metric), dev)
+    a = None if alive is None else _lib.upload(np.ascontiguousarray(alive, dtype=bool), dev)
+    w = None if weights is None else _lib.upload(np.asarray(weights, np.float64), dev)
+    return m, a, w
+
+
+def _mean(v, w):
+    v = v.double()
+    return v.mean() if w is None else (v * w).sum() / w.sum()
 
 
 def conf_at_k(metric, conf, alive, ks, weights=None) -> dict[int, float]:
-    """Conf@k (reference rollout.py:317-334): per board the alive trial of highest board
-    confidence among the first k (first maximum), mean metric."""
-    N, K = metric.shape
-    out = {}
-    for k in ks:
-        k = min(k, K)
-        c = np.where(alive[:, :k], conf[:, :k], -np.inf)
-        best = c.argmax(axis=1)
-        out[k] = float(np.average(metric[np.arange(N), best], weights=weights))
-    return out
+    """Conf@k for every k in ks from one run of K trials (reference rollout.py:317-334): per
+    board, the alive trial of highest board confidence among the first k (the first one on
+    ties: `nca_conf_select`), and the (weighted) mean of its metric. Computed on the GPU; one
+    copy of the results to the host."""
+    N, K = np.shape(metric)
+    m, a, w = _device_metric(metric, alive, weights)
+    c = _lib.upload(np.ascontiguousarray(conf, dtype=np.float32), m.device)
+    rows = torch.arange(N, device=m.device)
+    kk = [min(int(k), K) for k in ks]
+    vals = torch.stack([_mean(m[rows, conf_select(c, a, k)], w) for k in kk]).tolist()
+    return dict(zip(kk, vals))
 
 
 def pass_at_k(metric, alive, ks, weights=None) -> dict[int, float]:
-    """Pass@k (reference rollout.py:337-350)."""
-    N, K = metric.shape
-    return {
-        min(k, K): float(np.average((metric[:, : min(k, K)] & alive[:, : min(k, K)]).any(axis=1),
-                                    weights=weights))
-        for k in ks
-    }
+    """Pass@k (reference rollout.py:337-350): the (weighted) fraction of boards with a correct
+    alive trial among the first k. Computed on the GPU; one copy to the host."""
+    N, K = np.shape(metric)
+    m, a, w = _device_metric(metric, alive, weights)
+    ok = m.bool() & (a if a is not None else True)
+    kk = [min(int(k), K) for k in ks]
+    vals = torch.stack([_mean(ok[:, :k].any(dim=1), w) for k in kk]).tolist()
+    return dict(zip(kk, vals))
 
 
 def select_at_k(conf: torch.Tensor, alive: torch.Tensor | None, k: int) -> torch.Tensor:

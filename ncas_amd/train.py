@@ -1,5 +1,5 @@
-"""BPTT training on the HIP path: the chunk forward/backward operator, the reference engine's
-`train_iteration`, its loss weights and the replay pool.
+"""BPTT training on the HIP path: the chunk operator, the reference engine's training interface,
+its loss weights and the replay pool.
 
 * `bptt_chunk(model, x, given4, clamp, targets, weights, ...)` - forward a chunk of
   `len(weights)` steps keeping only its states (C ABI `nca_bptt_forward`), then the fused
@@ -8,31 +8,45 @@
   gradient of the initial state. Replaces the chunk of the reference's
   `Engine.train_iteration` (reference src/nca/engine/engine.py:478-497) that autograd or
   `torch.utils.checkpoint` segments would otherwise differentiate.
-* `Engine(model, rollout, chunk, amp).train_iteration(batch, seeds, c0, weights, grad_clip,
-  apply_update) -> (x, loss, grad_norm)` - the reference's interface (engine.py:366-517):
-  no-grad prefix [0, c0), the chunk with gradient, clipping, the update callback, no-grad
-  suffix; fire masks from per-step Philox keys `seeds` (as from `rng.step_seeds`).
-* `loss_weights(window, chunk)` - reference src/nca/engine/train.py:60-69.
-* `ReplayPool` - the replay buffer of reference src/nca/pool.py:26-204 (sample / write_back /
-  state_dict) for (B, H, W) token boards, on the model's device.
+* `EngineConfig` / `Engine(model, cfg, train_cfg, device)` - the reference engine's
+  constructor and `train_iteration(batch, seeds, c0, weights, grad_clip, apply_update) ->
+  (x, loss, grad_norm)` (reference engine.py:59-155, 167-207, 366-517): a no-grad fp32 prefix
+  [0, c0), the chunk with gradient (bf16 when `train_cfg["amp"]`), clipping, the update callback
+  (after the rollout or right after the backward, `update_after_rollout`), a no-grad fp32 suffix.
+  The chunk runs on the fused chunk operator when the loss is the cross-entropy of an mlp head
+  and no step noise is drawn; otherwise step by step through the differentiable HIP step
+  (`step.make_step`), with the loss of every step computed by torch on the GPU.
+* `loss_weights(window, chunk)` - the per-step weights of `train.loss_window` (reference
+  src/nca/engine/train.py:60-69).
+* `ReplayPool` - the replay buffer of reference src/nca/pool.py:26-204 for (N, H, W) token
+  boards: fresh boards, sampling with fresh replacements, write-back with ages, target swaps,
+  state_dict.
 
-The loss is the per-cell cross-entropy of the mlp head's logits (reference train.py:183-193)
-averaged over cells (or a loss mask), weighted per chunk step and normalised by the sum of
-the weights (step.py:243-245, engine.py:490). Gradients of bf16 cells are those of the rounded
-forward with straight-through rounding, computed in fp32.
+Fire masks come from Philox keyed on (per-step seed; row, step, cell), the same rule as every
+kernel, with global step indices: step s of the iteration uses seed `seeds[s]` and counter step
+s, whether it runs in the prefix, the chunk or the suffix. Step noise (reference
+src/nca/engine/rng.py:51-76: with probability p_t per board, N(0, sigma^2) on a p_s fraction of
+its cells) is drawn from a torch generator seeded with the step's seed.
+
+The chunk loss is sum_t w_t * step_loss(x_{t+1}) / max(sum_t w_t, 1) (reference
+src/nca/engine/step.py:243-245, engine.py:490) with step_loss the mean (or loss-mask weighted
+mean) over cells of the per-cell loss of reference src/nca/train.py:183-207 ("ce", "mse",
+"mse_mean"). Gradients of bf16 cells are those of the rounded forward with straight-through
+rounding, computed in fp32.
 """
 
 from __future__ import annotations
 
 import ctypes
-from dataclasses import dataclass
+from dataclasses import asdict, dataclass
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 from .inference import rollout_steps
-from .rng import fire_desc
+from .rng import fire_desc, fire_mask
 
 _GRAD_NAMES = ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")
 
@@ -44,16 +58,20 @@ def _params(model):
 
 
 def loss_weights(window, chunk: int, device=None) -> torch.Tensor:
-    """Per-chunk-step loss weights for `loss_window` ("all", "last" or an integer w)
-    (reference src/nca/engine/train.py:60-69)."""
-    w = torch.zeros(chunk, device=device)
+    """(chunk,) float weights of the chunk's steps for `train.loss_window` (reference
+    src/nca/engine/train.py:60-69): "all" supervises every step, "last" the final one, an integer
+    w the last w steps. The first supervised step of an integer window follows Python's rule
+    for a slice start (chunk - w, wrapped once when negative, then clipped at 0), which is what
+    the reference's slice assignment does."""
     if window == "all":
-        w[:] = 1.0
+        first = 0
     elif window == "last":
-        w[-1] = 1.0
+        first = chunk - 1
     else:
-        w[chunk - int(window):] = 1.0
-    return w
+        first = chunk - int(window)
+        if first < 0:
+            first = max(first + chunk, 0)
+    return (torch.arange(chunk, device=device) >= first).to(torch.float32)
 
 
 @dataclass
@@ -73,10 +91,12 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
     """Forward + backward of one BPTT chunk of `len(weights)` steps on the GPU.
 
     targets: (B, H, W) class indices in [0, n_out) (`model.output_index(tokens)`); masks:
-    injected fire masks (n, B, 1, H, W), else Philox keyed on `step_seeds` (n,) or `seed`."""
+    injected fire masks (n, B, 1, H, W), else Philox keyed on `step_seeds` (n,) or `seed`, with
+    counter steps step0 .. step0 + n - 1. `weights` is read on the host (a host array avoids a
+    device-to-host copy)."""
     cfg = model.cfg
     if cfg.head != "mlp":
-        raise ValueError("the BPTT loss is the cross-entropy of an mlp head")
+        raise ValueError("the fused chunk's loss is the cross-entropy of an mlp head")
     dev = _lib.require_device(x, given4, clamp, targets, masks, loss_mask, grad_final)
     B, C, H, W = x.shape
     n = len(weights)
@@ -110,9 +130,7 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
     # fp32 master weights for the backward GEMMs (rounded to bf16 on load for bf16 cells)
     params = _params(model)
     master = [p.detach().to(dev, torch.float32).contiguous() for p in params]
-    wts = _lib.CellWeights(master[0].data_ptr(), master[1].data_ptr(), master[2].data_ptr(),
-                           master[3].data_ptr(), master[4].data_ptr(), master[5].data_ptr(),
-                           master[6].data_ptr(), None)
+    wts = _lib.CellWeights(*[m.data_ptr() for m in master], None)
     grads = {name: torch.empty(p.shape, dtype=torch.float32, device=dev)
              for name, p in zip(_GRAD_NAMES, params)}
     gs = _lib.CellGrads(*[grads[k].data_ptr() for k in _GRAD_NAMES])
@@ -133,116 +151,358 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
     return ChunkResult(states[n].clone(), loss, grads, gx0, states.numel() * 4, ws_bytes)
 
 
-class Engine:
-    """The reference engine's training interface (reference src/nca/engine/engine.py:168-517)
-    on the HIP kernels: `rollout` steps per iteration with the BPTT chunk of `chunk` steps at
-    `[c0, c0 + chunk)`; bf16 when `amp`."""
+# ------------------------------------------------------------------------------ losses
+def cell_loss(model, x, targets, kind: str) -> torch.Tensor:
+    """(B, H, W) loss of every cell (reference src/nca/train.py:183-193): squared distance of the
+    output slice to the target token's embedding, summed ("mse") or averaged ("mse_mean") over
+    the output channels, or the cross-entropy of the mlp head's logits ("ce")."""
+    cfg = model.cfg
+    out = x[:, cfg.out_slice]
+    if kind in ("mse", "mse_mean"):
+        sq = (out - model.target_embedding(targets)).square()
+        return sq.sum(dim=1) if kind == "mse" else sq.mean(dim=1)
+    if kind == "ce":
+        if cfg.head != "mlp":
+            raise ValueError("the cross-entropy loss needs an mlp head")
+        logits = F.conv2d(out, model.head.weight, model.head.bias)
+        return F.cross_entropy(logits, model.output_index(targets), reduction="none")
+    raise ValueError(f"unknown loss {kind!r} (ce | mse | mse_mean)")
 
-    def __init__(self, model, rollout: int, chunk: int, amp: bool = False, p_fire=None):
+
+def step_loss(model, x, targets, kind: str, loss_mask=None) -> torch.Tensor:
+    """`cell_loss` averaged over the cells, or over the loss mask's weight (reference
+    src/nca/train.py:196-207)."""
+    per_cell = cell_loss(model, x, targets, kind)
+    if loss_mask is None:
+        return per_cell.mean()
+    return (per_cell * loss_mask).sum() / loss_mask.sum().clamp_min(1)
+
+
+# ------------------------------------------------------------------------------ the engine
+@dataclass
+class EngineConfig:
+    """The reference's engine options (reference src/nca/engine/engine.py:59-92), same fields
+    and defaults, so that a training config's `engine:` section loads unchanged. On the HIP
+    engine the backend switches and the compile / checkpoint / graph options have no effect:
+    there is one fused backend, and the BPTT chunk keeps only its states and recomputes the rest
+    in its backward. `update_after_rollout` is honoured; `microbatch` is refused (the chunk's
+    memory is states only, so a batch does not need splitting)."""
+
+    backend: str = "fused"
+    compile: bool = False
+    block: int = 1
+    compile_mode: str | None = None
+    compile_backward_only: bool = False
+    checkpoint_segment: int | str | None = "auto"
+    checkpoint_candidates: tuple = (1, 2, 4, 8, 16, 32)
+    vram_budget: float = 0.85
+    update_after_rollout: bool = True
+    project_before_pad: bool | None = None
+    fused_mix: bool | None = None
+    fused_update: bool | None = None
+    kernel_mix: bool = False
+    kernel_backward: bool | str = False
+    triton_mix: bool = False
+    microbatch: int | None = None
+    checkpoint_recursive: bool = False
+    channels_last: bool = False
+    normalized_backward: bool = False
+    compile_update: bool = False
+    sparse_mlp: bool = False
+    sparse_sobel: bool = False
+    cache_fire: bool = False
+    checkpoint_mlp: bool = False
+    skip_zero_loss: bool = False
+    linear_mlp: bool = False
+    clone_microbatch_grads: bool = False
+    linear_value: bool = False
+    attention_split_k: int = 1
+    iteration_graph: bool = False
+    triton_mlp: bool = False
+    dynamo_cache_size: int = 64
+
+    def __post_init__(self) -> None:
+        if self.backend not in ("reference", "fused", "hip"):
+            raise ValueError(f"unknown backend {self.backend!r} (reference | fused | hip)")
+        if self.block < 1:
+            raise ValueError("block must be >= 1")
+        if self.microbatch is not None:
+            raise ValueError("microbatch is not implemented by the HIP engine (the chunk keeps "
+                             "only its states, so the batch is not split)")
+        self.checkpoint_candidates = tuple(int(c) for c in self.checkpoint_candidates)
+
+    @classmethod
+    def from_dict(cls, d: dict | None) -> EngineConfig:
+        return cls(**(d or {}))
+
+    def to_dict(self) -> dict:
+        return asdict(self)
+
+
+@dataclass
+class StepDraw:
+    """The random tensors of one step (reference src/nca/engine/rng.py:42-48)."""
+
+    fire: torch.Tensor                 # (B, 1, H, W) float in {0, 1}
+    noise: torch.Tensor | None         # (B, C, H, W) or None
+    noise_mask: torch.Tensor | None    # (B, 1, H, W) bool or None
+
+
+def _noise_active(noise: dict | None) -> bool:
+    return noise is not None and all(noise[k] > 0 for k in ("sigma", "p_t", "p_s"))
+
+
+class Engine:
+    """The reference engine's training interface (reference src/nca/engine/engine.py:167-517)
+    on the HIP kernels. `train_cfg` is the resolved `train` section: `rollout`, `chunk`, `amp`,
+    `loss`, and `noise` / `perturb` for step noise."""
+
+    def __init__(self, model, cfg: EngineConfig | None, train_cfg: dict, device=None):
+        from .step import make_step
+
         model.kernel_support()
-        if model.cfg.head != "mlp":
-            raise ValueError("Engine trains mlp-head cells (cross-entropy loss)")
-        if not 1 <= chunk <= rollout:
+        self.model = model
+        self.cfg = cfg if cfg is not None else EngineConfig()
+        self.tr = train_cfg
+        self.device = torch.device(device) if device is not None else model.device
+        self.N, self.Nc = int(train_cfg["rollout"]), int(train_cfg["chunk"])
+        if not 1 <= self.Nc <= self.N:
             raise ValueError("need 1 <= chunk <= rollout")
-        self.model, self.N, self.Nc, self.amp = model, rollout, chunk, amp
-        self.p_fire = model.cfg.fire_rate if p_fire is None else p_fire
+        self.loss_kind = train_cfg.get("loss", "ce")
+        if self.loss_kind not in ("ce", "mse", "mse_mean"):
+            raise ValueError(f"unknown loss {self.loss_kind!r} (ce | mse | mse_mean)")
+        if self.loss_kind == "ce" and model.cfg.head != "mlp":
+            raise ValueError("the cross-entropy loss needs an mlp head")
+        self.step = make_step(model)
+        self.segment = None  # what the reference's EngineState reports: no checkpoint segments
         self.last_chunk: ChunkResult | None = None
+        self._weights_host = None
 
     @property
-    def precision(self) -> str:
-        return "bf16" if self.amp else "fp32"
+    def p_fire(self) -> float:
+        return self.model.cfg.fire_rate
 
-    def _run(self, x, batch, seeds):
+    @property
+    def noise_cfg(self) -> dict | None:
+        """Step noise of the rollout (reference engine.py:215-219): `noise` unless `perturb` is
+        off; None when inactive."""
+        noise = self.tr.get("noise") if self.tr.get("perturb", True) else None
+        return noise if _noise_active(noise) else None
+
+    @property
+    def fused_chunk(self) -> bool:
+        """Does the chunk run on the fused chunk operator (else step by step)?"""
+        return self.loss_kind == "ce" and self.model.cfg.head == "mlp" and self.noise_cfg is None
+
+    def to_dict(self) -> dict:
+        return {"config": self.cfg.to_dict(), "fused_chunk": self.fused_chunk, "segment": None}
+
+    # ------------------------------------------------------------------ random draws
+    def draw(self, seed: int, step: int, shape) -> StepDraw:
+        """Fire mask and noise of global step `step` whose seed is `seed`."""
+        B, C, H, W = shape
+        fire = fire_mask(B, H, W, int(seed), int(step), self.p_fire, device=self.device)
+        noise = self.noise_cfg
+        if noise is None:
+            return StepDraw(fire, None, None)
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(int(seed))
+        dev = self.device
+        hit = torch.rand((B, 1, 1, 1), generator=gen, device=dev) < noise["p_t"]
+        cells = torch.rand((B, 1, H, W), generator=gen, device=dev) < noise["p_s"]
+        mask = hit & cells
+        g = torch.randn((B, C, H, W), generator=gen, device=dev)
+        return StepDraw(fire, g * (noise["sigma"] * mask.to(g.dtype)), mask)
+
+    # ------------------------------------------------------------------ running steps
+    def forward_steps(self, x, given4, clamp, seeds, step0: int):
+        """The steps `seeds` (global steps step0, step0 + 1, ...) without gradient, in fp32 (the
+        reference runs the steps outside the chunk without autocast, engine.py:285-292): one
+        fused launch, or step by step when step noise is drawn."""
         if len(seeds) == 0:
             return x
         with torch.no_grad():
-            y, _, _ = rollout_steps(self.model, x, batch["given4"], batch["clamp"], len(seeds),
-                                    step_seeds=seeds, p_fire=self.p_fire,
-                                    precision=self.precision, want_conf=False)
-        return y
+            if self.noise_cfg is None:
+                y, _, _ = rollout_steps(self.model, x, given4, clamp, len(seeds),
+                                        step_seeds=np.asarray(seeds, dtype=np.int64),
+                                        step0=step0, p_fire=self.p_fire, precision="fp32",
+                                        want_conf=False)
+                return y
+            for i, s in enumerate(seeds):
+                d = self.draw(s, step0 + i, x.shape)
+                x = self.step(x, given4, clamp, d.fire, d.noise, d.noise_mask)
+            return x
+
+    def _host_weights(self, weights) -> np.ndarray:
+        """The loss weights on the host, copied once per weights tensor version (the training
+        loop passes the same tensor every iteration)."""
+        if not torch.is_tensor(weights):
+            return np.asarray(weights, dtype=np.float32)
+        c = self._weights_host
+        key = (id(weights), weights._version, weights.data_ptr())
+        if c is None or c[0] != key:
+            c = (key, weights.detach().cpu().numpy().astype(np.float32))
+            self._weights_host = c
+        return c[1]
+
+    def _chunk_steps(self, x, batch, seeds, step0, weights, precision):
+        """The chunk step by step through the differentiable step; returns (x, loss)."""
+        model = self.model
+        given4, clamp, targets = batch["given4"], batch["clamp"], batch["targets"]
+        loss_mask = batch.get("loss_mask")
+        x = x.detach()
+        total = None
+        for i, s in enumerate(seeds):
+            d = self.draw(s, step0 + i, x.shape)
+            x = self.step(x, given4, clamp, d.fire, d.noise, d.noise_mask)
+            if weights[i] == 0:
+                continue
+            term = float(weights[i]) * step_loss(model, x, targets, self.loss_kind, loss_mask)
+            total = term if total is None else total + term
+        if total is None:  # no supervised step: a zero loss that still reaches the parameters
+            total = sum(p.sum() for p in model.parameters()) * 0.0
+        return x, total / max(float(np.sum(weights)), 1.0)
 
     def train_iteration(self, batch: dict, seeds, c0: int, weights, grad_clip,
                         apply_update=None):
         """Roll the batch out for `rollout` steps with the BPTT chunk at `[c0, c0 + chunk)`,
         add the chunk loss's gradients to the parameters' `.grad`, clip them to `grad_clip`
-        (if not None) and call `apply_update(grad_norm)`. Returns (final state, loss, grad norm)
-        as device tensors (reference engine.py:366-517, update_after_rollout)."""
+        (if not None) and call `apply_update(grad_norm)` after the rollout or, with
+        `update_after_rollout` off, right after the backward. Returns (final state, loss, grad
+        norm) as device tensors, with no host synchronisation (reference engine.py:366-517)."""
         model = self.model
         seeds = np.asarray(seeds, dtype=np.int64)
         if len(seeds) != self.N:
             raise ValueError(f"need {self.N} step seeds")
         if not 0 <= c0 <= self.N - self.Nc:
             raise ValueError("the chunk must lie inside the rollout")
-        x = self._run(batch["x"], batch, seeds[:c0])
-        targets = model.output_index(batch["targets"])
-        res = bptt_chunk(model, x, batch["given4"], batch["clamp"], targets, weights,
-                         step_seeds=seeds[c0:c0 + self.Nc], p_fire=self.p_fire,
-                         precision=self.precision, loss_mask=batch.get("loss_mask"))
-        self.last_chunk = res
-        for name, p in zip(_GRAD_NAMES, _params(model)):
-            g = res.grads[name].reshape(p.shape).to(p.dtype)
-            p.grad = g if p.grad is None else p.grad + g
+        given4, clamp = batch["given4"], batch["clamp"]
+        lo, hi = c0, c0 + self.Nc
+        w = self._host_weights(weights)
+        if len(w) != self.Nc:
+            raise ValueError("need one loss weight per chunk step")
+        precision = "bf16" if self.tr.get("amp", False) else "fp32"
+        x = self.forward_steps(batch["x"], given4, clamp, seeds[:lo], 0)
+        if self.fused_chunk:
+            res = bptt_chunk(model, x, given4, clamp, model.output_index(batch["targets"]), w,
+                             step_seeds=seeds[lo:hi], step0=lo, p_fire=self.p_fire,
+                             precision=precision, loss_mask=batch.get("loss_mask"))
+            self.last_chunk = res
+            for name, p in zip(_GRAD_NAMES, _params(model)):
+                g = res.grads[name].reshape(p.shape).to(p.dtype)
+                p.grad = g if p.grad is None else p.grad + g
+            x, loss = res.x, res.loss
+        else:
+            with torch.enable_grad():
+                x, loss = self._chunk_steps(x, batch, seeds[lo:hi], lo, w, precision)
+                loss.backward()
+            x, loss = x.detach(), loss.detach()
         if grad_clip is not None:
             gn = torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
         else:
-            gn = res.loss.new_zeros(())
-        x = self._run(res.x, batch, seeds[c0 + self.Nc:])
-        if apply_update is not None:
+            gn = loss.new_zeros(())
+        if apply_update is not None and not self.cfg.update_after_rollout:
             apply_update(gn)
-        return x, res.loss, gn
+        x = self.forward_steps(x, given4, clamp, seeds[hi:], hi)
+        if apply_update is not None and self.cfg.update_after_rollout:
+            apply_update(gn)
+        return x, loss, gn
 
 
+# ------------------------------------------------------------------------------ replay pool
 class ReplayPool:
     """Replay buffer of (state, board) pairs (reference src/nca/pool.py:26-204) for boards given
-    as numpy (N, H, W) token grids with a boolean `given` mask (`tasks.Boards`)."""
+    as numpy (N, H, W) token grids with a boolean `given` mask (`tasks.Boards`), kept on the
+    model's device. Entries carry the state x, given4, clamp, inputs, targets, an optional
+    loss_mask (from the boards' meta) and their age in rollouts."""
+
+    KEYS = ("x", "given4", "clamp", "inputs", "targets", "loss_mask")
 
     def __init__(self, model, boards, size: int, rng: np.random.Generator,
-                 generator: torch.Generator | None = None):
+                 generator: torch.Generator | None = None, task=None, augment: bool = False):
         self.model, self.boards, self.size, self.rng = model, boards, size, rng
-        self.generator = generator
+        self.generator, self.task, self.augment = generator, task, augment
         self.device = model.device
-        fresh = self.fresh(size)
-        self.x, self.given4, self.clamp = fresh["x"], fresh["given4"], fresh["clamp"]
-        self.inputs, self.targets = fresh["inputs"], fresh["targets"]
+        for key, value in self.fresh(size).items():
+            setattr(self, key, value)
         self.age = torch.zeros(size, dtype=torch.long, device=self.device)
 
     def fresh(self, n: int) -> dict:
-        """`n` fresh boards drawn uniformly with freshly initialised states (pool.py:58-87)."""
-        idx = self.rng.integers(0, len(self.boards), size=n)
-        sub = self.boards.subset(idx)
-        inputs = _lib.upload(sub.inputs, self.device)
-        targets = _lib.upload(sub.targets, self.device)
-        given = _lib.upload(sub.given, self.device)
+        """`n` boards drawn uniformly (with replacement) from the board set, augmented when the
+        pool has a task that augments, each with a freshly initialised state."""
+        picks = self.rng.integers(0, len(self.boards), size=n)
+        chosen = self.boards.subset(picks)
+        if self.augment and self.task is not None:
+            chosen = self.task.augment(chosen, self.rng)
+        dev = self.device
+        inputs = _lib.upload(chosen.inputs, dev)
+        given = _lib.upload(chosen.given, dev)
         x, given4, clamp = self.model.init_state(inputs, given, None, self.generator)
-        return dict(x=x.detach(), given4=given4, clamp=clamp, inputs=inputs, targets=targets)
+        lm = chosen.meta.get("loss_mask")
+        return {"x": x.detach(), "given4": given4, "clamp": clamp, "inputs": inputs,
+                "targets": _lib.upload(chosen.targets, dev),
+                "loss_mask": None if lm is None else _lib.upload(np.asarray(lm, np.float32), dev)}
 
     def sample(self, batch_size: int, seed_ratio: float):
-        """`batch_size` pool entries without replacement, the first round(seed_ratio * batch)
-        replaced by fresh boards (pool.py:90-131). Returns (indices, batch dict of copies)."""
+        """`batch_size` distinct pool entries (copies), of which the first
+        round(seed_ratio * batch_size) are replaced by fresh boards of age 0. Returns (pool
+        indices, batch dict)."""
         idx = self.rng.choice(self.size, size=batch_size, replace=False)
-        di = _lib.upload(idx, self.device)
-        batch = {k: getattr(self, k).index_select(0, di)
-                 for k in ("x", "given4", "clamp", "inputs", "targets", "age")}
-        n_fresh = int(round(seed_ratio * batch_size))
-        if n_fresh > 0:
-            f = self.fresh(n_fresh)
-            for k in ("x", "given4", "clamp", "inputs", "targets"):
-                batch[k][:n_fresh] = f[k]
-            batch["age"][:n_fresh] = 0
+        rows = _lib.upload(idx, self.device)
+        batch = {k: (None if getattr(self, k) is None else getattr(self, k).index_select(0, rows))
+                 for k in self.KEYS + ("age",)}
+        n_new = int(round(seed_ratio * batch_size))
+        if n_new > 0:
+            for k, v in self.fresh(n_new).items():
+                if v is not None:
+                    batch[k][:n_new] = v
+            batch["age"][:n_new] = 0
         return idx, batch
 
+    def replace_boards(self, batch: dict, which: np.ndarray) -> None:
+        """Target swap with fresh boards: samples `which` get a new board (given cells, clamp
+        values, inputs, targets, loss mask) and keep their state, re-clamped
+        (reference pool.py:123-135)."""
+        if len(which) == 0:
+            return
+        new = self.fresh(len(which))
+        sel = _lib.upload(np.asarray(which), self.device)
+        for k in ("given4", "clamp", "inputs", "targets", "loss_mask"):
+            if batch.get(k) is not None:
+                batch[k][sel] = new[k]
+        batch["x"] = self.model.apply_clamp(batch["x"], batch["given4"], batch["clamp"])
+
+    def swap_from_pool(self, batch: dict, which: np.ndarray) -> None:
+        """Target swap from the pool (reference pool.py:137-165): samples `which` take the board
+        of a uniformly drawn pool entry and that entry's input channels on its given cells; the
+        rest of their state is kept and their age restarts at 0."""
+        if len(which) == 0:
+            return
+        src = _lib.upload(self.rng.integers(0, self.size, size=len(which)), self.device)
+        sel = _lib.upload(np.asarray(which), self.device)
+        for k in ("given4", "clamp", "inputs", "targets", "loss_mask"):
+            if batch.get(k) is not None:
+                batch[k][sel] = getattr(self, k)[src]
+        batch["age"][sel] = 0
+        sl = self.model.cfg.in_slice
+        g = batch["given4"][sel]
+        batch["x"][sel, sl] = torch.where(g, self.x[src][:, sl], batch["x"][sel, sl])
+        batch["x"] = self.model.apply_clamp(batch["x"], batch["given4"], batch["clamp"])
+
     def write_back(self, idx, batch: dict) -> None:
-        """Store the post-rollout states back (pool.py:166-179)."""
-        di = _lib.upload(idx, self.device)
+        """Store the batch's post-rollout states and boards at the pool indices they came from,
+        one rollout older (reference pool.py:166-179)."""
+        rows = _lib.upload(idx, self.device)
         with torch.no_grad():
-            self.x[di] = batch["x"].detach()
-        for k in ("given4", "clamp", "inputs", "targets"):
-            getattr(self, k)[di] = batch[k]
-        self.age[di] = batch["age"] + 1
+            self.x[rows] = batch["x"].detach()
+        for k in ("given4", "clamp", "inputs", "targets", "loss_mask"):
+            if getattr(self, k) is not None and batch.get(k) is not None:
+                getattr(self, k)[rows] = batch[k]
+        self.age[rows] = batch["age"] + 1
 
     def state_dict(self) -> dict:
-        return {k: getattr(self, k) for k in ("x", "given4", "clamp", "inputs", "targets", "age")}
+        return {k: getattr(self, k) for k in self.KEYS + ("age",)}
 
     def load_state_dict(self, d: dict) -> None:
         for k, v in d.items():
-            setattr(self, k, v.to(self.device))
+            setattr(self, k, None if v is None else v.to(self.device))

@@ -129,3 +129,19 @@ def oracle_cell(model) -> OracleCell:
         head_w=hw.clone().float(), head_b=None if hb is None else hb.clone().float(),
         pad_vec=model.pad_vec.detach().clone(),
     )
+
+
+def one_step_errors(cell, x0, states, given4, clamp, masks, precision):
+    """Max-abs error of every step of a GPU trajectory against the oracle's step from the GPU's
+    own previous state: states[t] (CPU) vs O.step(states[t - 1], masks[t]) (states[-1] = x0).
+    In bf16 this is the per-step bar: a trajectory comparison also counts the amplification of
+    bf16 rounding flips (fp32 sums in another order landing on the other side of a bf16 rounding
+    boundary), which grows with the number of steps for cells whose dynamics amplify them."""
+    from oracle import nca_oracle as O
+
+    errs, prev = [], x0
+    for t, s in enumerate(states):
+        ref = O.step(cell, prev, given4, clamp, masks[t], precision).float()
+        errs.append((s - ref).abs().max().item())
+        prev = s
+    return errs

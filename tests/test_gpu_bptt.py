@@ -1,5 +1,5 @@
 """The BPTT chunk on the GPU (nca_bptt_forward / nca_bptt_backward through the C ABI) against the
-fp64 autograd oracle, plus the engine's train_iteration around it.
+fp64 autograd oracle (the engine around it is tested in test_gpu_train.py).
 
 * fp32 cells: loss and every parameter gradient (and d L / d x0) within a relative norm error
   of 1e-4 of the oracle over multi-step chunks with sparse step weights, a loss mask, wall /
@@ -27,7 +27,7 @@ from cells import CELLS, DYN, boards_for, initial_state, make_model, oracle_cell
 from ncas_amd import _lib  # noqa: E402
 from ncas_amd.inference import rollout_steps  # noqa: E402
 from ncas_amd.tasks import maze_boards  # noqa: E402
-from ncas_amd.train import Engine, bptt_chunk  # noqa: E402
+from ncas_amd.train import bptt_chunk  # noqa: E402
 from oracle import nca_oracle as O  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -260,28 +260,3 @@ def test_bptt_30x30_hard_maze_chunk_matches_oracle():
     states = 33 * 64 * 32 * 900 * 4
     _say(f"full chunk: states {states / 2**20:.1f} MiB + workspace {ws / 2**20:.1f} MiB")
     assert 0 < ws < 512 * 2**20
-
-
-def test_engine_train_iteration_composes_prefix_chunk_suffix():
-    m, md, x, g4, cl, _, targets_idx = _case("maze_hard_c32", steps=1)
-    tokens = torch.tensor(m.cfg.output_tokens)[targets_idx]
-    batch = {"x": x.to(DEV), "given4": g4.to(DEV), "clamp": cl.to(DEV), "targets": tokens.to(DEV)}
-    seeds = np.arange(100, 110, dtype=np.int64)
-    eng = Engine(md, rollout=10, chunk=4, amp=False)
-    calls = []
-    for p in md.parameters():
-        p.grad = None
-    xf, loss, gn = eng.train_iteration(batch, seeds, 3, [1, 0, 1, 1], grad_clip=1e9,
-                                       apply_update=calls.append)
-    assert len(calls) == 1 and torch.equal(calls[0], gn)
-    with torch.no_grad():
-        x3, _, _ = rollout_steps(md, batch["x"], batch["given4"], batch["clamp"], 3,
-                                 step_seeds=seeds[:3], p_fire=m.cfg.fire_rate)
-        ref = bptt_chunk(md, x3, batch["given4"], batch["clamp"], targets_idx.to(DEV), [1, 0, 1, 1],
-                         step_seeds=seeds[3:7], p_fire=m.cfg.fire_rate)
-        xe, _, _ = rollout_steps(md, ref.x, batch["given4"], batch["clamp"], 3,
-                                 step_seeds=seeds[7:], p_fire=m.cfg.fire_rate)
-    assert torch.equal(xf, xe) and torch.equal(loss, ref.loss)
-    assert torch.equal(md.update.fc1.weight.grad, ref.grads["w1"].reshape(md.update.fc1.weight.shape))
-    total = torch.sqrt(sum((ref.grads[k].double() ** 2).sum() for k in NAMES))
-    assert abs(float(gn) - float(total)) <= 1e-5 * float(total)

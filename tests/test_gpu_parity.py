@@ -15,7 +15,7 @@ import pytest
 import torch
 
 sys.path.insert(0, __file__.rsplit("/", 1)[0])
-from cells import CELLS, boards_for, initial_state, make_model, oracle_cell  # noqa: E402
+from cells import CELLS, boards_for, initial_state, make_model, one_step_errors, oracle_cell  # noqa: E402
 
 from ncas_amd.inference import rollout_steps  # noqa: E402
 from ncas_amd.readout import conf_select, readout  # noqa: E402
@@ -30,14 +30,11 @@ DEV = torch.device("cuda:0")
 
 
 def state_error(name, precision, y, ref):
-    """Max violation ratio of the state tolerance (<= 1 passes). fp32: max-abs 1e-4. bf16:
-    max-abs 2e-2 for the north-star cells (|x| <= ~2); the reference's trained maze cells reach
-    |x| ~ 7, where one bf16 rounding flip of dx alone moves a state by up to 2^-7 |dx|, so there
-    the bound is 2e-2 + 2^-8 |x_ref| per element (2e-2 plus half a bf16 ulp of the value)."""
-    d = (y - ref).abs()
-    if precision == "bf16" and name.startswith("ref_"):
-        return (d / (TOL["bf16"] + ref.abs() * 2.0**-8)).max().item()
-    return d.max().item() / TOL[precision]
+    """Max-abs state error as a fraction of the north-star bar (<= 1 passes): 1e-4 (fp32) or
+    2e-2 (bf16), absolute for every cell, the reference's trained cells included (the reference
+    compares states absolutely, src/nca/engine/bench.py:500-509)."""
+    del name
+    return (y - ref).abs().max().item() / TOL[precision]
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -161,14 +158,6 @@ def test_step_under_bf16_autocast_is_the_bf16_path():
     assert a.dtype == torch.float32 and torch.equal(a, b)
 
 
-def test_step_refuses_autograd():
-    m, md, x, g4, cl = _case("maze_c16")
-    step = make_step(md)
-    fire = torch.ones(x.shape[0], 1, *x.shape[2:], device=DEV)
-    with pytest.raises(NotImplementedError):
-        step(x.to(DEV), g4.to(DEV), cl.to(DEV), fire)
-
-
 # ------------------------------------------------------------------------------ rollouts
 @pytest.mark.parametrize("precision", ["fp32", "bf16"])
 @pytest.mark.parametrize("name", list(CELLS))
@@ -182,18 +171,28 @@ def test_rollout_64_steps_matches_oracle(name, precision):
     xr, fired_ref = O.rollout(cell, x, g4, cl, 64, precision, seed=5, row0=11, step0=3, p_fire=p,
                               trace=lambda t, s: ref_states.append(s.clone()))
     xd, gd, cd = x.to(DEV), g4.to(DEV), cl.to(DEV)
+    B, C, H, W = x.shape
+    states = []
     with torch.no_grad():
         cur = xd.clone()
         fired = torch.zeros(x.shape[0], dtype=torch.int64)
-        worst = 0.0
         for t in range(64):
             cur, _, f = rollout_steps(md, cur, gd, cd, 1, seed=5, row0=11, step0=3 + t, p_fire=p,
                                       precision=precision, want_fired=True)
             fired += f.cpu().long()
-            worst = max(worst, (cur.cpu() - ref_states[t]).abs().max().item())
+            states.append(cur.cpu())
         fused, conf, ff = rollout_steps(md, xd, gd, cd, 64, seed=5, row0=11, step0=3, p_fire=p,
                                         precision=precision, want_fired=True)
-    assert worst <= 1.0, worst
+    traj = [(s - r).abs().max().item() for s, r in zip(states, ref_states)]
+    masks = [O.fire_masks_np(5, 11, B, 3 + t, H, W, p) for t in range(64)]
+    step_errs = one_step_errors(cell, x, states, g4, cl, masks, precision)
+    _say(f"worst one-step error {max(step_errs):.3g}, trajectory drift {max(traj):.3g} "
+         f"(bar {TOL[precision]})")
+    assert max(step_errs) <= TOL[precision]
+    if precision == "fp32":
+        assert max(traj) <= TOL["fp32"]
+    else:  # bf16: rounding flips amplify along the trajectory; O(1) errors would mean a bug
+        assert max(traj) <= 5 * TOL["bf16"]
     assert torch.equal(fused, cur), "fused rollout differs from chained single steps"
     assert torch.equal(fired, fired_ref) and torch.equal(ff.cpu().long(), fired_ref)
     # the in-kernel board confidence is the readout of the final state, bit for bit
@@ -276,9 +275,10 @@ def test_full_c3_batch_rows_match_oracle():
 
 
 def test_decode_and_selection_bit_exact_fp32():
-    """fp32 trajectory of 256 rows (32 boards x K=8) over 64 steps: decoded argmax and conf@K
-    indices equal the oracle's; near-ties (logit or confidence gaps below what fp32 summation
-    order can move) are counted and must not occur."""
+    """fp32 trajectory of 256 rows (32 boards x K=8) over 64 steps: every decoded argmax and
+    every conf@K index equals the oracle's trajectory's, with no exception for near-ties; the
+    smallest top-2 logit gap and the smallest conf@K gap are printed (the margins that fp32
+    summation-order differences would have to cross)."""
     _say("decode + conf@K")
     m, md, x, g4, cl = _case("sudoku_c64", n_boards=32, k=8)
     cell = oracle_cell(m)
@@ -290,22 +290,50 @@ def test_decode_and_selection_bit_exact_fp32():
     # decode of the same state is bit-exact
     gc, gb, ga = O.readout(cell, y.cpu())
     assert np.array_equal(am.cpu().numpy(), ga) and np.array_equal(cb.cpu().numpy(), gb)
-    # trajectory-level: same argmax except at near-ties of the oracle's logits
-    logits = torch.einsum("vc,bchw->bvhw", cell.head_w, xr[:, cell.out_offset:cell.out_offset + cell.c_out]) \
+    # trajectory level: every cell's argmax
+    logits = torch.einsum("vc,bchw->bvhw", cell.head_w,
+                          xr[:, cell.out_offset:cell.out_offset + cell.c_out]) \
         + cell.head_b[None, :, None, None]
     top2 = logits.topk(2, dim=1).values
-    near = ((top2[:, 0] - top2[:, 1]) < 1e-4).numpy()
-    mism = am.cpu().numpy() != ra
-    assert not (mism & ~near).any()
-    _say("near-tie cells:", int(near.sum()), "of", near.size, "mismatches:", int(mism.sum()))
+    margin = float((top2[:, 0] - top2[:, 1]).min())
+    mism = int((am.cpu().numpy() != ra).sum())
+    _say(f"argmax mismatches {mism} of {ra.size}, smallest top-2 logit gap {margin:.3g}")
+    assert mism == 0
     # conf@K selection
     N, K = 32, 8
     sel = conf_select(conf.view(N, K), None, K).cpu().numpy()
     ref = clib.conf_select(rb.reshape(N, K), None, K)
     srt = np.sort(rb.reshape(N, K), axis=1)
-    gap = srt[:, -1] - srt[:, -2]
-    assert np.array_equal(sel[gap > 1e-5], ref[gap > 1e-5])
-    _say("near-tie boards:", int((gap <= 1e-5).sum()), "of", N)
+    _say(f"smallest conf@K gap {float((srt[:, -1] - srt[:, -2]).min()):.3g}")
+    assert np.array_equal(sel, ref)
+
+
+def test_conf_at_k_and_pass_at_k_on_the_gpu():
+    """The GPU conf@K / pass@K: the reference's inline known answers
+    (tests/test_rollout.py:63-68, tests/test_regressions_evaluation.py:68-73), then random
+    metrics with ties, dead trials and board weights against the oracle's numpy rule."""
+    from ncas_amd.rollout import conf_at_k, pass_at_k
+
+    metric = np.array([[True, False, False], [False, False, True]])
+    conf = np.array([[0.1, 0.9, 0.5], [0.2, 0.3, 0.9]])
+    alive = np.ones((2, 3), dtype=bool)
+    assert conf_at_k(metric, conf, alive, [1, 2, 3]) == {1: 0.5, 2: 0.0, 3: 0.5}
+    assert pass_at_k(metric, alive, [1, 3]) == {1: 0.5, 3: 1.0}
+    m1, c1, a1 = np.array([[1.0], [0.0]]), np.ones((2, 1)), np.ones((2, 1), bool)
+    assert conf_at_k(m1, c1, a1, [1])[1] == 0.5
+    assert conf_at_k(m1, c1, a1, [1], weights=np.array([0.9, 0.1]))[1] == 0.9
+    rng = np.random.default_rng(3)
+    N, K = 300, 16
+    metric = rng.random((N, K)) < 0.4
+    conf = (rng.integers(0, 6, (N, K)) / 6).astype(np.float32)  # many ties
+    alive = rng.random((N, K)) < 0.8
+    w = rng.random(N)
+    ks = [1, 2, 5, 16, 40]
+    for weights in (None, w):
+        got, ref = conf_at_k(metric, conf, alive, ks, weights), O.conf_at_k(metric, conf, alive, ks, weights)
+        assert got.keys() == ref.keys() and all(abs(got[k] - ref[k]) <= 1e-12 for k in ref)
+        got, ref = pass_at_k(metric, alive, ks, weights), O.pass_at_k(metric, alive, ks, weights)
+        assert got.keys() == ref.keys() and all(abs(got[k] - ref[k]) <= 1e-12 for k in ref)
 
 
 def test_rollout_api_end_to_end():
@@ -333,13 +361,17 @@ def test_rollout_api_end_to_end():
 @pytest.mark.parametrize("name", ["maze_c16", "sudoku_c64", "maze_hard_c32", "ref_maze_ood"])
 @pytest.mark.parametrize("n_boards,k", [(5, 3), (1, 1), (33, 2)])
 def test_wave_specialised_and_generic_kernels_agree(name, n_boards, k):
-    """bf16 rollouts run by the wave-specialised kernel (default) and by the generic kernel both
-    match the oracle, for odd row counts (a partial last workgroup, an empty row group)."""
+    """bf16 rollouts run by the wave-specialised kernel (default) and by the generic kernel,
+    for odd row counts (a partial last workgroup, an empty row group): one step from the same
+    state (the 24-step state of each) matches the oracle's step within 2e-2, fired counts are
+    exact, and the 24-step trajectories stay within the drift guard of the oracle's."""
     from ncas_amd import _lib
 
     _say("ws vs generic", name, n_boards, k)
     m, md, x, g4, cl = _case(name, n_boards=n_boards, k=k)
-    xr, fr = O.rollout(oracle_cell(m), x, g4, cl, 24, "bf16", seed=4, p_fire=0.6)
+    cell = oracle_cell(m)
+    B, C, H, W = x.shape
+    xr, fr = O.rollout(cell, x, g4, cl, 24, "bf16", seed=4, p_fire=0.6)
     out = {}
     L = _lib.load()
     try:
@@ -348,10 +380,15 @@ def test_wave_specialised_and_generic_kernels_agree(name, n_boards, k):
             with torch.no_grad():
                 y, conf, f = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 24, seed=4,
                                            p_fire=0.6, precision="bf16", want_fired=True)
+                y1, _, _ = rollout_steps(md, y, g4.to(DEV), cl.to(DEV), 1, seed=4, step0=24,
+                                         p_fire=0.6, precision="bf16")
             out[path] = (y.cpu(), conf.cpu(), f.cpu())
+            ref1 = O.step(cell, y.cpu(), g4, cl, O.fire_masks_np(4, 0, B, 24, H, W, 0.6), "bf16")
+            assert (y1.cpu() - ref1).abs().max().item() <= TOL["bf16"], path
     finally:
         L.nca_set_kernel_path(0)
     for path in (0, 1):
-        assert state_error(name, "bf16", out[path][0], xr) <= 1.0, path
+        # 24 bf16 steps from the same state: trajectories within the drift guard of the oracle's
+        assert state_error(name, "bf16", out[path][0], xr) <= 5, path
         assert torch.equal(out[path][2].long(), fr), path
-    assert (out[0][0] - out[1][0]).abs().max().item() <= TOL["bf16"] * 2
+    assert (out[0][0] - out[1][0]).abs().max().item() <= TOL["bf16"] * 5

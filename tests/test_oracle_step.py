@@ -281,22 +281,19 @@ def test_readout_argmax_first_maximum_on_ties():
 # ---------------------------------------------------------------- conf@K (rollout.py:317-350)
 
 def test_conf_at_k_known_answers():
-    """tests/test_rollout.py:63-68 and tests/test_regressions_evaluation.py:68-73."""
-    from ncas_amd.rollout import conf_at_k, pass_at_k
-
+    """The oracle's conf@K / pass@K on the reference's inline known answers
+    (tests/test_rollout.py:63-68 and tests/test_regressions_evaluation.py:68-73); the product's
+    GPU versions are checked against the same answers in test_gpu_parity.py."""
     metric = np.array([[True, False, False], [False, False, True]])
     conf = np.array([[0.1, 0.9, 0.5], [0.2, 0.3, 0.9]])
     alive = np.ones((2, 3), dtype=bool)
-    for f in (conf_at_k, O.conf_at_k):
-        assert f(metric, conf, alive, [1, 2, 3]) == {1: 0.5, 2: 0.0, 3: 0.5}
-    for f in (pass_at_k, O.pass_at_k):
-        assert f(metric, alive, [1, 3]) == {1: 0.5, 3: 1.0}
+    assert O.conf_at_k(metric, conf, alive, [1, 2, 3]) == {1: 0.5, 2: 0.0, 3: 0.5}
+    assert O.pass_at_k(metric, alive, [1, 3]) == {1: 0.5, 3: 1.0}
     metric = np.array([[1.0], [0.0]])
     conf = np.ones((2, 1))
     alive = np.ones((2, 1), bool)
-    for f in (conf_at_k, O.conf_at_k):
-        assert f(metric, conf, alive, [1])[1] == 0.5
-        assert f(metric, conf, alive, [1], weights=np.array([0.9, 0.1]))[1] == 0.9
+    assert O.conf_at_k(metric, conf, alive, [1])[1] == 0.5
+    assert O.conf_at_k(metric, conf, alive, [1], weights=np.array([0.9, 0.1]))[1] == 0.9
 
 def test_conf_select_c_matches_numpy_first_argmax():
     rng = np.random.default_rng(17)
