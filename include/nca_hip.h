@@ -147,6 +147,25 @@ int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, 
                    float *conf_out, int32_t *fired_out, void *workspace, size_t workspace_bytes,
                    void *stream);
 
+/* Bytes of the device scratch that nca_rollout_noalloc uses instead of a caller workspace. */
+#define NCA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+/* nca_rollout_ws without a workspace argument and without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The per-step path's state
+ * buffers live in a device array of the library of NCA_NOALLOC_SCRATCH_BYTES (128 MiB: two
+ * states of 16 boards of 201 x 201 cells with C = 16 take 83 MB), which every GPU the library
+ * runs on holds from its first call until the process ends. A call whose per-step path needs
+ * more (nca_rollout_workspace_bytes) returns NCA_ERR_UNSUPPORTED. Every call on one GPU shares
+ * that array and the previous call's contents stay in it (nothing in it needs to start at
+ * zero): calls that overlap on one GPU (other streams or threads) race, and the caller must
+ * order them. Results equal nca_rollout_ws's bit for bit. */
+int nca_rollout_noalloc(const nca_cell_desc *cell, const void *packed, int64_t rows,
+                        int32_t height, int32_t width, const float *x_in, const uint8_t *given,
+                        const float *clamp, float *x_out, const nca_fire_desc *fire,
+                        int32_t n_steps, const float *noise, float *conf_out, int32_t *fired_out,
+                        void *stream);
+
 /* One step with an injected fire mask (rows, H, W) fp32 in {0,1}: the make_step drop-in. */
 int nca_step(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
              int32_t width, const float *x, const uint8_t *given, const float *clamp,

@@ -14,6 +14,7 @@ import torch
 _SO = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnca_hip.so")
 
 NCA_OK, NCA_ERR_INVALID, NCA_ERR_UNSUPPORTED, NCA_ERR_HIP = 0, 1, 2, 3
+NOALLOC_SCRATCH_BYTES = 128 << 20  # NCA_NOALLOC_SCRATCH_BYTES of include/nca_hip.h
 PADDING = {"zero": 0, "wall": 1, "wrap": 2}
 HEAD = {"mlp": 0, "l2": 1}
 PRECISION = {"fp32": 0, "bf16": 1}
@@ -36,6 +37,7 @@ EXPORTS = (
     "nca_bptt_backward",
     "nca_step_backward_workspace_bytes",
     "nca_step_backward",
+    "nca_rollout_noalloc",
 )
 
 
@@ -120,6 +122,10 @@ def load():
     L.nca_rollout_ws.argtypes = [
         ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, ctypes.POINTER(FireDesc),
         i32, vp, vp, vp, vp, ctypes.c_size_t, vp,
+    ]
+    L.nca_rollout_noalloc.argtypes = [
+        ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp, vp, ctypes.POINTER(FireDesc),
+        i32, vp, vp, vp, vp,
     ]
     L.nca_rollout_workspace_bytes.argtypes = [ctypes.POINTER(CellDesc), i64, i32, i32]
     L.nca_rollout_workspace_bytes.restype = ctypes.c_size_t

@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 
 #include "nca_hip.h"
 #include "nca_device.h"
@@ -512,6 +513,40 @@ int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows
 
 }  // namespace nca
 
+// ------------------------------------------------------------------------------------------
+// The allocation-free entry point's scratch: the per-step path's state buffers in a device
+// array of the library's code object, so that every GPU the library runs on holds its own copy
+// until the process ends. Host code never passes `scratch` itself to a kernel (on the host it is
+// only a stand-in for the symbol): it looks up each device's address once, on that device's
+// first call, and passes that.
+static __device__ __align__(256) unsigned char scratch[NCA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`.
+int scratch_address(void **out) {
+    int dev = 0;
+    int rc = hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxDevices) return fail(NCA_ERR_UNSUPPORTED, "device %d (0..%d)", dev, kMaxDevices - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (rc) return rc;
+        if (!p) return fail(NCA_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return NCA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char *nca_last_error(void) { return g_err; }
@@ -602,6 +637,30 @@ int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, 
     p.adaptive = fire->adaptive;
     p.given_confident = fire->given_confident;
     return dispatch_rollout(cell, p, as_stream(stream), workspace, workspace_bytes);
+}
+
+int nca_rollout_noalloc(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                        int32_t width, const float *x_in, const uint8_t *given, const float *clamp,
+                        float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
+                        float *conf_out, int32_t *fired_out, void *stream) {
+    g_err[0] = 0;
+    int rc = check_cell(cell);
+    if (rc) return rc;
+    if ((rc = check_grid(rows, height, width))) return rc;
+    if (n_steps < 0) return fail(NCA_ERR_INVALID, "n_steps=%d", n_steps);
+    // the per-step path's workspace must fit the scratch (the other paths need none)
+    if (nca_rollout_workspace_bytes(cell, rows, height, width) > 0) {
+        const size_t need = per_step_need(cell, rows, height, width, n_steps, x_in == x_out);
+        if (need > NCA_NOALLOC_SCRATCH_BYTES)
+            return fail(NCA_ERR_UNSUPPORTED,
+                        "this call needs %zu bytes of workspace, above the %zu-byte scratch of "
+                        "nca_rollout_noalloc (use nca_rollout_ws)",
+                        need, (size_t)NCA_NOALLOC_SCRATCH_BYTES);
+    }
+    void *ws = nullptr;
+    if ((rc = scratch_address(&ws))) return rc;
+    return nca_rollout_ws(cell, packed, rows, height, width, x_in, given, clamp, x_out, fire, n_steps, noise,
+                          conf_out, fired_out, ws, NCA_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int nca_rollout(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
