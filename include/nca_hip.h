@@ -259,12 +259,21 @@ int nca_version(void);
 
 /* Kernel selection: 0 = automatic (the streamed bf16 kernel where the grid allows it, the
  * resident kernel where the rows fit LDS, else the per-step path: the wave-per-tile kernel for
- * bf16 cells with 16 channels, the halo-window kernel otherwise), 1 = never the streamed kernel,
- * 2 = always the per-step path, 3 = always the per-step path on the halo-window kernel.
- * Per calling thread (other threads keep their own setting); used by the tests to check the paths
- * against each other and by the bench to time the per-step regime. No counterpart in the
+ * bf16 cells with 16 channels, the halo-window kernel for other cells; with
+ * nca_set_window_steps(T >= 2), bf16 cells with 16 channels on the temporally blocked kernel, T
+ * steps per launch on LDS-resident windows, for calls of two or more steps with uniform firing
+ * and no noise), 1 = never the streamed kernel, 2 = always the per-step path with one step per
+ * launch, 3 = always the per-step path on the halo-window kernel, 4 = the temporally blocked
+ * kernel wherever it applies (2 steps per launch unless set), also on grids the resident kernels
+ * take. Per calling thread (other threads keep their own setting); used by the tests to check
+ * the paths against each other and by the bench to time each regime. No counterpart in the
  * reference. */
 int nca_set_kernel_path(int path);
+
+/* Steps per launch of the temporally blocked kernel (its windows' halo width), 1..8, or 0 for
+ * the automatic choice (one step per launch: the per-step kernels). Per calling thread. No
+ * counterpart in the reference (the reference has no temporal blocking). */
+int nca_set_window_steps(int steps);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,7 @@ EXPORTS = (
     "nca_last_error",
     "nca_version",
     "nca_set_kernel_path",
+    "nca_set_window_steps",
     "nca_bptt_workspace_bytes",
     "nca_bptt_forward",
     "nca_bptt_backward",
@@ -151,6 +152,7 @@ def load():
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
     L.nca_set_kernel_path.argtypes = [ctypes.c_int]
+    L.nca_set_window_steps.argtypes = [ctypes.c_int]
     for name in EXPORTS:
         getattr(L, name).restype = getattr(L, name).restype or ctypes.c_int
     _lib = L

@@ -16,6 +16,7 @@
 #include "nca_stream.h"
 #include "nca_tiled_launch.h"
 #include "nca_status.h"
+#include "nca_window16.h"
 
 namespace {
 
@@ -52,9 +53,16 @@ namespace {
 constexpr unsigned kLdsBytes = 160u * 1024u;  // gfx950 LDS per workgroup
 
 // Kernel selection (nca_set_kernel_path): 0 automatic, 1 generic resident kernel for bf16,
-// 2 the halo-tiled per-step kernel for every grid, 3 the halo-window kernel for every grid. Per
-// thread, so that a thread choosing a path never changes another thread's calls.
+// 2 the per-step kernels for every grid (no temporal blocking), 3 the halo-window per-step kernel
+// for every grid, 4 the temporally blocked kernel wherever it applies, also on grids the
+// resident kernels take. Per thread, so that a thread choosing a path never changes another
+// thread's calls; so is the temporally blocked kernel's step count (nca_set_window_steps).
 thread_local int g_path = 0;
+thread_local int g_window_steps = 0;
+// The automatic choice is one step per launch: on the 201x201 mazes the temporally blocked
+// kernel (2 to 4 steps per launch) measured 63 to 79 us per step against 46 to 50 us for the
+// wave-per-tile kernel, whose state stays in the Infinity Cache between steps.
+constexpr int kDefaultWindowSteps = 1;
 
 bool shape_supported(int C, int hidden) {
     return (C == 16 && hidden == 128) || (C == 32 && hidden == 256) || (C == 64 && hidden == 256);
@@ -328,23 +336,40 @@ bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
     return pa < pb + nb && pb < pa + na;
 }
 
-// Workspace bytes the per-step path asks for (run_tiled): two state buffers for three or more
-// steps, one for two steps or an in-place single step, none otherwise.
-size_t per_step_need(const nca_cell_desc *d, int64_t rows, int H, int W, int n, bool alias) {
-    const size_t sb = state_bytes(d, rows, H, W);
-    return n >= 3 ? 2 * sb : (n == 2 || (n == 1 && alias)) ? sb : 0;
+// Steps per launch on the per-step path: T > 1 when the call runs on the temporally blocked
+// kernel (bf16 cells with C = 16, uniform firing without a float mask, no noise, two or more
+// steps, a window fits), else 1.
+int steps_per_launch(const nca_cell_desc *d, int H, int W, int n, bool noise, bool adaptive, bool fire_f32) {
+    if (g_path == 2 || g_path == 3) return 1;
+    if (d->channels != 16 || d->hidden != 128 || d->precision != NCA_BF16) return 1;
+    if (noise || adaptive || fire_f32 || n < 2) return 1;
+    int T = g_window_steps > 0 ? g_window_steps : g_path == 4 ? 2 : kDefaultWindowSteps;
+    const bool wrap = d->padding == NCA_PAD_WRAP;
+    while (T > 1 && (nca::window16_windows(H, T, wrap) < 1 || nca::window16_windows(W, T, wrap) < 1)) --T;
+    if (T < 2) return 1;
+    return T;
 }
 
-// The per-step path: n_steps launches of the halo-tiled kernel. The first step reads the
-// caller's NCHW x_in and the last writes NCHW x_out; the steps in between alternate between the
-// two halves A, B of the workspace in cell-major order. One step in place goes through A.
+// Workspace bytes the per-step path asks for (run_tiled): two state buffers for three or more
+// launches, one for two launches or an in-place single launch, none otherwise.
+size_t per_step_need(const nca_cell_desc *d, int64_t rows, int H, int W, int n, bool alias, int spl) {
+    const size_t sb = state_bytes(d, rows, H, W);
+    const int launches = spl > 1 ? (n + spl - 1) / spl : n;
+    return launches >= 3 ? 2 * sb : (launches == 2 || (launches == 1 && alias)) ? sb : 0;
+}
+
+// The per-step path: launches of one step each (the wave-per-tile or halo-window kernel) or of
+// T steps each (the temporally blocked kernel). The first launch reads the caller's NCHW x_in
+// and the last writes NCHW x_out; the launches in between alternate between the two halves A, B
+// of the workspace in cell-major order. A single launch in place goes through A.
 int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t st, void *ws, size_t ws_bytes) {
     const size_t sb = state_bytes(d, p.rows, p.H, p.W);
     const int n = p.n_steps;
     const bool alias = p.x_in == p.x_out;
     if (!alias && overlaps(p.x_in, sb, p.x_out, sb))
         return fail(NCA_ERR_INVALID, "x_in and x_out overlap without being the same buffer");
-    const size_t need = per_step_need(d, p.rows, p.H, p.W, n, alias);
+    const int spl = steps_per_launch(d, p.H, p.W, n, p.noise != nullptr, p.adaptive != 0, p.fire_f32 != nullptr);
+    const size_t need = per_step_need(d, p.rows, p.H, p.W, n, alias, spl);
     if (need) {
         if (!ws || ws_bytes < need)
             return fail(NCA_ERR_UNSUPPORTED,
@@ -369,22 +394,30 @@ int run_tiled(const nca_cell_desc *d, const nca::RolloutParams &p, hipStream_t s
         }
     } else {
         const float *src = p.x_in;
-        for (int s = 0; s < n; ++s) {
-            const bool last = s == n - 1;
-            float *dst = last ? (alias && n == 1 ? A : p.x_out) : ((s & 1) ? B : A);
+        const int launches = spl > 1 ? (n + spl - 1) / spl : n;
+        for (int l = 0, s = 0; l < launches; ++l) {
+            const int k = spl > 1 ? (n - s < spl ? n - s : spl) : 1;  // steps of this launch
+            const bool last = l == launches - 1;
+            float *dst = last ? (alias && launches == 1 ? A : p.x_out) : ((l & 1) ? B : A);
             nca::RolloutParams q = p;
             q.x_in = src;
             q.x_out = dst;
             q.noise = s == 0 ? p.noise : nullptr;
-            bool ok = false;
-            int rc = hip_check(nca::tiled_step(d->channels, d->hidden, d->precision == NCA_BF16, q, s, s == 0,
-                                               s == 0, last, st, g_path == 3, &ok),
-                               "tiled step launch");
-            if (rc) return rc;
-            if (!ok)
-                return fail(NCA_ERR_UNSUPPORTED, "no window of a %dx%d grid with C=%d fits the LDS", p.H, p.W,
-                            d->channels);
+            if (spl > 1) {
+                int rc = hip_check(nca::window16_steps(q, s, k, s == 0, s == 0, last, st), "windowed launch");
+                if (rc) return rc;
+            } else {
+                bool ok = false;
+                int rc = hip_check(nca::tiled_step(d->channels, d->hidden, d->precision == NCA_BF16, q, s, s == 0,
+                                                   s == 0, last, st, g_path == 3, &ok),
+                                   "tiled step launch");
+                if (rc) return rc;
+                if (!ok)
+                    return fail(NCA_ERR_UNSUPPORTED, "no window of a %dx%d grid with C=%d fits the LDS", p.H, p.W,
+                                d->channels);
+            }
             src = dst;
+            s += k;
         }
         if (src != p.x_out) {
             int rc = hip_check(hipMemcpyAsync(p.x_out, src, sb, hipMemcpyDeviceToDevice, st), "state copy");
@@ -554,8 +587,16 @@ const char *nca_last_error(void) { return g_err; }
 int nca_version(void) { return 100; }
 
 int nca_set_kernel_path(int path) {
-    if (path < 0 || path > 3) return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic, 2 tiled, 3 windows)", path);
+    if (path < 0 || path > 4)
+        return fail(NCA_ERR_INVALID, "path=%d (0 auto, 1 generic, 2 per-step, 3 halo-window, 4 temporal blocking)",
+                    path);
     g_path = path;
+    return NCA_OK;
+}
+
+int nca_set_window_steps(int steps) {
+    if (steps < 0 || steps > nca::kWinMaxT) return fail(NCA_ERR_INVALID, "steps=%d (0 automatic, 1..%d)", steps, nca::kWinMaxT);
+    g_window_steps = steps;
     return NCA_OK;
 }
 
@@ -650,7 +691,9 @@ int nca_rollout_noalloc(const nca_cell_desc *cell, const void *packed, int64_t r
     if (n_steps < 0) return fail(NCA_ERR_INVALID, "n_steps=%d", n_steps);
     // the per-step path's workspace must fit the scratch (the other paths need none)
     if (nca_rollout_workspace_bytes(cell, rows, height, width) > 0) {
-        const size_t need = per_step_need(cell, rows, height, width, n_steps, x_in == x_out);
+        const int spl = steps_per_launch(cell, height, width, n_steps, noise != nullptr, fire && fire->adaptive,
+                                         false);
+        const size_t need = per_step_need(cell, rows, height, width, n_steps, x_in == x_out, spl);
         if (need > NCA_NOALLOC_SCRATCH_BYTES)
             return fail(NCA_ERR_UNSUPPORTED,
                         "this call needs %zu bytes of workspace, above the %zu-byte scratch of "

@@ -6,6 +6,7 @@
 #include "nca_step16.h"
 #include "nca_tiled_launch.h"
 #include "nca_tiled.h"
+#include "nca_window16.h"
 
 namespace nca {
 
@@ -106,6 +107,45 @@ hipError_t launch_stream16(const RolloutParams &p, int step, int first, hipStrea
 }
 
 }  // namespace
+
+int window16_windows(int L, int T, bool wrap) {
+    if (T < 1 || T > kWinMaxT || 2 * T >= kWinMax) return 0;
+    for (int n = 1; n <= L; ++n) {
+        int widest = 0;
+        for (int i = 0; i < n; ++i) {
+            const WinAxis a = win_axis(i, n, L, T, wrap);
+            const int wdt = a.h0 + (a.hi - a.lo) + a.h1;
+            widest = wdt > widest ? wdt : widest;
+        }
+        if (widest <= kWinMax) return n;
+    }
+    return 0;
+}
+
+hipError_t window16_steps(const RolloutParams &p, int step, int T, int first, int in_nchw, int out_nchw,
+                          hipStream_t st) {
+    Win16Params wp;
+    memset(&wp, 0, sizeof(wp));
+    wp.a = p;
+    wp.step = step;
+    wp.T = T;
+    wp.first = first;
+    wp.in_nchw = in_nchw;
+    wp.out_nchw = out_nchw;
+    const bool wrap = p.padding == 2;
+    wp.nwy = window16_windows(p.H, T, wrap);
+    wp.nwx = window16_windows(p.W, T, wrap);
+    if (wp.nwy < 1 || wp.nwx < 1) return hipErrorInvalidValue;
+    wp.n_windows = p.rows * (int64_t)wp.nwy * wp.nwx;
+    if (wp.n_windows < 1) return hipSuccess;
+    if (wp.n_windows > 0x7fffffff) return hipErrorInvalidValue;
+    auto kfn = first ? rollout_window16<true> : rollout_window16<false>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)kWinLds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kfn, dim3((unsigned)wp.n_windows), dim3(512), kWinLds, st, wp);
+    return hipGetLastError();
+}
 
 hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, int in_nchw,
                       int out_nchw, hipStream_t st, bool windows, bool *ok) {

@@ -17,4 +17,12 @@ namespace nca {
 hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, int in_nchw,
                       int out_nchw, hipStream_t st, bool windows, bool *ok);
 
+// Temporal blocking (rollout_window16): bf16 cells with C = 16 and 128 hidden units, uniform
+// firing (Philox or injected u8 masks), no noise. window16_plan gives the windows per board
+// along an axis of length L for T steps per launch (0: no window of at most kWinMax cells fits).
+int window16_windows(int L, int T, bool wrap);
+// Steps step .. step + T - 1 of the call in one launch: p.x_in -> p.x_out (distinct buffers).
+hipError_t window16_steps(const RolloutParams &p, int step, int T, int first, int in_nchw, int out_nchw,
+                          hipStream_t st);
+
 }  // namespace nca
