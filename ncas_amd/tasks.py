@@ -64,6 +64,70 @@ class Boards:
                       np.repeat(self.given, k, 0), meta)
 
 
+# ---------------------------------------------------------------------------------- tasks
+class Task:
+    """What the rollout, the trainer and the metrics need to know about a board family
+    (reference src/nca/tasks/base.py:89-149): given cells show their input token in decoded
+    boards (`fill_given`), the scored cells are the mutable ones (`eval_mask`), "exact" is the
+    main metric, and there is no augmentation."""
+
+    name = "task"
+    main_metric = "exact"
+    fill_given = True
+
+    def eval_mask(self, boards: Boards) -> np.ndarray:
+        return ~boards.given
+
+    def augment(self, boards: Boards, rng: np.random.Generator) -> Boards:
+        return boards
+
+    def metrics(self, pred: np.ndarray, boards: Boards) -> dict[str, np.ndarray]:
+        """Per-board "exact" (every scored cell right) and "cell_acc" of predicted tokens
+        (N, H, W)."""
+        scored = self.eval_mask(boards)
+        right = (pred == boards.targets) & scored
+        n = scored.sum(axis=(1, 2))
+        hits = right.sum(axis=(1, 2))
+        return {"exact": hits == n, "cell_acc": hits / np.maximum(n, 1)}
+
+
+class MazeTask(Task):
+    """Mazes of `maze_boards` (open / wall / start / goal inputs, the BFS path as target)."""
+
+    name = "maze"
+
+    def __init__(self, extra_openings: float = 0.0, min_path_len: int | None = None):
+        self.extra_openings, self.min_path_len = extra_openings, min_path_len
+
+    def generate(self, n: int, size: int, seed: int) -> Boards:
+        return maze_boards(n, size, seed, self.extra_openings, self.min_path_len)
+
+
+class SudokuTask(Task):
+    """Sudoku boards of `sudoku_boards` (clues as inputs, the solved grid as target)."""
+
+    name = "sudoku"
+
+    def __init__(self, clues: tuple[int, int] = (17, 30)):
+        self.clues = tuple(clues)
+
+    def generate(self, n: int, size: int, seed: int) -> Boards:
+        if size != 9:
+            raise ValueError("sudoku boards are 9x9")
+        return sudoku_boards(n, seed, self.clues)
+
+
+def get_task(name: str, **kwargs) -> Task:
+    """"maze", "maze_hard" (10 % extra openings) or "sudoku"."""
+    if name == "maze":
+        return MazeTask(**kwargs)
+    if name == "maze_hard":
+        return MazeTask(**{"extra_openings": 0.10, **kwargs})
+    if name == "sudoku":
+        return SudokuTask(**kwargs)
+    raise ValueError(f"unknown task {name!r} (maze | maze_hard | sudoku)")
+
+
 # ---------------------------------------------------------------------------------- mazes
 def carve_perfect_maze(k: int, rng: np.random.Generator) -> np.ndarray:
     """(2k+1, 2k+1) uint8 grid of WALL / OPEN: a spanning tree of the k x k lattice grown by

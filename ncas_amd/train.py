@@ -273,6 +273,9 @@ class Engine:
             raise ValueError(f"unknown loss {self.loss_kind!r} (ce | mse | mse_mean)")
         if self.loss_kind == "ce" and model.cfg.head != "mlp":
             raise ValueError("the cross-entropy loss needs an mlp head")
+        if self.loss_kind != "ce" and model.cfg.head not in ("l2", "cosine"):
+            raise ValueError("the MSE losses compare the output slice with token embeddings: "
+                             "they need an embedding head (l2)")
         self.step = make_step(model)
         self.segment = None  # what the reference's EngineState reports: no checkpoint segments
         self.last_chunk: ChunkResult | None = None
