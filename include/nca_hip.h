@@ -43,6 +43,8 @@
  *                        perception backward (ops.py:79-94); checked against the reference step's
  *                        gradients by tests/test_engine_ops.py:251-294
  *   nca_step_backward_workspace_bytes <- nothing in the reference (autograd allocates)
+ *   nca_prune_select  <- niche_capped_pruning (src/nca/pruning.py:22-65) at the pruning steps of
+ *                        rollout() (src/nca/rollout.py:249-275)
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -146,6 +148,19 @@ int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, 
                    float *x_out, const nca_fire_desc *fire, int32_t n_steps, const float *noise,
                    float *conf_out, int32_t *fired_out, void *workspace, size_t workspace_bytes,
                    void *stream);
+
+/* Niche-capped diversity pruning of K trials per board (reference src/nca/pruning.py:22-65,
+ * used by rollout() at its pruning steps, src/nca/rollout.py:249-275): decoded (n_boards,
+ * k_trials, cells) int32 decoded boards, conf (n_boards, k_trials) board confidences, alive
+ * (n_boards, k_trials) {0,1}; writes the trials that stay alive to alive_out (may alias alive).
+ * A board with a > 1 alive trials keeps a / 2 of them: trials with identical decoded boards
+ * form a niche, each niche's members by confidence (highest first, ties to the lower trial) with
+ * at most n_cap kept, taken round-robin across the niches in a random order. The order is the
+ * build's own (Philox4x32-10 keyed on (seed; niche representative, event, board, 1)), where the
+ * reference draws numpy's rng.permutation. k_trials <= 1024. Deterministic. */
+int nca_prune_select(const int32_t *decoded, const float *conf, const uint8_t *alive,
+                     int32_t n_boards, int32_t k_trials, int32_t cells, int32_t n_cap,
+                     uint64_t seed, int64_t event, uint8_t *alive_out, void *stream);
 
 /* Bytes of the device scratch that nca_rollout_noalloc uses instead of a caller workspace. */
 #define NCA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)

@@ -39,6 +39,7 @@ EXPORTS = (
     "nca_step_backward_workspace_bytes",
     "nca_step_backward",
     "nca_rollout_noalloc",
+    "nca_prune_select",
 )
 
 
@@ -149,6 +150,7 @@ def load():
         ctypes.POINTER(CellDesc), vp, ctypes.POINTER(CellWeights), i64, i32, i32, vp, vp, vp, vp,
         ctypes.POINTER(CellGrads), vp, vp, ctypes.c_size_t, vp,
     ]
+    L.nca_prune_select.argtypes = [vp, vp, vp, i32, i32, i32, i32, ctypes.c_uint64, i64, vp, vp]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
     L.nca_set_kernel_path.argtypes = [ctypes.c_int]

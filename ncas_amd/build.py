@@ -31,6 +31,7 @@ SOURCES = {
     "nca_stream32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_tiled.hip": [],
     "nca_bptt.hip": [],
+    "nca_prune.hip": [],
 }
 
 

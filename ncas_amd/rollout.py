@@ -12,7 +12,9 @@ points run as one launch of the LDS-resident kernel (`inference.rollout_steps`).
 Everything a rollout reports is computed on the GPU (decode, board confidence, the per-board
 exact / cell-accuracy scores over `task.eval_mask`, fired-cell counts) and kept there until one
 copy to the host at the end of the call (the reference copies at every record step,
-rollout.py:277-288). Test-time noise and damage are not implemented and raise ValueError.
+rollout.py:277-288). Pruning (niche-capped halving of the K trials, reference rollout.py:
+249-275) selects on the GPU and compacts the surviving rows. Test-time noise and damage are not
+implemented and raise ValueError.
 
 `conf_at_k` / `pass_at_k` are the reference's selection metrics (rollout.py:317-350) computed on
 the GPU: the conf@K choice is the `nca_conf_select` wavefront reduction, and the metric of the
@@ -106,12 +108,18 @@ def _eval_mask(task, boards) -> np.ndarray:
 @torch.no_grad()
 def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None,
             progress: bool = False) -> RolloutResult:
+    """Run every board `rc.k` times (reference rollout.py:86-306). With `rc.pruning`
+    ({"m", "n_cap"}) the ensemble of each board is halved at m - 1 equidistant steps
+    (`pruning.prune_select`) and the pruned trajectories leave the batch (rows compacted on the
+    GPU); a pruned trajectory keeps its last state's decode, confidence and counts, also in the
+    traces of the later record steps. After a pruning step the surviving rows are renumbered
+    0, 1, ... in the pass for the Philox row counter."""
     if rc.noise is not None or rc.damage_at is not None:
         raise ValueError("test-time noise and damage are not implemented by the HIP rollout")
-    if rc.pruning:
-        raise ValueError("pruning is not implemented by the HIP rollout")
     if task_ids is not None or model.cfg.time_steps:
         raise ValueError("task / time embeddings are not implemented by the HIP rollout")
+    from .pruning import prune_select
+
     model.eval()
     device = model.device
     if device.type != "cuda":
@@ -128,52 +136,92 @@ def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None
     if record and (not steps or steps[-1] != rc.depth):
         steps.append(rc.depth)
     T = len(steps)
+    prune_steps, n_cap = set(), 3
+    if rc.pruning:
+        m = int(rc.pruning["m"])
+        n_cap = int(rc.pruning.get("n_cap", 3))
+        stride = rc.depth // m
+        prune_steps = {i * stride for i in range(1, m)}
+    bounds = sorted({rc.depth, *steps, *prune_steps})
     rows_total = N * K
     # every output lives on the device until the end of the call
     pred = torch.empty((rows_total, H, W), dtype=torch.int64, device=device)
     conf_out = torch.empty((rows_total,), dtype=torch.float32, device=device)
     upd_out = torch.empty((rows_total,), dtype=torch.float64, device=device)
+    alive_out = torch.ones((rows_total,), dtype=torch.bool, device=device)
     tr = {k: torch.zeros((rows_total, T), dtype=dt, device=device) for k, dt in
           (("exact", torch.bool), ("cell", torch.float32), ("conf", torch.float32),
            ("upd", torch.float64))} if record else None
     scored_all = _eval_mask(task, boards)
+    event = 0
     for start in range(0, N, per_pass):
         stop_b = min(N, start + per_pass)
         n = stop_b - start
         sub = boards.subset(np.arange(start, stop_b))
-        rows = slice(start * K, stop_b * K)
+        base = start * K
         inputs = _lib.upload(np.repeat(sub.inputs, K, 0), device)
         targets = _lib.upload(np.repeat(sub.targets, K, 0), device)
         given = _lib.upload(np.repeat(sub.given, K, 0), device)
         scored = _lib.upload(np.repeat(scored_all[start:stop_b], K, 0), device)
-        score = _Scorer(model, task, inputs, targets, given, scored)
         x, given4, clamp = model.init_state(inputs, given, None, gen)
         x = x.float().contiguous()
-        updates = torch.zeros(n * K, dtype=torch.float64, device=device)
-        t = 0
-        for t_rec, stop in enumerate(steps + ([] if record else [rc.depth])):
+        B = n * K
+        idx = torch.arange(base, base + B, device=device)  # flat (board, trial) row of each row
+        updates = torch.zeros(B, dtype=torch.float64, device=device)
+        t, t_rec = 0, 0
+
+        def store(rows, dec, cell, exact, conf, upd, t_from):
+            pred[rows] = dec
+            conf_out[rows] = conf
+            upd_out[rows] = upd
+            if record and t_from < T:
+                tr["exact"][rows, t_from:] = exact[:, None]
+                tr["cell"][rows, t_from:] = cell.float()[:, None]
+                tr["conf"][rows, t_from:] = conf[:, None]
+                tr["upd"][rows, t_from:] = upd[:, None]
+
+        for stop in bounds:
             x, _, fired = rollout_steps(
                 model, x, given4, clamp, stop - t, seed=seed, p_fire=rc.fire_rate,
                 p_low=rc.p_low, tau=rc.tau, given_confident=rc.given_confident,
-                row0=start * K, step0=t, precision=precision, out=x, want_conf=False,
+                row0=base, step0=t, precision=precision, out=x, want_conf=False,
                 want_fired=True,
             )
             updates += fired.double()
             t = stop
-            if record:
+            score = _Scorer(model, task, inputs, targets, given, scored)
+            if stop in prune_steps:
+                dec, cell, exact, conf = score(x)
+                local = idx - base  # row of the (board, trial) in the pass's full layout
+                dec_full = torch.zeros((B, H, W), dtype=torch.int64, device=device)
+                conf_full = torch.full((B,), -float("inf"), device=device)
+                alive_full = torch.zeros(B, dtype=torch.bool, device=device)
+                dec_full[local], conf_full[local], alive_full[local] = dec, conf, True
+                keep = prune_select(dec_full.view(n, K, H * W), conf_full.view(n, K),
+                                    alive_full.view(n, K), n_cap, seed, event).view(B)[local]
+                event += 1
+                drop = ~keep
+                store(idx[drop], dec[drop], cell[drop], exact[drop], conf[drop], updates[drop],
+                      t_rec)
+                alive_out[idx[drop]] = False
+                sel = keep.nonzero().squeeze(1)  # one host wait per pruning step
+                x, given4, clamp = x[sel].contiguous(), given4[sel], clamp[sel]
+                inputs, targets, given, scored = inputs[sel], targets[sel], given[sel], scored[sel]
+                updates, idx = updates[sel], idx[sel]
+                score = _Scorer(model, task, inputs, targets, given, scored)
+            if record and t_rec < T and stop == steps[t_rec]:
                 _, cell, exact, conf = score(x)
-                tr["exact"][rows, t_rec] = exact
-                tr["cell"][rows, t_rec] = cell.float()
-                tr["conf"][rows, t_rec] = conf
-                tr["upd"][rows, t_rec] = updates
-        dec, _, _, conf = score(x)
-        pred[rows] = dec
-        conf_out[rows] = conf
-        upd_out[rows] = updates
+                tr["exact"][idx, t_rec] = exact
+                tr["cell"][idx, t_rec] = cell.float()
+                tr["conf"][idx, t_rec] = conf
+                tr["upd"][idx, t_rec] = updates
+                t_rec += 1
+        dec, cell, exact, conf = _Scorer(model, task, inputs, targets, given, scored)(x)
+        store(idx, dec, cell, exact, conf, updates, T)
     host = lambda t: t.cpu().numpy()  # noqa: E731
     return RolloutResult(
-        host(pred).reshape(N, K, H, W), host(conf_out).reshape(N, K), np.ones((N, K), bool),
-        host(upd_out).reshape(N, K), np.array(steps),
+        host(pred).reshape(N, K, H, W), host(conf_out).reshape(N, K),
+        host(alive_out).reshape(N, K), host(upd_out).reshape(N, K), np.array(steps),
         *((host(tr[k]).reshape(N, K, T) for k in ("exact", "cell", "conf", "upd")) if record
           else (None, None, None, None)),
     )
