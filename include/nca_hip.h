@@ -162,6 +162,27 @@ int nca_prune_select(const int32_t *decoded, const float *conf, const uint8_t *a
                      int32_t n_boards, int32_t k_trials, int32_t cells, int32_t n_cap,
                      uint64_t seed, int64_t event, uint8_t *alive_out, void *stream);
 
+/* Host-side batched board generation (the inputs of the workloads), on `threads` host threads
+ * (0 = all). Every board draws from its own Philox4x32-10 stream keyed on `seed`, so the
+ * output does not depend on the thread count. Buffers are host memory.
+ *
+ * nca_maze_boards <- generate_perfect_maze / generate_hard_maze (src/nca/tasks/maze.py:317-445):
+ * n mazes of size x size: a spanning tree of the (size/2)^2 lattice by randomised depth-first
+ * search, a fraction extra_openings of the interior walls between lattice cells removed, a
+ * random start on an open cell and a random goal at BFS distance >= min_path_len - 1 (>= 1 when
+ * min_path_len <= 0; up to max_tries draws per board). Tokens OPEN 0, WALL 1, START 2, GOAL 3,
+ * PATH 4 (targets mark the BFS shortest path); inputs / targets (n, size, size) int64, given
+ * (n, size, size) {0,1} (every non-open input), path_len (n) cells on the path. */
+int nca_maze_boards(int64_t n, int32_t size, uint64_t seed, double extra_openings,
+                    int32_t min_path_len, int32_t max_tries, int64_t *inputs, int64_t *targets,
+                    uint8_t *given, int64_t *path_len, int32_t threads);
+
+/* nca_sudoku_boards <- random_solution (src/nca/tasks/sudoku.py:290-294) plus a clue subset:
+ * n solved grids (targets, values 1..9) with a uniformly random number of clues in
+ * [clues_lo, clues_hi] kept at uniformly random cells (inputs, 0 elsewhere; given = clue). */
+int nca_sudoku_boards(int64_t n, uint64_t seed, int32_t clues_lo, int32_t clues_hi,
+                      int64_t *inputs, int64_t *targets, uint8_t *given, int32_t threads);
+
 /* Bytes of the device scratch that nca_rollout_noalloc uses instead of a caller workspace. */
 #define NCA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
 

@@ -40,6 +40,8 @@ EXPORTS = (
     "nca_step_backward",
     "nca_rollout_noalloc",
     "nca_prune_select",
+    "nca_maze_boards",
+    "nca_sudoku_boards",
 )
 
 
@@ -151,6 +153,9 @@ def load():
         ctypes.POINTER(CellGrads), vp, vp, ctypes.c_size_t, vp,
     ]
     L.nca_prune_select.argtypes = [vp, vp, vp, i32, i32, i32, i32, ctypes.c_uint64, i64, vp, vp]
+    L.nca_maze_boards.argtypes = [i64, i32, ctypes.c_uint64, ctypes.c_double, i32, i32, vp, vp, vp,
+                                  vp, i32]
+    L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
     L.nca_set_kernel_path.argtypes = [ctypes.c_int]

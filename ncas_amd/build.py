@@ -32,6 +32,7 @@ SOURCES = {
     "nca_tiled.hip": [],
     "nca_bptt.hip": [],
     "nca_prune.hip": [],
+    "nca_boards.cpp": [],
 }
 
 

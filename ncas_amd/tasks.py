@@ -1,31 +1,41 @@
-"""Boards and seeded input generators for the NCA workloads (host numpy).
+"""Boards, tasks and batched seeded input generators for the NCA workloads.
 
-`Boards` keeps the reference's container (reference src/nca/tasks/base.py:27-86): `(N, H, W)`
-int64 `inputs` / `targets`, bool `given`, per-board `meta`.
+`Boards` is the reference's board container (reference src/nca/tasks/base.py:27-86): `(N, H, W)`
+int64 `inputs` / `targets`, bool `given`, per-board `meta` arrays. `Boards.save` / `Boards.load`
+keep a set on disk as an uncompressed-or-compressed `.npz` with the keys `inputs`, `targets`,
+`given` and the per-board meta arrays (the reference's cached datasets, maze.py:494-512), read
+back without unpickling.
 
-Generators (the reference's own are pure-Python loops, reference src/nca/tasks/maze.py:317-445,
-src/nca/tasks/sudoku.py:290-294):
+Generators (the reference's are per-board Python loops, maze.py:317-445, sudoku.py:290-294) run
+in the library's native code on all host threads, one counter-based random stream per board, so
+a board depends only on (seed, board index):
 
 * `maze_boards` - perfect mazes by randomised depth-first search (recursive backtracker) on a
   k x k lattice, drawn on a (2k+1) x (2k+1) grid (cropped to an even size like the reference's
-  hard mazes), optionally with a fraction of the removable interior walls knocked out; start
-  and goal on open cells (for hard mazes at BFS distance >= min_path_len - 1); targets mark the
-  BFS shortest path. Tokens: OPEN=0, WALL=1, START=2, GOAL=3, PATH=4; given = walls, start,
-  goal (the reference's `inputs != EMPTY`, maze.py:932).
+  hard mazes), optionally with a fraction of the interior walls between two lattice cells
+  knocked out; start and goal on open cells (for hard mazes at BFS distance >= min_path_len - 1);
+  targets mark the BFS shortest path. Tokens: OPEN=0, WALL=1, START=2, GOAL=3, PATH=4;
+  given = walls, start, goal (the reference's `inputs != EMPTY`, maze.py:932).
 * `sudoku_boards` - random valid solved grids (a valid base pattern under the validity-
-  preserving symmetry group: digit relabelling, row / column permutations within bands /
-  stacks, band / stack permutations, transposition) with a uniformly random number of clues
-  in [17, 30] kept at uniformly random cells. Uniqueness of the solution is not required.
+  preserving symmetries: digit relabelling, row / column permutations within bands / stacks,
+  band / stack permutations, transposition) with a uniformly random number of clues in
+  [17, 30] kept at uniformly random cells. Uniqueness of the solution is not required.
+
+`Task` objects (`get_task`) give the scored cells, the metrics and `load(split, root, n, size,
+seed)`, which reads a cached `.npz` or generates and caches the set.
 """
 
 from __future__ import annotations
 
+import ctypes
+import os
 from collections import deque
 from dataclasses import dataclass, field
 
 import numpy as np
 
-from .model import MAZE_GOAL, MAZE_OPEN, MAZE_PATH, MAZE_START, MAZE_WALL
+from . import _lib
+from .model import MAZE_OPEN, MAZE_WALL
 
 
 @dataclass
@@ -36,32 +46,48 @@ class Boards:
     meta: dict = field(default_factory=dict)
 
     def __post_init__(self) -> None:
-        assert self.inputs.shape == self.targets.shape == self.given.shape, "shape mismatch"
-        assert self.inputs.ndim == 3, "boards must be (N, H, W)"
-        self.inputs = self.inputs.astype(np.int64)
-        self.targets = self.targets.astype(np.int64)
-        self.given = self.given.astype(bool)
+        shapes = {np.shape(self.inputs), np.shape(self.targets), np.shape(self.given)}
+        if len(shapes) != 1 or len(next(iter(shapes))) != 3:
+            raise AssertionError(f"boards must share one (N, H, W) shape, got {shapes}")
+        self.inputs = np.asarray(self.inputs).astype(np.int64, copy=False)
+        self.targets = np.asarray(self.targets).astype(np.int64, copy=False)
+        self.given = np.asarray(self.given).astype(bool, copy=False)
 
     def __len__(self) -> int:
-        return self.inputs.shape[0]
+        return len(self.inputs)
 
     @property
     def shape(self) -> tuple[int, int]:
-        return self.inputs.shape[1], self.inputs.shape[2]
+        return tuple(self.inputs.shape[1:])
+
+    def _per_board(self, fn) -> dict:
+        """The meta dict with `fn` applied to the per-board arrays (first dimension N)."""
+        n = len(self)
+        return {k: fn(v) if isinstance(v, np.ndarray) and len(v) == n and v.ndim else v
+                for k, v in self.meta.items()}
 
     def subset(self, idx) -> Boards:
         idx = np.asarray(idx)
-        meta = {k: (v[idx] if isinstance(v, np.ndarray) and v.shape[:1] == (len(self),) else v)
-                for k, v in self.meta.items()}
-        return Boards(self.inputs[idx], self.targets[idx], self.given[idx], meta)
+        return Boards(self.inputs[idx], self.targets[idx], self.given[idx],
+                      self._per_board(lambda v: v[idx]))
 
     def repeat(self, k: int) -> Boards:
-        """Board n becomes rows n*k .. n*k+k-1 (reference tasks/base.py:66-77)."""
-        n = len(self)
-        meta = {key: (np.repeat(v, k, axis=0) if isinstance(v, np.ndarray) and v.shape[:1] == (n,)
-                      else v) for key, v in self.meta.items()}
-        return Boards(np.repeat(self.inputs, k, 0), np.repeat(self.targets, k, 0),
-                      np.repeat(self.given, k, 0), meta)
+        """Board n becomes rows n*k .. n*k + k - 1 (reference tasks/base.py:66-77)."""
+        rep = lambda v: np.repeat(v, k, axis=0)  # noqa: E731
+        return Boards(rep(self.inputs), rep(self.targets), rep(self.given), self._per_board(rep))
+
+    def save(self, path) -> None:
+        """Write the set as an .npz (inputs, targets, given and the per-board meta arrays)."""
+        arrays = {"inputs": self.inputs, "targets": self.targets, "given": self.given}
+        arrays.update({k: v for k, v in self._per_board(lambda v: v).items()
+                       if isinstance(v, np.ndarray)})
+        np.savez_compressed(path, **arrays)
+
+    @classmethod
+    def load(cls, path) -> Boards:
+        with np.load(path, allow_pickle=False) as z:
+            meta = {k: z[k] for k in z.files if k not in ("inputs", "targets", "given")}
+            return cls(z["inputs"], z["targets"], z["given"], meta)
 
 
 # ---------------------------------------------------------------------------------- tasks
@@ -81,6 +107,23 @@ class Task:
     def augment(self, boards: Boards, rng: np.random.Generator) -> Boards:
         return boards
 
+    def generate(self, n: int, size: int, seed: int) -> Boards:
+        raise NotImplementedError
+
+    def cache_path(self, root, split: str, n: int, size: int, seed: int) -> str:
+        return os.path.join(root, f"{self.name}_{split}_{size}_n{n}_seed{seed}.npz")
+
+    def load(self, split: str, root, n: int, size: int, seed: int = 0) -> Boards:
+        """The split's boards from `root`'s cached .npz, generated and cached on a miss
+        (reference tasks/maze.py:505-512)."""
+        path = self.cache_path(root, split, n, size, seed)
+        if os.path.exists(path):
+            return Boards.load(path)
+        boards = self.generate(n, size, seed)
+        os.makedirs(root, exist_ok=True)
+        boards.save(path)
+        return boards
+
     def metrics(self, pred: np.ndarray, boards: Boards) -> dict[str, np.ndarray]:
         """Per-board "exact" (every scored cell right) and "cell_acc" of predicted tokens
         (N, H, W)."""
@@ -98,6 +141,8 @@ class MazeTask(Task):
 
     def __init__(self, extra_openings: float = 0.0, min_path_len: int | None = None):
         self.extra_openings, self.min_path_len = extra_openings, min_path_len
+        if extra_openings:
+            self.name = f"maze_x{extra_openings:g}"
 
     def generate(self, n: int, size: int, seed: int) -> Boards:
         return maze_boards(n, size, seed, self.extra_openings, self.min_path_len)
@@ -129,34 +174,31 @@ def get_task(name: str, **kwargs) -> Task:
 
 
 # ---------------------------------------------------------------------------------- mazes
-def carve_perfect_maze(k: int, rng: np.random.Generator) -> np.ndarray:
-    """(2k+1, 2k+1) uint8 grid of WALL / OPEN: a spanning tree of the k x k lattice grown by
-    randomised depth-first search (a neighbour drawn uniformly at every extension)."""
-    grid = np.full((2 * k + 1, 2 * k + 1), MAZE_WALL, dtype=np.uint8)
-    grid[1::2, 1::2] = MAZE_OPEN
-    if k <= 1:
-        return grid
-    seen = np.zeros((k, k), dtype=bool)
-    start = (int(rng.integers(k)), int(rng.integers(k)))
-    seen[start] = True
-    stack = [start]
-    while stack:
-        i, j = stack[-1]
-        nbrs = [(i + di, j + dj) for di, dj in ((-1, 0), (1, 0), (0, -1), (0, 1))
-                if 0 <= i + di < k and 0 <= j + dj < k and not seen[i + di, j + dj]]
-        if not nbrs:
-            stack.pop()
-            continue
-        ni, nj = nbrs[int(rng.integers(len(nbrs)))]
-        seen[ni, nj] = True
-        grid[i + ni + 1, j + nj + 1] = MAZE_OPEN  # the wall between (i, j) and (ni, nj)
-        stack.append((ni, nj))
-    return grid
+def _threads(threads: int | None) -> int:
+    return 0 if threads is None else int(threads)
+
+
+def maze_boards(n: int, size: int, seed: int = 0, extra_openings: float = 0.0,
+                min_path_len: int | None = None, max_tries: int = 1000,
+                threads: int | None = None) -> Boards:
+    """`n` seeded mazes of `size` x `size` (native code, `threads` host threads, all by default).
+    meta["path_len"] is the number of cells on the shortest path, both ends included."""
+    inputs = np.empty((n, size, size), np.int64)
+    targets = np.empty((n, size, size), np.int64)
+    given = np.empty((n, size, size), np.uint8)
+    plen = np.empty(n, np.int64)
+    P = ctypes.c_void_p
+    _lib.check(_lib.load().nca_maze_boards(
+        int(n), int(size), int(seed) & 0xFFFFFFFFFFFFFFFF, float(extra_openings),
+        int(min_path_len or 0), int(max_tries), P(inputs.ctypes.data), P(targets.ctypes.data),
+        P(given.ctypes.data), P(plen.ctypes.data), _threads(threads)), "nca_maze_boards")
+    return Boards(inputs, targets, given.astype(bool), {"path_len": plen})
 
 
 def bfs(passable: np.ndarray, src: tuple[int, int]) -> tuple[np.ndarray, np.ndarray]:
-    """Distances (-1 = unreachable) and BFS parents (flat index, -1) from src, neighbour order
-    up, down, left, right."""
+    """Distances (-1 = unreachable) and BFS parents (flat index, -1) from src over passable
+    cells, neighbour order up, down, left, right (reference maze.py:251-295 scores paths the
+    same way)."""
     H, W = passable.shape
     dist = np.full((H, W), -1, dtype=np.int64)
     parent = np.full((H, W), -1, dtype=np.int64)
@@ -173,87 +215,30 @@ def bfs(passable: np.ndarray, src: tuple[int, int]) -> tuple[np.ndarray, np.ndar
     return dist, parent
 
 
-def maze_boards(n: int, size: int, seed: int = 0, extra_openings: float = 0.0,
-                min_path_len: int | None = None, max_tries: int = 1000) -> Boards:
-    rng = np.random.default_rng(seed)
-    k = size // 2
-    inputs = np.zeros((n, size, size), np.int64)
-    targets = np.zeros((n, size, size), np.int64)
-    plen = np.zeros(n, np.int64)
-    for b in range(n):
-        for _ in range(max_tries):
-            grid = carve_perfect_maze(k, rng)
-            if extra_openings > 0:
-                ii, jj = np.nonzero(grid == MAZE_WALL)
-                inner = (ii > 0) & (jj > 0) & (ii < 2 * k) & (jj < 2 * k) & ((ii + jj) % 2 == 1)
-                cand = np.stack([ii[inner], jj[inner]], 1)
-                m = int(round(extra_openings * len(cand)))
-                if m:
-                    pick = cand[rng.choice(len(cand), size=m, replace=False)]
-                    grid[pick[:, 0], pick[:, 1]] = MAZE_OPEN
-            grid = np.ascontiguousarray(grid[:size, :size])
-            passable = grid != MAZE_WALL
-            free = np.argwhere(passable)
-            src = tuple(int(v) for v in free[rng.integers(len(free))])
-            dist, parent = bfs(passable, src)
-            need = 1 if min_path_len is None else min_path_len - 1
-            far = np.argwhere(dist >= need)
-            if len(far) == 0:
-                continue
-            dst = tuple(int(v) for v in far[rng.integers(len(far))])
-            tgt = grid.astype(np.int64)
-            cur = dst[0] * size + dst[1]
-            length = 1
-            while parent.flat[cur] >= 0:
-                cur = int(parent.flat[cur])
-                tgt.flat[cur] = MAZE_PATH
-                length += 1
-            inp = grid.astype(np.int64)
-            inp[src] = MAZE_START
-            inp[dst] = MAZE_GOAL
-            tgt[src] = MAZE_START
-            tgt[dst] = MAZE_GOAL
-            inputs[b], targets[b], plen[b] = inp, tgt, length
-            break
-        else:
-            raise RuntimeError("could not generate a maze satisfying min_path_len")
-    return Boards(inputs, targets, inputs != MAZE_OPEN, {"path_len": plen})
-
-
 # ---------------------------------------------------------------------------------- sudoku
-def random_solution(rng: np.random.Generator) -> np.ndarray:
-    """A random valid solved 9x9 grid (values 1..9)."""
-    r = np.arange(9)
-    base = (3 * (r[:, None] % 3) + r[:, None] // 3 + r[None, :]) % 9  # valid Latin-box pattern
-    rows = np.concatenate([3 * b + rng.permutation(3) for b in rng.permutation(3)])
-    cols = np.concatenate([3 * s + rng.permutation(3) for s in rng.permutation(3)])
-    g = base[rows][:, cols]
-    if rng.integers(2):
-        g = g.T
-    return rng.permutation(9)[g] + 1
-
-
 def is_valid_solution(grid: np.ndarray) -> bool:
+    """A solved 9x9 grid: every row, column and 3x3 box holds 1..9 once (reference
+    sudoku.py:151)."""
     g = np.asarray(grid, dtype=np.int64).reshape(9, 9)
     if g.min() < 1 or g.max() > 9:
         return False
-    full = set(range(1, 10))
-    for k in range(9):
-        box = g[3 * (k // 3): 3 * (k // 3) + 3, 3 * (k % 3): 3 * (k % 3) + 3]
-        if set(g[k].tolist()) != full or set(g[:, k].tolist()) != full or set(box.ravel().tolist()) != full:
-            return False
-    return True
+    boxes = g.reshape(3, 3, 3, 3).transpose(0, 2, 1, 3).reshape(9, 9)
+    digits = np.arange(1, 10)
+    return all(np.array_equal(np.sort(u, axis=1), np.tile(digits, (9, 1))) for u in (g, g.T, boxes))
 
 
-def sudoku_boards(n: int, seed: int = 0, clues: tuple[int, int] = (17, 30)) -> Boards:
-    rng = np.random.default_rng(seed)
-    sol = np.zeros((n, 9, 9), np.int64)
-    inp = np.zeros((n, 9, 9), np.int64)
-    for b in range(n):
-        s = random_solution(rng)
-        m = int(rng.integers(clues[0], clues[1] + 1))
-        keep = rng.choice(81, size=m, replace=False)
-        flat = np.zeros(81, np.int64)
-        flat[keep] = s.ravel()[keep]
-        sol[b], inp[b] = s, flat.reshape(9, 9)
-    return Boards(inp, sol, inp != 0, {"n_clues": (inp != 0).sum((1, 2))})
+def sudoku_boards(n: int, seed: int = 0, clues: tuple[int, int] = (17, 30),
+                  threads: int | None = None) -> Boards:
+    """`n` seeded Sudoku boards (native code): targets are valid solved grids, inputs keep a
+    uniformly random number of clues in `clues` (inclusive) at uniformly random cells, 0 elsewhere;
+    meta["n_clues"] is that number."""
+    inputs = np.empty((n, 9, 9), np.int64)
+    targets = np.empty((n, 9, 9), np.int64)
+    given = np.empty((n, 9, 9), np.uint8)
+    P = ctypes.c_void_p
+    _lib.check(_lib.load().nca_sudoku_boards(
+        int(n), int(seed) & 0xFFFFFFFFFFFFFFFF, int(clues[0]), int(clues[1]),
+        P(inputs.ctypes.data), P(targets.ctypes.data), P(given.ctypes.data), _threads(threads)),
+        "nca_sudoku_boards")
+    g = given.astype(bool)
+    return Boards(inputs, targets, g, {"n_clues": g.sum(axis=(1, 2))})

@@ -38,6 +38,28 @@ def _case(padding="wall", size=6, rows=2, steps=3, seed=0):
     return cell, x, g4, cl, masks, targets, weights
 
 
+def _kink_margin(cell, x, g4, cl, masks, padding):
+    """Smallest |fc1 pre-activation| over the chunk's steps (fp64)."""
+    xx, worst = x.double(), float("inf")
+    for t in range(masks.shape[0]):
+        B, C, H, W = xx.shape
+        z = O.perceive(O.pad(xx, padding, cell.pad_vec.double()), cell.kernels.double(), H, W)
+        a = z.permute(0, 2, 3, 1).reshape(-1, z.shape[1]) @ cell.w1.double().T + cell.b1.double()
+        worst = min(worst, a.abs().min().item())
+        xx = O.step(cell, xx, g4, cl, masks[t], "fp64")
+    return worst
+
+
+def _smooth_case(padding, size=5, margin=4e-5):
+    """The first seed whose fc1 pre-activations all stay `margin` away from the ReLU's kink:
+    finite differences of step 1e-6 are only valid away from it."""
+    for seed in range(20):
+        case = _case(padding, size=size, seed=seed)
+        if _kink_margin(*case[:5], padding) >= margin:
+            return case
+    raise AssertionError("no seed keeps the pre-activations away from the kink")
+
+
 def _loss_fn(cell, x, g4, cl, masks, targets, weights, name, precision="fp32", ste=True, lm=None):
     def f(t):
         c = O.OracleCell(**{**cell.__dict__, name: t}) if name != "x0" else cell
@@ -48,7 +70,7 @@ def _loss_fn(cell, x, g4, cl, masks, targets, weights, name, precision="fp32", s
 
 @pytest.mark.parametrize("padding", ["wall", "zero", "wrap"])
 def test_gradcheck_small_parameters_and_state(padding):
-    cell, x, g4, cl, masks, targets, weights = _case(padding, size=5)
+    cell, x, g4, cl, masks, targets, weights = _smooth_case(padding, size=5)
     for name in ("kernels", "b2", "head_w", "head_b", "x0"):
         base = x if name == "x0" else getattr(cell, name)
         t = base.detach().to(torch.float64).clone().requires_grad_(True)

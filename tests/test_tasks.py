@@ -1,5 +1,7 @@
-"""Input generators (host numpy): invariants of the seeded mazes and Sudoku grids (reference
-src/nca/tasks/maze.py:251-309, 317-445 and src/nca/tasks/sudoku.py:151, 290-294)."""
+"""Input generators (the library's batched host code, no GPU needed): invariants of the seeded
+mazes and Sudoku grids (reference src/nca/tasks/maze.py:251-309, 317-445 and
+src/nca/tasks/sudoku.py:151, 290-294), independence from the thread count, and the on-disk
+Boards format (maze.py:494-512)."""
 
 from __future__ import annotations
 
@@ -84,3 +86,41 @@ def test_boards_repeat_is_board_major():
     assert np.array_equal(s.targets, b.targets[[2, 0]])
     with pytest.raises(AssertionError):
         Boards(b.inputs, b.targets[:2], b.given)
+
+
+def test_generators_do_not_depend_on_the_thread_count():
+    a = maze_boards(24, 21, seed=7, extra_openings=0.1, threads=1)
+    b = maze_boards(24, 21, seed=7, extra_openings=0.1, threads=5)
+    assert np.array_equal(a.inputs, b.inputs) and np.array_equal(a.targets, b.targets)
+    assert np.array_equal(a.meta["path_len"], b.meta["path_len"])
+    s1, s2 = sudoku_boards(40, seed=3, threads=1), sudoku_boards(40, seed=3, threads=8)
+    assert np.array_equal(s1.inputs, s2.inputs) and np.array_equal(s1.targets, s2.targets)
+    # a board depends only on (seed, index): the first boards of a larger set are the same
+    assert np.array_equal(maze_boards(5, 21, seed=7, extra_openings=0.1).inputs, a.inputs[:5])
+
+
+def test_large_batches_of_hard_mazes():
+    b = maze_boards(1000, 30, seed=0, extra_openings=0.10)
+    assert b.inputs.shape == (1000, 30, 30)
+    assert (b.meta["path_len"] >= 2).all() and (b.inputs == MAZE_START).sum() == 1000
+    big = maze_boards(2, 201, seed=1)
+    passable = big.inputs[0] != MAZE_WALL
+    assert _open_edges(passable) == passable.sum() - 1
+
+
+def test_boards_save_load_and_task_cache(tmp_path):
+    from ncas_amd.tasks import get_task
+
+    b = maze_boards(7, 13, seed=2)
+    b.save(tmp_path / "m.npz")
+    c = Boards.load(tmp_path / "m.npz")
+    assert np.array_equal(c.inputs, b.inputs) and np.array_equal(c.given, b.given)
+    assert np.array_equal(c.meta["path_len"], b.meta["path_len"])
+    task = get_task("maze_hard")
+    first = task.load("train", tmp_path, n=6, size=30, seed=4)
+    path = task.cache_path(tmp_path, "train", 6, 30, 4)
+    assert path.endswith(".npz") and (tmp_path / path.split("/")[-1]).exists()
+    again = task.load("train", tmp_path, n=6, size=30, seed=4)
+    assert np.array_equal(first.targets, again.targets)
+    s = get_task("sudoku").load("val", tmp_path, n=5, size=9, seed=1)
+    assert np.array_equal(s.meta["n_clues"], s.given.sum(axis=(1, 2)))
