@@ -7,8 +7,11 @@ p_fire=0.5, D=256 steps in one launch of the LDS-resident kernel, then the conf@
 the 128 trials. Weights N(0, 0.02) (synthetic), states zero-initialised and clamped; inputs
 resident in HBM before the timed region.
 
-`--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16, D=13,000, p_fire=0.5)
-times the per-step path (one launch of the wave-per-tile kernel per step) the same way, and
+`--workload maze13` (8 DFS mazes 13x13, K=1, D=300, fp32: the smoke maze configuration) times the
+resident kernel. `--workload maze201` (16 DFS mazes 201x201, C=16, MLP 64 -> 128 -> 16,
+D=13,000, p_fire=0.5) times the per-step path (one launch of the wave-per-tile kernel per step)
+the same way, and beside it the temporally blocked regime (2 steps per launch on LDS-resident
+windows, `--window-steps`), and
 `--workload hardmaze30` (1,000 hard mazes
 30x30 with 10 % extra openings, K=64 -> 64,000 rows, C=32, MLP 128 -> 256 -> 32, D=200, p_fire=0.8
 gated to 0.2 above confidence 0.9) the streamed C=32 kernel (one board per workgroup, the whole
@@ -48,6 +51,11 @@ PEAK_TFLOPS = {"bf16": 2500.0, "fp32": 157.3}
 PEAK_HBM_GBS = 8000.0
 
 WORKLOADS = {
+    "maze13": dict(
+        preset="maze_c16", task="maze", boards=8, k=1, depth=300, grid=13, p_fire=0.5,
+        precision="fp32",
+        desc="smoke maze 13x13: 8 DFS mazes, K=1, D=300 steps, C=16, 4 kernels, MLP 64-128-16, "
+             "p_fire=0.5, fp32, one launch of the resident kernel"),
     "sudoku9": dict(
         preset="sudoku_c64", task="sudoku", boards=256, k=128, depth=256, grid=9, p_fire=0.5,
         desc="sudoku 9x9: 256 boards x K=128 trials = 32768 rows, D=256 steps, C=64, 4 kernels, "
@@ -169,10 +177,13 @@ def calibration_copy(mib: int) -> None:
     del a, b
 
 
-def run_gpu(wl, precision, steps, warmup):
+def run_gpu(wl, precision, steps, warmup, window_steps=0):
+    from ncas_amd import _lib
     from ncas_amd.inference import rollout_steps
     from ncas_amd.readout import conf_select
 
+    if _lib.load().nca_set_window_steps(window_steps) != 0:
+        raise ValueError(f"window steps {window_steps}")
     dev = torch.device("cuda:0")
     model, x, given4, clamp = make_workload(wl, dev)
     model.packed(precision, dev)
@@ -294,7 +305,13 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--workload", choices=list(WORKLOADS), default="sudoku9")
-    ap.add_argument("--precision", choices=["bf16", "fp32"], default="bf16")
+    ap.add_argument("--precision", choices=["bf16", "fp32"], default=None,
+                    help="compute type (default: the workload's, bf16 unless it names fp32)")
+    ap.add_argument("--window-steps", type=int, default=0,
+                    help="steps per launch of the temporally blocked kernel (maze201; 0: one "
+                         "step per launch)")
+    ap.add_argument("--no-regimes", action="store_true",
+                    help="maze201: skip the secondary timing of the other regime")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp32", action="store_true", help="skip the secondary fp32 run")
     ap.add_argument("--depth", type=int, default=0,
@@ -308,6 +325,8 @@ def main():
         sys.exit(2)
 
     wl = dict(WORKLOADS[args.workload])
+    if args.precision is None:
+        args.precision = wl.get("precision", "bf16")
     if args.depth:  # a shorter rollout of the same workload, for counter runs
         wl["depth"] = args.depth
     if args.calib_copy_mib:
@@ -334,7 +353,7 @@ def main():
         }
         print(json.dumps(line), flush=True)
         return
-    res = run_gpu(wl, args.precision, args.steps, args.warmup)
+    res = run_gpu(wl, args.precision, args.steps, args.warmup, args.window_steps)
     print(f"# gpu {args.workload} {args.precision}: {res['value']:.4g} cell-updates/s, "
           f"kernel ms {res['kernel_ms']}", file=sys.stderr, flush=True)
     other = None
@@ -343,6 +362,17 @@ def main():
         other = {"dtype": "fp32", "value": o["value"], "ms_per_step": o["ms_per_step"],
                  "roofline_frac": o["frac"], "achieved_tflops": o["achieved_tflops"]}
         print(f"# gpu fp32: {o['value']:.4g} cell-updates/s", file=sys.stderr, flush=True)
+    regimes = None
+    if args.workload == "maze201" and not args.no_regimes:
+        # the other C2 regime: per-step launches vs the temporally blocked kernel
+        alt = 2 if args.window_steps == 0 else 0
+        r2 = run_gpu(wl, args.precision, 1, 0, alt)
+        name = lambda t: "per_step" if t == 0 else f"temporal_T{t}"  # noqa: E731
+        regimes = {name(args.window_steps): {"kernel_ms_per_step": float(np.mean(res["kernel_ms"])) / wl["depth"],
+                                              "cell_updates_per_s": res["kernel_rate"]},
+                   name(alt): {"kernel_ms_per_step": float(np.mean(r2["kernel_ms"])) / wl["depth"],
+                               "cell_updates_per_s": r2["kernel_rate"]}}
+        print(f"# regimes {regimes}", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(wl)
     H = W = wl["grid"]
     line = {
@@ -372,8 +402,14 @@ def main():
     }
     if args.workload != "sudoku9":
         line["metric"] = f"cell-updates/sec on 1 MI355X ({H}x{W} {args.workload})"
+    if regimes:
+        line["regimes"] = regimes
     if cpu:
+        # the CPU baseline is the fp32 oracle: the like-for-like ratio is the fp32 GPU run's
         line["speedup_vs_cpu"] = res["value"] / cpu["value"]
+        fp32_value = res["value"] if args.precision == "fp32" else (other or {}).get("value")
+        if fp32_value:
+            line["speedup_vs_cpu_fp32"] = fp32_value / cpu["value"]
     print(json.dumps(line), flush=True)
 
 
