@@ -46,18 +46,25 @@
 // writes the caller's state into P and the clamped state into M; the update keeps those
 // channels of given cells at their M value, which is bitwise the reference's clamp at every step.
 //
-// LDS layouts are chosen for gfx950's banks so that the hot accesses are conflict-free:
+// LDS layouts (gfx950: 64 banks of 4 bytes; measured with 8 waves streaming one access pattern,
+// ds_read_b128 takes 4 cycles per instruction when conflict-free, ds_write_b128 13, ds_write_b64 6):
 //   * P: cell stride 144 B, padded row pitch RP = 144 (W + 2) + 224 and board pitch PB = 144 HW
-//     mod 256, so the byte address of stream cell p is 144 p + const mod 256 within a step;
-//   * M: 288 B per cell (64 fp32 + 32 B);
+//     mod 256, so the byte address of stream cell p is 144 p + const mod 256 within a step: the 16
+//     cells of a tile land on 16 distinct 16-byte bank groups. The stencil's tap loads still take
+//     8 cycles, not 4: the four 16-lane groups of one load read octets 16 B apart in the same
+//     cells, which gfx950 serves in two passes (the same loads with the groups 4 KB apart take
+//     one; removing the extra pass would save about 1 % of the launch);
+//   * M: 288 B per cell (64 fp32 + 32 B) (the update's b128 accesses: 4.4 cycles per read, 16
+//     per write);
 //   * Z: 576 B per tile row, features in quad-major order (16 iq + 4 head + ch), chunk c of row
-//     r stored at chunk c ^ (2 ((r >> 2) & 3));
+//     r stored at chunk c ^ (2 ((r >> 2) & 3)) (conflict-free reads and writes);
 //   * H: 544 B per tile row, 16-byte chunk c of row n stored at chunk c ^ ((n >> 2) & 1); the 16
 //     hidden values of fc1 lane (n, g) of hidden wave w are contiguous at physical position
 //     64 w + 16 g + 4 mt + v (logical hidden unit 64 w + 16 mt + 4 g + v); the fc2 fragments are
-//     packed in that order.
-// (Strides and swizzles measured conflict-free for these access patterns on gfx950; M at 272 B
-// and H at 528 B cost about a quarter more per read.)
+//     packed in that order (conflict-free reads and writes).
+// Per 16-cell interval the LDS serves about 70 KB of reads and 22 KB of writes, about 670 cycles of
+// its time, beside 768 MFMA cycles on each of SIMDs 2-3; the hidden waves' own Z loads and H stores
+// are on the interval's critical path (without them the launch would take about a fifth less).
 #pragma once
 
 #include <type_traits>
@@ -361,20 +368,16 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                 for (int e = 0; e < 8; ++e) zqb[q][k][e] = (__bf16)0.0f;
         // fcb: fc1 of tile i-2 (32 MFMAs from registers, m-tile by m-tile) and its epilogue ->
         // H[i & 1], each half stored as soon as its two m-tiles are done; fca: the Z operands of
-        // tile i-1 into zqb[i & 1], requested after the first m-tile, once the channel waves' loads
-        // that open the interval are served (fc1 of tile i-2 reads zqb[(i-1) & 1])
+        // tile i-1 into zqb[i & 1] (fc1 of tile i-2 reads zqb[(i-1) & 1]). The eight Z loads are
+        // spread over m-tiles 1 and 2, one after every second MFMA, rather than issued as a burst:
+        // the LDS is then still serving the channel waves' loads that open the interval, and a
+        // load the wave cannot issue holds back its next MFMA (about 1 % of the launch).
         auto hinterval = [&](auto fca_c, auto fcb_c, auto par_c) __attribute__((always_inline)) {
             constexpr bool FCA = decltype(fca_c)::value, FCB = decltype(fcb_c)::value;
             constexpr unsigned PAR = decltype(par_c)::value;
-            auto loadz = [&]() __attribute__((always_inline)) {
-                if (FCA) {
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int kt = 0; kt < S::KT1; ++kt)
-                        zqb[PAR][kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
-                                                                   64u * kt);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+            auto loadz1 = [&](int kt) __attribute__((always_inline)) {
+                zqb[PAR][kt] = *reinterpret_cast<const bf16x8 *>(smem + ((kt & 1) ? kZo : kZe) + (PAR ^ 1u) * S::ZBUF +
+                                                               64u * kt);
             };
             if (FCB) {
                 f32x4 acc[S::MT1];
@@ -382,8 +385,14 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                 for (int mt = 0; mt < S::MT1; ++mt) {
                     acc[mt] = b1v[mt];
 #pragma unroll
-                    for (int kt = 0; kt < S::KT1; ++kt)
+                    for (int kt = 0; kt < S::KT1; ++kt) {
                         acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][kt], zqb[PAR ^ 1u][kt], acc[mt], 0, 0, 0);
+                        if (FCA && (mt == 1 || mt == 2) && (kt & 1)) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            loadz1((mt - 1) * 4 + (kt >> 1));
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
                     if (mt & 1) {
                         uint4 hv;
                         hv.x = relu_bf16x2(cvt_pk_bf16(acc[mt - 1][0], acc[mt - 1][1]));
@@ -392,10 +401,10 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                         hv.w = relu_bf16x2(cvt_pk_bf16(acc[mt][2], acc[mt][3]));
                         lds_st128(smem, (mt == 1 ? kHw0 : kHw1) + PAR * S::HBUF, hv);
                     }
-                    if (mt == 0) loadz();
                 }
-            } else {
-                loadz();
+            } else if (FCA) {
+#pragma unroll
+                for (int kt = 0; kt < S::KT1; ++kt) loadz1(kt);
             }
         };
         int i = 0;
