@@ -240,7 +240,7 @@ def run_bptt(wl, precision, steps, warmup):
     boards = make_boards(wl, 0)
     pool = ReplayPool(model, boards, wl["boards"], np.random.default_rng(0),
                       torch.Generator(device=dev).manual_seed(0))
-    eng = Engine(model, rollout=wl["depth"], chunk=wl["depth"], amp=precision == "bf16")
+    eng = Engine(model, None, {"rollout": wl["depth"], "chunk": wl["depth"], "amp": precision == "bf16"}, dev)
     # The reference's hard-maze training settings (configs/maze_hard.yaml: lr 5e-4, weight decay
     # 1e-4, clip 1.0, linear warm-up over the first quarter of 10,000 steps).
     opt = torch.optim.AdamW(model.parameters(), lr=5e-4, weight_decay=1e-4)

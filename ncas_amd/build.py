@@ -30,7 +30,8 @@ SOURCES = {
     "nca_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_stream32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_tiled.hip": [],
-    "nca_bptt.hip": [],
+    # mlp_back32 keeps its weight fragments in AGPRs and its accumulators in VGPRs
+    "nca_bptt.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_prune.hip": [],
     "nca_boards.cpp": [],
 }

@@ -14,7 +14,7 @@
 //   stencil_z  z = perception of the saved state (feature-major, F x cells)
 //   MLP        h = relu(W1 z + b1); g_a = (W2^T g_dx) * [h > 0]; g_z = W1^T g_a: bf16 cells with
 //              32 channels and 256 hidden units in one fused kernel (mlp_back32, which also sums
-//              dW1, dW2 and db1), other cells on fp32 MFMA GEMMs
+//              dW1, dW2 and db1, and stores g_z as bf16), other cells on fp32 MFMA GEMMs
 //   stencil_back  g_x = g_u + the transposed stencil of g_z (padding-aware: wall / zero halos
 //              take no gradient, wrap halos give it to the wrapped cell), the next step's
 //              gradient, and partial sums of the kernel-weight gradient
@@ -22,9 +22,12 @@
 //
 // Every partial sum belongs to one of 256 fixed cell ranges (slots); each step adds its sums
 // into the slots, and one kernel adds the slots up in slot order after the last step, so the
-// gradients are deterministic (the same bits on every run). Gradients are the exact fp32
-// gradients of the forward as computed: for bf16 cells the rounding points are straight-through
-// (derivative 1), and the backward uses the forward's bf16-rounded weights and inputs.
+// gradients are deterministic (the same bits on every run). fp32 cells: the exact fp32
+// gradients of the forward as computed. bf16 cells: the rounding points are straight-through
+// (derivative 1), the backward uses the forward's bf16-rounded weights and inputs, and the
+// gradients of dx, of fc1's output and of z are rounded to bf16 where the reference's bf16
+// backward rounds them (they are gradients of bf16 tensors; src/nca/engine/triton_mlp.py:46-78),
+// which makes every MLP product of the backward a product of bf16 values.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -45,6 +48,7 @@ constexpr int kPlaneMax = 2048;  // cells of a board whose planes the LDS stenci
 
 struct Dims {
     int C, F, HD, c_in, in_off, c_out, out_off, n_out, padding, bf16;
+    int gz16;  // g_z is stored as bf16 (by the fused MLP backward), else fp32
     int H, W, HW;
     int64_t rows, M;  // M = rows * HW cells
 };
@@ -76,9 +80,16 @@ ParamLayout param_layout(const Dims &d) {
     return L;
 }
 
+// The fused MLP backward (mlp_back32) takes bf16 cells of 32 channels, 128 features and 256 hidden
+// units; it addresses z and g_z with 32-bit byte offsets.
+bool fused_mlp(const Dims &d) { return d.bf16 && d.C == 32 && d.F == 128 && d.HD == 256 && d.M * d.F * 4 < ((int64_t)1 << 32); }
+// Boards small enough to stage (row, channel) planes in LDS.
+bool planes_fit(const Dims &d) { return d.HW <= kPlaneMax && d.rows * d.C <= 0x7fffffff; }
+
 // Workspace (floats, 64-float aligned pieces). part holds kSplit slots of P partial sums
 // each (slot s: the cells of range s), added to by every step of the chunk and reduced once at
-// the end; lossacc holds the loss's kSplit slots.
+// the end; lossacc holds the loss's kSplit slots. The GEMM path's h and g_a (Hb, Ga) are not
+// needed by the fused kernel.
 struct WsLayout {
     int64_t Z, Hb, Ga, Gz, Gdx, Gu, Gx0, Gx1, part, acc, lossacc, dk, denom, img, total;
 };
@@ -86,15 +97,16 @@ struct WsLayout {
 WsLayout ws_layout(const Dims &d, int n) {
     (void)n;
     const ParamLayout P = param_layout(d);
+    const bool fused = fused_mlp(d);
     auto al = [](int64_t v) { return (v + 63) & ~(int64_t)63; };
     WsLayout L;
     int64_t o = 0;
     L.Z = o;
     o = al(o + (int64_t)d.F * d.M);
     L.Hb = o;
-    o = al(o + (int64_t)d.HD * d.M);
+    o = al(o + (fused ? 0 : (int64_t)d.HD * d.M));
     L.Ga = o;
-    o = al(o + (int64_t)d.HD * d.M);
+    o = al(o + (fused ? 0 : (int64_t)d.HD * d.M));
     L.Gz = o;
     o = al(o + (int64_t)d.F * d.M);
     L.Gdx = o;
@@ -132,6 +144,11 @@ __device__ __forceinline__ int neighbour(int i, int j, int dy, int dx, int H, in
     a = a < 0 ? H - 1 : (a >= H ? 0 : a);
     b = b < 0 ? W - 1 : (b >= W ? 0 : b);
     return (in || wrap) ? a * W + b : -1;
+}
+
+// Element i of g_z: fp32, or bf16 where the fused MLP backward wrote it (gz16).
+__device__ __forceinline__ float gz_at(const float *Gz, int gz16, int64_t i) {
+    return gz16 ? __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(Gz)[i] << 16) : Gz[i];
 }
 
 // Block-wide sum of one float per thread in a fixed tree order (deterministic).
@@ -338,7 +355,9 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             }
             if (gv && c >= d.in_off && c < d.in_off + d.c_in) g = 0.0f;
             a.Gu[cb + (int64_t)c * d.HW] = g;
-            const float gd = g * f;
+            // bf16 cells: dx is a bf16 tensor, so its gradient is bf16 (the reference's bf16
+            // backward; triton_mlp.py:46-78 receives it as bf16)
+            const float gd = d.bf16 ? nca::round_bf16(g * f) : g * f;
             a.Gdx[(int64_t)c * d.M + m] = gd;
             db2[j] = __fadd_rn(db2[j], gd);
         }
@@ -428,8 +447,18 @@ __device__ __forceinline__ float tap_value(const float *xr, const Dims &d, int i
     return d.bf16 ? nca::round_bf16(v) : v;
 }
 
+// z element i: fp32, or bf16 for the fused MLP backward (Z16)
+template <bool Z16>
+__device__ __forceinline__ void z_store(float *Z, int64_t i, float v) {
+    if (Z16)
+        reinterpret_cast<__bf16 *>(Z)[i] = (__bf16)v;  // v is a bf16 value
+    else
+        Z[i] = v;
+}
+
 // z (F x M, feature-major) of the state x (rows, C, H, W): thread (row, channel, cell) with
 // channel and cell from blockIdx.x, rows strided over blockIdx.y.
+template <bool Z16>
 __global__ void __launch_bounds__(kThreads) stencil_z_kernel(Dims d, const float *__restrict__ x,
                                                              const float *__restrict__ kern,
                                                              const float *__restrict__ padv, float *__restrict__ Z) {
@@ -448,7 +477,7 @@ __global__ void __launch_bounds__(kThreads) stencil_z_kernel(Dims d, const float
             float acc = 0.0f;
 #pragma unroll
             for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
-            Z[(int64_t)(k * d.C + c) * d.M + m] = d.bf16 ? nca::round_bf16(acc) : acc;
+            z_store<Z16>(Z, (int64_t)(k * d.C + c) * d.M + m, d.bf16 ? nca::round_bf16(acc) : acc);
         }
     }
 }
@@ -477,7 +506,7 @@ __global__ void __launch_bounds__(kBackThreads) stencil_back_kernel(
         for (; e < e1; e += kBackThreads) {
             const int row = pl / d.C, c = pl - row * d.C, i = q / d.W, j = q - i * d.W;
             const float *xr = x + (int64_t)pl * d.HW;
-            const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * d.HW;
+            const int64_t gzo = (int64_t)c * d.M + (int64_t)row * d.HW;
             const float hv = d.padding == 1 ? padv[c] : 0.0f;
             float xv[9];
 #pragma unroll
@@ -490,14 +519,14 @@ __global__ void __launch_bounds__(kBackThreads) stencil_back_kernel(
                 const int qc = qs < 0 ? 0 : qs;
                 float gv[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) gv[k] = gz[k * ks + qc];
+                for (int k = 0; k < 4; ++k) gv[k] = gz_at(Gz, d.gz16, gzo + k * ks + qc);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) g = qs >= 0 ? __builtin_fmaf(kern[k * 9 + t], gv[k], g) : g;
             }
             gx[e] = g;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float gzv = gz[k * ks + q];
+                const float gzv = gz_at(Gz, d.gz16, gzo + k * ks + q);
 #pragma unroll
                 for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gzv, xv[t], acc[k * 9 + t]);
             }
@@ -527,8 +556,27 @@ __device__ __forceinline__ void plane_taps(const float *xs, const Dims &d, int i
     }
 }
 
+// The 4 features of channel c at cell q (row `row`) from the staged plane xs: z[k] = the sum of
+// kernel k's taps in tap order (the forward's order), bf16 for bf16 cells.
+template <bool Z16>
+__device__ __forceinline__ void plane_z(const float *xs, const Dims &d, const float *kern, float hv, int64_t row, int c,
+                                        int q, float *Z) {
+    const int i = q / d.W, j = q - i * d.W;
+    float xv[9];
+    plane_taps(xs, d, i, j, hv, xv);
+    const int64_t m = row * d.HW + q;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
+        z_store<Z16>(Z, (int64_t)(k * d.C + c) * d.M + m, d.bf16 ? nca::round_bf16(acc) : acc);
+    }
+}
+
 // stencil_z for boards of at most kPlaneMax cells: workgroup p stages plane p = (row, channel)
 // of x in LDS and writes that channel's 4 features of the row's cells.
+template <bool Z16>
 __global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float *__restrict__ x,
                                                             const float *__restrict__ kern,
                                                             const float *__restrict__ padv, float *__restrict__ Z) {
@@ -551,19 +599,7 @@ __global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float 
     }
     __syncthreads();
     const float hv = d.padding == 1 ? padv[c] : 0.0f;
-    for (int q = threadIdx.x; q < d.HW; q += kThreads) {
-        const int i = q / d.W, j = q - i * d.W;
-        float xv[9];
-        plane_taps(xs, d, i, j, hv, xv);
-        const int64_t m = (int64_t)row * d.HW + q;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
-            Z[(int64_t)(k * d.C + c) * d.M + m] = d.bf16 ? nca::round_bf16(acc) : acc;
-        }
-    }
+    for (int q = threadIdx.x; q < d.HW; q += kThreads) plane_z<Z16>(xs, d, kern, hv, row, c, q, Z);
 }
 
 // stencil_back for boards of at most kPlaneMax cells: workgroup p stages plane p = (row,
@@ -581,7 +617,7 @@ __global__ void __launch_bounds__(kThreads) stencil_back_plane(Dims d, const flo
     const int pl = blockIdx.x, row = pl / d.C, c = pl - row * d.C;
     const float *xr = x + (int64_t)pl * d.HW;
     const int64_t ks = (int64_t)d.C * d.M;
-    const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * d.HW;
+    const int64_t gzo = (int64_t)c * d.M + (int64_t)row * d.HW;
     // staged 4 cells per thread at a time, every load issued before the LDS writes
     for (int q0 = 0; q0 < d.HW; q0 += 4 * kThreads) {
         float v[4][5];
@@ -590,7 +626,7 @@ __global__ void __launch_bounds__(kThreads) stencil_back_plane(Dims d, const flo
             const int q = q0 + u * kThreads + threadIdx.x, qc = q < d.HW ? q : 0;
             v[u][0] = xr[qc];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[u][1 + k] = gz[k * ks + qc];
+            for (int k = 0; k < 4; ++k) v[u][1 + k] = gz_at(Gz, d.gz16, gzo + k * ks + qc);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -644,7 +680,8 @@ constexpr int kStripPlanes = 4;  // (row, channel) planes per workgroup of stenc
 // column j) walks down rows [band R, band R + R) of column j with the 3x3 neighbourhood of x and
 // g_z in registers, loading one new row of 3 columns per cell (15 LDS reads instead of 45). Per
 // cell the sums run in the order of stencil_back_kernel; the kernel-weight sums of the
-// workgroup's planes go to slot b.
+// workgroup's planes go to slot b. GZ16: g_z is bf16.
+template <bool GZ16>
 __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const float *__restrict__ x,
                                                                const float *__restrict__ Gu,
                                                                const float *__restrict__ Gz,
@@ -673,21 +710,21 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
     auto gload = [&](int pl) {
         const int row = pl / d.C, c = pl - row * d.C;
         const float *xr = x + (int64_t)pl * HW, *ur = Gu + (int64_t)pl * HW;
-        const float *gz = Gz + (int64_t)c * d.M + (int64_t)row * HW;
+        const int64_t gzo = (int64_t)c * d.M + (int64_t)row * HW;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int q = u * kThreads + threadIdx.x, qc = q < HW ? q : 0;
             if (u * kThreads < HW) {  // uniform
                 pv[u][0] = xr[qc];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) pv[u][1 + k] = gz[k * ks + qc];
+                for (int k = 0; k < 4; ++k) pv[u][1 + k] = gz_at(Gz, GZ16, gzo + k * ks + qc);
                 pv[u][5] = ur[qc];
             }
         }
     };
     if (p0 < p1) gload(p0);
     for (int pl = p0; pl < p1; ++pl) {
-        const int row = pl / d.C, c = pl - row * d.C;
+        const int c = pl % d.C;
         __syncthreads();  // the previous plane's reads are done
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -844,7 +881,8 @@ struct GemmArgs {
     const float *bias;  // per row m
     const float *mask;
     int64_t ldmask;
-    int epi, round_in, round_out;  // round_in: round A to bf16 on load (the forward's bf16 weights)
+    int epi, round_in, round_out;  // round_in: round A to bf16 on load (the forward's bf16 weights);
+                                   // round_out: round the product to bf16 (before mask / ReLU)
     int accum;                     // add the result to C instead of storing it
 };
 
@@ -908,8 +946,9 @@ __global__ void __launch_bounds__(256) gemm_f32_kernel(GemmArgs g) {
                 if (g.epi == 1) {
                     if (g.round_out) r = nca::round_bf16(r);
                     r = r > 0.0f ? r : 0.0f;
-                } else if (g.epi == 2) {
-                    r = g.mask[gm * g.ldmask + gn] > 0.0f ? r : 0.0f;
+                } else {
+                    if (g.round_out) r = nca::round_bf16(r);
+                    if (g.epi == 2) r = g.mask[gm * g.ldmask + gn] > 0.0f ? r : 0.0f;
                 }
                 if (g.accum) r = __fadd_rn(Cz[gm * g.ldc + gn], r);
                 Cz[gm * g.ldc + gn] = r;
@@ -943,6 +982,7 @@ int check_dims(const nca_cell_desc *cell, int64_t rows, int32_t H, int32_t W, in
     d->n_out = cell->n_out;
     d->padding = cell->padding;
     d->bf16 = cell->precision == NCA_BF16;
+    d->gz16 = 0;
     d->H = H;
     d->W = W;
     if ((int64_t)H * W * d->C > 0x7fffffff) return nca::set_error(NCA_ERR_UNSUPPORTED, "BPTT grid too large");
@@ -1050,16 +1090,18 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
 
     // the partial-sum slots and the loss slots are contiguous
     hipLaunchKernelGGL(zero_f32, dim3(2048), dim3(256), 0, st, part, L.denom - L.part);
-    // the fused kernel addresses z and g_z with 32-bit byte offsets
-    const bool fused = d.bf16 && d.C == 32 && d.F == 128 && d.HD == 256 && d.M * d.F * 4 < ((int64_t)1 << 32);
+    const bool fused = fused_mlp(d);
     auto mlp_kfn = (d.M & 3) == 0 ? nca::mlp_back32<true> : nca::mlp_back32<false>;
     if (fused && (rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(mlp_kfn),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                                            (int)nca::Mb32::TOTAL),
                                        "mlp_back32 attribute")))
         return rc;
+    // the stencil kernels read g_z as bf16 where the fused kernel writes it
+    Dims ds = d;
+    ds.gz16 = fused ? 1 : 0;
     // boards small enough to stage (row, channel) planes in LDS
-    const bool planes_ok = d.HW <= kPlaneMax && d.rows * d.C <= 0x7fffffff;
+    const bool planes_ok = planes_fit(d);
     // ... and walked by columns for boards at most 256 wide (kernel-weight slot per 4 planes)
     const bool strips_ok = planes_ok && d.W <= kThreads;
     const int64_t strip_blocks = (d.rows * d.C + kStripPlanes - 1) / kStripPlanes;
@@ -1070,7 +1112,6 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
                            reinterpret_cast<unsigned char *>(ws + L.img));
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
     if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;
-
     const float *gin = grad_final;
     for (int t = n_chunk - 1; t >= 0 && d.M > 0; --t) {
         const float *xt = states + t * stride, *x1 = states + (t + 1) * stride;
@@ -1109,21 +1150,23 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
         // recompute z and h from the saved state
         if (planes_ok) {
-            hipLaunchKernelGGL(stencil_z_plane, dim3((unsigned)(d.rows * d.C)), dim3(kThreads), d.HW * sizeof(float), st,
-                               d, xt, kern, padv, Z);
+            auto zfn = fused ? stencil_z_plane<true> : stencil_z_plane<false>;
+            hipLaunchKernelGGL(zfn, dim3((unsigned)(d.rows * d.C)), dim3(kThreads), d.HW * sizeof(float), st, d, xt, kern,
+                               padv, Z);
         } else {
             const dim3 zgrid(grid_for((int64_t)d.C * d.HW), (unsigned)(d.rows < 65535 ? d.rows : 65535));
-            hipLaunchKernelGGL(stencil_z_kernel, zgrid, dim3(kThreads), 0, st, d, xt, kern, padv, Z);
+            hipLaunchKernelGGL(fused ? stencil_z_kernel<true> : stencil_z_kernel<false>, zgrid, dim3(kThreads), 0, st, d,
+                               xt, kern, padv, Z);
         }
         if ((rc = nca::hip_status(hipGetLastError(), "bptt front / stencil"))) return rc;
         GemmArgs g;
         if (fused) {
             nca::MlpBackArgs ma;
-            ma.Z = Z;
+            ma.Z = reinterpret_cast<const uint16_t *>(Z);
             ma.Gdx = Gdx;
             ma.img = reinterpret_cast<const unsigned char *>(ws + L.img);
             ma.b1 = b1;
-            ma.Gz = Gz;
+            ma.Gz = reinterpret_cast<uint16_t *>(Gz);
             ma.part = part;
             ma.P = P.P;
             ma.offW1 = P.W1;
@@ -1146,25 +1189,26 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
             g.A = w->w2; g.sam = 1; g.sak = d.HD;
             g.B = Gdx; g.sbk = d.M; g.sbn = 1;
             g.Cm = Ga; g.ldc = d.M; g.M = d.HD; g.N = d.M; g.K = d.C; g.kps = d.C;
-            g.mask = Hb; g.ldmask = d.M; g.epi = 2; g.round_in = d.bf16;
+            g.mask = Hb; g.ldmask = d.M; g.epi = 2; g.round_in = d.bf16; g.round_out = d.bf16;
             if ((rc = gemm(g, 1, st))) return rc;
             // g_z = W1^T g_a: (F x HD) (HD x M)
             memset(&g, 0, sizeof(g));
             g.A = w->w1; g.sam = 1; g.sak = d.F;
             g.B = Ga; g.sbk = d.M; g.sbn = 1;
             g.Cm = Gz; g.ldc = d.M; g.M = d.F; g.N = d.M; g.K = d.HD; g.kps = d.HD;
-            g.round_in = d.bf16;
+            g.round_in = d.bf16; g.round_out = d.bf16;
             if ((rc = gemm(g, 1, st))) return rc;
         }
         // gradient of the step's input state and the kernel-weight partials
+        auto strip_fn = fused ? stencil_back_strip<true> : stencil_back_strip<false>;
         if (strips_ok)
-            hipLaunchKernelGGL(stencil_back_strip, dim3((unsigned)strip_blocks), dim3(kThreads),
-                               6 * d.HW * sizeof(float), st, d, xt, Gu, Gz, kern, padv, gx, ws + L.dk);
+            hipLaunchKernelGGL(strip_fn, dim3((unsigned)strip_blocks), dim3(kThreads), 6 * d.HW * sizeof(float), st, ds,
+                               xt, Gu, Gz, kern, padv, gx, ws + L.dk);
         else if (planes_ok)
             hipLaunchKernelGGL(stencil_back_plane, dim3((unsigned)(d.rows * d.C)), dim3(kThreads),
-                               5 * d.HW * sizeof(float), st, d, xt, Gu, Gz, kern, padv, gx, ws + L.dk);
+                               5 * d.HW * sizeof(float), st, ds, xt, Gu, Gz, kern, padv, gx, ws + L.dk);
         else
-            hipLaunchKernelGGL(stencil_back_kernel, dim3(kSplit), dim3(kBackThreads), 0, st, d, xt, Gu, Gz, kern, padv,
+            hipLaunchKernelGGL(stencil_back_kernel, dim3(kSplit), dim3(kBackThreads), 0, st, ds, xt, Gu, Gz, kern, padv,
                                gx, part, P.P, P.K);
         if (!fused) {
             // weight-gradient partials over kSplit cell ranges

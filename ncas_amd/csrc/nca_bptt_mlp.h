@@ -2,15 +2,18 @@
 // 256 hidden units (gfx950): for a tile of 32 cells,
 //
 //   h    = relu(bf16(W1 z + b1))            recomputed (the forward's rounding points)
-//   g_a  = (W2^T g_dx) * [h > 0]
-//   g_z  = W1^T g_a                          -> HBM, for the transposed stencil
+//   g_a  = bf16(W2^T g_dx) * [h > 0]
+//   g_z  = bf16(W1^T g_a)                    -> HBM as bf16, for the transposed stencil
 //   dW1 += g_a z^T,  dW2 += g_dx h^T,  db1 += sum over cells of g_a   (registers)
 //
-// with every product on v_mfma_f32_16x16x32_bf16. W1, W2 (rounded from the fp32 master weights),
-// z and h are bf16 values, so their products are exact; the fp32 gradient operands g_dx and g_a
-// are split into three bf16 parts (v = hi + mid + lo exactly: each part takes the next 8 bits of
-// the significand), each multiplied exactly and accumulated in fp32, lo first. The results are
-// fp32 sums of the exact products, like an fp32 GEMM's, in another order.
+// with every product on v_mfma_f32_16x16x32_bf16. The gradients take the reference's bf16
+// backward rounding points: g_dx arrives as bf16 values (the gradient of the bf16 tensor dx), the
+// gradient of fc1's output and the gradient of z are rounded to bf16 (reference
+// src/nca/engine/triton_mlp.py:46-78: gh = bf16(G W2) masked by h > 0, gx = bf16(gh W1)). W1, W2
+// (rounded from the fp32 master weights), z, h, g_dx and g_a are then all bf16 values, so every
+// product is exact and accumulates in fp32; the weight gradients stay fp32 sums over the
+// cells (the reference rounds each step's weight gradient to bf16 as well; these are exact
+// sums in another order).
 //
 // One workgroup per cell range (its slot of the partial sums), 8 waves; wave w owns hidden units
 // [32w, 32w + 32) for fc1, g_a and the weight gradients, whose accumulators stay in registers for
@@ -20,22 +23,21 @@
 // that each later product finds its operand in registers: D[cell 4g + i][hidden r] of two cell
 // tiles is an operand whose k runs over 8 cells in the order perm(g, j) = j < 4 ? 4g + j :
 // 16 + 4g + j - 4; the LDS operands of those products use the same cell order. g_z sums over all
-// hidden units, so g_a goes through LDS (its three bf16 parts, hidden units of each 32-block in
-// the same perm order) and wave w computes g_z for features [32(w >> 1), +32) x cells
-// [16(w & 1), +16).
+// hidden units, so g_a goes through LDS (hidden units of each 32-block in the same perm order)
+// and wave w computes g_z for features [16w, 16w + 16) of the tile's 32 cells, with its W1^T
+// fragments (8 KB) held in registers.
 //
 // Per tile: the tile's z and g_dx (prefetched into registers during the previous tile) are stored
-// to LDS; barrier; fc1, g_a, the g_a parts to LDS, dW2 and dW1; barrier; g_z.
+// to LDS; barrier; fc1, g_a, g_a to LDS, dW2 and dW1; barrier; g_z.
 //
 // LDS, rows padded by one 16-byte chunk (row strides of 17, 5 and 33 chunks) so that 8
 // consecutive lanes of a 16-byte access to 8 consecutive rows touch distinct chunks of the 64
 // banks, and every address in the tile loop is a per-lane base plus a constant:
 //   ZA   z [cell 32][feature 128] bf16, 272-byte rows
 //   ZB   z [feature 128][cell 32 in perm order] bf16, 80-byte rows
-//   GA   g_dx parts [3][cell 32][channel 32] bf16, 80-byte rows
-//   GB   g_dx parts [3][channel 32][cell 32 in perm order] bf16, 80-byte rows
-//   GAL  g_a parts [3][cell 32][hidden 256, perm order in each 32-block] bf16, 528-byte rows
-//   W1T  W1^T [feature 128][hidden 256, perm order in each 32-block] bf16, 528-byte rows
+//   GA   g_dx [cell 32][channel 32] bf16, 80-byte rows
+//   GB   g_dx [channel 32][cell 32 in perm order] bf16, 80-byte rows
+//   GAL  g_a [cell 32][hidden 256, perm order in each 32-block] bf16, 528-byte rows
 //   B1   b1 fp32
 #pragma once
 
@@ -44,11 +46,11 @@
 namespace nca {
 
 struct MlpBackArgs {
-    const float *Z;    // z (F x M), bf16 values
-    const float *Gdx;  // g_dx (C x M)
+    const uint16_t *Z;  // z (F x M) as bf16
+    const float *Gdx;  // g_dx (C x M), bf16 values
     const unsigned char *img;  // the weight image written by mlp_back32_prep
     const float *b1;   // HD
-    float *Gz;         // g_z (F x M)
+    uint16_t *Gz;      // g_z (F x M) as bf16
     float *part;       // partial-sum slots, P floats each; workgroup s adds into slot s
     int64_t P, offW1, offB1, offW2, M;
     int per;  // cells per workgroup, a multiple of 32
@@ -56,15 +58,12 @@ struct MlpBackArgs {
 
 struct Mb32 {
     static constexpr unsigned ZAR = 272, ZBR = 80, GR = 80, AR = 528;  // row strides
-    static constexpr unsigned GPART = 32 * GR;   // bytes of one g_dx part
-    static constexpr unsigned APART = 32 * AR;   // bytes of one g_a part
-    static constexpr unsigned ZA = 0, ZB = ZA + 32 * ZAR, GA = ZB + 128 * ZBR, GB = GA + 3 * GPART,
-                              GAL = GB + 3 * GPART, W1T = GAL + 3 * APART, B1 = W1T + 128 * AR,
-                              TOTAL = B1 + 1024;
-    // weight image: W1T exactly as in LDS, then per (wave, lane) the W1 fragments [ht][kb] and
-    // the W2 fragments [ht], 16 bytes each
-    static constexpr unsigned IMG_W1T = 0, IMG_W1F = 128 * AR, IMG_W2F = IMG_W1F + 512 * 8 * 16,
-                              IMG_BYTES = IMG_W2F + 512 * 2 * 16;
+    static constexpr unsigned ZA = 0, ZB = ZA + 32 * ZAR, GA = ZB + 128 * ZBR, GB = GA + 32 * GR,
+                              GAL = GB + 32 * GR, B1 = GAL + 32 * AR, TOTAL = B1 + 1024;
+    // weight image: per (wave, lane) the W1 fragments [ht][kb], the W2 fragments [ht] and the
+    // W1^T fragments [kb], 16 bytes each
+    static constexpr unsigned IMG_W1F = 0, IMG_W2F = IMG_W1F + 512 * 8 * 16, IMG_W1TF = IMG_W2F + 512 * 2 * 16,
+                              IMG_BYTES = IMG_W1TF + 512 * 8 * 16;
 };
 
 typedef float mb_f32x4 __attribute__((ext_vector_type(4)));
@@ -80,41 +79,14 @@ __device__ __forceinline__ bf16x8 mb_pack8(const float v[8]) {
                      cvt_pk_bf16(v[6], v[7])};
     return __builtin_bit_cast(bf16x8, u);
 }
-// a = hi + mid + lo and b likewise, exactly; each part packed as a bf16 pair (a in the low half).
-__device__ __forceinline__ void mb_split(float a, float b, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
-    hi = cvt_pk_bf16(a, b);
-    const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xffff0000u);
-    mid = cvt_pk_bf16(ra, rb);
-    const float sa = ra - __uint_as_float(mid << 16), sb = rb - __uint_as_float(mid & 0xffff0000u);
-    lo = cvt_pk_bf16(sa, sb);
-}
-// eight floats -> three bf16x8 parts
-__device__ __forceinline__ void mb_split8(const float v[8], uint4 p[3]) {
-    mb_split(v[0], v[1], p[0].x, p[1].x, p[2].x);
-    mb_split(v[2], v[3], p[0].y, p[1].y, p[2].y);
-    mb_split(v[4], v[5], p[0].z, p[1].z, p[2].z);
-    mb_split(v[6], v[7], p[0].w, p[1].w, p[2].w);
-}
 __device__ __forceinline__ int mb_perm(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4; }
 
-// The weight image of mlp_back32 from the fp32 master weights (rounded to bf16): W1^T in the
-// kernel's LDS layout (hidden units of each 32-block in perm order, padding zero) and the
-// register fragments of every (wave, lane). One workgroup of 512 threads.
+// The weight image of mlp_back32 from the fp32 master weights (rounded to bf16): the register
+// fragments of every (wave, lane): W1 for fc1, W2 for g_a, and W1^T for g_z (the A operand of
+// feature tile w, hidden block kb in perm order). One workgroup of 512 threads.
 __global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const float *w2, unsigned char *img) {
     typedef Mb32 S;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
-    for (int e = tid; e < 128 * 33; e += 512) {
-        const int f = e / 33, c = e - f * 33;
-        uint4 u = {0u, 0u, 0u, 0u};
-        if (c < 32) {
-            const int kb = c >> 2, q = c & 3;
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = w1[(32 * kb + mb_perm(q, j)) * 128 + f];
-            u = __builtin_bit_cast(uint4, mb_pack8(v));
-        }
-        *reinterpret_cast<uint4 *>(img + S::IMG_W1T + f * S::AR + 16 * c) = u;
-    }
 #pragma unroll
     for (int ht = 0; ht < 2; ++ht) {
         const int hid = 32 * w + 16 * ht + r;
@@ -130,6 +102,13 @@ __global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const fl
         for (int j = 0; j < 8; ++j) v[j] = w2[(8 * g + j) * 256 + hid];
         *reinterpret_cast<bf16x8 *>(img + S::IMG_W2F + (tid * 2 + ht) * 16) = mb_pack8(v);
     }
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = w1[(32 * kb + mb_perm(g, j)) * 128 + 16 * w + r];
+        *reinterpret_cast<bf16x8 *>(img + S::IMG_W1TF + (tid * 8 + kb) * 16) = mb_pack8(v);
+    }
 }
 
 // VEC: M is a multiple of 4, so the cell quads of a tile are 16-byte aligned.
@@ -144,12 +123,11 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
     if (mb0 >= M) return;  // uniform: an empty range adds nothing to its slot
     const int64_t mb1 = mb0 + a.per < M ? mb0 + a.per : M;
 
-    // ---- set-up: W1^T and b1 into LDS, W1 / W2 fragments into registers
-    for (int e = tid; e < (int)(128 * S::AR / 16); e += 512)
-        lds_st128(smem, S::W1T + 16 * e, *reinterpret_cast<const uint4 *>(a.img + S::IMG_W1T + 16 * e));
+    // ---- set-up: b1 into LDS, W1 / W2 / W1^T fragments into registers
     if (tid < 256) reinterpret_cast<float *>(smem + S::B1)[tid] = a.b1[tid];
-    bf16x8 w1f[2][4];  // [ht][kb]: W1[32w + 16ht + r][32kb + 8g + j]
-    bf16x8 w2f[2];     // [ht]: W2[8g + j][32w + 16ht + r]
+    bf16x8 w1f[2][4];   // [ht][kb]: W1[32w + 16ht + r][32kb + 8g + j]
+    bf16x8 w2f[2];      // [ht]: W2[8g + j][32w + 16ht + r]
+    bf16x8 w1t[8];      // [kb]: W1[32kb + perm(g, j)][16w + r]
 #pragma unroll
     for (int ht = 0; ht < 2; ++ht) {
 #pragma unroll
@@ -157,6 +135,18 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             w1f[ht][kb] = *reinterpret_cast<const bf16x8 *>(a.img + S::IMG_W1F + (tid * 8 + 4 * ht + kb) * 16);
         w2f[ht] = *reinterpret_cast<const bf16x8 *>(a.img + S::IMG_W2F + (tid * 2 + ht) * 16);
     }
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) w1t[kb] = *reinterpret_cast<const bf16x8 *>(a.img + S::IMG_W1TF + (tid * 8 + kb) * 16);
+    // the weight fragments live in AGPRs (MFMA reads its A / B operands from them), leaving the
+    // VGPRs to the accumulators and the tile's operands
+#pragma unroll
+    for (int ht = 0; ht < 2; ++ht) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) asm volatile("" : "+a"(w1f[ht][kb]));
+        asm volatile("" : "+a"(w2f[ht]));
+    }
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) asm volatile("" : "+a"(w1t[kb]));
     mb_f32x4 dw1[2][8], dw2[2][2];  // dw1[ht][ft]: D[hid 32w+16ht+4g+i][f 16ft+r]; dw2[ct][ht]: D[ch 16ct+4g+i][hid 32w+16ht+r]
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
@@ -175,7 +165,7 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
     const int lrow = tid >> 2, q = tid & 3;
     const unsigned char *zb = reinterpret_cast<const unsigned char *>(a.Z);
     const unsigned char *gb = reinterpret_cast<const unsigned char *>(a.Gdx);
-    const uint32_t rowb = (uint32_t)lrow * (uint32_t)M * 4u;
+    const uint32_t rowb = (uint32_t)lrow * (uint32_t)M * 4u, rowz = (uint32_t)lrow * (uint32_t)M * 2u;
     float pz[8], pg[8];
     auto load8 = [&](const unsigned char *base, int64_t m0, float v[8]) {
 #pragma unroll
@@ -198,12 +188,33 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             }
         }
     };
+    auto load8z = [&](int64_t m0, float v[8]) {  // z: bf16
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t m = m0 + 16 * h + 4 * q;
+            if (VEC) {
+                const bool ok = m < mb1;
+                const uint2 x = *reinterpret_cast<const uint2 *>(zb + rowz + (uint32_t)(ok ? m : mb0) * 2u);
+                v[4 * h] = __uint_as_float(x.x << 16);
+                v[4 * h + 1] = __uint_as_float(x.x & 0xffff0000u);
+                v[4 * h + 2] = __uint_as_float(x.y << 16);
+                v[4 * h + 3] = __uint_as_float(x.y & 0xffff0000u);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = m + e < mb1;
+                    const uint32_t u = *reinterpret_cast<const uint16_t *>(zb + rowz + (uint32_t)(ok ? m + e : mb0) * 2u);
+                    v[4 * h + e] = __uint_as_float(u << 16);
+                }
+            }
+        }
+    };
     auto zero_past = [&](int64_t m0, float v[8]) {  // cells past the range
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = m0 + mb_perm(q, j) < mb1 ? v[j] : 0.0f;
     };
     auto load_tile = [&](int64_t m0) {
-        load8(zb, m0, pz);
+        load8z(m0, pz);
         if (w < 2) load8(gb, m0, pg);
     };
     auto store_tile = [&](int64_t m0) {
@@ -214,17 +225,12 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             *reinterpret_cast<__bf16 *>(smem + S::ZA + mb_perm(q, j) * S::ZAR + 2 * lrow) = (__bf16)pz[j];
-        if (w < 2) {  // GB row lrow chunk q; GA column lrow of rows perm(q, j); three parts
-            uint4 p[3];
-            mb_split8(pg, p);
+        if (w < 2) {  // GB row lrow chunk q; GA column lrow of rows perm(q, j)
+            const bf16x8 pv = mb_pack8(pg);
+            *reinterpret_cast<bf16x8 *>(smem + S::GB + lrow * S::GR + 16 * q) = pv;
 #pragma unroll
-            for (int sp = 0; sp < 3; ++sp) {
-                lds_st128(smem, S::GB + sp * S::GPART + lrow * S::GR + 16 * q, p[sp]);
-                const bf16x8 pv = __builtin_bit_cast(bf16x8, p[sp]);
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    *reinterpret_cast<__bf16 *>(smem + S::GA + sp * S::GPART + mb_perm(q, j) * S::GR + 2 * lrow) = pv[j];
-            }
+            for (int j = 0; j < 8; ++j)
+                *reinterpret_cast<__bf16 *>(smem + S::GA + mb_perm(q, j) * S::GR + 2 * lrow) = pv[j];
         }
     };
 
@@ -243,7 +249,7 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
 #pragma unroll
             for (int y = 0; y < 2; ++y) hT[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
         // operands of fc1 read up front; those of g_a while fc1 finishes
-        bf16x8 zf[4][2], gf[3][2];
+        bf16x8 zf[4][2], gf[2];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             const unsigned zo = S::ZA + r * S::ZAR + 16 * (4 * kb + g);
@@ -261,10 +267,7 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int sp = 0; sp < 3; ++sp)
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-                gf[sp][ct] = mb_ld(smem, S::GA + sp * S::GPART + (16 * ct + r) * S::GR + 16 * g);
+        for (int ct = 0; ct < 2; ++ct) gf[ct] = mb_ld(smem, S::GA + (16 * ct + r) * S::GR + 16 * g);
         __builtin_amdgcn_sched_barrier(0);
         {
             const float *b1L = reinterpret_cast<const float *>(smem + S::B1);
@@ -281,24 +284,18 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             }
         }
 
-        // ---- g_a = (W2^T g_dx) * [h > 0]: gaT[ct][ht] like hT (parts lo, mid, hi)
+        // ---- g_a = bf16(W2^T g_dx) * [h > 0]: gaT[ct][ht] like hT
         mb_f32x4 gaT[2][2];
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-            for (int y = 0; y < 2; ++y) gaT[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int sp = 2; sp >= 0; --sp)
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-                for (int ht = 0; ht < 2; ++ht) gaT[ct][ht] = mb_mfma(gf[sp][ct], w2f[ht], gaT[ct][ht]);
+            for (int ht = 0; ht < 2; ++ht) gaT[ct][ht] = mb_mfma(gf[ct], w2f[ht], mb_f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int x = 0; x < 2; ++x)
 #pragma unroll
             for (int y = 0; y < 2; ++y)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) gaT[x][y][i] = hT[x][y][i] > 0.0f ? gaT[x][y][i] : 0.0f;
+                for (int i = 0; i < 4; ++i) gaT[x][y][i] = hT[x][y][i] > 0.0f ? round_bf16(gaT[x][y][i]) : 0.0f;
         // db1: this lane's hidden unit 32w + 16ht + r over cells 16ct + 4g + i
 #pragma unroll
         for (int ht = 0; ht < 2; ++ht)
@@ -306,17 +303,13 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) db1[ht] = __fadd_rn(db1[ht], gaT[ct][ht][i]);
-        // g_a parts, k over cells in perm order: ap[ht][sp] element j = part sp of
-        // g_a[hid 32w + 16ht + r][cell perm(g, j)]
-        bf16x8 ap[2][3];
+        // g_a, k over cells in perm order: ap[ht] element j = g_a[hid 32w + 16ht + r][cell perm(g, j)]
+        bf16x8 ap[2];
 #pragma unroll
         for (int ht = 0; ht < 2; ++ht) {
             const float v[8] = {gaT[0][ht][0], gaT[0][ht][1], gaT[0][ht][2], gaT[0][ht][3],
                                 gaT[1][ht][0], gaT[1][ht][1], gaT[1][ht][2], gaT[1][ht][3]};
-            uint4 p[3];
-            mb_split8(v, p);
-#pragma unroll
-            for (int sp = 0; sp < 3; ++sp) ap[ht][sp] = __builtin_bit_cast(bf16x8, p[sp]);
+            ap[ht] = mb_pack8(v);
         }
         // ... and into GAL for g_z: hidden offset o = 16ht + r of block w sits at chunk r >> 2,
         // element 4ht + (r & 3) of the block's perm order
@@ -325,13 +318,10 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             const int cell = mb_perm(g, j);
             const unsigned base = S::GAL + cell * S::AR + 16 * (4 * w + (r >> 2)) + 2 * (r & 3);
 #pragma unroll
-            for (int ht = 0; ht < 2; ++ht)
-#pragma unroll
-                for (int sp = 0; sp < 3; ++sp)
-                    *reinterpret_cast<__bf16 *>(smem + base + sp * S::APART + 8 * ht) = ap[ht][sp][j];
+            for (int ht = 0; ht < 2; ++ht) *reinterpret_cast<__bf16 *>(smem + base + 8 * ht) = ap[ht][j];
         }
 
-        // ---- dW2 += g_dx h^T: A = g_dx parts [channel][cells perm], B = h^T (exact bf16)
+        // ---- dW2 += g_dx h^T: A = g_dx [channel][cells perm], B = h^T
         {
             bf16x8 hb[2];
 #pragma unroll
@@ -341,74 +331,52 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
                 hb[ht] = mb_pack8(v);
             }
 #pragma unroll
-            for (int sp = 2; sp >= 0; --sp)
+            for (int ct = 0; ct < 2; ++ct) {
+                const bf16x8 gbv = mb_ld(smem, S::GB + (16 * ct + r) * S::GR + 16 * g);
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    const int c = 16 * ct + r;
-                    const bf16x8 gb = mb_ld(smem, S::GB + sp * S::GPART + c * S::GR + 16 * g);
-#pragma unroll
-                    for (int ht = 0; ht < 2; ++ht) dw2[ct][ht] = mb_mfma(gb, hb[ht], dw2[ct][ht]);
-                }
+                for (int ht = 0; ht < 2; ++ht) dw2[ct][ht] = mb_mfma(gbv, hb[ht], dw2[ct][ht]);
+            }
         }
-        // ---- dW1 += g_a z^T: A = g_a parts (hidden x cells perm), B = z [cells perm][feature]
+        // ---- dW1 += g_a z^T: A = g_a (hidden x cells perm), B = z [cells perm][feature]
 #pragma unroll
         for (int ft = 0; ft < 8; ft += 2) {
             const int f0 = 16 * ft + r, f1 = f0 + 16;
             const bf16x8 zb0 = mb_ld(smem, S::ZB + f0 * S::ZBR + 16 * g);
             const bf16x8 zb1 = mb_ld(smem, S::ZB + f1 * S::ZBR + 16 * g);
 #pragma unroll
-            for (int sp = 2; sp >= 0; --sp)
-#pragma unroll
-                for (int ht = 0; ht < 2; ++ht) {
-                    dw1[ht][ft] = mb_mfma(ap[ht][sp], zb0, dw1[ht][ft]);
-                    dw1[ht][ft + 1] = mb_mfma(ap[ht][sp], zb1, dw1[ht][ft + 1]);
-                }
+            for (int ht = 0; ht < 2; ++ht) {
+                dw1[ht][ft] = mb_mfma(ap[ht], zb0, dw1[ht][ft]);
+                dw1[ht][ft + 1] = mb_mfma(ap[ht], zb1, dw1[ht][ft + 1]);
+            }
         }
         __syncthreads();
 
-        // ---- g_z = W1^T g_a: features 16 fb + 4g + i (fb = 2(w >> 1) + f) of cell 16ct + r,
-        //      even and odd hidden blocks in separate chains
+        // ---- g_z = bf16(W1^T g_a): features 16w + 4g + i of cells 16ct + r, even and odd hidden
+        //      blocks in separate chains
         {
-            const int ct = w & 1, fb = 2 * (w >> 1);
             mb_f32x4 gz[2][2];
 #pragma unroll
             for (int x = 0; x < 2; ++x)
 #pragma unroll
                 for (int y = 0; y < 2; ++y) gz[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
-            const int cell = 16 * ct + r;
-            // operands of hidden block kb + 1 are read while block kb multiplies
-            const unsigned ao = S::W1T + (16 * fb + r) * S::AR + 16 * g;
-            const unsigned bo = S::GAL + cell * S::AR + 16 * g;
-            bf16x8 A[2][2], B[2][3];
-            auto ld = [&](int kb, int sl) {
-                A[sl][0] = mb_ld(smem, ao + 64 * kb);
-                A[sl][1] = mb_ld(smem, ao + 16 * S::AR + 64 * kb);
-#pragma unroll
-                for (int sp = 0; sp < 3; ++sp) B[sl][sp] = mb_ld(smem, bo + sp * S::APART + 64 * kb);
-            };
-            ld(0, 0);
+            const unsigned bo = S::GAL + r * S::AR + 16 * g;
 #pragma unroll
             for (int kb = 0; kb < 8; ++kb) {
-                if (kb + 1 < 8) ld(kb + 1, (kb + 1) & 1);
-                __builtin_amdgcn_sched_barrier(0);
-                const int sl = kb & 1;
-#pragma unroll
-                for (int sp = 2; sp >= 0; --sp) {
-                    gz[0][sl] = mb_mfma(A[sl][0], B[sl][sp], gz[0][sl]);
-                    gz[1][sl] = mb_mfma(A[sl][1], B[sl][sp], gz[1][sl]);
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                const bf16x8 B0 = mb_ld(smem, bo + 64 * kb), B1 = mb_ld(smem, bo + 16 * S::AR + 64 * kb);
+                gz[0][kb & 1] = mb_mfma(w1t[kb], B0, gz[0][kb & 1]);
+                gz[1][kb & 1] = mb_mfma(w1t[kb], B1, gz[1][kb & 1]);
             }
-            const int64_t m = m0 + cell;
-            if (m < mb1) {
-                unsigned char *gzb = reinterpret_cast<unsigned char *>(a.Gz);
-                const uint32_t o0 = ((uint32_t)(16 * fb + 4 * g) * (uint32_t)M + (uint32_t)m) * 4u;
+            unsigned char *gzb = reinterpret_cast<unsigned char *>(a.Gz);
 #pragma unroll
-                for (int f = 0; f < 2; ++f)
+            for (int ct = 0; ct < 2; ++ct) {
+                const int64_t m = m0 + 16 * ct + r;
+                if (m < mb1) {
+                    const uint32_t o0 = ((uint32_t)(16 * w + 4 * g) * (uint32_t)M + (uint32_t)m) * 2u;
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        *reinterpret_cast<float *>(gzb + o0 + (uint32_t)(16 * f + i) * (uint32_t)M * 4u) =
-                            __fadd_rn(gz[f][0][i], gz[f][1][i]);
+                        *reinterpret_cast<__bf16 *>(gzb + o0 + (uint32_t)i * (uint32_t)M * 2u) =
+                            (__bf16)__fadd_rn(gz[ct][0][i], gz[ct][1][i]);
+                }
             }
         }
     }

@@ -26,7 +26,11 @@ Precision modes: "fp32" and "fp64" compute everything in that type. "bf16" repro
 rounding points of the reference under `torch.autocast(bfloat16)` (engine/step.py:240-242,
 ops.py:237): the perception input and the kernels are rounded to bf16 (autocast casts a conv's
 operands), z, h (fc1 output, ReLU applied in bf16) and dx (fc2 output) are bf16, products are
-exact in fp32 and accumulate in fp32, and the residual update and clamp stay fp32.
+exact in fp32 and accumulate in fp32, and the residual update and clamp stay fp32. The bf16
+chunk's gradients go straight through the rounding points (`ste`); with `grad_round` the
+gradients reaching dx, h and z are rounded to bf16 as in the reference's bf16 backward
+(engine/triton_mlp.py:46-78), pinned against a written-out numpy backward in
+tests/test_oracle_bptt.py.
 
 Cells are described by `OracleCell`, a plain record of tensors, so that the oracle does not
 depend on the product's classes.
@@ -115,14 +119,35 @@ class _RoundBF16(torch.autograd.Function):
         return g
 
 
+class _RoundBF16Grad(torch.autograd.Function):
+    """Round to bf16 in the forward and round the incoming gradient to bf16 in the backward: the
+    gradient of a bf16 tensor of the reference's autocast step is itself bf16 (a bf16 op's
+    backward produces bf16 gradients), so the gradients reaching dx (fc2's output), h (fc1's
+    output) and z (the perception's output) are rounded there. The Triton MLP backward of the
+    reference's fused engine rounds at the same points: G = grad(dx) in bf16, gh = bf16(G W2)
+    masked by h > 0, gx = bf16(gh W1) (reference src/nca/engine/triton_mlp.py:46-78)."""
+
+    @staticmethod
+    def forward(ctx, t):
+        return t.to(torch.bfloat16).to(t.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(torch.bfloat16).to(g.dtype)
+
+
 def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32",
-                 dtype: torch.dtype | None = None, ste: bool = False) -> torch.Tensor:
+                 dtype: torch.dtype | None = None, ste: bool = False,
+                 grad_round: bool = False) -> torch.Tensor:
     """Perception + MLP: the proposed dx of every cell (model.py:489-495). `dtype` overrides the
-    compute type (fp64 for gradients); `ste` makes the bf16 rounding points straight-through."""
+    compute type (fp64 for gradients); `ste` makes the bf16 rounding points straight-through;
+    `grad_round` (with `ste`) also rounds the gradients of z, h and dx to bf16, the reference's
+    bf16 backward (the perception input's and the weights' gradients stay unrounded)."""
     B, C, H, W = x.shape
     dt = dtype or _dtype(precision)
     bf = precision == "bf16"
     _bf = _RoundBF16.apply if ste else globals()["_bf"]
+    _bfg = _RoundBF16Grad.apply if (ste and grad_round) else _bf
     x = x.to(dt)
     xp = pad(x, cell.padding, cell.pad_vec.to(dt))
     k = cell.kernels.to(dt)
@@ -130,18 +155,18 @@ def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32",
         xp, k = _bf(xp), _bf(k)
     z = perceive(xp, k, H, W)
     if bf:
-        z = _bf(z)
+        z = _bfg(z)
     rows = z.permute(0, 2, 3, 1).reshape(-1, z.shape[1])
     w1, b1, w2, b2 = (t.to(dt) for t in (cell.w1, cell.b1, cell.w2, cell.b2))
     if bf:
         w1, b1, w2, b2 = _bf(w1), _bf(b1), _bf(w2), _bf(b2)
     h = rows @ w1.T + b1
     if bf:
-        h = _bf(h)
+        h = _bfg(h)
     h = torch.relu(h)
     dx = h @ w2.T + b2
     if bf:
-        dx = _bf(dx)
+        dx = _bfg(dx)
     return dx.reshape(B, H, W, C).permute(0, 3, 1, 2)
 
 
@@ -153,11 +178,12 @@ def apply_clamp(cell: OracleCell, x, given4, clamp):
     return out
 
 
-def step(cell: OracleCell, x, given4, clamp, fire, precision="fp32", noise=None, dtype=None, ste=False):
+def step(cell: OracleCell, x, given4, clamp, fire, precision="fp32", noise=None, dtype=None, ste=False,
+         grad_round=False):
     """One step (model.py:503-559 without time embedding / normalisation). fire: (B,1,H,W)."""
     dt = dtype or _dtype(precision)
     x = x.to(dt)
-    dx = sense_update(cell, x, precision, dtype, ste)
+    dx = sense_update(cell, x, precision, dtype, ste, grad_round)
     u = x + fire.to(dt) * dx.to(dt)
     if noise is not None:
         u = u + noise.to(dt)
@@ -226,22 +252,23 @@ def rollout(
 
 
 def chunk_loss(cell: OracleCell, x0, given4, clamp, masks, targets, weights, precision="fp32",
-               loss_mask=None, ste=True, final_cotangent=None):
+               loss_mask=None, ste=True, final_cotangent=None, grad_round=False):
     """The BPTT chunk's loss (engine.py:474-490 with the chunk's run_block, step.py:236-245):
     `n` steps from x0 with fire masks `masks` (n, B, 1, H, W), then
     L = sum_t w_t * step_loss(x_{t+1}) / max(sum_t w_t, 1), where step_loss is the mean (or the
     loss_mask weighted mean, train.py:196-207) over cells of the cross-entropy of the mlp head's
     logits against `targets` (B, H, W) class indices (train.py:190-192). Computed in fp64,
     differentiable w.r.t. the cell's tensors and x0; bf16 cells round at the forward's points
-    (straight-through when `ste`). `final_cotangent` adds sum(x_n * final_cotangent), whose
-    gradient w.r.t. the last state is that cotangent (a later loss's gradient)."""
+    (straight-through when `ste`; with `grad_round` the gradients of z, h and dx are rounded to
+    bf16 as in the reference's bf16 backward). `final_cotangent` adds sum(x_n * final_cotangent),
+    whose gradient w.r.t. the last state is that cotangent (a later loss's gradient)."""
     dt = torch.float64
     x = x0.to(dt)
     w = torch.as_tensor(weights, dtype=dt)
     total = x.new_zeros(())
     sl = slice(cell.out_offset, cell.out_offset + cell.c_out)
     for t in range(masks.shape[0]):
-        x = step(cell, x, given4, clamp, masks[t], precision, dtype=dt, ste=ste)
+        x = step(cell, x, given4, clamp, masks[t], precision, dtype=dt, ste=ste, grad_round=grad_round)
         if w[t] == 0:
             continue
         logits = torch.einsum("vc,bchw->bvhw", cell.head_w.to(dt), x[:, sl]) \
@@ -260,8 +287,9 @@ def chunk_loss(cell: OracleCell, x0, given4, clamp, masks, targets, weights, pre
 
 
 def bptt_chunk(cell: OracleCell, x0, given4, clamp, masks, targets, weights, precision="fp32",
-               loss_mask=None, grad_x0=False, ste=True, final_cotangent=None):
-    """`chunk_loss` and its gradients by torch autograd in fp64.
+               loss_mask=None, grad_x0=False, ste=True, final_cotangent=None, grad_round=False):
+    """`chunk_loss` and its gradients by torch autograd in fp64 (`grad_round`: the reference's
+    bf16 gradient rounding points, see `_RoundBF16Grad`).
 
     Returns (loss float, grads dict of fp64 tensors: kernels, w1, b1, w2, b2, head_w, head_b,
     and x0 when grad_x0)."""
@@ -271,7 +299,7 @@ def bptt_chunk(cell: OracleCell, x0, given4, clamp, masks, targets, weights, pre
     c = OracleCell(**{**cell.__dict__, **params})
     x = x0.detach().to(dt).clone().requires_grad_(grad_x0)
     loss = chunk_loss(c, x, given4, clamp, masks, targets, weights, precision, loss_mask, ste,
-                      final_cotangent)
+                      final_cotangent, grad_round)
     wrt = [params[k] for k in names] + ([x] if grad_x0 else [])
     if not loss.requires_grad:  # every step weight is zero: a constant loss
         grads = [None] * len(wrt)

@@ -140,7 +140,11 @@ def test_bptt_argument_checks(lib):
     c32 = _cell(channels=32, hidden=256, c_in=4, c_out=4, out_offset=4, n_out=2, padding=1)
     n = lib.nca_bptt_workspace_bytes(ctypes.byref(c32), 64, 30, 30, 32)
     M = 64 * 900
-    assert n >= 4 * M * (2 * 128 + 2 * 256 + 4 * 32)  # z, g_z, h, g_a, g_dx, g_u, 2 x g_x
+    # bf16, 32 channels, 256 hidden units: the fused MLP backward (z, g_z, g_dx, g_u, 2 x g_x)
+    assert 4 * M * (2 * 128 + 4 * 32) <= n < 4 * M * (2 * 128 + 2 * 256 + 4 * 32)
+    c32f = _cell(channels=32, hidden=256, c_in=4, c_out=4, out_offset=4, n_out=2, padding=1, precision=0)
+    nf = lib.nca_bptt_workspace_bytes(ctypes.byref(c32f), 64, 30, 30, 32)
+    assert nf >= 4 * M * (2 * 128 + 2 * 256 + 4 * 32)  # fp32 GEMM path: also h and g_a
     assert lib.nca_bptt_workspace_bytes(ctypes.byref(_cell(head_kind=1)), 4, 9, 9, 8) == 0
     assert b"mlp head" in lib.nca_last_error()
     fire = _lib.FireDesc(seed=1, p_fire=0.5)

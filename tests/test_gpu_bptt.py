@@ -6,7 +6,9 @@ fp64 autograd oracle (the engine around it is tested in test_gpu_train.py).
   wrap padding and injected or Philox fire masks.
 * bf16 cells: the single-step vector-Jacobian product from the GPU's own state (so that both
   sides differentiate the same rounded operands) within 1e-3; multi-step chunks within 1e-2
-  of the oracle (a bf16 rounding flip in the forward moves a state by up to 2e-2).
+  of the oracle (a bf16 rounding flip in the forward moves a state by up to 2e-2). The oracle
+  rounds the gradients of dx, h and z to bf16 (`grad_round`) as the reference's bf16 backward
+  does (src/nca/engine/triton_mlp.py:46-78), like the kernels.
 * The chunk's saved states are the rollout kernels' states bit for bit; gradients are
   bitwise reproducible; chaining two chunks through grad_final / grad_x0 equals one chunk.
 """
@@ -106,7 +108,7 @@ def test_bptt_bf16_single_step_vjp_from_the_gpu_state(name):
     res = _gpu_chunk(md, xs, g4, cl, targets, [1.0], "bf16", masks=masks[:1].to(DEV),
                      grad_final=cot.to(DEV))
     loss, ref = O.bptt_chunk(oracle_cell(m), xs, g4, cl, masks[:1].double(), targets, [1.0],
-                             "bf16", grad_x0=True, final_cotangent=cot.double())
+                             "bf16", grad_x0=True, final_cotangent=cot.double(), grad_round=True)
     worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
     _say("bf16 vjp worst rel", worst, "x0", _rel(res.grad_x0, ref["x0"]))
     assert worst <= 1e-3
@@ -119,7 +121,7 @@ def test_bptt_bf16_chunk_near_oracle(name):
     weights = [0.5, 0.0, 1.0, 0.0, 1.0]
     res = _gpu_chunk(md, x, g4, cl, targets, weights, "bf16", masks=masks.to(DEV))
     loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, weights, "bf16",
-                             grad_x0=True)
+                             grad_x0=True, grad_round=True)
     worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
     _say("bf16 chunk worst rel", worst, "loss", float(res.loss), loss)
     assert abs(float(res.loss) - loss) <= 1e-4 * abs(loss)
@@ -191,14 +193,14 @@ def test_bptt_bf16_odd_cell_count_13x13():
     res = _gpu_chunk(md, xs, g4, cl, targets, [1.0], "bf16", masks=masks[:1].to(DEV),
                      grad_final=cot.to(DEV))
     loss, ref = O.bptt_chunk(oracle_cell(m), xs, g4, cl, masks[:1].double(), targets, [1.0],
-                             "bf16", grad_x0=True, final_cotangent=cot.double())
+                             "bf16", grad_x0=True, final_cotangent=cot.double(), grad_round=True)
     worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
     _say("vjp worst rel", worst)
     assert worst <= 1e-3 and _rel(res.grad_x0, ref["x0"]) <= 1e-3
     w = [1.0, 0.0, 0.5, 1.0]
     res = _gpu_chunk(md, x, g4, cl, targets, w, "bf16", masks=masks.to(DEV))
     loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, w, "bf16",
-                             grad_x0=True)
+                             grad_x0=True, grad_round=True)
     worst = max(_rel(res.grads[k], ref[k]) for k in NAMES)
     _say("chunk worst rel", worst)
     assert abs(float(res.loss) - loss) <= 1e-4 * abs(loss)

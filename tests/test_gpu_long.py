@@ -200,7 +200,7 @@ def test_bptt_bf16_30x30_32_step_chunk():
         res = bptt_chunk(md, x.to(DEV), g4.to(DEV), cl.to(DEV), targets.to(DEV), weights,
                          step_seeds=seeds, p_fire=0.8, precision="bf16", want_grad_x0=True)
     loss, ref = O.bptt_chunk(oracle_cell(m), x, g4, cl, masks.double(), targets, weights, "bf16",
-                             grad_x0=True)
+                             grad_x0=True, grad_round=True)
 
     def rel(a, r):
         a, r = a.detach().double().cpu().reshape(-1), r.detach().double().cpu().reshape(-1)

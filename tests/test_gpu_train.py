@@ -2,7 +2,8 @@
 engine's train_iteration, against the fp64 autograd oracle.
 
 * The step's vector-Jacobian product (state, clamp values, noise, every step parameter) within a
-  relative norm error of 1e-4 (fp32) / 1e-3 (bf16, straight-through rounding) of the oracle,
+  relative norm error of 1e-4 (fp32) / 1e-3 (bf16: straight-through rounding points, with the
+  gradients of dx, h and z rounded to bf16 like the reference's bf16 backward) of the oracle,
   for every cell (mlp and l2 heads), fire masks {Philox, 0, 1, 0.5} and noise; `make_step`
   under autograd gives the same gradients (reference tests/test_engine_ops.py:251-294).
 * `Engine(model, cfg, train_cfg, device).train_iteration` equals its composition (prefix, chunk,
@@ -64,7 +65,8 @@ def oracle_step_vjp(m, x, g4, cl, fire, noise, cot, precision):
     xx = x.detach().to(dt).clone().requires_grad_(True)
     cc = cl.detach().to(dt).clone().requires_grad_(True)
     nz = None if noise is None else noise.detach().to(dt).clone().requires_grad_(True)
-    y = O.step(c, xx, g4, cc, fire.to(dt), precision, nz, dtype=dt, ste=True)
+    y = O.step(c, xx, g4, cc, fire.to(dt), precision, nz, dtype=dt, ste=True,
+               grad_round=precision == "bf16")
     wrt = [xx, cc] + ([nz] if nz is not None else []) + [params[k] for k in STEP_NAMES]
     g = torch.autograd.grad((y * cot.to(dt)).sum(), wrt, allow_unused=True)
     g = [torch.zeros_like(w) if v is None else v for v, w in zip(g, wrt)]
@@ -247,7 +249,8 @@ def test_engine_amp_runs_prefix_and_suffix_in_fp32():
     # the chunk: bf16, from the GPU's prefix state
     tgt = md.output_index(batch["targets"]).cpu()
     cmasks = _masks(seeds[c0:c0 + Nc], c0, B, H, W, p)
-    ref_loss, ref = O.bptt_chunk(cell, xp.cpu(), g4, cl, cmasks.double(), tgt, w, "bf16")
+    ref_loss, ref = O.bptt_chunk(cell, xp.cpu(), g4, cl, cmasks.double(), tgt, w, "bf16",
+                                 grad_round=True)
     assert abs(float(loss) - ref_loss) <= 1e-2 * abs(ref_loss)
     got = _grads(md)
     for k in NAMES:

@@ -142,6 +142,89 @@ def test_straight_through_bf16_is_the_gradient_of_the_rounded_forward():
     assert abs(float(fd) - float((g16["head_w"] * v).sum())) < 1e-6
 
 
+def _bfn(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(torch.float64).numpy()
+
+
+def _step_backward_np(cell, x, g4, cl, fire, G, padding):
+    """One bf16 step and its backward written out in numpy loops, with the reference's bf16
+    backward rounding (g_dx, the fc1-output gradient and g_z rounded to bf16; engine/triton_mlp.py
+    46-78): an independent statement of what `grad_round` must compute. B = 1."""
+    K = _bfn(cell.kernels.double().numpy().reshape(-1, 3, 3))        # (4, 3, 3)
+    W1, b1 = _bfn(cell.w1.double().numpy()), _bfn(cell.b1.double().numpy())
+    W2, b2 = _bfn(cell.w2.double().numpy()), _bfn(cell.b2.double().numpy())
+    x = x.double().numpy()[0]                                         # (C, H, W)
+    C, H, W = x.shape
+    nk = K.shape[0]
+    pv = cell.pad_vec.double().numpy()
+    xp = np.zeros((C, H + 2, W + 2))
+    for c in range(C):
+        for i in range(-1, H + 1):
+            for j in range(-1, W + 1):
+                inside = 0 <= i < H and 0 <= j < W
+                if inside or padding == "wrap":
+                    xp[c, i + 1, j + 1] = x[c, i % H, j % W]
+                else:
+                    xp[c, i + 1, j + 1] = pv[c] if padding == "wall" else 0.0
+    xp = _bfn(xp)
+    z = np.zeros((nk * C, H, W))
+    for k in range(nk):
+        for c in range(C):
+            for i in range(H):
+                for j in range(W):
+                    z[k * C + c, i, j] = sum(K[k, a, b] * xp[c, i + a, j + b] for a in range(3) for b in range(3))
+    z = _bfn(z)
+    rows = z.reshape(nk * C, H * W).T                                 # (cells, F)
+    hpre = _bfn(rows @ W1.T + b1)
+    h = np.maximum(hpre, 0.0)
+    dx = _bfn(h @ W2.T + b2)                                          # (cells, C)
+    f = fire.double().numpy().reshape(H * W)
+    g = G.double().numpy()[0].reshape(C, H * W).T.copy()              # (cells, C)
+    gv = g4.numpy().reshape(H * W)
+    sl = slice(cell.in_offset, cell.in_offset + cell.c_in)
+    g[gv, sl] = 0.0                                                   # clamp backward
+    gdx = _bfn(g * f[:, None])
+    gh = _bfn(gdx @ W2) * (hpre > 0)
+    gz = _bfn(gh @ W1)                                                # (cells, F)
+    gx = g.T.reshape(C, H, W).copy()
+    gzp = gz.T.reshape(nk * C, H, W)
+    dK = np.zeros((nk, 3, 3))
+    gxp = np.zeros((C, H + 2, W + 2))
+    for k in range(nk):
+        for c in range(C):
+            for i in range(H):
+                for j in range(W):
+                    for a in range(3):
+                        for b in range(3):
+                            gxp[c, i + a, j + b] += K[k, a, b] * gzp[k * C + c, i, j]
+                            dK[k, a, b] += gzp[k * C + c, i, j] * xp[c, i + a, j + b]
+    for c in range(C):
+        for i in range(-1, H + 1):
+            for j in range(-1, W + 1):
+                if (0 <= i < H and 0 <= j < W) or padding == "wrap":
+                    gx[c, i % H, j % W] += gxp[c, i + 1, j + 1]
+    return {"x0": gx[None], "kernels": dK.reshape(nk, 1, 3, 3), "w1": gh.T @ rows, "b1": gh.sum(0), "w2": gdx.T @ h,
+            "b2": gdx.sum(0)}
+
+
+@pytest.mark.parametrize("padding", ["wall", "wrap"])
+def test_bf16_gradient_rounding_matches_a_written_out_backward(padding):
+    """`grad_round` (the reference's bf16 backward rounding points) against the numpy loops
+    above on one step with a final cotangent; the straight-through gradient differs from it
+    (the rounding points matter at this size)."""
+    cell, x, g4, cl, masks, targets, _ = _case(padding, size=5, rows=1, steps=1)
+    G = torch.randn(x.shape, generator=torch.Generator().manual_seed(3), dtype=torch.float64) * 0.3
+    _, got = O.bptt_chunk(cell, x, g4, cl, masks, targets, [0.0], "bf16", grad_x0=True,
+                          final_cotangent=G, grad_round=True)
+    _, ste = O.bptt_chunk(cell, x, g4, cl, masks, targets, [0.0], "bf16", grad_x0=True,
+                          final_cotangent=G)
+    ref = _step_backward_np(cell, x, g4, cl, masks[0], G, padding)
+    for k, v in ref.items():
+        g = got[k].numpy().reshape(v.shape)
+        assert np.abs(g - v).max() <= 1e-12 * max(1.0, np.abs(v).max()), k
+    assert any(float((ste[k] - got[k]).abs().max()) > 0 for k in ("w1", "kernels", "x0"))
+
+
 def test_replay_pool_sample_and_write_back():
     from ncas_amd.model import build_model
     from ncas_amd.train import ReplayPool
