@@ -285,20 +285,17 @@ constexpr int kFrontCh = 8;  // channels per front block (the channel count is a
 // gives g_dx = g_u * fire. The block adds its sums of g_dx (db2) into its slot; the blocks of
 // channel group 0 also add the loss and the head's weight / bias gradients. Every load of a cell
 // is issued before its arithmetic. n_out, c_out <= NO.
+// The front of cell range s, channel group cg (one workgroup): red and hwL in LDS.
 template <int NO>
-__global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
-    __shared__ float red[(kThreads / 64) * 32];
-    // the head's weights and bias in LDS: read in the loop next to the gradient stores, from global
-    // memory each read would wait behind them
-    __shared__ float hwL[NO * NO + NO];
+__device__ void front_body(const FrontArgs &a, int s, int cg, float *red, float *hwL) {
     const Dims &d = a.d;
     for (int i = threadIdx.x; i < d.n_out * d.c_out; i += kThreads) hwL[i] = a.head_w[i];
     for (int i = threadIdx.x; i < d.n_out; i += kThreads) hwL[NO * NO + i] = a.head_b[i];
     __syncthreads();
-    const int s = blockIdx.x, c0 = kFrontCh * blockIdx.y;
+    const int c0 = kFrontCh * cg;
     const int per = (int)((d.M + kSplit - 1) / kSplit), m0 = s * per;
     const int m1 = m0 + per < (int)d.M ? m0 + per : (int)d.M;
-    const bool head = blockIdx.y == 0;
+    const bool head = cg == 0;
     // small heads (n_out, c_out <= 4): the head's gradient sums kept in registers, hs[v NO + c] of
     // g_l[v] x1[out_off + c] and hs[NO NO + v] of g_l[v]
     constexpr bool kRegHead = NO <= 4;
@@ -435,6 +432,15 @@ __global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
             *pp = __fadd_rn(*pp, rh);
         }
     }
+}
+
+template <int NO>
+__global__ void __launch_bounds__(kThreads) front_kernel(FrontArgs a) {
+    __shared__ float red[(kThreads / 64) * 32];
+    // the head's weights and bias in LDS: read in the loop next to the gradient stores, from global
+    // memory each read would wait behind them
+    __shared__ float hwL[NO * NO + NO];
+    front_body<NO>(a, blockIdx.x, blockIdx.y, red, hwL);
 }
 
 // The perception input of tap (dy, dx) of cell (i, j) of row xr: the state (or the halo value
@@ -577,11 +583,9 @@ __device__ __forceinline__ void plane_z(const float *xs, const Dims &d, const fl
 // stencil_z for boards of at most kPlaneMax cells: workgroup p stages plane p = (row, channel)
 // of x in LDS and writes that channel's 4 features of the row's cells.
 template <bool Z16>
-__global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float *__restrict__ x,
-                                                            const float *__restrict__ kern,
-                                                            const float *__restrict__ padv, float *__restrict__ Z) {
-    extern __shared__ float xs[];  // HW floats
-    const int pl = blockIdx.x, row = pl / d.C, c = pl - row * d.C;
+__device__ void z_plane_body(const Dims &d, const float *__restrict__ x, const float *__restrict__ kern,
+                             const float *__restrict__ padv, float *__restrict__ Z, int pl, float *xs) {
+    const int row = pl / d.C, c = pl - row * d.C;
     const float *xr = x + (int64_t)pl * d.HW;
     // staged 8 cells per thread at a time, every load issued before the LDS writes
     for (int q0 = 0; q0 < d.HW; q0 += 8 * kThreads) {
@@ -600,6 +604,30 @@ __global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float 
     __syncthreads();
     const float hv = d.padding == 1 ? padv[c] : 0.0f;
     for (int q = threadIdx.x; q < d.HW; q += kThreads) plane_z<Z16>(xs, d, kern, hv, row, c, q, Z);
+}
+
+template <bool Z16>
+__global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float *__restrict__ x,
+                                                            const float *__restrict__ kern,
+                                                            const float *__restrict__ padv, float *__restrict__ Z) {
+    extern __shared__ float xs[];  // HW floats
+    z_plane_body<Z16>(d, x, kern, padv, Z, blockIdx.x, xs);
+}
+
+// The front (kSplit x C / 8 workgroups) and the bf16 z (rows x C workgroups) of one step in one
+// launch: they are independent, and each alone leaves most of the GPU idle.
+template <int NO>
+__global__ void __launch_bounds__(kThreads) front_z_kernel(FrontArgs a, const float *__restrict__ x,
+                                                           const float *__restrict__ kern,
+                                                           const float *__restrict__ padv, float *__restrict__ Z) {
+    extern __shared__ float xs[];  // HW floats (z workgroups)
+    __shared__ float red[(kThreads / 64) * 32];
+    __shared__ float hwL[NO * NO + NO];
+    const int nf = kSplit * (a.d.C / kFrontCh);
+    if ((int)blockIdx.x < nf)
+        front_body<NO>(a, (int)blockIdx.x % kSplit, (int)blockIdx.x / kSplit, red, hwL);
+    else
+        z_plane_body<true>(a.d, x, kern, padv, Z, (int)blockIdx.x - nf, xs);
 }
 
 // stencil_back for boards of at most kPlaneMax cells: workgroup p stages plane p = (row,
@@ -1146,14 +1174,20 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         fa.offHW = P.HW;
         fa.offHB = P.HB;
         const int no = d.n_out > d.c_out ? d.n_out : d.c_out;
-        auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
-        hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
-        // recompute z and h from the saved state
-        if (planes_ok) {
+        // recompute z (and, in the MLP stage, h) from the saved state
+        if (fused && planes_ok) {  // front and z in one launch
+            auto fz = no <= 4 ? front_z_kernel<4> : no <= 8 ? front_z_kernel<8> : front_z_kernel<16>;
+            hipLaunchKernelGGL(fz, dim3((unsigned)(kSplit * (d.C / kFrontCh) + d.rows * d.C)), dim3(kThreads),
+                               d.HW * sizeof(float), st, fa, xt, kern, padv, Z);
+        } else if (planes_ok) {
+            auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
+            hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
             auto zfn = fused ? stencil_z_plane<true> : stencil_z_plane<false>;
             hipLaunchKernelGGL(zfn, dim3((unsigned)(d.rows * d.C)), dim3(kThreads), d.HW * sizeof(float), st, d, xt, kern,
                                padv, Z);
         } else {
+            auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
+            hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
             const dim3 zgrid(grid_for((int64_t)d.C * d.HW), (unsigned)(d.rows < 65535 ? d.rows : 65535));
             hipLaunchKernelGGL(fused ? stencil_z_kernel<true> : stencil_z_kernel<false>, zgrid, dim3(kThreads), 0, st, d,
                                xt, kern, padv, Z);
