@@ -19,9 +19,10 @@ rollout in one launch). `--workload bptt30` times one training iteration: 64
 states sampled from a replay pool of 1,024 (30x30 DFS mazes, C=32 cell, bf16 forward with fp32
 master weights), a 32-step BPTT chunk with the per-cell cross-entropy on the 2-class path
 targets, AdamW, write-back; it reports cell-steps/s and the peak activation memory. Its roofline
-prices 4x the forward FLOPs per cell-step against the fp32 peak (the gradients are fp32
-arithmetic) and also reports the same rate against the bf16 peak (frac_of_bf16_peak): the
-backward's products run on bf16 MFMA as exact three-part splits of the fp32 operands.
+prices 4x the forward FLOPs per cell-step against the dense MFMA peak of the chunk's compute
+type (bf16: the forward and every product of the backward run on bf16 MFMA, the backward with
+the reference's bf16 gradient rounding points), with the same rate against the fp32 peak beside
+it (frac_of_fp32_peak).
 
 value = rows * H * W * D * steps / wall seconds (cell-updates/s). The roofline block prices the
 rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) per cell-update, the
@@ -275,7 +276,7 @@ def run_bptt(wl, precision, steps, warmup):
     res = eng.last_chunk
     return {
         "value": rate, "ms_per_step": wall / steps * 1e3, "kernel_ms": None,
-        "kernel_rate": rate, "achieved_tflops": tflops, "frac": tflops / PEAK_TFLOPS["fp32"],
+        "kernel_rate": rate, "achieved_tflops": tflops,
         "rows": wl["batch"], "loss": [float(v) for v in losses],
         "peak_activation_bytes": int(peak),
         "states_bytes": res.states_bytes, "workspace_bytes": res.workspace_bytes,
@@ -341,12 +342,10 @@ def main():
             "config": {"workload": wl["desc"], "rows": res["rows"], "grid": [30, 30],
                        "depth": wl["depth"]},
             "roofline": {"bound": "mfma", "achieved": res["achieved_tflops"],
-                         "peak": PEAK_TFLOPS["fp32"], "unit": "TFLOP/s", "frac": res["frac"],
+                         "peak": PEAK_TFLOPS[args.precision], "unit": "TFLOP/s",
+                         "frac": res["achieved_tflops"] / PEAK_TFLOPS[args.precision],
                          "traffic": None,
-                         # the gradients are fp32 arithmetic, but their products run on bf16
-                         # MFMA as exact three-part splits of the fp32 operands (and the
-                         # forward is bf16): the same rate against the bf16 dense peak
-                         "frac_of_bf16_peak": res["achieved_tflops"] / PEAK_TFLOPS["bf16"]},
+                         "frac_of_fp32_peak": res["achieved_tflops"] / PEAK_TFLOPS["fp32"]},
             "peak_activation_bytes": res["peak_activation_bytes"],
             "states_bytes": res["states_bytes"], "workspace_bytes": res["workspace_bytes"],
             "loss": res["loss"],
