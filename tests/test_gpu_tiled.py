@@ -253,3 +253,29 @@ def test_wave_tile_kernel_equals_window_kernel_bitwise(H, W, B, padding):
             out[path] = (y, f, y1, f1)
         for a, b in zip(out[2], out[3]):
             assert torch.equal(a, b), kwr
+
+
+def test_wave_tile_kernel_guard_for_more_than_2_to_26_cells():
+    """The wave-per-tile kernel addresses the cell-major state with 32-bit byte offsets; calls
+    with rows * H * W * 64 >= 2^32 (1,664 boards of 201x201, 4.3 GB per state) take the
+    halo-window kernel instead. The last boards of such a call equal the same boards run alone
+    (on the wave-per-tile kernel) bit for bit, over two steps (the second reads the cell-major
+    workspace)."""
+    B, H, W = 1664, 201, 201
+    assert B * H * W * 64 >= 2**32
+    _say("offset guard", B, H, W)
+    m = perturbed_model("maze_c16", 2, *DYN["maze_c16"])
+    md = copy.deepcopy(m).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    with torch.no_grad():
+        x = torch.randn((B, 16, H, W), generator=g, device=DEV) * 0.3
+        g4 = torch.rand((B, 1, H, W), generator=g, device=DEV) < 0.3
+        cl = torch.randn((B, m.cfg.c_in, H, W), generator=g, device=DEV)
+        y, _, _ = rollout_steps(md, x, g4, cl, 2, seed=5, row0=3, p_fire=0.5, precision="bf16",
+                                want_conf=False)
+        tail = slice(B - 2, B)
+        y2, _, _ = rollout_steps(md, x[tail].contiguous(), g4[tail].contiguous(), cl[tail].contiguous(), 2,
+                                 seed=5, row0=3 + B - 2, p_fire=0.5, precision="bf16", want_conf=False)
+        assert torch.equal(y[tail], y2)
+        del x, y
+        torch.cuda.empty_cache()
