@@ -228,6 +228,7 @@ def run_gpu(wl, precision, steps, warmup, window_steps=0):
         "frac": tflops / PEAK_TFLOPS[precision],
         "best_first": best[:4].tolist(),
         "rows": rows,
+        "cell_updates": cell_updates,
     }
 
 
@@ -283,20 +284,39 @@ def run_bptt(wl, precision, steps, warmup):
     }
 
 
+# LDS ceiling of the streamed C=64 kernel (9x9 bf16): per 16-cell tile its waves read 70 KB
+# from LDS (the stencil's taps, Z four times, H twice, the state) and write 22 KB (Z, H, the state
+# and its bf16 copy); gfx950's LDS serves 256 B/cycle of conflict-free ds_read_b128 and 80 B/cycle
+# of ds_write_b128 / b64 per CU (measured), at the 2.4 GHz peak clock of the MFMA figure.
+LDS_CYCLES_PER_CELL_STREAM64 = (70 * 1024 / 256 + 22 * 1024 / 80) / 16
+CLOCK_HZ = 2.4e9
+N_CU = 256
+
+
 def roofline(name, wl, precision, res):
-    """Binding ceiling of the workload's dominant kernel: MFMA FLOPs for the resident kernels
-    (sudoku9, hardmaze30); the lower of MFMA FLOPs and HBM bytes for the per-step path (maze201)."""
+    """Binding ceiling of the workload's dominant kernel: the lowest of its MFMA (FLOPs), LDS
+    (the streamed C=64 kernel's own LDS traffic) and HBM (algorithmic bytes) ceilings, each in
+    cell-updates/s; MFMA for the resident kernels (sudoku9, hardmaze30, maze13), the lower of
+    MFMA and HBM for the per-step path (maze201)."""
     flops = flop_per_cell_update(wl["preset"])
     mfma_ceiling = PEAK_TFLOPS[precision] * 1e12 / flops
     block = {"bound": "mfma", "achieved": res["achieved_tflops"], "peak": PEAK_TFLOPS[precision],
              "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic_from_profiles(name, precision)}
+    ceilings = {"unit": "cell-updates/s", "mfma": mfma_ceiling, "lds": None, "hbm": None}
+    if name == "sudoku9" and precision == "bf16":
+        ceilings["lds"] = N_CU * CLOCK_HZ / LDS_CYCLES_PER_CELL_STREAM64
     if name == "maze201":
         nbytes = hbm_bytes_per_cell_update(wl["preset"])
         hbm_ceiling = PEAK_HBM_GBS * 1e9 / nbytes
+        ceilings["hbm"] = hbm_ceiling
         if hbm_ceiling < mfma_ceiling:
             gbs = res["kernel_rate"] * nbytes / 1e9
             block.update(bound="hbm", achieved=gbs, peak=PEAK_HBM_GBS, unit="GB/s",
                          frac=gbs / PEAK_HBM_GBS)
+    elif block["traffic"]:
+        # the resident kernels touch HBM once per launch: the measured bytes per cell-update
+        ceilings["hbm"] = PEAK_HBM_GBS * 1e9 / (block["traffic"] / res["cell_updates"])
+    block["ceilings"] = ceilings
     return block
 
 
