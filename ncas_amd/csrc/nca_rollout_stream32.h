@@ -55,8 +55,15 @@
 // LDS layouts (conflict-free for the access patterns here on gfx950's 64 banks):
 //   * M: 128 B per cell; 16-lane groups read or write two cells x 8 quads;
 //   * Z: 256 B per tile row (features in quad-major order 16 quad + 4 kernel + ch), 16-byte chunk c
-//     of row r stored at chunk c ^ zsw(r), zsw(r) = (r & 8) | (r & 3) << 1 | (r >> 2 & 1);
+//     of row r stored at chunk c ^ zsw(r);
 //   * D: per partial 16 rows of 128 B (32 fp32), chunk c of row r stored at c ^ (r >> 1 & 7).
+// gfx950 serves a ds_read_b128 in four cycles of 16 lanes: lanes 0-3 and 12-15 of a 16-lane group
+// with lanes 4-11 of the next group (groups 0/1 and 2/3), then the remaining 16; the 16 lanes of a
+// cycle must read distinct 16-byte slots of the 256-byte bank row (measured: a two-way conflict in
+// those sets doubles the instruction's 4 cycles). zsw maps rows 0-3, 12-15 to 0-7 and rows 4-11 to
+// 8-15 and keeps bit 0 of the chunk free, so the hidden waves' operand loads (group g reads chunk
+// 4 kt + g of rows 0-15) fill each cycle's 16 slots; the stencil's stores of 8 rows x 4 chunks still
+// meet every slot twice.
 #pragma once
 
 #include "nca_stream_util.h"
@@ -121,8 +128,11 @@ struct St32Params {
     unsigned off_w1q, off_w2k;
 };
 
-// zsw: the Z row swizzle (a permutation of 0..15)
-__device__ __forceinline__ unsigned zsw(unsigned r) { return (r & 8u) | ((r & 3u) << 1) | ((r >> 2) & 1u); }
+// zsw: the Z row swizzle (a permutation of 0..15): bits 1-2 from r & 3, bit 0 = r >> 3, bit 3 = bit 2
+// of r xor bit 3 of r
+__device__ __forceinline__ unsigned zsw(unsigned r) {
+    return ((r & 3u) << 1) | ((r >> 3) & 1u) | ((((r >> 2) ^ (r >> 3)) & 1u) << 3);
+}
 
 // GATED: confidence-gated firing (a.adaptive), compiled out of the plain kernel
 // REC: also write the state after every step to a.x_rec (the BPTT chunk's forward).
@@ -385,8 +395,9 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             }
         };
         // gated firing: the update lanes decide a cell's mask for the step from its state at the
-        // step's start (the output quad of M before the update, read by all 8 lanes of the cell);
-        // the head (at most 4 outputs over at most 4 channels) is held in registers
+        // step's start (the output quad of M before the update, read by all 8 lanes of the cell:
+        // 8 cycles, cheaper than one lane's decision handed on by a ballot); the head (at most 4
+        // outputs over at most 4 channels) is held in registers
         const int oqi = a.out_off >> 2;
         const bool oq = GATED && q8 == oqi;
         float hw4[4][4], hb4[4];
@@ -590,7 +601,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 const int qc = cbU + cl - (nxt ? HWn : 0);
                 unsigned fbit = fb & 1u;
                 if (GATED) {
-                    // every lane of the cell makes the same decision from the same values
+                    // the output-quad lane's decision (its m4 is the output quad) to all 8 lanes
                     const float xq[4] = {mo4.x, mo4.y, mo4.z, mo4.w};
                     const unsigned f = gated_fire(xq, fb) ? 1u : 0u;
                     fbit = f;
