@@ -23,22 +23,30 @@
 // that each later product finds its operand in registers: D[cell 4g + i][hidden r] of two cell
 // tiles is an operand whose k runs over 8 cells in the order perm(g, j) = j < 4 ? 4g + j :
 // 16 + 4g + j - 4; the LDS operands of those products use the same cell order. g_z sums over all
-// hidden units, so g_a goes through LDS (hidden units of each 32-block in the same perm order)
-// and wave w computes g_z for features [16w, 16w + 16) of the tile's 32 cells, with its W1^T
-// fragments (8 KB) held in registers.
+// hidden units, so g_a goes through LDS and wave w computes g_z for features [16w, 16w + 16) of
+// the tile's 32 cells, with its W1^T fragments (8 KB) held in registers.
 //
 // Per tile: the tile's z and g_dx (prefetched into registers during the previous tile) are stored
 // to LDS; barrier; fc1, g_a, g_a to LDS, dW2 and dW1; barrier; g_z.
 //
-// LDS, rows padded by one 16-byte chunk (row strides of 17, 5 and 33 chunks) so that 8
-// consecutive lanes of a 16-byte access to 8 consecutive rows touch distinct chunks of the 64
-// banks, and every address in the tile loop is a per-lane base plus a constant:
-//   ZA   z [cell 32][feature 128] bf16, 272-byte rows
-//   ZB   z [feature 128][cell 32 in perm order] bf16, 80-byte rows
-//   GA   g_dx [cell 32][channel 32] bf16, 80-byte rows
-//   GB   g_dx [channel 32][cell 32 in perm order] bf16, 80-byte rows
-//   GAL  g_a [cell 32][hidden 256, perm order in each 32-block] bf16, 528-byte rows
+// LDS: every buffer is k-major with the cells of a row contiguous, in rows of 64 bytes (32 bf16)
+// whose 16-byte chunk c sits at chunk c ^ ((row >> 1) & 3):
+//   ZB   z [feature 128][cell 32 in perm order]
+//   GB   g_dx [channel 32][cell 32 in perm order]
+//   GL   g_a [hidden 256][cell 32]
 //   B1   b1 fp32
+// An operand whose k runs along the rows (z and g_dx for fc1 and g_a, with k over features and
+// channels; g_a for g_z, with k over hidden units) is read with ds_read_b64_tr_b16, which within
+// each 16-lane group gives lane i element i & 3 of the 8-byte loads of lanes 4m + (i >> 2),
+// m < 4: lane 4m + s loads cells 4s .. 4s+3 of k-row m, so lane i receives cell i of k-rows
+// 0..3; two such loads make an 8-element operand. The tile's stores are then whole 16-byte chunks
+// (z and g_dx as loaded, 8 cells of one row) and 8-byte pieces (g_a, 4 cells of one hidden unit),
+// where a [cell][k] layout took a 2-byte store per element. The row swizzle makes the 16-byte
+// operand reads (lane (r, g): chunk g of row r) conflict-free for gfx950's ds_read_b128, which
+// serves lanes 0-3 and 12-15 of one 16-lane group with lanes 4-11 of the next in one cycle, and
+// the transposed reads of g_a take the 2.6 cycles of a plain ds_read_b64; those of z and g_dx take
+// 4 (measured with a probe replaying each access pattern from 8 waves). Every address in the
+// tile loop is a per-lane base plus a constant.
 #pragma once
 
 #include "nca_stream_util.h"
@@ -57,9 +65,8 @@ struct MlpBackArgs {
 };
 
 struct Mb32 {
-    static constexpr unsigned ZAR = 272, ZBR = 80, GR = 80, AR = 528;  // row strides
-    static constexpr unsigned ZA = 0, ZB = ZA + 32 * ZAR, GA = ZB + 128 * ZBR, GB = GA + 32 * GR,
-                              GAL = GB + 32 * GR, B1 = GAL + 32 * AR, TOTAL = B1 + 1024;
+    static constexpr unsigned RS = 64;  // bytes per LDS row: 32 bf16
+    static constexpr unsigned ZB = 0, GB = ZB + 128 * RS, GL = GB + 32 * RS, B1 = GL + 256 * RS, TOTAL = B1 + 1024;
     // weight image: per (wave, lane) the W1 fragments [ht][kb], the W2 fragments [ht] and the
     // W1^T fragments [kb], 16 bytes each
     static constexpr unsigned IMG_W1F = 0, IMG_W2F = IMG_W1F + 512 * 8 * 16, IMG_W1TF = IMG_W2F + 512 * 2 * 16,
@@ -80,6 +87,19 @@ __device__ __forceinline__ bf16x8 mb_pack8(const float v[8]) {
     return __builtin_bit_cast(bf16x8, u);
 }
 __device__ __forceinline__ int mb_perm(int g, int j) { return j < 4 ? 4 * g + j : 16 + 4 * g + j - 4; }
+// byte offset of 16-byte chunk c of LDS row `row`
+__device__ __forceinline__ unsigned mb_off(unsigned row, unsigned c) { return row * Mb32::RS + 16u * (c ^ ((row >> 1) & 3u)); }
+// ds_read_b64_tr_b16 at byte offset off of the LDS
+__device__ __forceinline__ s16x4 mb_ldtr(const unsigned char *s, unsigned off) {
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4 *)((__attribute__((address_space(3))) const unsigned char *)s + off));
+}
+// the 8-element operand of two transposed loads (k-rows 0-3, then 4-7)
+__device__ __forceinline__ bf16x8 mb_cat(s16x4 lo, s16x4 hi) {
+    const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+    return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
 
 // The weight image of mlp_back32 from the fp32 master weights (rounded to bf16): the register
 // fragments of every (wave, lane): W1 for fc1, W2 for g_a, and W1^T for g_z (the A operand of
@@ -217,22 +237,27 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         load8z(m0, pz);
         if (w < 2) load8(gb, m0, pg);
     };
-    auto store_tile = [&](int64_t m0) {
+    const unsigned o_st = mb_off((unsigned)lrow, (unsigned)q);
+    auto store_tile = [&](int64_t m0) {  // ZB (GB) row lrow chunk q: cells perm(q, 0..7)
         zero_past(m0, pz);
         if (w < 2) zero_past(m0, pg);
-        // ZB row lrow chunk q; ZA column lrow of rows perm(q, j)
-        *reinterpret_cast<bf16x8 *>(smem + S::ZB + lrow * S::ZBR + 16 * q) = mb_pack8(pz);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            *reinterpret_cast<__bf16 *>(smem + S::ZA + mb_perm(q, j) * S::ZAR + 2 * lrow) = (__bf16)pz[j];
-        if (w < 2) {  // GB row lrow chunk q; GA column lrow of rows perm(q, j)
-            const bf16x8 pv = mb_pack8(pg);
-            *reinterpret_cast<bf16x8 *>(smem + S::GB + lrow * S::GR + 16 * q) = pv;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                *reinterpret_cast<__bf16 *>(smem + S::GA + mb_perm(q, j) * S::GR + 2 * lrow) = pv[j];
-        }
+        *reinterpret_cast<bf16x8 *>(smem + S::ZB + o_st) = mb_pack8(pz);
+        if (w < 2) *reinterpret_cast<bf16x8 *>(smem + S::GB + o_st) = mb_pack8(pg);
     };
+    // per-lane LDS offsets of the tile loop. Transposed operand loads: lane 4m + s of the group
+    // loads cells 4s .. 4s+3 of k-row 8g + m (fc1, g_a; +4 for k-rows 4-7), in perm order chunk s,
+    // half ct; for g_z cells 16ct + 4s .. +3 (chunk 2ct + s / 2, half s & 1) of hidden row
+    // 4g + m (+16 for k-rows 4-7) of each 32-block
+    const unsigned tm = (unsigned)r >> 2, ts = (unsigned)r & 3u;
+    const unsigned o_tr0 = mb_off(8u * g + tm, ts), o_tr1 = mb_off(8u * g + 4u + tm, ts);
+    unsigned o_gl[2][2];  // [ct][k-rows 0-3 / 4-7]
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        o_gl[ct][0] = mb_off(4u * g + tm, 2u * ct + (ts >> 1)) + 8u * (ts & 1u);
+        o_gl[ct][1] = mb_off(4u * g + 16u + tm, 2u * ct + (ts >> 1)) + 8u * (ts & 1u);
+    }
+    // 16-byte operand loads: chunk g of row r (+16 rows per tile or feature block)
+    const unsigned o_rg = mb_off((unsigned)r, (unsigned)g);
 
     const int ntile = (int)((mb1 - mb0 + 31) / 32);
     load_tile(mb0);
@@ -251,11 +276,12 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         // operands of fc1 read up front; those of g_a while fc1 finishes
         bf16x8 zf[4][2], gf[2];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const unsigned zo = S::ZA + r * S::ZAR + 16 * (4 * kb + g);
-            zf[kb][0] = mb_ld(smem, zo);
-            zf[kb][1] = mb_ld(smem, zo + 16 * S::ZAR);
-        }
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const unsigned zo = S::ZB + 32u * S::RS * kb + 8u * ct;  // k-rows 32 kb + 8g + m
+                zf[kb][ct] = mb_cat(mb_ldtr(smem, zo + o_tr0), mb_ldtr(smem, zo + o_tr1));
+            }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
@@ -267,7 +293,8 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) gf[ct] = mb_ld(smem, S::GA + (16 * ct + r) * S::GR + 16 * g);
+        for (int ct = 0; ct < 2; ++ct)
+            gf[ct] = mb_cat(mb_ldtr(smem, S::GB + 8u * ct + o_tr0), mb_ldtr(smem, S::GB + 8u * ct + o_tr1));
         __builtin_amdgcn_sched_barrier(0);
         {
             const float *b1L = reinterpret_cast<const float *>(smem + S::B1);
@@ -311,14 +338,16 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
                                 gaT[1][ht][0], gaT[1][ht][1], gaT[1][ht][2], gaT[1][ht][3]};
             ap[ht] = mb_pack8(v);
         }
-        // ... and into GAL for g_z: hidden offset o = 16ht + r of block w sits at chunk r >> 2,
-        // element 4ht + (r & 3) of the block's perm order
+        // ... and into GL for g_z: hidden row 32w + 16ht + r, cells 16ct + 4g .. +3 (chunk
+        // 2ct + g / 2, half g & 1): the ct halves of ap
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int cell = mb_perm(g, j);
-            const unsigned base = S::GAL + cell * S::AR + 16 * (4 * w + (r >> 2)) + 2 * (r & 3);
+        for (int ht = 0; ht < 2; ++ht) {
+            const uint4 u = __builtin_bit_cast(uint4, ap[ht]);
+            const unsigned row = 32u * (unsigned)w + 16u * ht + (unsigned)r;
 #pragma unroll
-            for (int ht = 0; ht < 2; ++ht) *reinterpret_cast<__bf16 *>(smem + base + 8 * ht) = ap[ht][j];
+            for (int ct = 0; ct < 2; ++ct)
+                *reinterpret_cast<uint2 *>(smem + S::GL + mb_off(row, 2u * ct + ((unsigned)g >> 1)) + 8u * (g & 1)) =
+                    ct ? make_uint2(u.z, u.w) : make_uint2(u.x, u.y);
         }
 
         // ---- dW2 += g_dx h^T: A = g_dx [channel][cells perm], B = h^T
@@ -332,7 +361,7 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             }
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
-                const bf16x8 gbv = mb_ld(smem, S::GB + (16 * ct + r) * S::GR + 16 * g);
+                const bf16x8 gbv = mb_ld(smem, S::GB + 16u * S::RS * ct + o_rg);
 #pragma unroll
                 for (int ht = 0; ht < 2; ++ht) dw2[ct][ht] = mb_mfma(gbv, hb[ht], dw2[ct][ht]);
             }
@@ -340,9 +369,8 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         // ---- dW1 += g_a z^T: A = g_a (hidden x cells perm), B = z [cells perm][feature]
 #pragma unroll
         for (int ft = 0; ft < 8; ft += 2) {
-            const int f0 = 16 * ft + r, f1 = f0 + 16;
-            const bf16x8 zb0 = mb_ld(smem, S::ZB + f0 * S::ZBR + 16 * g);
-            const bf16x8 zb1 = mb_ld(smem, S::ZB + f1 * S::ZBR + 16 * g);
+            const bf16x8 zb0 = mb_ld(smem, S::ZB + 16u * S::RS * ft + o_rg);  // feature 16 ft + r
+            const bf16x8 zb1 = mb_ld(smem, S::ZB + 16u * S::RS * (ft + 1) + o_rg);
 #pragma unroll
             for (int ht = 0; ht < 2; ++ht) {
                 dw1[ht][ft] = mb_mfma(ap[ht], zb0, dw1[ht][ft]);
@@ -359,10 +387,12 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             for (int x = 0; x < 2; ++x)
 #pragma unroll
                 for (int y = 0; y < 2; ++y) gz[x][y] = mb_f32x4{0.f, 0.f, 0.f, 0.f};
-            const unsigned bo = S::GAL + r * S::AR + 16 * g;
 #pragma unroll
             for (int kb = 0; kb < 8; ++kb) {
-                const bf16x8 B0 = mb_ld(smem, bo + 64 * kb), B1 = mb_ld(smem, bo + 16 * S::AR + 64 * kb);
+                // k = 8g + j over hidden units 32 kb + perm(g, j): rows 32 kb + 4g + m, then +16
+                const unsigned bo = S::GL + 32u * S::RS * kb;
+                const bf16x8 B0 = mb_cat(mb_ldtr(smem, bo + o_gl[0][0]), mb_ldtr(smem, bo + o_gl[0][1]));
+                const bf16x8 B1 = mb_cat(mb_ldtr(smem, bo + o_gl[1][0]), mb_ldtr(smem, bo + o_gl[1][1]));
                 gz[0][kb & 1] = mb_mfma(w1t[kb], B0, gz[0][kb & 1]);
                 gz[1][kb & 1] = mb_mfma(w1t[kb], B1, gz[1][kb & 1]);
             }
