@@ -186,7 +186,12 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
     const unsigned char *zb = reinterpret_cast<const unsigned char *>(a.Z);
     const unsigned char *gb = reinterpret_cast<const unsigned char *>(a.Gdx);
     const uint32_t rowb = (uint32_t)lrow * (uint32_t)M * 4u, rowz = (uint32_t)lrow * (uint32_t)M * 2u;
-    float pz[8], pg[8];
+    // z arrives as raw bf16 words, kept unconverted until the tile is stored: any use at the load
+    // would make the compiler wait for it there. VEC: pzv[h] = cells perm(q, 4h .. 4h+3);
+    // otherwise pzs[j] = cell perm(q, j) in the low 16 bits
+    uint2 pzv[2];
+    uint32_t pzs[8];
+    float pg[8];
     auto load8 = [&](const unsigned char *base, int64_t m0, float v[8]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -208,23 +213,18 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
             }
         }
     };
-    auto load8z = [&](int64_t m0, float v[8]) {  // z: bf16
+    auto load8z = [&](int64_t m0) {  // z: bf16
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int64_t m = m0 + 16 * h + 4 * q;
             if (VEC) {
                 const bool ok = m < mb1;
-                const uint2 x = *reinterpret_cast<const uint2 *>(zb + rowz + (uint32_t)(ok ? m : mb0) * 2u);
-                v[4 * h] = __uint_as_float(x.x << 16);
-                v[4 * h + 1] = __uint_as_float(x.x & 0xffff0000u);
-                v[4 * h + 2] = __uint_as_float(x.y << 16);
-                v[4 * h + 3] = __uint_as_float(x.y & 0xffff0000u);
+                pzv[h] = *reinterpret_cast<const uint2 *>(zb + rowz + (uint32_t)(ok ? m : mb0) * 2u);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const bool ok = m + e < mb1;
-                    const uint32_t u = *reinterpret_cast<const uint16_t *>(zb + rowz + (uint32_t)(ok ? m + e : mb0) * 2u);
-                    v[4 * h + e] = __uint_as_float(u << 16);
+                    pzs[4 * h + e] = *reinterpret_cast<const uint16_t *>(zb + rowz + (uint32_t)(ok ? m + e : mb0) * 2u);
                 }
             }
         }
@@ -234,15 +234,24 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
         for (int j = 0; j < 8; ++j) v[j] = m0 + mb_perm(q, j) < mb1 ? v[j] : 0.0f;
     };
     auto load_tile = [&](int64_t m0) {
-        load8z(m0, pz);
+        load8z(m0);
         if (w < 2) load8(gb, m0, pg);
     };
     const unsigned o_st = mb_off((unsigned)lrow, (unsigned)q);
     auto store_tile = [&](int64_t m0) {  // ZB (GB) row lrow chunk q: cells perm(q, 0..7)
-        zero_past(m0, pz);
-        if (w < 2) zero_past(m0, pg);
-        *reinterpret_cast<bf16x8 *>(smem + S::ZB + o_st) = mb_pack8(pz);
-        if (w < 2) *reinterpret_cast<bf16x8 *>(smem + S::GB + o_st) = mb_pack8(pg);
+        uint32_t zw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t v = VEC ? ((e & 1) ? pzv[e >> 1].y : pzv[e >> 1].x) : (pzs[2 * e] | (pzs[2 * e + 1] << 16));
+            if (m0 + mb_perm(q, 2 * e) >= mb1) v &= 0xffff0000u;  // cells past the range
+            if (m0 + mb_perm(q, 2 * e + 1) >= mb1) v &= 0x0000ffffu;
+            zw[e] = v;
+        }
+        *reinterpret_cast<uint4 *>(smem + S::ZB + o_st) = make_uint4(zw[0], zw[1], zw[2], zw[3]);
+        if (w < 2) {
+            zero_past(m0, pg);
+            *reinterpret_cast<bf16x8 *>(smem + S::GB + o_st) = mb_pack8(pg);
+        }
     };
     // per-lane LDS offsets of the tile loop. Transposed operand loads: lane 4m + s of the group
     // loads cells 4s .. 4s+3 of k-row 8g + m (fc1, g_a; +4 for k-rows 4-7), in perm order chunk s,
@@ -259,8 +268,17 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
     // 16-byte operand loads: chunk g of row r (+16 rows per tile or feature block)
     const unsigned o_rg = mb_off((unsigned)r, (unsigned)g);
 
+    // g_z's buffer (below 2^31 bytes, checked by the host); the third dword is gfx9's format word
+    const __amdgpu_buffer_rsrc_t gz_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(a.Gz, (short)0, (int)(M * 128 * 2), 0x00020000);
     const int ntile = (int)((mb1 - mb0 + 31) / 32);
     load_tile(mb0);
+    // the first tile's loads complete here, so that the loop's wait for each prefetch counts the
+    // previous tile's stores issued after it (else the first iteration's state, with no stores
+    // behind the loads, makes every iteration wait for them as well)
+    if (VEC) asm volatile("" : : "v"(pzv[0]), "v"(pzv[1]));
+    else asm volatile("" : : "v"(pzs[0]), "v"(pzs[7]));
+    if (w < 2) asm volatile("" : : "v"(pg[0]), "v"(pg[7]));
     for (int t = 0; t < ntile; ++t) {
         const int64_t m0 = mb0 + 32 * (int64_t)t;
         store_tile(m0);
@@ -396,16 +414,18 @@ __global__ void __launch_bounds__(512, 1) mlp_back32(MlpBackArgs a) {
                 gz[0][kb & 1] = mb_mfma(w1t[kb], B0, gz[0][kb & 1]);
                 gz[1][kb & 1] = mb_mfma(w1t[kb], B1, gz[1][kb & 1]);
             }
-            unsigned char *gzb = reinterpret_cast<unsigned char *>(a.Gz);
+            // raw buffer stores: a lane past the range gets an offset beyond the buffer, whose
+            // store the hardware drops, so the stores need no branch (a branch around them
+            // leaves their number unknown to the next tile's wait for its prefetched loads)
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
                 const int64_t m = m0 + 16 * ct + r;
-                if (m < mb1) {
-                    const uint32_t o0 = ((uint32_t)(16 * w + 4 * g) * (uint32_t)M + (uint32_t)m) * 2u;
+                const uint32_t o0 = ((uint32_t)(16 * w + 4 * g) * (uint32_t)M + (uint32_t)m) * 2u;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        *reinterpret_cast<__bf16 *>(gzb + o0 + (uint32_t)i * (uint32_t)M * 2u) =
-                            (__bf16)__fadd_rn(gz[ct][0][i], gz[ct][1][i]);
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t off = m < mb1 ? o0 + (uint32_t)i * (uint32_t)M * 2u : 0x80000000u;
+                    const __bf16 v = (__bf16)__fadd_rn(gz[ct][0][i], gz[ct][1][i]);
+                    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), gz_rsrc, off, 0, 0);
                 }
             }
         }
