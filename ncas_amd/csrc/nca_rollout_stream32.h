@@ -128,11 +128,8 @@ struct St32Params {
     unsigned off_w1q, off_w2k;
 };
 
-// zsw: the Z row swizzle (a permutation of 0..15): bits 1-2 from r & 3, bit 0 = r >> 3, bit 3 = bit 2
-// of r xor bit 3 of r
-__device__ __forceinline__ unsigned zsw(unsigned r) {
-    return ((r & 3u) << 1) | ((r >> 3) & 1u) | ((((r >> 2) ^ (r >> 3)) & 1u) << 3);
-}
+// zsw: the Z row swizzle (a permutation of 0..15)
+__device__ __forceinline__ unsigned zsw(unsigned r) { return row_swz16(r); }
 
 // GATED: confidence-gated firing (a.adaptive), compiled out of the plain kernel
 // REC: also write the state after every step to a.x_rec (the BPTT chunk's forward).

@@ -12,10 +12,13 @@
 // inside it (the border holds the padding value on board-edge sides). The core of every window
 // is the board split into nwy x nwx near-equal rectangles, so every cell is written once.
 //
-// LDS: the fp32 state M (64 B per cell, read and written only by the cell's own lanes, updated
-// in place), the bf16 perception copy P twice (P_cur read by the stencils of a step, P_next
-// written by its updates; 32 B per cell, window plus border), the given flags, b1, and per wave
-// one 4352-byte staging block for z (16 x 144 B) and then h (16 x 272 B).
+// LDS: the fp32 state M (four planes of 16 B per cell, one per channel quad, each plane 256-byte
+// aligned, so that a tile's 16 cells fill the 16 slots of a bank row; read and written only by the
+// cell's own lanes, updated in place), the bf16 perception copy P twice (P_cur read by the
+// stencils of a step, P_next written by its updates; 32 B per cell, window plus border), the
+// given flags, and per wave one 4096-byte staging block for z (16 rows of 128 B) and then h (16
+// rows of 256 B), whose 16-byte chunks are permuted per row (row_swz8, row_swz16) so that the
+// MFMA operand reads are conflict-free. b1 lives in registers.
 //
 // Each cell of a step is computed exactly like the per-step kernel (step_stream16): lane
 // (r = lane & 15, g = lane >> 4) of a 16-cell tile (a row segment of the computed region) owns
@@ -35,11 +38,15 @@ constexpr int kWinMax = 30;                   // window edge in cells, halo incl
 constexpr int kWinStride = kWinMax + 2;       // P row stride in cells: window plus border ring
 constexpr int kWinMaxT = 8;                   // steps per launch (the halo width)
 constexpr unsigned kWinPBytes = kWinStride * kWinStride * 32;  // one bf16 perception copy
-constexpr unsigned kWinMBytes = kWinMax * kWinMax * 64;        // fp32 state
+constexpr unsigned kWinMPlane = (kWinMax * kWinMax * 16 + 255) & ~255u;  // one channel quad of the state
+constexpr unsigned kWinMBytes = 4 * kWinMPlane;                           // fp32 state
 constexpr unsigned kWinGBytes = (kWinMax * kWinMax + 15) & ~15u;
-constexpr unsigned kWinStage = 16 * 272;      // per wave: z (16 x 144 B), then h (16 x 272 B)
+constexpr unsigned kWinStage = 16 * 256;      // per wave: z (16 x 128 B), then h (16 x 256 B)
 constexpr int kWinWaves = 8;
-constexpr unsigned kWinLds = 2 * kWinPBytes + kWinMBytes + kWinGBytes + kWinWaves * kWinStage + 128 * 4;
+constexpr unsigned kWinLds = 2 * kWinPBytes + kWinMBytes + kWinGBytes + kWinWaves * kWinStage;
+// staging offsets: chunk c of z row r, of h row r
+__device__ __forceinline__ unsigned win_zoff(unsigned r, unsigned c) { return r * 128u + 16u * (c ^ row_swz8(r)); }
+__device__ __forceinline__ unsigned win_hoff(unsigned r, unsigned c) { return r * 256u + 16u * (c ^ row_swz16(r)); }
 
 struct Win16Params {
     RolloutParams a;        // x_in -> x_out of the launch
@@ -81,7 +88,6 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
     unsigned char *M = win_lds + 2 * kWinPBytes;
     unsigned char *G = M + kWinMBytes;
     unsigned char *stage = G + kWinGBytes;
-    float *b1L = reinterpret_cast<float *>(stage + kWinWaves * kWinStage);
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int H = a.H, W = a.W, HWn = H * W;
@@ -117,7 +123,9 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
     for (int kt = 0; kt < 4; ++kt) w2f[kt] = reinterpret_cast<const bf16x8 *>(a.packed + a.off_w2)[(size_t)kt * 64 + lane];
     const float *b1 = reinterpret_cast<const float *>(a.packed + a.off_b1);
     const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
-    if (tid < HD) b1L[tid] = b1[tid];
+    float4 b1v[8];  // fc1's initial accumulators: hidden units 16 mt + 4g .. +3
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) b1v[mt] = *reinterpret_cast<const float4 *>(b1 + 16 * mt + 4 * g);
     float b2v[4];
     bool insl[4];
 #pragma unroll
@@ -146,7 +154,7 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
             } else {
                 v = *reinterpret_cast<const float4 *>(a.x_in + (row * HWn + cell) * C + 4 * q);
             }
-            lds_st128f(M, (unsigned)(c * 64 + 16 * q), v);
+            lds_st128f(M, (unsigned)q * kWinMPlane + (unsigned)c * 16u, v);
             lds_st64(P0, (unsigned)(((wy + 1) * kWinStride + wx + 1) * 32 + 8 * q),
                      uint2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)});
             if (q == 0) G[c] = a.given[row * HWn + cell];
@@ -262,34 +270,34 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
                             sacc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), sacc, false);
                         z[c] = sacc;
                     }
-                    *reinterpret_cast<uint2 *>(zw + r * 144 + 2 * (k * C + 4 * g)) =
+                    // features 16k + 4g .. +3: chunk 2k + g / 2, half g & 1
+                    *reinterpret_cast<uint2 *>(zw + win_zoff(r, 2 * k + (g >> 1)) + 8 * (g & 1)) =
                         uint2{pack_bf16x2(z[0], z[1]), pack_bf16x2(z[2], z[3])};
                 }
             }
             // 3. fc1
             __builtin_amdgcn_wave_barrier();
-            const bf16x8 zf0 = *reinterpret_cast<const bf16x8 *>(zw + r * 144 + 16 * g);
-            const bf16x8 zf1 = *reinterpret_cast<const bf16x8 *>(zw + r * 144 + 64 + 16 * g);
+            const bf16x8 zf0 = *reinterpret_cast<const bf16x8 *>(zw + win_zoff(r, g));
+            const bf16x8 zf1 = *reinterpret_cast<const bf16x8 *>(zw + win_zoff(r, 4 + g));
             typedef float w16_f32x4 __attribute__((ext_vector_type(4)));
             w16_f32x4 h[8];
 #pragma unroll
             for (int mt = 0; mt < 8; ++mt) {
-                const float4 bq = *reinterpret_cast<const float4 *>(b1L + 16 * mt + 4 * g);
-                h[mt] = w16_f32x4{bq.x, bq.y, bq.z, bq.w};
+                h[mt] = w16_f32x4{b1v[mt].x, b1v[mt].y, b1v[mt].z, b1v[mt].w};
                 h[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][0], zf0, h[mt], 0, 0, 0);
                 h[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1f[mt][1], zf1, h[mt], 0, 0, 0);
             }
             // 4. fc2 on the ReLU'd bf16 activations (the staging block now holds h: the z reads
             // above fed the MFMAs whose results these writes store)
 #pragma unroll
-            for (int mt = 0; mt < 8; ++mt)
-                *reinterpret_cast<uint2 *>(zw + r * 272 + 2 * (16 * mt + 4 * g)) =
+            for (int mt = 0; mt < 8; ++mt)  // hidden 16 mt + 4g .. +3: chunk 2 mt + g / 2, half g & 1
+                *reinterpret_cast<uint2 *>(zw + win_hoff(r, 2 * mt + (g >> 1)) + 8 * (g & 1)) =
                     uint2{relu_bf16x2(cvt_pk_bf16(h[mt][0], h[mt][1])), relu_bf16x2(cvt_pk_bf16(h[mt][2], h[mt][3]))};
             __builtin_amdgcn_wave_barrier();
             w16_f32x4 dx = w16_f32x4{b2v[0], b2v[1], b2v[2], b2v[3]};
 #pragma unroll
             for (int kt = 0; kt < 4; ++kt) {
-                const bf16x8 hf = *reinterpret_cast<const bf16x8 *>(zw + r * 272 + 2 * (32 * kt + 8 * g));
+                const bf16x8 hf = *reinterpret_cast<const bf16x8 *>(zw + win_hoff(r, 4 * kt + g));
                 dx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w2f[kt], hf, dx, 0, 0, 0);
             }
             // 5. update of the cell's quad
@@ -307,7 +315,8 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
             }
             const int mc = wy * WW + wxc;
             const bool gv = G[mc] != 0;
-            const float4 xq = lds_ld128f(M, (unsigned)(mc * 64 + 16 * g));
+            const unsigned moff = (unsigned)g * kWinMPlane + (unsigned)mc * 16u;
+            const float4 xq = lds_ld128f(M, moff);
             float xo[4] = {xq.x, xq.y, xq.z, xq.w};
             if (FIRST && s == 0 && gv) {
 #pragma unroll
@@ -323,7 +332,7 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
                 u[v] = (gv && insl[v]) ? xo[v] : uv;
             }
             if (valid) {
-                lds_st128f(M, (unsigned)(mc * 64 + 16 * g), make_float4(u[0], u[1], u[2], u[3]));
+                lds_st128f(M, moff, make_float4(u[0], u[1], u[2], u[3]));
                 lds_st64(Pn, (unsigned)(pidx * 32 + 8 * g), uint2{pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3])});
             }
             // fired cells of the core, once per cell (quad 0)
@@ -342,7 +351,7 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
             const int c = e >> 2, q = e & 3;
             const int cy = c / CWn, cx = c - cy * CWn;
             const int mc = (cy + ay.h0) * WW + cx + ax.h0;
-            const float4 v = lds_ld128f(M, (unsigned)(mc * 64 + 16 * q));
+            const float4 v = lds_ld128f(M, (unsigned)q * kWinMPlane + (unsigned)mc * 16u);
             const int cell = (ay.lo + cy) * W + ax.lo + cx;
             if (wp.out_nchw) {
                 float *xr = a.x_out + (row * C + 4 * q) * (int64_t)HWn + cell;
