@@ -81,7 +81,7 @@ __host__ __device__ inline WinAxis win_axis(int i, int n, int L, int T, bool wra
 
 template <bool FIRST>
 __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
-    constexpr int C = 16, HD = 128;
+    constexpr int C = 16;
     const RolloutParams &a = wp.a;
     extern __shared__ __attribute__((aligned(16))) unsigned char win_lds[];
     unsigned char *const P0 = win_lds, *const P1 = win_lds + kWinPBytes;
