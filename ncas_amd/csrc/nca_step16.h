@@ -334,6 +334,16 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     for (; t < t_end; t += 8) {
         TileCur cu;
         unpack(nx, cu);  // this tile's loads, consumed before the buffer takes the next tile's
+        // the unpacked values are materialised here, before the next tile's loads are issued:
+        // left to sink to their uses (past the Philox branch) they keep the buffer's old values
+        // alive across its new loads, and the compiler then carries the buffer in two register
+        // sets copied at the end of every iteration (38 moves per tile)
+#pragma unroll
+        for (int tt = 0; tt < 9; ++tt) asm volatile("" : "+v"(cu.tb[tt][0]), "+v"(cu.tb[tt][1]));
+        asm volatile("" : "+v"(cu.xo[0]), "+v"(cu.xo[1]), "+v"(cu.xo[2]), "+v"(cu.xo[3]));
+        asm volatile("" : "+v"(cu.fin), "+v"(cu.gv), "+v"(cu.fu8));
+        if (FIRST) asm volatile("" : "+v"(cu.cv[0]), "+v"(cu.cv[1]), "+v"(cu.cv[2]), "+v"(cu.cv[3]));
+        asm volatile("" ::: "memory");
         int64_t rn = row;
         int tn = tir;
         advance(rn, tn);
