@@ -137,27 +137,47 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
     // ---- load the window: M (fp32), P_cur (bf16), given flags; the border ring of both P copies
     // holds the padding value on board-edge sides (wall: pad_vec, zero: 0) and 0 elsewhere
     {
+        // a thread's loads all go out before its LDS stores: one store after each load would
+        // wait for every load in turn (a quarter of a 2-step window's time)
+        constexpr int kPer = (kWinMax * kWinMax * 4 + 511) / 512;
         const int n = WH * WW * 4;
-        for (int e = tid; e < n; e += 512) {
-            const int c = e >> 2, q = e & 3;
-            const int wy = c / WW, wx = c - wy * WW;
-            int bi = by0 + wy, bj = bx0 + wx;
-            if (wrap) {
-                bi = ((bi % H) + H) % H;
-                bj = ((bj % W) + W) % W;
+        float4 lv[kPer];
+        unsigned char lg[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int e = tid + 512 * k;
+            lv[k] = float4{0.f, 0.f, 0.f, 0.f};
+            lg[k] = 0;
+            if (e < n) {
+                const int c = e >> 2, q = e & 3;
+                const int wy = c / WW, wx = c - wy * WW;
+                int bi = by0 + wy, bj = bx0 + wx;
+                if (wrap) {
+                    bi = ((bi % H) + H) % H;
+                    bj = ((bj % W) + W) % W;
+                }
+                const int cell = bi * W + bj;
+                if (wp.in_nchw) {
+                    const float *xr = a.x_in + (row * C + 4 * q) * (int64_t)HWn + cell;
+                    lv[k] = float4{xr[0], xr[HWn], xr[2 * (int64_t)HWn], xr[3 * (int64_t)HWn]};
+                } else {
+                    lv[k] = *reinterpret_cast<const float4 *>(a.x_in + (row * HWn + cell) * C + 4 * q);
+                }
+                if (q == 0) lg[k] = a.given[row * HWn + cell];
             }
-            const int cell = bi * W + bj;
-            float4 v;
-            if (wp.in_nchw) {
-                const float *xr = a.x_in + (row * C + 4 * q) * (int64_t)HWn + cell;
-                v = float4{xr[0], xr[HWn], xr[2 * (int64_t)HWn], xr[3 * (int64_t)HWn]};
-            } else {
-                v = *reinterpret_cast<const float4 *>(a.x_in + (row * HWn + cell) * C + 4 * q);
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int e = tid + 512 * k;
+            if (e < n) {
+                const int c = e >> 2, q = e & 3;
+                const int wy = c / WW, wx = c - wy * WW;
+                const float4 v = lv[k];
+                lds_st128f(M, (unsigned)q * kWinMPlane + (unsigned)c * 16u, v);
+                lds_st64(P0, (unsigned)(((wy + 1) * kWinStride + wx + 1) * 32 + 8 * q),
+                         uint2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)});
+                if (q == 0) G[c] = lg[k];
             }
-            lds_st128f(M, (unsigned)q * kWinMPlane + (unsigned)c * 16u, v);
-            lds_st64(P0, (unsigned)(((wy + 1) * kWinStride + wx + 1) * 32 + 8 * q),
-                     uint2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)});
-            if (q == 0) G[c] = a.given[row * HWn + cell];
         }
         const int nb = 2 * (WW + 2) + 2 * WH;  // border cells
         for (int e = tid; e < nb * 4; e += 512) {
