@@ -172,16 +172,45 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     for (int e = tid; e < (HWn + 31) / 32; e += NT) givenL[e] = 0u;
     __syncthreads();
     {
+        // batches of 8 loads per thread issued before their stores (a store after each load would
+        // wait for every load in turn: 56 round trips per thread for a 30x30 board)
+        constexpr int kB = 8;
         const float *xr = a.x_in + row * S::C * HWn;
+        const int N = S::C * HWn;
+        for (int e0 = tid; e0 < N; e0 += NT * kB) {
+            float v[kB];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) {
+                const int e = e0 + NT * k;
+                v[k] = xr[e < N ? e : N - 1];
+            }
+#pragma unroll
+            for (int k = 0; k < kB; ++k) {
+                const int e = e0 + NT * k;
+                if (e < N) {
+                    const int ch = e / HWn, q = e - ch * HWn;
+                    m_at(q, ch) = v[k];
+                }
+            }
+        }
+        // whether the caller's state already holds the clamp values in the input slice of given
+        // cells (the usual case; otherwise the first step's updates take them from the clamp)
+        const int N2 = a.c_in * HWn;
         int need = 0;
-        for (int e = tid; e < S::C * HWn; e += NT) {
-            const int ch = e / HWn, q = e - ch * HWn;
-            const float v = xr[e];
-            m_at(q, ch) = v;
-            const int ci = ch - a.in_off;
-            if (ci >= 0 && ci < a.c_in && a.given[row * HWn + q] &&
-                __float_as_uint(v) != __float_as_uint(a.clamp[(row * a.c_in + ci) * HWn + q]))
-                need = 1;
+        for (int e0 = tid; e0 < N2; e0 += NT * kB) {
+            unsigned xv[kB], cv[kB];
+            unsigned char gv[kB];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) {
+                const int e = e0 + NT * k, ec = e < N2 ? e : N2 - 1;
+                const int ci = ec / HWn, q = ec - ci * HWn;
+                xv[k] = __float_as_uint(xr[(a.in_off + ci) * HWn + q]);
+                cv[k] = __float_as_uint(a.clamp[(row * a.c_in + ci) * HWn + q]);
+                gv[k] = a.given[row * HWn + q];
+            }
+#pragma unroll
+            for (int k = 0; k < kB; ++k)
+                if (e0 + NT * k < N2 && gv[k] && xv[k] != cv[k]) need = 1;
         }
         if (need) flagsL[1] = 1;
     }
@@ -677,12 +706,22 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     }
     __syncthreads();
 
-    // ---- write back
+    // ---- write back (LDS reads in batches of 8 ahead of their stores)
     {
+        constexpr int kB = 8;
         float *xr = a.x_out + row * S::C * HWn;
-        for (int e = tid; e < S::C * HWn; e += NT) {
-            const int ch = e / HWn, q = e - ch * HWn;
-            xr[e] = m_at(q, ch);
+        const int N = S::C * HWn;
+        for (int e0 = tid; e0 < N; e0 += NT * kB) {
+            float v[kB];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) {
+                const int e = e0 + NT * k, ec = e < N ? e : N - 1;
+                const int ch = ec / HWn, q = ec - ch * HWn;
+                v[k] = m_at(q, ch);
+            }
+#pragma unroll
+            for (int k = 0; k < kB; ++k)
+                if (e0 + NT * k < N) xr[e0 + NT * k] = v[k];
         }
     }
     if (a.conf_out) {
