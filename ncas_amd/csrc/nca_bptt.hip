@@ -731,6 +731,8 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
     float acc[36];
 #pragma unroll
     for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
+    // this workgroup's slot of kernel-weight sums (its own, so read here, long before it is added to)
+    const float dk_old = threadIdx.x < 36 ? dk[(int64_t)blockIdx.x * 36 + threadIdx.x] : 0.0f;
     const int p0 = blockIdx.x * kStripPlanes;
     const int p1 = p0 + kStripPlanes < d.rows * d.C ? p0 + kStripPlanes : (int)(d.rows * d.C);
     // a plane's 6 arrays, 8 cells per thread (HW <= kPlaneMax = 8 kThreads), in registers
@@ -825,10 +827,7 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
         }
     }
     const float r = block_sums<36, kThreads / 64>(acc, red);
-    if (threadIdx.x < 36) {
-        float *pp = dk + (int64_t)blockIdx.x * 36 + threadIdx.x;
-        *pp = __fadd_rn(*pp, r);
-    }
+    if (threadIdx.x < 36) dk[(int64_t)blockIdx.x * 36 + threadIdx.x] = __fadd_rn(dk_old, r);
 }
 
 // acc[v] += the sum of the planes' kernel-weight slots: block v, each thread a fixed strided
