@@ -165,9 +165,15 @@ __device__ float block_sum(float v, float *red) {
     return r;
 }
 
+// the value of the lane that DPP control CTRL selects (no LDS traffic)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
 // Block-wide sums of N floats per thread over a block of WAVES waves: each wave folds its lanes
-// with a fixed xor butterfly (both partners of an exchange add the same two values, so every
-// lane ends with the same bits), then thread i < N adds the waves' totals in wave order.
+// in a fixed order of symmetric pairings (both partners of an exchange add the same two values,
+// so every lane ends with the same bits), then thread i < N adds the waves' totals in wave order.
 // Returns the block total of v[i] in thread i (0 in threads >= N); red holds WAVES * N floats.
 template <int N, int WAVES>
 __device__ float block_sums(const float (&v)[N], float *red) {
@@ -175,8 +181,15 @@ __device__ float block_sums(const float (&v)[N], float *red) {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         float x = v[i];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) x = __fadd_rn(x, __shfl_xor(x, o));
+        // lanes paired with lane ^ 1, ^ 2 (quad_perm), 7 - i and 15 - i within the row (half mirror,
+        // mirror: by then the 4 lanes of a quad, and the 8 of a half row, hold the same value),
+        // then ^ 16 and ^ 32: partners add the same two values, so every lane ends with the same bits
+        x = __fadd_rn(x, dpp_f32<0xb1>(x));   // quad_perm [1, 0, 3, 2]
+        x = __fadd_rn(x, dpp_f32<0x4e>(x));   // quad_perm [2, 3, 0, 1]
+        x = __fadd_rn(x, dpp_f32<0x141>(x));  // row_half_mirror
+        x = __fadd_rn(x, dpp_f32<0x140>(x));  // row_mirror
+        x = __fadd_rn(x, __shfl_xor(x, 16));
+        x = __fadd_rn(x, __shfl_xor(x, 32));
         if (lane == 0) red[wave * N + i] = x;
     }
     __syncthreads();
