@@ -784,27 +784,30 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
         if (!active || i0 >= i1) continue;
         const float hv = d.padding == 1 ? padv[c] : 0.0f;
         // window row a of cell row i is grid row i + a - 1: x taps (halo value, bf16-rounded)
-        // and g_z (zero with a flag for halo cells: no transposed contribution)
+        // and g_z (zero at halo cells: no transposed contribution, so the taps need no branch).
+        // The three window rows live in a ring of register slots (row i - 1, i, i + 1 in slots
+        // S0, S1, S2, rotating by one per row), so sliding the window copies nothing.
         float xw[3][3], gw[3][4][3];
-        bool hw[3][3];
-        auto load_row = [&](int a, int ii) {
+        auto load_row = [&](int a, int ii) __attribute__((always_inline)) {
             const bool rh = (ii < 0 || ii >= H) && !wrap;
             const int ir = ii < 0 ? H - 1 : (ii >= H ? 0 : ii);
 #pragma unroll
             for (int b = 0; b < 3; ++b) {
+                // every q is a cell of the plane (wrapped), so the loads need no branch
                 const bool h = rh || jh[b];
                 const int q = ir * W + jc[b];
-                const float xv = h ? hv : xs[q];
+                const float xl = xs[q];
+                const float xv = h ? hv : xl;
                 xw[a][b] = d.bf16 ? nca::round_bf16(xv) : xv;
-                hw[a][b] = h;
+                const unsigned keep = h ? 0u : 0xffffffffu;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) gw[a][k][b] = gs[k * HW + q];
+                for (int k = 0; k < 4; ++k) gw[a][k][b] = __uint_as_float(__float_as_uint(gs[k * HW + q]) & keep);
             }
         };
-        load_row(0, i0 - 1);
-        load_row(1, i0);
-        for (int i = i0; i < i1; ++i) {
-            load_row(2, i + 1);
+        auto cell = [&](int i, auto s0_c, auto s1_c, auto s2_c) __attribute__((always_inline)) {
+            constexpr int S0 = decltype(s0_c)::value, S1 = decltype(s1_c)::value, S2 = decltype(s2_c)::value;
+            constexpr int SL[3] = {S0, S1, S2};
+            load_row(S2, i + 1);
             const int64_t e = (int64_t)pl * HW + i * W + j;
             float g = us[i * W + j];
 #pragma unroll
@@ -812,31 +815,26 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
                 // tap t = (dy, dx) reads x at (i + dy, j + dx); the cell whose tap t reads this
                 // cell is (i - dy, j - dx): window position (1 - dy, 1 - dx)
                 const int a = 2 - t / 3, b = 2 - t % 3;
-                if (!hw[a][b]) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], gw[a][k][b], g);
-                }
+                for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], gw[SL[a]][k][b], g);
             }
             gx[e] = g;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float gzv = gw[1][k][1];
+                const float gzv = gw[S1][k][1];
 #pragma unroll
-                for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gzv, xw[t / 3][t % 3], acc[k * 9 + t]);
+                for (int t = 0; t < 9; ++t) acc[k * 9 + t] = __builtin_fmaf(gzv, xw[SL[t / 3]][t % 3], acc[k * 9 + t]);
             }
-            // slide the window down one row
-#pragma unroll
-            for (int b = 0; b < 3; ++b) {
-                xw[0][b] = xw[1][b];
-                xw[1][b] = xw[2][b];
-                hw[0][b] = hw[1][b];
-                hw[1][b] = hw[2][b];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    gw[0][k][b] = gw[1][k][b];
-                    gw[1][k][b] = gw[2][k][b];
-                }
-            }
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        load_row(0, i0 - 1);
+        load_row(1, i0);
+        for (int i = i0; i < i1; i += 3) {
+            cell(i, I0{}, I1{}, I2{});
+            if (i + 1 < i1) cell(i + 1, I1{}, I2{}, I0{});
+            if (i + 2 < i1) cell(i + 2, I2{}, I0{}, I1{});
         }
     }
     const float r = block_sums<36, kThreads / 64>(acc, red);
