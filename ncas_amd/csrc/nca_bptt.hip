@@ -744,6 +744,13 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
     float acc[36];
 #pragma unroll
     for (int v = 0; v < 36; ++v) acc[v] = 0.0f;
+    // the kernel weights in VGPRs (held in scalar registers they spill and reload in the row loop)
+    float kr[36];
+#pragma unroll
+    for (int v = 0; v < 36; ++v) {
+        kr[v] = kern[v];
+        asm volatile("" : "+v"(kr[v]));
+    }
     // this workgroup's slot of kernel-weight sums (its own, so read here, long before it is added to)
     const float dk_old = threadIdx.x < 36 ? dk[(int64_t)blockIdx.x * 36 + threadIdx.x] : 0.0f;
     const int p0 = blockIdx.x * kStripPlanes;
@@ -816,7 +823,7 @@ __global__ void __launch_bounds__(kThreads) stencil_back_strip(Dims d, const flo
                 // cell is (i - dy, j - dx): window position (1 - dy, 1 - dx)
                 const int a = 2 - t / 3, b = 2 - t % 3;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kern[k * 9 + t], gw[SL[a]][k][b], g);
+                for (int k = 0; k < 4; ++k) g = __builtin_fmaf(kr[k * 9 + t], gw[SL[a]][k][b], g);
             }
             gx[e] = g;
 #pragma unroll
