@@ -32,6 +32,7 @@
  *   nca_bptt_forward  <- the BPTT chunk's forward in Engine.train_iteration (run_steps with grad,
  *                        src/nca/engine/engine.py:478-489 -> run_block, step.py:212-246): the
  *                        chunk's states, kept instead of autograd's per-step activations
+ *   nca_bptt_forward_ws <- the same, with a workspace that lets boards run in pieces of rows
  *   nca_bptt_backward <- its backward ((loss * scale).backward(), engine.py:497, through
  *                        _FusedCellUpdate.backward ops.py:269-294, the MLP and the shared-kernel
  *                        perception backward ops.py:79-94) with the loss of step.py:243-245 /
@@ -256,6 +257,17 @@ size_t nca_bptt_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t
 int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
                      int32_t width, const float *x0, const uint8_t *given, const float *clamp,
                      const nca_fire_desc *fire, int32_t n_chunk, float *states, void *stream);
+
+/* nca_bptt_forward with a device workspace of workspace_bytes (the backward's, at least
+ * nca_bptt_workspace_bytes of the same shape, may be passed; nothing in it is kept): the streamed
+ * kernel then runs each board in two or three pieces of rows on as many workgroups, exchanging
+ * their boundary rows through the workspace every step, when the device has a CU for every
+ * piece. States are the same bit for bit. Replaces the same reference call as nca_bptt_forward
+ * (src/nca/engine/engine.py:478-489, the chunk's forward under autograd). */
+int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
+                        int32_t width, const float *x0, const uint8_t *given, const float *clamp,
+                        const nca_fire_desc *fire, int32_t n_chunk, float *states, void *workspace,
+                        size_t workspace_bytes, void *stream);
 
 /* Backward of the chunk whose forward wrote `states` (same cell, packed weights, fire desc).
  * w->w1 and w->w2 are the fp32 master weights (rounded to bf16 on load for bf16 cells, as the

@@ -35,6 +35,7 @@ EXPORTS = (
     "nca_set_window_steps",
     "nca_bptt_workspace_bytes",
     "nca_bptt_forward",
+    "nca_bptt_forward_ws",
     "nca_bptt_backward",
     "nca_step_backward_workspace_bytes",
     "nca_step_backward",
@@ -141,6 +142,8 @@ def load():
     L.nca_bptt_workspace_bytes.restype = ctypes.c_size_t
     L.nca_bptt_forward.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp,
                                    ctypes.POINTER(FireDesc), i32, vp, vp]
+    L.nca_bptt_forward_ws.argtypes = [ctypes.POINTER(CellDesc), vp, i64, i32, i32, vp, vp, vp,
+                                      ctypes.POINTER(FireDesc), i32, vp, vp, ctypes.c_size_t, vp]
     L.nca_bptt_backward.argtypes = [
         ctypes.POINTER(CellDesc), vp, ctypes.POINTER(CellWeights), i64, i32, i32, vp, vp,
         ctypes.POINTER(FireDesc), i32, ctypes.POINTER(BpttLoss), vp, ctypes.POINTER(CellGrads), vp,

@@ -514,9 +514,38 @@ int check_grid(int64_t rows, int H, int W) {
 
 namespace nca {
 
+namespace {
+
+// CUs of the current device (cached per device)
+int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) return 0;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+int recorded_pieces(const nca_cell_desc *cell, int64_t rows, int H, int W) {
+    return nca::stream32_pieces(rows, H, W, cell->c_out, cell->n_out, kLdsBytes, device_cus());
+}
+
+}  // namespace
+
+size_t recorded_xch_bytes(const nca_cell_desc *cell, int64_t rows, int H, int W) {
+    if (check_cell(cell) || check_grid(rows, H, W) || !takes_stream32(cell, rows, H, W)) {
+        g_err[0] = 0;
+        return 0;
+    }
+    return nca::stream32_xch_bytes(rows, recorded_pieces(cell, rows, H, W), W);
+}
+
 int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows, int H, int W, const float *x_in,
                      const uint8_t *given, const float *clamp, float *x_out, const nca_fire_desc *fire, int n_steps,
-                     float *x_rec, int64_t rec_stride, hipStream_t st, bool *used) {
+                     float *x_rec, int64_t rec_stride, hipStream_t st, bool *used, void *xch, size_t xch_bytes) {
     *used = false;
     // anything the checks of nca_rollout_ws would refuse is left to the caller's fallback
     if (check_cell(cell) || check_grid(rows, H, W)) {
@@ -541,7 +570,10 @@ int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows
     p.tau = fire->tau;
     p.x_rec = x_rec;
     p.rec_stride = rec_stride;
-    return hip_check(nca::launch_stream32(p, st, kLdsBytes, used), "streamed rollout launch");
+    int P = xch ? recorded_pieces(cell, rows, H, W) : 1;
+    if (P > 1 && xch_bytes < nca::stream32_xch_bytes(rows, P, W)) P = 1;
+    return hip_check(nca::launch_stream32(p, st, kLdsBytes, used, P, static_cast<uint64_t *>(xch)),
+                     "streamed rollout launch");
 }
 
 }  // namespace nca

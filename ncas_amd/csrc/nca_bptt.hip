@@ -1055,12 +1055,22 @@ size_t nca_bptt_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t
                                 int32_t n_chunk) {
     Dims d;
     if (nca_packed_weights_bytes(cell) == 0 || check_dims(cell, rows, height, width, n_chunk, &d)) return 0;
-    return (size_t)ws_layout(d, n_chunk).total * sizeof(float);
+    const size_t bwd = (size_t)ws_layout(d, n_chunk).total * sizeof(float);
+    // the forward's row exchange when its boards run in pieces (nca_bptt_forward_ws)
+    const size_t xch = nca::recorded_xch_bytes(cell, rows, height, width);
+    return bwd > xch ? bwd : xch;
 }
 
 int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height, int32_t width,
                      const float *x0, const uint8_t *given, const float *clamp, const nca_fire_desc *fire,
                      int32_t n_chunk, float *states, void *stream) {
+    return nca_bptt_forward_ws(cell, packed, rows, height, width, x0, given, clamp, fire, n_chunk, states, nullptr, 0,
+                               stream);
+}
+
+int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height, int32_t width,
+                        const float *x0, const uint8_t *given, const float *clamp, const nca_fire_desc *fire,
+                        int32_t n_chunk, float *states, void *workspace, size_t workspace_bytes, void *stream) {
     nca::clear_error();
     Dims d;
     int rc = check_dims(cell, rows, height, width, n_chunk, &d);
@@ -1077,7 +1087,7 @@ int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows
     // the whole chunk in one launch of the streamed kernel where it takes the cell and grid
     bool used = false;
     if ((rc = nca::rollout_recorded(cell, packed, rows, height, width, x0, given, clamp, states + n_chunk * sn, fire,
-                                    n_chunk, states + sn, sn, st, &used)))
+                                    n_chunk, states + sn, sn, st, &used, workspace, workspace_bytes)))
         return rc;
     if (used) return NCA_OK;
     for (int t = 0; t < n_chunk; ++t) {

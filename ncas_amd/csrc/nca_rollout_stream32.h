@@ -83,12 +83,17 @@ struct St32 {
     static constexpr int NSLOT = 4;  // fire ring steps
 };
 
+// re-reads of an exchange word before a piece gives up on its neighbour (about a second; after
+// that its halo rows are NaN and it waits no more)
+constexpr int kHaloSpin = 1 << 20;
+
 struct St32Plan {
-    unsigned M, Z, D, cinfo, ring, given, head, evp, flags, total;
+    unsigned M, Z, D, cinfo, ring, given, head, evp, flags, gidx, total;
     int NM, RING;
 };
 
-inline St32Plan st32_plan(int H, int W, int c_out, int n_out) {
+// H: the rows one workgroup runs (a board's, or a piece's); pieces: with the board-cell table
+inline St32Plan st32_plan(int H, int W, int c_out, int n_out, bool pieces = false) {
     using S = St32;
     St32Plan p;
     const int HWn = H * W;
@@ -111,8 +116,10 @@ inline St32Plan st32_plan(int H, int W, int c_out, int n_out) {
     o = st_al16(o + (unsigned)(n_out * c_out + n_out) * 4u);
     p.evp = o;  // a copy of the call's parameters for the per-step draws
     o = st_al16(o + (unsigned)sizeof(RolloutParams));
-    p.flags = o;  // [0] fired count, [1] first-step clamp needed
-    o = st_al16(o + 8u);
+    p.flags = o;  // [0] fired count, [1] first-step clamp needed, [2..5] two per-step keys
+    o = st_al16(o + 24u);
+    p.gidx = o;  // pieces: u16 board cell of stream position q, q < HW
+    if (pieces) o = st_al16(o + (unsigned)HWn * 2u);
     p.total = o;
     return p;
 }
@@ -124,8 +131,13 @@ struct St32Params {
     // sum of exponentials, conf_s computed on the host with IEEE division); fast_conf selects it
     float conf_s;
     int fast_conf;
-    unsigned l_M, l_Z, l_D, l_cinfo, l_ring, l_given, l_head, l_evp, l_flags;
+    unsigned l_M, l_Z, l_D, l_cinfo, l_ring, l_given, l_head, l_evp, l_flags, l_gidx;
     unsigned off_w1q, off_w2k;
+    // board pieces (recording kernel only): P workgroups per board, piece p runs board rows
+    // [p Hp, p Hp + Hp) (the last piece may have fewer); xch: the exchange slots, (rows, P, 2, 4,
+    // W, 32) words of (step tag << 32 | fp32 bits), all zero at the launch
+    int P, Hp;
+    uint64_t *xch;
 };
 
 // zsw: the Z row swizzle (a permutation of 0..15)
@@ -141,8 +153,17 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int H = a.H, W = a.W, HWn = H * W, RING = sp.RING;
-    const int64_t row = blockIdx.x;
+    // the workgroup runs rows [r0, r0 + Hs) of board `row`: all of it, or piece `piece` of P. An
+    // even piece streams its rows top to bottom, an odd one bottom to top, so two neighbours
+    // meet at rows both stream first or both stream last; M keeps the board's orientation.
+    const int P = REC ? sp.P : 1;
+    const int64_t row = P > 1 ? (int64_t)(blockIdx.x / (unsigned)P) : (int64_t)blockIdx.x;
+    const int piece = P > 1 ? (int)(blockIdx.x - (unsigned)row * (unsigned)P) : 0;
+    const int W = a.W, Ht = a.H, HWt = Ht * W;
+    const int r0 = piece * sp.Hp;
+    const int Hs = P > 1 ? (Ht - r0 < sp.Hp ? Ht - r0 : sp.Hp) : Ht;
+    const bool down = (piece & 1) == 0;
+    const int HWn = Hs * W, RING = S::NSLOT * HWn;
     const int tb = tid - 256;  // thread index among the channel waves
 
     float *headL = reinterpret_cast<float *>(smem + sp.l_head);
@@ -151,9 +172,14 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     unsigned *givenL = reinterpret_cast<unsigned *>(smem + sp.l_given);
     unsigned char *ring = smem + sp.l_ring;
 
+    // M cell and board cell of stream position q (row q / W of the workgroup's stream)
     auto m_index = [&](int q) -> int {
-        const int i = q / W, j = q - i * W;
-        return (i + 1) * (W + 1) + j + 1;
+        const int k = q / W, j = q - k * W;
+        return ((down ? k : Hs - 1 - k) + 1) * (W + 1) + j + 1;
+    };
+    auto g_index = [&](int q) -> int {
+        const int k = q / W, j = q - k * W;
+        return (r0 + (down ? k : Hs - 1 - k)) * W + j;
     };
     auto m_at = [&](int q, int ch) -> float & {
         return *reinterpret_cast<float *>(smem + sp.l_M + (unsigned)m_index(q) * S::MS + 4u * (unsigned)ch);
@@ -175,21 +201,26 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
         // batches of 8 loads per thread issued before their stores (a store after each load would
         // wait for every load in turn: 56 round trips per thread for a 30x30 board)
         constexpr int kB = 8;
-        const float *xr = a.x_in + row * S::C * HWn;
-        const int N = S::C * HWn;
+        const float *xr = a.x_in + row * S::C * HWt;
+        // board rows rlo .. rhi: the workgroup's and, for a piece, the halo rows inside the board
+        const int rlo = r0 > 0 ? r0 - 1 : 0, rhi = r0 + Hs < Ht ? r0 + Hs : Ht - 1;
+        const int NR = (rhi - rlo + 1) * W;
+        const int N = S::C * NR;
+        float *M = reinterpret_cast<float *>(smem + sp.l_M);
         for (int e0 = tid; e0 < N; e0 += NT * kB) {
             float v[kB];
 #pragma unroll
             for (int k = 0; k < kB; ++k) {
-                const int e = e0 + NT * k;
-                v[k] = xr[e < N ? e : N - 1];
+                const int e = e0 + NT * k, ec = e < N ? e : N - 1;
+                const int ch = ec / NR, c = ec - ch * NR;
+                v[k] = xr[ch * HWt + rlo * W + c];
             }
 #pragma unroll
             for (int k = 0; k < kB; ++k) {
                 const int e = e0 + NT * k;
                 if (e < N) {
-                    const int ch = e / HWn, q = e - ch * HWn;
-                    m_at(q, ch) = v[k];
+                    const int ch = e / NR, c = e - ch * NR, rr = c / W, j = c - rr * W;
+                    M[((rlo + rr - r0 + 1) * (W + 1) + j + 1) * S::C + ch] = v[k];
                 }
             }
         }
@@ -203,10 +234,10 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
 #pragma unroll
             for (int k = 0; k < kB; ++k) {
                 const int e = e0 + NT * k, ec = e < N2 ? e : N2 - 1;
-                const int ci = ec / HWn, q = ec - ci * HWn;
-                xv[k] = __float_as_uint(xr[(a.in_off + ci) * HWn + q]);
-                cv[k] = __float_as_uint(a.clamp[(row * a.c_in + ci) * HWn + q]);
-                gv[k] = a.given[row * HWn + q];
+                const int ci = ec / HWn, q = g_index(ec - ci * HWn);
+                xv[k] = __float_as_uint(xr[(a.in_off + ci) * HWt + q]);
+                cv[k] = __float_as_uint(a.clamp[(row * a.c_in + ci) * HWt + q]);
+                gv[k] = a.given[row * HWt + q];
             }
 #pragma unroll
             for (int k = 0; k < kB; ++k)
@@ -215,8 +246,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
         if (need) flagsL[1] = 1;
     }
     for (int c = tid; c < HWn + 16; c += NT) cinfo[c] = (unsigned short)m_index(c < HWn ? c : c - HWn);
+    unsigned short *gidxL = reinterpret_cast<unsigned short *>(smem + sp.l_gidx);
+    if (P > 1)
+        for (int c = tid; c < HWn; c += NT) gidxL[c] = (unsigned short)g_index(c);
     for (int q = tid; q < HWn; q += NT)
-        if (a.given[row * HWn + q]) atomicOr(&givenL[q >> 5], 1u << (q & 31));
+        if (a.given[row * HWt + g_index(q)]) atomicOr(&givenL[q >> 5], 1u << (q & 31));
     for (int e = tid; e < (int)(sizeof(RolloutParams) / 4); e += NT)
         reinterpret_cast<unsigned *>(smem + sp.l_evp)[e] = reinterpret_cast<const unsigned *>(&a)[e];
     {
@@ -234,45 +268,75 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
         ring[o] = (unsigned char)v;
         if (o < 16) ring[RING + o] = (unsigned char)v;
     };
-    const int nq4 = (HWn + 3) >> 2;
-    auto draw = [&](const RolloutParams &pa, int s) __attribute__((always_inline)) {
-        for (int it = tb; it < nq4; it += 256) {
+    // the Philox draws go by the board's groups of 4 cells: those holding the workgroup's cells,
+    // at most 256 (H W <= 1024, checked by the host), one per channel-wave thread, the update
+    // waves' threads first (the stencil waves set the interval's pace). A thread's group, the
+    // stream positions of its cells in the workgroup (or -1) and their given bits (bit 16) are
+    // found once here, so a step's draw is one Philox evaluation and four ring stores.
+    const int qlo = r0 * W, qhi = qlo + HWn;
+    const int it0 = qlo >> 2, it1 = (qhi + 3) >> 2;
+    const int dit = it0 + (255 - tb);  // this thread's group (channel waves; none if >= it1)
+    int dq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int qt = 4 * dit + e;  // board cell
+        int v = -1;
+        if (wave >= 4 && dit < it1 && qt >= qlo && qt < qhi) {
+            const int tl = qt / W - r0, j = qt - (qt / W) * W;
+            const int q = (down ? tl : Hs - 1 - tl) * W + j;  // its stream position
+            v = q | (int)(((givenL[q >> 5] >> (q & 31)) & 1u) << 16);
+        }
+        dq[e] = v;
+    }
+    const bool count_fired = a.fired_out != nullptr && !a.adaptive;
+    // per-step keys for the draws of steps 2, 3, ..: slot s & 1, written 4 intervals after the
+    // previous draw by one stencil lane (so no draw waits for a global load)
+    uint64_t *keyL = reinterpret_cast<uint64_t *>(flagsL + 2);
+    auto draw = [&](const RolloutParams &pa, int s, uint64_t key) __attribute__((always_inline)) {
+        unsigned fired = 0;
+        if (dit < it1) {
             float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-            if (!pa.fire_u8) {
-                const uint64_t key = pa.step_seeds ? pa.step_seeds[s] : pa.seed;
-                cell_uniforms4(key, (uint32_t)(pa.row0 + row), (uint32_t)(pa.step0 + s), (uint32_t)it, u);
-            }
-            int cnt = 0;
+            if (!pa.fire_u8)
+                cell_uniforms4(key, (uint32_t)(pa.row0 + row), (uint32_t)(pa.step0 + s), (uint32_t)dit, u);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int q = 4 * it + e;
-                if (q >= HWn) continue;
-                const unsigned gv = (givenL[q >> 5] >> (q & 31)) & 1u;
+                if (dq[e] < 0) continue;
+                const int q = dq[e] & 0xffff;
                 unsigned b;
                 if (pa.fire_u8) {
-                    b = pa.fire_u8[((int64_t)s * pa.rows + row) * HWn + q] != 0;
+                    b = pa.fire_u8[((int64_t)s * pa.rows + row) * HWt + 4 * dit + e] != 0;
                 } else {
                     const unsigned b0 = u[e] < pa.p, b1 = u[e] < pa.p_low;
                     b = pa.adaptive ? (b0 | (b1 << 1)) : b0;
                 }
-                ring_put(s, q, b | (gv << 7));
-                if (!pa.adaptive) cnt += (int)(b & 1u);
+                ring_put(s, q, b | ((unsigned)(dq[e] >> 16) << 7));
+                fired += b & 1u;
             }
-            if (cnt) atomicAdd(&flagsL[0], cnt);
+        }
+        if (count_fired) {
+            // the wave's fired cells from the bits of the lanes' counts (0 .. 4)
+            const int tot = __popcll(__ballot(fired & 1u)) + 2 * __popcll(__ballot(fired & 2u)) +
+                            4 * __popcll(__ballot(fired & 4u));
+            if (lane == 0 && tot) atomicAdd(&flagsL[0], tot);
         }
     };
     if (wave >= 4 && a.n_steps > 0) {
-        draw(a, 0);
-        if (a.n_steps > 1) draw(a, 1);
+        draw(a, 0, a.step_seeds ? a.step_seeds[0] : a.seed);
+        if (a.n_steps > 1) draw(a, 1, a.step_seeds ? a.step_seeds[1] : a.seed);
     }
+    if (tid == 256 && a.step_seeds && a.n_steps > 2) keyL[0] = a.step_seeds[2];
     __syncthreads();
 
     using F_ = std::integral_constant<bool, false>;
     using T_ = std::integral_constant<bool, true>;
     using P0 = std::integral_constant<unsigned, 0>;
     using P1 = std::integral_constant<unsigned, 1>;
-    const int T = sp.T;
+    const int T = P > 1 ? (int)(((int64_t)a.n_steps * HWn + 15) >> 4) : sp.T;
     const int total = a.n_steps * HWn;
+    // a piece's neighbours: on the side of its first stream row (the row above for an even
+    // piece, below for an odd one) and on the side of its last
+    const bool has_first = P > 1 && (down ? piece > 0 : piece < P - 1);
+    const bool has_last = P > 1 && (down ? piece < P - 1 : piece > 0);
     const int g = lane >> 4, n = lane & 15;
     const int ws = wave & 3;
 
@@ -412,12 +476,22 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
         // the per-step draws: when the update stage enters step sd, step sd + 2 is drawn (its
         // ring slot was last read by the updates of step sd - 2)
         int sd = 0, ev_draw = 3;
+        int kput = -1;  // stencil lane 0 of wave 4: the interval that stores knext into keyL
+        uint64_t knext = 0;
         auto events = [&]() __attribute__((always_inline)) {
             if (i == ev_draw) {
                 const RolloutParams &ea = *reinterpret_cast<const RolloutParams *>(smem + sp.l_evp);
-                if (sd + 2 < ea.n_steps) draw(ea, sd + 2);
+                if (sd + 2 < ea.n_steps) draw(ea, sd + 2, ea.step_seeds ? keyL[sd & 1] : ea.seed);
+                if (tb == 0 && ea.step_seeds && sd + 3 < ea.n_steps) {
+                    knext = ea.step_seeds[sd + 3];  // the next draw's key, (sd + 3) & 1 = (sd + 1) & 1
+                    kput = i + 4;
+                }
                 ++sd;
                 ev_draw = ((sd * HWn) >> 4) + 3;
+            }
+            if (i == kput) {
+                keyL[sd & 1] = knext;
+                kput = -1;
             }
         };
         // gated firing: the update lanes decide a cell's mask for the step from its state at the
@@ -557,20 +631,94 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 if (cbS >= HWn) cbS -= HWn;
                 xs1 = xs2;
             };
+            // pieces: M's halo rows hold the neighbours' rows of the state the stencil reads.
+            // Refresh k (k = 0 .. n_steps - 1) brings the last side's row of state k and the first
+            // side's row of state k + 1; its loads are issued in interval hB = ((k HW) >> 4) + 9,
+            // checked and stored in interval hB + 4. The last side's old row (state k - 1) was
+            // last read by taps loaded before interval (k HW) >> 4 and the new one is first read
+            // by the taps of step k's last row, loaded from interval ((k HW + (Hs - 1) W) >> 4) - 1
+            // >= hB + 5 ((Hs - 1) W >= 240, checked by the host); the first side's old row (state
+            // k) by step k's first row, loaded before interval ((k HW) >> 4) + 2, the new one from
+            // interval (((k + 1) HW) >> 4) - 1 >= hB + 5. A neighbour writes its last row of state
+            // k in its step k - 1 and its first row of state k + 1 early in step k, intervals
+            // before hB when the two run in step. A word whose tag is not yet that state's is
+            // read again; after kHaloSpin reads the halo takes NaN (which reaches every result),
+            // no later refresh waits, and the kernel still ends.
+            const int th = tid - 256;  // 0 .. 127 over the stencil waves
+            const int NE = W * S::C;
+            const int nf = down ? piece - 1 : piece + 1, nl = down ? piece + 1 : piece - 1;
+            const int mrow_f = down ? 0 : Hs + 1, mrow_l = down ? Hs + 1 : 0;
+            int hk = 0, hB = 9;
+            bool hfail = false;  // a wait ran out: no later wait (the results are NaN already)
+            uint64_t hv[2][8];
+            auto xslot = [&](int side, int nb, int st) -> const uint64_t * {
+                return sp.xch + (((row * P + nb) * 2 + side) * 4 + (st & 3)) * (int64_t)NE;
+            };
+            auto halo_load = [&](int side, int nb, int st) __attribute__((always_inline)) {
+                const uint64_t *src = xslot(side, nb, st);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int e = th + 128 * k;
+                    hv[side][k] = e < NE ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+                }
+            };
+            auto halo_store = [&](int side, int nb, int st, int mrow) __attribute__((always_inline)) {
+                const uint64_t *src = xslot(side, nb, st);
+                float *Mh = reinterpret_cast<float *>(smem + sp.l_M + (unsigned)(mrow * (W + 1) + 1) * S::MS);
+                // the words not yet tagged st are read again together (one round trip a try)
+                auto stale = [&](int k) { return th + 128 * k < NE && (uint32_t)(hv[side][k] >> 32) != (uint32_t)st; };
+                for (int n = 0; !hfail; ++n) {
+                    bool any = false;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) any |= stale(k);
+                    if (!any) break;
+                    if (n == kHaloSpin) {
+                        hfail = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+                        if (stale(k))
+                            hv[side][k] = __hip_atomic_load(src + th + 128 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int e = th + 128 * k;
+                    if (e < NE) {
+                        const uint64_t wd = hv[side][k];
+                        Mh[e] = (uint32_t)(wd >> 32) == (uint32_t)st ? __uint_as_float((uint32_t)wd) : __builtin_nanf("");
+                    }
+                }
+            };
+            auto halo_ev = [&]() __attribute__((always_inline)) {
+                if (i == hB) {
+                    if (has_last && hk >= 1) halo_load(1, nl, hk);
+                    if (has_first && hk + 1 < a.n_steps) halo_load(0, nf, hk + 1);
+                } else if (i == hB + 4) {
+                    if (has_last && hk >= 1) halo_store(1, nl, hk, mrow_l);
+                    if (has_first && hk + 1 < a.n_steps) halo_store(0, nf, hk + 1, mrow_f);
+                    ++hk;
+                    hB = ((hk * HWn) >> 4) + 9;
+                }
+            };
             i = 0;
             while (i + 1 < T) {
                 sinterval(P0{});
                 events();
+                if (P > 1) halo_ev();
                 advance();
                 __syncthreads();
                 sinterval(P1{});
                 events();
+                if (P > 1) halo_ev();
                 advance();
                 __syncthreads();
             }
             if (i < T) {
                 sinterval(P0{});
                 events();
+                if (P > 1) halo_ev();
                 advance();
                 __syncthreads();
             }
@@ -621,10 +769,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 float4 pd[4];
 #pragma unroll
                 for (int p = 0; p < 4; ++p) pd[p] = lds_ld128f(smem, kDr + (PAR ^ 1u) * S::DBUF + (unsigned)p * S::DPART);
-                // the cell's step and board cell
+                // the cell's step, stream position and board cell
                 const bool nxt = cbU + cl >= HWn;
                 const int sc = usU + (nxt ? 1 : 0);
                 const int qc = cbU + cl - (nxt ? HWn : 0);
+                const int qg = P > 1 ? (int)gidxL[qc] : qc;
                 unsigned fbit = fb & 1u;
                 if (GATED) {
                     // the output-quad lane's decision (its m4 is the output quad) to all 8 lanes
@@ -648,7 +797,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
 #pragma unroll
                         for (int v = 0; v < 4; ++v)
                             if (imv[v])
-                                xk[v] = a.clamp[(row * a.c_in + (4 * q8 + v - a.in_off)) * HWn + qc];
+                                xk[v] = a.clamp[(row * a.c_in + (4 * q8 + v - a.in_off)) * HWt + qg];
                     }
                 }
                 float u[4];
@@ -663,9 +812,30 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 if (ok) {
                     lds_st128f(smem, madr, make_float4(u[0], u[1], u[2], u[3]));
                     if (REC) {  // every step's state, for the BPTT chunk
-                        float *xr = a.x_rec + (int64_t)sc * a.rec_stride + ((int64_t)row * S::C + 4 * q8) * HWn + qc;
+                        float *xr = a.x_rec + (int64_t)sc * a.rec_stride + ((int64_t)row * S::C + 4 * q8) * HWt + qg;
 #pragma unroll
-                        for (int v = 0; v < 4; ++v) xr[(int64_t)v * HWn] = u[v];
+                        for (int v = 0; v < 4; ++v) xr[(int64_t)v * HWt] = u[v];
+                        if (P > 1) {
+                            // a piece's first and last stream rows go to the exchange slots of
+                            // state sc + 1, tagged with it (single-copy atomic 8-byte words, so a
+                            // reader sees a value with its own step's tag)
+                            int side = -1, j = 0;
+                            if (qc < W && has_first) {
+                                side = 0;
+                                j = qc;
+                            } else if (qc >= HWn - W && has_last) {
+                                side = 1;
+                                j = qc - (HWn - W);
+                            }
+                            if (side >= 0) {
+                                uint64_t *xo = sp.xch + ((((row * P + piece) * 2 + side) * 4 + ((sc + 1) & 3)) * W + j) * 32 + 4 * q8;
+                                const uint64_t tag = (uint64_t)(uint32_t)(sc + 1) << 32;
+#pragma unroll
+                                for (int v = 0; v < 4; ++v)
+                                    __hip_atomic_store(xo + v, tag | __float_as_uint(u[v]), __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+                            }
+                        }
                     }
                 }
             };
@@ -709,19 +879,21 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     // ---- write back (LDS reads in batches of 8 ahead of their stores)
     {
         constexpr int kB = 8;
-        float *xr = a.x_out + row * S::C * HWn;
+        float *xr = a.x_out + row * S::C * HWt;
         const int N = S::C * HWn;
         for (int e0 = tid; e0 < N; e0 += NT * kB) {
             float v[kB];
+            int o[kB];
 #pragma unroll
             for (int k = 0; k < kB; ++k) {
                 const int e = e0 + NT * k, ec = e < N ? e : N - 1;
                 const int ch = ec / HWn, q = ec - ch * HWn;
                 v[k] = m_at(q, ch);
+                o[k] = P > 1 ? ch * HWt + g_index(q) : ec;
             }
 #pragma unroll
             for (int k = 0; k < kB; ++k)
-                if (e0 + NT * k < N) xr[e0 + NT * k] = v[k];
+                if (e0 + NT * k < N) xr[o[k]] = v[k];
         }
     }
     if (a.conf_out) {

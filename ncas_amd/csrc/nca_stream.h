@@ -17,7 +17,15 @@ bool stream32_fits(int H, int W, int padding, int c_out, int n_out, unsigned lds
 
 // Launches the streamed C = 32 kernel when the call fits it (stream32_fits, no noise, no
 // single-step fp32 mask, gated firing with the output slice in one channel quad) and sets *used;
-// otherwise leaves *used false.
-hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used);
+// otherwise leaves *used false. pieces > 1 (recording calls without per-board outputs): that many
+// workgroups per board, exchanging boundary rows through xch (stream32_xch_bytes, cleared by the
+// call).
+hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used, int pieces = 1,
+                           uint64_t *xch = nullptr);
+
+// Workgroups per board for a recording call on a device of `cus` CUs (1: whole boards), and the
+// exchange bytes that takes.
+int stream32_pieces(int64_t rows, int H, int W, int c_out, int n_out, unsigned lds_limit, int cus);
+size_t stream32_xch_bytes(int64_t rows, int P, int W);
 
 }  // namespace nca

@@ -40,16 +40,45 @@ static float conf_threshold(float tau) {
 }
 
 // One board per workgroup: needs W <= 31 (in-place update distance), H W >= W + 81 (taps loaded an
-// interval ahead hold the step's state), wall or zero padding (the border cells are constants),
+// interval ahead hold the step's state), H W <= 1024 (a step's draw is one group of 4 cells per
+// channel-wave thread), wall or zero padding (the border cells are constants),
 // for gated firing the output slice inside one channel quad and at most 4 outputs, and the plan
 // within the LDS.
 bool stream32_fits(int H, int W, int padding, int c_out, int n_out, unsigned lds_limit) {
-    if (W > 31 || H < 1 || W < 1 || H * W < W + 81 || padding == 2) return false;
+    if (W > 31 || H < 1 || W < 1 || H * W < W + 81 || H * W > 1024 || padding == 2) return false;
     const St32Plan L = st32_plan(H, W, c_out, n_out);
     return L.total <= lds_limit && L.NM < 65536;
 }
 
-hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used) {
+// Pieces per board for the recording kernel (1: whole boards). P in {3, 2} when the rows' P
+// workgroups all fit the device at once (rows P <= cus, one workgroup per CU), every piece has
+// (Hs - 1) W >= 240 (a halo refresh fits between the taps that read the old and the new row) and
+// the piece's plan fits the LDS.
+int stream32_pieces(int64_t rows, int H, int W, int c_out, int n_out, unsigned lds_limit, int cus) {
+    for (int P = 3; P >= 2; --P) {
+        const int Hp = (H + P - 1) / P, last = H - (P - 1) * Hp;
+        if (last < 1 || rows * P > cus) continue;
+        const int Hm = last < Hp ? last : Hp;
+        if ((Hm - 1) * W < 240) continue;
+        if (st32_plan(Hp, W, c_out, n_out, true).total > lds_limit) continue;
+        return P;
+    }
+    return 1;
+}
+
+size_t stream32_xch_bytes(int64_t rows, int P, int W) {
+    return P > 1 ? (size_t)rows * P * 2 * 4 * W * St32::C * sizeof(uint64_t) : 0;
+}
+
+__global__ void xch_clear(uint64_t *x, int64_t n) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x)
+        x[e] = 0;
+}
+
+// pieces > 1 (recording only): P workgroups per board exchanging their boundary rows through xch,
+// stream32_xch_bytes of device memory that this call clears before the launch
+hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used, int pieces,
+                           uint64_t *xch) {
     *used = false;
     if (p.noise || p.fire_f32) return hipSuccess;
     if (!stream32_fits(p.H, p.W, p.padding, p.c_out, p.n_out, lds_limit)) return hipSuccess;
@@ -57,10 +86,16 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
     const int hw = p.H * p.W;
     if ((int64_t)p.n_steps * hw + 64 > 0x7fffffff) return hipSuccess;
     if (p.rows > 0x7fffffff) return hipSuccess;
-    const St32Plan L = st32_plan(p.H, p.W, p.c_out, p.n_out);
+    const int P = (pieces > 1 && p.x_rec && !p.adaptive && !p.conf_out && !p.fired_out && xch) ? pieces : 1;
+    const int Hp = (p.H + P - 1) / P;
+    const St32Plan L = st32_plan(P > 1 ? Hp : p.H, p.W, p.c_out, p.n_out, P > 1);
     St32Params sp;
     memset(&sp, 0, sizeof(sp));
     sp.a = p;
+    sp.P = P;
+    sp.Hp = P > 1 ? Hp : 0;
+    sp.xch = P > 1 ? xch : nullptr;
+    sp.l_gidx = L.gidx;
     sp.NM = L.NM;
     sp.RING = L.RING;
     sp.T = (int)(((int64_t)p.n_steps * hw + 15) / 16);
@@ -80,11 +115,19 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
     if (p.x_rec && p.adaptive) return hipSuccess;  // recording is for uniform firing
     auto kfn = p.adaptive ? rollout_stream32<true, false>
                           : (p.x_rec ? rollout_stream32<false, true> : rollout_stream32<false, false>);
+    // pieces: more than half the LDS, so no two workgroups share a CU (each piece runs alongside
+    // its neighbours)
+    const unsigned lds = P > 1 && L.total <= lds_limit / 2 ? lds_limit / 2 + 16u : L.total;
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)L.total);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     if (p.rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(kfn, dim3((unsigned)p.rows), dim3(512), L.total, st, sp);
+    if (P > 1) {
+        const int64_t n = (int64_t)(stream32_xch_bytes(p.rows, P, p.W) / sizeof(uint64_t));
+        hipLaunchKernelGGL(xch_clear, dim3(256), dim3(256), 0, st, xch, n);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kfn, dim3((unsigned)(p.rows * P)), dim3(512), lds, st, sp);
     *used = true;
     return hipGetLastError();
 }

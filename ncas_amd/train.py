@@ -2,7 +2,7 @@
 its loss weights and the replay pool.
 
 * `bptt_chunk(model, x, given4, clamp, targets, weights, ...)` - forward a chunk of
-  `len(weights)` steps keeping only its states (C ABI `nca_bptt_forward`), then the fused
+  `len(weights)` steps keeping only its states (C ABI `nca_bptt_forward_ws`), then the fused
   backward that recomputes perception and hidden activations from those states
   (`nca_bptt_backward`). Returns the final state, the loss, the parameter gradients and the
   gradient of the initial state. Replaces the chunk of the reference's
@@ -124,9 +124,16 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                    step0, ss, m8)
     states = torch.empty((n + 1, B, C, H, W), dtype=torch.float32, device=dev)
     stream = _lib.stream_of(dev)
-    _lib.check(L.nca_bptt_forward(ctypes.byref(pk.desc), pk.buf.data_ptr(), B, H, W,
-                                  xs.data_ptr(), g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd),
-                                  n, states.data_ptr(), stream), "nca_bptt_forward")
+    ws_bytes = L.nca_bptt_workspace_bytes(ctypes.byref(pk.desc), B, H, W, n)
+    if ws_bytes == 0:
+        _lib.check(_lib.NCA_ERR_UNSUPPORTED, "nca_bptt_workspace_bytes")
+    ws = torch.empty((ws_bytes // 4,), dtype=torch.float32, device=dev)
+    # the forward may run boards in pieces of rows, exchanging rows through the workspace (which
+    # the backward then overwrites)
+    _lib.check(L.nca_bptt_forward_ws(ctypes.byref(pk.desc), pk.buf.data_ptr(), B, H, W,
+                                     xs.data_ptr(), g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd),
+                                     n, states.data_ptr(), ws.data_ptr(), ws_bytes, stream),
+               "nca_bptt_forward_ws")
     # fp32 master weights for the backward GEMMs (rounded to bf16 on load for bf16 cells)
     params = _params(model)
     master = [p.detach().to(dev, torch.float32).contiguous() for p in params]
@@ -137,10 +144,6 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
     gx0 = torch.empty_like(xs) if want_grad_x0 else None
     loss = torch.empty((), dtype=torch.float32, device=dev)
     lossd = _lib.BpttLoss(tg.data_ptr(), _lib.ptr(lm), w_host.ctypes.data_as(ctypes.c_void_p))
-    ws_bytes = L.nca_bptt_workspace_bytes(ctypes.byref(pk.desc), B, H, W, n)
-    if ws_bytes == 0:
-        _lib.check(_lib.NCA_ERR_UNSUPPORTED, "nca_bptt_workspace_bytes")
-    ws = torch.empty((ws_bytes // 4,), dtype=torch.float32, device=dev)
     _lib.check(L.nca_bptt_backward(ctypes.byref(pk.desc), pk.buf.data_ptr(), ctypes.byref(wts), B,
                                    H, W, states.data_ptr(), g8.data_ptr(), ctypes.byref(fd), n,
                                    ctypes.byref(lossd), _lib.ptr(gf), ctypes.byref(gs),

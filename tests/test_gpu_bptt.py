@@ -174,6 +174,55 @@ def test_bptt_forward_records_every_rollout_state(fire, size):
             assert torch.equal(states[t], y), t
 
 
+@pytest.mark.parametrize("fire", ["seed", "step_seeds", "masks"])
+@pytest.mark.parametrize("hw", [(30, 30), (20, 30), (25, 30), (30, 20)])
+def test_bptt_forward_in_pieces_equals_whole_boards(fire, hw):
+    """nca_bptt_forward_ws with a workspace runs each board in pieces of rows on two or three
+    workgroups (30x30: three pieces of 10 rows; 20x30 and 30x20: two equal pieces; 25x30: pieces
+    of 13 and 12 rows) that exchange their boundary rows every step: every recorded state equals
+    the whole-board forward's bit for bit, with Philox keys, per-step keys or injected masks."""
+    from ncas_amd.rng import fire_desc
+    H, W = hw
+    _say("bptt forward pieces", fire, H, W)
+    m = perturbed_model("maze_hard_c32", 3, *DYN["maze_hard_c32"])
+    b = maze_boards(4, 30, 3, extra_openings=0.1)
+    x, g4, cl = initial_state(m, b, k=2, sigma=0.15, seed=3)
+    x, g4, cl = (t[:, :, :H, :W].contiguous() for t in (x, g4, cl))
+    md = copy.deepcopy(m).to(DEV)
+    B, C = x.shape[:2]
+    n = 9
+    xd, cd = x.to(DEV), cl.to(DEV)
+    g8 = g4.to(DEV).to(torch.uint8).contiguous()
+    ss = m8 = None
+    if fire == "step_seeds":
+        ss = torch.as_tensor(np.arange(11, 11 + n, dtype=np.int64) * (2**33 + 7)).to(DEV)
+    if fire == "masks":
+        g = torch.Generator().manual_seed(8)
+        m8 = (torch.rand((n, B, 1, H, W), generator=g) < 0.6).to(torch.uint8).to(DEV).contiguous()
+    fd = fire_desc(6, 0.7, None, None, True, 2, 5, ss, m8)
+    pk = md.packed("bf16", DEV)
+    L = _lib.load()
+    ws_bytes = L.nca_bptt_workspace_bytes(ctypes.byref(pk.desc), B, H, W, n)
+    assert ws_bytes > 0
+    ws = torch.full((ws_bytes // 4,), float("nan"), device=DEV)
+    # two calls on the same workspace: the second, from another state, finds the first one's
+    # exchange words there (tagged with the same steps) unless the call clears them
+    for x0 in (xd, (xd * 0.5 + 0.25).contiguous()):
+        whole = torch.full((n + 1, B, C, H, W), float("nan"), device=DEV)
+        _lib.check(L.nca_bptt_forward(ctypes.byref(pk.desc), pk.buf.data_ptr(), B, H, W,
+                                      x0.data_ptr(), g8.data_ptr(), cd.data_ptr(), ctypes.byref(fd),
+                                      n, whole.data_ptr(), _lib.stream_of(DEV)), "nca_bptt_forward")
+        pieces = torch.full((n + 1, B, C, H, W), float("nan"), device=DEV)
+        _lib.check(L.nca_bptt_forward_ws(ctypes.byref(pk.desc), pk.buf.data_ptr(), B, H, W,
+                                         x0.data_ptr(), g8.data_ptr(), cd.data_ptr(),
+                                         ctypes.byref(fd), n, pieces.data_ptr(), ws.data_ptr(),
+                                         ws_bytes, _lib.stream_of(DEV)), "nca_bptt_forward_ws")
+        torch.cuda.synchronize()
+        assert not torch.isnan(whole).any()
+        for t in range(n + 1):
+            assert torch.equal(pieces[t], whole[t]), t
+
+
 def test_bptt_bf16_odd_cell_count_13x13():
     """bf16 C=32 on 13x13 boards, 3 rows (507 cells: the fused MLP backward's unaligned path, the
     streamed forward): the single-step VJP from the GPU's state within 1e-3 of the oracle and a
