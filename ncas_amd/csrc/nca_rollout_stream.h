@@ -243,10 +243,22 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
     // masks), one Philox evaluation per 4 cells
     const int nq4 = (HWn + 3) >> 2;
     const bool batched = !a.adaptive && !a.fire_u8;
+    // fired cells are counted only for a caller that asks for them
+    const bool count_fired = a.fired_out != nullptr;
+    // a batch has at most 256 items when NB > 1 (one per channel-wave thread): this thread's
+    // first item (board, step of the batch, group of 4 cells), found once
+    const int per_row = NB * nq4;
+    const int dr0 = tb >= 0 ? tb / per_row : 0, drem0 = tb - dr0 * per_row;
+    const int dsl0 = drem0 / nq4, dqq0 = drem0 - dsl0 * nq4;
     auto draw_batch = [&](const RolloutParams &pa, int b) __attribute__((always_inline)) {
-        const int per_row = NB * nq4;
         for (int it = tb; it < R * per_row; it += 256) {
-            const int r = it / per_row, rem = it - r * per_row, sl = rem / nq4, qq = rem - sl * nq4;
+            int r = dr0, sl = dsl0, qq = dqq0;
+            if (it != tb) {
+                r = it / per_row;
+                const int rem = it - r * per_row;
+                sl = rem / nq4;
+                qq = rem - sl * nq4;
+            }
             const int s = b * NB + sl;
             if (s >= pa.n_steps) continue;
             float u[4] = {1.0f, 1.0f, 1.0f, 1.0f};
@@ -264,7 +276,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                     cnt += f;
                 }
             }
-            if (cnt) atomicAdd(&firedL[r], cnt);
+            if (count_fired && cnt) atomicAdd(&firedL[r], cnt);
         }
     };
     // masks of board r for step s: adaptive gating reads the board's current state (the state
@@ -301,7 +313,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream64(StParams sp) {
                 ring_put(s, r, q, f);
                 cnt += f;
             }
-            if (cnt) atomicAdd(&firedL[r], cnt);
+            if (count_fired && cnt) atomicAdd(&firedL[r], cnt);
         }
     };
     __syncthreads();
