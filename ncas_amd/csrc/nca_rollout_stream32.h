@@ -633,8 +633,9 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             };
             // pieces: M's halo rows hold the neighbours' rows of the state the stencil reads.
             // Refresh k (k = 0 .. n_steps - 1) brings the last side's row of state k and the first
-            // side's row of state k + 1; its loads are issued in interval hB = ((k HW) >> 4) + 9,
-            // checked and stored in interval hB + 4. The last side's old row (state k - 1) was
+            // side's row of state k + 1; its loads are issued in interval hB = (((k HW) >> 4) + 9)
+            // rounded down to even, checked and stored in interval hB + 4. The last side's old
+            // row (state k - 1) was
             // last read by taps loaded before interval (k HW) >> 4 and the new one is first read
             // by the taps of step k's last row, loaded from interval ((k HW + (Hs - 1) W) >> 4) - 1
             // >= hB + 5 ((Hs - 1) W >= 240, checked by the host); the first side's old row (state
@@ -648,25 +649,27 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             const int NE = W * S::C;
             const int nf = down ? piece - 1 : piece + 1, nl = down ? piece + 1 : piece - 1;
             const int mrow_f = down ? 0 : Hs + 1, mrow_l = down ? Hs + 1 : 0;
-            int hk = 0, hB = 9;
+            int hk = 0, hB = 8;  // refresh hk's block starts at interval hB (even)
             bool hfail = false;  // a wait ran out: no later wait (the results are NaN already)
-            uint64_t hv[2][8];
             auto xslot = [&](int side, int nb, int st) -> const uint64_t * {
                 return sp.xch + (((row * P + nb) * 2 + side) * 4 + (st & 3)) * (int64_t)NE;
             };
-            auto halo_load = [&](int side, int nb, int st) __attribute__((always_inline)) {
+            // the 8 words of a thread are loaded together, unconditionally (a lane past the row
+            // reads its last word and ignores it): a conditional load gets a wait of its own
+            auto halo_load = [&](uint64_t(&hw)[8], int side, int nb, int st) __attribute__((always_inline)) {
                 const uint64_t *src = xslot(side, nb, st);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int e = th + 128 * k;
-                    hv[side][k] = e < NE ? __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+                    hw[k] = __hip_atomic_load(src + (e < NE ? e : NE - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             };
-            auto halo_store = [&](int side, int nb, int st, int mrow) __attribute__((always_inline)) {
+            auto halo_store = [&](uint64_t(&hw)[8], int side, int nb, int st, int mrow) __attribute__((always_inline)) {
                 const uint64_t *src = xslot(side, nb, st);
                 float *Mh = reinterpret_cast<float *>(smem + sp.l_M + (unsigned)(mrow * (W + 1) + 1) * S::MS);
-                // the words not yet tagged st are read again together (one round trip a try)
-                auto stale = [&](int k) { return th + 128 * k < NE && (uint32_t)(hv[side][k] >> 32) != (uint32_t)st; };
+                // while a word is not yet tagged st, the thread's words are read again together
+                // (one round trip a try)
+                auto stale = [&](int k) { return th + 128 * k < NE && (uint32_t)(hw[k] >> 32) != (uint32_t)st; };
                 for (int n = 0; !hfail; ++n) {
                     bool any = false;
 #pragma unroll
@@ -677,48 +680,71 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-                    for (int k = 0; k < 8; ++k)
-                        if (stale(k))
-                            hv[side][k] = __hip_atomic_load(src + th + 128 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    halo_load(hw, side, nb, st);  // a word already tagged st keeps its value
                 }
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const int e = th + 128 * k;
                     if (e < NE) {
-                        const uint64_t wd = hv[side][k];
+                        const uint64_t wd = hw[k];
                         Mh[e] = (uint32_t)(wd >> 32) == (uint32_t)st ? __uint_as_float((uint32_t)wd) : __builtin_nanf("");
                     }
                 }
             };
-            auto halo_ev = [&]() __attribute__((always_inline)) {
-                if (i == hB) {
-                    if (has_last && hk >= 1) halo_load(1, nl, hk);
-                    if (has_first && hk + 1 < a.n_steps) halo_load(0, nf, hk + 1);
-                } else if (i == hB + 4) {
-                    if (has_last && hk >= 1) halo_store(1, nl, hk, mrow_l);
-                    if (has_first && hk + 1 < a.n_steps) halo_store(0, nf, hk + 1, mrow_f);
-                    ++hk;
-                    hB = ((hk * HWn) >> 4) + 9;
-                }
-            };
-            i = 0;
-            while (i + 1 < T) {
+            // a refresh runs as a block of six intervals from hB: the loads in the first, the
+            // check and the stores in the fifth, so its words are not live in the other intervals
+            auto halo_block = [&]() __attribute__((always_inline)) {
+                const bool hl = has_last && hk >= 1, hf = has_first && hk + 1 < a.n_steps;
+                uint64_t hwl[8], hwf[8];
                 sinterval(P0{});
                 events();
-                if (P > 1) halo_ev();
+                if (hl) halo_load(hwl, 1, nl, hk);
+                if (hf) halo_load(hwf, 0, nf, hk + 1);
                 advance();
                 __syncthreads();
                 sinterval(P1{});
                 events();
-                if (P > 1) halo_ev();
+                advance();
+                __syncthreads();
+                sinterval(P0{});
+                events();
+                advance();
+                __syncthreads();
+                sinterval(P1{});
+                events();
+                advance();
+                __syncthreads();
+                sinterval(P0{});
+                events();
+                if (hl) halo_store(hwl, 1, nl, hk, mrow_l);
+                if (hf) halo_store(hwf, 0, nf, hk + 1, mrow_f);
+                advance();
+                __syncthreads();
+                sinterval(P1{});
+                events();
+                advance();
+                __syncthreads();
+                ++hk;
+                hB = ((((hk * HWn) >> 4) + 9) & ~1);
+            };
+            i = 0;
+            while (i + 1 < T) {
+                if (P > 1 && i == hB && hk < a.n_steps) {  // i is even here
+                    halo_block();
+                    continue;
+                }
+                sinterval(P0{});
+                events();
+                advance();
+                __syncthreads();
+                sinterval(P1{});
+                events();
                 advance();
                 __syncthreads();
             }
             if (i < T) {
                 sinterval(P0{});
                 events();
-                if (P > 1) halo_ev();
                 advance();
                 __syncthreads();
             }
@@ -734,6 +760,9 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 const float *b2 = reinterpret_cast<const float *>(a.packed + a.off_b2);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) b2v[v] = b2[4 * q8 + v];
+                // complete before the loop: a load still pending where the loop starts makes every
+                // interval wait for all vector memory operations (the state stores included)
+                asm volatile("" ::"v"(b2v));
             }
             // all ones where the lane's channel 4 q8 + v lies in the clamped input slice
             unsigned imv[4];
@@ -798,6 +827,10 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                         for (int v = 0; v < 4; ++v)
                             if (imv[v])
                                 xk[v] = a.clamp[(row * a.c_in + (4 * q8 + v - a.in_off)) * HWt + qg];
+                        // the loads complete here, in this rare branch: a wait where the paths
+                        // meet would also wait for every interval's state stores
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) asm volatile("" ::"v"(xk[v]));
                     }
                 }
                 float u[4];
