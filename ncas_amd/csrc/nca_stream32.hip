@@ -118,8 +118,10 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
     // pieces: more than half the LDS, so no two workgroups share a CU (each piece runs alongside
     // its neighbours)
     const unsigned lds = P > 1 && L.total <= lds_limit / 2 ? lds_limit / 2 + 16u : L.total;
+    // the attribute is the limit for every launch of the function (whole boards and pieces take
+    // different sizes), so calls from several host threads cannot undercut one another's
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit);
     if (e != hipSuccess) return e;
     if (p.rows <= 0) return hipSuccess;
     if (P > 1) {
