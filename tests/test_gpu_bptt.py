@@ -223,6 +223,42 @@ def test_bptt_forward_in_pieces_equals_whole_boards(fire, hw):
             assert torch.equal(pieces[t], whole[t]), t
 
 
+@pytest.mark.parametrize("padding,n,rows", [("zero", 1, 8), ("zero", 2, 8), ("wall", 3, 100), ("wall", 2, 130)])
+def test_bptt_forward_in_pieces_edges(padding, n, rows):
+    """Random 30x30 states: chunks of 1 step (no exchange) and 2 (one exchange) with zero
+    padding; 100 rows (three pieces would need 300 CUs, so fewer) and 130 rows (whole boards on a
+    256-CU device). nca_bptt_forward_ws records the whole-board forward's states bit for bit."""
+    from ncas_amd.rng import fire_desc
+    _say("bptt forward pieces edges", padding, n, rows)
+    kw = {"padding": padding}
+    if padding != "wall":
+        kw["wall_token"] = None
+    m = perturbed_model("maze_hard_c32", 5, *DYN["maze_hard_c32"], **kw)
+    md = copy.deepcopy(m).to(DEV)
+    g = torch.Generator().manual_seed(rows * 10 + n)
+    H = W = 30
+    x = (torch.randn((rows, 32, H, W), generator=g) * 0.3).to(DEV)
+    g8 = (torch.rand((rows, 1, H, W), generator=g) < 0.3).to(torch.uint8).to(DEV).contiguous()
+    cl = torch.randn((rows, m.cfg.c_in, H, W), generator=g).to(DEV)
+    fd = fire_desc(9, 0.7, None, None, True, 0, 3, None, None)
+    pk = md.packed("bf16", DEV)
+    L = _lib.load()
+    whole = torch.full((n + 1, rows, 32, H, W), float("nan"), device=DEV)
+    _lib.check(L.nca_bptt_forward(ctypes.byref(pk.desc), pk.buf.data_ptr(), rows, H, W, x.data_ptr(),
+                                  g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd), n, whole.data_ptr(),
+                                  _lib.stream_of(DEV)), "nca_bptt_forward")
+    ws_bytes = L.nca_bptt_workspace_bytes(ctypes.byref(pk.desc), rows, H, W, n)
+    ws = torch.full((ws_bytes // 4,), float("nan"), device=DEV)
+    pieces = torch.full_like(whole, float("nan"))
+    _lib.check(L.nca_bptt_forward_ws(ctypes.byref(pk.desc), pk.buf.data_ptr(), rows, H, W, x.data_ptr(),
+                                     g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd), n, pieces.data_ptr(),
+                                     ws.data_ptr(), ws_bytes, _lib.stream_of(DEV)), "nca_bptt_forward_ws")
+    torch.cuda.synchronize()
+    assert not torch.isnan(whole).any()
+    for t in range(n + 1):
+        assert torch.equal(pieces[t], whole[t]), t
+
+
 def test_bptt_bf16_odd_cell_count_13x13():
     """bf16 C=32 on 13x13 boards, 3 rows (507 cells: the fused MLP backward's unaligned path, the
     streamed forward): the single-step VJP from the GPU's state within 1e-3 of the oracle and a
