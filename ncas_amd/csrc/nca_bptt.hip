@@ -575,24 +575,6 @@ __device__ __forceinline__ void plane_taps(const float *xs, const Dims &d, int i
     }
 }
 
-// The 4 features of channel c at cell q (row `row`) from the staged plane xs: z[k] = the sum of
-// kernel k's taps in tap order (the forward's order), bf16 for bf16 cells.
-template <bool Z16>
-__device__ __forceinline__ void plane_z(const float *xs, const Dims &d, const float *kern, float hv, int64_t row, int c,
-                                        int q, float *Z) {
-    const int i = q / d.W, j = q - i * d.W;
-    float xv[9];
-    plane_taps(xs, d, i, j, hv, xv);
-    const int64_t m = row * d.HW + q;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
-        z_store<Z16>(Z, (int64_t)(k * d.C + c) * d.M + m, d.bf16 ? nca::round_bf16(acc) : acc);
-    }
-}
-
 // stencil_z for boards of at most kPlaneMax cells: workgroup p stages plane p = (row, channel)
 // of x in LDS and writes that channel's 4 features of the row's cells.
 template <bool Z16>
@@ -600,30 +582,86 @@ __device__ void z_plane_body(const Dims &d, const float *__restrict__ x, const f
                              const float *__restrict__ padv, float *__restrict__ Z, int pl, float *xs) {
     const int row = pl / d.C, c = pl - row * d.C;
     const float *xr = x + (int64_t)pl * d.HW;
-    // staged 8 cells per thread at a time, every load issued before the LDS writes
-    for (int q0 = 0; q0 < d.HW; q0 += 8 * kThreads) {
+    const int H = d.H, W = d.W, W2 = W + 2, N2 = (H + 2) * W2;
+    const float hv = d.padding == 1 ? padv[c] : 0.0f;
+    const bool wrap = d.padding == 2;
+    // the plane with a one-cell border (the padding value, or the wrapped cells) in LDS,
+    // (H + 2) x (W + 2), each value rounded to bf16 once for bf16 cells; 8 cells per thread at a
+    // time, every load issued before the LDS writes
+    for (int e0 = 0; e0 < N2; e0 += 8 * kThreads) {
         float v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int q = q0 + u * kThreads + threadIdx.x;
-            v[u] = xr[q < d.HW ? q : 0];
+            const int e = e0 + u * kThreads + threadIdx.x;
+            const int bi = e / W2 - 1, bj = e - (bi + 1) * W2 - 1;
+            const bool in = bi >= 0 && bi < H && bj >= 0 && bj < W;
+            const int ai = bi < 0 ? H - 1 : (bi >= H ? 0 : bi), aj = bj < 0 ? W - 1 : (bj >= W ? 0 : bj);
+            const bool take = e < N2 && (in || wrap);
+            const float xv = xr[take ? ai * W + aj : 0];
+            v[u] = take ? xv : hv;
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int q = q0 + u * kThreads + threadIdx.x;
-            if (q < d.HW) xs[q] = v[u];
+            const int e = e0 + u * kThreads + threadIdx.x;
+            if (e < N2) xs[e] = d.bf16 ? nca::round_bf16(v[u]) : v[u];
         }
     }
     __syncthreads();
-    const float hv = d.padding == 1 ? padv[c] : 0.0f;
-    for (int q = threadIdx.x; q < d.HW; q += kThreads) plane_z<Z16>(xs, d, kern, hv, row, c, q, Z);
+    // the 4 features of cell (i, j) from its 3x3 window, taps in the forward's order
+    auto cell = [&](int i, int j, const float (&w0)[3], const float (&w1)[3], const float (&w2)[3]) {
+        const float xv[9] = {w0[0], w0[1], w0[2], w1[0], w1[1], w1[2], w2[0], w2[1], w2[2]};
+        const int64_t m = row * d.HW + i * W + j;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 9; ++t) acc = __builtin_fmaf(kern[k * 9 + t], xv[t], acc);
+            z_store<Z16>(Z, (int64_t)(k * d.C + c) * d.M + m, d.bf16 ? nca::round_bf16(acc) : acc);
+        }
+    };
+    if (W <= kThreads) {
+        // thread (band, column j) walks down rows [band R, band R + R) of column j with the window
+        // in registers, reading one new row of 3 values per cell
+        const int bands = kThreads / W, j = threadIdx.x % W, band = threadIdx.x / W;
+        if (band >= bands) return;
+        const int R = (H + bands - 1) / bands, i0 = band * R, i1 = i0 + R < H ? i0 + R : H;
+        if (i0 >= i1) return;
+        float w0[3], w1[3], w2[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            w0[k] = xs[i0 * W2 + j + k];  // bordered row i0 - 1 + 1
+            w1[k] = xs[(i0 + 1) * W2 + j + k];
+        }
+        for (int i = i0; i < i1; ++i) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) w2[k] = xs[(i + 2) * W2 + j + k];
+            cell(i, j, w0, w1, w2);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                w0[k] = w1[k];
+                w1[k] = w2[k];
+            }
+        }
+    } else {
+        for (int q = threadIdx.x; q < d.HW; q += kThreads) {
+            const int i = q / W, j = q - i * W;
+            float w0[3], w1[3], w2[3];
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                w0[k] = xs[i * W2 + j + k];
+                w1[k] = xs[(i + 1) * W2 + j + k];
+                w2[k] = xs[(i + 2) * W2 + j + k];
+            }
+            cell(i, j, w0, w1, w2);
+        }
+    }
 }
 
 template <bool Z16>
 __global__ void __launch_bounds__(kThreads) stencil_z_plane(Dims d, const float *__restrict__ x,
                                                             const float *__restrict__ kern,
                                                             const float *__restrict__ padv, float *__restrict__ Z) {
-    extern __shared__ float xs[];  // HW floats
+    extern __shared__ float xs[];  // (H + 2) (W + 2) floats
     z_plane_body<Z16>(d, x, kern, padv, Z, blockIdx.x, xs);
 }
 
@@ -633,7 +671,7 @@ template <int NO>
 __global__ void __launch_bounds__(kThreads) front_z_kernel(FrontArgs a, const float *__restrict__ x,
                                                            const float *__restrict__ kern,
                                                            const float *__restrict__ padv, float *__restrict__ Z) {
-    extern __shared__ float xs[];  // HW floats (z workgroups)
+    extern __shared__ float xs[];  // (H + 2) (W + 2) floats (z workgroups)
     __shared__ float red[(kThreads / 64) * 32];
     __shared__ float hwL[NO * NO + NO];
     const int nf = kSplit * (a.d.C / kFrontCh);
@@ -1159,6 +1197,8 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
     const bool planes_ok = planes_fit(d);
     // ... and walked by columns for boards at most 256 wide (kernel-weight slot per 4 planes)
     const bool strips_ok = planes_ok && d.W <= kThreads;
+    // the z workgroups' bordered plane
+    const size_t zlds = (size_t)(d.H + 2) * (d.W + 2) * sizeof(float);
     const int64_t strip_blocks = (d.rows * d.C + kStripPlanes - 1) / kStripPlanes;
     // cells per workgroup of the fused kernel: whole 32-cell tiles
     const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
@@ -1205,12 +1245,12 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         if (fused && planes_ok) {  // front and z in one launch
             auto fz = no <= 4 ? front_z_kernel<4> : no <= 8 ? front_z_kernel<8> : front_z_kernel<16>;
             hipLaunchKernelGGL(fz, dim3((unsigned)(kSplit * (d.C / kFrontCh) + d.rows * d.C)), dim3(kThreads),
-                               d.HW * sizeof(float), st, fa, xt, kern, padv, Z);
+                               zlds, st, fa, xt, kern, padv, Z);
         } else if (planes_ok) {
             auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
             hipLaunchKernelGGL(front, dim3(kSplit, d.C / kFrontCh), dim3(kThreads), 0, st, fa);
             auto zfn = fused ? stencil_z_plane<true> : stencil_z_plane<false>;
-            hipLaunchKernelGGL(zfn, dim3((unsigned)(d.rows * d.C)), dim3(kThreads), d.HW * sizeof(float), st, d, xt, kern,
+            hipLaunchKernelGGL(zfn, dim3((unsigned)(d.rows * d.C)), dim3(kThreads), zlds, st, d, xt, kern,
                                padv, Z);
         } else {
             auto front = no <= 4 ? front_kernel<4> : no <= 8 ? front_kernel<8> : front_kernel<16>;
