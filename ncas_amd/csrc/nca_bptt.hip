@@ -945,6 +945,21 @@ __global__ void copy_kernel(const float *src, float *dst, int64_t n) {
         dst[i] = src[i];
 }
 
+// The summed parameter gradients (contiguous in acc) out to the caller's tensors, one launch:
+// segment k is n[k] floats from acc + off[k] to dst[k] (null: skipped).
+struct GradOut {
+    float *dst[7];
+    int64_t off[7], n[7];
+};
+
+__global__ void grads_out_kernel(const float *acc, GradOut g) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+#pragma unroll
+    for (int k = 0; k < 7; ++k)
+        if (g.dst[k])
+            for (int64_t i = t; i < g.n[k]; i += stride) g.dst[k][i] = acc[g.off[k] + i];
+}
+
 // ------------------------------------------------------------------------------------------
 // fp32 GEMM on v_mfma_f32_16x16x4_f32: C (M x N) = A (M x K) B (K x N) with strided operands
 // (A(m, k) = A[m sam + k sak], B(k, n) = B[k sbk + n sbn], one of each pair of strides being 1),
@@ -1344,15 +1359,16 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         }
     }
     // the gradients in the reference's parameter layouts
-    hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.K, grads->kernels, (int64_t)36);
-    hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, acc + P.W1, grads->w1, (int64_t)d.HD * d.F);
-    hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.B1, grads->b1, (int64_t)d.HD);
-    hipLaunchKernelGGL(copy_kernel, dim3(64), dim3(256), 0, st, acc + P.W2, grads->w2, (int64_t)d.C * d.HD);
-    hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(256), 0, st, acc + P.B2, grads->b2, (int64_t)d.C);
-    if (grads->head_w)
-        hipLaunchKernelGGL(copy_kernel, dim3(4), dim3(256), 0, st, acc + P.HW, grads->head_w, (int64_t)d.n_out * d.c_out);
-    if (grads->head_b)
-        hipLaunchKernelGGL(copy_kernel, dim3(1), dim3(64), 0, st, acc + P.HB, grads->head_b, (int64_t)d.n_out);
+    GradOut go;
+    float *gdst[7] = {grads->kernels, grads->w1, grads->b1, grads->w2, grads->b2, grads->head_w, grads->head_b};
+    const int64_t goff[7] = {P.K, P.W1, P.B1, P.W2, P.B2, P.HW, P.HB};
+    const int64_t gn[7] = {36, (int64_t)d.HD * d.F, d.HD, (int64_t)d.C * d.HD, d.C, (int64_t)d.n_out * d.c_out, d.n_out};
+    for (int k = 0; k < 7; ++k) {
+        go.dst[k] = gdst[k];
+        go.off[k] = goff[k];
+        go.n[k] = gn[k];
+    }
+    hipLaunchKernelGGL(grads_out_kernel, dim3(128), dim3(256), 0, st, acc, go);
     if (loss_out) {
         if (n_chunk > 0 && d.M > 0)
             hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossacc, loss_out);
