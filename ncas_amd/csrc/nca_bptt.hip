@@ -926,9 +926,18 @@ __global__ void __launch_bounds__(kThreads) rowsum_kernel(const float *__restric
 
 // acc[i] = the sum of the kSplit slots in slot order.
 __global__ void reduce_acc_kernel(const float *part, int64_t P, float *acc) {
+    // slot order; 64 slots' loads issued before their additions (4 round trips for 256 slots)
+    constexpr int kB = 64;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < P; i += (int64_t)gridDim.x * blockDim.x) {
         float s = 0.0f;
-        for (int k = 0; k < kSplit; ++k) s = __fadd_rn(s, part[k * P + i]);
+        for (int k0 = 0; k0 < kSplit; k0 += kB) {
+            float v[kB];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) v[k] = k0 + k < kSplit ? part[(int64_t)(k0 + k) * P + i] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < kB; ++k)
+                if (k0 + k < kSplit) s = __fadd_rn(s, v[k]);
+        }
         acc[i] = s;
     }
 }
@@ -1218,7 +1227,7 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
     // cells per workgroup of the fused kernel: whole 32-cell tiles
     const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
     if (fused)
-        hipLaunchKernelGGL(nca::mlp_back32_prep, dim3(1), dim3(512), 0, st, w->w1, w->w2,
+        hipLaunchKernelGGL(nca::mlp_back32_prep, dim3(nca::kMb32PrepBlocks), dim3(512), 0, st, w->w1, w->w2,
                            reinterpret_cast<unsigned char *>(ws + L.img));
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
     if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;

@@ -103,28 +103,28 @@ __device__ __forceinline__ bf16x8 mb_cat(s16x4 lo, s16x4 hi) {
 
 // The weight image of mlp_back32 from the fp32 master weights (rounded to bf16): the register
 // fragments of every (wave, lane): W1 for fc1, W2 for g_a, and W1^T for g_z (the A operand of
-// feature tile w, hidden block kb in perm order). One workgroup of 512 threads.
+// feature tile w, hidden block kb in perm order). 18 workgroups of 512 threads, one per fragment
+// of a lane (W1 [ht][kb]: 0-7, W2 [ht]: 8-9, W1^T [kb]: 10-17), so that a thread's chain is one
+// fragment's 8 loads.
+constexpr int kMb32PrepBlocks = 18;
+
 __global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const float *w2, unsigned char *img) {
     typedef Mb32 S;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
+    const int f = blockIdx.x;
+    float v[8];
+    if (f < 8) {
+        const int ht = f >> 2, kb = f & 3, hid = 32 * w + 16 * ht + r;
 #pragma unroll
-    for (int ht = 0; ht < 2; ++ht) {
-        const int hid = 32 * w + 16 * ht + r;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = w1[hid * 128 + 32 * kb + 8 * g + j];
-            *reinterpret_cast<bf16x8 *>(img + S::IMG_W1F + (tid * 8 + 4 * ht + kb) * 16) = mb_pack8(v);
-        }
-        float v[8];
+        for (int j = 0; j < 8; ++j) v[j] = w1[hid * 128 + 32 * kb + 8 * g + j];
+        *reinterpret_cast<bf16x8 *>(img + S::IMG_W1F + (tid * 8 + 4 * ht + kb) * 16) = mb_pack8(v);
+    } else if (f < 10) {
+        const int ht = f - 8, hid = 32 * w + 16 * ht + r;
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = w2[(8 * g + j) * 256 + hid];
         *reinterpret_cast<bf16x8 *>(img + S::IMG_W2F + (tid * 2 + ht) * 16) = mb_pack8(v);
-    }
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb) {
-        float v[8];
+    } else {
+        const int kb = f - 10;
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = w1[(32 * kb + mb_perm(g, j)) * 128 + 16 * w + r];
         *reinterpret_cast<bf16x8 *>(img + S::IMG_W1TF + (tid * 8 + kb) * 16) = mb_pack8(v);
