@@ -99,8 +99,8 @@ nca::PackedLayout layout_of(const nca_cell_desc *d) {
 
 // ------------------------------------------------------------------------------------------
 // Weight packing
-__global__ void pack_small(const float *src, int n, float *dst, int round_bf16) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+__device__ __forceinline__ void pack_small(const float *src, int n, float *dst, int round_bf16, int b, int nb) {
+    for (int i = b * blockDim.x + threadIdx.x; i < n; i += nb * blockDim.x) {
         const float v = src ? src[i] : 0.0f;
         dst[i] = round_bf16 ? nca::round_bf16(v) : v;
     }
@@ -109,11 +109,11 @@ __global__ void pack_small(const float *src, int n, float *dst, int round_bf16) 
 // A fragments of an (M x K) row-major matrix (M, K multiples of 16 and of the k-tile). qC > 0
 // (bf16 only) reorders the k axis quad-major: fragment column k = 16 iq + 4 head + ch reads
 // matrix column head * qC + 4 iq + ch.
-__global__ void pack_frags(const float *src, int M, int K, int bf16, int qC, void *dst) {
+__device__ __forceinline__ void pack_frags(const float *src, int M, int K, int bf16, int qC, void *dst, int b, int nb) {
     const int total = M * K;
     const int ktile = bf16 ? 32 : 4;
     const int nkt = K / ktile;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    for (int e = b * blockDim.x + threadIdx.x; e < total; e += nb * blockDim.x) {
         int m, k;
         if (bf16) {
             const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
@@ -134,10 +134,10 @@ __global__ void pack_frags(const float *src, int M, int K, int bf16, int qC, voi
 
 // fc2 fragments of the streamed kernel (see nca_layout.h), bf16: the k axis follows the order in
 // which fc1's accumulators are stored, p = 64 w + 16 g + 4 mt + v -> hidden 64 w + 16 mt + 4 g + v.
-__global__ void pack_w2h(const float *w2, int C, int HD, __bf16 *dst) {
+__device__ __forceinline__ void pack_w2h(const float *w2, int C, int HD, __bf16 *dst, int b, int nb) {
     const int nkt = HD / 32;
     const int total = C * HD;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    for (int e = b * blockDim.x + threadIdx.x; e < total; e += nb * blockDim.x) {
         const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
         const int kt = blk % nkt, m = blk / nkt;
         const int ch = 16 * m + (lane & 15);
@@ -150,15 +150,50 @@ __global__ void pack_w2h(const float *w2, int C, int HD, __bf16 *dst) {
 // fc2 fragments per hidden quarter (see nca_layout.h), bf16: the k axis of quarter q follows the
 // order of fc1's accumulators in the wave that owns it, slot s of lane group g of k-tile k ->
 // hidden q HD/4 + 16 (2 k + s / 4) + 4 g + s % 4.
-__global__ void pack_w2k(const float *w2, int C, int HD, __bf16 *dst) {
+__device__ __forceinline__ void pack_w2k(const float *w2, int C, int HD, __bf16 *dst, int b, int nb) {
     const int hpw = HD / 4, kt2n = hpw / 32, mt2n = C / 16;
     const int total = C * HD;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    for (int e = b * blockDim.x + threadIdx.x; e < total; e += nb * blockDim.x) {
         const int s = e & 7, lane = (e >> 3) & 63, blk = e >> 9;
         const int kt = blk % kt2n, m2 = (blk / kt2n) % mt2n, q = blk / (kt2n * mt2n);
         const int ch = 16 * m2 + (lane & 15);
         const int hid = q * hpw + 16 * (2 * kt + s / 4) + 4 * (lane >> 4) + (s % 4);
         dst[e] = (__bf16)w2[(size_t)ch * HD + hid];
+    }
+}
+
+// The whole packing in one launch: workgroups [64 k, 64 k + 64) build fragment layout k (W1, W2,
+// and for bf16 cells W2 for the hidden-major fc2, W1 quad-major, W2 k-major), the last one the
+// small vectors (kernels, b1, b2, head, padding value).
+struct PackArgs {
+    const float *kernels, *w1, *b1, *w2, *b2, *head_w, *head_b, *pad_vec;
+    int nk, HD, C, F, nhw, nhb, bf;
+    unsigned char *pk;
+    nca::PackedLayout L;
+};
+
+__global__ void pack_all(PackArgs a) {
+    constexpr int kPB = 64;
+    const int b = blockIdx.x, part = b / kPB, pb = b - part * kPB;
+    const int nfrag = a.bf ? 5 : 2;
+    unsigned char *pk = a.pk;
+    if (part >= nfrag) {
+        pack_small(a.kernels, a.nk, reinterpret_cast<float *>(pk + a.L.kern), a.bf, 0, 1);
+        pack_small(a.b1, a.HD, reinterpret_cast<float *>(pk + a.L.b1), a.bf, 0, 1);
+        pack_small(a.b2, a.C, reinterpret_cast<float *>(pk + a.L.b2), a.bf, 0, 1);
+        pack_small(a.head_w, a.nhw, reinterpret_cast<float *>(pk + a.L.headw), 0, 0, 1);
+        pack_small(a.head_b, a.nhb, reinterpret_cast<float *>(pk + a.L.headb), 0, 0, 1);
+        pack_small(a.pad_vec, a.C, reinterpret_cast<float *>(pk + a.L.padv), 0, 0, 1);
+    } else if (part == 0) {
+        pack_frags(a.w1, a.HD, a.F, a.bf, 0, (void *)(pk + a.L.w1), pb, kPB);
+    } else if (part == 1) {
+        pack_frags(a.w2, a.C, a.HD, a.bf, 0, (void *)(pk + a.L.w2), pb, kPB);
+    } else if (part == 2) {
+        pack_w2h(a.w2, a.C, a.HD, reinterpret_cast<__bf16 *>(pk + a.L.w2h), pb, kPB);
+    } else if (part == 3) {
+        pack_frags(a.w1, a.HD, a.F, 1, a.C, (void *)(pk + a.L.w1q), pb, kPB);
+    } else {
+        pack_w2k(a.w2, a.C, a.HD, reinterpret_cast<__bf16 *>(pk + a.L.w2k), pb, kPB);
     }
 }
 
@@ -656,22 +691,26 @@ int nca_pack_weights(const nca_cell_desc *cell, const nca_cell_weights *w, void 
     hipStream_t st = as_stream(stream);
     unsigned char *pk = static_cast<unsigned char *>(packed);
     const int C = cell->channels, HD = cell->hidden, F = cell->heads * C;
-    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->kernels, cell->heads * 9,
-                       reinterpret_cast<float *>(pk + L.kern), (int)bf);
-    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->b1, HD, reinterpret_cast<float *>(pk + L.b1), (int)bf);
-    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->b2, C, reinterpret_cast<float *>(pk + L.b2), (int)bf);
-    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->head_w, cell->n_out * cell->c_out,
-                       reinterpret_cast<float *>(pk + L.headw), 0);
-    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->head_b, cell->n_out,
-                       reinterpret_cast<float *>(pk + L.headb), 0);
-    hipLaunchKernelGGL(pack_small, dim3(1), dim3(256), 0, st, w->pad_vec, C, reinterpret_cast<float *>(pk + L.padv), 0);
-    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, (int)bf, 0, (void *)(pk + L.w1));
-    hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w2, C, HD, (int)bf, 0, (void *)(pk + L.w2));
-    if (bf) {
-        hipLaunchKernelGGL(pack_w2h, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2h));
-        hipLaunchKernelGGL(pack_frags, dim3(64), dim3(256), 0, st, w->w1, HD, F, 1, C, (void *)(pk + L.w1q));
-        hipLaunchKernelGGL(pack_w2k, dim3(64), dim3(256), 0, st, w->w2, C, HD, reinterpret_cast<__bf16 *>(pk + L.w2k));
-    }
+    PackArgs pa;
+    memset(&pa, 0, sizeof(pa));
+    pa.kernels = w->kernels;
+    pa.w1 = w->w1;
+    pa.b1 = w->b1;
+    pa.w2 = w->w2;
+    pa.b2 = w->b2;
+    pa.head_w = w->head_w;
+    pa.head_b = w->head_b;
+    pa.pad_vec = w->pad_vec;
+    pa.nk = cell->heads * 9;
+    pa.HD = HD;
+    pa.C = C;
+    pa.F = F;
+    pa.nhw = cell->n_out * cell->c_out;
+    pa.nhb = cell->n_out;
+    pa.bf = bf ? 1 : 0;
+    pa.pk = pk;
+    pa.L = L;
+    hipLaunchKernelGGL(pack_all, dim3((bf ? 5 : 2) * 64 + 1), dim3(256), 0, st, pa);
     return hip_check(hipGetLastError(), "pack launch");
 }
 
