@@ -125,13 +125,14 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         // wall / zero padding the wrapped cell is loaded and replaced), and the halo flags
         const int ro[3] = {i > 0 ? -W : (H - 1) * W, 0, i < H - 1 ? W : -(H - 1) * W};
         const int co[3] = {j > 0 ? -1 : W - 1, 0, j < W - 1 ? 1 : -(W - 1)};
-        const bool rp[3] = {i == 0 && !wrap, false, i == H - 1 && !wrap};
-        const bool cp[3] = {j == 0 && !wrap, false, j == W - 1 && !wrap};
-        in.padm = 0;
+        // halo taps: the top row of taps (bits 0-2), the bottom (6-8), the left column (0, 3, 6),
+        // the right (2, 5, 8)
+        in.padm = wrap ? 0
+                       : ((i == 0 ? 0x007 : 0) | (i == H - 1 ? 0x1c0 : 0) | (j == 0 ? 0x049 : 0) |
+                          (j == W - 1 ? 0x124 : 0));
 #pragma unroll
         for (int tt = 0; tt < 9; ++tt) {
             const int dy = tt / 3, dx = tt % 3;
-            in.padm |= (rp[dy] || cp[dx]) ? 1 << tt : 0;
             if (IN_NCHW) {
                 const float *xr = a.x_in + (row * C + 4 * g) * (int64_t)HWn + qc + ro[dy] + co[dx];
                 in.tp[tt] = float4{xr[0], xr[HWn], xr[2 * HWn], xr[3 * HWn]};
@@ -176,9 +177,18 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     auto unpack = [&](const TileIn &in, TileCur &cu) __attribute__((always_inline)) {
 #pragma unroll
         for (int tt = 0; tt < 9; ++tt) {
-            const bool pad = (in.padm >> tt) & 1;
-            cu.tb[tt][0] = pad ? pqb[0] : pack_bf16x2(in.tp[tt].x, in.tp[tt].y);
-            cu.tb[tt][1] = pad ? pqb[1] : pack_bf16x2(in.tp[tt].z, in.tp[tt].w);
+            cu.tb[tt][0] = pack_bf16x2(in.tp[tt].x, in.tp[tt].y);
+            cu.tb[tt][1] = pack_bf16x2(in.tp[tt].z, in.tp[tt].w);
+        }
+        // the padding value replaces halo taps only in tiles with a cell on the grid's edge (a
+        // branch uniform over the wave; most tiles have none)
+        if (__builtin_amdgcn_ballot_w64(in.padm != 0)) {
+#pragma unroll
+            for (int tt = 0; tt < 9; ++tt) {
+                const bool pad = (in.padm >> tt) & 1;
+                cu.tb[tt][0] = pad ? pqb[0] : cu.tb[tt][0];
+                cu.tb[tt][1] = pad ? pqb[1] : cu.tb[tt][1];
+            }
         }
         cu.xo[0] = in.tp[4].x;
         cu.xo[1] = in.tp[4].y;
