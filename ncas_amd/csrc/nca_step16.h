@@ -83,7 +83,6 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     }
     const float4 pq = a.padding == 1 ? reinterpret_cast<const float4 *>(a.packed + a.off_padv)[g]
                                      : float4{0.f, 0.f, 0.f, 0.f};
-    const uint32_t pqb[2] = {pack_bf16x2(pq.x, pq.y), pack_bf16x2(pq.z, pq.w)};
     const uint64_t key = a.step_seeds ? a.step_seeds[sp.step] : a.seed;
     __syncthreads();
 
@@ -167,28 +166,36 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         fired_run = 0;
     };
 
-    // what the compute of a tile keeps of its loads: the taps as bf16 pairs (halo taps replaced
-    // by the padding value), the cell's fp32 quad, flags and mask / clamp values
+    // what the compute of a tile keeps of its loads: the taps as bf16 pairs of one channel (taps
+    // 2p and 2p + 1, tap 8 with a zero; halo taps replaced by the padding value), the cell's fp32
+    // quad, flags and mask / clamp values
     struct TileCur {
-        uint32_t tb[9][2];
+        uint32_t pr[5][4];  // [tap pair][channel]
         float xo[4], fin, cv[4];
         int gv, fu8;
     };
     auto unpack = [&](const TileIn &in, TileCur &cu) __attribute__((always_inline)) {
+        auto pack = [&](const float4 *tp) __attribute__((always_inline)) {
 #pragma unroll
-        for (int tt = 0; tt < 9; ++tt) {
-            cu.tb[tt][0] = pack_bf16x2(in.tp[tt].x, in.tp[tt].y);
-            cu.tb[tt][1] = pack_bf16x2(in.tp[tt].z, in.tp[tt].w);
-        }
-        // the padding value replaces halo taps only in tiles with a cell on the grid's edge (a
-        // branch uniform over the wave; most tiles have none)
-        if (__builtin_amdgcn_ballot_w64(in.padm != 0)) {
-#pragma unroll
-            for (int tt = 0; tt < 9; ++tt) {
-                const bool pad = (in.padm >> tt) & 1;
-                cu.tb[tt][0] = pad ? pqb[0] : cu.tb[tt][0];
-                cu.tb[tt][1] = pad ? pqb[1] : cu.tb[tt][1];
+            for (int p2 = 0; p2 < 4; ++p2) {
+                cu.pr[p2][0] = pack_bf16x2(tp[2 * p2].x, tp[2 * p2 + 1].x);
+                cu.pr[p2][1] = pack_bf16x2(tp[2 * p2].y, tp[2 * p2 + 1].y);
+                cu.pr[p2][2] = pack_bf16x2(tp[2 * p2].z, tp[2 * p2 + 1].z);
+                cu.pr[p2][3] = pack_bf16x2(tp[2 * p2].w, tp[2 * p2 + 1].w);
             }
+            cu.pr[4][0] = pack_bf16x2(tp[8].x, 0.0f);
+            cu.pr[4][1] = pack_bf16x2(tp[8].y, 0.0f);
+            cu.pr[4][2] = pack_bf16x2(tp[8].z, 0.0f);
+            cu.pr[4][3] = pack_bf16x2(tp[8].w, 0.0f);
+        };
+        pack(in.tp);
+        // tiles with a cell on the grid's edge pack again with the padding value in place of the
+        // halo taps (a branch uniform over the wave; most tiles have none)
+        if (__builtin_amdgcn_ballot_w64(in.padm != 0)) {
+            float4 tp[9];
+#pragma unroll
+            for (int tt = 0; tt < 9; ++tt) tp[tt] = ((in.padm >> tt) & 1) ? pq : in.tp[tt];
+            pack(tp);
         }
         cu.xo[0] = in.tp[4].x;
         cu.xo[1] = in.tp[4].y;
@@ -227,20 +234,7 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
 
         // 2. perception: bf16 tap pairs per channel, v_dot2 against the kernel pairs
         {
-            const uint32_t(&tb)[9][2] = cur.tb;  // taps as bf16 pairs (channels 0,1 and 2,3)
-            uint32_t pr[5][4];  // [tap pair][channel]
-#pragma unroll
-            for (int p2 = 0; p2 < 4; ++p2) {
-                const uint32_t *x0 = tb[2 * p2], *x1 = tb[2 * p2 + 1];
-                pr[p2][0] = __builtin_amdgcn_perm(x1[0], x0[0], 0x05040100u);
-                pr[p2][1] = __builtin_amdgcn_perm(x1[0], x0[0], 0x07060302u);
-                pr[p2][2] = __builtin_amdgcn_perm(x1[1], x0[1], 0x05040100u);
-                pr[p2][3] = __builtin_amdgcn_perm(x1[1], x0[1], 0x07060302u);
-            }
-            pr[4][0] = tb[8][0] & 0xffffu;
-            pr[4][1] = tb[8][0] >> 16;
-            pr[4][2] = tb[8][1] & 0xffffu;
-            pr[4][3] = tb[8][1] >> 16;
+            const uint32_t(&pr)[5][4] = cur.pr;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 float z[4];
@@ -349,7 +343,8 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         // alive across its new loads, and the compiler then carries the buffer in two register
         // sets copied at the end of every iteration (38 moves per tile)
 #pragma unroll
-        for (int tt = 0; tt < 9; ++tt) asm volatile("" : "+v"(cu.tb[tt][0]), "+v"(cu.tb[tt][1]));
+        for (int p2 = 0; p2 < 5; ++p2)
+            asm volatile("" : "+v"(cu.pr[p2][0]), "+v"(cu.pr[p2][1]), "+v"(cu.pr[p2][2]), "+v"(cu.pr[p2][3]));
         asm volatile("" : "+v"(cu.xo[0]), "+v"(cu.xo[1]), "+v"(cu.xo[2]), "+v"(cu.xo[3]));
         asm volatile("" : "+v"(cu.fin), "+v"(cu.gv), "+v"(cu.fu8));
         if (FIRST) asm volatile("" : "+v"(cu.cv[0]), "+v"(cu.cv[1]), "+v"(cu.cv[2]), "+v"(cu.cv[3]));
