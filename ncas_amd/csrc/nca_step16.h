@@ -207,25 +207,25 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) cu.cv[v] = in.cv[v];
     };
-    // Philox fire bits of 4 tiles at a time: lane (r, g) draws cell r of the wave's tile g tiles
-    // ahead (one evaluation per cell quad, its element r & 3: tiles start at multiples of 16
-    // cells), and a ballot gives bit 16 k + r = cell r of tile k
-    uint64_t fmask = 0;
+    // Philox fire bits of 16 tiles at a time: lane L evaluates cell quad L & 3 of the wave's tile
+    // L >> 2 tiles ahead (tiles start at multiples of 16 cells; all four of an evaluation's
+    // uniforms are used), and ballot e gives bit 4 k + j = cell 4 j + e of tile k
+    uint64_t fb[4] = {0, 0, 0, 0};
     int kgrp = 0;
     const int tpr = sp.tiles_per_row;
-    auto draw4 = [&](int64_t row, int tir) {
-        int ti = tir + 8 * g;
+    const int fbit = 4 * (r & 3) + (r >> 2);  // cell r's bit in a tile's 16-bit mask
+    auto draw16 = [&](int64_t row, int tir) {
+        int ti = tir + 8 * (lane >> 2);
         int64_t rw = row;
         while (ti >= tpr) {
             ti -= tpr;
             ++rw;
         }
         float u4[4];
-        const uint32_t qd = (uint32_t)((16 * ti + r) >> 2);
-        cell_uniforms4(key, (uint32_t)(a.row0 + rw), (uint32_t)(a.step0 + sp.step), qd, u4);
-        const int e4 = r & 3;
-        const float uq = e4 == 0 ? u4[0] : e4 == 1 ? u4[1] : e4 == 2 ? u4[2] : u4[3];
-        fmask = __ballot(uq < a.p);
+        cell_uniforms4(key, (uint32_t)(a.row0 + rw), (uint32_t)(a.step0 + sp.step), (uint32_t)(4 * ti + (lane & 3)),
+                       u4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) fb[e] = __ballot(u4[e] < a.p);
     };
     // one tile: the cells' new states to x_out
     auto process = [&](const TileCur &cur, int64_t row, int tir) __attribute__((always_inline)) {
@@ -283,7 +283,11 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         } else if (a.fire_u8) {
             f = cur.fu8 ? 1.0f : 0.0f;
         } else {
-            f = ((fmask >> (16 * kgrp + r)) & 1ull) ? 1.0f : 0.0f;
+            // tile kgrp's 16 bits, cell 4 j + e at bit 4 e + j (the same for every lane)
+            uint32_t m16 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) m16 |= (uint32_t)((fb[e] >> (4 * kgrp)) & 0xfull) << (4 * e);
+            f = ((m16 >> fbit) & 1u) ? 1.0f : 0.0f;
         }
         const bool gv = cur.gv != 0;
         float xo[4] = {cur.xo[0], cur.xo[1], cur.xo[2], cur.xo[3]};
@@ -356,9 +360,9 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         // join makes the compiler wait for them before the tile's compute
         const bool more = t + 8 < t_end;
         load_tile(more ? rn : row, more ? tn : tir, nx);
-        if (philox && kgrp == 0) draw4(row, tir);
+        if (philox && kgrp == 0) draw16(row, tir);
         process(cu, row, tir);
-        kgrp = (kgrp + 1) & 3;
+        kgrp = (kgrp + 1) & 15;
         row = rn;
         tir = tn;
     }
