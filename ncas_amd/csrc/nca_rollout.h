@@ -390,9 +390,9 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    float s = 0.0f;
+                    float s = dot2_bf16_zero(pr[0][c], kp[k][0]);
 #pragma unroll
-                    for (int p2 = 0; p2 < 5; ++p2)
+                    for (int p2 = 1; p2 < 5; ++p2)
                         s = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), s, false);
                     acc[k][c] = s;
                 }
@@ -597,9 +597,9 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
 #pragma unroll
             for (int j = kt * CH; j < (kt + 1) * CH && j < 16; ++j) {
                 const int k = j >> 2, c = j & 3;
-                float sum = 0.0f;
+                float sum = dot2_bf16_zero(pr[0][c], kp[k][0]);
 #pragma unroll
-                for (int p2 = 0; p2 < 5; ++p2)
+                for (int p2 = 1; p2 < 5; ++p2)
                     sum = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), sum, false);
                 zs[j] = sum;
             }

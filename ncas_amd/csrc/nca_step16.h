@@ -240,10 +240,7 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
                 float z[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    // the chain opens with the three-operand form and a zero accumulator operand
-                    // (the two-operand v_dot2c form needs the zero moved into its destination)
-                    float s;
-                    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(s) : "v"(pr[0][c]), "v"(kp[k][0]));
+                    float s = dot2_bf16_zero(pr[0][c], kp[k][0]);
 #pragma unroll
                     for (int p2 = 1; p2 < 5; ++p2)
                         s = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), s, false);

@@ -219,9 +219,9 @@ __global__ void __launch_bounds__(256, 1) step_tiled(TiledParams tp) {
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    float s = 0.0f;
+                    float s = dot2_bf16_zero(pr[0][c], kp[k][0]);
 #pragma unroll
-                    for (int p2 = 0; p2 < 5; ++p2)
+                    for (int p2 = 1; p2 < 5; ++p2)
                         s = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), s, false);
                     acc[k][c] = s;
                 }

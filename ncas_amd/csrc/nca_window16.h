@@ -284,9 +284,9 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
                     float z[4];
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        float sacc = 0.0f;
+                        float sacc = dot2_bf16_zero(pr[0][c], kp[k][0]);
 #pragma unroll
-                        for (int p2 = 0; p2 < 5; ++p2)
+                        for (int p2 = 1; p2 < 5; ++p2)
                             sacc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), sacc, false);
                         z[c] = sacc;
                     }
