@@ -46,6 +46,10 @@
  *   nca_step_backward_workspace_bytes <- nothing in the reference (autograd allocates)
  *   nca_prune_select  <- niche_capped_pruning (src/nca/pruning.py:22-65) at the pruning steps of
  *                        rollout() (src/nca/rollout.py:249-275)
+ *   nca_prune_select_rows <- the same on rollout()'s compacted batch (rollout.py:249-271)
+ *   nca_maze_metrics  <- the maze tasks' "valid" / "optimal" metrics (src/nca/tasks/maze.py:
+ *                        251-295, 843-866)
+ *   nca_sudoku_valid  <- the Sudoku tasks' "valid" metric (src/nca/tasks/sudoku.py:151, 987-995)
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -162,6 +166,37 @@ int nca_rollout_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, 
 int nca_prune_select(const int32_t *decoded, const float *conf, const uint8_t *alive,
                      int32_t n_boards, int32_t k_trials, int32_t cells, int32_t n_cap,
                      uint64_t seed, int64_t event, uint8_t *alive_out, void *stream);
+
+/* The same selection on a compacted batch (the rows rollout() still runs after earlier pruning
+ * steps, src/nca/rollout.py:249-271): decoded (n_rows, cells) int32 and conf (n_rows) of the
+ * alive trials only, row_trial (n_rows) int64 the flat (board, trial) index board * k_trials +
+ * trial of each row, strictly increasing. keep (n_rows) gets 1 for the rows whose trial
+ * survives. Results equal nca_prune_select's on the full layout with the absent trials dead. */
+int nca_prune_select_rows(const int32_t *decoded, const float *conf, const int64_t *row_trial,
+                          int64_t n_rows, int32_t n_boards, int32_t k_trials, int32_t cells,
+                          int32_t n_cap, uint64_t seed, int64_t event, uint8_t *keep,
+                          void *stream);
+
+/* Task metrics of decoded boards, one value per row; row r belongs to board r / k_per_board of
+ * the per-board arrays (k_per_board = K scores an (N, K) rollout result without repeating the
+ * boards). Device buffers: pred (rows, H, W) int64 tokens; inputs / targets (boards, H, W)
+ * int64; given (boards, H, W) {0,1}; outputs (rows) {0,1}.
+ *
+ * nca_maze_metrics <- _MazeTask._metrics' "valid" / "optimal" (src/nca/tasks/maze.py:843-866)
+ * with path_validity (maze.py:251-295): the predicted path (pred == path_token on non-given
+ * cells, plus the inputs' endpoint cells, tokens end_token_a / end_token_b) is one simple
+ * 4-connected path between exactly two endpoints ("valid"), and as long as the target path,
+ * i.e. the target's path_token cells plus the endpoints ("optimal"). (H + 2) * (W + 2) <= 65536. */
+int nca_maze_metrics(const int64_t *pred, const int64_t *inputs, const int64_t *targets,
+                     const uint8_t *given, int64_t rows, int32_t k_per_board, int32_t height,
+                     int32_t width, int64_t path_token, int64_t end_token_a,
+                     int64_t end_token_b, uint8_t *valid, uint8_t *optimal, void *stream);
+
+/* nca_sudoku_valid <- SudokuOOD.metrics' "valid" (src/nca/tasks/sudoku.py:987-995) with
+ * is_valid_solution (sudoku.py:151-164): the grid filled with the inputs on given cells and pred
+ * elsewhere has values 1..9 and every row, column and 3x3 box holds each digit once. 9x9 boards. */
+int nca_sudoku_valid(const int64_t *pred, const int64_t *inputs, const uint8_t *given,
+                     int64_t rows, int32_t k_per_board, uint8_t *valid, void *stream);
 
 /* Host-side batched board generation (the inputs of the workloads), on `threads` host threads
  * (0 = all). Every board draws from its own Philox4x32-10 stream keyed on `seed`, so the

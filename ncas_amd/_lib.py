@@ -41,6 +41,9 @@ EXPORTS = (
     "nca_step_backward",
     "nca_rollout_noalloc",
     "nca_prune_select",
+    "nca_prune_select_rows",
+    "nca_maze_metrics",
+    "nca_sudoku_valid",
     "nca_maze_boards",
     "nca_sudoku_boards",
 )
@@ -156,6 +159,10 @@ def load():
         ctypes.POINTER(CellGrads), vp, vp, ctypes.c_size_t, vp,
     ]
     L.nca_prune_select.argtypes = [vp, vp, vp, i32, i32, i32, i32, ctypes.c_uint64, i64, vp, vp]
+    L.nca_prune_select_rows.argtypes = [vp, vp, vp, i64, i32, i32, i32, i32, ctypes.c_uint64,
+                                        i64, vp, vp]
+    L.nca_maze_metrics.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, i64, i64, i64, vp, vp, vp]
+    L.nca_sudoku_valid.argtypes = [vp, vp, vp, i64, i32, vp, vp]
     L.nca_maze_boards.argtypes = [i64, i32, ctypes.c_uint64, ctypes.c_double, i32, i32, vp, vp, vp,
                                   vp, i32]
     L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]

@@ -33,6 +33,7 @@ SOURCES = {
     # mlp_back32 keeps its weight fragments in AGPRs and its accumulators in VGPRs
     "nca_bptt.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_prune.hip": [],
+    "nca_metrics.hip": [],
     "nca_boards.cpp": [],
 }
 
@@ -51,13 +52,20 @@ def _run(cmd, verbose):
         print(errs, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link the shared library; always recompiles."""
-    objs = []
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every HIP source (in parallel, `jobs` compilers at once) and link the shared
+    library; always recompiles."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objs, cmds = [], []
     for src, extra in SOURCES.items():
         obj = os.path.join(CSRC, os.path.splitext(src)[0] + ".o")
-        _run([HIPCC, *FLAGS, *extra, "-I", INCLUDE, "-c", "-o", obj, os.path.join(CSRC, src)], verbose)
+        cmds.append([HIPCC, *FLAGS, *extra, "-I", INCLUDE, "-c", "-o", obj, os.path.join(CSRC, src)])
         objs.append(obj)
+    jobs = jobs or min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(jobs) as ex:
+        for fut in [ex.submit(_run, cmd, verbose) for cmd in cmds]:
+            fut.result()
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
     for obj in objs:

@@ -29,11 +29,31 @@ namespace {
 constexpr int kPruneThreads = 256;
 constexpr int kPruneMaxK = 1024;
 
+// First index r in [0, n) with v[r] >= key (v increasing).
+__device__ __forceinline__ int64_t lower_bound(const int64_t *v, int64_t n, int64_t key) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (v[mid] < key) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// COMPACT = false: the (n_boards, K) layout, trial k of board n at row n * K + k, alive flags in
+// `alive`, the new alive mask written to out[n * K + k].
+// COMPACT = true: only the alive trials are present, as rows whose flat (board, trial) index
+// board * K + trial is row_trial[row] (strictly increasing over the rows); out[row] is 1 when
+// the row's trial survives.
+template <bool COMPACT>
 __global__ void __launch_bounds__(kPruneThreads) prune_kernel(const int32_t *__restrict__ dec,
                                                                const float *__restrict__ conf,
-                                                               const uint8_t *__restrict__ alive, int K,
-                                                               int cells, int n_cap, uint64_t seed, uint32_t event,
-                                                               uint8_t *__restrict__ alive_out) {
+                                                               const uint8_t *__restrict__ alive,
+                                                               const int64_t *__restrict__ row_trial,
+                                                               int64_t n_rows, int K, int cells, int n_cap,
+                                                               uint64_t seed, uint32_t event,
+                                                               uint8_t *__restrict__ out) {
+    __shared__ int src[kPruneMaxK];     // row holding trial k, -1 when the trial is not alive
     __shared__ unsigned long long hsh[kPruneMaxK];
     __shared__ float cf[kPruneMaxK];
     __shared__ int rep[kPruneMaxK];     // niche representative of an alive trial, -1 if dead
@@ -42,41 +62,60 @@ __global__ void __launch_bounds__(kPruneThreads) prune_kernel(const int32_t *__r
     __shared__ int npos[kPruneMaxK];    // position of the niche (representatives only)
     __shared__ int n_alive_s, n_capped_s;
     const int n = blockIdx.x, tid = threadIdx.x;
-    const int32_t *db = dec + (int64_t)n * K * cells;
+    const int64_t base = (int64_t)n * K;
     if (tid == 0) {
         n_alive_s = 0;
         n_capped_s = 0;
     }
+    if (COMPACT) {
+        for (int k = tid; k < K; k += kPruneThreads) src[k] = -1;
+        __syncthreads();
+        const int64_t lo = lower_bound(row_trial, n_rows, base), hi = lower_bound(row_trial, n_rows, base + K);
+        for (int64_t r = lo + tid; r < hi; r += kPruneThreads) {
+            const int64_t t = row_trial[r] - base;
+            if (t >= 0 && t < K) src[t] = (int)r;
+        }
+    } else {
+        for (int k = tid; k < K; k += kPruneThreads) src[k] = alive[base + k] ? (int)(base + k) : -1;
+    }
     __syncthreads();
     // hash of every alive trial's board
     for (int k = tid; k < K; k += kPruneThreads) {
-        const bool al = alive[(int64_t)n * K + k] != 0;
+        const int s = src[k];
         unsigned long long h = 1469598103934665603ull;
-        if (al) {
-            const int32_t *b = db + (int64_t)k * cells;
-            for (int c = 0; c < cells; ++c) {
-                h ^= (uint32_t)b[c];
+        float c = 0.0f;
+        if (s >= 0) {
+            const int32_t *b = dec + (int64_t)s * cells;
+            for (int q = 0; q < cells; ++q) {
+                h ^= (uint32_t)b[q];
                 h *= 1099511628211ull;
             }
+            c = conf[s];
             atomicAdd(&n_alive_s, 1);
         }
         hsh[k] = h;
-        cf[k] = conf[(int64_t)n * K + k];
-        rep[k] = al ? k : -1;
+        cf[k] = c;
+        rep[k] = s >= 0 ? k : -1;
     }
     __syncthreads();
     const int n_alive = n_alive_s;
     if (n_alive <= 1) {
-        for (int k = tid; k < K; k += kPruneThreads) alive_out[(int64_t)n * K + k] = alive[(int64_t)n * K + k];
+        for (int k = tid; k < K; k += kPruneThreads) {
+            if (COMPACT) {
+                if (src[k] >= 0) out[src[k]] = 1;
+            } else {
+                out[base + k] = src[k] >= 0 ? 1 : 0;
+            }
+        }
         return;
     }
     // representative: the first alive trial with the same board
     for (int k = tid; k < K; k += kPruneThreads) {
         if (rep[k] < 0) continue;
-        const int32_t *bk = db + (int64_t)k * cells;
+        const int32_t *bk = dec + (int64_t)src[k] * cells;
         for (int j = 0; j < k; ++j) {
             if (rep[j] < 0 || hsh[j] != hsh[k]) continue;
-            const int32_t *bj = db + (int64_t)j * cells;
+            const int32_t *bj = dec + (int64_t)src[j] * cells;
             bool same = true;
             for (int c = 0; c < cells && same; ++c) same = bj[c] == bk[c];
             if (same) {
@@ -129,7 +168,11 @@ __global__ void __launch_bounds__(kPruneThreads) prune_kernel(const int32_t *__r
             }
             keep = rank < keep_n;
         }
-        alive_out[(int64_t)n * K + k] = keep ? 1 : 0;
+        if (COMPACT) {
+            if (src[k] >= 0) out[src[k]] = keep ? 1 : 0;
+        } else {
+            out[base + k] = keep ? 1 : 0;
+        }
     }
 }
 
@@ -146,7 +189,26 @@ extern "C" int nca_prune_select(const int32_t *decoded, const float *conf, const
     if (!decoded || !conf || !alive || !alive_out) return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
     if (event < 0 || event > 0xffffffffll) return nca::set_error(NCA_ERR_INVALID, "event out of range");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(prune_kernel, dim3((unsigned)n_boards), dim3(kPruneThreads), 0, st, decoded, conf, alive,
-                       (int)k_trials, (int)cells, (int)n_cap, seed, (uint32_t)event, alive_out);
+    hipLaunchKernelGGL(prune_kernel<false>, dim3((unsigned)n_boards), dim3(kPruneThreads), 0, st, decoded, conf,
+                       alive, (const int64_t *)nullptr, (int64_t)0, (int)k_trials, (int)cells, (int)n_cap, seed,
+                       (uint32_t)event, alive_out);
+    return nca::hip_status(hipGetLastError(), "prune launch");
+}
+
+extern "C" int nca_prune_select_rows(const int32_t *decoded, const float *conf, const int64_t *row_trial,
+                                     int64_t n_rows, int32_t n_boards, int32_t k_trials, int32_t cells,
+                                     int32_t n_cap, uint64_t seed, int64_t event, uint8_t *keep, void *stream) {
+    nca::clear_error();
+    if (n_rows < 0 || n_boards < 0 || k_trials < 1 || cells < 1 || n_cap < 1)
+        return nca::set_error(NCA_ERR_INVALID, "n_rows >= 0, n_boards >= 0, k_trials >= 1, cells >= 1, n_cap >= 1");
+    if (k_trials > kPruneMaxK) return nca::set_error(NCA_ERR_UNSUPPORTED, "pruning takes at most 1024 trials per board");
+    if (n_rows > (int64_t)n_boards * k_trials) return nca::set_error(NCA_ERR_INVALID, "more rows than (board, trial) pairs");
+    if (n_rows == 0 || n_boards == 0) return NCA_OK;
+    if (!decoded || !conf || !row_trial || !keep) return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    if (event < 0 || event > 0xffffffffll) return nca::set_error(NCA_ERR_INVALID, "event out of range");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(prune_kernel<true>, dim3((unsigned)n_boards), dim3(kPruneThreads), 0, st, decoded, conf,
+                       (const uint8_t *)nullptr, row_trial, n_rows, (int)k_trials, (int)cells, (int)n_cap, seed,
+                       (uint32_t)event, keep);
     return nca::hip_status(hipGetLastError(), "prune launch");
 }

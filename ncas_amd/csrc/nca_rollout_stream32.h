@@ -665,7 +665,6 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 }
             };
             auto halo_store = [&](uint64_t(&hw)[8], int side, int nb, int st, int mrow) __attribute__((always_inline)) {
-                const uint64_t *src = xslot(side, nb, st);
                 float *Mh = reinterpret_cast<float *>(smem + sp.l_M + (unsigned)(mrow * (W + 1) + 1) * S::MS);
                 // while a word is not yet tagged st, the thread's words are read again together
                 // (one round trip a try)

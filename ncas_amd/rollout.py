@@ -64,8 +64,9 @@ class RolloutResult:
     trace_cell_acc: np.ndarray | None
     trace_conf: np.ndarray | None
     trace_updates: np.ndarray | None
-    boards_trace: np.ndarray | None = None
+    boards_trace: np.ndarray | None = None  # (record_boards, T, H, W) trial 0's decodes
     damage_masks: np.ndarray | None = None
+    metrics: dict | None = None  # task metrics of the final boards, name -> (N, K)
 
     @property
     def n_boards(self) -> int:
@@ -81,22 +82,6 @@ def decode_tokens(model, x, given, inputs, fill_given: bool = True):
     return (torch.where(given, inputs, dec) if fill_given else dec), conf
 
 
-class _Scorer:
-    """Per-row scores of a pass, on the device: decoded board, cell accuracy and exactness over
-    the scored cells, board confidence (reference rollout.py:181-184)."""
-
-    def __init__(self, model, task, inputs, targets, given, scored):
-        self.model, self.inputs, self.targets, self.given = model, inputs, targets, given
-        self.fill_given = getattr(task, "fill_given", True)
-        self.scored = scored
-        self.n_scored = scored.sum(dim=(1, 2)).clamp_min(1)
-
-    def __call__(self, x):
-        dec, conf = decode_tokens(self.model, x, self.given, self.inputs, self.fill_given)
-        correct = ((dec == self.targets) & self.scored).sum(dim=(1, 2))
-        return dec, correct / self.n_scored, correct == self.n_scored, conf
-
-
 def _eval_mask(task, boards) -> np.ndarray:
     """The scored cells (reference tasks/base.py:126-132): the task's eval_mask, by default the
     mutable cells."""
@@ -105,25 +90,141 @@ def _eval_mask(task, boards) -> np.ndarray:
     return ~boards.given
 
 
+class _Batch:
+    """The rows one pass of `rollout` still runs, on the device: the state and its clamp, the
+    boards' tokens repeated per trial, the fired-cell counts and `flat`, the (board, trial) index
+    of each row in the whole result (board-major, reference rollout.py:143-146). Dropping rows
+    (pruning) keeps every per-row tensor aligned."""
+
+    ROW_KEYS = ("x", "given4", "clamp", "inputs", "targets", "given", "scored", "updates", "flat")
+
+    def __init__(self, model, task, **rows):
+        self.model, self.task = model, task
+        self.fill_given = getattr(task, "fill_given", True)
+        for k in self.ROW_KEYS:
+            setattr(self, k, rows[k])
+
+    def __len__(self) -> int:
+        return self.x.shape[0]
+
+    def score(self) -> tuple[torch.Tensor, torch.Tensor, dict]:
+        """(decoded boards, board confidence, task metrics) of the current states; the metrics
+        are the task's per-row device metrics (exact, cell_acc, and e.g. valid / optimal)."""
+        dec, conf = decode_tokens(self.model, self.x, self.given, self.inputs, self.fill_given)
+        metrics = self.task.device_metrics(dec, self.inputs, self.targets, self.given,
+                                           self.scored)
+        return dec, conf, metrics
+
+    def keep(self, rows: torch.Tensor) -> None:
+        """Keep only `rows` (a sorted index tensor), in order."""
+        for k in self.ROW_KEYS:
+            setattr(self, k, getattr(self, k).index_select(0, rows))
+        self.x = self.x.contiguous()
+
+
+class _Outputs:
+    """Everything a rollout reports, on the device until `to_host`: the final decode, confidence,
+    alive flag, fired counts and task metrics per (board, trial) row, the per-record-step traces
+    and the decoded boards of trial 0 of the first `n_boards_trace` boards."""
+
+    TRACES = (("exact", torch.bool), ("cell", torch.float32), ("conf", torch.float32),
+              ("upd", torch.float64))
+
+    def __init__(self, rows: int, H: int, W: int, T: int, n_boards_trace: int, device):
+        self.rows, self.T, self.device = rows, T, device
+        self.pred = torch.empty((rows, H, W), dtype=torch.int64, device=device)
+        self.conf = torch.empty((rows,), dtype=torch.float32, device=device)
+        self.upd = torch.empty((rows,), dtype=torch.float64, device=device)
+        self.alive = torch.ones((rows,), dtype=torch.bool, device=device)
+        self.metrics: dict[str, torch.Tensor] = {}
+        self.trace = ({k: torch.zeros((rows, T), dtype=dt, device=device) for k, dt in self.TRACES}
+                      if T else None)
+        self.boards = (torch.zeros((n_boards_trace, T, H, W), dtype=torch.int64, device=device)
+                       if n_boards_trace and T else None)
+
+    def final(self, b: _Batch, rows: torch.Tensor, dec, conf, metrics, t_from: int) -> None:
+        """The last values of the batch rows `rows` (positions in b): a trajectory that ends
+        before the last record step keeps them in the later trace columns."""
+        flat = b.flat[rows]
+        self.pred[flat] = dec[rows]
+        self.conf[flat] = conf[rows]
+        self.upd[flat] = b.updates[rows]
+        for name, v in metrics.items():
+            if name not in self.metrics:
+                self.metrics[name] = torch.zeros((self.rows,), dtype=v.dtype, device=self.device)
+            self.metrics[name][flat] = v[rows]
+        if self.trace is not None and t_from < self.T:
+            vals = (metrics["exact"], metrics["cell_acc"].float(), conf, b.updates)
+            for (k, _), v in zip(self.TRACES, vals):
+                self.trace[k][flat, t_from:] = v[rows][:, None]
+
+    def record(self, b: _Batch, t_rec: int, dec, conf, metrics, K: int, board0: int,
+               n_boards: int) -> None:
+        """Trace column t_rec of the batch's rows, and trial 0's decoded board of the traced
+        boards among the pass's boards board0 .. board0 + n_boards - 1 (reference
+        rollout.py:277-288)."""
+        for (k, _), v in zip(self.TRACES, (metrics["exact"], metrics["cell_acc"].float(), conf,
+                                            b.updates)):
+            self.trace[k][b.flat, t_rec] = v
+        nb = 0 if self.boards is None else min(n_boards, self.boards.shape[0] - board0)
+        if nb > 0:
+            # the current decodes go into the result first, so a trial 0 pruned earlier shows
+            # its last decode, as in the reference
+            self.pred[b.flat] = dec
+            first = torch.arange(board0, board0 + nb, device=self.device) * K
+            self.boards[board0:board0 + nb, t_rec] = self.pred[first]
+
+    def to_host(self, N: int, K: int, H: int, W: int, steps) -> RolloutResult:
+        host = lambda t: t.cpu().numpy()  # noqa: E731
+        tr = self.trace
+        return RolloutResult(
+            host(self.pred).reshape(N, K, H, W), host(self.conf).reshape(N, K),
+            host(self.alive).reshape(N, K), host(self.upd).reshape(N, K), np.array(steps),
+            *((host(tr[k]).reshape(N, K, self.T) for k, _ in self.TRACES) if tr is not None
+              else (None, None, None, None)),
+            boards_trace=None if self.boards is None else host(self.boards),
+            metrics={k: host(v).reshape(N, K) for k, v in self.metrics.items()},
+        )
+
+
+def _schedule(rc: RolloutConfig) -> tuple[list[int], set[int]]:
+    """(record steps, pruning steps). Record every `record_every` steps and at the end (reference
+    rollout.py:116-118); prune at the m - 1 equidistant steps i * (depth // m), i = 1 .. m - 1,
+    which never include step 0 (reference rollout.py:163-167, 249)."""
+    steps = []
+    if rc.record_every > 0:
+        steps = list(range(rc.record_every, rc.depth + 1, rc.record_every))
+        if not steps or steps[-1] != rc.depth:
+            steps.append(rc.depth)
+    prune = set()
+    if rc.pruning:
+        m = int(rc.pruning["m"])
+        prune = {i * (rc.depth // m) for i in range(1, m)} - {0}
+    return steps, prune
+
+
 @torch.no_grad()
 def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None,
             progress: bool = False) -> RolloutResult:
     """Run every board `rc.k` times (reference rollout.py:86-306). With `rc.pruning`
     ({"m", "n_cap"}) the ensemble of each board is halved at m - 1 equidistant steps
-    (`pruning.prune_select`) and the pruned trajectories leave the batch (rows compacted on the
-    GPU); a pruned trajectory keeps its last state's decode, confidence and counts, also in the
-    traces of the later record steps. After a pruning step the surviving rows are renumbered
-    0, 1, ... in the pass for the Philox row counter."""
+    (`pruning.prune_select_rows` on the running rows) and the pruned trajectories leave the batch;
+    a pruned trajectory keeps its last state's decode, confidence, counts and metrics, also in
+    the traces of the later record steps. After a pruning step the surviving rows are
+    renumbered 0, 1, ... in the pass for the Philox row counter. `rc.record_boards` keeps trial
+    0's decoded board of the first boards at every record step (`boards_trace`)."""
     if rc.noise is not None or rc.damage_at is not None:
         raise ValueError("test-time noise and damage are not implemented by the HIP rollout")
     if task_ids is not None or model.cfg.time_steps:
         raise ValueError("task / time embeddings are not implemented by the HIP rollout")
-    from .pruning import prune_select
+    from .pruning import prune_select_rows
+    from .tasks import Task
 
     model.eval()
     device = model.device
     if device.type != "cuda":
         raise ValueError("the HIP rollout needs the model on the GPU")
+    task = task if task is not None else Task()
     N = len(boards)
     H, W = boards.shape
     K = rc.k
@@ -131,100 +232,64 @@ def rollout(model, task, boards, rc: RolloutConfig, seed: int = 0, task_ids=None
     gen = torch.Generator(device=device)
     gen.manual_seed(seed)
     precision = "bf16" if rc.amp else "fp32"
-    record = rc.record_every > 0
-    steps = list(range(rc.record_every, rc.depth + 1, rc.record_every)) if record else []
-    if record and (not steps or steps[-1] != rc.depth):
-        steps.append(rc.depth)
-    T = len(steps)
-    prune_steps, n_cap = set(), 3
-    if rc.pruning:
-        m = int(rc.pruning["m"])
-        n_cap = int(rc.pruning.get("n_cap", 3))
-        stride = rc.depth // m
-        prune_steps = {i * stride for i in range(1, m)}
+    steps, prune_steps = _schedule(rc)
+    n_cap = int(rc.pruning.get("n_cap", 3)) if rc.pruning else 3
     bounds = sorted({rc.depth, *steps, *prune_steps})
-    rows_total = N * K
-    # every output lives on the device until the end of the call
-    pred = torch.empty((rows_total, H, W), dtype=torch.int64, device=device)
-    conf_out = torch.empty((rows_total,), dtype=torch.float32, device=device)
-    upd_out = torch.empty((rows_total,), dtype=torch.float64, device=device)
-    alive_out = torch.ones((rows_total,), dtype=torch.bool, device=device)
-    tr = {k: torch.zeros((rows_total, T), dtype=dt, device=device) for k, dt in
-          (("exact", torch.bool), ("cell", torch.float32), ("conf", torch.float32),
-           ("upd", torch.float64))} if record else None
+    out = _Outputs(N * K, H, W, len(steps), rc.record_boards, device)
     scored_all = _eval_mask(task, boards)
     event = 0
     for start in range(0, N, per_pass):
         stop_b = min(N, start + per_pass)
-        n = stop_b - start
-        sub = boards.subset(np.arange(start, stop_b))
         base = start * K
-        inputs = _lib.upload(np.repeat(sub.inputs, K, 0), device)
-        targets = _lib.upload(np.repeat(sub.targets, K, 0), device)
-        given = _lib.upload(np.repeat(sub.given, K, 0), device)
-        scored = _lib.upload(np.repeat(scored_all[start:stop_b], K, 0), device)
+        sub = boards.subset(np.arange(start, stop_b))
+        up = lambda a: _lib.upload(np.repeat(a, K, 0), device)  # noqa: E731
+        inputs, given = up(sub.inputs), up(sub.given)
         x, given4, clamp = model.init_state(inputs, given, None, gen)
-        x = x.float().contiguous()
-        B = n * K
-        idx = torch.arange(base, base + B, device=device)  # flat (board, trial) row of each row
-        updates = torch.zeros(B, dtype=torch.float64, device=device)
+        B = len(sub) * K
+        b = _Batch(model, task, x=x.float().contiguous(), given4=given4, clamp=clamp,
+                   inputs=inputs, targets=up(sub.targets), given=given,
+                   scored=up(scored_all[start:stop_b]),
+                   updates=torch.zeros(B, dtype=torch.float64, device=device),
+                   flat=torch.arange(base, base + B, device=device))
         t, t_rec = 0, 0
-
-        def store(rows, dec, cell, exact, conf, upd, t_from):
-            pred[rows] = dec
-            conf_out[rows] = conf
-            upd_out[rows] = upd
-            if record and t_from < T:
-                tr["exact"][rows, t_from:] = exact[:, None]
-                tr["cell"][rows, t_from:] = cell.float()[:, None]
-                tr["conf"][rows, t_from:] = conf[:, None]
-                tr["upd"][rows, t_from:] = upd[:, None]
-
         for stop in bounds:
-            x, _, fired = rollout_steps(
-                model, x, given4, clamp, stop - t, seed=seed, p_fire=rc.fire_rate,
+            b.x, _, fired = rollout_steps(
+                model, b.x, b.given4, b.clamp, stop - t, seed=seed, p_fire=rc.fire_rate,
                 p_low=rc.p_low, tau=rc.tau, given_confident=rc.given_confident,
-                row0=base, step0=t, precision=precision, out=x, want_conf=False,
+                row0=base, step0=t, precision=precision, out=b.x, want_conf=False,
                 want_fired=True,
             )
-            updates += fired.double()
+            b.updates += fired.double()
             t = stop
-            score = _Scorer(model, task, inputs, targets, given, scored)
+            scores = None
             if stop in prune_steps:
-                dec, cell, exact, conf = score(x)
-                local = idx - base  # row of the (board, trial) in the pass's full layout
-                dec_full = torch.zeros((B, H, W), dtype=torch.int64, device=device)
-                conf_full = torch.full((B,), -float("inf"), device=device)
-                alive_full = torch.zeros(B, dtype=torch.bool, device=device)
-                dec_full[local], conf_full[local], alive_full[local] = dec, conf, True
-                keep = prune_select(dec_full.view(n, K, H * W), conf_full.view(n, K),
-                                    alive_full.view(n, K), n_cap, seed, event).view(B)[local]
+                scores = b.score()
+                dec, conf, _ = scores
+                keep = prune_select_rows(dec, conf, b.flat - base, len(sub), K, n_cap, seed,
+                                         event)
                 event += 1
-                drop = ~keep
-                store(idx[drop], dec[drop], cell[drop], exact[drop], conf[drop], updates[drop],
-                      t_rec)
-                alive_out[idx[drop]] = False
-                sel = keep.nonzero().squeeze(1)  # one host wait per pruning step
-                x, given4, clamp = x[sel].contiguous(), given4[sel], clamp[sel]
-                inputs, targets, given, scored = inputs[sel], targets[sel], given[sel], scored[sel]
-                updates, idx = updates[sel], idx[sel]
-                score = _Scorer(model, task, inputs, targets, given, scored)
-            if record and t_rec < T and stop == steps[t_rec]:
-                _, cell, exact, conf = score(x)
-                tr["exact"][idx, t_rec] = exact
-                tr["cell"][idx, t_rec] = cell.float()
-                tr["conf"][idx, t_rec] = conf
-                tr["upd"][idx, t_rec] = updates
+                gone = (~keep).nonzero().squeeze(1)  # one host wait per pruning step
+                if len(gone):
+                    out.final(b, gone, *scores, t_rec)
+                    out.alive[b.flat[gone]] = False
+                    b.keep(keep.nonzero().squeeze(1))
+                    scores = None
+            if t_rec < len(steps) and stop == steps[t_rec]:
+                out.record(b, t_rec, *(scores or b.score()), K, start, len(sub))
                 t_rec += 1
-        dec, cell, exact, conf = _Scorer(model, task, inputs, targets, given, scored)(x)
-        store(idx, dec, cell, exact, conf, updates, T)
-    host = lambda t: t.cpu().numpy()  # noqa: E731
-    return RolloutResult(
-        host(pred).reshape(N, K, H, W), host(conf_out).reshape(N, K),
-        host(alive_out).reshape(N, K), host(upd_out).reshape(N, K), np.array(steps),
-        *((host(tr[k]).reshape(N, K, T) for k in ("exact", "cell", "conf", "upd")) if record
-          else (None, None, None, None)),
-    )
+        out.final(b, torch.arange(len(b), device=device), *b.score(), len(steps))
+    return out.to_host(N, K, H, W, steps)
+
+
+def score_candidates(task, res: RolloutResult, boards) -> dict[str, np.ndarray]:
+    """Task metrics of every (board, trial) of a rollout result: dict of (N, K) arrays
+    (reference rollout.py:309-314). `rollout` computes them on the GPU with the final states;
+    for a result without them they are computed from `res.pred` on the GPU."""
+    if res.metrics:
+        return res.metrics
+    N, K, H, W = res.pred.shape
+    return {k: v.reshape(N, K) for k, v in task.metrics(res.pred.reshape(N * K, H, W), boards,
+                                                         k=K).items()}
 
 
 def _device_metric(metric, alive, weights):

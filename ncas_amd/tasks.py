@@ -22,7 +22,9 @@ a board depends only on (seed, board index):
   [17, 30] kept at uniformly random cells. Uniqueness of the solution is not required.
 
 `Task` objects (`get_task`) give the scored cells, the metrics and `load(split, root, n, size,
-seed)`, which reads a cached `.npz` or generates and caches the set.
+seed)`, which reads a cached `.npz` or generates and caches the set. Metrics are computed on the
+GPU for every (board, trial) row: "exact" and "cell_acc" for every task, plus the mazes' path
+"valid" / "optimal" (`nca_maze_metrics`) and Sudoku's "valid" (`nca_sudoku_valid`).
 """
 
 from __future__ import annotations
@@ -33,9 +35,10 @@ from collections import deque
 from dataclasses import dataclass, field
 
 import numpy as np
+import torch
 
 from . import _lib
-from .model import MAZE_OPEN, MAZE_WALL
+from .model import MAZE_GOAL, MAZE_OPEN, MAZE_PATH, MAZE_START, MAZE_WALL
 
 
 @dataclass
@@ -124,32 +127,86 @@ class Task:
         boards.save(path)
         return boards
 
-    def metrics(self, pred: np.ndarray, boards: Boards) -> dict[str, np.ndarray]:
-        """Per-board "exact" (every scored cell right) and "cell_acc" of predicted tokens
-        (N, H, W)."""
-        scored = self.eval_mask(boards)
-        right = (pred == boards.targets) & scored
-        n = scored.sum(axis=(1, 2))
-        hits = right.sum(axis=(1, 2))
-        return {"exact": hits == n, "cell_acc": hits / np.maximum(n, 1)}
+    def device_metrics(self, pred: torch.Tensor, inputs: torch.Tensor, targets: torch.Tensor,
+                       given: torch.Tensor, scored: torch.Tensor, k: int = 1
+                       ) -> dict[str, torch.Tensor]:
+        """Per-row metrics of decoded boards on the GPU: pred (rows, H, W) int64 tokens; inputs,
+        targets (boards, H, W) int64, given and scored (boards, H, W) bool, with row r on board
+        r // k. "exact": every scored cell right; "cell_acc": the fraction of scored cells right
+        (reference tasks/base.py:126-149)."""
+        B, H, W = targets.shape
+        right = (pred.view(B, k, H, W) == targets[:, None]) & scored[:, None]
+        hits = right.sum(dim=(2, 3))
+        n = scored.sum(dim=(1, 2))[:, None]
+        return {"exact": (hits == n).view(-1), "cell_acc": (hits / n.clamp_min(1)).view(-1)}
+
+    def metrics(self, pred, boards: Boards, k: int = 1) -> dict[str, np.ndarray]:
+        """The metrics of decoded boards pred (len(boards) * k, H, W), row r scored against board
+        r // k (the reference's `metrics(pred, boards)` for k = 1), computed on the current GPU
+        with one copy of the results to the host."""
+        dev = torch.device("cuda", torch.cuda.current_device())
+        bt = self.board_tensors(boards, dev)
+        p = torch.as_tensor(pred)
+        p = (p if p.is_cuda else _lib.upload(np.ascontiguousarray(p.numpy()), dev)).to(torch.int64)
+        out = self.device_metrics(p.reshape(-1, *boards.shape).contiguous(), *bt, k=k)
+        host = {name: v.cpu().numpy() for name, v in out.items()}
+        return host
+
+    def board_tensors(self, boards: Boards, device) -> tuple[torch.Tensor, ...]:
+        """(inputs, targets, given, scored) of `boards` on the device."""
+        up = lambda a: _lib.upload(np.ascontiguousarray(a), device)  # noqa: E731
+        return (up(boards.inputs), up(boards.targets), up(boards.given),
+                up(np.asarray(self.eval_mask(boards), dtype=bool)))
 
 
 class MazeTask(Task):
-    """Mazes of `maze_boards` (open / wall / start / goal inputs, the BFS path as target)."""
+    """Mazes of `maze_boards` (open / wall / start / goal inputs, the BFS path as target).
+
+    Metrics add "valid" (the decoded path cells plus the two endpoints form one simple
+    4-connected path between the endpoints) and "optimal" (valid and as long as the target path)
+    of reference tasks/maze.py:843-866, computed by `nca_maze_metrics`. `path_token` and
+    `endpoint_tokens` name the vocabulary: this build's maze tokens by default, the reference's
+    (PATH 1, ENDPOINT 3) for its Maze-OOD boards."""
 
     name = "maze"
+    path_token = MAZE_PATH
+    endpoint_tokens = (MAZE_START, MAZE_GOAL)
 
-    def __init__(self, extra_openings: float = 0.0, min_path_len: int | None = None):
+    def __init__(self, extra_openings: float = 0.0, min_path_len: int | None = None,
+                 path_token: int | None = None, endpoint_tokens: tuple[int, ...] | None = None):
         self.extra_openings, self.min_path_len = extra_openings, min_path_len
         if extra_openings:
             self.name = f"maze_x{extra_openings:g}"
+        if path_token is not None:
+            self.path_token = int(path_token)
+        if endpoint_tokens is not None:
+            self.endpoint_tokens = tuple(int(t) for t in endpoint_tokens)
+        if not 1 <= len(self.endpoint_tokens) <= 2:
+            raise ValueError("endpoint_tokens: one or two tokens")
 
     def generate(self, n: int, size: int, seed: int) -> Boards:
         return maze_boards(n, size, seed, self.extra_openings, self.min_path_len)
 
+    def device_metrics(self, pred, inputs, targets, given, scored, k: int = 1):
+        out = super().device_metrics(pred, inputs, targets, given, scored, k)
+        rows, H, W = pred.shape
+        valid = torch.empty(rows, dtype=torch.uint8, device=pred.device)
+        optimal = torch.empty_like(valid)
+        ends = self.endpoint_tokens + self.endpoint_tokens[-1:]
+        g8 = given.to(torch.uint8).contiguous()
+        _lib.check(_lib.load().nca_maze_metrics(
+            pred.data_ptr(), inputs.contiguous().data_ptr(), targets.contiguous().data_ptr(),
+            g8.data_ptr(), rows, int(k), H, W, int(self.path_token), int(ends[0]), int(ends[1]),
+            valid.data_ptr(), optimal.data_ptr(), _lib.stream_of(pred.device)),
+            "nca_maze_metrics")
+        out["valid"], out["optimal"] = valid.bool(), optimal.bool()
+        return out
+
 
 class SudokuTask(Task):
-    """Sudoku boards of `sudoku_boards` (clues as inputs, the solved grid as target)."""
+    """Sudoku boards of `sudoku_boards` (clues as inputs, the solved grid as target). Metrics add
+    "valid" (the grid filled with the clues satisfies every row, column and box constraint,
+    reference tasks/sudoku.py:987-995), computed by `nca_sudoku_valid`."""
 
     name = "sudoku"
 
@@ -160,6 +217,19 @@ class SudokuTask(Task):
         if size != 9:
             raise ValueError("sudoku boards are 9x9")
         return sudoku_boards(n, seed, self.clues)
+
+    def device_metrics(self, pred, inputs, targets, given, scored, k: int = 1):
+        out = super().device_metrics(pred, inputs, targets, given, scored, k)
+        rows, H, W = pred.shape
+        if (H, W) != (9, 9):
+            raise ValueError("sudoku boards are 9x9")
+        valid = torch.empty(rows, dtype=torch.uint8, device=pred.device)
+        g8 = given.to(torch.uint8).contiguous()
+        _lib.check(_lib.load().nca_sudoku_valid(
+            pred.data_ptr(), inputs.contiguous().data_ptr(), g8.data_ptr(), rows, int(k),
+            valid.data_ptr(), _lib.stream_of(pred.device)), "nca_sudoku_valid")
+        out["valid"] = valid.bool()
+        return out
 
 
 def get_task(name: str, **kwargs) -> Task:
