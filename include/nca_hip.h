@@ -50,6 +50,10 @@
  *   nca_maze_metrics  <- the maze tasks' "valid" / "optimal" metrics (src/nca/tasks/maze.py:
  *                        251-295, 843-866)
  *   nca_sudoku_valid  <- the Sudoku tasks' "valid" metric (src/nca/tasks/sudoku.py:151, 987-995)
+ *   nca_adamw_ema     <- clip_grad_norm_ + AdamW.step + zero_grad + the EMA loop of train_fast's
+ *                        update (src/nca/engine/train.py:262-273)
+ *   nca_damage_clamp  <- apply_damage + apply_clamp of the training batch (src/nca/perturb.py:
+ *                        43-106, src/nca/train.py:219-244)
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -197,6 +201,46 @@ int nca_maze_metrics(const int64_t *pred, const int64_t *inputs, const int64_t *
  * elsewhere has values 1..9 and every row, column and 3x3 box holds each digit once. 9x9 boards. */
 int nca_sudoku_valid(const int64_t *pred, const int64_t *inputs, const uint8_t *given,
                      int64_t rows, int32_t k_per_board, uint8_t *valid, void *stream);
+
+/* The training step's update, fused: clip + AdamW + EMA + zero_grad in one launch
+ * (<- the reference's clip_grad_norm_ in Engine.train_iteration, src/nca/engine/engine.py, and
+ * its apply_update: the host test of the norm, torch.optim.AdamW.step, zero_grad and the EMA loop,
+ * src/nca/engine/train.py:262-273). Flat fp32 device buffers of n elements: every parameter of
+ * the cell back to back (params, their gradient, AdamW's two moments, the EMA weights).
+ * counters (2) int64 on the device: [0] the number of applied AdamW steps (torch's `step`), [1]
+ * the number of skipped iterations. One call: gn = ||grads||_2 (fixed summation order), written
+ * to *grad_norm; with max_norm > 0 the gradient is scaled by min(1, max_norm / (gn + 1e-6));
+ * when gn is finite counters[0] += 1 and AdamW updates params, exp_avg and exp_avg_sq with the
+ * bias corrections of that count, else counters[1] += 1 and they keep their values; then
+ * ema = d ema + (1 - d) params (ema_decay d >= 0; d < 0 leaves ema alone, which may be NULL) and
+ * grads = 0. No host synchronisation; deterministic. */
+typedef struct {
+    double lr;           /* this iteration's learning rate (the schedule applied) */
+    double beta1, beta2;
+    double eps;
+    double weight_decay; /* decoupled: params *= 1 - lr * weight_decay */
+    double ema_decay;    /* this iteration's EMA decay, < 0 for none */
+    double max_norm;     /* clip threshold, <= 0 for no clipping */
+} nca_adamw_desc;
+
+int nca_adamw_ema(float *params, float *grads, float *exp_avg, float *exp_avg_sq, float *ema,
+                  int64_t n, const nca_adamw_desc *desc, int64_t *counters, float *grad_norm,
+                  void *stream);
+
+enum { NCA_DAMAGE_OURS = 0, NCA_DAMAGE_OFFICIAL = 1 };  /* perturb.py:43-83 geometries */
+
+/* nca_damage_clamp <- apply_damage + apply_clamp of the training batch (src/nca/perturb.py:
+ * 86-106, src/nca/train.py:219-244): in place on x (rows, channels, H, W) fp32, every channel of
+ * a cell inside one of the discs is set to fill, then the channels [in_offset, in_offset + c_in)
+ * of given cells take the clamp values (given (rows, H, W) {0,1} and clamp (rows, c_in, H, W);
+ * given NULL: no clamp). discs (n_discs, 4) fp64 on the device: (row, cy, cx, r^2). Inside:
+ * NCA_DAMAGE_OURS (y - cy)^2 + (x - cx)^2 <= r^2 with y, x the cell's row and column;
+ * NCA_DAMAGE_OFFICIAL the same < r^2 with y, x = numpy linspace(-1, 1) coordinates; fp64, each
+ * operation rounded once, as numpy evaluates it. */
+int nca_damage_clamp(float *x, int64_t rows, int32_t channels, int32_t height, int32_t width,
+                     const double *discs, int32_t n_discs, int32_t geometry, float fill,
+                     const uint8_t *given, const float *clamp, int32_t c_in, int32_t in_offset,
+                     void *stream);
 
 /* Host-side batched board generation (the inputs of the workloads), on `threads` host threads
  * (0 = all). Every board draws from its own Philox4x32-10 stream keyed on `seed`, so the

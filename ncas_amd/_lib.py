@@ -18,6 +18,7 @@ NOALLOC_SCRATCH_BYTES = 128 << 20  # NCA_NOALLOC_SCRATCH_BYTES of include/nca_hi
 PADDING = {"zero": 0, "wall": 1, "wrap": 2}
 HEAD = {"mlp": 0, "l2": 1}
 PRECISION = {"fp32": 0, "bf16": 1}
+DAMAGE_GEOMETRY = {"ours": 0, "official": 1}
 
 EXPORTS = (
     "nca_packed_weights_bytes",
@@ -44,6 +45,8 @@ EXPORTS = (
     "nca_prune_select_rows",
     "nca_maze_metrics",
     "nca_sudoku_valid",
+    "nca_adamw_ema",
+    "nca_damage_clamp",
     "nca_maze_boards",
     "nca_sudoku_boards",
 )
@@ -95,6 +98,11 @@ class FireDesc(ctypes.Structure):
 
 class CellGrads(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")]
+
+
+class AdamWDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in ("lr", "beta1", "beta2", "eps", "weight_decay",
+                                                "ema_decay", "max_norm")]
 
 
 class BpttLoss(ctypes.Structure):
@@ -163,6 +171,9 @@ def load():
                                         i64, vp, vp]
     L.nca_maze_metrics.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, i64, i64, i64, vp, vp, vp]
     L.nca_sudoku_valid.argtypes = [vp, vp, vp, i64, i32, vp, vp]
+    L.nca_adamw_ema.argtypes = [vp, vp, vp, vp, vp, i64, ctypes.POINTER(AdamWDesc), vp, vp, vp]
+    L.nca_damage_clamp.argtypes = [vp, i64, i32, i32, i32, vp, i32, i32, ctypes.c_float, vp, vp,
+                                   i32, i32, vp]
     L.nca_maze_boards.argtypes = [i64, i32, ctypes.c_uint64, ctypes.c_double, i32, i32, vp, vp, vp,
                                   vp, i32]
     L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]

@@ -34,6 +34,7 @@ SOURCES = {
     "nca_bptt.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "nca_prune.hip": [],
     "nca_metrics.hip": [],
+    "nca_train.hip": [],
     "nca_boards.cpp": [],
 }
 

@@ -1,0 +1,191 @@
+// The training step around the BPTT chunk, fused on the GPU:
+//
+// nca_adamw_ema - one launch per iteration after the backward: the L2 norm of the summed
+//   gradient, clipping to max_norm, the finiteness test, AdamW with decoupled weight decay and
+//   bias correction, the exponential moving average of the weights and the zeroing of the
+//   gradient, over flat fp32 buffers (every parameter of the cell back to back). The reference
+//   runs clip_grad_norm_ (src/nca/engine/engine.py), a host test of the norm, torch's AdamW, a
+//   Python loop of EMA updates and zero_grad (src/nca/engine/train.py:262-273). Here the norm's
+//   test and the count of applied steps (AdamW's `step`, which a skipped iteration does not
+//   advance) live on the device, so an iteration needs no host synchronisation; a single
+//   workgroup sums the squares in a fixed order (each thread a strided run in fp64, then fixed
+//   butterflies), so the update is deterministic and a run resumed from a checkpoint repeats the
+//   uninterrupted run bit for bit. The per-element arithmetic is torch's multi-tensor AdamW's,
+//   operation for operation in fp32 with the same scalars: p *= 1 - lr wd; m = lerp(m, g, 1 - b1);
+//   v = v b2 + (1 - b2) g g; p += -(lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps).
+//
+// nca_damage_clamp - the damage perturbation (src/nca/perturb.py:43-106: the state set to `fill`
+//   inside discs) and the clamp of the given cells' input channels (model.py:430-438) in one pass
+//   over the state, in place. The discs are drawn on the host (their random stream is the
+//   trainer's numpy generator) and handed over as (row, cy, cx, r^2) in fp64; a cell is inside
+//   when (y - cy)^2 + (x - cx)^2 <= r^2 with y, x its row and column ("ours"), or < r^2 with y, x
+//   the numpy linspace(-1, 1) coordinates ("official"), evaluated in fp64 with one rounding per
+//   operation, as numpy evaluates it.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "nca_hip.h"
+#include "nca_status.h"
+
+namespace {
+
+constexpr int kOptThreads = 1024;
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__global__ void __launch_bounds__(kOptThreads)
+    adamw_ema_kernel(float *__restrict__ p, float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
+                     float *__restrict__ e, int64_t n, nca_adamw_desc d, int64_t *__restrict__ counters,
+                     float *__restrict__ grad_norm) {
+    __shared__ double part[kOptThreads / 64];
+    __shared__ float s_coef, s_wd, s_w1, s_b2, s_w2, s_bc2, s_eps, s_step, s_ed, s_ea;
+    __shared__ int s_ok, s_clip, s_ema;
+    const int tid = threadIdx.x;
+    double acc = 0.0;
+    for (int64_t i = tid; i < n; i += kOptThreads) {
+        const double x = (double)g[i];
+        acc += x * x;
+    }
+    acc = wave_sum(acc);
+    if ((tid & 63) == 0) part[tid >> 6] = acc;
+    __syncthreads();
+    if (tid == 0) {
+        double s = 0.0;
+        for (int w = 0; w < kOptThreads / 64; ++w) s += part[w];
+        const float gn = (float)sqrt(s);
+        const bool ok = isfinite(gn);
+        grad_norm[0] = gn;
+        s_clip = d.max_norm > 0.0;
+        float coef = (float)d.max_norm / (gn + 1e-6f);
+        s_coef = coef < 1.0f ? coef : 1.0f;
+        s_ok = ok;
+        s_ema = d.ema_decay >= 0.0;
+        s_ed = (float)d.ema_decay;
+        s_ea = (float)(1.0 - d.ema_decay);
+        if (ok) {
+            const int64_t t = counters[0] + 1;
+            counters[0] = t;
+            const double bc1 = 1.0 - pow(d.beta1, (double)t), bc2 = 1.0 - pow(d.beta2, (double)t);
+            s_wd = (float)(1.0 - d.lr * d.weight_decay);
+            s_w1 = (float)(1.0 - d.beta1);
+            s_b2 = (float)d.beta2;
+            s_w2 = (float)(1.0 - d.beta2);
+            s_bc2 = (float)sqrt(bc2);
+            s_eps = (float)d.eps;
+            s_step = (float)(-(d.lr / bc1));
+        } else {
+            counters[1] += 1;
+        }
+    }
+    __syncthreads();
+    const bool ok = s_ok, clip = s_clip, ema = s_ema;
+    const float coef = s_coef, wd = s_wd, w1 = s_w1, b2 = s_b2, w2 = s_w2, bc2 = s_bc2, eps = s_eps,
+                step = s_step, ed = s_ed, ea = s_ea;
+    for (int64_t i = tid; i < n; i += kOptThreads) {
+        float pi = p[i];
+        if (ok) {
+            float gi = g[i];
+            if (clip) gi = gi * coef;
+            pi = pi * wd;
+            float mi = m[i];
+            mi = w1 < 0.5f ? mi + w1 * (gi - mi) : gi - (gi - mi) * (1.0f - w1);
+            float vi = v[i] * b2;
+            vi = vi + w2 * (gi * gi);
+            const float den = sqrtf(vi) / bc2 + eps;
+            pi = pi + step * (mi / den);
+            p[i] = pi;
+            m[i] = mi;
+            v[i] = vi;
+        }
+        if (ema) {
+            float ei = e[i] * ed;
+            e[i] = ei + ea * pi;
+        }
+        g[i] = 0.0f;
+    }
+}
+
+constexpr int kDamageThreads = 256;
+
+__device__ __forceinline__ double linspace_pm1(int i, int num) {
+    // numpy.linspace(-1, 1, num)[i]: i * (2 / (num - 1)) - 1, the last point exactly 1
+    if (num == 1) return -1.0;
+    if (i == num - 1) return 1.0;
+    return __dadd_rn(__dmul_rn((double)i, __ddiv_rn(2.0, (double)(num - 1))), -1.0);
+}
+
+__global__ void __launch_bounds__(kDamageThreads)
+    damage_clamp_kernel(float *__restrict__ x, int64_t rows, int C, int H, int W, const double *__restrict__ discs,
+                        int n_discs, int official, float fill, const uint8_t *__restrict__ given,
+                        const float *__restrict__ clamp, int c_in, int in_offset) {
+    const int64_t HW = (int64_t)H * W;
+    const int64_t cell = (int64_t)blockIdx.x * kDamageThreads + threadIdx.x;
+    if (cell >= rows * HW) return;
+    const int64_t row = cell / HW, rc = cell - row * HW;
+    const int i = (int)(rc / W), j = (int)(rc - (int64_t)(rc / W) * W);
+    const double y = official ? linspace_pm1(i, H) : (double)i;
+    const double xx = official ? linspace_pm1(j, W) : (double)j;
+    bool hit = false;
+    for (int k = 0; k < n_discs && !hit; ++k) {
+        const double *dk = discs + 4 * k;
+        if ((int64_t)dk[0] != row) continue;
+        const double dy = __dsub_rn(y, dk[1]), dx = __dsub_rn(xx, dk[2]);
+        const double s = __dadd_rn(__dmul_rn(dy, dy), __dmul_rn(dx, dx));
+        hit = official ? s < dk[3] : s <= dk[3];
+    }
+    float *xr = x + row * C * HW + rc;
+    if (hit)
+        for (int c = 0; c < C; ++c) xr[c * HW] = fill;
+    if (given && given[row * HW + rc]) {
+        const float *cr = clamp + row * c_in * HW + rc;
+        for (int c = 0; c < c_in; ++c) xr[(in_offset + c) * HW] = cr[c * HW];
+    }
+}
+
+}  // namespace
+
+extern "C" int nca_adamw_ema(float *params, float *grads, float *exp_avg, float *exp_avg_sq, float *ema, int64_t n,
+                             const nca_adamw_desc *desc, int64_t *counters, float *grad_norm, void *stream) {
+    nca::clear_error();
+    if (!desc) return nca::set_error(NCA_ERR_INVALID, "NULL descriptor");
+    if (n < 1) return nca::set_error(NCA_ERR_INVALID, "n >= 1");
+    if (!params || !grads || !exp_avg || !exp_avg_sq || !counters || !grad_norm)
+        return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    if (desc->ema_decay >= 0.0 && !ema) return nca::set_error(NCA_ERR_INVALID, "ema_decay >= 0 needs the EMA buffer");
+    if (!(desc->beta1 >= 0.0 && desc->beta1 < 1.0 && desc->beta2 >= 0.0 && desc->beta2 < 1.0 && desc->eps >= 0.0 &&
+          desc->lr >= 0.0 && desc->weight_decay >= 0.0 && desc->ema_decay <= 1.0))
+        return nca::set_error(NCA_ERR_INVALID, "0 <= beta1, beta2 < 1; eps, lr, weight_decay >= 0; ema_decay <= 1");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(adamw_ema_kernel, dim3(1), dim3(kOptThreads), 0, st, params, grads, exp_avg, exp_avg_sq, ema, n,
+                       *desc, counters, grad_norm);
+    return nca::hip_status(hipGetLastError(), "adamw launch");
+}
+
+extern "C" int nca_damage_clamp(float *x, int64_t rows, int32_t channels, int32_t height, int32_t width,
+                                const double *discs, int32_t n_discs, int32_t geometry, float fill,
+                                const uint8_t *given, const float *clamp, int32_t c_in, int32_t in_offset,
+                                void *stream) {
+    nca::clear_error();
+    if (rows < 0 || channels < 1 || height < 1 || width < 1 || n_discs < 0)
+        return nca::set_error(NCA_ERR_INVALID, "rows >= 0, channels, height, width >= 1, n_discs >= 0");
+    if (geometry != NCA_DAMAGE_OURS && geometry != NCA_DAMAGE_OFFICIAL)
+        return nca::set_error(NCA_ERR_INVALID, "geometry: NCA_DAMAGE_OURS or NCA_DAMAGE_OFFICIAL");
+    if (given && (!clamp || c_in < 1 || in_offset < 0 || in_offset + c_in > channels))
+        return nca::set_error(NCA_ERR_INVALID, "the clamp needs clamp values and 0 <= in_offset < in_offset + c_in <= channels");
+    if (rows == 0) return NCA_OK;
+    if (!x || (n_discs > 0 && !discs)) return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    const int64_t cells = rows * (int64_t)height * width;
+    const int64_t blocks = (cells + kDamageThreads - 1) / kDamageThreads;
+    if (blocks > 0x7fffffffll) return nca::set_error(NCA_ERR_UNSUPPORTED, "too many cells for one call");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(damage_clamp_kernel, dim3((unsigned)blocks), dim3(kDamageThreads), 0, st, x, rows,
+                       (int)channels, (int)height, (int)width, discs, (int)n_discs,
+                       geometry == NCA_DAMAGE_OFFICIAL ? 1 : 0, fill, given, clamp, (int)c_in, (int)in_offset);
+    return nca::hip_status(hipGetLastError(), "damage launch");
+}

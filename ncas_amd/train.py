@@ -394,9 +394,16 @@ class Engine:
                              step_seeds=seeds[lo:hi], step0=lo, p_fire=self.p_fire,
                              precision=precision, loss_mask=batch.get("loss_mask"))
             self.last_chunk = res
-            for name, p in zip(_GRAD_NAMES, _params(model)):
-                g = res.grads[name].reshape(p.shape).to(p.dtype)
-                p.grad = g if p.grad is None else p.grad + g
+            # added into existing gradients in place (one launch), so a gradient that is a view
+            # of a flat buffer (optim.FusedUpdate) stays one
+            params = _params(model)
+            grads = [res.grads[n].reshape(p.shape).to(p.dtype) for n, p in zip(_GRAD_NAMES, params)]
+            have = [(p.grad, g) for p, g in zip(params, grads) if p.grad is not None]
+            if have:
+                torch._foreach_add_([a for a, _ in have], [g for _, g in have])
+            for p, g in zip(params, grads):
+                if p.grad is None:
+                    p.grad = g
             x, loss = res.x, res.loss
         else:
             with torch.enable_grad():

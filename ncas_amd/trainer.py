@@ -1,20 +1,24 @@
 """The training recipe around the HIP engine: a counterpart of the reference's `train_fast`
 (reference src/nca/engine/train.py:87-386) for the cells and tasks of this engine.
 
-Every iteration: draw a batch from the replay pool (fresh boards at `seed_ratio`), perturb it
-(target swap, damage discs, then the clamp; optionally the public code's batch noise), draw a
-chunk start and the per-step seeds from the run's numpy generator, run
-`Engine.train_iteration` (step noise inside the rollout when `train.noise` is active), and in its
-update callback step AdamW when the gradient norm is finite, advance the learning-rate schedule
-(linear warm-up, then constant or cosine) and the exponential moving average of the weights;
-then write the rollout's final states back to the pool. Checkpoints hold the model, the EMA, the
-optimiser, the schedule, the pool, both random generators and the step, so a run interrupted at a
-checkpoint resumes exactly (bit for bit: every kernel of the path sums in a fixed order).
+The run is an object (`_Run`) with one method per phase: restore, iterate, log, checkpoint,
+finish. An iteration samples a batch from the replay pool (fresh boards at `seed_ratio`),
+perturbs it (target swaps; the damage discs and the clamp in one GPU pass; optionally the
+public code's batch noise), draws a chunk start and the per-step seeds from the run's numpy
+generator, and runs `Engine.train_iteration` (step noise inside the rollout when `train.noise`
+is active) whose update callback is one launch of the fused update (`optim.FusedUpdate`,
+`nca_adamw_ema`): gradient norm, clipping, the finiteness test, AdamW with this iteration's
+learning rate (linear warm-up, then constant or cosine), the EMA and the zeroing of the
+gradient, with the skip decision and the step counts kept on the device, so nothing waits for
+the host. The final states go back to the pool. Checkpoints hold the model, the EMA, the
+update's moments and counters, the schedule's position, the pool, both random generators and
+the step; a run interrupted at a checkpoint resumes bit for bit (every kernel of the path,
+the update's norm included, sums in a fixed order).
 
 Files of a run directory, like the reference's: `run.json` (config, seed, parameter count, model
 config, engine), `log.jsonl` (loss, grad norm, lr, batch accuracy, pool age, iteration seconds,
-peak memory; evaluations), `checkpoint.pt`, `final.pt` (the EMA weights and the model config)
-and `summary.json`. Checkpoints are read back with `weights_only=True`.
+peak memory; evaluations), `checkpoint.pt`, `final.pt` (the EMA weights, the model config and
+the run config) and `summary.json`. Checkpoints are read back with `weights_only=True`.
 
 Config sections: `task` ({name, args, train: {n, size, seed}, val: {n, size, seed}}), `model`
 ({preset, overrides}), `train` (the keys of `DEFAULTS`), `engine` (`train.EngineConfig`).
@@ -31,10 +35,11 @@ from pathlib import Path
 import numpy as np
 import torch
 
-from . import _lib
+from . import perturb
 from .model import NCA, NCAConfig, build_model
+from .optim import FusedUpdate
 from .rng import step_seeds
-from .rollout import RolloutConfig, rollout
+from .rollout import RolloutConfig, decode_tokens, rollout
 from .tasks import get_task
 from .train import Engine, EngineConfig, ReplayPool, loss_weights
 
@@ -96,64 +101,22 @@ def ema_decay(tr: dict, step: int) -> float:
 
 
 # ------------------------------------------------------------------------------ perturbations
-def damage_masks(B: int, H: int, W: int, n: int, r_min: float, r_max: float,
-                 rng: np.random.Generator, hit: np.ndarray, geometry: str = "ours") -> np.ndarray:
-    """(B, H, W) bool union of `n` random discs on each board with `hit` (reference
-    src/nca/perturb.py:43-83). "ours": centres anywhere on the grid, radius r ~ U(r_min, r_max)
-    times min(H, W), closed discs; "official": coordinates in [-1, 1], centres in
-    [-0.5, 0.5]^2, radius in those units, open discs."""
-    out = np.zeros((B, H, W), dtype=bool)
-    if geometry == "official":
-        ys = np.linspace(-1.0, 1.0, H)[:, None]
-        xs = np.linspace(-1.0, 1.0, W)[None, :]
-    else:
-        ys = np.arange(H)[:, None].astype(np.float64)
-        xs = np.arange(W)[None, :].astype(np.float64)
-    for b in np.nonzero(hit)[0]:
-        for _ in range(n):
-            if geometry == "official":
-                cy, cx = rng.uniform(-0.5, 0.5, size=2)
-                r = rng.uniform(r_min, r_max)
-                out[b] |= (ys - cy) ** 2 + (xs - cx) ** 2 < r * r
-            else:
-                cy, cx = rng.uniform(0, H), rng.uniform(0, W)
-                r = rng.uniform(r_min, r_max) * min(H, W)
-                out[b] |= (ys - cy) ** 2 + (xs - cx) ** 2 <= r * r
-    return out
-
-
 def perturb_batch(model, pool: ReplayPool, batch: dict, tr: dict, rng: np.random.Generator,
                   gen_dev: torch.Generator) -> None:
     """The pre-rollout perturbations, in place (reference src/nca/train.py:219-252): target
-    swap (fresh boards or other pool entries), damage (the state set to `fill` inside random
-    discs of a fraction `p` of the boards), the clamp, and the optional batch noise."""
-    B = batch["x"].shape[0]
-    which = np.nonzero(rng.random(B) < tr["swap"]["p"])[0]
-    if tr["swap_source"] == "pool":
-        pool.swap_from_pool(batch, which)
-    else:
-        pool.replace_boards(batch, which)
+    swaps (fresh boards or other pool entries), then the damage discs and the clamp in one pass
+    on the GPU (`perturb.damage_clamp`), then the optional batch noise. The host draws only the
+    swap rows and the discs' geometry from the run's generator."""
+    B, _, H, W = batch["x"].shape
+    rows = perturb.swap_rows(rng, B, tr["swap"]["p"])
+    (pool.swap_from_pool if tr["swap_source"] == "pool" else pool.replace_boards)(batch, rows)
     d = tr["damage"]
     hit = rng.random(B) < d["p"]
-    if hit.any():
-        _, _, H, W = batch["x"].shape
-        m = damage_masks(B, H, W, d["n"], d["r_min"], d["r_max"], rng, hit, d["geometry"])
-        batch["x"] = batch["x"].masked_fill(_lib.upload(m, pool.device)[:, None], d["fill"])
-    batch["x"] = model.apply_clamp(batch["x"], batch["given4"], batch["clamp"])
-    bn = tr["batch_noise"]
-    if bn is not None:
-        x = batch["x"]
-        Bn, C, H, W = x.shape
-        dev = x.device
-        boards = torch.rand((Bn, 1, 1, 1), generator=gen_dev, device=dev) < bn["p"]
-        cells = torch.rand((Bn, 1, H, W), generator=gen_dev, device=dev) < bn["ps"]
-        noise = torch.randn(x.shape, generator=gen_dev, device=dev) * bn["sigma"]
-        keep = boards & cells
-        in_ch = torch.zeros((1, C, 1, 1), dtype=torch.bool, device=dev)
-        in_ch[:, model.cfg.in_slice] = True
-        keep = keep & ~(batch["given4"] & in_ch)
-        batch["x"] = model.apply_clamp(x + noise * keep.to(x.dtype), batch["given4"],
-                                       batch["clamp"])
+    discs = perturb.draw_discs(rng, hit, H, W, d["n"], d["r_min"], d["r_max"], d["geometry"])
+    batch["x"] = perturb.damage_clamp(model, batch["x"].float().contiguous(), batch["given4"],
+                                      batch["clamp"], discs, d["fill"], d["geometry"])
+    if tr["batch_noise"] is not None:
+        perturb.batch_noise(model, batch, tr["batch_noise"], gen_dev)
 
 
 # ------------------------------------------------------------------------------ run pieces
@@ -178,24 +141,30 @@ def build_run_model(cfg: dict) -> NCA:
     return model
 
 
-def load_model(path) -> tuple[NCA, dict]:
-    """(model, checkpoint) of a `final.pt`, read with weights_only=True."""
+def load_model(path, device=None) -> tuple[NCA, dict]:
+    """(model with the EMA weights, run config) of a `final.pt` (reference src/nca/train.py:
+    694-701), read with weights_only=True."""
     ck = torch.load(path, map_location="cpu", weights_only=True)
     model = NCA(NCAConfig.from_dict(ck["model_config"]))
     model.load_state_dict(ck["model"])
-    return model, ck
+    if device is not None:
+        model = model.to(device)
+    return model.eval(), ck.get("config")
 
 
 @torch.no_grad()
 def evaluate(model, task, boards, ev: dict, rollout_steps: int, seed: int) -> dict:
-    """Quick validation: one rollout of ev["n"] boards for ev["depth"] (default: the training
-    rollout) steps with ev["k"] trials, first trial's exact rate and cell accuracy."""
-    n = min(ev["n"], len(boards))
+    """Quick validation (reference src/nca/train.py:674-691): one rollout of ev["n"] boards for
+    ev["depth"] (default: the training rollout) steps with ev["k"] trials; the mean of every task
+    metric over the trials, trial 0's cell accuracy and the mean board confidence."""
+    n = min(ev["n"] or len(boards), len(boards))
     sub = boards.subset(np.arange(n))
-    rc = RolloutConfig(depth=ev["depth"] or rollout_steps, k=ev["k"])
-    res = rollout(model, task, sub, rc, seed=seed)
-    m = task.metrics(res.pred[:, 0], sub)
-    return {"val_exact": float(m["exact"].mean()), "val_cell_acc": float(m["cell_acc"].mean())}
+    res = rollout(model, task, sub, RolloutConfig(depth=ev["depth"] or rollout_steps, k=ev["k"]),
+                  seed=seed)
+    out = {f"val_{k}": float(np.mean(v)) for k, v in res.metrics.items()}
+    out["val_cell_acc"] = float(np.mean(res.metrics["cell_acc"][:, 0]))
+    out["val_conf"] = float(res.conf.mean())
+    return out
 
 
 def _rng_state(rng: np.random.Generator) -> dict:
@@ -211,15 +180,137 @@ def _set_rng_state(rng: np.random.Generator, d: dict) -> None:
                                "has_uint32": d["has_uint32"], "uinteger": d["uinteger"]}
 
 
-def _json_line(rec: dict) -> str:
-    return json.dumps(rec) + "\n"
+def _append_json(path: Path, rec: dict) -> None:
+    with open(path, "a") as f:
+        f.write(json.dumps(rec) + "\n")
+
+
+class _Run:
+    """One training run's state and its phases. Everything that a checkpoint must restore for an
+    exact resume lives here: the model and its EMA (views of the fused update's flat buffers),
+    the update's moments and counters, the replay pool, the numpy generator (swaps, damage,
+    chunk starts, step seeds) and the device generator (fresh states, batch noise)."""
+
+    def __init__(self, cfg: dict, out: Path, seed: int, dev: torch.device, quiet: bool):
+        self.cfg, self.out, self.seed, self.dev, self.quiet = cfg, out, seed, dev, quiet
+        self.tr = tr = resolve_train_cfg(cfg)
+        torch.manual_seed(seed)
+        self.rng = np.random.default_rng(seed)
+        self.gen_dev = torch.Generator(device=dev)
+        self.gen_dev.manual_seed(seed)
+        self.task, self.train_boards, self.val_boards = build_task_and_data(cfg["task"])
+        self.model = build_run_model(cfg).to(dev)
+        self.ema = copy.deepcopy(self.model).eval()
+        for p in self.ema.parameters():
+            p.requires_grad_(False)
+        self.update = FusedUpdate(self.model, self.ema, tr["lr"], tr["betas"],
+                                  weight_decay=tr["weight_decay"])
+        mult = tr["pool_mult"] if tr["replay"] else 1
+        self.seed_ratio = tr["seed_ratio"] if tr["replay"] else 1.0
+        self.pool = ReplayPool(self.model, self.train_boards, mult * tr["batch_size"], self.rng,
+                               self.gen_dev, task=self.task, augment=tr["augment"])
+        self.engine = Engine(self.model, EngineConfig.from_dict(cfg.get("engine")), tr, dev)
+        self.weights = loss_weights(tr["loss_window"], self.engine.Nc, dev)
+        self.n_params = sum(p.numel() for p in self.model.parameters())
+        self.step0 = 0
+        self.last_eval: dict = {}
+
+    @property
+    def ckpt_path(self) -> Path:
+        return self.out / "checkpoint.pt"
+
+    # ------------------------------------------------------------------ checkpoints
+    def save_checkpoint(self, step: int) -> None:
+        torch.save(dict(model=self.model.state_dict(), ema=self.ema.state_dict(),
+                        opt=self.update.state_dict(), sched={"last_epoch": step},
+                        pool={k: v for k, v in self.pool.state_dict().items() if v is not None},
+                        rng=_rng_state(self.rng), gen_dev=self.gen_dev.get_state(), step=step),
+                   self.ckpt_path)
+
+    def restore(self) -> int:
+        """Load the checkpoint into every piece of state; returns its step."""
+        ck = torch.load(self.ckpt_path, map_location=self.dev, weights_only=True)
+        self.model.load_state_dict(ck["model"])
+        self.ema.load_state_dict(ck["ema"])
+        self.update.load_state_dict(ck["opt"])
+        self.pool.load_state_dict(ck["pool"])
+        _set_rng_state(self.rng, ck["rng"])
+        self.gen_dev.set_state(ck["gen_dev"].cpu())
+        self.step0 = int(ck["step"])
+        return self.step0
+
+    # ------------------------------------------------------------------ one iteration
+    def iterate(self, step: int):
+        """Sample and perturb a batch, run the engine's iteration with the fused update, write
+        the final states back. Returns (batch, final state, loss)."""
+        tr, eng = self.tr, self.engine
+        idx, batch = self.pool.sample(tr["batch_size"], self.seed_ratio)
+        if tr["perturb"]:
+            perturb_batch(self.model, self.pool, batch, tr, self.rng, self.gen_dev)
+        c0 = int(self.rng.integers(0, eng.N - eng.Nc + 1))
+        seeds = step_seeds(self.rng, eng.N)
+        lr = tr["lr"] * lr_at(step, tr["steps"], tr)
+        update = lambda _gn: self.update.step(lr, ema_decay(tr, step), tr["grad_clip"])  # noqa: E731
+        x, loss, _ = eng.train_iteration(batch, seeds, c0, self.weights, None, update)
+        batch["x"] = x.detach()
+        self.pool.write_back(idx, batch)
+        return batch, x, loss
+
+    def log_record(self, step: int, batch: dict, x, loss, t0: float, t_window: float,
+                   n_window: int) -> dict:
+        """The log line of iteration `step` (one host copy of the device statistics)."""
+        with torch.no_grad():
+            dec, _ = decode_tokens(self.model, x, batch["given4"][:, 0], batch["inputs"],
+                                   self.task.fill_given)
+            lm = batch.get("loss_mask")
+            scored = ~batch["given4"][:, 0] if lm is None else lm > 0
+            right = ((dec == batch["targets"]) & scored).sum(dim=(1, 2)).float()
+            n_sc = scored.sum(dim=(1, 2)).clamp_min(1)
+            cell, exact, age, lo, gn, skipped = torch.stack([
+                (right / n_sc).mean(), (right == n_sc).float().mean(),
+                batch["age"].float().mean(), loss.float(), self.update.grad_norm,
+                self.update.skipped.float()]).tolist()
+        now = time.time()
+        tr = self.tr
+        return dict(step=step + 1, loss=lo, grad_norm=gn,
+                    lr=tr["lr"] * lr_at(step + 1, tr["steps"], tr), batch_cell_acc=cell,
+                    batch_exact=exact, mean_age=age, skipped_steps=int(skipped),
+                    elapsed=now - t0, iter_seconds=(now - t_window) / max(1, n_window),
+                    peak_mem_gb=torch.cuda.max_memory_allocated(self.dev) / 2**30)
+
+    # ------------------------------------------------------------------ files
+    def write_run_json(self) -> None:
+        (self.out / "run.json").write_text(json.dumps({
+            "config": self.cfg, "seed": self.seed, "params": self.n_params,
+            "model_config": self.model.cfg.to_dict(), "engine": self.engine.to_dict(),
+            "device": f"{self.dev} ({torch.cuda.get_device_name(self.dev)})",
+            "torch": torch.__version__, "update": "nca_adamw_ema",
+        }, indent=1, default=str))
+
+    def finish(self, end_step: int, seconds: float) -> dict:
+        tr = self.tr
+        final = dict(model=self.ema.state_dict(), model_config=self.model.cfg.to_dict(),
+                     config=self.cfg, seed=self.seed, step=end_step)
+        summary = {"final_eval": self.last_eval, "train_seconds": seconds, "steps": end_step,
+                   "start_step": self.step0, "params": self.n_params,
+                   "skipped_steps": int(self.update.skipped), "engine": self.engine.to_dict(),
+                   "training_complete": end_step == tr["steps"],
+                   "peak_mem_gb": torch.cuda.max_memory_allocated(self.dev) / 2**30}
+        if end_step < tr["steps"]:
+            final.update(target_steps=tr["steps"], training_complete=False)
+            summary["target_steps"] = tr["steps"]
+        torch.save(final, self.out / "final.pt")
+        (self.out / "summary.json").write_text(json.dumps(summary, indent=1))
+        return self.last_eval
 
 
 def train_fast(cfg: dict, out_dir, seed: int = 0, device=None, resume: bool = True,
                quiet: bool = False, stop_at_step: int | None = None) -> dict:
-    """Train one model on the HIP engine; resumable from `out_dir/checkpoint.pt`. With
-    `stop_at_step` the run stops there (the learning-rate horizon stays `train.steps`) and marks
-    its summary `training_complete: false`. Returns the last evaluation."""
+    """Train one model on the HIP engine, resumable from `out_dir/checkpoint.pt` (the reference's
+    `train_fast`, src/nca/engine/train.py:87-386, and its run files). With `stop_at_step` the run
+    stops there (the learning-rate horizon stays `train.steps`) and marks its summary
+    `training_complete: false`. A finished run is not trained again: its summary's last
+    evaluation is returned. Returns the last evaluation."""
     out = Path(out_dir)
     out.mkdir(parents=True, exist_ok=True)
     tr = resolve_train_cfg(cfg)
@@ -230,131 +321,39 @@ def train_fast(cfg: dict, out_dir, seed: int = 0, device=None, resume: bool = Tr
     if dev.type != "cuda":
         raise ValueError("the HIP engine trains on the GPU")
     torch.cuda.reset_peak_memory_stats(dev)
-    torch.manual_seed(seed)
-    rng = np.random.default_rng(seed)
-    gen_dev = torch.Generator(device=dev)
-    gen_dev.manual_seed(seed)
-
-    task, train_boards, val_boards = build_task_and_data(cfg["task"])
-    model = build_run_model(cfg).to(dev)
-    ema = copy.deepcopy(model).eval()
-    for p in ema.parameters():
-        p.requires_grad_(False)
-    opt = torch.optim.AdamW(model.parameters(), lr=tr["lr"], weight_decay=tr["weight_decay"],
-                            betas=tuple(tr["betas"]))
-    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda s: lr_at(s, tr["steps"], tr))
-    pool_size = (tr["pool_mult"] if tr["replay"] else 1) * tr["batch_size"]
-    seed_ratio = tr["seed_ratio"] if tr["replay"] else 1.0
-    pool = ReplayPool(model, train_boards, pool_size, rng, gen_dev, task=task,
-                      augment=tr["augment"])
-    ecfg = EngineConfig.from_dict(cfg.get("engine"))
-    engine = Engine(model, ecfg, tr, dev)
-    N, Nc = engine.N, engine.Nc
-    weights = loss_weights(tr["loss_window"], Nc, dev)
-
-    step0 = 0
-    ckpt_path, log_path = out / "checkpoint.pt", out / "log.jsonl"
-    if resume and ckpt_path.exists():
-        ck = torch.load(ckpt_path, map_location=dev, weights_only=True)
-        model.load_state_dict(ck["model"])
-        ema.load_state_dict(ck["ema"])
-        opt.load_state_dict(ck["opt"])
-        sched.load_state_dict(ck["sched"])
-        pool.load_state_dict(ck["pool"])
-        _set_rng_state(rng, ck["rng"])
-        gen_dev.set_state(ck["gen_dev"].cpu())
-        step0 = int(ck["step"])
+    run = _Run(cfg, out, seed, dev, quiet)
+    if resume and run.ckpt_path.exists():
+        step0 = run.restore()
+        summary = out / "summary.json"
+        if step0 >= tr["steps"] and summary.exists():
+            return json.loads(summary.read_text()).get("final_eval", {})
         if step0 >= end_step:
             raise ValueError("stop_at_step must be after the resumed checkpoint")
         if not quiet:
             print(f"resumed from step {step0}")
-    n_params = sum(p.numel() for p in model.parameters())
-    (out / "run.json").write_text(json.dumps({
-        "config": cfg, "seed": seed, "params": n_params, "model_config": model.cfg.to_dict(),
-        "engine": engine.to_dict(), "device": f"{dev} ({torch.cuda.get_device_name(dev)})",
-        "torch": torch.__version__,
-    }, indent=1, default=str))
-
-    n_skipped = 0
-    last_eval: dict = {}
-    t_start = window_t0 = time.time()
-    window_n = 0
-    model.train()
-    for step in range(step0, end_step):
-        idx, batch = pool.sample(tr["batch_size"], seed_ratio)
-        if tr["perturb"]:
-            perturb_batch(model, pool, batch, tr, rng, gen_dev)
-        c0 = int(rng.integers(0, N - Nc + 1))
-        seeds = step_seeds(rng, N)
-
-        def apply_update(gn, step=step):
-            nonlocal n_skipped
-            if bool(torch.isfinite(gn)):  # one host wait per iteration, like the reference
-                opt.step()
-            else:
-                n_skipped += 1
-            opt.zero_grad(set_to_none=True)
-            sched.step()
-            d = ema_decay(tr, step)
-            with torch.no_grad():
-                for pe, pm in zip(ema.parameters(), model.parameters()):
-                    pe.mul_(d).add_(pm.detach(), alpha=1 - d)
-
-        x, loss, gn = engine.train_iteration(batch, seeds, c0, weights, tr["grad_clip"],
-                                             apply_update)
-        batch["x"] = x.detach()
-        pool.write_back(idx, batch)
-        window_n += 1
-        if (step + 1) % tr["log_every"] == 0 or step == step0:
-            with torch.no_grad():
-                from .rollout import decode_tokens
-
-                dec, _ = decode_tokens(model, x, batch["given4"][:, 0], batch["inputs"],
-                                       task.fill_given)
-                lm = batch.get("loss_mask")
-                scored = ~batch["given4"][:, 0] if lm is None else lm > 0
-                right = ((dec == batch["targets"]) & scored).sum(dim=(1, 2)).float()
-                n_sc = scored.sum(dim=(1, 2)).clamp_min(1)
-                stats = torch.stack([(right / n_sc).mean(), (right == n_sc).float().mean(),
-                                     batch["age"].float().mean(), loss, gn]).tolist()
-            now = time.time()
-            rec = dict(step=step + 1, loss=stats[3], grad_norm=stats[4],
-                       lr=sched.get_last_lr()[0], batch_cell_acc=stats[0], batch_exact=stats[1],
-                       mean_age=stats[2], skipped_steps=n_skipped, elapsed=now - t_start,
-                       iter_seconds=(now - window_t0) / max(1, window_n),
-                       peak_mem_gb=torch.cuda.max_memory_allocated(dev) / 2**30)
-            window_t0, window_n = now, 0
-            with open(log_path, "a") as f:
-                f.write(_json_line(rec))
+    run.write_run_json()
+    log_path = out / "log.jsonl"
+    t0 = t_window = time.time()
+    n_window = 0
+    run.model.train()
+    for step in range(run.step0, end_step):
+        batch, x, loss = run.iterate(step)
+        n_window += 1
+        last = step + 1 == end_step
+        if (step + 1) % tr["log_every"] == 0 or step == run.step0:
+            rec = run.log_record(step, batch, x, loss, t0, t_window, n_window)
+            t_window, n_window = time.time(), 0
+            _append_json(log_path, rec)
             if not quiet:
                 print(f"step {step + 1}/{tr['steps']} loss {rec['loss']:.4f} "
                       f"cell {rec['batch_cell_acc']:.3f} exact {rec['batch_exact']:.3f} "
                       f"{rec['iter_seconds']:.3f} s/it")
-        if val_boards is not None and ((step + 1) % tr["eval_every"] == 0 or step + 1 == end_step):
-            last_eval = evaluate(ema, task, val_boards, tr["eval"], N, seed)
-            last_eval["step"] = step + 1
-            with open(log_path, "a") as f:
-                f.write(_json_line({"eval": last_eval}))
-            model.train()
-            window_t0 = time.time()
-        if (step + 1) % tr["checkpoint_every"] == 0 or step + 1 == end_step:
-            torch.save(dict(model=model.state_dict(), ema=ema.state_dict(),
-                            opt=opt.state_dict(), sched=sched.state_dict(),
-                            pool={k: v for k, v in pool.state_dict().items() if v is not None},
-                            rng=_rng_state(rng), gen_dev=gen_dev.get_state(), step=step + 1),
-                       ckpt_path)
-
-    final = dict(model=ema.state_dict(), model_config=model.cfg.to_dict(), seed=seed,
-                 step=end_step)
-    if end_step < tr["steps"]:
-        final.update(target_steps=tr["steps"], training_complete=False)
-    torch.save(final, out / "final.pt")
-    summary = {"final_eval": last_eval, "train_seconds": time.time() - t_start,
-               "steps": end_step, "start_step": step0, "params": n_params,
-               "skipped_steps": n_skipped, "engine": engine.to_dict(),
-               "training_complete": end_step == tr["steps"],
-               "peak_mem_gb": torch.cuda.max_memory_allocated(dev) / 2**30}
-    if end_step < tr["steps"]:
-        summary["target_steps"] = tr["steps"]
-    (out / "summary.json").write_text(json.dumps(summary, indent=1))
-    return last_eval
+        if run.val_boards is not None and ((step + 1) % tr["eval_every"] == 0 or last):
+            run.last_eval = {**evaluate(run.ema, run.task, run.val_boards, tr["eval"],
+                                        run.engine.N, seed), "step": step + 1}
+            _append_json(log_path, {"eval": run.last_eval})
+            run.model.train()
+            t_window = time.time()
+        if (step + 1) % tr["checkpoint_every"] == 0 or last:
+            run.save_checkpoint(step + 1)
+    return run.finish(end_step, time.time() - t0)
