@@ -18,11 +18,17 @@ gated to 0.2 above confidence 0.9) the streamed C=32 kernel (one board per workg
 rollout in one launch). `--workload bptt30` times one training iteration: 64
 states sampled from a replay pool of 1,024 (30x30 DFS mazes, C=32 cell, bf16 forward with fp32
 master weights), a 32-step BPTT chunk with the per-cell cross-entropy on the 2-class path
-targets, AdamW, write-back; it reports cell-steps/s and the peak activation memory. Its roofline
+targets, the fused clip + AdamW + EMA update, write-back; it reports cell-steps/s and the peak
+activation memory. Its roofline
 prices 4x the forward FLOPs per cell-step against the dense MFMA peak of the chunk's compute
 type (bf16: the forward and every product of the backward run on bf16 MFMA, the backward with
 the reference's bf16 gradient rounding points), with the same rate against the fp32 peak beside
 it (frac_of_fp32_peak).
+
+The default run (the Sudoku workload) adds a `configs` block with every other configuration
+measured the same way, each with its roofline and CPU baseline: maze13 (C1), maze201 (C2, both
+regimes), hardmaze30 (C4) and bptt30 (C5, with the peak activation memory); `--no-configs`
+skips it.
 
 value = rows * H * W * D * steps / wall seconds (cell-updates/s). The roofline block prices the
 rollout kernel's algorithmic FLOPs (2 * (36 C + F * hidden + hidden * C) per cell-update, the
@@ -163,9 +169,66 @@ def cpu_baseline(wl, budget_s: float = 15.0):
         "unit": "cell-updates/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "cpu_model": cpu_model(),
         "sample": f"{rows} rows of the {H}x{W} C={model.cfg.channels} workload x {steps} steps, "
                   f"fp32, {dt:.1f} s",
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_bptt(wl, budget_s: float = 8.0):
+    """The CPU oracle's BPTT chunk (fp32 autograd of the restated chunk loss, the reference's
+    unfused path) on a board sample of the workload; cell-steps/s."""
+    from ncas_amd.model import build_model, init_weights
+    from oracle import nca_oracle as O
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from cells import oracle_cell
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    model = init_weights(build_model(wl["preset"]), seed=0, std=0.02, zero_last=False)
+    base = oracle_cell(model)
+    names = ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")
+    boards = make_boards(dict(wl, boards=2), 0)
+    inputs = torch.from_numpy(boards.inputs)
+    given4 = torch.from_numpy(boards.given)[:, None]
+    clamp = model.clamp_values(inputs)
+    B, H, W = inputs.shape
+    x0 = model.apply_clamp(torch.zeros(B, model.cfg.channels, H, W), given4, clamp)
+    targets = model.output_index(torch.from_numpy(boards.targets))
+    n = wl["depth"]
+    masks = torch.stack([O.fire_masks_np(0, 0, B, s, H, W, wl["p_fire"]) for s in range(n)])
+    weights = [1.0] * n
+
+    def once():
+        params = {k: getattr(base, k).detach().float().clone().requires_grad_(True)
+                  for k in names}
+        cell = O.OracleCell(**{**base.__dict__, **params})
+        loss = O.chunk_loss(cell, x0, given4, clamp, masks, targets, weights, "fp32",
+                            dtype=torch.float32)
+        loss.backward()
+
+    once()  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < budget_s and reps < 20):
+        once()
+        reps += 1
+    dt = time.perf_counter() - t0
+    return {"value": B * H * W * n * reps / dt, "unit": "cell-steps/s",
+            "cores": torch.get_num_threads(), "kind": "port", "cpu_model": cpu_model(),
+            "sample": f"{B} boards of the {H}x{W} C={model.cfg.channels} chunk x {n} steps x "
+                      f"{reps} forward + backward, fp32 autograd, {dt:.1f} s"}
 
 
 def calibration_copy(mib: int) -> None:
@@ -233,29 +296,34 @@ def run_gpu(wl, precision, steps, warmup, window_steps=0):
 
 
 def run_bptt(wl, precision, steps, warmup):
-    """Training iterations: pool sample -> 32-step BPTT chunk -> AdamW -> write-back."""
+    """Training iterations: pool sample -> 32-step BPTT chunk -> fused clip + AdamW + EMA ->
+    write-back."""
     from ncas_amd.model import build_model, init_weights
+    from ncas_amd.optim import FusedUpdate
     from ncas_amd.train import Engine, ReplayPool
 
     dev = torch.device("cuda:0")
     model = init_weights(build_model(wl["preset"]), seed=0, std=0.02, zero_last=False).to(dev)
+    ema = init_weights(build_model(wl["preset"]), seed=0, std=0.02, zero_last=False).to(dev)
     boards = make_boards(wl, 0)
     pool = ReplayPool(model, boards, wl["boards"], np.random.default_rng(0),
                       torch.Generator(device=dev).manual_seed(0))
     eng = Engine(model, None, {"rollout": wl["depth"], "chunk": wl["depth"], "amp": precision == "bf16"}, dev)
     # The reference's hard-maze training settings (configs/maze_hard.yaml: lr 5e-4, weight decay
-    # 1e-4, clip 1.0, linear warm-up over the first quarter of 10,000 steps).
-    opt = torch.optim.AdamW(model.parameters(), lr=5e-4, weight_decay=1e-4)
-    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda s: min(1.0, (s + 1) / 2500))
+    # 1e-4, clip 1.0, linear warm-up over the first quarter of 10,000 steps), EMA 0.999.
+    upd = FusedUpdate(model, ema, 5e-4, weight_decay=1e-4)
     rng = np.random.default_rng(1)
     weights = [1.0] * wl["depth"]
+    it = [0]
 
     def one():
         idx, batch = pool.sample(wl["batch"], 0.25)
         seeds = rng.integers(0, 2**62, size=wl["depth"])
-        opt.zero_grad(set_to_none=True)
-        x, loss, gn = eng.train_iteration(batch, seeds, 0, weights, 1.0, lambda g: opt.step())
-        sched.step()
+        lr = 5e-4 * min(1.0, (it[0] + 1) / 2500)
+        d = min(0.999, (1 + it[0]) / (10 + it[0]))
+        x, loss, _ = eng.train_iteration(batch, seeds, 0, weights, None,
+                                         lambda _g: upd.step(lr, d, 1.0))
+        it[0] += 1
         batch["x"] = x
         pool.write_back(idx, batch)
         return loss
@@ -281,6 +349,7 @@ def run_bptt(wl, precision, steps, warmup):
         "rows": wl["batch"], "loss": [float(v) for v in losses],
         "peak_activation_bytes": int(peak),
         "states_bytes": res.states_bytes, "workspace_bytes": res.workspace_bytes,
+        "skipped": int(upd.skipped),
     }
 
 
@@ -320,6 +389,98 @@ def roofline(name, wl, precision, res):
     return block
 
 
+def bptt_entry(wl, precision, steps, warmup, cpu_budget=None):
+    """The BPTT workload's measurement: cell-steps/s of whole training iterations, the roofline
+    of 4x the forward FLOPs per cell-step against the dense MFMA peak of the chunk's compute type
+    (fp32 peak beside it), the peak activation memory and the CPU oracle's chunk."""
+    res = run_bptt(wl, precision, steps, warmup)
+    return {
+        "metric": "BPTT cell-steps/sec on 1 MI355X (30x30 C=32, batch 64, 32-step chunk)",
+        "value": res["value"], "unit": "cell-steps/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": precision, "data": "synthetic",
+        "config": {"workload": wl["desc"], "rows": res["rows"], "grid": [wl["grid"]] * 2,
+                   "depth": wl["depth"]},
+        "roofline": {"bound": "mfma", "achieved": res["achieved_tflops"],
+                     "peak": PEAK_TFLOPS[precision], "unit": "TFLOP/s",
+                     "frac": res["achieved_tflops"] / PEAK_TFLOPS[precision], "traffic": None,
+                     "frac_of_fp32_peak": res["achieved_tflops"] / PEAK_TFLOPS["fp32"]},
+        "peak_activation_bytes": res["peak_activation_bytes"],
+        "states_bytes": res["states_bytes"], "workspace_bytes": res["workspace_bytes"],
+        "skipped_updates": res["skipped"], "loss": res["loss"],
+        "cpu_baseline": None if cpu_budget is None else cpu_baseline_bptt(wl, cpu_budget),
+    }
+
+
+def rollout_entry(name, wl, precision, steps, warmup, window_steps=0, cpu_budget=None,
+                  fp32=False, regimes=False):
+    """A rollout workload's measurement: cell-updates/s over the wall clock, the dominant
+    kernel's roofline (HIP events on its stream), optionally the fp32 run beside a bf16 one, the
+    other C2 regime, and the CPU oracle on a row sample."""
+    res = run_gpu(wl, precision, steps, warmup, window_steps)
+    print(f"# gpu {name} {precision}: {res['value']:.4g} cell-updates/s, kernel ms "
+          f"{[round(v, 3) for v in res['kernel_ms']]}", file=sys.stderr, flush=True)
+    H = W = wl["grid"]
+    entry = {
+        "metric": f"cell-updates/sec on 1 MI355X ({H}x{W} {name})",
+        "value": res["value"], "unit": "cell-updates/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": precision, "data": "synthetic",
+        "config": {"workload": wl["desc"], "rows": res["rows"], "grid": [H, W],
+                   "depth": wl["depth"], "k_trials": wl["k"]},
+        "roofline": roofline(name, wl, precision, res),
+        "kernel_ms": res["kernel_ms"],
+    }
+    if fp32 and precision == "bf16":
+        o = run_gpu(wl, "fp32", max(1, min(steps, 2)), 0)
+        entry["secondary"] = {"dtype": "fp32", "value": o["value"],
+                              "ms_per_step": o["ms_per_step"], "roofline_frac": o["frac"],
+                              "achieved_tflops": o["achieved_tflops"]}
+        print(f"# gpu fp32: {o['value']:.4g} cell-updates/s", file=sys.stderr, flush=True)
+    if regimes:
+        # the other C2 regime: per-step launches vs the temporally blocked kernel
+        alt = 2 if window_steps == 0 else 0
+        r2 = run_gpu(wl, precision, 1, 0, alt)
+        label = lambda t: "per_step" if t == 0 else f"temporal_T{t}"  # noqa: E731
+        entry["regimes"] = {
+            label(t): {"kernel_ms_per_step": float(np.mean(r["kernel_ms"])) / wl["depth"],
+                       "cell_updates_per_s": r["kernel_rate"],
+                       "roofline": roofline(name, wl, precision, r)}
+            for t, r in ((window_steps, res), (alt, r2))}
+        print(f"# regimes {entry['regimes']}", file=sys.stderr, flush=True)
+    cpu = None if cpu_budget is None else cpu_baseline(wl, cpu_budget)
+    entry["cpu_baseline"] = cpu
+    if cpu:
+        # the CPU baseline is the fp32 oracle: the like-for-like ratio is the fp32 GPU run's
+        entry["speedup_vs_cpu"] = res["value"] / cpu["value"]
+        fp32_value = res["value"] if precision == "fp32" else entry.get("secondary", {}).get("value")
+        if fp32_value:
+            entry["speedup_vs_cpu_fp32"] = fp32_value / cpu["value"]
+    return entry
+
+
+# every configuration beside the headline: (workload, precision, steps, warmup, CPU seconds)
+CONFIG_RUNS = (("maze13", "fp32", 10, 2, 4.0), ("maze201", "bf16", 2, 1, 4.0),
+               ("hardmaze30", "bf16", 2, 1, 4.0), ("bptt30", "bf16", 20, 3, 6.0))
+
+
+def configs_block() -> dict:
+    """C1, C2 (both regimes), C4 and C5 measured the same way as the headline."""
+    out = {}
+    for name, precision, steps, warmup, budget in CONFIG_RUNS:
+        wl = dict(WORKLOADS[name])
+        if name == "bptt30":
+            e = bptt_entry(wl, precision, steps, warmup, budget)
+        else:
+            e = rollout_entry(name, wl, precision, steps, warmup, cpu_budget=budget,
+                              regimes=name == "maze201")
+        e.pop("kernel_ms", None)
+        e.pop("loss", None)
+        out[name] = e
+        print(f"# config {name}: {e['value']:.4g} {e['unit']}", file=sys.stderr, flush=True)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -335,6 +496,8 @@ def main():
                     help="maze201: skip the secondary timing of the other regime")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-fp32", action="store_true", help="skip the secondary fp32 run")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations of the default run")
     ap.add_argument("--depth", type=int, default=0,
                     help="steps per rollout instead of the workload's own (profiling runs only)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
@@ -352,83 +515,19 @@ def main():
         wl["depth"] = args.depth
     if args.calib_copy_mib:
         calibration_copy(args.calib_copy_mib)
+    budget = None if args.no_cpu else 15.0
     if args.workload == "bptt30":
-        res = run_bptt(wl, args.precision, args.steps, args.warmup)
-        line = {
-            "metric": "BPTT cell-steps/sec on 1 MI355X (30x30 C=32, batch 64, 32-step chunk)",
-            "value": res["value"], "unit": "cell-steps/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": res["ms_per_step"], "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": args.precision, "data": "synthetic",
-            "config": {"workload": wl["desc"], "rows": res["rows"], "grid": [30, 30],
-                       "depth": wl["depth"]},
-            "roofline": {"bound": "mfma", "achieved": res["achieved_tflops"],
-                         "peak": PEAK_TFLOPS[args.precision], "unit": "TFLOP/s",
-                         "frac": res["achieved_tflops"] / PEAK_TFLOPS[args.precision],
-                         "traffic": None,
-                         "frac_of_fp32_peak": res["achieved_tflops"] / PEAK_TFLOPS["fp32"]},
-            "peak_activation_bytes": res["peak_activation_bytes"],
-            "states_bytes": res["states_bytes"], "workspace_bytes": res["workspace_bytes"],
-            "loss": res["loss"],
-        }
+        line = bptt_entry(wl, args.precision, args.steps, args.warmup,
+                          None if args.no_cpu else 8.0)
         print(json.dumps(line), flush=True)
         return
-    res = run_gpu(wl, args.precision, args.steps, args.warmup, args.window_steps)
-    print(f"# gpu {args.workload} {args.precision}: {res['value']:.4g} cell-updates/s, "
-          f"kernel ms {res['kernel_ms']}", file=sys.stderr, flush=True)
-    other = None
-    if not args.no_fp32 and args.precision == "bf16":
-        o = run_gpu(wl, "fp32", max(1, min(args.steps, 2)), 0)
-        other = {"dtype": "fp32", "value": o["value"], "ms_per_step": o["ms_per_step"],
-                 "roofline_frac": o["frac"], "achieved_tflops": o["achieved_tflops"]}
-        print(f"# gpu fp32: {o['value']:.4g} cell-updates/s", file=sys.stderr, flush=True)
-    regimes = None
-    if args.workload == "maze201" and not args.no_regimes:
-        # the other C2 regime: per-step launches vs the temporally blocked kernel
-        alt = 2 if args.window_steps == 0 else 0
-        r2 = run_gpu(wl, args.precision, 1, 0, alt)
-        name = lambda t: "per_step" if t == 0 else f"temporal_T{t}"  # noqa: E731
-        regimes = {name(args.window_steps): {"kernel_ms_per_step": float(np.mean(res["kernel_ms"])) / wl["depth"],
-                                              "cell_updates_per_s": res["kernel_rate"]},
-                   name(alt): {"kernel_ms_per_step": float(np.mean(r2["kernel_ms"])) / wl["depth"],
-                               "cell_updates_per_s": r2["kernel_rate"]}}
-        print(f"# regimes {regimes}", file=sys.stderr, flush=True)
-    cpu = None if args.no_cpu else cpu_baseline(wl)
-    H = W = wl["grid"]
-    line = {
-        "metric": "cell-updates/sec on 1 MI355X (9x9 K=128 D=256) + % of roofline",
-        "value": res["value"],
-        "unit": "cell-updates/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": res["ms_per_step"],
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": args.precision,
-        "data": "synthetic",
-        "config": {
-            "workload": wl["desc"],
-            "rows": res["rows"],
-            "grid": [H, W],
-            "depth": wl["depth"],
-            "k_trials": wl["k"],
-        },
-        "roofline": roofline(args.workload, wl, args.precision, res),
-        "cpu_baseline": cpu,
-        "kernel_ms": res["kernel_ms"],
-        "secondary": other,
-    }
-    if args.workload != "sudoku9":
-        line["metric"] = f"cell-updates/sec on 1 MI355X ({H}x{W} {args.workload})"
-    if regimes:
-        line["regimes"] = regimes
-    if cpu:
-        # the CPU baseline is the fp32 oracle: the like-for-like ratio is the fp32 GPU run's
-        line["speedup_vs_cpu"] = res["value"] / cpu["value"]
-        fp32_value = res["value"] if args.precision == "fp32" else (other or {}).get("value")
-        if fp32_value:
-            line["speedup_vs_cpu_fp32"] = fp32_value / cpu["value"]
+    line = rollout_entry(args.workload, wl, args.precision, args.steps, args.warmup,
+                         args.window_steps, budget, fp32=not args.no_fp32,
+                         regimes=args.workload == "maze201" and not args.no_regimes)
+    if args.workload == "sudoku9":
+        line["metric"] = "cell-updates/sec on 1 MI355X (9x9 K=128 D=256) + % of roofline"
+        if not args.no_configs and not args.depth:
+            line["configs"] = configs_block()
     print(json.dumps(line), flush=True)
 
 

@@ -252,7 +252,8 @@ def rollout(
 
 
 def chunk_loss(cell: OracleCell, x0, given4, clamp, masks, targets, weights, precision="fp32",
-               loss_mask=None, ste=True, final_cotangent=None, grad_round=False):
+               loss_mask=None, ste=True, final_cotangent=None, grad_round=False,
+               dtype=torch.float64):
     """The BPTT chunk's loss (engine.py:474-490 with the chunk's run_block, step.py:236-245):
     `n` steps from x0 with fire masks `masks` (n, B, 1, H, W), then
     L = sum_t w_t * step_loss(x_{t+1}) / max(sum_t w_t, 1), where step_loss is the mean (or the
@@ -261,8 +262,9 @@ def chunk_loss(cell: OracleCell, x0, given4, clamp, masks, targets, weights, pre
     differentiable w.r.t. the cell's tensors and x0; bf16 cells round at the forward's points
     (straight-through when `ste`; with `grad_round` the gradients of z, h and dx are rounded to
     bf16 as in the reference's bf16 backward). `final_cotangent` adds sum(x_n * final_cotangent),
-    whose gradient w.r.t. the last state is that cotangent (a later loss's gradient)."""
-    dt = torch.float64
+    whose gradient w.r.t. the last state is that cotangent (a later loss's gradient). `dtype`:
+    the arithmetic type (fp64 for the parity checks; fp32 times the reference's CPU path)."""
+    dt = dtype
     x = x0.to(dt)
     w = torch.as_tensor(weights, dtype=dt)
     total = x.new_zeros(())
