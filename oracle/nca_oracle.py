@@ -136,16 +136,64 @@ class _RoundBF16Grad(torch.autograd.Function):
         return g.to(torch.bfloat16).to(g.dtype)
 
 
+# fp32 summation orders of the bf16 step: torch's own, one rounding of the exact sum, and blocks
+# of 32 or 8 products (each block's exact sum rounded to fp32, the blocks added in fp32 in
+# ascending or, "r" prefix, descending order)
+SUM_ORDERS = ("torch", "exact", "block32", "block8", "rblock32")
+
+
+def _blocks(order: str) -> tuple[int, bool]:
+    """(block width, descending) of a "block<N>" / "rblock<N>" order."""
+    rev = order.startswith("r")
+    return int(order[6 if rev else 5:]), rev
+
+
+def _perceive_ordered(xp: torch.Tensor, k: torch.Tensor, H: int, W: int, order: str):
+    """`perceive` with another fp32 summation order of the 9 taps: "exact" sums the (exact)
+    products in fp64 and rounds once; the block orders add them one by one in fp32 in row-major
+    tap order (descending for "r" orders)."""
+    if order == "exact":
+        return perceive(xp.double(), k.double(), H, W).to(xp.dtype)
+    _, rev = _blocks(order)
+    B, C = xp.shape[:2]
+    K = k.shape[0]
+    acc = torch.zeros((B, K, C, H, W), dtype=xp.dtype)
+    taps = [(dy, dx) for dy in range(3) for dx in range(3)]
+    for dy, dx in (taps[::-1] if rev else taps):
+        tap = xp[:, None, :, dy:dy + H, dx:dx + W]
+        acc = acc + tap * k[:, 0, dy, dx].to(xp.dtype)[None, :, None, None, None]
+    return acc.reshape(B, K * C, H, W)
+
+
+def _linear_ordered(a: torch.Tensor, w: torch.Tensor, b: torch.Tensor, order: str):
+    """a @ w.T + b with another fp32 summation order: "exact" sums every dot product and its
+    bias in fp64 and rounds once; a block order rounds each block of N products' exact sum to
+    fp32 and adds the blocks one by one to the bias in fp32."""
+    if order == "exact":
+        return (a.double() @ w.double().T + b.double()).to(a.dtype)
+    n, rev = _blocks(order)
+    acc = b.to(a.dtype).expand(a.shape[0], w.shape[0]).clone()
+    starts = list(range(0, a.shape[1], n))
+    for k0 in (starts[::-1] if rev else starts):
+        acc = acc + (a[:, k0:k0 + n].double() @ w[:, k0:k0 + n].double().T).to(a.dtype)
+    return acc
+
+
 def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32",
                  dtype: torch.dtype | None = None, ste: bool = False,
-                 grad_round: bool = False) -> torch.Tensor:
+                 grad_round: bool = False, order: str = "torch") -> torch.Tensor:
     """Perception + MLP: the proposed dx of every cell (model.py:489-495). `dtype` overrides the
     compute type (fp64 for gradients); `ste` makes the bf16 rounding points straight-through;
     `grad_round` (with `ste`) also rounds the gradients of z, h and dx to bf16, the reference's
-    bf16 backward (the perception input's and the weights' gradients stay unrounded)."""
+    bf16 backward (the perception input's and the weights' gradients stay unrounded). `order`
+    changes only the fp32 summation order of the stencil and the two linear layers ("torch":
+    torch's conv2d and GEMM; the others: see `_perceive_ordered`, `_linear_ordered`),
+    which measures how far two correct fp32 implementations of the same bf16 step drift apart."""
     B, C, H, W = x.shape
     dt = dtype or _dtype(precision)
     bf = precision == "bf16"
+    if order not in SUM_ORDERS:
+        raise ValueError(f"order {order!r}")
     _bf = _RoundBF16.apply if ste else globals()["_bf"]
     _bfg = _RoundBF16Grad.apply if (ste and grad_round) else _bf
     x = x.to(dt)
@@ -153,18 +201,18 @@ def sense_update(cell: OracleCell, x: torch.Tensor, precision: str = "fp32",
     k = cell.kernels.to(dt)
     if bf:
         xp, k = _bf(xp), _bf(k)
-    z = perceive(xp, k, H, W)
+    z = perceive(xp, k, H, W) if order == "torch" else _perceive_ordered(xp, k, H, W, order)
     if bf:
         z = _bfg(z)
     rows = z.permute(0, 2, 3, 1).reshape(-1, z.shape[1])
     w1, b1, w2, b2 = (t.to(dt) for t in (cell.w1, cell.b1, cell.w2, cell.b2))
     if bf:
         w1, b1, w2, b2 = _bf(w1), _bf(b1), _bf(w2), _bf(b2)
-    h = rows @ w1.T + b1
+    h = rows @ w1.T + b1 if order == "torch" else _linear_ordered(rows, w1, b1, order)
     if bf:
         h = _bfg(h)
     h = torch.relu(h)
-    dx = h @ w2.T + b2
+    dx = h @ w2.T + b2 if order == "torch" else _linear_ordered(h, w2, b2, order)
     if bf:
         dx = _bfg(dx)
     return dx.reshape(B, H, W, C).permute(0, 3, 1, 2)
@@ -179,11 +227,11 @@ def apply_clamp(cell: OracleCell, x, given4, clamp):
 
 
 def step(cell: OracleCell, x, given4, clamp, fire, precision="fp32", noise=None, dtype=None, ste=False,
-         grad_round=False):
+         grad_round=False, order="torch"):
     """One step (model.py:503-559 without time embedding / normalisation). fire: (B,1,H,W)."""
     dt = dtype or _dtype(precision)
     x = x.to(dt)
-    dx = sense_update(cell, x, precision, dtype, ste, grad_round)
+    dx = sense_update(cell, x, precision, dtype, ste, grad_round, order)
     u = x + fire.to(dt) * dx.to(dt)
     if noise is not None:
         u = u + noise.to(dt)
@@ -218,10 +266,12 @@ def rollout(
     given_confident: bool = True,
     masks: torch.Tensor | None = None,
     trace=None,
+    order: str = "torch",
 ):
     """`n_steps` steps from x with Philox fire masks (or injected `masks` (n, B, 1, H, W)).
 
     Returns (x_final fp32, fired per row (B,) int64). `trace(t, x)` is called after each step.
+    `order`: the fp32 summation order of every step (`sense_update`).
     Adaptive firing (p_low, tau) reads the pre-step confidence of every cell, like
     rollout.py:220-222 -> model.py:589-593, with given cells counted as confident when
     `given_confident` (rollout.py:36).
@@ -243,7 +293,7 @@ def rollout(
             )
             fire = torch.from_numpy(m.astype(np.float32)).reshape(B, 1, H, W).to(x.dtype)
         fired += fire.reshape(B, -1).sum(1).to(torch.int64)
-        x = step(cell, x, given4, clamp, fire, precision)
+        x = step(cell, x, given4, clamp, fire, precision, order=order)
         if precision != "fp64":
             x = x.float()
         if trace is not None:
@@ -289,19 +339,21 @@ def chunk_loss(cell: OracleCell, x0, given4, clamp, masks, targets, weights, pre
 
 
 def bptt_chunk(cell: OracleCell, x0, given4, clamp, masks, targets, weights, precision="fp32",
-               loss_mask=None, grad_x0=False, ste=True, final_cotangent=None, grad_round=False):
+               loss_mask=None, grad_x0=False, ste=True, final_cotangent=None, grad_round=False,
+               dtype=torch.float64):
     """`chunk_loss` and its gradients by torch autograd in fp64 (`grad_round`: the reference's
-    bf16 gradient rounding points, see `_RoundBF16Grad`).
+    bf16 gradient rounding points, see `_RoundBF16Grad`; `dtype` float32 sums every product in
+    fp32 instead, which measures how much the sums' precision alone moves the result).
 
-    Returns (loss float, grads dict of fp64 tensors: kernels, w1, b1, w2, b2, head_w, head_b,
+    Returns (loss float, grads dict of `dtype` tensors: kernels, w1, b1, w2, b2, head_w, head_b,
     and x0 when grad_x0)."""
-    dt = torch.float64
+    dt = dtype
     names = ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")
     params = {k: getattr(cell, k).detach().to(dt).clone().requires_grad_(True) for k in names}
     c = OracleCell(**{**cell.__dict__, **params})
     x = x0.detach().to(dt).clone().requires_grad_(grad_x0)
     loss = chunk_loss(c, x, given4, clamp, masks, targets, weights, precision, loss_mask, ste,
-                      final_cotangent, grad_round)
+                      final_cotangent, grad_round, dtype=dt)
     wrt = [params[k] for k in names] + ([x] if grad_x0 else [])
     if not loss.requires_grad:  # every step weight is zero: a constant loss
         grads = [None] * len(wrt)

@@ -145,3 +145,37 @@ def one_step_errors(cell, x0, states, given4, clamp, masks, precision):
         errs.append((s - ref).abs().max().item())
         prev = s
     return errs
+
+
+# ------------------------------------------------------------------------------ bf16 drift
+# How far the oracle's own bf16 trajectory moves when only the fp32 summation order of its sums
+# changes: the largest max-abs state difference, over the trajectory's steps and over every pair
+# of the oracle's orders (oracle.nca_oracle.SUM_ORDERS: torch's conv / GEMM, one rounding of the
+# exact sum, blocks of 32 or 8 products ascending, blocks of 32 descending), for the exact
+# configuration of each GPU trajectory test. A bf16 step rounds z, h and dx after fp32 sums, so
+# two correct implementations that sum in different orders land on different sides of a bf16
+# rounding boundary now and then, and the cell's dynamics amplify those flips along a trajectory.
+# The GPU kernels are one more summation order: their trajectories are held within
+# DRIFT_MARGIN times these values. tests/test_oracle_drift.py recomputes every value and fails
+# when one here is above what it measures (values are rounded down). "bptt_x0": the relative
+# norm difference of the chunk's initial-state gradient between fp32 and fp64 sums.
+BF16_SELF_DRIFT = {
+    "rollout64/maze_c16": 0.0301, "rollout64/sudoku_c64": 0.0024,
+    "rollout64/maze_hard_c32": 0.0153, "rollout64/ref_maze_ood": 0.0401,
+    "rollout64/ref_maze_hard": 0.0266,
+    "stream32_uniform": 0.0136, "stream32_gated/configured": 0.0046,
+    "stream32_gated/median": 0.0046, "maze201": 0.2047,
+    "ws24/maze_c16/5x3": 0.0131, "ws24/maze_c16/1x1": 0.0083, "ws24/maze_c16/33x2": 0.0148,
+    "ws24/sudoku_c64/5x3": 0.0016, "ws24/sudoku_c64/1x1": 0.0010,
+    "ws24/sudoku_c64/33x2": 0.0017, "ws24/maze_hard_c32/5x3": 0.0080,
+    "ws24/maze_hard_c32/1x1": 0.0073, "ws24/maze_hard_c32/33x2": 0.0089,
+    "ws24/ref_maze_ood/5x3": 0.0092, "ws24/ref_maze_ood/1x1": 0.00006,
+    "ws24/ref_maze_ood/33x2": 0.0265,
+    "bptt_x0": 0.0284,
+}
+DRIFT_MARGIN = 1.5
+
+
+def drift_guard(key: str) -> float:
+    """The GPU's bf16 trajectory guard for configuration `key`."""
+    return DRIFT_MARGIN * BF16_SELF_DRIFT[key]

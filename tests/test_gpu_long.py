@@ -6,15 +6,17 @@ training shape, on the GPU through the C ABI.
   uniform firing and with confidence-gated firing (tau 0.9 as configured, and tau at the median
   confidence). For gated firing the oracle's own gating decision from the GPU's state equals the
   GPU's mask bit for bit at every step. The drift of the whole trajectory from the oracle's is
-  printed and held under 5x the bar (bf16 rounding flips amplify along a trajectory; a wrong
-  tap or weight shows as an O(1) error).
+  held within 1.5x the oracle's own drift when only its fp32 summation order changes
+  (cells.BF16_SELF_DRIFT, measured by tests/test_oracle_drift.py): bf16 rounding flips amplify
+  along a trajectory the same way for any correct summation order.
 * The 201x201 maze cell (C=16) on the per-step path: the wave-per-tile kernel in bf16 (the same
-  per-step bar and drift guard) and the halo-window kernel in fp32 (every one of 64 trajectory
+  per-step bar; the trajectory within 1.5x the oracle's own 64-step drift, 0.20) and the
+  halo-window kernel in fp32 (every one of 64 trajectory
   states within 1e-4), 2 boards, fired counts exact, fused == chained.
 * The BPTT chunk at its training shape: 30x30 hard mazes, C=32, bf16, a 32-step chunk (2
   boards): loss and every parameter gradient within a relative norm error of 2e-2 of the fp64
   straight-through oracle; the gradient of the initial state, which passes 32 bf16-rounded
-  Jacobians, within 5e-2.
+  Jacobians, within 1.5x the relative difference between the oracle's own fp32 and fp64 sums.
 """
 
 from __future__ import annotations
@@ -27,7 +29,8 @@ import pytest
 import torch
 
 sys.path.insert(0, __file__.rsplit("/", 1)[0])
-from cells import DYN, initial_state, one_step_errors, oracle_cell, perturbed_model  # noqa: E402
+from cells import (DYN, drift_guard, initial_state, one_step_errors, oracle_cell,  # noqa: E402
+                   perturbed_model)
 
 from ncas_amd import _lib  # noqa: E402
 from ncas_amd.inference import rollout_steps  # noqa: E402
@@ -95,9 +98,9 @@ def test_stream32_30x30_uniform_64_steps():
     step_errs = one_step_errors(cell, x, host, g4, cl, masks, "bf16")
     drift = [(s - r).abs().max().item() for s, r in zip(host, ref)]
     _say(f"worst one-step error {max(step_errs):.3g}, trajectory drift {max(drift):.3g} "
-         f"(at step {int(np.argmax(drift))})")
+         f"(at step {int(np.argmax(drift))}, guard {drift_guard('stream32_uniform'):.3g})")
     assert max(step_errs) <= TOL["bf16"]
-    assert max(drift) <= 5 * TOL["bf16"]
+    assert max(drift) <= drift_guard("stream32_uniform")
     assert torch.equal(fired, fr)
     with torch.no_grad():
         fused, _, ff = rollout_steps(md, xd, gd, cd, STEPS, step0=5, precision="bf16",
@@ -140,10 +143,11 @@ def test_stream32_30x30_gated_64_steps(tau_kind):
     host = [s.cpu() for s in states]
     step_errs = one_step_errors(cell, x, host, g4, cl, masks, "bf16")
     drift = [(s - r).abs().max().item() for s, r in zip(host, ref)]
+    guard = drift_guard(f"stream32_gated/{tau_kind}")
     _say(f"worst one-step error {max(step_errs):.3g}, trajectory drift {max(drift):.3g} "
-         f"(at step {int(np.argmax(drift))})")
+         f"(at step {int(np.argmax(drift))}, guard {guard:.3g})")
     assert max(step_errs) <= TOL["bf16"]
-    assert max(drift) <= 5 * TOL["bf16"]
+    assert max(drift) <= guard
     with torch.no_grad():
         fused, _, ff = rollout_steps(md, xd, gd, cd, STEPS, precision="bf16", want_fired=True, **kw)
     assert torch.equal(fused, states[-1]) and torch.equal(ff.cpu().long(), fired)
@@ -178,9 +182,9 @@ def test_maze201_per_step_path_64_steps(precision, path):
         masks = [O.fire_masks_np(3, 1, B, t, H, W, 0.5) for t in range(STEPS)]
         step_errs = one_step_errors(cell, x, host, g4, cl, masks, "bf16")
         _say(f"worst one-step error {max(step_errs):.3g}, trajectory drift {max(drift):.3g} "
-             f"(at step {int(np.argmax(drift))})")
+             f"(at step {int(np.argmax(drift))}, guard {drift_guard('maze201'):.3g})")
         assert max(step_errs) <= TOL["bf16"]
-        assert max(drift) <= 5 * TOL["bf16"]
+        assert max(drift) <= drift_guard("maze201")
     assert torch.equal(fired, fr)
     assert torch.equal(fused, states[-1]) and torch.equal(ff.cpu().long(), fr)
 
@@ -211,4 +215,4 @@ def test_bptt_bf16_30x30_32_step_chunk():
     _say("loss", float(res.loss), loss, "relative gradient errors", errs)
     assert abs(float(res.loss) - loss) <= 2e-2 * abs(loss)
     assert max(errs[k] for k in NAMES) <= 2e-2
-    assert errs["x0"] <= 5e-2
+    assert errs["x0"] <= drift_guard("bptt_x0")

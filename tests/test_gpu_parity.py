@@ -15,7 +15,8 @@ import pytest
 import torch
 
 sys.path.insert(0, __file__.rsplit("/", 1)[0])
-from cells import CELLS, boards_for, initial_state, make_model, one_step_errors, oracle_cell  # noqa: E402
+from cells import (CELLS, boards_for, drift_guard, initial_state, make_model,  # noqa: E402
+                   one_step_errors, oracle_cell)
 
 from ncas_amd.inference import rollout_steps  # noqa: E402
 from ncas_amd.readout import conf_select, readout  # noqa: E402
@@ -191,8 +192,8 @@ def test_rollout_64_steps_matches_oracle(name, precision):
     assert max(step_errs) <= TOL[precision]
     if precision == "fp32":
         assert max(traj) <= TOL["fp32"]
-    else:  # bf16: rounding flips amplify along the trajectory; O(1) errors would mean a bug
-        assert max(traj) <= 5 * TOL["bf16"]
+    else:  # bf16: within 1.5x the oracle's own drift under another fp32 summation order
+        assert max(traj) <= drift_guard(f"rollout64/{name}"), drift_guard(f"rollout64/{name}")
     assert torch.equal(fused, cur), "fused rollout differs from chained single steps"
     assert torch.equal(fired, fired_ref) and torch.equal(ff.cpu().long(), fired_ref)
     # the in-kernel board confidence is the readout of the final state, bit for bit
@@ -364,7 +365,8 @@ def test_wave_specialised_and_generic_kernels_agree(name, n_boards, k):
     """bf16 rollouts run by the wave-specialised kernel (default) and by the generic kernel,
     for odd row counts (a partial last workgroup, an empty row group): one step from the same
     state (the 24-step state of each) matches the oracle's step within 2e-2, fired counts are
-    exact, and the 24-step trajectories stay within the drift guard of the oracle's."""
+    exact, the 24-step states stay within 1.5x the oracle's own drift under another summation
+    order, and the two kernels agree bit for bit where they sum in the same order."""
     from ncas_amd import _lib
 
     _say("ws vs generic", name, n_boards, k)
@@ -387,8 +389,15 @@ def test_wave_specialised_and_generic_kernels_agree(name, n_boards, k):
             assert (y1.cpu() - ref1).abs().max().item() <= TOL["bf16"], path
     finally:
         L.nca_set_kernel_path(0)
+    guard = drift_guard(f"ws24/{name}/{n_boards}x{k}")
+    _say("drift per path", [(out[p][0] - xr).abs().max().item() for p in (0, 1)], "guard",
+         guard, "between paths", (out[0][0] - out[1][0]).abs().max().item())
     for path in (0, 1):
-        # 24 bf16 steps from the same state: trajectories within the drift guard of the oracle's
-        assert state_error(name, "bf16", out[path][0], xr) <= 5, path
+        # 24 bf16 steps from the same state: within 1.5x the oracle's own drift under another fp32
+        # summation order
+        assert (out[path][0] - xr).abs().max().item() <= guard, path
         assert torch.equal(out[path][2].long(), fr), path
-    assert (out[0][0] - out[1][0]).abs().max().item() <= TOL["bf16"] * 5
+    if name == "sudoku_c64":  # the C=64 kernels sum fc1 / fc2 in different orders
+        assert (out[0][0] - out[1][0]).abs().max().item() <= guard
+    else:  # the C=16 / C=32 wave-specialised and generic kernels sum in the same order
+        assert torch.equal(out[0][0], out[1][0])
