@@ -275,17 +275,29 @@ def test_full_c3_batch_rows_match_oracle():
         assert torch.isfinite(conf).all()
 
 
-def test_decode_and_selection_bit_exact_fp32():
-    """fp32 trajectory of 256 rows (32 boards x K=8) over 64 steps: every decoded argmax and
-    every conf@K index equals the oracle's trajectory's, with no exception for near-ties; the
-    smallest top-2 logit gap and the smallest conf@K gap are printed (the margins that fp32
-    summation-order differences would have to cross)."""
-    _say("decode + conf@K")
-    m, md, x, g4, cl = _case("sudoku_c64", n_boards=32, k=8)
+@pytest.mark.parametrize("weights,n_boards,k,depth", [
+    ("perturbed", 32, 8, 64),
+    ("perturbed", 4, 128, 256),  # the Sudoku conf@K workload's K and D
+    ("benchmark", 4, 128, 256),  # ... with its synthetic N(0, 0.02) weights and zero state
+])
+def test_decode_and_selection_bit_exact_fp32(weights, n_boards, k, depth):
+    """fp32 trajectories of n_boards x k rows over `depth` steps: every decoded argmax and every
+    conf@K index (k' = 1, 8, 32, k) equals the oracle trajectory's, with no exception for
+    near-ties; the smallest top-2 logit gap and the smallest conf@K gap are printed (the margins
+    that fp32 summation-order differences would have to cross)."""
+    _say("decode + conf@K", weights, n_boards, k, depth)
+    if weights == "perturbed":
+        m, md, x, g4, cl = _case("sudoku_c64", n_boards=n_boards, k=k)
+    else:
+        from ncas_amd.model import build_model, init_weights
+
+        m = init_weights(build_model("sudoku_c64"), seed=0, std=0.02, zero_last=False)
+        md = copy.deepcopy(m).to(DEV)
+        x, g4, cl = initial_state(m, boards_for("sudoku_c64", n_boards, 9, 0), k=k)
     cell = oracle_cell(m)
-    xr, _ = O.rollout(cell, x, g4, cl, 64, "fp32", seed=21)
+    xr, _ = O.rollout(cell, x, g4, cl, depth, "fp32", seed=21)
     with torch.no_grad():
-        y, conf, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), 64, seed=21)
+        y, conf, _ = rollout_steps(md, x.to(DEV), g4.to(DEV), cl.to(DEV), depth, seed=21)
         cc, cb, am = readout(md, y)
     rc, rb, ra = O.readout(cell, xr)
     # decode of the same state is bit-exact
@@ -298,15 +310,18 @@ def test_decode_and_selection_bit_exact_fp32():
     top2 = logits.topk(2, dim=1).values
     margin = float((top2[:, 0] - top2[:, 1]).min())
     mism = int((am.cpu().numpy() != ra).sum())
-    _say(f"argmax mismatches {mism} of {ra.size}, smallest top-2 logit gap {margin:.3g}")
+    _say(f"argmax mismatches {mism} of {ra.size}, smallest top-2 logit gap {margin:.3g}, "
+         f"largest state difference {(y.cpu() - xr).abs().max().item():.3g}")
     assert mism == 0
-    # conf@K selection
-    N, K = 32, 8
-    sel = conf_select(conf.view(N, K), None, K).cpu().numpy()
-    ref = clib.conf_select(rb.reshape(N, K), None, K)
-    srt = np.sort(rb.reshape(N, K), axis=1)
+    # conf@K selection, for several k'
+    srt = np.sort(rb.reshape(n_boards, k), axis=1)
     _say(f"smallest conf@K gap {float((srt[:, -1] - srt[:, -2]).min()):.3g}")
-    assert np.array_equal(sel, ref)
+    for kk in sorted({1, 8, 32, k}):
+        if kk > k:
+            continue
+        sel = conf_select(conf.view(n_boards, k), None, kk).cpu().numpy()
+        ref = clib.conf_select(rb.reshape(n_boards, k), None, kk)
+        assert np.array_equal(sel, ref), kk
 
 
 def test_conf_at_k_and_pass_at_k_on_the_gpu():
