@@ -213,7 +213,8 @@ int nca_sudoku_valid(const int64_t *pred, const int64_t *inputs, const uint8_t *
  * when gn is finite counters[0] += 1 and AdamW updates params, exp_avg and exp_avg_sq with the
  * bias corrections of that count, else counters[1] += 1 and they keep their values; then
  * ema = d ema + (1 - d) params (ema_decay d >= 0; d < 0 leaves ema alone, which may be NULL) and
- * grads = 0. No host synchronisation; deterministic. */
+ * grads = 0. workspace: NCA_ADAMW_WORKSPACE_BYTES of device memory (nothing in it is kept). Two
+ * launches, no host synchronisation; deterministic. */
 typedef struct {
     double lr;           /* this iteration's learning rate (the schedule applied) */
     double beta1, beta2;
@@ -223,9 +224,11 @@ typedef struct {
     double max_norm;     /* clip threshold, <= 0 for no clipping */
 } nca_adamw_desc;
 
+#define NCA_ADAMW_WORKSPACE_BYTES 1024 /* device workspace of nca_adamw_ema (the block sums) */
+
 int nca_adamw_ema(float *params, float *grads, float *exp_avg, float *exp_avg_sq, float *ema,
                   int64_t n, const nca_adamw_desc *desc, int64_t *counters, float *grad_norm,
-                  void *stream);
+                  void *workspace, void *stream);
 
 enum { NCA_DAMAGE_OURS = 0, NCA_DAMAGE_OFFICIAL = 1 };  /* perturb.py:43-83 geometries */
 
@@ -341,8 +344,14 @@ int nca_bptt_forward(const nca_cell_desc *cell, const void *packed, int64_t rows
  * nca_bptt_workspace_bytes of the same shape, may be passed; nothing in it is kept): the streamed
  * kernel then runs each board in two or three pieces of rows on as many workgroups, exchanging
  * their boundary rows through the workspace every step, when the device has a CU for every
- * piece. States are the same bit for bit. Replaces the same reference call as nca_bptt_forward
- * (src/nca/engine/engine.py:478-489, the chunk's forward under autograd). */
+ * piece. States are the same bit for bit in every case: a piece waits for its neighbour's rows
+ * a bounded time (about a second); if the pieces of a board are not resident together (CUs held
+ * by other work) and a wait runs out, the workspace's first 32-bit word is set to 1 and a repair
+ * launch queued behind the pieces recomputes every board whole (when no wait ran out, that
+ * launch's workgroups return at once). With workspace_bytes >= 256 the word is 0 otherwise, until
+ * the workspace is next written (nca_bptt_backward overwrites it). Replaces the same reference
+ * call as nca_bptt_forward (src/nca/engine/engine.py:478-489, the chunk's forward under
+ * autograd). */
 int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t rows, int32_t height,
                         int32_t width, const float *x0, const uint8_t *given, const float *clamp,
                         const nca_fire_desc *fire, int32_t n_chunk, float *states, void *workspace,
@@ -401,6 +410,21 @@ int nca_set_kernel_path(int path);
  * the automatic choice (one step per launch: the per-step kernels). Per calling thread. No
  * counterpart in the reference (the reference has no temporal blocking). */
 int nca_set_window_steps(int steps);
+
+/* Pieces per board that nca_bptt_forward_ws plans for this shape on a device of `cus` CUs
+ * (cus <= 0: the current device): 2 or 3 when every board's pieces fit the device at once, each
+ * piece has enough rows and fits the LDS; 1 for whole boards; 0 for an unsupported cell or
+ * grid. Host only. No counterpart in the reference. */
+int32_t nca_bptt_forward_pieces(const nca_cell_desc *cell, int64_t rows, int32_t height,
+                                int32_t width, int32_t cus);
+
+/* Test settings of the pieces of nca_bptt_forward_ws, for every thread: spin_limit > 0 bounds a
+ * wait for a neighbour's rows to that many re-reads; force_timeout != 0 makes every wait run out
+ * (it looks for a tag that never comes), so a test sees the status word set and the repair run
+ * while every kernel still ends; plan_cus > 0 plans pieces as for a device of that many CUs (more
+ * workgroups than the device holds at once, so the pieces of some boards are not resident
+ * together). (0, 0, 0) in use. No counterpart in the reference. */
+int nca_set_piece_debug(int32_t spin_limit, int32_t force_timeout, int32_t plan_cus);
 
 #ifdef __cplusplus
 }

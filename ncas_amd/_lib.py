@@ -15,6 +15,7 @@ _SO = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnca_hip.so")
 
 NCA_OK, NCA_ERR_INVALID, NCA_ERR_UNSUPPORTED, NCA_ERR_HIP = 0, 1, 2, 3
 NOALLOC_SCRATCH_BYTES = 128 << 20  # NCA_NOALLOC_SCRATCH_BYTES of include/nca_hip.h
+ADAMW_WORKSPACE_BYTES = 1024  # NCA_ADAMW_WORKSPACE_BYTES
 PADDING = {"zero": 0, "wall": 1, "wrap": 2}
 HEAD = {"mlp": 0, "l2": 1}
 PRECISION = {"fp32": 0, "bf16": 1}
@@ -46,6 +47,8 @@ EXPORTS = (
     "nca_maze_metrics",
     "nca_sudoku_valid",
     "nca_adamw_ema",
+    "nca_bptt_forward_pieces",
+    "nca_set_piece_debug",
     "nca_damage_clamp",
     "nca_maze_boards",
     "nca_sudoku_boards",
@@ -171,12 +174,15 @@ def load():
                                         i64, vp, vp]
     L.nca_maze_metrics.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, i64, i64, i64, vp, vp, vp]
     L.nca_sudoku_valid.argtypes = [vp, vp, vp, i64, i32, vp, vp]
-    L.nca_adamw_ema.argtypes = [vp, vp, vp, vp, vp, i64, ctypes.POINTER(AdamWDesc), vp, vp, vp]
+    L.nca_adamw_ema.argtypes = [vp, vp, vp, vp, vp, i64, ctypes.POINTER(AdamWDesc), vp, vp, vp,
+                                vp]
     L.nca_damage_clamp.argtypes = [vp, i64, i32, i32, i32, vp, i32, i32, ctypes.c_float, vp, vp,
                                    i32, i32, vp]
     L.nca_maze_boards.argtypes = [i64, i32, ctypes.c_uint64, ctypes.c_double, i32, i32, vp, vp, vp,
                                   vp, i32]
     L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]
+    L.nca_bptt_forward_pieces.argtypes = [ctypes.POINTER(CellDesc), i64, i32, i32, i32]
+    L.nca_set_piece_debug.argtypes = [i32, i32, i32]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
     L.nca_set_kernel_path.argtypes = [ctypes.c_int]

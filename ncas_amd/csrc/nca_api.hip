@@ -549,9 +549,15 @@ int check_grid(int64_t rows, int H, int W) {
 
 namespace nca {
 
+// CUs of the current device (cached per device)
+int device_cus();
+
 namespace {
 
-// CUs of the current device (cached per device)
+int recorded_pieces(const nca_cell_desc *cell, int64_t rows, int H, int W);
+
+}  // namespace
+
 int device_cus() {
     static int cus[64];
     int dev = 0;
@@ -563,6 +569,8 @@ int device_cus() {
     }
     return cus[dev];
 }
+
+namespace {
 
 int recorded_pieces(const nca_cell_desc *cell, int64_t rows, int H, int W) {
     return nca::stream32_pieces(rows, H, W, cell->c_out, cell->n_out, kLdsBytes, device_cus());
@@ -659,6 +667,23 @@ int nca_set_kernel_path(int path) {
                     path);
     g_path = path;
     return NCA_OK;
+}
+
+int nca_set_piece_debug(int32_t spin_limit, int32_t force_timeout, int32_t plan_cus) {
+    if (spin_limit < 0 || plan_cus < 0) return fail(NCA_ERR_INVALID, "spin_limit >= 0, plan_cus >= 0");
+    nca::g_piece_debug.spin_limit = spin_limit;
+    nca::g_piece_debug.force_timeout = force_timeout ? 1 : 0;
+    nca::g_piece_debug.plan_cus = plan_cus;
+    return NCA_OK;
+}
+
+int32_t nca_bptt_forward_pieces(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width,
+                                int32_t cus) {
+    g_err[0] = 0;
+    if (check_cell(cell) || check_grid(rows, height, width)) return 0;
+    if (!takes_stream32(cell, rows, height, width)) return 1;
+    return nca::stream32_pieces(rows, height, width, cell->c_out, cell->n_out, kLdsBytes,
+                                cus > 0 ? cus : nca::device_cus());
 }
 
 int nca_set_window_steps(int steps) {

@@ -39,6 +39,7 @@
 #include "nca_device.h"
 #include "nca_layout.h"
 #include "nca_status.h"
+#include "nca_stream.h"
 
 namespace {
 
@@ -1146,6 +1147,12 @@ int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t r
         rc = nca::hip_status(hipMemcpyAsync(states, x0, sn * sizeof(float), hipMemcpyDeviceToDevice, st), "state copy");
         if (rc) return rc;
     }
+    // the workspace's first word reports whether a wait of the boards' pieces ran out: zero unless
+    // this call sets it
+    if (workspace && workspace_bytes >= nca::kXchStatusBytes &&
+        (rc = nca::hip_status(nca::clear_words(static_cast<uint64_t *>(workspace), nca::kXchStatusBytes / 8, st),
+                              "status clear")))
+        return rc;
     // the whole chunk in one launch of the streamed kernel where it takes the cell and grid
     bool used = false;
     if ((rc = nca::rollout_recorded(cell, packed, rows, height, width, x0, given, clamp, states + n_chunk * sn, fire,

@@ -138,6 +138,14 @@ struct St32Params {
     // W, 32) words of (step tag << 32 | fp32 bits), all zero at the launch
     int P, Hp;
     uint64_t *xch;
+    // a piece whose wait for a neighbour's row runs out sets *halo_status to 1 (the host clears
+    // it); a wait re-reads at most spin_limit times; tag_skew (0 in use) makes every wait look
+    // for a tag that never comes, so the host can force the bounded waits to run out
+    uint32_t *halo_status;
+    int spin_limit, tag_skew;
+    // the repair launch after a launch in pieces: whole boards, run only when *run_if != 0 (a
+    // piece's wait ran out), otherwise every workgroup returns at once
+    const uint32_t *run_if;
 };
 
 // zsw: the Z row swizzle (a permutation of 0..15)
@@ -152,6 +160,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
     const RolloutParams &a = sp.a;
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
 
+    if (REC && sp.run_if && __hip_atomic_load(sp.run_if, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // the workgroup runs rows [r0, r0 + Hs) of board `row`: all of it, or piece `piece` of P. An
     // even piece streams its rows top to bottom, an odd one bottom to top, so two neighbours
@@ -643,8 +652,11 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
             // interval (((k + 1) HW) >> 4) - 1 >= hB + 5. A neighbour writes its last row of state
             // k in its step k - 1 and its first row of state k + 1 early in step k, intervals
             // before hB when the two run in step. A word whose tag is not yet that state's is
-            // read again; after kHaloSpin reads the halo takes NaN (which reaches every result),
-            // no later refresh waits, and the kernel still ends.
+            // read again; after sp.spin_limit reads (kHaloSpin, about a second, in use) the halo
+            // takes NaN (which reaches every result), *sp.halo_status is set, no later refresh
+            // of the thread waits, and the kernel still ends; the host's repair launch then
+            // recomputes the boards whole (a wait runs out only when the pieces of a board are
+            // not resident together).
             const int th = tid - 256;  // 0 .. 127 over the stencil waves
             const int NE = W * S::C;
             const int nf = down ? piece - 1 : piece + 1, nl = down ? piece + 1 : piece - 1;
@@ -668,14 +680,16 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 float *Mh = reinterpret_cast<float *>(smem + sp.l_M + (unsigned)(mrow * (W + 1) + 1) * S::MS);
                 // while a word is not yet tagged st, the thread's words are read again together
                 // (one round trip a try)
-                auto stale = [&](int k) { return th + 128 * k < NE && (uint32_t)(hw[k] >> 32) != (uint32_t)st; };
+                const uint32_t want = (uint32_t)(st + sp.tag_skew);
+                auto stale = [&](int k) { return th + 128 * k < NE && (uint32_t)(hw[k] >> 32) != want; };
                 for (int n = 0; !hfail; ++n) {
                     bool any = false;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) any |= stale(k);
                     if (!any) break;
-                    if (n == kHaloSpin) {
+                    if (n >= sp.spin_limit) {
                         hfail = true;
+                        __hip_atomic_fetch_or(sp.halo_status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         break;
                     }
                     __builtin_amdgcn_s_sleep(2);

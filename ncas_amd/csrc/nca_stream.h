@@ -24,8 +24,23 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
                            uint64_t *xch = nullptr);
 
 // Workgroups per board for a recording call on a device of `cus` CUs (1: whole boards), and the
-// exchange bytes that takes.
+// exchange bytes that takes: a status block of kXchStatusBytes (its first word is set to 1 when
+// a piece's wait for its neighbour ran out) and the exchange slots.
 int stream32_pieces(int64_t rows, int H, int W, int c_out, int n_out, unsigned lds_limit, int cus);
 size_t stream32_xch_bytes(int64_t rows, int P, int W);
+constexpr size_t kXchStatusBytes = 256;
+
+// Zero n 8-byte words on the stream (a kernel, so the call can sit in a captured graph).
+hipError_t clear_words(uint64_t *x, int64_t n, hipStream_t st);
+
+// Test settings of the pieces' bounded waits and of their planning (nca_set_piece_debug):
+// spin_limit > 0 replaces the wait's limit of re-reads; force_timeout makes every wait look for a
+// tag that never comes (so it runs out after spin_limit re-reads); plan_cus > 0 plans pieces as
+// for a device of that many CUs (a launch too large to be resident is then refused and the
+// boards run whole). All zero in use.
+struct PieceDebug {
+    int spin_limit = 0, force_timeout = 0, plan_cus = 0;
+};
+extern PieceDebug g_piece_debug;
 
 }  // namespace nca

@@ -55,6 +55,7 @@ bool stream32_fits(int H, int W, int padding, int c_out, int n_out, unsigned lds
 // (Hs - 1) W >= 240 (a halo refresh fits between the taps that read the old and the new row) and
 // the piece's plan fits the LDS.
 int stream32_pieces(int64_t rows, int H, int W, int c_out, int n_out, unsigned lds_limit, int cus) {
+    if (g_piece_debug.plan_cus > 0) cus = g_piece_debug.plan_cus;
     for (int P = 3; P >= 2; --P) {
         const int Hp = (H + P - 1) / P, last = H - (P - 1) * Hp;
         if (last < 1 || rows * P > cus) continue;
@@ -67,7 +68,7 @@ int stream32_pieces(int64_t rows, int H, int W, int c_out, int n_out, unsigned l
 }
 
 size_t stream32_xch_bytes(int64_t rows, int P, int W) {
-    return P > 1 ? (size_t)rows * P * 2 * 4 * W * St32::C * sizeof(uint64_t) : 0;
+    return P > 1 ? kXchStatusBytes + (size_t)rows * P * 2 * 4 * W * St32::C * sizeof(uint64_t) : 0;
 }
 
 __global__ void xch_clear(uint64_t *x, int64_t n) {
@@ -75,8 +76,18 @@ __global__ void xch_clear(uint64_t *x, int64_t n) {
         x[e] = 0;
 }
 
+hipError_t clear_words(uint64_t *x, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const int64_t b = (n + 255) / 256;
+    hipLaunchKernelGGL(xch_clear, dim3((unsigned)(b < 256 ? b : 256)), dim3(256), 0, st, x, n);
+    return hipGetLastError();
+}
+
+PieceDebug g_piece_debug;
+
 // pieces > 1 (recording only): P workgroups per board exchanging their boundary rows through xch,
-// stream32_xch_bytes of device memory that this call clears before the launch
+// stream32_xch_bytes of device memory that this call clears before the launch, then the repair
+// launch (whole boards, run only if a piece's wait ran out)
 hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_limit, bool *used, int pieces,
                            uint64_t *xch) {
     *used = false;
@@ -86,52 +97,73 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
     const int hw = p.H * p.W;
     if ((int64_t)p.n_steps * hw + 64 > 0x7fffffff) return hipSuccess;
     if (p.rows > 0x7fffffff) return hipSuccess;
-    const int P = (pieces > 1 && p.x_rec && !p.adaptive && !p.conf_out && !p.fired_out && xch) ? pieces : 1;
-    const int Hp = (p.H + P - 1) / P;
-    const St32Plan L = st32_plan(P > 1 ? Hp : p.H, p.W, p.c_out, p.n_out, P > 1);
-    St32Params sp;
-    memset(&sp, 0, sizeof(sp));
-    sp.a = p;
-    sp.P = P;
-    sp.Hp = P > 1 ? Hp : 0;
-    sp.xch = P > 1 ? xch : nullptr;
-    sp.l_gidx = L.gidx;
-    sp.NM = L.NM;
-    sp.RING = L.RING;
-    sp.T = (int)(((int64_t)p.n_steps * hw + 15) / 16);
-    sp.l_M = L.M;
-    sp.l_Z = L.Z;
-    sp.l_D = L.D;
-    sp.l_cinfo = L.cinfo;
-    sp.l_ring = L.ring;
-    sp.l_given = L.given;
-    sp.l_head = L.head;
-    sp.l_evp = L.evp;
-    sp.l_flags = L.flags;
-    sp.off_w1q = p.off_w1q;
-    sp.off_w2k = p.off_w2k;
-    sp.fast_conf = p.adaptive && p.head_kind == 0 && p.n_out == 2;
-    sp.conf_s = conf_threshold(p.tau);
     if (p.x_rec && p.adaptive) return hipSuccess;  // recording is for uniform firing
+    const int P = (pieces > 1 && p.x_rec && !p.adaptive && !p.conf_out && !p.fired_out && xch) ? pieces : 1;
     auto kfn = p.adaptive ? rollout_stream32<true, false>
                           : (p.x_rec ? rollout_stream32<false, true> : rollout_stream32<false, false>);
-    // pieces: more than half the LDS, so no two workgroups share a CU (each piece runs alongside
-    // its neighbours)
-    const unsigned lds = P > 1 && L.total <= lds_limit / 2 ? lds_limit / 2 + 16u : L.total;
     // the attribute is the limit for every launch of the function (whole boards and pieces take
     // different sizes), so calls from several host threads cannot undercut one another's
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kfn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit);
     if (e != hipSuccess) return e;
     if (p.rows <= 0) return hipSuccess;
+    uint32_t *status = P > 1 ? reinterpret_cast<uint32_t *>(xch) : nullptr;
+    // one launch of np workgroups per board (1: whole boards); run_if: the repair launch
+    auto launch = [&](int np, const uint32_t *run_if) -> hipError_t {
+        const int Hp = (p.H + np - 1) / np;
+        const St32Plan L = st32_plan(np > 1 ? Hp : p.H, p.W, p.c_out, p.n_out, np > 1);
+        St32Params sp;
+        memset(&sp, 0, sizeof(sp));
+        sp.a = p;
+        sp.P = np;
+        sp.Hp = np > 1 ? Hp : 0;
+        sp.xch = np > 1 ? xch + kXchStatusBytes / sizeof(uint64_t) : nullptr;
+        sp.halo_status = np > 1 ? status : nullptr;
+        sp.spin_limit = g_piece_debug.spin_limit > 0 ? g_piece_debug.spin_limit : kHaloSpin;
+        sp.tag_skew = g_piece_debug.force_timeout ? (1 << 30) : 0;
+        sp.run_if = run_if;
+        sp.l_gidx = L.gidx;
+        sp.NM = L.NM;
+        sp.RING = L.RING;
+        sp.T = (int)(((int64_t)p.n_steps * hw + 15) / 16);
+        sp.l_M = L.M;
+        sp.l_Z = L.Z;
+        sp.l_D = L.D;
+        sp.l_cinfo = L.cinfo;
+        sp.l_ring = L.ring;
+        sp.l_given = L.given;
+        sp.l_head = L.head;
+        sp.l_evp = L.evp;
+        sp.l_flags = L.flags;
+        sp.off_w1q = p.off_w1q;
+        sp.off_w2k = p.off_w2k;
+        sp.fast_conf = p.adaptive && p.head_kind == 0 && p.n_out == 2;
+        sp.conf_s = conf_threshold(p.tau);
+        // pieces: more than half the LDS, so no two workgroups share a CU (each piece runs
+        // alongside its neighbours)
+        const unsigned lds = np > 1 && L.total <= lds_limit / 2 ? lds_limit / 2 + 16u : L.total;
+        hipLaunchKernelGGL(kfn, dim3((unsigned)(p.rows * np)), dim3(512), lds, st, sp);
+        return hipGetLastError();
+    };
     if (P > 1) {
         const int64_t n = (int64_t)(stream32_xch_bytes(p.rows, P, p.W) / sizeof(uint64_t));
         hipLaunchKernelGGL(xch_clear, dim3(256), dim3(256), 0, st, xch, n);
         if ((e = hipGetLastError()) != hipSuccess) return e;
+        // The pieces of a board wait on one another, and nothing makes the runtime keep them
+        // resident together (a cooperative launch would, but on this runtime it held the host
+        // back for the rest of the training iteration: 3.5 - 5.3 ms per 64-board 30x30 iteration
+        // against 3.4 ms, and 3.6 - 3.8 ms from a stream of its own). A wait that runs out sets
+        // the status word instead, and the repair launch then recomputes every board whole,
+        // overwriting the pieces' states, so the states are right in every case; when no wait ran
+        // out its workgroups return at once (a few microseconds).
+        if ((e = launch(P, nullptr)) != hipSuccess) return e;
+        if ((e = launch(1, status)) != hipSuccess) return e;
+        *used = true;
+        return hipSuccess;
     }
-    hipLaunchKernelGGL(kfn, dim3((unsigned)(p.rows * P)), dim3(512), lds, st, sp);
+    if ((e = launch(1, nullptr)) != hipSuccess) return e;
     *used = true;
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 }  // namespace nca

@@ -7,10 +7,10 @@
 //   runs clip_grad_norm_ (src/nca/engine/engine.py), a host test of the norm, torch's AdamW, a
 //   Python loop of EMA updates and zero_grad (src/nca/engine/train.py:262-273). Here the norm's
 //   test and the count of applied steps (AdamW's `step`, which a skipped iteration does not
-//   advance) live on the device, so an iteration needs no host synchronisation; a single
-//   workgroup sums the squares in a fixed order (each thread a strided run in fp64, then fixed
-//   butterflies), so the update is deterministic and a run resumed from a checkpoint repeats the
-//   uninterrupted run bit for bit. The per-element arithmetic is torch's multi-tensor AdamW's,
+//   advance) live on the device, so an iteration needs no host synchronisation; the squares are
+//   summed in a fixed order (fp64: each thread a strided run, fixed butterflies, the blocks'
+//   sums in block order), so the update is deterministic and a run resumed from a checkpoint
+//   repeats the uninterrupted run bit for bit. The per-element arithmetic is torch's multi-tensor AdamW's,
 //   operation for operation in fp32 with the same scalars: p *= 1 - lr wd; m = lerp(m, g, 1 - b1);
 //   v = v b2 + (1 - b2) g g; p += -(lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps).
 //
@@ -31,7 +31,15 @@
 
 namespace {
 
-constexpr int kOptThreads = 1024;
+// Two launches over a fixed grid: the first writes each block's sum of squares (the blocks'
+// elements are a fixed grid-stride partition, a thread's squares are added in a fixed order, then
+// fixed butterflies) and a copy of the applied-step count; the second has every block add the
+// partial sums in the same order, so every block sees the same norm and decision, and update its
+// elements. Only the second kernel's block 0 writes the counters, and no block reads them there
+// (the copy stands in), so no block can see another's update.
+constexpr int kOptBlocks = 64;
+constexpr int kOptThreads = 256;
+constexpr int kUnroll = 4;
 
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
@@ -40,37 +48,54 @@ __device__ __forceinline__ double wave_sum(double v) {
 }
 
 __global__ void __launch_bounds__(kOptThreads)
-    adamw_ema_kernel(float *__restrict__ p, float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
-                     float *__restrict__ e, int64_t n, nca_adamw_desc d, int64_t *__restrict__ counters,
-                     float *__restrict__ grad_norm) {
+    adamw_norm_kernel(const float *__restrict__ g, int64_t n, const int64_t *__restrict__ counters,
+                      double *__restrict__ ws) {
     __shared__ double part[kOptThreads / 64];
-    __shared__ float s_coef, s_wd, s_w1, s_b2, s_w2, s_bc2, s_eps, s_step, s_ed, s_ea;
-    __shared__ int s_ok, s_clip, s_ema;
     const int tid = threadIdx.x;
+    const int64_t stride = (int64_t)kOptBlocks * kOptThreads;
     double acc = 0.0;
-    for (int64_t i = tid; i < n; i += kOptThreads) {
-        const double x = (double)g[i];
-        acc += x * x;
+    for (int64_t base = (int64_t)blockIdx.x * kOptThreads + tid; base < n; base += stride * kUnroll) {
+        float gv[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t i = base + (int64_t)u * stride;
+            gv[u] = i < n ? g[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) acc += (double)gv[u] * (double)gv[u];
     }
     acc = wave_sum(acc);
     if ((tid & 63) == 0) part[tid >> 6] = acc;
     __syncthreads();
     if (tid == 0) {
-        double s = 0.0;
-        for (int w = 0; w < kOptThreads / 64; ++w) s += part[w];
-        const float gn = (float)sqrt(s);
+        double b = 0.0;
+        for (int w = 0; w < kOptThreads / 64; ++w) b += part[w];
+        ws[blockIdx.x] = b;
+        if (blockIdx.x == 0) ws[kOptBlocks] = (double)counters[0];
+    }
+}
+
+__global__ void __launch_bounds__(kOptThreads)
+    adamw_ema_kernel(float *__restrict__ p, float *__restrict__ g, float *__restrict__ m, float *__restrict__ v,
+                     float *__restrict__ e, int64_t n, nca_adamw_desc d, int64_t *__restrict__ counters,
+                     float *__restrict__ grad_norm, const double *__restrict__ ws) {
+    __shared__ float s_coef, s_wd, s_w1, s_b2, s_w2, s_bc2, s_eps, s_step, s_ed, s_ea;
+    __shared__ int s_ok, s_clip, s_ema;
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+        double sum = 0.0;
+        for (int b = 0; b < kOptBlocks; ++b) sum += ws[b];
+        const float gn = (float)sqrt(sum);
         const bool ok = isfinite(gn);
-        grad_norm[0] = gn;
         s_clip = d.max_norm > 0.0;
-        float coef = (float)d.max_norm / (gn + 1e-6f);
+        const float coef = (float)d.max_norm / (gn + 1e-6f);
         s_coef = coef < 1.0f ? coef : 1.0f;
         s_ok = ok;
         s_ema = d.ema_decay >= 0.0;
         s_ed = (float)d.ema_decay;
         s_ea = (float)(1.0 - d.ema_decay);
+        const int64_t t = (int64_t)ws[kOptBlocks] + 1;
         if (ok) {
-            const int64_t t = counters[0] + 1;
-            counters[0] = t;
             const double bc1 = 1.0 - pow(d.beta1, (double)t), bc2 = 1.0 - pow(d.beta2, (double)t);
             s_wd = (float)(1.0 - d.lr * d.weight_decay);
             s_w1 = (float)(1.0 - d.beta1);
@@ -79,35 +104,57 @@ __global__ void __launch_bounds__(kOptThreads)
             s_bc2 = (float)sqrt(bc2);
             s_eps = (float)d.eps;
             s_step = (float)(-(d.lr / bc1));
-        } else {
-            counters[1] += 1;
+        }
+        if (blockIdx.x == 0) {
+            grad_norm[0] = gn;
+            if (ok)
+                counters[0] = t;
+            else
+                counters[1] += 1;
         }
     }
     __syncthreads();
     const bool ok = s_ok, clip = s_clip, ema = s_ema;
     const float coef = s_coef, wd = s_wd, w1 = s_w1, b2 = s_b2, w2 = s_w2, bc2 = s_bc2, eps = s_eps,
                 step = s_step, ed = s_ed, ea = s_ea;
-    for (int64_t i = tid; i < n; i += kOptThreads) {
-        float pi = p[i];
-        if (ok) {
-            float gi = g[i];
-            if (clip) gi = gi * coef;
-            pi = pi * wd;
-            float mi = m[i];
-            mi = w1 < 0.5f ? mi + w1 * (gi - mi) : gi - (gi - mi) * (1.0f - w1);
-            float vi = v[i] * b2;
-            vi = vi + w2 * (gi * gi);
-            const float den = sqrtf(vi) / bc2 + eps;
-            pi = pi + step * (mi / den);
-            p[i] = pi;
-            m[i] = mi;
-            v[i] = vi;
+    const int64_t stride = (int64_t)kOptBlocks * kOptThreads;
+    for (int64_t base = (int64_t)blockIdx.x * kOptThreads + tid; base < n; base += stride * kUnroll) {
+        float pv[kUnroll], gv[kUnroll], mv[kUnroll], vv[kUnroll], ev[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t i = base + (int64_t)u * stride;
+            const bool in = i < n;
+            pv[u] = in ? p[i] : 0.0f;
+            gv[u] = in && ok ? g[i] : 0.0f;
+            mv[u] = in && ok ? m[i] : 0.0f;
+            vv[u] = in && ok ? v[i] : 0.0f;
+            ev[u] = in && ema ? e[i] : 0.0f;
         }
-        if (ema) {
-            float ei = e[i] * ed;
-            e[i] = ei + ea * pi;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t i = base + (int64_t)u * stride;
+            if (i >= n) break;
+            float pi = pv[u];
+            if (ok) {
+                float gi = gv[u];
+                if (clip) gi = gi * coef;
+                pi = pi * wd;
+                float mi = mv[u];
+                mi = w1 < 0.5f ? mi + w1 * (gi - mi) : gi - (gi - mi) * (1.0f - w1);
+                float vi = vv[u] * b2;
+                vi = vi + w2 * (gi * gi);
+                const float den = sqrtf(vi) / bc2 + eps;
+                pi = pi + step * (mi / den);
+                p[i] = pi;
+                m[i] = mi;
+                v[i] = vi;
+            }
+            if (ema) {
+                const float ei = ev[u] * ed;
+                e[i] = ei + ea * pi;
+            }
+            g[i] = 0.0f;
         }
-        g[i] = 0.0f;
     }
 }
 
@@ -151,19 +198,25 @@ __global__ void __launch_bounds__(kDamageThreads)
 }  // namespace
 
 extern "C" int nca_adamw_ema(float *params, float *grads, float *exp_avg, float *exp_avg_sq, float *ema, int64_t n,
-                             const nca_adamw_desc *desc, int64_t *counters, float *grad_norm, void *stream) {
+                             const nca_adamw_desc *desc, int64_t *counters, float *grad_norm, void *workspace,
+                             void *stream) {
     nca::clear_error();
     if (!desc) return nca::set_error(NCA_ERR_INVALID, "NULL descriptor");
     if (n < 1) return nca::set_error(NCA_ERR_INVALID, "n >= 1");
-    if (!params || !grads || !exp_avg || !exp_avg_sq || !counters || !grad_norm)
+    if (!params || !grads || !exp_avg || !exp_avg_sq || !counters || !grad_norm || !workspace)
         return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    static_assert((kOptBlocks + 1) * sizeof(double) <= NCA_ADAMW_WORKSPACE_BYTES, "workspace size");
     if (desc->ema_decay >= 0.0 && !ema) return nca::set_error(NCA_ERR_INVALID, "ema_decay >= 0 needs the EMA buffer");
     if (!(desc->beta1 >= 0.0 && desc->beta1 < 1.0 && desc->beta2 >= 0.0 && desc->beta2 < 1.0 && desc->eps >= 0.0 &&
           desc->lr >= 0.0 && desc->weight_decay >= 0.0 && desc->ema_decay <= 1.0))
         return nca::set_error(NCA_ERR_INVALID, "0 <= beta1, beta2 < 1; eps, lr, weight_decay >= 0; ema_decay <= 1");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(adamw_ema_kernel, dim3(1), dim3(kOptThreads), 0, st, params, grads, exp_avg, exp_avg_sq, ema, n,
-                       *desc, counters, grad_norm);
+    double *ws = static_cast<double *>(workspace);
+    hipLaunchKernelGGL(adamw_norm_kernel, dim3(kOptBlocks), dim3(kOptThreads), 0, st, grads, n, counters, ws);
+    int rc = nca::hip_status(hipGetLastError(), "adamw norm launch");
+    if (rc) return rc;
+    hipLaunchKernelGGL(adamw_ema_kernel, dim3(kOptBlocks), dim3(kOptThreads), 0, st, params, grads, exp_avg, exp_avg_sq,
+                       ema, n, *desc, counters, grad_norm, ws);
     return nca::hip_status(hipGetLastError(), "adamw launch");
 }
 

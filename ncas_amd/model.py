@@ -322,11 +322,25 @@ class NCA(nn.Module):
         lo = self.cfg.out_offset - self.cfg.in_offset
         return self.embed[targets][..., lo: lo + self.cfg.c_out].permute(0, 3, 1, 2)
 
+    def token_table(self, kind: str, device) -> torch.Tensor:
+        """Small lookup tables on the device, uploaded once per device without a host wait:
+        "tokens" (class index -> output token) and "index" (token -> class index, 0 for tokens
+        that are no output)."""
+        key = (kind, str(device))
+        cache = self.__dict__.setdefault("_tables", {})
+        t = cache.get(key)
+        if t is None:
+            if kind == "tokens":
+                host = np.asarray(self.cfg.output_tokens, dtype=np.int64)
+            else:
+                host = np.zeros(self.cfg.vocab_size, dtype=np.int64)
+                for i, tok in enumerate(self.cfg.output_tokens):
+                    host[tok] = i
+            t = cache[key] = _lib.upload(host, torch.device(device))
+        return t
+
     def output_index(self, targets):
-        lut = torch.zeros(self.cfg.vocab_size, dtype=torch.long, device=targets.device)
-        for i, t in enumerate(self.cfg.output_tokens):
-            lut[t] = i
-        return lut[targets]
+        return self.token_table("index", targets.device)[targets]
 
     # ------------------------------------------------------------------ HIP operators
     def step(self, x, given4, clamp, fire_mask, noise=None, clock=None, precision="fp32"):
@@ -351,8 +365,7 @@ class NCA(nn.Module):
 
     def decode(self, x):
         idx = self.readout(x)[2].long()
-        tokens = torch.tensor(self.cfg.output_tokens, device=x.device)
-        return tokens[idx]
+        return self.token_table("tokens", x.device)[idx]
 
     def extra_repr(self) -> str:
         return ", ".join(f"{k}={v}" for k, v in self.cfg.to_dict().items())

@@ -56,6 +56,7 @@ class FusedUpdate:
         self.exp_avg_sq = torch.zeros_like(self.flat)
         self.counters = torch.zeros(2, dtype=torch.int64, device=dev)  # applied, skipped
         self.grad_norm = torch.zeros((), dtype=torch.float32, device=dev)
+        self._ws = torch.empty(_lib.ADAMW_WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
         off = 0
         self._slices = []
         for p in self.params:
@@ -79,7 +80,8 @@ class FusedUpdate:
         _lib.check(_lib.load().nca_adamw_ema(
             self.flat.data_ptr(), self.grad.data_ptr(), self.exp_avg.data_ptr(),
             self.exp_avg_sq.data_ptr(), _lib.ptr(self.ema), self.n, ctypes.byref(d),
-            self.counters.data_ptr(), self.grad_norm.data_ptr(), _lib.stream_of(dev)),
+            self.counters.data_ptr(), self.grad_norm.data_ptr(), self._ws.data_ptr(),
+            _lib.stream_of(dev)),
             "nca_adamw_ema")
         # the kernel wrote the parameters behind torch's back: bump their version counters, so
         # caches keyed on them (the models' packed weights) see the change

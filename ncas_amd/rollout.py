@@ -77,8 +77,7 @@ def decode_tokens(model, x, given, inputs, fill_given: bool = True):
     """Decoded tokens (B, H, W) and board confidence (B,) of states x. With `fill_given` (maze,
     Sudoku) given cells show their input token (reference rollout.py:74-82)."""
     _, conf, idx = readout(model, x)
-    tokens = torch.tensor(model.cfg.output_tokens, device=x.device)
-    dec = tokens[idx.long()]
+    dec = model.token_table("tokens", x.device)[idx.long()]
     return (torch.where(given, inputs, dec) if fill_given else dec), conf
 
 

@@ -82,6 +82,9 @@ class ChunkResult:
     grad_x0: torch.Tensor | None
     states_bytes: int            # bytes of the kept chunk states
     workspace_bytes: int         # bytes of the backward's workspace
+    halo_failed: torch.Tensor | None = None  # device bool: a wait of the forward's board
+    #                pieces ran out and the forward was recomputed on whole boards (the states
+    #                are right either way)
 
 
 def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step_seeds=None,
@@ -134,6 +137,8 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                                      xs.data_ptr(), g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd),
                                      n, states.data_ptr(), ws.data_ptr(), ws_bytes, stream),
                "nca_bptt_forward_ws")
+    # the forward's status word, read on the stream before the backward overwrites the workspace
+    halo_failed = ws[:1].view(torch.int32) != 0
     # fp32 master weights for the backward GEMMs (rounded to bf16 on load for bf16 cells)
     params = _params(model)
     master = [p.detach().to(dev, torch.float32).contiguous() for p in params]
@@ -151,7 +156,8 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                                    stream), "nca_bptt_backward")
     # no wait: the host arrays were read during the calls, and the device buffers freed here are
     # reused only by later work on the same stream
-    return ChunkResult(states[n].clone(), loss, grads, gx0, states.numel() * 4, ws_bytes)
+    return ChunkResult(states[n].clone(), loss, grads, gx0, states.numel() * 4, ws_bytes,
+                       halo_failed)
 
 
 # ------------------------------------------------------------------------------ losses

@@ -182,3 +182,29 @@ def test_operators_refuse_cpu_tensors():
     c = torch.zeros(1, 4, 13, 13)
     with pytest.raises((ValueError, RuntimeError)):
         rollout_steps(m, x, g, c, 2)
+
+
+def test_bptt_forward_piece_plan(lib):
+    """The planning of nca_bptt_forward_ws's board pieces (host only): three pieces while every
+    board's pieces fit the CUs at once, else two, else whole boards; none for grids whose pieces
+    would be too short for a halo refresh, for fp32 cells (no streamed kernel) and an unsupported
+    cell; the test override of the CU count (nca_set_piece_debug) replaces the device's."""
+    c32 = _cell(channels=32, hidden=256, c_in=4, c_out=4, out_offset=4, n_out=2, padding=1)
+    plan = lambda rows, H=30, W=30, cus=256, c=c32: lib.nca_bptt_forward_pieces(  # noqa: E731
+        ctypes.byref(c), rows, H, W, cus)
+    assert plan(64) == 3 and plan(85) == 3 and plan(86) == 2 and plan(128) == 2
+    assert plan(129) == 1 and plan(1000) == 1
+    assert plan(64, cus=128) == 2 and plan(64, cus=100) == 1
+    assert plan(8, H=13, W=13) == 1  # pieces of 5 rows: too short
+    assert plan(8, H=20, W=30) == 2  # 10-row pieces; thirds of 7 rows are too short
+    c32f = _cell(channels=32, hidden=256, c_in=4, c_out=4, out_offset=4, n_out=2, padding=1,
+                 precision=0)
+    assert plan(64, c=c32f) == 1
+    assert plan(64, c=_cell(channels=24)) == 0
+    try:
+        assert lib.nca_set_piece_debug(0, 0, 10_000) == 0
+        assert plan(1000, cus=256) == 3  # the override wins
+    finally:
+        lib.nca_set_piece_debug(0, 0, 0)
+    assert plan(1000) == 1
+    assert lib.nca_set_piece_debug(-1, 0, 0) == _lib.NCA_ERR_INVALID

@@ -347,3 +347,89 @@ def test_bptt_30x30_hard_maze_chunk_matches_oracle():
     states = 33 * 64 * 32 * 900 * 4
     _say(f"full chunk: states {states / 2**20:.1f} MiB + workspace {ws / 2**20:.1f} MiB")
     assert 0 < ws < 512 * 2**20
+
+
+def _pieces_case(rows, n=4, seed=7):
+    from ncas_amd.rng import fire_desc
+    m = perturbed_model("maze_hard_c32", seed, *DYN["maze_hard_c32"])
+    md = copy.deepcopy(m).to(DEV)
+    g = torch.Generator().manual_seed(seed)
+    H = W = 30
+    x = (torch.randn((rows, 32, H, W), generator=g) * 0.3).to(DEV)
+    g8 = (torch.rand((rows, 1, H, W), generator=g) < 0.3).to(torch.uint8).to(DEV).contiguous()
+    cl = torch.randn((rows, m.cfg.c_in, H, W), generator=g).to(DEV)
+    fd = fire_desc(9, 0.7, None, None, True, 0, 3, None, None)
+    return md, md.packed("bf16", DEV), x, g8, cl, fd, n
+
+
+def _forward(L, pk, x, g8, cl, fd, n, ws=None):
+    rows, C, H, W = x.shape
+    out = torch.full((n + 1, rows, C, H, W), float("nan"), device=DEV)
+    nbytes = 0 if ws is None else ws.numel() * 4
+    _lib.check(L.nca_bptt_forward_ws(ctypes.byref(pk.desc), pk.buf.data_ptr(), rows, H, W,
+                                     x.data_ptr(), g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd),
+                                     n, out.data_ptr(), None if ws is None else ws.data_ptr(),
+                                     nbytes, _lib.stream_of(DEV)), "nca_bptt_forward_ws")
+    return out
+
+
+def test_bptt_pieces_status_word():
+    """The forward in pieces (64 boards of 30x30: three pieces each) leaves the workspace's status
+    word at 0; with the pieces' waits forced to run out (a host setting: every wait looks for a
+    tag that never comes and gives up after 4 re-reads) every kernel still ends, the word is 1,
+    and the repair launch has recomputed the boards whole: the states still equal the whole-board
+    forward's bit for bit. bptt_chunk reports the word as ChunkResult.halo_failed."""
+    _say("bptt pieces status")
+    L = _lib.load()
+    md, pk, x, g8, cl, fd, n = _pieces_case(64)
+    assert L.nca_bptt_forward_pieces(ctypes.byref(pk.desc), 64, 30, 30, 0) == 3
+    ws_bytes = L.nca_bptt_workspace_bytes(ctypes.byref(pk.desc), 64, 30, 30, n)
+    ws = torch.full((ws_bytes // 4,), float("nan"), device=DEV)
+    whole = _forward(L, pk, x, g8, cl, fd, n)
+    good = _forward(L, pk, x, g8, cl, fd, n, ws)
+    torch.cuda.synchronize()
+    assert int(ws[:1].view(torch.int32).item()) == 0
+    assert torch.equal(good, whole)
+    targets = torch.zeros((64, 30, 30), dtype=torch.int64, device=DEV)
+    ref = bptt_chunk(md, x, g8.bool(), cl, targets, [1.0] * n, seed=9, p_fire=0.7,
+                     precision="bf16")
+    try:
+        assert L.nca_set_piece_debug(4, 1, 0) == 0
+        forced = _forward(L, pk, x, g8, cl, fd, n, ws)
+        torch.cuda.synchronize()
+        assert int(ws[:1].view(torch.int32).item()) == 1
+        assert torch.equal(forced, whole)
+        res = bptt_chunk(md, x, g8.bool(), cl, targets, [1.0] * n, seed=9, p_fire=0.7,
+                         precision="bf16")
+        assert bool(res.halo_failed.all())
+        assert torch.equal(res.x, ref.x) and torch.equal(res.loss, ref.loss)
+        assert all(torch.equal(res.grads[k], ref.grads[k]) for k in ref.grads)
+    finally:
+        L.nca_set_piece_debug(0, 0, 0)
+    again = _forward(L, pk, x, g8, cl, fd, n, ws)
+    torch.cuda.synchronize()
+    assert int(ws[:1].view(torch.int32).item()) == 0 and torch.equal(again, whole)
+    assert not bool(ref.halo_failed.any())
+
+
+def test_bptt_pieces_not_resident_together():
+    """Planned as for a device of 10,000 CUs, 200 boards take three pieces each: 600 workgroups of
+    which at most one fits a CU, more than the device holds at once, so the pieces of some boards
+    are not resident together. With the waits bounded to 64 re-reads, a piece whose neighbour is
+    not resident gives up (the status word is then 1 and the repair recomputes the boards whole);
+    either way the states equal the whole-board forward's bit for bit."""
+    _say("bptt pieces not resident together")
+    L = _lib.load()
+    md, pk, x, g8, cl, fd, n = _pieces_case(200, n=3, seed=8)
+    whole = _forward(L, pk, x, g8, cl, fd, n)
+    try:
+        assert L.nca_set_piece_debug(64, 0, 10_000) == 0
+        assert L.nca_bptt_forward_pieces(ctypes.byref(pk.desc), 200, 30, 30, 0) == 3
+        ws_bytes = L.nca_bptt_workspace_bytes(ctypes.byref(pk.desc), 200, 30, 30, n)
+        ws = torch.full((ws_bytes // 4,), float("nan"), device=DEV)
+        got = _forward(L, pk, x, g8, cl, fd, n, ws)
+        torch.cuda.synchronize()
+    finally:
+        L.nca_set_piece_debug(0, 0, 0)
+    _say("status word", int(ws[:1].view(torch.int32).item()))
+    assert torch.equal(got, whole)
