@@ -8,8 +8,9 @@
 //      reference src/nca/model.py:140-152), with the cell's given flag, injected mask and clamp
 //      values, all loaded for the next tile while this one computes (vmcnt counts in order, so a
 //      tile's own loads must all be older than the next tile's);
-//   2. the 3x3 perception of its 4 channels on v_dot2_f32_bf16 over tap pairs (the taps rounded
-//      to bf16 like the forward's perception buffer) -> z, through a wave-private LDS block to
+//   2. the 3x3 perception of its 4 channels on v_mfma_f32_4x4x4_16b_bf16 over tap pairs (the taps
+//      rounded to bf16 like the forward's perception buffer; one pair per MFMA, which sums
+//      exactly as the other kernels' v_dot2 chains do) -> z, through a wave-private LDS block to
 //      the fc1 operand layout;
 //   3. fc1 on v_mfma_f32_16x16x32_bf16 (W1 fragments in registers, b1 from LDS as the initial
 //      accumulators), ReLU and bf16 rounding, through the wave's LDS block to fc2's operand
@@ -39,6 +40,7 @@ struct Step16Params {
 };
 
 typedef float s16_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // FIRST equals sp.first: the clamp values are loaded (and the loop carries them) on a call's
 // first step only
@@ -53,14 +55,25 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int H = a.H, W = a.W, HWn = H * W;
 
-    // ---- constants: stencil kernels as bf16 pairs, W1 / W2 fragments, biases
+    // ---- constants: stencil B operands, W1 / W2 fragments, biases
+    // The stencil runs on v_mfma_f32_4x4x4_16b_bf16: block b = lane / 4 multiplies 4 cells' tap
+    // pairs (A rows) by the 4 kernels (B columns, kernel j = lane & 3). Each MFMA adds one tap pair
+    // to the accumulator: the B operand holds kernel j's pair in k slots 0-1 or 2-3 and zeros in
+    // the others, so the A operand can be two adjacent packed pairs of the lane's channel as they
+    // are. One pair of products plus the accumulator rounds exactly like v_dot2_f32_bf16 (checked
+    // bit for bit on 16.8M operand sets, the zeros in either half, unit and tiny magnitudes), so
+    // the five MFMAs per channel give the v_dot2 chain's sums of the other kernels bit for bit.
     const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
-    uint32_t kp[4][5];
+    s16x4 kb[5];
+    {
+        const int j = r & 3;
+        uint32_t kp[5];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+        for (int p2 = 0; p2 < 4; ++p2) kp[p2] = pack_bf16x2(kern[j * 9 + 2 * p2], kern[j * 9 + 2 * p2 + 1]);
+        kp[4] = pack_bf16x2(kern[j * 9 + 8], 0.0f);
 #pragma unroll
-        for (int pr = 0; pr < 4; ++pr) kp[k][pr] = pack_bf16x2(kern[k * 9 + 2 * pr], kern[k * 9 + 2 * pr + 1]);
-        kp[k][4] = pack_bf16x2(kern[k * 9 + 8], 0.0f);
+        for (int p2 = 0; p2 < 5; ++p2)
+            kb[p2] = __builtin_bit_cast(s16x4, (p2 & 1) ? make_uint2(0u, kp[p2]) : make_uint2(kp[p2], 0u));
     }
     bf16x8 w1f[8][2];  // [m-tile][k-tile]: W1[16 mt + r][32 kt + 8g + j]
 #pragma unroll
@@ -169,24 +182,24 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     // what the compute of a tile keeps of its loads: the taps as bf16 pairs of one channel (taps
     // 2p and 2p + 1, tap 8 with a zero; halo taps replaced by the padding value), the cell's fp32
     // quad, flags and mask / clamp values
+    // the stencil's A operands of channel c: taps 0-3 and 4-7 as two bf16 pairs each, tap 8 with
+    // a zero (pairs (t0, t1), (t2, t3) / (t4, t5), (t6, t7) / (t8, 0), 0)
     struct TileCur {
-        uint32_t pr[5][4];  // [tap pair][channel]
+        u32x2 ta[4], tb[4], tc[4];
         float xo[4], fin, cv[4];
         int gv, fu8;
     };
     auto unpack = [&](const TileIn &in, TileCur &cu) __attribute__((always_inline)) {
         auto pack = [&](const float4 *tp) __attribute__((always_inline)) {
+            const float *f[9];
 #pragma unroll
-            for (int p2 = 0; p2 < 4; ++p2) {
-                cu.pr[p2][0] = pack_bf16x2(tp[2 * p2].x, tp[2 * p2 + 1].x);
-                cu.pr[p2][1] = pack_bf16x2(tp[2 * p2].y, tp[2 * p2 + 1].y);
-                cu.pr[p2][2] = pack_bf16x2(tp[2 * p2].z, tp[2 * p2 + 1].z);
-                cu.pr[p2][3] = pack_bf16x2(tp[2 * p2].w, tp[2 * p2 + 1].w);
+            for (int tt = 0; tt < 9; ++tt) f[tt] = reinterpret_cast<const float *>(&tp[tt]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                cu.ta[c] = u32x2{pack_bf16x2(f[0][c], f[1][c]), pack_bf16x2(f[2][c], f[3][c])};
+                cu.tb[c] = u32x2{pack_bf16x2(f[4][c], f[5][c]), pack_bf16x2(f[6][c], f[7][c])};
+                cu.tc[c] = u32x2{pack_bf16x2(f[8][c], 0.0f), 0u};
             }
-            cu.pr[4][0] = pack_bf16x2(tp[8].x, 0.0f);
-            cu.pr[4][1] = pack_bf16x2(tp[8].y, 0.0f);
-            cu.pr[4][2] = pack_bf16x2(tp[8].z, 0.0f);
-            cu.pr[4][3] = pack_bf16x2(tp[8].w, 0.0f);
         };
         pack(in.tp);
         // tiles with a cell on the grid's edge pack again with the padding value in place of the
@@ -232,24 +245,25 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         const int q = 16 * tir + r;
         const bool valid = q < HWn;
 
-        // 2. perception: bf16 tap pairs per channel, v_dot2 against the kernel pairs
+        // 2. perception: per channel of the lane's quad, five MFMAs over the tap pairs; lane
+        // (r, g) receives z of kernel j = r & 3 for cells 4 (r >> 2) + i, channel 4 g + c
         {
-            const uint32_t(&pr)[5][4] = cur.pr;
+            s16_f32x4 zc[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float z[4];
+            for (int c = 0; c < 4; ++c) zc[c] = s16_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p2 = 0; p2 < 5; ++p2)
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    float s = dot2_bf16_zero(pr[0][c], kp[k][0]);
-#pragma unroll
-                    for (int p2 = 1; p2 < 5; ++p2)
-                        s = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), s, false);
-                    z[c] = s;
+                    const u32x2 av = p2 < 2 ? cur.ta[c] : p2 < 4 ? cur.tb[c] : cur.tc[c];
+                    zc[c] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, av), kb[p2], zc[c], 0, 0,
+                                                                   0);
                 }
-                // feature k C + 4g + c of cell r
-                *reinterpret_cast<uint2 *>(zw + r * 144 + 2 * (k * C + 4 * g)) =
-                    uint2{pack_bf16x2(z[0], z[1]), pack_bf16x2(z[2], z[3])};
-            }
+            const int j = r & 3, c0 = 4 * (r >> 2);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)  // feature j C + 4g + c of cell c0 + i
+                *reinterpret_cast<uint2 *>(zw + (c0 + i) * 144 + 2 * (j * C + 4 * g)) =
+                    uint2{pack_bf16x2(zc[0][i], zc[1][i]), pack_bf16x2(zc[2][i], zc[3][i])};
         }
         // 3. fc1 (the LDS block is this wave's own: its writes above precede these reads, a
         // wave's LDS operations complete in order)
@@ -347,8 +361,7 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         // alive across its new loads, and the compiler then carries the buffer in two register
         // sets copied at the end of every iteration (38 moves per tile)
 #pragma unroll
-        for (int p2 = 0; p2 < 5; ++p2)
-            asm volatile("" : "+v"(cu.pr[p2][0]), "+v"(cu.pr[p2][1]), "+v"(cu.pr[p2][2]), "+v"(cu.pr[p2][3]));
+        for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(cu.ta[c]), "+v"(cu.tb[c]), "+v"(cu.tc[c]));
         asm volatile("" : "+v"(cu.xo[0]), "+v"(cu.xo[1]), "+v"(cu.xo[2]), "+v"(cu.xo[3]));
         asm volatile("" : "+v"(cu.fin), "+v"(cu.gv), "+v"(cu.fu8));
         if (FIRST) asm volatile("" : "+v"(cu.cv[0]), "+v"(cu.cv[1]), "+v"(cu.cv[2]), "+v"(cu.cv[3]));

@@ -104,13 +104,19 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
     const int by0 = ay.lo - ay.h0, bx0 = ax.lo - ax.h0;  // board coordinates of window cell (0, 0)
 
     // ---- constants (as step_stream16)
+    // the stencil's B operands on v_mfma_f32_4x4x4_16b_bf16, as in step_stream16: kernel j = lane & 3,
+    // one tap pair per MFMA (zeros in the other k slots), which sums as the v_dot2 chain does
     const float *kern = reinterpret_cast<const float *>(a.packed + a.off_kern);
-    uint32_t kp[4][5];
+    s16x4 kb[5];
+    {
+        const int j = r & 3;
+        uint32_t kp[5];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+        for (int p2 = 0; p2 < 4; ++p2) kp[p2] = pack_bf16x2(kern[j * 9 + 2 * p2], kern[j * 9 + 2 * p2 + 1]);
+        kp[4] = pack_bf16x2(kern[j * 9 + 8], 0.0f);
 #pragma unroll
-        for (int pr = 0; pr < 4; ++pr) kp[k][pr] = pack_bf16x2(kern[k * 9 + 2 * pr], kern[k * 9 + 2 * pr + 1]);
-        kp[k][4] = pack_bf16x2(kern[k * 9 + 8], 0.0f);
+        for (int p2 = 0; p2 < 5; ++p2)
+            kb[p2] = __builtin_bit_cast(s16x4, (p2 & 1) ? make_uint2(0u, kp[p2]) : make_uint2(kp[p2], 0u));
     }
     bf16x8 w1f[8][2];
 #pragma unroll
@@ -264,36 +270,45 @@ __global__ void __launch_bounds__(512, 1) rollout_window16(Win16Params wp) {
                 tb[tt][0] = v.x;
                 tb[tt][1] = v.y;
             }
-            // 2. perception (v_dot2 over tap pairs) -> z in the staging block
+            // 2. perception (five 4x4x4 MFMAs per channel over the tap pairs) -> z in the staging
+            // block; lane (r, g) receives kernel j = r & 3 of cells 4 (r >> 2) + i, channel 4 g + c
             {
-                uint32_t pr[5][4];
+                typedef uint32_t w16_u32x2 __attribute__((ext_vector_type(2)));
+                w16_u32x2 ta[4], tbp[4], tc[4];
 #pragma unroll
-                for (int p2 = 0; p2 < 4; ++p2) {
-                    const uint32_t *x0 = tb[2 * p2], *x1 = tb[2 * p2 + 1];
-                    pr[p2][0] = __builtin_amdgcn_perm(x1[0], x0[0], 0x05040100u);
-                    pr[p2][1] = __builtin_amdgcn_perm(x1[0], x0[0], 0x07060302u);
-                    pr[p2][2] = __builtin_amdgcn_perm(x1[1], x0[1], 0x05040100u);
-                    pr[p2][3] = __builtin_amdgcn_perm(x1[1], x0[1], 0x07060302u);
+                for (int q = 0; q < 2; ++q) {  // taps 4q .. 4q + 3 -> ta (q = 0) or tbp (q = 1)
+                    const uint32_t *x0 = tb[4 * q], *x1 = tb[4 * q + 1], *x2 = tb[4 * q + 2], *x3 = tb[4 * q + 3];
+                    w16_u32x2 *dst = q ? tbp : ta;
+                    dst[0] = w16_u32x2{__builtin_amdgcn_perm(x1[0], x0[0], 0x05040100u),
+                                       __builtin_amdgcn_perm(x3[0], x2[0], 0x05040100u)};
+                    dst[1] = w16_u32x2{__builtin_amdgcn_perm(x1[0], x0[0], 0x07060302u),
+                                       __builtin_amdgcn_perm(x3[0], x2[0], 0x07060302u)};
+                    dst[2] = w16_u32x2{__builtin_amdgcn_perm(x1[1], x0[1], 0x05040100u),
+                                       __builtin_amdgcn_perm(x3[1], x2[1], 0x05040100u)};
+                    dst[3] = w16_u32x2{__builtin_amdgcn_perm(x1[1], x0[1], 0x07060302u),
+                                       __builtin_amdgcn_perm(x3[1], x2[1], 0x07060302u)};
                 }
-                pr[4][0] = tb[8][0] & 0xffffu;
-                pr[4][1] = tb[8][0] >> 16;
-                pr[4][2] = tb[8][1] & 0xffffu;
-                pr[4][3] = tb[8][1] >> 16;
+                tc[0] = w16_u32x2{tb[8][0] & 0xffffu, 0u};
+                tc[1] = w16_u32x2{tb[8][0] >> 16, 0u};
+                tc[2] = w16_u32x2{tb[8][1] & 0xffffu, 0u};
+                tc[3] = w16_u32x2{tb[8][1] >> 16, 0u};
+                typedef float w16_zf32x4 __attribute__((ext_vector_type(4)));
+                w16_zf32x4 zc[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    float z[4];
+                for (int c = 0; c < 4; ++c) zc[c] = w16_zf32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int p2 = 0; p2 < 5; ++p2)
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        float sacc = dot2_bf16_zero(pr[0][c], kp[k][0]);
-#pragma unroll
-                        for (int p2 = 1; p2 < 5; ++p2)
-                            sacc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(pr[p2][c]), as_bf16x2(kp[k][p2]), sacc, false);
-                        z[c] = sacc;
+                        const w16_u32x2 av = p2 < 2 ? ta[c] : p2 < 4 ? tbp[c] : tc[c];
+                        zc[c] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, av), kb[p2], zc[c], 0,
+                                                                       0, 0);
                     }
-                    // features 16k + 4g .. +3: chunk 2k + g / 2, half g & 1
-                    *reinterpret_cast<uint2 *>(zw + win_zoff(r, 2 * k + (g >> 1)) + 8 * (g & 1)) =
-                        uint2{pack_bf16x2(z[0], z[1]), pack_bf16x2(z[2], z[3])};
-                }
+                const int j = r & 3, c0 = 4 * (r >> 2);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)  // features 16 j + 4g .. +3 of cell c0 + i: chunk 2j + g / 2, half g & 1
+                    *reinterpret_cast<uint2 *>(zw + win_zoff(c0 + i, 2 * j + (g >> 1)) + 8 * (g & 1)) =
+                        uint2{pack_bf16x2(zc[0][i], zc[1][i]), pack_bf16x2(zc[2][i], zc[3][i])};
             }
             // 3. fc1
             __builtin_amdgcn_wave_barrier();
