@@ -426,6 +426,13 @@ int32_t nca_bptt_forward_pieces(const nca_cell_desc *cell, int64_t rows, int32_t
  * together). (0, 0, 0) in use. No counterpart in the reference. */
 int nca_set_piece_debug(int32_t spin_limit, int32_t force_timeout, int32_t plan_cus);
 
+/* Test setting of nca_bptt_backward's path: 0 automatic (bf16 cells of 32 channels, 128 features
+ * and 256 hidden units run the chunk's whole backward as one launch, on pieces of boards where
+ * the device holds them, else on whole boards; other cells, three launches per step), 1 three
+ * launches per step, 2 the one-launch backward on whole boards. The gradients of the paths agree
+ * to fp32 rounding. No counterpart in the reference. */
+int nca_set_bptt_backward_path(int32_t path);
+
 #ifdef __cplusplus
 }
 #endif

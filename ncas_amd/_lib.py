@@ -49,6 +49,7 @@ EXPORTS = (
     "nca_adamw_ema",
     "nca_bptt_forward_pieces",
     "nca_set_piece_debug",
+    "nca_set_bptt_backward_path",
     "nca_damage_clamp",
     "nca_maze_boards",
     "nca_sudoku_boards",
@@ -183,6 +184,7 @@ def load():
     L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]
     L.nca_bptt_forward_pieces.argtypes = [ctypes.POINTER(CellDesc), i64, i32, i32, i32]
     L.nca_set_piece_debug.argtypes = [i32, i32, i32]
+    L.nca_set_bptt_backward_path.argtypes = [i32]
     L.nca_last_error.restype = ctypes.c_char_p
     L.nca_version.restype = ctypes.c_int
     L.nca_set_kernel_path.argtypes = [ctypes.c_int]

@@ -677,6 +677,12 @@ int nca_set_piece_debug(int32_t spin_limit, int32_t force_timeout, int32_t plan_
     return NCA_OK;
 }
 
+int nca_set_bptt_backward_path(int32_t path) {
+    if (path < 0 || path > 2) return fail(NCA_ERR_INVALID, "path=%d (0 automatic, 1 per-step launches, 2 whole boards)", path);
+    nca::g_piece_debug.back_path = path;
+    return NCA_OK;
+}
+
 int32_t nca_bptt_forward_pieces(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width,
                                 int32_t cus) {
     g_err[0] = 0;

@@ -257,13 +257,13 @@ __device__ __forceinline__ void load_out(const Dims &d, const float *x1c, float 
 // v >= n_out, and everywhere on a step without a loss term) and the cell's loss term (reference
 // src/nca/train.py:183-207). n_out, c_out <= NO.
 template <int NO>
-__device__ __forceinline__ float head_grad(const FrontArgs &a, const float *hw, const float *hb, const float xo[NO], int tgt,
-                                           float mk, float gl[NO]) {
-    const Dims &d = a.d;
+__device__ __forceinline__ float head_grad_core(const Dims &d, float wscale, bool masked, const float *denom,
+                                                const float *hw, const float *hb, const float xo[NO], int tgt, float mk,
+                                                float gl[NO]) {
 #pragma unroll
     for (int v = 0; v < NO; ++v) gl[v] = 0.0f;
-    if (a.wscale == 0.0f) return 0.0f;
-    const float scale = a.mask ? a.wscale * mk / *a.denom : a.wscale;
+    if (wscale == 0.0f) return 0.0f;
+    const float scale = masked ? wscale * mk / *denom : wscale;
     float l[NO];
     float mx = -INFINITY;
 #pragma unroll
@@ -278,17 +278,23 @@ __device__ __forceinline__ float head_grad(const FrontArgs &a, const float *hw, 
             mx = fmaxf(mx, acc);
         }
     }
-    float s = 0.0f, lt = mx;
+    float s = 0.0f, lt = mx, e[NO];
 #pragma unroll
     for (int v = 0; v < NO; ++v)
         if (v < d.n_out) {
-            s += expf(l[v] - mx);
+            e[v] = expf(l[v] - mx);
+            s += e[v];
             if (v == tgt) lt = l[v];
         }
 #pragma unroll
     for (int v = 0; v < NO; ++v)
-        if (v < d.n_out) gl[v] = (expf(l[v] - mx) / s - (v == tgt ? 1.0f : 0.0f)) * scale;
+        if (v < d.n_out) gl[v] = (e[v] / s - (v == tgt ? 1.0f : 0.0f)) * scale;
     return (mx + logf(s) - lt) * scale;
+}
+template <int NO>
+__device__ __forceinline__ float head_grad(const FrontArgs &a, const float *hw, const float *hb, const float xo[NO], int tgt,
+                                           float mk, float gl[NO]) {
+    return head_grad_core<NO>(a.d, a.wscale, a.mask != nullptr, a.denom, hw, hb, xo, tgt, mk, gl);
 }
 
 constexpr int kFrontCh = 8;  // channels per front block (the channel count is a multiple of 8)
@@ -1112,6 +1118,12 @@ unsigned grid_for(int64_t n) {
 
 }  // namespace
 
+#include "nca_bptt_fused.h"
+
+namespace nca {
+int device_cus();
+}
+
 extern "C" {
 
 size_t nca_bptt_workspace_bytes(const nca_cell_desc *cell, int64_t rows, int32_t height, int32_t width,
@@ -1174,6 +1186,47 @@ int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t r
 }  // extern "C"
 
 namespace {
+
+// The one-launch backward of a chunk (nca_bptt_fused.h) where it takes the call: pieces > 1 per
+// board when the boards' pieces fit the device at once (rows * pieces workgroups on as many CUs,
+// at most kSplit slots), each piece's plan fits the LDS and the exchange slots fit the
+// workspace's z region; else whole boards (pieces = 1, at most kSplit boards); pieces = 0: the
+// three launches per step. The whole-board plan must fit either way (it is the pieces' repair).
+struct FusedChoice {
+    int pieces = 0, Hp = 0;
+    FusedPlan plan, whole;
+    size_t xch_bytes = 0;  // pieces: the status block and the exchange slots
+};
+
+FusedChoice fused_choice(const Dims &d, int n, bool fire_f32, const WsLayout &L) {
+    FusedChoice c;
+    constexpr unsigned kLds = 160u * 1024u;
+    const int path = nca::g_piece_debug.back_path;
+    if (path == 1 || !fused_mlp(d) || fire_f32 || n < 1 || n > kFusedMaxChunk || d.M <= 0) return c;
+    if (d.n_out > 4 || d.c_out > 4 || d.rows > kSplit) return c;
+    c.whole = fused_plan(false, d.H, d.W);
+    if (c.whole.total > kLds) return c;
+    if (path != 2 && d.W <= 32) {
+        int cus = nca::g_piece_debug.plan_cus > 0 ? nca::g_piece_debug.plan_cus : nca::device_cus();
+        if (cus > kSplit) cus = kSplit;
+        for (int P = 4; P >= 2; --P) {
+            const int Hp = (d.H + P - 1) / P;
+            if ((P - 1) * Hp >= d.H || d.rows * P > cus) continue;
+            const FusedPlan pl = fused_plan(true, Hp, d.W);
+            const size_t xb = nca::kXchStatusBytes + (size_t)d.rows * P * 4 * 64 * d.W * sizeof(uint64_t);
+            if (pl.total > kLds || xb > (size_t)(L.Gz - L.Z) * sizeof(float)) continue;
+            c.pieces = P;
+            c.Hp = Hp;
+            c.plan = pl;
+            c.xch_bytes = xb;
+            return c;
+        }
+    }
+    c.pieces = 1;
+    c.Hp = d.H;
+    c.plan = c.whole;
+    return c;
+}
 
 // The backward of n_chunk steps (nca_bptt_backward). Step t reads its input state at
 // states + t * stride and its output at states + (t + 1) * stride; stride 0 (the single-step VJP,
@@ -1238,8 +1291,98 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
                            reinterpret_cast<unsigned char *>(ws + L.img));
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
     if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;
+    const FusedChoice fc = fused_choice(d, n_chunk, fire_f32 != nullptr, L);
+    if (fc.pieces > 0) {
+        FusedArgs A;
+        memset(&A, 0, sizeof(A));
+        A.fa.d = d;
+        A.fa.given = given;
+        A.fa.targets = loss->targets;
+        A.fa.mask = loss->loss_mask;
+        A.fa.denom = denom;
+        A.fa.head_w = headw;
+        A.fa.head_b = headb;
+        A.fa.fire_u8 = fire->fire_in;
+        A.fa.key_ptr = fire->step_seeds;
+        A.fa.key = fire->seed;
+        A.fa.row0 = fire->row0;
+        A.fa.step = (uint32_t)fire->step0;
+        A.fa.p = fire->p_fire;
+        A.states = states;
+        A.stride = stride;
+        A.n = n_chunk;
+        for (int t = 0; t < n_chunk; ++t) {
+            const float wt = loss->step_weights[t] / wden;
+            A.wscale[t] = loss->loss_mask ? wt : wt / (float)d.M;
+        }
+        A.grad_final = grad_final;
+        A.grad_x0 = grad_x0;
+        A.img = reinterpret_cast<const unsigned char *>(ws + L.img);
+        A.b1 = b1;
+        A.kern = kern;
+        A.padv = padv;
+        A.part = part;
+        A.lossacc = lossacc;
+        A.P = P.P;
+        A.offK = P.K;
+        A.offW1 = P.W1;
+        A.offB1 = P.B1;
+        A.offW2 = P.W2;
+        A.offB2 = P.B2;
+        A.offHW = P.HW;
+        A.offHB = P.HB;
+        A.gz_g = reinterpret_cast<uint16_t *>(ws + L.Gz);
+        A.gx_g = ws + L.Gx0;
+        A.spin_limit = nca::g_piece_debug.spin_limit > 0 ? nca::g_piece_debug.spin_limit : nca::kHaloSpin;
+        A.tag_skew = nca::g_piece_debug.force_timeout ? (1 << 30) : 0;
+        auto set_plan = [&](FusedArgs &a, const FusedPlan &pl) {
+            a.l_GZ = pl.GZ;
+            a.l_GX = pl.GX;
+            a.l_XS = pl.XS;
+            a.l_MLP = pl.MLP;
+            a.l_FI = pl.FI;
+            a.l_RED = pl.RED;
+            a.l_ACC = pl.ACC;
+            a.l_HWL = pl.HWL;
+        };
+        auto kp = bptt_back_fused<true>;
+        auto kw = bptt_back_fused<false>;
+        if ((rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kw),
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)fc.whole.total),
+                                  "fused backward attribute")))
+            return rc;
+        FusedArgs Aw = A;  // whole boards
+        Aw.pieces = 1;
+        Aw.Hp = d.H;
+        set_plan(Aw, fc.whole);
+        if (fc.pieces > 1) {
+            // the status word (bytes 8 .. 11 of the workspace; bytes 0 .. 3 hold the forward's) and
+            // the exchange slots after the status block, cleared here
+            uint64_t *wsw = static_cast<uint64_t *>(workspace);
+            A.status = reinterpret_cast<uint32_t *>(workspace) + 2;
+            A.xch = wsw + nca::kXchStatusBytes / sizeof(uint64_t);
+            A.pieces = fc.pieces;
+            A.Hp = fc.Hp;
+            A.gz_rows = fc.Hp + 2;
+            set_plan(A, fc.plan);
+            if ((rc = nca::hip_status(nca::clear_words(wsw + 1, (int64_t)(fc.xch_bytes / sizeof(uint64_t)) - 1, st),
+                                      "fused backward exchange clear")))
+                return rc;
+            if ((rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kp),
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)fc.plan.total),
+                                      "fused backward attribute")))
+                return rc;
+            hipLaunchKernelGGL(kp, dim3((unsigned)(d.rows * fc.pieces)), dim3(kFusedThreads), fc.plan.total, st, A);
+            if ((rc = nca::hip_status(hipGetLastError(), "fused backward (pieces)"))) return rc;
+            // the repair: whole boards, only if a piece's wait ran out
+            Aw.run_if = A.status;
+            Aw.zero_slots = (int)(d.rows * fc.pieces);
+        }
+        hipLaunchKernelGGL(kw, dim3((unsigned)d.rows), dim3(kFusedThreads), fc.whole.total, st, Aw);
+        if ((rc = nca::hip_status(hipGetLastError(), "fused backward (whole boards)"))) return rc;
+    }
     const float *gin = grad_final;
-    for (int t = n_chunk - 1; t >= 0 && d.M > 0; --t) {
+    for (int t = n_chunk - 1; t >= 0 && d.M > 0 && fc.pieces == 0; --t) {
         const float *xt = states + t * stride, *x1 = states + (t + 1) * stride;
         float *gx = (t == 0 && grad_x0) ? grad_x0 : Gx[t & 1];
         // front: loss gradient, clamp and fire
@@ -1365,7 +1508,7 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
     }
     // the slots summed in slot order
     hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
-    if (planes_ok)
+    if (planes_ok && fc.pieces == 0)
         hipLaunchKernelGGL(reduce_dk, dim3(36), dim3(kThreads), 0, st, ws + L.dk, strips_ok ? strip_blocks : d.rows * d.C,
                            acc + P.K);
     if (grad_x0) {

@@ -83,9 +83,8 @@ struct St32 {
     static constexpr int NSLOT = 4;  // fire ring steps
 };
 
-// re-reads of an exchange word before a piece gives up on its neighbour (about a second; after
-// that its halo rows are NaN and it waits no more)
-constexpr int kHaloSpin = 1 << 20;
+// (kHaloSpin, nca_stream.h: re-reads of an exchange word before a piece gives up on its
+// neighbour; after that its halo rows are NaN and it waits no more)
 
 struct St32Plan {
     unsigned M, Z, D, cinfo, ring, given, head, evp, flags, gidx, total;

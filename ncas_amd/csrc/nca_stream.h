@@ -30,6 +30,9 @@ int stream32_pieces(int64_t rows, int H, int W, int c_out, int n_out, unsigned l
 size_t stream32_xch_bytes(int64_t rows, int P, int W);
 constexpr size_t kXchStatusBytes = 256;
 
+// re-reads of an exchange word before a piece gives up on its neighbour (about a second)
+constexpr int kHaloSpin = 1 << 20;
+
 // Zero n 8-byte words on the stream (a kernel, so the call can sit in a captured graph).
 hipError_t clear_words(uint64_t *x, int64_t n, hipStream_t st);
 
@@ -37,9 +40,10 @@ hipError_t clear_words(uint64_t *x, int64_t n, hipStream_t st);
 // spin_limit > 0 replaces the wait's limit of re-reads; force_timeout makes every wait look for a
 // tag that never comes (so it runs out after spin_limit re-reads); plan_cus > 0 plans pieces as
 // for a device of that many CUs (a launch too large to be resident is then refused and the
-// boards run whole). All zero in use.
+// boards run whole). All zero in use. back_path (nca_set_bptt_backward_path): 0 automatic, 1 the
+// backward as three launches per step, 2 the one-launch backward on whole boards.
 struct PieceDebug {
-    int spin_limit = 0, force_timeout = 0, plan_cus = 0;
+    int spin_limit = 0, force_timeout = 0, plan_cus = 0, back_path = 0;
 };
 extern PieceDebug g_piece_debug;
 

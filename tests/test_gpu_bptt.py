@@ -392,20 +392,30 @@ def test_bptt_pieces_status_word():
     assert torch.equal(good, whole)
     targets = torch.zeros((64, 30, 30), dtype=torch.int64, device=DEV)
     ref = bptt_chunk(md, x, g8.bool(), cl, targets, [1.0] * n, seed=9, p_fire=0.7,
-                     precision="bf16")
+                     precision="bf16", want_grad_x0=True)
     try:
+        # the one-launch backward on whole boards: what the backward's repair launch computes
+        assert L.nca_set_bptt_backward_path(2) == 0
+        ref_whole = bptt_chunk(md, x, g8.bool(), cl, targets, [1.0] * n, seed=9, p_fire=0.7,
+                               precision="bf16", want_grad_x0=True)
+        assert L.nca_set_bptt_backward_path(0) == 0
         assert L.nca_set_piece_debug(4, 1, 0) == 0
         forced = _forward(L, pk, x, g8, cl, fd, n, ws)
         torch.cuda.synchronize()
         assert int(ws[:1].view(torch.int32).item()) == 1
         assert torch.equal(forced, whole)
+        # the forward's and the backward's pieces give up; both repair launches run
         res = bptt_chunk(md, x, g8.bool(), cl, targets, [1.0] * n, seed=9, p_fire=0.7,
-                         precision="bf16")
+                         precision="bf16", want_grad_x0=True)
         assert bool(res.halo_failed.all())
-        assert torch.equal(res.x, ref.x) and torch.equal(res.loss, ref.loss)
-        assert all(torch.equal(res.grads[k], ref.grads[k]) for k in ref.grads)
+        assert torch.equal(res.x, ref.x) and torch.equal(res.grad_x0, ref.grad_x0)
+        assert torch.equal(res.loss, ref_whole.loss) and torch.equal(res.grad_x0, ref_whole.grad_x0)
+        assert all(torch.equal(res.grads[k], ref_whole.grads[k]) for k in ref.grads)
+        for k in NAMES:
+            assert _rel(res.grads[k], ref.grads[k]) <= 1e-5, k
     finally:
         L.nca_set_piece_debug(0, 0, 0)
+        L.nca_set_bptt_backward_path(0)
     again = _forward(L, pk, x, g8, cl, fd, n, ws)
     torch.cuda.synchronize()
     assert int(ws[:1].view(torch.int32).item()) == 0 and torch.equal(again, whole)
@@ -433,3 +443,63 @@ def test_bptt_pieces_not_resident_together():
         L.nca_set_piece_debug(0, 0, 0)
     _say("status word", int(ws[:1].view(torch.int32).item()))
     assert torch.equal(got, whole)
+
+
+def _with_padding(m, padding):
+    from dataclasses import replace
+
+    from ncas_amd.model import NCA
+
+    m2 = NCA(replace(m.cfg, padding=padding))
+    m2.load_state_dict(m.state_dict())
+    return m2
+
+
+@pytest.mark.parametrize("padding,size,rows,fire", [
+    ("wall", 30, 8, "seed"),     # four pieces of 8, 8, 8, 6 rows
+    ("wrap", 30, 8, "masks"),    # the top and bottom pieces exchange across the wrap
+    ("wall", 13, 6, "masks"),    # pieces of 4, 4, 4 and 1 rows
+    ("wrap", 13, 100, "seed"),   # two pieces of 7 and 6 rows (200 workgroups)
+    ("wrap", 30, 100, "masks"),  # too many boards for pieces that fit the LDS: whole boards
+    ("wall", 30, 300, "seed"),   # more boards than slots: three launches per step
+])
+def test_bptt_one_launch_backward_equals_per_step_launches(padding, size, rows, fire):
+    """The chunk's backward as one launch (bf16 C=32 cells; on pieces of boards exchanging g_z
+    rows, or on whole boards) against the same backward as three launches per step: each step's
+    per-cell arithmetic is the same in both, so d L / d x0 agrees bit for bit; the parameter
+    gradients and the loss are the same sums over cells in another fixed order (fp32 rounding).
+    With a loss mask, sparse step weights and grad_final."""
+    _say("bptt one-launch backward", padding, size, rows, fire)
+    L = _lib.load()
+    m = perturbed_model("maze_hard_c32", 3, *DYN["maze_hard_c32"])
+    if padding != m.cfg.padding:
+        m = _with_padding(m, padding)
+    md = copy.deepcopy(m).to(DEV)
+    b = maze_boards(rows, size, 0, extra_openings=0.1)
+    x, g4, cl = initial_state(m, b, k=1, sigma=0.15, seed=1)
+    targets = m.output_index(torch.from_numpy(b.targets))
+    n, w = 6, [1.0, 0.0, 0.5, 1.0, 0.0, 1.0]
+    g = torch.Generator().manual_seed(5)
+    kw = {"grad_final": (torch.randn(x.shape, generator=g) * 1e-3).to(DEV),
+          "loss_mask": (torch.rand((rows, size, size), generator=g) < 0.8).float().to(DEV)}
+    if fire == "masks":
+        kw["masks"] = (torch.rand((n, rows, 1, size, size), generator=g) < 0.7).float().to(DEV)
+    else:
+        kw["seed"] = 11
+    out = {}
+    try:
+        for path in (1, 0, 2):
+            assert L.nca_set_bptt_backward_path(path) == 0
+            out[path] = _gpu_chunk(md, x, g4, cl, targets, w, "bf16", **kw)
+    finally:
+        L.nca_set_bptt_backward_path(0)
+    per = out[1]
+    for path in (0, 2):
+        res = out[path]
+        assert torch.equal(res.x, per.x)
+        assert torch.equal(res.grad_x0, per.grad_x0), path
+        worst = max(_rel(res.grads[k], per.grads[k]) for k in NAMES)
+        _say("path", path, "worst rel", worst, "loss", float(res.loss), float(per.loss))
+        for k in NAMES:
+            assert _rel(res.grads[k], per.grads[k]) <= 1e-5, (path, k)
+        assert abs(float(res.loss) - float(per.loss)) <= 1e-6 * abs(float(per.loss))
