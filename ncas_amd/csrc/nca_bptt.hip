@@ -87,7 +87,7 @@ bool fused_mlp(const Dims &d) { return d.bf16 && d.C == 32 && d.F == 128 && d.HD
 // Boards small enough to stage (row, channel) planes in LDS.
 bool planes_fit(const Dims &d) { return d.HW <= kPlaneMax && d.rows * d.C <= 0x7fffffff; }
 
-// Workspace (floats, 64-float aligned pieces). part holds kSplit slots of P partial sums
+// Workspace (floats, 64-float aligned pieces, after the status block). part holds kSplit slots of P partial sums
 // each (slot s: the cells of range s), added to by every step of the chunk and reduced once at
 // the end; lossacc holds the loss's kSplit slots. The GEMM path's h and g_a (Hb, Ga) are not
 // needed by the fused kernel.
@@ -101,7 +101,9 @@ WsLayout ws_layout(const Dims &d, int n) {
     const bool fused = fused_mlp(d);
     auto al = [](int64_t v) { return (v + 63) & ~(int64_t)63; };
     WsLayout L;
-    int64_t o = 0;
+    // the first kXchStatusBytes hold the status words of the forward's and the one-launch
+    // backward's pieces; nothing else writes them
+    int64_t o = (int64_t)(nca::kXchStatusBytes / sizeof(float));
     L.Z = o;
     o = al(o + (int64_t)d.F * d.M);
     L.Hb = o;

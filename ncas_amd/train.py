@@ -85,6 +85,8 @@ class ChunkResult:
     halo_failed: torch.Tensor | None = None  # device bool: a wait of the forward's board
     #                pieces ran out and the forward was recomputed on whole boards (the states
     #                are right either way)
+    back_repaired: torch.Tensor | None = None  # device bool: the same for the one-launch
+    #                backward's pieces (the gradients were recomputed on whole boards)
 
 
 def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step_seeds=None,
@@ -154,10 +156,12 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                                    ctypes.byref(lossd), _lib.ptr(gf), ctypes.byref(gs),
                                    _lib.ptr(gx0), loss.data_ptr(), ws.data_ptr(), ws_bytes,
                                    stream), "nca_bptt_backward")
+    # the one-launch backward's status word (bytes 8 .. 11; zero when it did not run in pieces)
+    back_repaired = ws[2:3].view(torch.int32) != 0
     # no wait: the host arrays were read during the calls, and the device buffers freed here are
     # reused only by later work on the same stream
     return ChunkResult(states[n].clone(), loss, grads, gx0, states.numel() * 4, ws_bytes,
-                       halo_failed)
+                       halo_failed, back_repaired)
 
 
 # ------------------------------------------------------------------------------ losses

@@ -378,7 +378,9 @@ def test_bptt_pieces_status_word():
     word at 0; with the pieces' waits forced to run out (a host setting: every wait looks for a
     tag that never comes and gives up after 4 re-reads) every kernel still ends, the word is 1,
     and the repair launch has recomputed the boards whole: the states still equal the whole-board
-    forward's bit for bit. bptt_chunk reports the word as ChunkResult.halo_failed."""
+    forward's bit for bit. bptt_chunk reports the word as ChunkResult.halo_failed. The one-launch
+    backward's pieces give up the same way and its repair launch recomputes the gradients on
+    whole boards (ChunkResult.back_repaired): equal to the whole-board path bit for bit."""
     _say("bptt pieces status")
     L = _lib.load()
     md, pk, x, g8, cl, fd, n = _pieces_case(64)
@@ -407,7 +409,7 @@ def test_bptt_pieces_status_word():
         # the forward's and the backward's pieces give up; both repair launches run
         res = bptt_chunk(md, x, g8.bool(), cl, targets, [1.0] * n, seed=9, p_fire=0.7,
                          precision="bf16", want_grad_x0=True)
-        assert bool(res.halo_failed.all())
+        assert bool(res.halo_failed.all()) and bool(res.back_repaired.all())
         assert torch.equal(res.x, ref.x) and torch.equal(res.grad_x0, ref.grad_x0)
         assert torch.equal(res.loss, ref_whole.loss) and torch.equal(res.grad_x0, ref_whole.grad_x0)
         assert all(torch.equal(res.grads[k], ref_whole.grads[k]) for k in ref.grads)
@@ -419,7 +421,7 @@ def test_bptt_pieces_status_word():
     again = _forward(L, pk, x, g8, cl, fd, n, ws)
     torch.cuda.synchronize()
     assert int(ws[:1].view(torch.int32).item()) == 0 and torch.equal(again, whole)
-    assert not bool(ref.halo_failed.any())
+    assert not bool(ref.halo_failed.any()) and not bool(ref.back_repaired.any())
 
 
 def test_bptt_pieces_not_resident_together():
