@@ -41,6 +41,7 @@ struct Step16Params {
 
 typedef float s16_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // FIRST equals sp.first: the clamp values are loaded (and the loop carries them) on a call's
 // first step only
@@ -105,6 +106,10 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
     if (t_end > sp.n_tiles) t_end = sp.n_tiles;
     unsigned char *zw = zL[w];
     unsigned char *hw = zL[w] + 16 * 144;
+    // the cell-major output state (below 2^31 bytes, checked by the host); the third dword is
+    // gfx9's format word
+    const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        a.x_out, (short)0, OUT_NCHW ? 0 : (int)(a.rows * HWn * C * (int64_t)sizeof(float)), 0x00020000);
 
     // everything tile t loads: taps (float4 per tap), given flag, injected mask, clamp values
     struct TileIn {
@@ -156,10 +161,15 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
             }
         }
         in.gv = a.given[row * HWn + qc];
-        in.fin = 0.0f;
-        in.fu8 = 0;
-        if (a.fire_f32) in.fin = a.fire_f32[row * HWn + qc];
-        if (a.fire_u8) in.fu8 = a.fire_u8[((int64_t)sp.step * a.rows + row) * HWn + qc];
+        // the injected masks are loaded without a branch (a mask that is absent loads some other
+        // element of the row instead, unused): a memory access under a branch leaves the compiler
+        // unsure how many are in flight, and it then waits for all of them, the tile's store
+        // included, before the next tile
+        const float *fsrc = a.fire_f32 ? a.fire_f32 + (row * HWn + qc) : a.x_in + (row * HWn + qc);
+        const unsigned char *usrc =
+            a.fire_u8 ? a.fire_u8 + (((int64_t)sp.step * a.rows + row) * HWn + qc) : a.given + (row * HWn + qc);
+        in.fin = *fsrc;
+        in.fu8 = *usrc;
         if (FIRST) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
@@ -316,23 +326,23 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
             const float uv = __fadd_rn(xo[v], __fmul_rn(f, round_bf16(dx[v])));
             u[v] = (gv && insl[v]) ? xo[v] : uv;
         }
-        if (valid) {
-            if (OUT_NCHW) {
+        if (OUT_NCHW) {
+            if (valid) {
                 float *xr = a.x_out + (row * C + 4 * g) * (int64_t)HWn + q;
 #pragma unroll
                 for (int v = 0; v < 4; ++v) xr[(int64_t)v * HWn] = u[v];
-            } else {
-                *reinterpret_cast<float4 *>(a.x_out + (row * HWn + q) * C + 4 * g) = make_float4(u[0], u[1], u[2], u[3]);
             }
+        } else {
+            // cells past the row's end store at an offset beyond the buffer, which the hardware
+            // drops, so the store needs no branch
+            const uint32_t off = valid ? ((uint32_t)(row * HWn + q) * (uint32_t)C + 4u * (uint32_t)g) * 4u : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(u[0]), __float_as_uint(u[1]),
+                                                         __float_as_uint(u[2]), __float_as_uint(u[3])},
+                                                   out_rsrc, off, 0, 0);
         }
-        // fired cells, counted once per cell (quad 0) and added per row
-        if (a.fired_out) {
-            if (row != cur_row) {
-                if (cur_row >= 0) flush_fired();
-                cur_row = row;
-            }
-            fired_run += (valid && g == 0 && f != 0.0f) ? 1 : 0;
-        }
+        // fired cells, counted once per cell (quad 0) and added per row (the row's flush is at
+        // the top of the tile, before its loads)
+        if (a.fired_out) fired_run += (valid && g == 0 && f != 0.0f) ? 1 : 0;
     };
 
     // the wave's tiles t = t_begin + w + 8k, at (row, tile of the row) tracked without division;
@@ -366,6 +376,10 @@ __global__ void __launch_bounds__(512, 1) step_stream16(Step16Params sp) {
         asm volatile("" : "+v"(cu.fin), "+v"(cu.gv), "+v"(cu.fu8));
         if (FIRST) asm volatile("" : "+v"(cu.cv[0]), "+v"(cu.cv[1]), "+v"(cu.cv[2]), "+v"(cu.cv[3]));
         asm volatile("" ::: "memory");
+        if (a.fired_out && row != cur_row) {
+            if (cur_row >= 0) flush_fired();
+            cur_row = row;
+        }
         int64_t rn = row;
         int tn = tir;
         advance(rn, tn);

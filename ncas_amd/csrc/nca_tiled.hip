@@ -150,9 +150,10 @@ hipError_t window16_steps(const RolloutParams &p, int step, int T, int first, in
 hipError_t tiled_step(int C, int HD, bool bf16, const RolloutParams &p, int step, int first, int in_nchw,
                       int out_nchw, hipStream_t st, bool windows, bool *ok) {
     *ok = false;
-    // the wave-per-tile kernel addresses the cell-major state with 32-bit byte offsets: larger
-    // batches run on the halo-window kernel
-    const bool offsets32 = p.rows * (int64_t)p.H * p.W * 16 * (int64_t)sizeof(float) < ((int64_t)1 << 32);
+    // the wave-per-tile kernel addresses the cell-major state with 31-bit byte offsets (its
+    // stores put cells past a row's end at offset 2^31, beyond the buffer): larger batches run on
+    // the halo-window kernel
+    const bool offsets32 = p.rows * (int64_t)p.H * p.W * 16 * (int64_t)sizeof(float) < ((int64_t)1 << 31);
     if (C == 16 && HD == 128 && bf16 && !windows && !p.noise && !p.adaptive && offsets32) {
         *ok = true;
         if (in_nchw)
