@@ -1346,6 +1346,7 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
             a.l_RED = pl.RED;
             a.l_ACC = pl.ACC;
             a.l_HWL = pl.HWL;
+            a.l_FB = pl.FB;
         };
         auto kp = bptt_back_fused<true>;
         auto kw = bptt_back_fused<false>;

@@ -64,16 +64,16 @@ struct FusedArgs {
     int spin_limit, tag_skew;
     const uint32_t *run_if;  // whole boards: run only if *run_if != 0 (the repair launch)
     int zero_slots;          // the repair: slots [gridDim.x, zero_slots) are zeroed
-    unsigned l_GZ, l_GX, l_XS, l_MLP, l_FI, l_RED, l_ACC, l_HWL;
+    unsigned l_GZ, l_GX, l_XS, l_MLP, l_FI, l_RED, l_ACC, l_HWL, l_FB;
     int gz_rows;  // rows of a g_z plane in LDS (Hp + 2)
 };
 
 // LDS plan: GZ g_z [k 4][row Hw + 2][col W][c 32] bf16 and GX [cell][c 32] fp32 (pieces only),
-// XS x_t [row Hw + 2][col W + 2][c 32] bf16, the MLP buffers of mlp_back32, the front's per-cell
-// head terms FI [2 tiles][32][24], the reduction scratch, the chunk's small sums (dk 36, db2 32, head and
-// loss 21) and the head's weights.
+// XS x_t [row Hw + 2][col W + 2][c 32] bf16, the MLP buffers of mlp_back32, the per-cell
+// head terms FI [3 tiles][32][12], the reduction scratch, the chunk's small sums (dk 36, db2 32, head and
+// loss 21), the head's weights and FB, the step's fire bits of the workgroup's cells (a byte each).
 struct FusedPlan {
-    unsigned GZ, GX, XS, MLP, FI, RED, ACC, HWL, total;
+    unsigned GZ, GX, XS, MLP, FI, RED, ACC, HWL, FB, total;
 };
 
 inline FusedPlan fused_plan(bool pieces, int Hw, int W) {
@@ -88,13 +88,15 @@ inline FusedPlan fused_plan(bool pieces, int Hw, int W) {
     p.MLP = o;
     o += nca::Mb32::TOTAL;
     p.FI = o;
-    o += 2u * 32u * 24u * 4u;
+    o += 3u * 32u * 12u * 4u;
     p.RED = o;
     o += 4u * 40u * 4u;
     p.ACC = o;
     o += 96u * 4u;
     p.HWL = o;
     o += 20u * 4u;
+    p.FB = o;
+    o += 2u * (((unsigned)(Hw * W) + 15u) & ~15u);
     p.total = o;
     return p;
 }
@@ -133,7 +135,9 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
     float *fiL = reinterpret_cast<float *>(smem + A.l_FI);
     float *redL = reinterpret_cast<float *>(smem + A.l_RED);
     float *dkacc = reinterpret_cast<float *>(smem + A.l_ACC), *hacc = dkacc + 68;
+    // hacc: the loss (0), the head weights' gradient (1 + 4 v + c), its bias's (17 + v)
     float *hwL = reinterpret_cast<float *>(smem + A.l_HWL);
+    unsigned char *fbL = smem + A.l_FB;  // the step's fire bits of the workgroup's cells
     const int64_t xb = (int64_t)board * 32 * HW;  // channel 0 of the board in a state
     const int64_t mb = (int64_t)board * HW;       // the board's first cell
 
@@ -194,6 +198,22 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
     mb_f32x4 dkw = {0.f, 0.f, 0.f, 0.f};         // this wave's kernel-weight sums (lanes 0 .. 8)
     // wave 0: db2 of channels 16 ct + 4 g + i in column r of the product with a matrix of ones
     mb_f32x4 db2m[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // the z waves' stencil B operands: column k = lane % 4 is kernel k, taps 0-3 / 4-7; tap 8 in
+    // the k slot of the channel's place in its quad (the forward's operands)
+    nca::s16x4 kzb0, kzb1, kzb2[4];
+    {
+        const int k = lane & 3;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kzb0[e] = nca::bf16_bits(A.kern[k * 9 + e]);
+            kzb1[e] = nca::bf16_bits(A.kern[k * 9 + 4 + e]);
+        }
+        const short k8 = nca::bf16_bits(A.kern[k * 9 + 8]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kzb2[c][e] = e == c ? k8 : (short)0;
+    }
     const nca::bf16x8 ones8 = __builtin_bit_cast(nca::bf16x8, make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
 
     // MLP operand offsets (mlp_back32's)
@@ -314,13 +334,81 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
     };
     __syncthreads();
 
+    // The head terms of the chunk's tile G (tiles numbered across the chunk's steps, tile tt of
+    // the si-th step processed is G = si ntile + tt) go to FI buffer G % 3, a row of 12 floats per
+    // cell: gl = d loss / d logits (0-3), the output channels xo (4-7) and the loss term (8), zero
+    // for cells past the workgroup's, and 1 (9). The first z wave computes them two tiles at a time ahead
+    // of the front (lanes 0-31: cells of tile G + 1, lanes 32-63: of tile G + 2, in the tiles
+    // G = 0, 2, 4, ...); the front reads gl, the second z wave sums the loss and the head's
+    // gradient products gl[v] xo[c]. The inputs are loaded first (head_load, raw: nothing selects
+    // on a load when it is issued, so the compiler waits for them only at their use in
+    // head_terms; an absent tensor loads another element of the step's state instead, which the
+    // use ignores).
+    const int ntile = (nw + 31) / 32;
+    struct HeadIn {
+        float xo[4], mk;
+        int tgt;
+    };
+    auto head_load = [&](int ts, int tt) {
+        HeadIn hi;
+        const int j = (tid - FT) & 31, mt = 32 * tt + j;
+        const int q = r0 * W + (mt < nw ? mt : 0);
+        const int64_t m = mb + q;
+        const float *xs1 = A.states + (int64_t)(ts + 1) * A.stride + xb;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) hi.xo[c] = xs1[(int64_t)(d.out_off + (c < d.c_out ? c : 0)) * HW + q];
+        hi.tgt = *(A.fa.targets ? A.fa.targets + m : reinterpret_cast<const int32_t *>(xs1 + q));
+        hi.mk = *(A.fa.mask ? A.fa.mask + m : xs1 + q);
+        return hi;
+    };
+    auto head_terms = [&](const HeadIn &hi, int ts, int tt, int fb) {
+        const int j = (tid - FT) & 31;
+        const bool ok = 32 * tt + j < nw;
+        float xo[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xo[c] = c < d.c_out ? hi.xo[c] : 0.0f;
+        const int tgt = A.fa.targets ? hi.tgt : 0;  // no targets: a step without a loss term
+        const float mk = A.fa.mask ? hi.mk : 0.0f;
+        float gl[4];
+        const float lc =
+            head_grad_core<4>(d, A.wscale[ts], A.fa.mask != nullptr, A.fa.denom, hwL, hwL + 16, xo, tgt, mk, gl);
+        float *fi = fiL + fb * 384 + j * 12;
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        *reinterpret_cast<float4 *>(fi) = ok ? make_float4(gl[0], gl[1], gl[2], gl[3]) : z4;
+        *reinterpret_cast<float4 *>(fi + 4) = ok ? make_float4(xo[0], xo[1], xo[2], xo[3]) : z4;
+        fi[8] = ok ? lc : 0.0f;
+        fi[9] = 1.0f;  // the factor of the sums that are not products
+    };
+    // the Philox fire bits of step ts for the workgroup's cells into FB buffer ts & 1, one
+    // evaluation per 4 cells of the board (the uniforms of cells 4 g4 .. 4 g4 + 3); threads
+    // [t0, t0 + nt)
+    const unsigned fbs = ((unsigned)nw + 15u) & ~15u;
+    auto fire_bits = [&](int ts, int t0, int nt) {
+        const int qa = r0 * W, qe = qa + nw;
+        const uint64_t key = A.fa.key_ptr ? A.fa.key_ptr[ts] : A.fa.key;
+        unsigned char *fo = fbL + (unsigned)(ts & 1) * fbs;
+        for (int g4 = (qa >> 2) + tid - t0; g4 < (qe + 3) >> 2; g4 += nt) {
+            float u[4];
+            nca::cell_uniforms4(key, (uint32_t)(A.fa.row0 + board), A.fa.step + (uint32_t)ts, (uint32_t)g4, u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int q = 4 * g4 + e;
+                if (q >= qa && q < qe) fo[q - qa] = u[e] < A.fa.p ? 1 : 0;
+            }
+        }
+    };
+    int G = 0;  // the chunk's tile in progress
     for (int t = A.n - 1; t >= 0; --t) {
         asm volatile("" : "+v"(tid));
         lane = tid & 63;
         r = lane & 15;
         g = lane >> 4;
-        const float *x1 = A.states + (int64_t)(t + 1) * A.stride + xb;
-        // ---- x_t of rows r0 - 1 .. r1 and columns -1 .. W into XS
+        // ---- x_t of rows r0 - 1 .. r1 and columns -1 .. W into XS; on the chunk's last step the
+        // head terms of its tile 0 and its fire bits (later steps get theirs during the step after)
+        if (t == A.n - 1) {
+            if (tid >= FT && tid < FT + 32) head_terms(head_load(t, 0), t, 0, 0);
+            if (!A.fa.fire_u8) fire_bits(t, 0, kFusedThreads);
+        }
         for (int e0 = tid; e0 < xs_items; e0 += XSU * kFusedThreads) {
             xs_load(t, e0);
             xs_store(e0);
@@ -328,24 +416,17 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
         __syncthreads();
 
         // ---- the workgroup's cells in tiles of 32. The front's per-cell inputs from global memory
-        // (the output channels of x_{t+1}, given, target, loss mask, injected fire) are loaded one
-        // tile ahead, so their latency passes during the previous tile's MLP
-        const int ntile = (nw + 31) / 32;
+        // (given, injected fire) are loaded one tile ahead, so their latency passes during the
+        // previous tile's MLP
         struct FrontIn {
-            float xo[4], mk;
-            int tgt;
             uint32_t gv, fb;
         };
         FrontIn fin;
         auto front_load = [&](int tl, FrontIn &fi) {
             const int j = tid & 31;
             const int mt = 32 * tl + j, mtc = mt < nw ? mt : 0;
-            const int q = r0 * W + mtc;
-            const int64_t m = mb + q;
-            load_out<4>(d, x1 + q, fi.xo);
+            const int64_t m = mb + r0 * W + mtc;
             fi.gv = A.fa.given[m];
-            fi.tgt = A.fa.targets ? A.fa.targets[m] : 0;
-            fi.mk = A.fa.mask ? A.fa.mask[m] : 0.0f;
             fi.fb = A.fa.fire_u8 ? A.fa.fire_u8[(int64_t)t * d.rows * HW + m] : 0u;
         };
         if (tid < FT) front_load(0, fin);
@@ -376,26 +457,13 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
                         gi[4 * h + 3] = v.w;
                     }
                 }
-                float xo[4] = {fin.xo[0], fin.xo[1], fin.xo[2], fin.xo[3]};
                 const bool gv = fin.gv != 0;
-                const int tgt = fin.tgt;
-                const float mk = fin.mk;
                 const uint32_t fbyte = fin.fb;
                 if (tl + 1 < ntile) front_load(tl + 1, fin);
-                float f;
-                if (A.fa.fire_u8) {
-                    f = fbyte ? 1.0f : 0.0f;
-                } else {
-                    float u[4];
-                    nca::cell_uniforms4(A.fa.key_ptr ? A.fa.key_ptr[t] : A.fa.key, (uint32_t)(A.fa.row0 + board),
-                                        A.fa.step + (uint32_t)t, (uint32_t)(q >> 2), u);
-                    const int e4 = q & 3;
-                    const float uq = e4 == 0 ? u[0] : e4 == 1 ? u[1] : e4 == 2 ? u[2] : u[3];
-                    f = uq < A.fa.p ? 1.0f : 0.0f;
-                }
-                float gl[4];
-                const float lc = head_grad_core<4>(d, A.wscale[t], A.fa.mask != nullptr, A.fa.denom, hwL, hwL + 16,
-                                                   xo, tgt, mk, gl);
+                const float f = (A.fa.fire_u8 ? fbyte : (uint32_t)fbL[(unsigned)(t & 1) * fbs + mtc]) ? 1.0f : 0.0f;
+                // d loss / d logits of the cell, from the head terms of this tile
+                const float4 glv = *reinterpret_cast<const float4 *>(fiL + (G % 3) * 384 + j * 12);
+                const float gl[4] = {glv.x, glv.y, glv.z, glv.w};
                 const unsigned pg = (unsigned)((j & 15) >> 2), pj = (unsigned)((j & 3) + 4 * (j >> 4));
 #pragma unroll
                 for (int h = 0; h < FCH / 4; ++h) {
@@ -419,47 +487,76 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
                     }
                     if (ok) gx_st(mt, FCH / 4 * oc + h, make_float4(gu[0], gu[1], gu[2], gu[3]));
                 }
-                if (oc == 0) {  // the cell's loss term and head products (summed by the z waves)
-                    float *fi = fiL + (tl & 1) * 768 + j * 24;
-                    fi[0] = ok ? lc : 0.0f;
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) fi[1 + v * 4 + c] = ok ? gl[v] * xo[c] : 0.0f;
-                        fi[17 + v] = ok ? gl[v] : 0.0f;
-                    }
-                }
             } else {
-                const int u = tid - FT, c = u & 31, co = u >> 5;
-                for (int e = 0; e < FCH; ++e) {
-                    const int j = FCH * co + e, mt = 32 * tl + j;
-                    const bool ok = mt < nw;
-                    const int mc = ok ? mt : 0;
-                    const int pr = mc / W, col = mc - pr * W;
-                    uint32_t tv[9];
+                // z of the tile as the forward computes it, on v_mfma_f32_4x4x4_16b_bf16: block
+                // bz = (cell group m, channel octet o) of the two z waves; its row i is cell 4 m + i,
+                // whose lane loads the 9 taps of the octet; per channel c the taps 0-3, 4-7 (bf16
+                // pairs) and tap 8 (with its quad, kernel weight in slot c % 4) take one MFMA
+                // each. Output lane (block, kernel k) holds z of the group's 4 cells.
+                const int u = tid - FT;
+                // the first z wave, in the tiles G = 0, 2, 4, ...: the head terms of tiles G + 1
+                // (lanes 0-31) and G + 2 (lanes 32-63), inputs loaded now and used after the z work
+                const int hG = G + 1 + (u >> 5), hsi = hG / ntile;
+                const int hts = A.n - 1 - hsi, htt = hG - hsi * ntile;
+                const bool head_now = u < 64 && (G & 1) == 0 && hts >= 0;
+                HeadIn hin;
+                if (head_now) hin = head_load(hts, htt);
+                if (u >= 64 && tl == 0 && t > 0 && !A.fa.fire_u8)
+                    fire_bits(t - 1, FT + 64, 64);  // the second z wave: the next step's fire bits
+                const int bz = u >> 2, m = bz & 7, o = bz >> 3;
+                const int jc = 32 * tl + 4 * m + (u & 3), mc = jc < nw ? jc : 0;
+                const int pr = mc / W, col = mc - pr * W;
+                uint4 tq[9];
 #pragma unroll
-                    for (int tp = 0; tp < 9; ++tp)
-                        tv[tp] = *reinterpret_cast<const uint16_t *>(
-                            smem + A.l_XS + (unsigned)(((pr + tp / 3) * W2 + col + tp % 3) * 64 + 2 * c));
-                    const unsigned pg = (unsigned)((j & 15) >> 2), pj = (unsigned)((j & 3) + 4 * (j >> 4));
+                for (int tp = 0; tp < 9; ++tp)
+                    tq[tp] = *reinterpret_cast<const uint4 *>(
+                        smem + A.l_XS + (unsigned)(((pr + tp / 3) * W2 + col + tp % 3) * 64 + 16 * o));
+                auto word = [&](const uint4 &v, int c) -> uint32_t {
+                    const int wd = c >> 1;
+                    return wd == 0 ? v.x : wd == 1 ? v.y : wd == 2 ? v.z : v.w;
+                };
+                const int kz = u & 3;
+                const unsigned zrow0 = (unsigned)(32 * kz + 8 * o);
+                const unsigned zcol = 8u * (unsigned)(m >> 2);
+                const int jv = 32 * tl + 4 * m;  // the group's first tile cell
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        float acc = 0.0f;
+                for (int c = 0; c < 8; ++c) {
+                    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                    const nca::s16x4 sa0 = __builtin_bit_cast(
+                        nca::s16x4, make_uint2(__builtin_amdgcn_perm(word(tq[1], c), word(tq[0], c), sel),
+                                               __builtin_amdgcn_perm(word(tq[3], c), word(tq[2], c), sel)));
+                    const nca::s16x4 sa1 = __builtin_bit_cast(
+                        nca::s16x4, make_uint2(__builtin_amdgcn_perm(word(tq[5], c), word(tq[4], c), sel),
+                                               __builtin_amdgcn_perm(word(tq[7], c), word(tq[6], c), sel)));
+                    const nca::s16x4 a2 =
+                        __builtin_bit_cast(nca::s16x4, c < 4 ? make_uint2(tq[8].x, tq[8].y) : make_uint2(tq[8].z, tq[8].w));
+                    nca::f32x4 dz = {0.f, 0.f, 0.f, 0.f};
+                    dz = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa0, kzb0, dz, 0, 0, 0);
+                    dz = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(sa1, kzb1, dz, 0, 0, 0);
+                    dz = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a2, kzb2[c & 3], dz, 0, 0, 0);
 #pragma unroll
-                        for (int tp = 0; tp < 9; ++tp)
-                            acc = __builtin_fmaf(A.kern[k * 9 + tp], __uint_as_float(tv[tp] << 16), acc);
-                        *reinterpret_cast<__bf16 *>(ms + S::ZB + mb_off((unsigned)(32 * k + c), pg) + 2u * pj) =
-                            (__bf16)(ok ? acc : 0.0f);
-                    }
+                    for (int i = 0; i < 4; ++i) dz[i] = jv + i < nw ? dz[i] : 0.0f;
+                    nca::lds_st64(smem, A.l_MLP + S::ZB + mb_off(zrow0 + (unsigned)c, (unsigned)(m & 3)) + zcol,
+                                  make_uint2(nca::cvt_pk_bf16(dz[0], dz[1]), nca::cvt_pk_bf16(dz[2], dz[3])));
                 }
-                // the previous tile's head and loss terms (FI buffer (tl - 1) & 1), one value per
-                // thread of the first z wave, added to the chunk's sums in tile order
-                if (tl > 0 && u < 21) {
-                    const float *fp = fiL + ((tl - 1) & 1) * 768 + u;
+                if (head_now) head_terms(hin, hts, htt, hG % 3);
+                // this tile's loss and head terms (FI buffer G % 3), summed by the second z wave
+                // and added to the chunk's sums in tile order: term uu is the loss (0), a product
+                // gl[v] xo[c] (1 + 4 v + c) or gl[v] (17 + v) (a product with the row's 1); lane
+                // 3 uu + sg sums the cells 11 sg .. 11 sg + 10 of the tile, lane 3 uu adds the three
+                // partial sums in order
+                if (u >= 64) {
+                    const int u3 = u - 64, uu = u3 / 3, sg = u3 - 3 * uu;
+                    const int ea = uu == 0 ? 8 : (uu <= 16 ? (uu - 1) >> 2 : uu - 17);
+                    const int eb = uu >= 1 && uu <= 16 ? 4 + ((uu - 1) & 3) : 9;
+                    const float *fp = fiL + (G % 3) * 384 + 11 * sg * 12;
+                    const int nseg = sg < 2 ? 11 : 10;
                     float sacc = 0.0f;
-#pragma unroll 8
-                    for (int jj = 0; jj < 32; ++jj) sacc = __fadd_rn(sacc, fp[jj * 24]);
-                    hacc[u] = __fadd_rn(hacc[u], sacc);
+#pragma unroll
+                    for (int jj = 0; jj < 11; ++jj)
+                        if (jj < nseg) sacc = __fadd_rn(sacc, __fmul_rn(fp[jj * 12 + ea], fp[jj * 12 + eb]));
+                    const float p1 = __shfl(sacc, (lane + 1) & 63), p2 = __shfl(sacc, (lane + 2) & 63);
+                    if (sg == 0 && uu < 21) hacc[uu] = __fadd_rn(hacc[uu], __fadd_rn(__fadd_rn(sacc, p1), p2));
                 }
             }
             __syncthreads();
@@ -616,13 +713,7 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
                     }
                 }
             }
-        }
-        if (tid >= FT && tid - FT < 21) {  // the last tile's head and loss terms
-            const float *fp = fiL + ((ntile - 1) & 1) * 768 + (tid - FT);
-            float sacc = 0.0f;
-#pragma unroll 8
-            for (int jj = 0; jj < 32; ++jj) sacc = __fadd_rn(sacc, fp[jj * 24]);
-            hacc[tid - FT] = __fadd_rn(hacc[tid - FT], sacc);
+            ++G;
         }
         __syncthreads();  // g_z of every cell of the workgroup is stored
 
