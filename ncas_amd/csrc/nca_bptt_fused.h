@@ -71,7 +71,8 @@ struct FusedArgs {
 // LDS plan: GZ g_z [k 4][row Hw + 2][col W][c 32] bf16 and GX [cell][c 32] fp32 (pieces only),
 // XS x_t [row Hw + 2][col W + 2][c 32] bf16, the MLP buffers of mlp_back32, the per-cell
 // head terms FI [3 tiles][32][12], the reduction scratch, the chunk's small sums (dk 36, db2 32, head and
-// loss 21), the head's weights and FB, the step's fire bits of the workgroup's cells (a byte each).
+// loss 21), the head's weights (floats 0-19 of HWL; 24-31 zero; 32-67 the perception kernels; 68-99
+// the wall value) and FB, the step's fire bits of the workgroup's cells (a byte each).
 struct FusedPlan {
     unsigned GZ, GX, XS, MLP, FI, RED, ACC, HWL, FB, total;
 };
@@ -94,7 +95,7 @@ inline FusedPlan fused_plan(bool pieces, int Hw, int W) {
     p.ACC = o;
     o += 96u * 4u;
     p.HWL = o;
-    o += 20u * 4u;
+    o += 100u * 4u;
     p.FB = o;
     o += 2u * (((unsigned)(Hw * W) + 15u) & ~15u);
     p.total = o;
@@ -146,6 +147,9 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
     for (int e = tid; e < 256; e += kFusedThreads) reinterpret_cast<float *>(ms + S::B1)[e] = A.b1[e];
     if (tid < d.n_out * d.c_out) hwL[tid] = A.fa.head_w[tid];
     if (tid < d.n_out) hwL[16 + tid] = A.fa.head_b[tid];
+    if (tid < 8) hwL[24 + tid] = 0.0f;  // zeros read by the transposed stencil's taps outside the board
+    if (tid < 36) hwL[32 + tid] = A.kern[tid];  // the perception kernels, read from LDS in the loops
+    if (tid < 32) hwL[68 + tid] = A.padv[tid];  // the wall value of each channel
     if (tid < 96) dkacc[tid] = 0.0f;
     nca::bf16x8 w1f[NH][2][4], w2f[NH][2], w1t[NH][8];
 #pragma unroll
@@ -266,12 +270,9 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
             const int ac = bc < 0 ? bc + W : (bc >= W ? bc - W : bc);
             const bool take = in || wrap;
             const int q = take ? ar * W + ac : 0;
+            // raw loads (the padding value replaces those of cells outside the board in xs_store)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = 8 * o + u;
-                const float xv = xs_src[(int64_t)c * HW + q];
-                xsv[uu][u] = take ? xv : (d.padding == 1 ? A.padv[c] : 0.0f);
-            }
+            for (int u = 0; u < 8; ++u) xsv[uu][u] = xs_src[(int64_t)(8 * o + u) * HW + q];
         }
     };
     auto xs_store = [&](int e0) {
@@ -280,6 +281,11 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
             const int e = e0 + uu * kFusedThreads;
             if (e < xs_items) {
                 const int pc = e % W2, rest = e / W2, o = rest & 3, pr = rest >> 2;
+                const int br = r0 - 1 + pr, bc = pc - 1;
+                if (!wrap && !(br >= 0 && br < H && bc >= 0 && bc < W)) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) xsv[uu][u] = d.padding == 1 ? hwL[68 + 8 * o + u] : 0.0f;
+                }
                 const uint4 pk = {nca::cvt_pk_bf16(xsv[uu][0], xsv[uu][1]), nca::cvt_pk_bf16(xsv[uu][2], xsv[uu][3]),
                                   nca::cvt_pk_bf16(xsv[uu][4], xsv[uu][5]), nca::cvt_pk_bf16(xsv[uu][6], xsv[uu][7])};
                 nca::lds_st128(smem, A.l_XS + (unsigned)((pr * W2 + pc) * 64 + o * 16), pk);
@@ -291,6 +297,19 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
     // (cell, channel quad), the quads of a cell on consecutive threads; an item's 36 loads are
     // issued before its arithmetic
     auto gx_rows = [&](int ra, int rb) {
+        // the kernels' LDS offset, opaque here: the compiler would otherwise keep the 36 weights
+        // in registers through the whole step loop (they never change), crowding the staging
+        unsigned kofs = A.l_HWL + 128u;
+        asm volatile("" : "+s"(kofs));
+        float kwv[36];  // loaded once per call
+#pragma unroll
+        for (int e = 0; e < 9; ++e) {
+            const float4 v = nca::lds_ld128f(smem, kofs + 16u * (unsigned)e);
+            kwv[4 * e] = v.x;
+            kwv[4 * e + 1] = v.y;
+            kwv[4 * e + 2] = v.z;
+            kwv[4 * e + 3] = v.w;
+        }
         for (int it = ra * W * 8 + tid; it < rb * W * 8; it += kFusedThreads) {
             const int mt = it >> 3, cq = it & 7, c0 = 4 * cq;
             const int pr = mt / W, col = mt - pr * W, bi = r0 + pr;
@@ -298,31 +317,33 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
             uint2 zv[9][4];
 #pragma unroll
             for (int tp = 0; tp < 9; ++tp) {
-                // tap tp = (dy, dx) of cell (bi - dy, col - dx) reads this cell
+                // tap tp = (dy, dx) of cell (bi - dy, col - dx) reads this cell; outside the board
+                // (wall or zero padding) it reads zeros (pieces: 8 zero bytes in LDS)
                 const int dy = tp / 3 - 1, dx = tp % 3 - 1;
                 int sc = col - dx;
-                sc = sc < 0 ? sc + W : (sc >= W ? sc - W : sc);
                 const int sb = bi - dy;
+                const bool ok = wrap | (((unsigned)sc < (unsigned)W) & ((unsigned)sb < (unsigned)H));  // no branches
+                sc = sc < 0 ? sc + W : (sc >= W ? sc - W : sc);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     if (PIECES) {
-                        zv[tp][k] = nca::lds_ld64(smem, gz_lds(k, pr - dy, sc, c0));
+                        unsigned ad = ok ? gz_lds(k, pr - dy, sc, c0) : A.l_HWL + 96u;
+                        asm("" : "+v"(ad));  // a select of the address, not a branch around the load
+                        zv[tp][k] = nca::lds_ld64(smem, ad);
                     } else {
                         const int sr = sb < 0 ? sb + H : (sb >= H ? sb - H : sb);
-                        zv[tp][k] = *reinterpret_cast<const uint2 *>(gz_glb(k, sr, sc, c0));
+                        const uint2 z = *reinterpret_cast<const uint2 *>(gz_glb(k, sr, sc, c0));
+                        zv[tp][k] = ok ? z : make_uint2(0u, 0u);
                     }
                 }
             }
             float gq[4] = {gu.x, gu.y, gu.z, gu.w};
 #pragma unroll
             for (int tp = 0; tp < 9; ++tp) {
-                const int dy = tp / 3 - 1, dx = tp % 3 - 1;
-                const int sc = col - dx, sb = bi - dy;
-                const bool ok = ((sc >= 0 && sc < W) || wrap) && ((sb >= 0 && sb < H) || wrap);
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const float kw = A.kern[k * 9 + tp];
-                    const uint2 z = ok ? zv[tp][k] : make_uint2(0u, 0u);
+                    const float kw = kwv[k * 9 + tp];
+                    const uint2 z = zv[tp][k];
                     gq[0] = __builtin_fmaf(kw, nca::bf16_lo(z.x), gq[0]);
                     gq[1] = __builtin_fmaf(kw, nca::bf16_hi(z.x), gq[1]);
                     gq[2] = __builtin_fmaf(kw, nca::bf16_lo(z.y), gq[2]);
