@@ -738,6 +738,36 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
         }
         __syncthreads();  // g_z of every cell of the workgroup is stored
 
+        // ---- the kernel-weight sums dk[k][tap] += sum over channels of g_z[k][c] x_tap[c]: one
+        // v_mfma_f32_16x16x32_bf16 per cell (A rows k < 4 of g_z, k over the 32 channels; B
+        // columns tap < 9 of XS; products of bf16 values, exact), cells strided over the waves;
+        // lane (tap n, group 0) holds dk[i][n] in element i
+        auto dk_operands = [&](int mt, nca::bf16x8 &za, nca::bf16x8 &xbv) {
+            const int pr = mt / W, col = mt - pr * W;
+            if (r < 4) {
+                if (PIECES)
+                    za = mb_ld(smem, gz_lds(r, pr, col, 8 * g));
+                else
+                    za = *reinterpret_cast<const nca::bf16x8 *>(gz_glb(r, pr, col, 8 * g));
+            } else {
+                za = __builtin_bit_cast(nca::bf16x8, make_uint4(0u, 0u, 0u, 0u));
+            }
+            if (r < 9)
+                xbv = mb_ld(smem, A.l_XS + (unsigned)(((pr + r / 3) * W2 + col + r % 3) * 64 + 16 * g));
+            else
+                xbv = __builtin_bit_cast(nca::bf16x8, make_uint4(0u, 0u, 0u, 0u));
+        };
+        auto dk_sums = [&]() {
+            for (int mt = w; mt < nw; mt += 4 * NWV) {  // four cells at a time (their loads together)
+                nca::bf16x8 za[4], xq[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (mt + k * NWV < nw) dk_operands(mt + k * NWV, za[k], xq[k]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (mt + k * NWV < nw) dkw = mb_mfma(za[k], xq[k], dkw);
+            }
+        };
         if (PIECES) {
             // ---- exchange: side 0 is the piece's first row, side 1 its last; the piece above
             // sends its last row (into row -1), the piece below its first (into row Hw)
@@ -759,8 +789,10 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
                 __hip_atomic_store(slot(piece, side) + ee, ((uint64_t)tag << 32) | v, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             }
-            // the interior rows' g_x needs no neighbour's row: it runs while their rows arrive
+            // the interior rows' g_x and the kernel-weight sums need no neighbour's row: they run
+            // while their rows arrive
             if (Hw > 2) gx_rows(1, Hw - 1);
+            dk_sums();
             // receive: at most 4096 words (2 NE, W <= 32, checked by the host), in passes of 8 a
             // thread; the words of a pass are loaded together, and all of them again
             // while one is stale
@@ -807,34 +839,7 @@ __global__ void __launch_bounds__(kFusedThreads, 1) bptt_back_fused(FusedArgs A)
             if (Hw > 1) gx_rows(Hw - 1, Hw);
         } else {
             gx_rows(0, Hw);
-        }
-        // ---- the kernel-weight sums dk[k][tap] += sum over channels of g_z[k][c] x_tap[c]: one
-        // v_mfma_f32_16x16x32_bf16 per cell (A rows k < 4 of g_z, k over the 32 channels; B
-        // columns tap < 9 of XS; products of bf16 values, exact), cells strided over the waves;
-        // lane (tap n, group 0) holds dk[i][n] in element i
-        auto dk_operands = [&](int mt, nca::bf16x8 &za, nca::bf16x8 &xbv) {
-            const int pr = mt / W, col = mt - pr * W;
-            if (r < 4) {
-                if (PIECES)
-                    za = mb_ld(smem, gz_lds(r, pr, col, 8 * g));
-                else
-                    za = *reinterpret_cast<const nca::bf16x8 *>(gz_glb(r, pr, col, 8 * g));
-            } else {
-                za = __builtin_bit_cast(nca::bf16x8, make_uint4(0u, 0u, 0u, 0u));
-            }
-            if (r < 9)
-                xbv = mb_ld(smem, A.l_XS + (unsigned)(((pr + r / 3) * W2 + col + r % 3) * 64 + 16 * g));
-            else
-                xbv = __builtin_bit_cast(nca::bf16x8, make_uint4(0u, 0u, 0u, 0u));
-        };
-        for (int mt = w; mt < nw; mt += 4 * NWV) {  // four cells at a time (their loads together)
-            nca::bf16x8 za[4], xq[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (mt + k * NWV < nw) dk_operands(mt + k * NWV, za[k], xq[k]);
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (mt + k * NWV < nw) dkw = mb_mfma(za[k], xq[k], dkw);
+            dk_sums();
         }
         asm volatile("" : "+a"(dkw));
         __syncthreads();
