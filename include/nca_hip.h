@@ -54,6 +54,9 @@
  *                        update (src/nca/engine/train.py:262-273)
  *   nca_damage_clamp  <- apply_damage + apply_clamp of the training batch (src/nca/perturb.py:
  *                        43-106, src/nca/train.py:219-244)
+ *   nca_pool_rows     <- the replay pool's per-tensor indexing of a training iteration
+ *                        (src/nca/pool.py:96-179: sample's gathers and fresh boards, write_back's
+ *                        scatters and the age counters)
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -244,6 +247,23 @@ int nca_damage_clamp(float *x, int64_t rows, int32_t channels, int32_t height, i
                      const double *discs, int32_t n_discs, int32_t geometry, float fill,
                      const uint8_t *given, const float *clamp, int32_t c_in, int32_t in_offset,
                      void *stream);
+
+/* nca_pool_rows <- the replay pool's indexing (src/nca/pool.py:96-179), every tensor of a batch
+ * in one launch. Item i copies, for r < n_rows, row src_row[r] of src (row r when src_row is
+ * NULL; nothing when src_row[r] < 0) to row dst_row[r] of dst (row r when NULL); rows are
+ * row_bytes apart in both. mode 0 copies, mode 1 adds one to each int64 of the row (the pool's
+ * age), mode 2 writes zeros (src unused). src_row / dst_row are device int64 arrays of n_rows;
+ * at most 16 items; rows written by two items or two r race. */
+typedef struct {
+    const void *src;
+    void *dst;
+    const int64_t *src_row;
+    const int64_t *dst_row;
+    int64_t row_bytes;
+    int32_t mode;
+} nca_pool_row_copy;
+
+int nca_pool_rows(const nca_pool_row_copy *items, int32_t n_items, int64_t n_rows, void *stream);
 
 /* Host-side batched board generation (the inputs of the workloads), on `threads` host threads
  * (0 = all). Every board draws from its own Philox4x32-10 stream keyed on `seed`, so the

@@ -51,6 +51,7 @@ EXPORTS = (
     "nca_set_piece_debug",
     "nca_set_bptt_backward_path",
     "nca_damage_clamp",
+    "nca_pool_rows",
     "nca_maze_boards",
     "nca_sudoku_boards",
 )
@@ -107,6 +108,17 @@ class CellGrads(ctypes.Structure):
 class AdamWDesc(ctypes.Structure):
     _fields_ = [(n, ctypes.c_double) for n in ("lr", "beta1", "beta2", "eps", "weight_decay",
                                                 "ema_decay", "max_norm")]
+
+
+class PoolRowCopy(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p),
+        ("dst", ctypes.c_void_p),
+        ("src_row", ctypes.c_void_p),
+        ("dst_row", ctypes.c_void_p),
+        ("row_bytes", ctypes.c_int64),
+        ("mode", ctypes.c_int32),
+    ]
 
 
 class BpttLoss(ctypes.Structure):
@@ -179,6 +191,7 @@ def load():
                                 vp]
     L.nca_damage_clamp.argtypes = [vp, i64, i32, i32, i32, vp, i32, i32, ctypes.c_float, vp, vp,
                                    i32, i32, vp]
+    L.nca_pool_rows.argtypes = [ctypes.POINTER(PoolRowCopy), i32, i64, vp]
     L.nca_maze_boards.argtypes = [i64, i32, ctypes.c_uint64, ctypes.c_double, i32, i32, vp, vp, vp,
                                   vp, i32]
     L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]

@@ -14,6 +14,10 @@
 //   operation for operation in fp32 with the same scalars: p *= 1 - lr wd; m = lerp(m, g, 1 - b1);
 //   v = v b2 + (1 - b2) g g; p += -(lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps).
 //
+// nca_pool_rows - the replay pool's gathers and scatters of a training iteration (every key of a
+//   batch, the fresh boards' rows and the age counters) in one launch: the reference indexes each
+//   of the pool's tensors on its own (src/nca/pool.py:96-179), one kernel per tensor and step.
+//
 // nca_damage_clamp - the damage perturbation (src/nca/perturb.py:43-106: the state set to `fill`
 //   inside discs) and the clamp of the given cells' input channels (model.py:430-438) in one pass
 //   over the state, in place. The discs are drawn on the host (their random stream is the
@@ -25,6 +29,7 @@
 
 #include <math.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "nca_hip.h"
 #include "nca_status.h"
@@ -195,7 +200,67 @@ __global__ void __launch_bounds__(kDamageThreads)
     }
 }
 
+// ---- replay-pool row copies: item i copies row src_row[r] (r when NULL; none when < 0) of its
+// source to row dst_row[r] (r when NULL) of its destination, for r < n_rows, 16 bytes at a time
+// where the rows and pointers allow it (else 4, else 1); mode 1 adds one to every int64 of the row,
+// mode 2 writes zeros (no source)
+constexpr int kRowItems = 16;
+constexpr int kRowThreads = 256;
+struct RowArgs {
+    nca_pool_row_copy it[kRowItems];
+    int n_items;
+    int64_t n_rows;
+};
+
+__global__ void __launch_bounds__(kRowThreads) pool_rows_kernel(RowArgs a) {
+    const int64_t r = blockIdx.x;
+    const nca_pool_row_copy &c = a.it[blockIdx.y];
+    const int64_t sr = c.src_row ? c.src_row[r] : r;
+    if (sr < 0) return;
+    const int64_t dr = c.dst_row ? c.dst_row[r] : r;
+    unsigned char *dst = static_cast<unsigned char *>(c.dst) + dr * c.row_bytes;
+    const unsigned char *src = c.mode == 2 ? nullptr : static_cast<const unsigned char *>(c.src) + sr * c.row_bytes;
+    if (c.mode == 1) {
+        for (int64_t e = threadIdx.x; e < c.row_bytes / 8; e += kRowThreads)
+            reinterpret_cast<int64_t *>(dst)[e] = reinterpret_cast<const int64_t *>(src)[e] + 1;
+        return;
+    }
+    const uintptr_t al = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | (uintptr_t)c.row_bytes;
+    if ((al & 15u) == 0) {
+        for (int64_t e = threadIdx.x; e < c.row_bytes / 16; e += kRowThreads)
+            reinterpret_cast<uint4 *>(dst)[e] = src ? reinterpret_cast<const uint4 *>(src)[e] : make_uint4(0u, 0u, 0u, 0u);
+    } else if ((al & 3u) == 0) {
+        for (int64_t e = threadIdx.x; e < c.row_bytes / 4; e += kRowThreads)
+            reinterpret_cast<uint32_t *>(dst)[e] = src ? reinterpret_cast<const uint32_t *>(src)[e] : 0u;
+    } else {
+        for (int64_t e = threadIdx.x; e < c.row_bytes; e += kRowThreads) dst[e] = src ? src[e] : (unsigned char)0;
+    }
+}
+
 }  // namespace
+
+extern "C" int nca_pool_rows(const nca_pool_row_copy *items, int32_t n_items, int64_t n_rows, void *stream) {
+    nca::clear_error();
+    if (n_items < 0 || n_items > kRowItems || n_rows < 0)
+        return nca::set_error(NCA_ERR_INVALID, "0 <= n_items <= 16, n_rows >= 0");
+    if (n_items == 0 || n_rows == 0) return NCA_OK;
+    if (!items) return nca::set_error(NCA_ERR_INVALID, "NULL items");
+    if (n_rows > 0x7fffffffll) return nca::set_error(NCA_ERR_UNSUPPORTED, "n_rows < 2^31");
+    RowArgs a;
+    memset(&a, 0, sizeof(a));
+    for (int i = 0; i < n_items; ++i) {
+        const nca_pool_row_copy &c = items[i];
+        if (!c.dst || (c.mode != 2 && !c.src) || c.row_bytes < 0 || c.mode < 0 || c.mode > 2)
+            return nca::set_error(NCA_ERR_INVALID, "an item needs dst, src (modes 0, 1), row_bytes >= 0, mode 0-2");
+        if (c.mode == 1 && c.row_bytes % 8 != 0) return nca::set_error(NCA_ERR_INVALID, "mode 1 rows hold int64 values");
+        a.it[i] = c;
+    }
+    a.n_items = n_items;
+    a.n_rows = n_rows;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(pool_rows_kernel, dim3((unsigned)n_rows, (unsigned)n_items), dim3(kRowThreads), 0, st, a);
+    return nca::hip_status(hipGetLastError(), "pool rows launch");
+}
 
 extern "C" int nca_adamw_ema(float *params, float *grads, float *exp_avg, float *exp_avg_sq, float *ema, int64_t n,
                              const nca_adamw_desc *desc, int64_t *counters, float *grad_norm, void *workspace,

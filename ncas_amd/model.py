@@ -325,7 +325,7 @@ class NCA(nn.Module):
     def token_table(self, kind: str, device) -> torch.Tensor:
         """Small lookup tables on the device, uploaded once per device without a host wait:
         "tokens" (class index -> output token) and "index" (token -> class index, 0 for tokens
-        that are no output)."""
+        that are no output; "index32" the same as int32)."""
         key = (kind, str(device))
         cache = self.__dict__.setdefault("_tables", {})
         t = cache.get(key)
@@ -333,14 +333,15 @@ class NCA(nn.Module):
             if kind == "tokens":
                 host = np.asarray(self.cfg.output_tokens, dtype=np.int64)
             else:
-                host = np.zeros(self.cfg.vocab_size, dtype=np.int64)
+                host = np.zeros(self.cfg.vocab_size, dtype=np.int32 if kind == "index32" else np.int64)
                 for i, tok in enumerate(self.cfg.output_tokens):
                     host[tok] = i
             t = cache[key] = _lib.upload(host, torch.device(device))
         return t
 
-    def output_index(self, targets):
-        return self.token_table("index", targets.device)[targets]
+    def output_index(self, targets, dtype=torch.int64):
+        """Class indices of target tokens (int64, or int32 with dtype=torch.int32)."""
+        return self.token_table("index32" if dtype == torch.int32 else "index", targets.device)[targets]
 
     # ------------------------------------------------------------------ HIP operators
     def step(self, x, given4, clamp, fire_mask, noise=None, clock=None, precision="fp32"):

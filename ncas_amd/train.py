@@ -110,7 +110,7 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
     pk = model.packed(precision, dev)
     L = _lib.load()
     xs = x.detach().to(torch.float32).contiguous()
-    g8 = given4.detach().to(torch.uint8).contiguous()
+    g8 = (given4.detach().view(torch.uint8) if given4.dtype == torch.bool else given4.detach().to(torch.uint8)).contiguous()
     cl = clamp.detach().to(torch.float32).contiguous()
     tg = targets.detach().to(torch.int32).contiguous()
     lm = None if loss_mask is None else loss_mask.detach().to(torch.float32).contiguous()
@@ -139,8 +139,6 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                                      xs.data_ptr(), g8.data_ptr(), cl.data_ptr(), ctypes.byref(fd),
                                      n, states.data_ptr(), ws.data_ptr(), ws_bytes, stream),
                "nca_bptt_forward_ws")
-    # the forward's status word, read on the stream before the backward overwrites the workspace
-    halo_failed = ws[:1].view(torch.int32) != 0
     # fp32 master weights for the backward GEMMs (rounded to bf16 on load for bf16 cells)
     params = _params(model)
     master = [p.detach().to(dev, torch.float32).contiguous() for p in params]
@@ -156,8 +154,10 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
                                    ctypes.byref(lossd), _lib.ptr(gf), ctypes.byref(gs),
                                    _lib.ptr(gx0), loss.data_ptr(), ws.data_ptr(), ws_bytes,
                                    stream), "nca_bptt_backward")
-    # the one-launch backward's status word (bytes 8 .. 11; zero when it did not run in pieces)
-    back_repaired = ws[2:3].view(torch.int32) != 0
+    # the status words of the forward's pieces (bytes 0 .. 3, which the backward leaves alone) and of
+    # the one-launch backward's (bytes 8 .. 11; zero when it did not run in pieces), in one test
+    flags = ws[:3].view(torch.int32)[0::2] != 0
+    halo_failed, back_repaired = flags[0:1], flags[1:2]
     # no wait: the host arrays were read during the calls, and the device buffers freed here are
     # reused only by later work on the same stream
     return ChunkResult(states[n].clone(), loss, grads, gx0, states.numel() * 4, ws_bytes,
@@ -400,7 +400,7 @@ class Engine:
         precision = "bf16" if self.tr.get("amp", False) else "fp32"
         x = self.forward_steps(batch["x"], given4, clamp, seeds[:lo], 0)
         if self.fused_chunk:
-            res = bptt_chunk(model, x, given4, clamp, model.output_index(batch["targets"]), w,
+            res = bptt_chunk(model, x, given4, clamp, model.output_index(batch["targets"], torch.int32), w,
                              step_seeds=seeds[lo:hi], step0=lo, p_fire=self.p_fire,
                              precision=precision, loss_mask=batch.get("loss_mask"))
             self.last_chunk = res
@@ -446,40 +446,104 @@ class ReplayPool:
         self.model, self.boards, self.size, self.rng = model, boards, size, rng
         self.generator, self.task, self.augment = generator, task, augment
         self.device = model.device
+        # tensors of their own (fresh's are views of one upload, which a checkpoint cannot hold)
         for key, value in self.fresh(size).items():
-            setattr(self, key, value)
+            setattr(self, key, None if value is None else value.clone())
         self.age = torch.zeros(size, dtype=torch.long, device=self.device)
 
-    def fresh(self, n: int) -> dict:
+    def _upload_many(self, arrays) -> list:
+        """Host arrays on the device in one copy (one buffer, each array at a 16-byte boundary),
+        as contiguous tensors of their dtypes and shapes (views of that buffer)."""
+        arrays = [np.ascontiguousarray(a) for a in arrays]
+        offs, total = [], 0
+        for a in arrays:
+            offs.append(total)
+            total += (a.nbytes + 15) & ~15
+        host = np.zeros(max(total, 1), np.uint8)
+        for a, o in zip(arrays, offs):
+            host[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
+        dev = _lib.upload(host, self.device)
+        return [dev[o:o + a.nbytes].view(torch.from_numpy(a[:0].reshape(-1)).dtype).view(a.shape)
+                for a, o in zip(arrays, offs)]
+
+    def fresh(self, n: int, extra=()) -> dict:
         """`n` boards drawn uniformly (with replacement) from the board set, augmented when the
-        pool has a task that augments, each with a freshly initialised state."""
+        pool has a task that augments, each with a freshly initialised state. The boards' arrays
+        (and the host arrays in `extra`, returned under "_extra") go to the device in one copy."""
         picks = self.rng.integers(0, len(self.boards), size=n)
         chosen = self.boards.subset(picks)
         if self.augment and self.task is not None:
             chosen = self.task.augment(chosen, self.rng)
-        dev = self.device
-        inputs = _lib.upload(chosen.inputs, dev)
-        given = _lib.upload(chosen.given, dev)
-        x, given4, clamp = self.model.init_state(inputs, given, None, self.generator)
         lm = chosen.meta.get("loss_mask")
-        return {"x": x.detach(), "given4": given4, "clamp": clamp, "inputs": inputs,
-                "targets": _lib.upload(chosen.targets, dev),
-                "loss_mask": None if lm is None else _lib.upload(np.asarray(lm, np.float32), dev)}
+        host = [chosen.inputs, chosen.given, chosen.targets]
+        if lm is not None:
+            host.append(np.asarray(lm, np.float32))
+        dev = self._upload_many(host + list(extra))
+        inputs, given, targets = dev[:3]
+        x, given4, clamp = self.model.init_state(inputs, given, None, self.generator)
+        out = {"x": x.detach(), "given4": given4, "clamp": clamp, "inputs": inputs, "targets": targets,
+               "loss_mask": None if lm is None else dev[3]}
+        if extra:
+            out["_extra"] = dev[len(host):]
+        return out
+
+    def _rows(self, items, n_rows: int) -> None:
+        """One launch of nca_pool_rows over (src, dst, src_row, dst_row, mode) items (a pool on a
+        CPU device indexes with torch)."""
+        if self.device.type != "cuda":
+            with torch.no_grad():
+                for src, dst, srow, drow, mode in items:
+                    if srow is not None:
+                        sel = srow >= 0
+                        dst[sel] = 0 if mode == 2 else src[srow[sel]]
+                    else:
+                        dst[drow] = src + 1 if mode == 1 else src
+            return
+        arr = (_lib.PoolRowCopy * len(items))()
+        for i, (src, dst, srow, drow, mode) in enumerate(items):
+            if src is not None and (src.dtype != dst.dtype or src.shape[1:] != dst.shape[1:]):
+                raise ValueError("pool rows: dtype or row shape mismatch")
+            if not dst.is_contiguous() or (src is not None and not src.is_contiguous()):
+                raise ValueError("pool rows: tensors must be contiguous")
+            arr[i] = _lib.PoolRowCopy(None if src is None else src.data_ptr(), dst.data_ptr(),
+                                      None if srow is None else srow.data_ptr(),
+                                      None if drow is None else drow.data_ptr(),
+                                      dst[0].numel() * dst.element_size(), mode)
+        _lib.check(_lib.load().nca_pool_rows(arr, len(items), n_rows, _lib.stream_of(self.device)),
+                   "nca_pool_rows")
 
     def sample(self, batch_size: int, seed_ratio: float):
         """`batch_size` distinct pool entries (copies), of which the first
         round(seed_ratio * batch_size) are replaced by fresh boards of age 0. Returns (pool
         indices, batch dict)."""
         idx = self.rng.choice(self.size, size=batch_size, replace=False)
-        rows = _lib.upload(idx, self.device)
-        batch = {k: (None if getattr(self, k) is None else getattr(self, k).index_select(0, rows))
-                 for k in self.KEYS + ("age",)}
         n_new = int(round(seed_ratio * batch_size))
+        # row maps: the pool rows (idx), the pool row of each batch row (-1 for the fresh ones)
+        # and the fresh row of each batch row (-1 for the others); one upload with the boards
+        maps = np.full((3, batch_size), -1, np.int64)
+        maps[0] = idx
+        maps[1, n_new:] = idx[n_new:]
+        maps[2, :n_new] = np.arange(n_new)
         if n_new > 0:
-            for k, v in self.fresh(n_new).items():
-                if v is not None:
-                    batch[k][:n_new] = v
-            batch["age"][:n_new] = 0
+            new = self.fresh(n_new, extra=(maps,))
+            maps_d = new.pop("_extra")[0]
+        else:
+            new, maps_d = {}, _lib.upload(maps, self.device)
+        batch, items = {}, []
+        for k in self.KEYS + ("age",):
+            src = getattr(self, k)
+            if src is None:
+                batch[k] = None
+                continue
+            batch[k] = torch.empty((batch_size,) + tuple(src.shape[1:]), dtype=src.dtype, device=src.device)
+            items.append((src, batch[k], maps_d[1], None, 0))
+            if n_new > 0:
+                if k == "age":
+                    items.append((None, batch[k], maps_d[2], None, 2))  # fresh boards: age 0
+                else:
+                    items.append((new[k], batch[k], maps_d[2], None, 0))
+        self._rows(items, batch_size)
+        self._last_rows = (idx, maps_d[0])
         return idx, batch
 
     def replace_boards(self, batch: dict, which: np.ndarray) -> None:
@@ -515,13 +579,14 @@ class ReplayPool:
     def write_back(self, idx, batch: dict) -> None:
         """Store the batch's post-rollout states and boards at the pool indices they came from,
         one rollout older (reference pool.py:166-179)."""
-        rows = _lib.upload(idx, self.device)
-        with torch.no_grad():
-            self.x[rows] = batch["x"].detach()
-        for k in ("given4", "clamp", "inputs", "targets", "loss_mask"):
+        last = getattr(self, "_last_rows", None)
+        rows = last[1] if last is not None and last[0] is idx else _lib.upload(np.asarray(idx, np.int64), self.device)
+        items = []
+        for k in self.KEYS:
             if getattr(self, k) is not None and batch.get(k) is not None:
-                getattr(self, k)[rows] = batch[k]
-        self.age[rows] = batch["age"] + 1
+                items.append((batch[k].detach().contiguous(), getattr(self, k), None, rows, 0))
+        items.append((batch["age"].contiguous(), self.age, None, rows, 1))  # one rollout older
+        self._rows(items, len(idx))
 
     def state_dict(self) -> dict:
         return {k: getattr(self, k) for k in self.KEYS + ("age",)}
