@@ -336,6 +336,8 @@ typedef struct nca_cell_grads {
     float *b2;      /* (C) */
     float *head_w;  /* (n_out, c_out, 1, 1) */
     float *head_b;  /* (n_out) */
+    int32_t accumulate; /* 0: the gradients are written; 1: added to the buffers' contents (as
+                           autograd adds into .grad) */
 } nca_cell_grads;
 
 /* The chunk loss: sum_t w_t * step_loss(x_{t+1}) / max(sum_t w_t, 1), step_loss = the mean over

@@ -102,7 +102,8 @@ class FireDesc(ctypes.Structure):
 
 
 class CellGrads(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_void_p) for n in ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")]
+    _fields_ = [(n, ctypes.c_void_p) for n in ("kernels", "w1", "b1", "w2", "b2", "head_w", "head_b")] + [
+        ("accumulate", ctypes.c_int32)]
 
 
 class AdamWDesc(ctypes.Structure):

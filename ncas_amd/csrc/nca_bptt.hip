@@ -206,6 +206,13 @@ __device__ float block_sums(const float (&v)[N], float *red) {
     return r;
 }
 
+// two ranges cleared in one launch: n floats at p and m 8-byte words at q
+__global__ void zero_f32_words(float *p, int64_t n, uint64_t *q, int64_t m) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = t; i < n; i += stride) p[i] = 0.0f;
+    for (int64_t i = t; i < m; i += stride) q[i] = 0;
+}
+
 __global__ void zero_f32(float *p, int64_t n) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = 0.0f;
@@ -968,14 +975,50 @@ __global__ void copy_kernel(const float *src, float *dst, int64_t n) {
 struct GradOut {
     float *dst[7];
     int64_t off[7], n[7];
+    int accumulate;  // add into dst rather than write it
 };
+
+__device__ __forceinline__ void grad_put(const GradOut &g, int k, int64_t i, float v) {
+    float *p = g.dst[k] + i;
+    *p = g.accumulate ? __fadd_rn(*p, v) : v;
+}
 
 __global__ void grads_out_kernel(const float *acc, GradOut g) {
     const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
 #pragma unroll
     for (int k = 0; k < 7; ++k)
         if (g.dst[k])
-            for (int64_t i = t; i < g.n[k]; i += stride) g.dst[k][i] = acc[g.off[k] + i];
+            for (int64_t i = t; i < g.n[k]; i += stride) grad_put(g, k, i, acc[g.off[k] + i]);
+}
+
+// The end of a backward in one launch: the slots summed in slot order (reduce_acc_kernel's sums),
+// each parameter's gradient put straight into the caller's tensor (grads_out_kernel's), and the
+// last block's loss (loss_kernel's), when nothing is added to acc between them.
+__global__ void finish_kernel(const float *part, int64_t P, float *acc, GradOut g, const float *lossacc, float *loss_out) {
+    if (blockIdx.x == gridDim.x - 1) {
+        if (loss_out) {
+            __shared__ float red[kThreads];
+            const float s = block_sum(threadIdx.x < kSplit ? lossacc[threadIdx.x] : 0.0f, red);
+            if (threadIdx.x == 0) *loss_out = s;
+        }
+        return;
+    }
+    constexpr int kB = 64;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < P; i += (int64_t)(gridDim.x - 1) * blockDim.x) {
+        float s = 0.0f;
+        for (int k0 = 0; k0 < kSplit; k0 += kB) {
+            float v[kB];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) v[k] = k0 + k < kSplit ? part[(int64_t)(k0 + k) * P + i] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < kB; ++k)
+                if (k0 + k < kSplit) s = __fadd_rn(s, v[k]);
+        }
+        acc[i] = s;
+#pragma unroll
+        for (int k = 0; k < 7; ++k)
+            if (g.dst[k] && i >= g.off[k] && i < g.off[k] + g.n[k]) grad_put(g, k, i - g.off[k], s);
+    }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1161,16 +1204,17 @@ int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t r
         rc = nca::hip_status(hipMemcpyAsync(states, x0, sn * sizeof(float), hipMemcpyDeviceToDevice, st), "state copy");
         if (rc) return rc;
     }
-    // the workspace's first word reports whether a wait of the boards' pieces ran out: zero unless
-    // this call sets it
-    if (workspace && workspace_bytes >= nca::kXchStatusBytes &&
-        (rc = nca::hip_status(nca::clear_words(static_cast<uint64_t *>(workspace), nca::kXchStatusBytes / 8, st),
-                              "status clear")))
-        return rc;
     // the whole chunk in one launch of the streamed kernel where it takes the cell and grid
     bool used = false;
+    int pieces = 1;
     if ((rc = nca::rollout_recorded(cell, packed, rows, height, width, x0, given, clamp, states + n_chunk * sn, fire,
-                                    n_chunk, states + sn, sn, st, &used, workspace, workspace_bytes)))
+                                    n_chunk, states + sn, sn, st, &used, workspace, workspace_bytes, &pieces)))
+        return rc;
+    // the workspace's first word reports whether a wait of the boards' pieces ran out: zero unless
+    // this call sets it (the launch of pieces clears it itself)
+    if (pieces == 1 && workspace && workspace_bytes >= nca::kXchStatusBytes &&
+        (rc = nca::hip_status(nca::clear_words(static_cast<uint64_t *>(workspace), nca::kXchStatusBytes / 8, st),
+                              "status clear")))
         return rc;
     if (used) return NCA_OK;
     for (int t = 0; t < n_chunk; ++t) {
@@ -1267,8 +1311,12 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
     float *lossacc = ws + L.lossacc, *denom = ws + L.denom;
     const int64_t sn = d.rows * d.C * (int64_t)d.HW;
 
-    // the partial-sum slots and the loss slots are contiguous
-    hipLaunchKernelGGL(zero_f32, dim3(2048), dim3(256), 0, st, part, L.denom - L.part);
+    // the partial-sum slots and the loss slots are contiguous; with the one-launch backward on
+    // pieces of boards, its status word and exchange slots are cleared by the same launch
+    const FusedChoice fc = fused_choice(d, n_chunk, fire_f32 != nullptr, L);
+    uint64_t *const wsw = static_cast<uint64_t *>(workspace);
+    const int64_t xch_words = fc.pieces > 1 ? (int64_t)(fc.xch_bytes / sizeof(uint64_t)) - 1 : 0;
+    hipLaunchKernelGGL(zero_f32_words, dim3(2048), dim3(256), 0, st, part, L.denom - L.part, wsw + 1, xch_words);
     const bool fused = fused_mlp(d);
     auto mlp_kfn = (d.M & 3) == 0 ? nca::mlp_back32<true> : nca::mlp_back32<false>;
     if (fused && (rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(mlp_kfn),
@@ -1293,7 +1341,6 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
                            reinterpret_cast<unsigned char *>(ws + L.img));
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);
     if ((rc = nca::hip_status(hipGetLastError(), "bptt setup"))) return rc;
-    const FusedChoice fc = fused_choice(d, n_chunk, fire_f32 != nullptr, L);
     if (fc.pieces > 0) {
         FusedArgs A;
         memset(&A, 0, sizeof(A));
@@ -1360,17 +1407,13 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         set_plan(Aw, fc.whole);
         if (fc.pieces > 1) {
             // the status word (bytes 8 .. 11 of the workspace; bytes 0 .. 3 hold the forward's) and
-            // the exchange slots after the status block, cleared here
-            uint64_t *wsw = static_cast<uint64_t *>(workspace);
+            // the exchange slots after the status block, cleared with the slots above
             A.status = reinterpret_cast<uint32_t *>(workspace) + 2;
             A.xch = wsw + nca::kXchStatusBytes / sizeof(uint64_t);
             A.pieces = fc.pieces;
             A.Hp = fc.Hp;
             A.gz_rows = fc.Hp + 2;
             set_plan(A, fc.plan);
-            if ((rc = nca::hip_status(nca::clear_words(wsw + 1, (int64_t)(fc.xch_bytes / sizeof(uint64_t)) - 1, st),
-                                      "fused backward exchange clear")))
-                return rc;
             if ((rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(kp),
                                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)fc.plan.total),
                                       "fused backward attribute")))
@@ -1509,18 +1552,13 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         if ((rc = nca::hip_status(hipGetLastError(), "bptt step kernels"))) return rc;
         gin = gx;
     }
-    // the slots summed in slot order
-    hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
-    if (planes_ok && fc.pieces == 0)
-        hipLaunchKernelGGL(reduce_dk, dim3(36), dim3(kThreads), 0, st, ws + L.dk, strips_ok ? strip_blocks : d.rows * d.C,
-                           acc + P.K);
     if (grad_x0) {
         if (n_chunk == 0 || d.M == 0) {
             if (grad_final) hipLaunchKernelGGL(copy_kernel, dim3(256), dim3(256), 0, st, grad_final, grad_x0, sn);
             else hipLaunchKernelGGL(zero_f32, dim3(256), dim3(256), 0, st, grad_x0, sn);
         }
     }
-    // the gradients in the reference's parameter layouts
+    // the gradients in the reference's parameter layouts (written, or added to the caller's)
     GradOut go;
     float *gdst[7] = {grads->kernels, grads->w1, grads->b1, grads->w2, grads->b2, grads->head_w, grads->head_b};
     const int64_t goff[7] = {P.K, P.W1, P.B1, P.W2, P.B2, P.HW, P.HB};
@@ -1530,13 +1568,20 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
         go.off[k] = goff[k];
         go.n[k] = gn[k];
     }
-    hipLaunchKernelGGL(grads_out_kernel, dim3(128), dim3(256), 0, st, acc, go);
-    if (loss_out) {
-        if (n_chunk > 0 && d.M > 0)
-            hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossacc, loss_out);
-        else
-            hipLaunchKernelGGL(zero_f32, dim3(1), dim3(64), 0, st, loss_out, (int64_t)1);
+    go.accumulate = grads->accumulate != 0;
+    const bool has_loss = n_chunk > 0 && d.M > 0;
+    if (planes_ok && fc.pieces == 0) {
+        // the slots summed in slot order, the strips' kernel-weight sums added, then the gradients
+        hipLaunchKernelGGL(reduce_acc_kernel, dim3((unsigned)((P.P + 255) / 256)), dim3(256), 0, st, part, P.P, acc);
+        hipLaunchKernelGGL(reduce_dk, dim3(36), dim3(kThreads), 0, st, ws + L.dk, strips_ok ? strip_blocks : d.rows * d.C,
+                           acc + P.K);
+        hipLaunchKernelGGL(grads_out_kernel, dim3(128), dim3(256), 0, st, acc, go);
+        if (loss_out && has_loss) hipLaunchKernelGGL(loss_kernel, dim3(1), dim3(kThreads), 0, st, lossacc, loss_out);
+    } else {
+        hipLaunchKernelGGL(finish_kernel, dim3((unsigned)((P.P + kThreads - 1) / kThreads) + 1u), dim3(kThreads), 0, st,
+                           part, P.P, acc, go, lossacc, has_loss ? loss_out : nullptr);
     }
+    if (loss_out && !has_loss) hipLaunchKernelGGL(zero_f32, dim3(1), dim3(64), 0, st, loss_out, (int64_t)1);
     return nca::hip_status(hipGetLastError(), "bptt finish");
 }
 

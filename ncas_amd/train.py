@@ -92,13 +92,15 @@ class ChunkResult:
 def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step_seeds=None,
                masks=None, p_fire: float | None = None, row0: int = 0, step0: int = 0,
                precision: str = "fp32", loss_mask=None, grad_final=None,
-               want_grad_x0: bool = False) -> ChunkResult:
+               want_grad_x0: bool = False, accumulate_into=None) -> ChunkResult:
     """Forward + backward of one BPTT chunk of `len(weights)` steps on the GPU.
 
     targets: (B, H, W) class indices in [0, n_out) (`model.output_index(tokens)`); masks:
     injected fire masks (n, B, 1, H, W), else Philox keyed on `step_seeds` (n,) or `seed`, with
     counter steps step0 .. step0 + n - 1. `weights` is read on the host (a host array avoids a
-    device-to-host copy)."""
+    device-to-host copy). With `accumulate_into` (the parameters' fp32 gradient tensors, in the
+    model's parameter order) the gradients are added into those tensors, as autograd adds into
+    .grad, and the result's `grads` is None."""
     cfg = model.cfg
     if cfg.head != "mlp":
         raise ValueError("the fused chunk's loss is the cross-entropy of an mlp head")
@@ -143,9 +145,18 @@ def bptt_chunk(model, x, given4, clamp, targets, weights, *, seed: int = 0, step
     params = _params(model)
     master = [p.detach().to(dev, torch.float32).contiguous() for p in params]
     wts = _lib.CellWeights(*[m.data_ptr() for m in master], None)
-    grads = {name: torch.empty(p.shape, dtype=torch.float32, device=dev)
-             for name, p in zip(_GRAD_NAMES, params)}
-    gs = _lib.CellGrads(*[grads[k].data_ptr() for k in _GRAD_NAMES])
+    if accumulate_into is not None:
+        acc = list(accumulate_into)
+        if len(acc) != len(params) or any(
+                a.dtype != torch.float32 or a.device != dev or not a.is_contiguous() or a.shape != p.shape
+                for a, p in zip(acc, params)):
+            raise ValueError("accumulate_into: the parameters' contiguous fp32 gradients on the device")
+        grads = None
+        gs = _lib.CellGrads(*[a.data_ptr() for a in acc], 1)
+    else:
+        grads = {name: torch.empty(p.shape, dtype=torch.float32, device=dev)
+                 for name, p in zip(_GRAD_NAMES, params)}
+        gs = _lib.CellGrads(*[grads[k].data_ptr() for k in _GRAD_NAMES], 0)
     gx0 = torch.empty_like(xs) if want_grad_x0 else None
     loss = torch.empty((), dtype=torch.float32, device=dev)
     lossd = _lib.BpttLoss(tg.data_ptr(), _lib.ptr(lm), w_host.ctypes.data_as(ctypes.c_void_p))
@@ -400,20 +411,27 @@ class Engine:
         precision = "bf16" if self.tr.get("amp", False) else "fp32"
         x = self.forward_steps(batch["x"], given4, clamp, seeds[:lo], 0)
         if self.fused_chunk:
+            params = _params(model)
+            # the gradients are added straight into .grad where every parameter has an fp32 one
+            # (optim.FusedUpdate's views of its flat buffer), else into .grad afterwards
+            into = [p.grad for p in params]
+            direct = all(g is not None and g.dtype == torch.float32 and g.is_contiguous() and g.device == x.device
+                         for g in into)
             res = bptt_chunk(model, x, given4, clamp, model.output_index(batch["targets"], torch.int32), w,
                              step_seeds=seeds[lo:hi], step0=lo, p_fire=self.p_fire,
-                             precision=precision, loss_mask=batch.get("loss_mask"))
+                             precision=precision, loss_mask=batch.get("loss_mask"),
+                             accumulate_into=into if direct else None)
             self.last_chunk = res
-            # added into existing gradients in place (one launch), so a gradient that is a view
-            # of a flat buffer (optim.FusedUpdate) stays one
-            params = _params(model)
-            grads = [res.grads[n].reshape(p.shape).to(p.dtype) for n, p in zip(_GRAD_NAMES, params)]
-            have = [(p.grad, g) for p, g in zip(params, grads) if p.grad is not None]
-            if have:
-                torch._foreach_add_([a for a, _ in have], [g for _, g in have])
-            for p, g in zip(params, grads):
-                if p.grad is None:
-                    p.grad = g
+            if not direct:
+                # added into existing gradients in place (one launch), so a gradient that is a view
+                # of a flat buffer stays one
+                grads = [res.grads[n].reshape(p.shape).to(p.dtype) for n, p in zip(_GRAD_NAMES, params)]
+                have = [(p.grad, g) for p, g in zip(params, grads) if p.grad is not None]
+                if have:
+                    torch._foreach_add_([a for a, _ in have], [g for _, g in have])
+                for p, g in zip(params, grads):
+                    if p.grad is None:
+                        p.grad = g
             x, loss = res.x, res.loss
         else:
             with torch.enable_grad():
@@ -423,7 +441,9 @@ class Engine:
         if grad_clip is not None:
             gn = torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)
         else:
-            gn = loss.new_zeros(())
+            gn = self.__dict__.get("_zero_norm")
+            if gn is None or gn.device != loss.device:
+                gn = self._zero_norm = loss.new_zeros(())
         if apply_update is not None and not self.cfg.update_after_rollout:
             apply_update(gn)
         x = self.forward_steps(x, given4, clamp, seeds[hi:], hi)
