@@ -57,6 +57,8 @@
  *   nca_pool_rows     <- the replay pool's per-tensor indexing of a training iteration
  *                        (src/nca/pool.py:96-179: sample's gathers and fresh boards, write_back's
  *                        scatters and the age counters)
+ *   nca_init_state    <- NCA.init_state (src/nca/model.py:384-412) with clamp_values and
+ *                        apply_clamp (model.py:378-382, 430-438)
  */
 #ifndef NCA_HIP_H
 #define NCA_HIP_H
@@ -264,6 +266,17 @@ typedef struct {
 } nca_pool_row_copy;
 
 int nca_pool_rows(const nca_pool_row_copy *items, int32_t n_items, int64_t n_rows, void *stream);
+
+/* nca_init_state <- NCA.init_state (src/nca/model.py:384-412) for the noise drawn by the caller:
+ * x (rows, channels, hw) = uniform ? (noise * 2 - 1) * sigma : noise * sigma, one rounding per
+ * operation as the reference's torch expressions; clamp (rows, c_in, hw) = embed[token] (the
+ * clamp values, model.py:378-382; embed is (vocab, c_in)); channels [in_off, in_off + c_in) of
+ * given cells take the clamp values (apply_clamp, model.py:430-438). tokens int64 (rows, hw),
+ * given (rows, hw) bytes, noise (rows, channels, hw) fp32; a token outside [0, vocab) gets NaN
+ * clamp values. */
+int nca_init_state(const float *noise, const int64_t *tokens, const uint8_t *given, const float *embed,
+                   int32_t vocab, int64_t rows, int32_t channels, int32_t c_in, int32_t in_off, int32_t hw,
+                   int32_t uniform, float sigma, float *x, float *clamp, void *stream);
 
 /* Host-side batched board generation (the inputs of the workloads), on `threads` host threads
  * (0 = all). Every board draws from its own Philox4x32-10 stream keyed on `seed`, so the

@@ -52,6 +52,7 @@ EXPORTS = (
     "nca_set_bptt_backward_path",
     "nca_damage_clamp",
     "nca_pool_rows",
+    "nca_init_state",
     "nca_maze_boards",
     "nca_sudoku_boards",
 )
@@ -193,6 +194,7 @@ def load():
     L.nca_damage_clamp.argtypes = [vp, i64, i32, i32, i32, vp, i32, i32, ctypes.c_float, vp, vp,
                                    i32, i32, vp]
     L.nca_pool_rows.argtypes = [ctypes.POINTER(PoolRowCopy), i32, i64, vp]
+    L.nca_init_state.argtypes = [vp, vp, vp, vp, i32, i64, i32, i32, i32, i32, i32, ctypes.c_float, vp, vp, vp]
     L.nca_maze_boards.argtypes = [i64, i32, ctypes.c_uint64, ctypes.c_double, i32, i32, vp, vp, vp,
                                   vp, i32]
     L.nca_sudoku_boards.argtypes = [i64, ctypes.c_uint64, i32, i32, vp, vp, vp, i32]

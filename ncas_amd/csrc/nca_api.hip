@@ -589,7 +589,7 @@ size_t recorded_xch_bytes(const nca_cell_desc *cell, int64_t rows, int H, int W)
 int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows, int H, int W, const float *x_in,
                      const uint8_t *given, const float *clamp, float *x_out, const nca_fire_desc *fire, int n_steps,
                      float *x_rec, int64_t rec_stride, hipStream_t st, bool *used, void *xch, size_t xch_bytes,
-                     int *pieces) {
+                     int *pieces, float *x_rec0) {
     *used = false;
     if (pieces) *pieces = 1;
     // anything the checks of nca_rollout_ws would refuse is left to the caller's fallback
@@ -615,6 +615,7 @@ int rollout_recorded(const nca_cell_desc *cell, const void *packed, int64_t rows
     p.tau = fire->tau;
     p.x_rec = x_rec;
     p.rec_stride = rec_stride;
+    p.x_rec0 = x_rec0;
     int P = xch ? recorded_pieces(cell, rows, H, W) : 1;
     if (P > 1 && xch_bytes < nca::stream32_xch_bytes(rows, P, W)) P = 1;
     const int rc = hip_check(nca::launch_stream32(p, st, kLdsBytes, used, P, static_cast<uint64_t *>(xch)),

@@ -213,6 +213,24 @@ __global__ void zero_f32_words(float *p, int64_t n, uint64_t *q, int64_t m) {
     for (int64_t i = t; i < m; i += stride) q[i] = 0;
 }
 
+// the one-launch backward's set-up: blocks below kMb32PrepBlocks build mlp_back32_prep's weight
+// image, the others clear m 8-byte words at q (the status word and exchange slots of its pieces)
+// and the n1 and n2 floats at p1 and p2 (the partial-sum and loss slots no workgroup writes)
+constexpr int kPrepClearBlocks = 128;
+__global__ void __launch_bounds__(512) prep_clear_kernel(const float *w1, const float *w2, unsigned char *img,
+                                                         uint64_t *q, int64_t m, float *p1, int64_t n1, float *p2,
+                                                         int64_t n2) {
+    if ((int)blockIdx.x < nca::kMb32PrepBlocks) {
+        nca::mb32_prep_fragment(blockIdx.x, w1, w2, img);
+        return;
+    }
+    const int64_t t = (blockIdx.x - nca::kMb32PrepBlocks) * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)(gridDim.x - nca::kMb32PrepBlocks) * blockDim.x;
+    for (int64_t i = t; i < m; i += stride) q[i] = 0;
+    for (int64_t i = t; i < n1; i += stride) p1[i] = 0.0f;
+    for (int64_t i = t; i < n2; i += stride) p2[i] = 0.0f;
+}
+
 __global__ void zero_f32(float *p, int64_t n) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = 0.0f;
@@ -1200,15 +1218,16 @@ int nca_bptt_forward_ws(const nca_cell_desc *cell, const void *packed, int64_t r
     const int64_t sn = d.rows * d.C * (int64_t)d.HW;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (rows == 0) return NCA_OK;
-    if (states != x0) {
-        rc = nca::hip_status(hipMemcpyAsync(states, x0, sn * sizeof(float), hipMemcpyDeviceToDevice, st), "state copy");
-        if (rc) return rc;
-    }
-    // the whole chunk in one launch of the streamed kernel where it takes the cell and grid
+    // the whole chunk in one launch of the streamed kernel where it takes the cell and grid (which
+    // also copies x0 into states[0]); else a copy and one launch per step
     bool used = false;
     int pieces = 1;
     if ((rc = nca::rollout_recorded(cell, packed, rows, height, width, x0, given, clamp, states + n_chunk * sn, fire,
-                                    n_chunk, states + sn, sn, st, &used, workspace, workspace_bytes, &pieces)))
+                                    n_chunk, states + sn, sn, st, &used, workspace, workspace_bytes, &pieces,
+                                    states != x0 ? states : nullptr)))
+        return rc;
+    if (!used && states != x0 &&
+        (rc = nca::hip_status(hipMemcpyAsync(states, x0, sn * sizeof(float), hipMemcpyDeviceToDevice, st), "state copy")))
         return rc;
     // the workspace's first word reports whether a wait of the boards' pieces ran out: zero unless
     // this call sets it (the launch of pieces clears it itself)
@@ -1316,8 +1335,18 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
     const FusedChoice fc = fused_choice(d, n_chunk, fire_f32 != nullptr, L);
     uint64_t *const wsw = static_cast<uint64_t *>(workspace);
     const int64_t xch_words = fc.pieces > 1 ? (int64_t)(fc.xch_bytes / sizeof(uint64_t)) - 1 : 0;
-    hipLaunchKernelGGL(zero_f32_words, dim3(2048), dim3(256), 0, st, part, L.denom - L.part, wsw + 1, xch_words);
     const bool fused = fused_mlp(d);
+    if (fc.pieces > 0) {
+        // the one-launch backward writes every value of its workgroups' slots (and the finish
+        // launch writes acc): only the slots beyond them, the exchange words and the status word
+        // need clearing, in the launch that builds the weight image
+        const int64_t written = d.rows * (int64_t)fc.pieces;
+        hipLaunchKernelGGL(prep_clear_kernel, dim3(nca::kMb32PrepBlocks + kPrepClearBlocks), dim3(512), 0, st, w->w1,
+                           w->w2, reinterpret_cast<unsigned char *>(ws + L.img), wsw + 1, xch_words,
+                           part + written * P.P, (kSplit - written) * P.P, lossacc + written, kSplit - written);
+    } else {
+        hipLaunchKernelGGL(zero_f32_words, dim3(2048), dim3(256), 0, st, part, L.denom - L.part, wsw + 1, xch_words);
+    }
     auto mlp_kfn = (d.M & 3) == 0 ? nca::mlp_back32<true> : nca::mlp_back32<false>;
     if (fused && (rc = nca::hip_status(hipFuncSetAttribute(reinterpret_cast<const void *>(mlp_kfn),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1336,7 +1365,7 @@ int backward_impl(const Dims &d, const void *packed, const nca_cell_weights *w,
     const int64_t strip_blocks = (d.rows * d.C + kStripPlanes - 1) / kStripPlanes;
     // cells per workgroup of the fused kernel: whole 32-cell tiles
     const int per32 = (int)((((d.M + kSplit - 1) / kSplit) + 31) / 32 * 32);
-    if (fused)
+    if (fused && fc.pieces == 0)
         hipLaunchKernelGGL(nca::mlp_back32_prep, dim3(nca::kMb32PrepBlocks), dim3(512), 0, st, w->w1, w->w2,
                            reinterpret_cast<unsigned char *>(ws + L.img));
     if (loss->loss_mask && d.M > 0) hipLaunchKernelGGL(mask_sum, dim3(1), dim3(kThreads), 0, st, loss->loss_mask, d.M, denom);

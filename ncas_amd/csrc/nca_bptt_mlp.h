@@ -108,10 +108,9 @@ __device__ __forceinline__ bf16x8 mb_cat(s16x4 lo, s16x4 hi) {
 // fragment's 8 loads.
 constexpr int kMb32PrepBlocks = 18;
 
-__global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const float *w2, unsigned char *img) {
+__device__ __forceinline__ void mb32_prep_fragment(int f, const float *w1, const float *w2, unsigned char *img) {
     typedef Mb32 S;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r = lane & 15, g = lane >> 4;
-    const int f = blockIdx.x;
     float v[8];
     if (f < 8) {
         const int ht = f >> 2, kb = f & 3, hid = 32 * w + 16 * ht + r;
@@ -129,6 +128,10 @@ __global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const fl
         for (int j = 0; j < 8; ++j) v[j] = w1[(32 * kb + mb_perm(g, j)) * 128 + 16 * w + r];
         *reinterpret_cast<bf16x8 *>(img + S::IMG_W1TF + (tid * 8 + kb) * 16) = mb_pack8(v);
     }
+}
+
+__global__ void __launch_bounds__(512) mlp_back32_prep(const float *w1, const float *w2, unsigned char *img) {
+    mb32_prep_fragment(blockIdx.x, w1, w2, img);
 }
 
 // VEC: M is a multiple of 4, so the cell quads of a tile are 16-byte aligned.

@@ -53,6 +53,7 @@ struct RolloutParams {
     int32_t *fired_out;
     float *x_rec;        // or null: the state after step s of the call goes to x_rec + s rec_stride
     int64_t rec_stride;  // (the streamed C = 32 kernel only)
+    float *x_rec0;       // or null: the call's input state copied there (the same kernel, with x_rec)
     int64_t rows;
     int H, W;
     int c_in, in_off, c_out, out_off, n_out, head_kind, padding;

@@ -229,6 +229,10 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                 if (e < N) {
                     const int ch = e / NR, c = e - ch * NR, rr = c / W, j = c - rr * W;
                     M[((rlo + rr - r0 + 1) * (W + 1) + j + 1) * S::C + ch] = v[k];
+                    // the copy of the caller's state (the chunk's first record): the workgroup's
+                    // own rows only
+                    if (REC && a.x_rec0 && rlo + rr >= r0 && rlo + rr < r0 + Hs)
+                        a.x_rec0[row * S::C * HWt + ch * HWt + rlo * W + c] = v[k];
                 }
             }
         }

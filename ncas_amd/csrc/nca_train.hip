@@ -18,6 +18,11 @@
 //   batch, the fresh boards' rows and the age counters) in one launch: the reference indexes each
 //   of the pool's tensors on its own (src/nca/pool.py:96-179), one kernel per tensor and step.
 //
+// nca_init_state - a batch's initial state (model.py:384-412): the noise scaled as the reference
+//   scales it, the clamp values (the input tokens' embeddings, model.py:378-382) and their
+//   application to the given cells' input channels (model.py:430-438) in one pass; the
+//   reference's torch ops take six launches.
+//
 // nca_damage_clamp - the damage perturbation (src/nca/perturb.py:43-106: the state set to `fill`
 //   inside discs) and the clamp of the given cells' input channels (model.py:430-438) in one pass
 //   over the state, in place. The discs are drawn on the host (their random stream is the
@@ -237,7 +242,53 @@ __global__ void __launch_bounds__(kRowThreads) pool_rows_kernel(RowArgs a) {
     }
 }
 
+// One thread per state element (row, channel, cell): coalesced over the cells of a plane.
+constexpr int kInitThreads = 256;
+
+__global__ void __launch_bounds__(kInitThreads)
+    init_state_kernel(const float *__restrict__ noise, const int64_t *__restrict__ tokens,
+                      const uint8_t *__restrict__ given, const float *__restrict__ embed, int vocab, int64_t rows,
+                      int C, int c_in, int in_off, int hw, int uniform, float sigma, float *__restrict__ x,
+                      float *__restrict__ clamp) {
+    const int64_t o = (int64_t)blockIdx.x * kInitThreads + threadIdx.x;
+    if (o >= rows * C * (int64_t)hw) return;
+    const int64_t bc = o / hw;
+    const int q = (int)(o - bc * hw);
+    const int64_t b = bc / C;
+    const int c = (int)(bc - b * C);
+    const float r = noise[o];
+    // the reference's expressions, one rounding per operation: (rand * 2 - 1) * sigma or
+    // randn * sigma
+    float v = uniform ? __fmul_rn(__fsub_rn(__fmul_rn(r, 2.0f), 1.0f), sigma) : __fmul_rn(r, sigma);
+    const int ci = c - in_off;
+    if (ci >= 0 && ci < c_in) {
+        const int64_t tok = tokens[b * hw + q];
+        const float cv = tok >= 0 && tok < vocab ? embed[tok * c_in + ci] : __int_as_float(0x7fc00000);
+        clamp[(b * c_in + ci) * hw + q] = cv;
+        if (given[b * hw + q]) v = cv;
+    }
+    x[o] = v;
+}
+
 }  // namespace
+
+extern "C" int nca_init_state(const float *noise, const int64_t *tokens, const uint8_t *given, const float *embed,
+                              int32_t vocab, int64_t rows, int32_t channels, int32_t c_in, int32_t in_off,
+                              int32_t hw, int32_t uniform, float sigma, float *x, float *clamp, void *stream) {
+    nca::clear_error();
+    if (rows < 0 || channels < 1 || c_in < 0 || in_off < 0 || in_off + c_in > channels || hw < 1 || vocab < 1)
+        return nca::set_error(NCA_ERR_INVALID, "rows >= 0, 0 <= in_off, in_off + c_in <= channels, hw >= 1, vocab >= 1");
+    if (rows == 0) return NCA_OK;
+    if (!noise || !tokens || !given || !x || (c_in > 0 && (!embed || !clamp)))
+        return nca::set_error(NCA_ERR_INVALID, "NULL pointer argument");
+    const int64_t n = rows * (int64_t)channels * hw;
+    if (n > 0x7fffffffll * kInitThreads) return nca::set_error(NCA_ERR_UNSUPPORTED, "too many state elements");
+    const unsigned blocks = (unsigned)((n + kInitThreads - 1) / kInitThreads);
+    hipLaunchKernelGGL(init_state_kernel, dim3(blocks), dim3(kInitThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                       noise, tokens, given, embed, (int)vocab, rows, (int)channels, (int)c_in, (int)in_off, (int)hw,
+                       (int)uniform, sigma, x, clamp);
+    return nca::hip_status(hipGetLastError(), "init state launch");
+}
 
 extern "C" int nca_pool_rows(const nca_pool_row_copy *items, int32_t n_items, int64_t n_rows, void *stream) {
     nca::clear_error();

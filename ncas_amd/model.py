@@ -310,12 +310,29 @@ class NCA(nn.Module):
         cfg = self.cfg
         B, H, W = inputs.shape
         shape = (B, cfg.channels, H, W)
-        if cfg.init_uniform:
-            x = (torch.rand(shape, generator=generator, device=self.device) * 2 - 1) * cfg.sigma_init
-        else:
-            x = torch.randn(shape, generator=generator, device=self.device) * cfg.sigma_init
-        given4 = given[:, None].to(self.device)
-        clamp = self.clamp_values(inputs.to(self.device))
+        dev = self.device
+        draw = torch.rand if cfg.init_uniform else torch.randn
+        noise = draw(shape, generator=generator, device=dev)
+        given = given.to(dev)
+        given4 = given[:, None]
+        if dev.type == "cuda":
+            # the scaling, the clamp values and their application in one launch (nca_init_state)
+            sl = cfg.in_slice
+            emb = self.embed.detach().to(torch.float32).contiguous()
+            tok = inputs.to(dev, torch.int64).contiguous()
+            g8 = (given.contiguous().view(torch.uint8) if given.dtype == torch.bool
+                  else (given != 0).to(torch.uint8).contiguous())
+            x = torch.empty(shape, dtype=torch.float32, device=dev)
+            clamp = torch.empty((B, emb.shape[1], H, W), dtype=torch.float32, device=dev)
+            if emb.shape[1] != sl.stop - sl.start:
+                raise ValueError("the embedding width must equal the clamped input slice")
+            _lib.check(_lib.load().nca_init_state(
+                noise.data_ptr(), tok.data_ptr(), g8.data_ptr(), emb.data_ptr(), emb.shape[0], B,
+                cfg.channels, emb.shape[1], sl.start, H * W, int(bool(cfg.init_uniform)),
+                float(cfg.sigma_init), x.data_ptr(), clamp.data_ptr(), _lib.stream_of(dev)), "nca_init_state")
+            return x, given4, clamp
+        x = ((noise * 2 - 1) if cfg.init_uniform else noise) * cfg.sigma_init
+        clamp = self.clamp_values(inputs.to(dev))
         return self.apply_clamp(x, given4, clamp), given4, clamp
 
     def target_embedding(self, targets):

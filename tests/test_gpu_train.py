@@ -335,6 +335,37 @@ def test_engine_mse_loss_with_an_l2_head():
         assert _rel(got[k], ref[k]) <= 1e-4, (k, _rel(got[k], ref[k]))
 
 
+@pytest.mark.parametrize("name", ["maze_c16", "sudoku_c64", "maze_hard_c32", "ref_maze_ood"])
+@pytest.mark.parametrize("uniform", [False, True])
+def test_init_state_matches_the_reference_expressions(name, uniform):
+    """nca_init_state (model.init_state on the GPU) against the reference's torch expressions
+    (src/nca/model.py:384-412: noise scaled, embed[inputs] as clamp, the clamp on the given
+    cells' input channels) evaluated on the same draw: bit for bit."""
+    preset, size = CELLS[name]
+    m = make_model(name, 0)
+    m.cfg.init_uniform = uniform
+    m.cfg.sigma_init = 0.37
+    md = copy.deepcopy(m).to(DEV)
+    b = boards_for(preset, 5, size, 3)
+    inputs = torch.as_tensor(np.asarray(b.inputs)).to(DEV, torch.int64)
+    given = torch.as_tensor(np.asarray(b.given)).to(DEV, torch.bool)
+    _say("init_state", name, uniform, tuple(inputs.shape))
+    x, g4, cl = md.init_state(inputs, given, None, torch.Generator(device=DEV).manual_seed(11))
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    shape = (inputs.shape[0], md.cfg.channels) + tuple(inputs.shape[1:])
+    if uniform:
+        rx = (torch.rand(shape, generator=gen, device=DEV) * 2 - 1) * md.cfg.sigma_init
+    else:
+        rx = torch.randn(shape, generator=gen, device=DEV) * md.cfg.sigma_init
+    rcl = md.embed.detach()[inputs].permute(0, 3, 1, 2).contiguous()
+    sl = md.cfg.in_slice
+    rx[:, sl] = torch.where(given[:, None], rcl, rx[:, sl])
+    assert given.any() and (~given).any()
+    assert torch.equal(g4, given[:, None])
+    assert torch.equal(cl, rcl)
+    assert torch.equal(x, rx)
+
+
 def test_engine_step_noise():
     """Step noise (p_t, p_s, sigma): every step's noise is drawn from its seed; the rollout
     outside the chunk and the chunk's gradients match the oracle fed the same noise."""
