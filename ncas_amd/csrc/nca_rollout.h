@@ -438,6 +438,91 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
         }
     };
 
+    // ---- fp32 cells with C = 16 and 128 hidden units (one fc2 m-tile): the work of a tile split
+    // evenly over the four waves. fc2 is split by hidden unit: wave w's fc1 output (hidden unit
+    // 32 w + 16 mt + 4 g + v of cell n in lane (g, n)) is, as it lies in the registers, the B
+    // operand of fc2's k-tile (mt, v), whose A operand is W2[l16][32 w + 16 mt + 4 g + v]; the four
+    // partial sums (wave 0's from b2) meet in the H region and the update adds them in wave order.
+    // The stencil's kernel k runs on wave k, each output's tap chain in the order of `stencil`.
+    // (Otherwise wave 0 alone ran the stencil and fc2: twice the other waves' MFMA time.)
+    constexpr bool KSPLIT = !BF16 && C == 16 && HD == 128;
+    float w2p[2][4], kwv[9];
+    if constexpr (KSPLIT) {
+        const float *w2 = reinterpret_cast<const float *>(a.packed + a.off_w2);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) w2p[mt][v] = w2[(8 * wave + 4 * mt + g) * 64 + 16 * v + l16];
+#pragma unroll
+        for (int t9 = 0; t9 < 9; ++t9) kwv[t9] = kern[wave * 9 + t9];
+    }
+    float *RED = reinterpret_cast<float *>(Hb);  // [buffer][wave][cell][channel]
+    // fc1 of the tile in Z buffer zb and this wave's part of fc2 -> RED buffer rb
+    auto fc1_ks = [&](int zb, int rb) {
+        fr_t zf[S::KT1];
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt) zf[kt] = FR::load_lds(Zb, zb * S::ZBUF + l16 * S::ZS + kt * S::KT + g);
+        f32x4 acc[S::MT1];
+#pragma unroll
+        for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt)
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = FR::mfma(w1f[mt][kt], zf[kt], acc[mt]);
+        f32x4 part = b2v[0];  // b2 on wave 0, zeros on the others
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float h = acc[mt][v] > 0.0f ? acc[mt][v] : 0.0f;
+                part = FR::mfma(w2p[mt][v], h, part);
+            }
+        *reinterpret_cast<float4 *>(RED + ((rb * 4 + wave) * 16 + l16) * 16 + 4 * g) =
+            make_float4(part[0], part[1], part[2], part[3]);
+    };
+    // stencil kernel `wave` of tile t's cells (lane: cell l16, channel quad g) -> Z buffer zb
+    auto stencil_ks = [&](int pc, int zb, int cur) {
+        const int base = cur * PBUF + pc + 4 * g;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t9 = 0; t9 < 9; ++t9) {
+            float v[4];
+            lds_load4<false>(Pb, base + toff[t9], v);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = __builtin_fmaf(kwv[t9], v[c], acc[c]);
+        }
+        lds_store4<false>(Zb, zb * S::ZBUF + l16 * S::ZS + wave * C + 4 * g, acc);
+    };
+    // the update of tile t from RED buffer rb: lanes 0-15 of each wave, cell 4 wave + lane / 4,
+    // channel quad lane % 4
+    auto update_ks = [&](int t, int rb, int cur, int nxt, bool full) {
+        if (lane >= 16) return;
+        const int n = 4 * wave + (lane >> 2), c0 = 4 * (lane & 3);
+        const int gq = t * 16 + n, gc = gq < ncell ? gq : ncell - 1;
+        const int pc = cinfo[gc];
+        const float f = fireL[gc];
+        const bool gv = givenL[gc] != 0;
+        float xo[4];
+        lds_load4<false>(Pb, cur * PBUF + pc + c0, xo);
+        float4 pw[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) pw[w] = *reinterpret_cast<const float4 *>(RED + ((rb * 4 + w) * 16 + n) * 16 + c0);
+        float u[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float *q0 = &pw[0].x, *q1 = &pw[1].x, *q2 = &pw[2].x, *q3 = &pw[3].x;
+            const float dxv = __fadd_rn(__fadd_rn(__fadd_rn(q0[v], q1[v]), q2[v]), q3[v]);
+            float uv = __fadd_rn(xo[v], __fmul_rn(f, dxv));
+            if constexpr (NOISE) {
+                const int r = gc / HWn;
+                uv = __fadd_rn(uv, a.noise[((rbase + r) * C + c0 + v) * HWn + (gc - r * HWn)]);
+            }
+            const int c = c0 + v;
+            u[v] = (gv && c >= in_off && c < in_off + c_in) ? xo[v] : uv;
+        }
+        if (full || gq < ncell) lds_store4<false>(Pb, nxt * PBUF + pc + c0, u);
+    };
+
     // per-lane cell of the update of tile t: (cell, centre offset, fire, given)
     struct Upd {
         int gq, gc, pc;
@@ -657,16 +742,35 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
         }
     };
 
+    auto stencil_any = [&](int pc, int zb, int cur) {
+        if constexpr (KSPLIT)
+            stencil_ks(pc, zb, cur);
+        else
+            stencil(pc, zb, cur);
+    };
+    auto fc1_any = [&](int zb, int hb) {
+        if constexpr (KSPLIT)
+            fc1_ks(zb, hb);
+        else
+            fc1(zb, hb);
+    };
+    auto update_any = [&](int t, int hb, int cur, int nxt, bool full) {
+        if constexpr (KSPLIT)
+            update_ks(t, hb, cur, nxt, full);
+        else
+            fc2_update(upd_info(t), hb, cur, nxt, full);
+    };
+
     // ---- steps ------------------------------------------------------------------------------
     int cur = 0;
     for (int s = 0; s < a.n_steps; ++s) {
         const int nxt = cur ^ 1;
         draw_fire(s, cur);
-        stencil(stencil_pc(0), 0, cur);
+        stencil_any(stencil_pc(0), 0, cur);
         __syncthreads();
         // interval 0: fc1(0) + stencil(1)
-        fc1(0, 0);
-        if (ntile > 1) stencil(stencil_pc(1), 1, cur);
+        fc1_any(0, 0);
+        if (ntile > 1) stencil_any(stencil_pc(1), 1, cur);
         __syncthreads();
         // steady state: fc2/update(t-1), fc1(t), stencil(t+1) in one barrier interval; the cell
         // info of the next interval is read one interval ahead so that every LDS load of an
@@ -678,6 +782,10 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             const int spc_n = stencil_pc(t + 2 < ntile ? t + 2 : ntile - 1);
             if constexpr (BF16 && !NOISE) {
                 interval_bf16(ui, spc, t & 1, t & 1, (t - 1) & 1, (t + 1) & 1, cur, nxt);
+            } else if constexpr (KSPLIT) {
+                update_ks(t - 1, (t - 1) & 1, cur, nxt, true);
+                fc1_ks(t & 1, t & 1);
+                stencil_ks(spc, (t + 1) & 1, cur);
             } else {
                 fc2_update(ui, (t - 1) & 1, cur, nxt, true);
                 fc1(t & 1, t & 1);
@@ -688,11 +796,11 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             spc = spc_n;
         }
         if (ntile > 1) {
-            fc2_update(upd_info(ntile - 2), (ntile - 2) & 1, cur, nxt, false);
-            fc1((ntile - 1) & 1, (ntile - 1) & 1);
+            update_any(ntile - 2, (ntile - 2) & 1, cur, nxt, false);
+            fc1_any((ntile - 1) & 1, (ntile - 1) & 1);
             __syncthreads();
         }
-        fc2_update(upd_info(ntile - 1), (ntile - 1) & 1, cur, nxt, false);
+        update_any(ntile - 1, (ntile - 1) & 1, cur, nxt, false);
         __syncthreads();
         if (s == 0 && c_in > 0) {
             clamp_pass(nxt);

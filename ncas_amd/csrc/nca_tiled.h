@@ -168,9 +168,14 @@ __global__ void __launch_bounds__(256, 1) step_tiled(TiledParams tp) {
     fr_t w2f[T::KT2];
     f32x4 b2v;
     bool insl[4];
+    // fp32 cells with C = 16 and 128 hidden units sum fc2 as the resident kernel does: four partial
+    // sums over hidden units [32 p, 32 p + 32) (the first from b2), each an MFMA chain over k-tiles
+    // (mt, v) = hidden units 32 p + 16 mt + 4 k + v, k = 0..3, added in order p = 0..3
+    constexpr bool KS = !BF16 && C == 16 && HD == 128;
 #pragma unroll
     for (int kt = 0; kt < T::KT2; ++kt)
-        w2f[kt] = reinterpret_cast<const fr_t *>(a.packed + a.off_w2)[((size_t)mt2 * T::KT2 + kt) * 64 + lane];
+        w2f[kt] = reinterpret_cast<const fr_t *>(a.packed + a.off_w2)[KS ? (size_t)(8 * (kt >> 3) + 4 * ((kt >> 2) & 1) + g) * 64 + 16 * (kt & 3) + l16
+                                                                          : ((size_t)mt2 * T::KT2 + kt) * 64 + lane];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int c = 16 * mt2 + 4 * g + v;
@@ -280,11 +285,28 @@ __global__ void __launch_bounds__(256, 1) step_tiled(TiledParams tp) {
         const float xo[4] = {m4.x, m4.y, m4.z, m4.w};
         const int hrow = hb * T::HBUF + (tt2 * 16 + l16) * T::HS + (BF16 ? 8 * g : g);
         fr_t hf[T::KT2];
-#pragma unroll
-        for (int kt = 0; kt < T::KT2; ++kt) hf[kt] = FR::load_lds(Hb, hrow + kt * T::KT);
         f32x4 acc2 = b2v;
+        if constexpr (KS) {
+            // k-tile 8 p + 4 mt + v: hidden unit 32 p + 16 mt + 4 g + v of the lane's cell
+            const int hrow_k = hb * T::HBUF + (tt2 * 16 + l16) * T::HS + 4 * g;
 #pragma unroll
-        for (int kt = 0; kt < T::KT2; ++kt) acc2 = FR::mfma(w2f[kt], hf[kt], acc2);
+            for (int kt = 0; kt < T::KT2; ++kt) hf[kt] = FR::load_lds(Hb, hrow_k + 32 * (kt >> 3) + 16 * ((kt >> 2) & 1) + (kt & 3));
+            f32x4 part[4];
+#pragma unroll
+            for (int p4 = 0; p4 < 4; ++p4) {
+                part[p4] = p4 == 0 ? b2v : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k8 = 0; k8 < 8; ++k8) part[p4] = FR::mfma(w2f[8 * p4 + k8], hf[8 * p4 + k8], part[p4]);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                acc2[v] = __fadd_rn(__fadd_rn(__fadd_rn(part[0][v], part[1][v]), part[2][v]), part[3][v]);
+        } else {
+#pragma unroll
+            for (int kt = 0; kt < T::KT2; ++kt) hf[kt] = FR::load_lds(Hb, hrow + kt * T::KT);
+#pragma unroll
+            for (int kt = 0; kt < T::KT2; ++kt) acc2 = FR::mfma(w2f[kt], hf[kt], acc2);
+        }
         float u[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
