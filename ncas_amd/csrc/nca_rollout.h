@@ -742,6 +742,74 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
         }
     };
 
+    // the steady-state interval of the split fp32 path, hand-interleaved: every LDS load first
+    // (fc1's operands, the next tile's taps, the update's partial sums and state), then fc1's
+    // MFMAs k-tile by k-tile, each followed by one tap of the stencil (its four FMA chains advance
+    // one tap), then this wave's part of fc2 and the stores; the update's VALU last, beside the
+    // MFMA tail. sched_barrier(0) keeps the groups in this order; the arithmetic is that of
+    // update_ks, fc1_ks and stencil_ks.
+    auto interval_ks = [&](int t, int spc, int cur, int nxt) {
+        const int zb = t & 1;
+        fr_t zf[S::KT1];
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt) zf[kt] = FR::load_lds(Zb, zb * S::ZBUF + l16 * S::ZS + kt * S::KT + g);
+        const int sbase = cur * PBUF + spc + 4 * g;
+        float tp[9][4];
+#pragma unroll
+        for (int t9 = 0; t9 < 9; ++t9) lds_load4<false>(Pb, sbase + toff[t9], tp[t9]);
+        // the update of tile t-1 (lanes 0-15): cell 4 wave + lane / 4, channel quad lane % 4
+        const bool ul = lane < 16;
+        const int un = 4 * wave + ((lane & 15) >> 2), uc0 = 4 * (lane & 3);
+        const int ugq = (t - 1) * 16 + un, ugc = ugq < ncell ? ugq : ncell - 1;
+        const int upc = cinfo[ugc];
+        const float uf = fireL[ugc];
+        const bool ugv = givenL[ugc] != 0;
+        float uxo[4];
+        lds_load4<false>(Pb, cur * PBUF + upc + uc0, uxo);
+        float4 pw[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            pw[w] = *reinterpret_cast<const float4 *>(RED + ((((t - 1) & 1) * 4 + w) * 16 + un) * 16 + uc0);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 acc[S::MT1];
+#pragma unroll
+        for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = b1v[mt];
+        float sacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kt = 0; kt < S::KT1; ++kt) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mt = 0; mt < S::MT1; ++mt) acc[mt] = FR::mfma(w1f[mt][kt], zf[kt], acc[mt]);
+            if (kt < 9) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) sacc[c] = __builtin_fmaf(kwv[kt], tp[kt][c], sacc[c]);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        lds_store4<false>(Zb, ((t + 1) & 1) * S::ZBUF + l16 * S::ZS + wave * C + 4 * g, sacc);
+        f32x4 part = b2v[0];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float h = acc[mt][v] > 0.0f ? acc[mt][v] : 0.0f;
+                part = FR::mfma(w2p[mt][v], h, part);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        float u[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float *q0 = &pw[0].x, *q1 = &pw[1].x, *q2 = &pw[2].x, *q3 = &pw[3].x;
+            const float dxv = __fadd_rn(__fadd_rn(__fadd_rn(q0[v], q1[v]), q2[v]), q3[v]);
+            const float uv = __fadd_rn(uxo[v], __fmul_rn(uf, dxv));
+            const int c = uc0 + v;
+            u[v] = (ugv && c >= in_off && c < in_off + c_in) ? uxo[v] : uv;
+        }
+        if (ul) lds_store4<false>(Pb, nxt * PBUF + upc + uc0, u);
+        *reinterpret_cast<float4 *>(RED + ((zb * 4 + wave) * 16 + l16) * 16 + 4 * g) =
+            make_float4(part[0], part[1], part[2], part[3]);
+    };
+
     auto stencil_any = [&](int pc, int zb, int cur) {
         if constexpr (KSPLIT)
             stencil_ks(pc, zb, cur);
@@ -782,6 +850,8 @@ __global__ void __launch_bounds__(256, 1) rollout_resident(RolloutParams a) {
             const int spc_n = stencil_pc(t + 2 < ntile ? t + 2 : ntile - 1);
             if constexpr (BF16 && !NOISE) {
                 interval_bf16(ui, spc, t & 1, t & 1, (t - 1) & 1, (t + 1) & 1, cur, nxt);
+            } else if constexpr (KSPLIT && !NOISE) {
+                interval_ks(t, spc, cur, nxt);
             } else if constexpr (KSPLIT) {
                 update_ks(t - 1, (t - 1) & 1, cur, nxt, true);
                 fc1_ks(t & 1, t & 1);
