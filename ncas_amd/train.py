@@ -482,7 +482,7 @@ class ReplayPool:
         host = np.zeros(max(total, 1), np.uint8)
         for a, o in zip(arrays, offs):
             host[o:o + a.nbytes] = a.reshape(-1).view(np.uint8)
-        dev = _lib.upload(host, self.device)
+        dev = _lib.upload_beside(host, self.device)
         return [dev[o:o + a.nbytes].view(torch.from_numpy(a[:0].reshape(-1)).dtype).view(a.shape)
                 for a, o in zip(arrays, offs)]
 
