@@ -16,6 +16,10 @@
 //            u = x + fire * dx (+ noise); input-slice channels of given cells are frozen at
 //            their clamp value; written to the fp32 state and the other perception buffer.
 //
+// fp32 cells with C = 16 (one fc2 m-tile) split the work otherwise: each wave runs fc2 over its
+// own hidden units from its fc1 registers, the update adds the four partial sums, and the
+// stencil's kernel k runs on wave k (see KSPLIT below).
+//
 // Software pipeline: Z and H are double-buffered so that one barrier interval holds fc2 and the
 // update of tile t-1, fc1 of tile t and the stencil of tile t+1 - MFMA and VALU work of the same
 // wave that the hardware overlaps - with a single workgroup barrier per tile.
