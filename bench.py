@@ -385,6 +385,16 @@ def roofline(name, wl, precision, res):
     elif block["traffic"]:
         # the resident kernels touch HBM once per launch: the measured bytes per cell-update
         ceilings["hbm"] = PEAK_HBM_GBS * 1e9 / (block["traffic"] / res["cell_updates"])
+    if name == "maze13":
+        # one board per workgroup of the resident kernel (ceil(rows / 256) boards each): with
+        # fewer boards than CUs the rest of the chip idles, so the fraction of the occupied CUs'
+        # peak is given beside the chip's
+        rows = wl["boards"] * wl["k"]
+        per_wg = max(1, -(-rows // N_CU))
+        wgs = -(-rows // per_wg)
+        if wgs < N_CU:
+            block["workgroups"] = wgs
+            block["frac_of_occupied_cus"] = block["frac"] * N_CU / wgs
     block["ceilings"] = ceilings
     return block
 
