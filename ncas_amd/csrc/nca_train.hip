@@ -217,28 +217,48 @@ struct RowArgs {
     int64_t n_rows;
 };
 
+// Workgroup (r, item, chunk) copies bytes [chunk kRowChunk, (chunk + 1) kRowChunk) of the item's
+// row r: a 115 KB state row is 8 workgroups, and each thread issues its four 16-byte loads before
+// its stores (one workgroup per row, looping, took 17 us for a training batch: a round trip per
+// 4 KB).
+constexpr int64_t kRowChunk = 16384;
+
 __global__ void __launch_bounds__(kRowThreads) pool_rows_kernel(RowArgs a) {
     const int64_t r = blockIdx.x;
     const nca_pool_row_copy &c = a.it[blockIdx.y];
+    const int64_t lo = (int64_t)blockIdx.z * kRowChunk;
+    if (lo >= c.row_bytes) return;
+    const int64_t hi = c.row_bytes - lo < kRowChunk ? c.row_bytes : lo + kRowChunk;
     const int64_t sr = c.src_row ? c.src_row[r] : r;
     if (sr < 0) return;
     const int64_t dr = c.dst_row ? c.dst_row[r] : r;
     unsigned char *dst = static_cast<unsigned char *>(c.dst) + dr * c.row_bytes;
     const unsigned char *src = c.mode == 2 ? nullptr : static_cast<const unsigned char *>(c.src) + sr * c.row_bytes;
     if (c.mode == 1) {
-        for (int64_t e = threadIdx.x; e < c.row_bytes / 8; e += kRowThreads)
+        for (int64_t e = lo / 8 + threadIdx.x; e < hi / 8; e += kRowThreads)
             reinterpret_cast<int64_t *>(dst)[e] = reinterpret_cast<const int64_t *>(src)[e] + 1;
         return;
     }
     const uintptr_t al = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | (uintptr_t)c.row_bytes;
     if ((al & 15u) == 0) {
-        for (int64_t e = threadIdx.x; e < c.row_bytes / 16; e += kRowThreads)
-            reinterpret_cast<uint4 *>(dst)[e] = src ? reinterpret_cast<const uint4 *>(src)[e] : make_uint4(0u, 0u, 0u, 0u);
+        constexpr int kU = (int)(kRowChunk / 16 / kRowThreads);  // 4 quads a thread
+        const int64_t q0 = lo / 16 + threadIdx.x, qn = hi / 16;
+        uint4 v[kU];
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int64_t e = q0 + (int64_t)k * kRowThreads;
+            v[k] = (src && e < qn) ? reinterpret_cast<const uint4 *>(src)[e] : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int k = 0; k < kU; ++k) {
+            const int64_t e = q0 + (int64_t)k * kRowThreads;
+            if (e < qn) reinterpret_cast<uint4 *>(dst)[e] = v[k];
+        }
     } else if ((al & 3u) == 0) {
-        for (int64_t e = threadIdx.x; e < c.row_bytes / 4; e += kRowThreads)
+        for (int64_t e = lo / 4 + threadIdx.x; e < hi / 4; e += kRowThreads)
             reinterpret_cast<uint32_t *>(dst)[e] = src ? reinterpret_cast<const uint32_t *>(src)[e] : 0u;
     } else {
-        for (int64_t e = threadIdx.x; e < c.row_bytes; e += kRowThreads) dst[e] = src ? src[e] : (unsigned char)0;
+        for (int64_t e = lo + threadIdx.x; e < hi; e += kRowThreads) dst[e] = src ? src[e] : (unsigned char)0;
     }
 }
 
@@ -308,8 +328,15 @@ extern "C" int nca_pool_rows(const nca_pool_row_copy *items, int32_t n_items, in
     }
     a.n_items = n_items;
     a.n_rows = n_rows;
+    int64_t chunks = 1;
+    for (int i = 0; i < n_items; ++i) {
+        const int64_t k = (items[i].row_bytes + kRowChunk - 1) / kRowChunk;
+        if (k > chunks) chunks = k;
+    }
+    if (chunks > 65535) return nca::set_error(NCA_ERR_UNSUPPORTED, "rows of at most 1 GiB");
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(pool_rows_kernel, dim3((unsigned)n_rows, (unsigned)n_items), dim3(kRowThreads), 0, st, a);
+    hipLaunchKernelGGL(pool_rows_kernel, dim3((unsigned)n_rows, (unsigned)n_items, (unsigned)chunks), dim3(kRowThreads),
+                       0, st, a);
     return nca::hip_status(hipGetLastError(), "pool rows launch");
 }
 
