@@ -216,7 +216,7 @@ __global__ void zero_f32_words(float *p, int64_t n, uint64_t *q, int64_t m) {
 // the one-launch backward's set-up: blocks below kMb32PrepBlocks build mlp_back32_prep's weight
 // image, the others clear m 8-byte words at q (the status word and exchange slots of its pieces)
 // and the n1 and n2 floats at p1 and p2 (the partial-sum and loss slots no workgroup writes)
-constexpr int kPrepClearBlocks = 128;
+constexpr int kPrepClearBlocks = 238;
 __global__ void __launch_bounds__(512) prep_clear_kernel(const float *w1, const float *w2, unsigned char *img,
                                                          uint64_t *q, int64_t m, float *p1, int64_t n1, float *p2,
                                                          int64_t n2) {
@@ -226,7 +226,14 @@ __global__ void __launch_bounds__(512) prep_clear_kernel(const float *w1, const 
     }
     const int64_t t = (blockIdx.x - nca::kMb32PrepBlocks) * (int64_t)blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)(gridDim.x - nca::kMb32PrepBlocks) * blockDim.x;
-    for (int64_t i = t; i < m; i += stride) q[i] = 0;
+    // the words with 16-byte stores from the first 16-byte boundary (a leading and a trailing
+    // odd word with 8-byte ones)
+    const int64_t head = (reinterpret_cast<uintptr_t>(q) & 15u) ? 1 : 0;
+    const int64_t np = m > head ? (m - head) / 2 : 0;
+    if (t == 0 && head && m > 0) q[0] = 0;
+    if (t == 0 && m > head + 2 * np) q[m - 1] = 0;
+    uint4 *qp = reinterpret_cast<uint4 *>(q + head);
+    for (int64_t i = t; i < np; i += stride) qp[i] = make_uint4(0u, 0u, 0u, 0u);
     for (int64_t i = t; i < n1; i += stride) p1[i] = 0.0f;
     for (int64_t i = t; i < n2; i += stride) p2[i] = 0.0f;
 }

@@ -71,15 +71,22 @@ size_t stream32_xch_bytes(int64_t rows, int P, int W) {
     return P > 1 ? kXchStatusBytes + (size_t)rows * P * 2 * 4 * W * St32::C * sizeof(uint64_t) : 0;
 }
 
+// n 8-byte words at x cleared with 16-byte stores where x is 16-byte aligned (a leading odd word
+// and a trailing one with 8-byte stores)
 __global__ void xch_clear(uint64_t *x, int64_t n) {
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x)
-        x[e] = 0;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t head = (reinterpret_cast<uintptr_t>(x) & 15u) ? 1 : 0;
+    if (t == 0 && head && n > 0) x[0] = 0;
+    const int64_t np = (n - head) / 2;
+    uint4 *xp = reinterpret_cast<uint4 *>(x + head);
+    for (int64_t e = t; e < np; e += stride) xp[e] = make_uint4(0u, 0u, 0u, 0u);
+    if (t == 0 && head + 2 * np < n) x[n - 1] = 0;
 }
 
 hipError_t clear_words(uint64_t *x, int64_t n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    const int64_t b = (n + 255) / 256;
-    hipLaunchKernelGGL(xch_clear, dim3((unsigned)(b < 256 ? b : 256)), dim3(256), 0, st, x, n);
+    const int64_t b = (n / 2 + 255) / 256;
+    hipLaunchKernelGGL(xch_clear, dim3((unsigned)(b < 1024 ? (b > 0 ? b : 1) : 1024)), dim3(256), 0, st, x, n);
     return hipGetLastError();
 }
 
