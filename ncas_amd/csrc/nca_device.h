@@ -69,7 +69,7 @@ __device__ __forceinline__ void cell_uniforms4(uint64_t seed, uint32_t row, uint
 // CPU restatement computes the same bits. No contraction of a*b+c into fma is allowed here.
 #pragma clang fp contract(off)
 
-__device__ __forceinline__ float readout_expf(float x) {
+__host__ __device__ __forceinline__ float readout_expf(float x) {
     if (x < -87.0f) x = -87.0f;
     if (x > 0.0f) x = 0.0f;
     const float n = __builtin_rintf(x * 1.44269504088896341f);

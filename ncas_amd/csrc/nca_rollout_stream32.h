@@ -43,8 +43,9 @@
 // firing, bit 7 the cell's given flag. The channel waves draw the Philox uniforms of a whole step
 // two steps ahead (one evaluation per 4 cells); with gating the update chooses between the two
 // threshold bits. The decision needs only conf > tau: for a 2-output mlp head that is s < conf_s
-// on the sum of exponentials s (one exponential, no division), with conf_s found on the host with
-// the readout's own division.
+// on the sum of exponentials s, with conf_s found on the host with the readout's own division,
+// and since s = 1 + readout_expf(gap) grows with the gap between the two logits, a comparison of
+// the gap with a limit found on the host (no exponential, no division).
 //
 // Clamp (model.py:430-438): the first step's perception reads the caller's state and every step's
 // output holds the clamp values in the input slice of given cells. M starts as the caller's state;
@@ -127,8 +128,12 @@ struct St32Params {
     RolloutParams a;
     int NM, RING, T;
     // gated firing with an mlp head of 2 outputs: conf = 1/s > tau exactly when s < conf_s (s the
-    // sum of exponentials, conf_s computed on the host with IEEE division); fast_conf selects it
+    // sum of exponentials, conf_s computed on the host with IEEE division), and s = 1 +
+    // readout_expf(d) for the gap d = min - max of the two logits, which is non-decreasing in d, so
+    // exactly when d <= conf_d (found on the host through the same readout_expf); fast_conf
+    // selects it
     float conf_s;
+    float conf_d;
     int fast_conf;
     unsigned l_M, l_Z, l_D, l_cinfo, l_ring, l_given, l_head, l_evp, l_flags, l_gidx;
     unsigned off_w1q, off_w2k;
@@ -519,14 +524,14 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) hw4[v][c] = (v < a.n_out && c < a.c_out) ? headL[v * a.c_out + c] : 0.0f;
         }
-        const float tau = a.tau, conf_s = sp.conf_s;
+        const float tau = a.tau, conf_d = sp.conf_d;
         const bool gconf = a.given_confident != 0, fast = sp.fast_conf != 0;
         // the fire bit from a cell's drawn byte and its state's out-slice channels xo
         auto gated_fire = [&](const float xo[4], unsigned byte) -> bool {
             bool hi;
             if (fast) {
                 // two logits in cell_readout_fn's order; s = exp(l0 - m) + exp(l1 - m) where the
-                // larger term is exactly 1, so one exponential gives s
+                // larger term is exactly 1, so s < conf_s is a test on the gap alone
                 float l0 = hb4[0], l1 = hb4[1];
 #pragma unroll
                 for (int c = 0; c < 4; ++c)
@@ -535,8 +540,7 @@ __global__ void __launch_bounds__(512, 1) rollout_stream32(St32Params sp) {
                         l1 = __builtin_fmaf(hw4[1][c], xo[c], l1);
                     }
                 const float best = l1 > l0 ? l1 : l0;
-                const float e = readout_expf((l1 > l0 ? l0 : l1) - best);
-                hi = __fadd_rn(1.0f, e) < conf_s;
+                hi = (l1 > l0 ? l0 : l1) - best <= conf_d;
             } else {
                 hi = cell_readout4(xo, a.c_out, a.n_out, a.head_kind, hw4, hb4) > tau;
             }

@@ -39,6 +39,33 @@ static float conf_threshold(float tau) {
     return r;
 }
 
+// The gated decision of a 2-output mlp head, 1 + readout_expf(d) < conf_s for the logit gap
+// d = min - max <= 0, as d <= the returned limit: readout_expf is non-decreasing on [-87, 0]
+// (checked for every float of that range) and constant below it, so the decision holds on a
+// down-set of gaps, whose largest member a bisection over the magnitudes 0 .. 87 finds with the
+// same readout_expf. NaN: never (conf_s <= 1); +inf: always.
+static float conf_gap_limit(float conf_s) {
+    auto hi = [&](uint32_t mbits) {
+        float m;
+        memcpy(&m, &mbits, 4);
+        volatile float one = 1.0f;
+        return one + readout_expf(-m) < conf_s;
+    };
+    if (!(conf_s > 1.0f)) return __builtin_nanf("");
+    if (hi(0u)) return INFINITY;
+    uint32_t lo = 0u, top = 0x42ae0000u;  // 87.0f: hi(top) since 1 + readout_expf(-87) rounds to 1
+    while (top - lo > 1) {
+        const uint32_t mid = lo + (top - lo) / 2;
+        if (hi(mid))
+            top = mid;
+        else
+            lo = mid;
+    }
+    float m;
+    memcpy(&m, &top, 4);
+    return -m;
+}
+
 // One board per workgroup: needs W <= 31 (in-place update distance), H W >= W + 81 (taps loaded an
 // interval ahead hold the step's state), H W <= 1024 (a step's draw is one group of 4 cells per
 // channel-wave thread), wall or zero padding (the border cells are constants),
@@ -146,6 +173,7 @@ hipError_t launch_stream32(const RolloutParams &p, hipStream_t st, unsigned lds_
         sp.off_w2k = p.off_w2k;
         sp.fast_conf = p.adaptive && p.head_kind == 0 && p.n_out == 2;
         sp.conf_s = conf_threshold(p.tau);
+        sp.conf_d = conf_gap_limit(sp.conf_s);
         // pieces: more than half the LDS, so no two workgroups share a CU (each piece runs
         // alongside its neighbours)
         const unsigned lds = np > 1 && L.total <= lds_limit / 2 ? lds_limit / 2 + 16u : L.total;
